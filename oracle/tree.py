@@ -1,0 +1,352 @@
+"""Oracle: tree planner, canonical top-k, dense candidate tree, attention inputs.
+
+Test infrastructure only (see ``oracle/__init__.py``).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+MASK_MIN = {np.dtype(np.float32): np.finfo(np.float32).min, np.dtype(np.float64): np.finfo(np.float64).min}
+
+
+# --------------------------------------------------------------------------- planner
+def dense_node_count(topk_by_depth) -> int:
+    """Nodes of a dense tree: 1 + sum_d prod_{j<=d} k_j.
+
+    Follows ``flashgrpo/decoding/medusa_tree.py:46-52``.
+    """
+    total, width = 1, 1
+    for k in topk_by_depth:
+        width *= int(k)
+        total += width
+    return total
+
+
+def fit_topk_to_budget(topk_by_depth, node_budget, *, min_topk_by_depth=None, depth_weight_decay=0.5):
+    """Greedy decrement of per-depth branching until the dense tree fits.
+
+    Follows ``flashgrpo/decoding/medusa_tree.py:55-99``: each step removes one
+    candidate at the depth with the best (nodes saved / discounted utility loss)
+    ratio, ties broken by nodes saved then by the deeper depth; when no depth
+    can shrink, the deepest horizon is dropped.
+    """
+    budget = max(1, int(node_budget))
+    ks = [max(1, int(k)) for k in topk_by_depth]
+    mins_in = list(min_topk_by_depth or [])
+    floor = [max(1, min(ks[i], int(mins_in[i]) if i < len(mins_in) else 1)) for i in range(len(ks))]
+    decay = max(float(depth_weight_decay), 1e-3)
+    while ks and dense_node_count(ks) > budget:
+        best = None
+        now = dense_node_count(ks)
+        for d, k in enumerate(ks):
+            if k <= floor[d]:
+                continue
+            trial = ks[:d] + [k - 1] + ks[d + 1:]
+            saved = now - dense_node_count(trial)
+            loss = decay ** d * (math.log1p(k) - math.log(k))
+            score = (saved / max(loss, 1e-9), saved, d)
+            if best is None or score > best:
+                best = score
+        if best is not None:
+            ks[best[2]] -= 1
+        else:
+            ks.pop()
+            floor.pop()
+    return ks
+
+
+@dataclass
+class Plan:
+    node_budget_per_seq: int
+    active_heads: int
+    topk_by_depth: list
+    actual_nodes: int
+    mode: str
+    layout: str
+
+
+def plan_tree(*, active_batch_size, num_medusa_heads, tree_mode, tree_layout, cpeak_nodes,
+              min_tree_nodes_per_seq, max_tree_nodes_per_seq, max_tree_depth,
+              fixed_tree_topk_by_depth, adaptive_tree_enabled=False, adaptive_min_topk_by_depth=None) -> Plan:
+    """Per-step tree plan. Follows ``flashgrpo/decoding/medusa_tree.py:102-178``."""
+    if tree_layout not in ("dense", "sparse"):
+        raise ValueError(tree_layout)
+    layout = "dense"
+    bsz = max(1, int(active_batch_size))
+    if tree_mode == "fixed":
+        budget = int(max_tree_nodes_per_seq)
+        ks = [max(1, int(k)) for k in list(fixed_tree_topk_by_depth)[:num_medusa_heads]]
+        while ks and dense_node_count(ks) > budget:
+            ks[-1] -= 1
+            if ks[-1] <= 0:
+                ks.pop()
+        heads = min(len(ks), max(0, int(max_tree_depth) - 1))
+        ks = ks[:heads]
+    elif tree_mode == "concurrency_aware":
+        budget = int(cpeak_nodes) // bsz
+        budget = max(int(min_tree_nodes_per_seq), min(int(max_tree_nodes_per_seq), budget))
+        max_heads = min(int(num_medusa_heads), max(0, int(max_tree_depth) - 1))
+        defaults = list(fixed_tree_topk_by_depth) or [4, 3, 2, 1, 1]
+        ks = []
+        if adaptive_tree_enabled:
+            mins_in = list(adaptive_min_topk_by_depth or [])
+            floor = []
+            for d in range(max_heads):
+                mk = max(1, int(mins_in[d]) if d < len(mins_in) else 1)
+                if dense_node_count(floor + [mk]) > budget:
+                    break
+                floor.append(mk)
+                ks.append(max(mk, int(defaults[min(d, len(defaults) - 1)])))
+        else:
+            paths, used = 1, 1
+            for d in range(max_heads):
+                want = int(defaults[min(d, len(defaults) - 1)])
+                room = budget - used
+                if room <= 0:
+                    break
+                k = min(max(1, want), max(1, room // paths))
+                if used + paths * k > budget:
+                    k = room // paths
+                if k <= 0:
+                    break
+                ks.append(int(k))
+                paths *= int(k)
+                used += paths
+        heads = len(ks)
+    else:
+        raise ValueError(tree_mode)
+    return Plan(budget, heads, ks, dense_node_count(ks), tree_mode, layout)
+
+
+def topk_from_confidence(confidence, base_k, depth_idx, *, enabled, min_topk_by_depth, low, high):
+    """Map a confidence to a branching factor.
+
+    Follows ``flashgrpo/decoding/flash_medusa_decoder.py:341-360``.
+    """
+    base_k = max(1, int(base_k))
+    mins = list(min_topk_by_depth) or [1]
+    min_k = max(1, min(base_k, int(mins[min(depth_idx, len(mins) - 1)])))
+    if (not enabled) or base_k <= min_k:
+        return base_k
+    if not math.isfinite(float(confidence)):
+        return min_k
+    if high <= low:
+        return min_k if confidence >= high else base_k
+    if confidence <= low:
+        return base_k
+    if confidence >= high:
+        return min_k
+    ratio = (confidence - low) / (high - low)
+    return max(min_k, min(base_k, int(round(base_k - ratio * (base_k - min_k)))))
+
+
+def quantile_linear(values, q):
+    """Linear-interpolation quantile (``torch.quantile`` default), float64."""
+    v = np.sort(np.asarray(values, dtype=np.float64))
+    if v.size == 0:
+        return float("nan")
+    pos = q * (v.size - 1)
+    lo = int(math.floor(pos))
+    hi = min(lo + 1, v.size - 1)
+    return float(v[lo] + (v[hi] - v[lo]) * (pos - lo))
+
+
+# --------------------------------------------------------------------------- canonical top-k
+def sort_key32(x) -> np.ndarray:
+    """Order-preserving uint32 key of float32 values.
+
+    -0.0 maps to +0.0's key and every NaN to the largest key, so that ranking by
+    (key desc, index asc) is a total order that agrees with float comparison.
+    """
+    x = np.asarray(x, dtype=np.float32)
+    bits = x.view(np.uint32).astype(np.uint64)
+    neg = (bits >> 31) == 1
+    key = np.where(neg, (~bits) & 0xFFFFFFFF, bits | 0x80000000)
+    key = np.where(x == 0, np.uint64(0x80000000), key)
+    key = np.where(np.isnan(x), np.uint64(0xFFFFFFFF), key)
+    return key.astype(np.uint64)
+
+
+def rank_order(x) -> np.ndarray:
+    """Indices of a 1-D row sorted by (value desc, index asc)."""
+    key = sort_key32(x)
+    idx = np.arange(key.shape[-1], dtype=np.uint64)
+    comp = (key << np.uint64(32)) | (np.uint64(0xFFFFFFFF) - idx)
+    return np.argsort(~comp, kind="stable")
+
+
+def topk_canonical(x, k):
+    """Top-k of one row, ties broken toward the lower index. Returns (idx, values)."""
+    x = np.asarray(x, dtype=np.float32)
+    order = rank_order(x)[: int(k)]
+    return order.astype(np.int64), x[order]
+
+
+# --------------------------------------------------------------------------- trees
+@dataclass
+class Tree:
+    tokens: list
+    parents: list
+    depths: list
+    scores: list = field(default_factory=list)
+
+    def children(self, node):
+        return [i for i, p in enumerate(self.parents) if p == node]
+
+    def ancestors_including_self(self, node):
+        out = [node]
+        p = self.parents[node]
+        while p >= 0:
+            out.append(p)
+            p = self.parents[p]
+        return out[::-1]
+
+    @property
+    def node_count(self):
+        return len(self.tokens)
+
+
+def dense_topology(topk_by_depth, budget):
+    """Parent/depth/rank arrays of the dense BFS tree, truncated at ``budget``.
+
+    Node order is parent-major then candidate-rank, as assembled by
+    ``flashgrpo/decoding/medusa_tree.py:254-277``. ``rank[n]`` is the index of the
+    candidate that node ``n`` takes from its depth's top-k list.
+    """
+    parents, depths, ranks = [-1], [1], [0]
+    frontier = [0]
+    for d, k in enumerate(topk_by_depth):
+        if k <= 0:
+            break
+        nxt = []
+        stop = False
+        for p in frontier:
+            for r in range(int(k)):
+                parents.append(p)
+                depths.append(d + 2)
+                ranks.append(r)
+                nxt.append(len(parents) - 1)
+                if len(parents) >= budget:
+                    stop = True
+                    break
+            if stop:
+                break
+        frontier = nxt
+        if not frontier or len(parents) >= budget:
+            break
+    return parents, depths, ranks
+
+
+def build_batch_trees(roots, medusa_logits, plan: Plan):
+    """Dense candidate trees for a batch.
+
+    Follows ``flashgrpo/decoding/medusa_tree.py:228-278`` with the canonical
+    top-k tie order. ``medusa_logits`` is a list (one per head) of [B, V] arrays.
+    """
+    roots = [int(r) for r in roots]
+    cands = []
+    for d, k in enumerate(plan.topk_by_depth[: plan.active_heads]):
+        if d >= len(medusa_logits):
+            break
+        lg = np.asarray(medusa_logits[d], dtype=np.float32)
+        k = min(max(0, int(k)), lg.shape[-1])
+        if k <= 0:
+            break
+        cands.append([topk_canonical(lg[b], k) for b in range(lg.shape[0])])
+    trees = []
+    for b, root in enumerate(roots):
+        toks, pars, deps, scs = [root], [-1], [1], [0.0]
+        frontier = [0]
+        for d, rows in enumerate(cands):
+            ids, vals = rows[b]
+            nxt = []
+            full = False
+            for p in frontier:
+                for t, s in zip(ids.tolist(), vals.tolist()):
+                    toks.append(int(t))
+                    pars.append(p)
+                    deps.append(d + 2)
+                    scs.append(float(s))
+                    nxt.append(len(toks) - 1)
+                    if len(toks) >= plan.node_budget_per_seq:
+                        full = True
+                        break
+                if full:
+                    break
+            frontier = nxt
+            if not frontier or len(toks) >= plan.node_budget_per_seq:
+                break
+        trees.append(Tree(toks, pars, deps, scs))
+    return trees
+
+
+def build_dense_tree(root, medusa_logits_row, plan: Plan) -> Tree:
+    """Single-row tree. Follows ``flashgrpo/decoding/medusa_tree.py:200-225``."""
+    return build_batch_trees([root], [np.asarray(r)[None] for r in medusa_logits_row], plan)[0]
+
+
+def tree_attention_inputs(trees, full_attention_mask, logical_lengths, *, pad_token_id, dtype=np.float32):
+    """Flattened ids, additive 4-D mask, positions and node mask.
+
+    Follows ``flashgrpo/decoding/tree_attention.py:6-67``: node n attends to valid
+    prefix slots and to its ancestors-or-self; padded query rows attend to
+    themselves; position = logical_len + depth - 1 (0 for padding).
+    """
+    full_attention_mask = np.asarray(full_attention_mask)
+    B = len(trees)
+    nmax = max(max(t.node_count, 1) for t in trees)
+    past = full_attention_mask.shape[1]
+    ids = np.full((B, nmax), int(pad_token_id), dtype=np.int64)
+    depth = np.ones((B, nmax), dtype=np.int64)
+    valid = np.zeros((B, nmax), dtype=bool)
+    allowed_tree = np.zeros((B, nmax, nmax), dtype=bool)
+    for b, t in enumerate(trees):
+        n = t.node_count
+        ids[b, :n] = t.tokens
+        depth[b, :n] = t.depths
+        valid[b, :n] = True
+        for i in range(n):
+            for a in t.ancestors_including_self(i):
+                allowed_tree[b, i, a] = True
+        for i in range(n, nmax):
+            allowed_tree[b, i, i] = True
+    pos = np.asarray(logical_lengths, dtype=np.int64)[:, None] + depth - 1
+    pos[~valid] = 0
+    prefix = np.broadcast_to(full_attention_mask.astype(bool)[:, None, :], (B, nmax, past))
+    allowed = np.concatenate([prefix, allowed_tree], axis=-1)
+    dt = np.dtype(dtype)
+    mask = np.where(allowed, 0.0, MASK_MIN[dt]).astype(dt)[:, None]
+    return ids, mask, pos, valid
+
+
+def internal_slots(trees):
+    """Packed LM-head slot of each node that has children (-1 for leaves).
+
+    Follows ``flashgrpo/decoding/flash_medusa_decoder.py:391-412``: slots are
+    numbered row-major over (row, node).
+    """
+    nmax = max((t.node_count for t in trees), default=1)
+    slots = [[-1] * nmax for _ in trees]
+    rows, nodes = [], []
+    for b, t in enumerate(trees):
+        for n in range(t.node_count):
+            if t.children(n):
+                slots[b][n] = len(rows)
+                rows.append(b)
+                nodes.append(n)
+    return rows, nodes, slots
+
+
+def ancestor_bits(parents):
+    """64-bit ancestor-or-self mask of every node (bit m set if node m is on the path)."""
+    out = []
+    for n in range(len(parents)):
+        m, p = 1 << n, parents[n]
+        while p >= 0:
+            m |= 1 << p
+            p = parents[p]
+        out.append(m)
+    return out

@@ -1,0 +1,160 @@
+"""Pins the oracle's planner, canonical top-k, tree builder and attention inputs.
+
+Pins: the reference's own test inputs/known answers (tests/golden, built by
+tests/golden/make_golden.py), hand-derived planner tables, the dense-count closed
+form, torch.topk on tie-free data, and brute force on tiny trees.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import tree as T
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+CASES = json.load(open(os.path.join(GOLD, "reference_cases.json")))
+ARR = np.load(os.path.join(GOLD, "reference_arrays.npz"))
+
+
+def test_dense_node_count_closed_form():
+    rng = np.random.default_rng(0)
+    for _ in range(200):
+        ks = rng.integers(1, 6, size=rng.integers(0, 5)).tolist()
+        brute = 1 + sum(int(np.prod(ks[: i + 1])) for i in range(len(ks)))
+        assert T.dense_node_count(ks) == brute
+        parents, depths, _ = T.dense_topology(ks, 10 ** 6)
+        assert len(parents) == brute
+
+
+@pytest.mark.parametrize("case", CASES["planner"], ids=lambda c: str(c["kw"]["active_batch_size"]) + c["kw"]["tree_mode"])
+def test_plan_tree_matches_hand_derived_table(case):
+    p = T.plan_tree(**case["kw"])
+    for k, v in case["expect"].items():
+        assert getattr(p, k) == v, (k, getattr(p, k), v)
+
+
+def test_reference_planner_properties():
+    # flashgrpo/tests/test_flashgrpo_smoke.py:4-45
+    small, large = (T.plan_tree(**c["kw"]) for c in CASES["planner"][:2])
+    assert small.actual_nodes >= large.actual_nodes
+    adaptive = T.plan_tree(**CASES["planner"][2]["kw"])
+    assert adaptive.node_budget_per_seq == 4 and adaptive.active_heads == 3
+
+
+@pytest.mark.parametrize("case", CASES["fit"])
+def test_fit_topk_to_budget(case):
+    out = T.fit_topk_to_budget(case["topk"], case["budget"], min_topk_by_depth=case["mins"],
+                               depth_weight_decay=case["decay"])
+    assert out == case["expect"]
+    assert T.dense_node_count(out) <= max(1, case["budget"])
+
+
+def test_fit_never_exceeds_budget_and_is_maximal_per_depth():
+    rng = np.random.default_rng(1)
+    for _ in range(300):
+        ks = rng.integers(1, 6, size=rng.integers(1, 5)).tolist()
+        budget = int(rng.integers(1, 80))
+        out = T.fit_topk_to_budget(ks, budget)
+        assert T.dense_node_count(out) <= budget
+        assert len(out) <= len(ks) and all(1 <= o <= k for o, k in zip(out, ks))
+
+
+def test_seed7_batched_trees_match_torch_topk_golden():
+    # flashgrpo/tests/test_reflex_optimized.py:16-36 (expected from torch.topk + BFS)
+    case = CASES["seed7_tree"]
+    roots = ARR["seed7_roots"]
+    logits = list(ARR["seed7_logits"])
+    plan = T.Plan(case["budget"], 2, case["topk"], 10, "fixed", "dense")
+    trees = T.build_batch_trees(roots, logits, plan)
+    assert [(t.tokens, t.parents) for t in trees] == [(g["tokens"], g["parents"]) for g in case["trees"]]
+    per_row = [T.build_dense_tree(roots[b], [lg[b] for lg in logits], plan) for b in range(len(roots))]
+    assert [(t.tokens, t.parents) for t in trees] == [(t.tokens, t.parents) for t in per_row]
+
+
+def test_canonical_topk_tie_order_and_signed_zero():
+    x = np.array([1.0, 3.0, 3.0, -0.0, 0.0, 3.0, 2.0], np.float32)
+    idx, vals = T.topk_canonical(x, 5)
+    assert idx.tolist() == [1, 2, 5, 6, 0]
+    idx, _ = T.topk_canonical(np.array([-0.0, 0.0, -1.0], np.float32), 2)
+    assert idx.tolist() == [0, 1]
+    # bf16-style heavy ties: order must equal a stable descending sort
+    rng = np.random.default_rng(3)
+    y = np.round(rng.standard_normal(4000) * 4).astype(np.float32)
+    ref = np.argsort(-y.astype(np.float64), kind="stable")[:17]
+    assert T.topk_canonical(y, 17)[0].tolist() == ref.tolist()
+
+
+def test_topology_matches_built_trees_and_truncation():
+    rng = np.random.default_rng(5)
+    for ks, budget in [([4, 2], 16), ([4, 2, 1, 1], 32), ([4, 3, 2], 16), ([3, 3, 3], 20), ([2], 2)]:
+        B, V = 3, 50
+        logits = [rng.standard_normal((B, V)).astype(np.float32) for _ in ks]
+        plan = T.Plan(budget, len(ks), ks, T.dense_node_count(ks), "fixed", "dense")
+        trees = T.build_batch_trees(rng.integers(0, V, B), logits, plan)
+        parents, depths, ranks = T.dense_topology(ks, budget)
+        for b, t in enumerate(trees):
+            assert t.parents == parents and t.depths == depths
+            assert t.node_count == min(budget, T.dense_node_count(ks))
+            for n in range(1, t.node_count):
+                cand = T.topk_canonical(logits[depths[n] - 2][b], ks[depths[n] - 2])[0]
+                assert t.tokens[n] == cand[ranks[n]]
+
+
+def test_mask_known_answer():
+    # flashgrpo/tests/test_tree_attention_equivalence.py:9-20
+    c = CASES["mask"]
+    tree = T.Tree(c["tokens"], c["parents"], c["depths"])
+    ids, mask, pos, valid = T.tree_attention_inputs([tree], np.ones((1, c["past"]), np.int64),
+                                                    np.array([c["logical"]]), pad_token_id=0)
+    n, past = c["node"], c["past"]
+    assert valid[0, n]
+    for a in c["allowed_tree"]:
+        assert mask[0, 0, n, past + a] == 0
+    for a in c["masked_tree"]:
+        assert mask[0, 0, n, past + a] < -1e20
+    assert pos[0, n] == c["position"]
+
+
+def test_mask_brute_force_and_padding_rows():
+    trees = [T.Tree([1, 2, 3], [-1, 0, 1], [1, 2, 3]), T.Tree([4, 5, 6, 7, 8], [-1, 0, 0, 1, 2], [1, 2, 2, 3, 3])]
+    full = np.array([[0, 1, 1, 1], [1, 1, 1, 1]])
+    ids, mask, pos, valid = T.tree_attention_inputs(trees, full, full.sum(-1), pad_token_id=9)
+    assert ids[0].tolist() == [1, 2, 3, 9, 9] and valid[0].tolist() == [True] * 3 + [False] * 2
+    assert pos[0].tolist() == [3, 4, 5, 0, 0] and pos[1].tolist() == [4, 5, 5, 6, 6]
+    for b, t in enumerate(trees):
+        for n in range(5):
+            for m in range(5):
+                if n < t.node_count:
+                    want = m < t.node_count and m in t.ancestors_including_self(n)
+                else:
+                    want = m == n
+                assert (mask[b, 0, n, 4 + m] == 0) == want
+            assert ((mask[b, 0, n, :4] == 0) == full[b].astype(bool)).all()
+
+
+def test_internal_slots_match_reference_packed_layout():
+    # slot map of flashgrpo/tests/test_exact_acceptance_distribution.py:59-60
+    c = CASES["acceptance"]["packed"]
+    trees = [T.Tree(t["tokens"], t["parents"], [0] * 4) for t in c["trees"]]
+    rows, nodes, slots = T.internal_slots(trees)
+    assert slots == c["slots"] and rows == [0, 0, 1, 1] and nodes == [0, 1, 0, 2]
+
+
+def test_ancestor_bits():
+    parents = T.dense_topology([4, 2, 1, 1], 32)[0]
+    bits = T.ancestor_bits(parents)
+    t = T.Tree([0] * len(parents), parents, [0] * len(parents))
+    for n, m in enumerate(bits):
+        assert sorted(i for i in range(64) if m >> i & 1) == t.ancestors_including_self(n)
+
+
+def test_adaptive_confidence_mapping():
+    kw = dict(enabled=True, min_topk_by_depth=[1, 1, 1], low=0.15, high=0.45)
+    assert T.topk_from_confidence(0.01, 4, 0, **kw) == 4
+    assert T.topk_from_confidence(0.9, 4, 0, **kw) == 1
+    assert T.topk_from_confidence(0.25, 4, 0, **kw) == 3
+    assert T.topk_from_confidence(0.42, 4, 0, **kw) == 1
+    assert T.topk_from_confidence(float("nan"), 4, 0, **kw) == 1
+    assert T.topk_from_confidence(0.3, 4, 0, **dict(kw, enabled=False)) == 4
+    assert T.quantile_linear([0.1, 0.2, 0.3, 0.4], 0.25) == pytest.approx(0.175)
