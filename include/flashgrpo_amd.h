@@ -1,0 +1,149 @@
+/* flashgrpo_amd: C ABI of the MI355X (gfx950) speculative-rollout kernels.
+ *
+ * Every entry point is stream-ordered and asynchronous: device pointers in,
+ * device pointers out, `stream` is a hipStream_t (torch's current stream when
+ * called from Python). Nothing here allocates device memory; scratch space is a
+ * caller-provided `workspace`. Return value: 0 on success, <0 on error, with a
+ * message from fg_last_error() (thread-local). Shapes are validated on the host
+ * before any launch; index data that only exists on the device is bounds-checked
+ * in the kernel and reported through an `err_flag` word (0 = ok).
+ *
+ * dtype codes: 0 = fp32, 1 = bf16. Token ids and indices are int32.
+ *
+ * Reference interfaces replaced (ihbkaiser/ss-GRPO, flashgrpo/):
+ *   fg_medusa_heads     models/medusa_heads.py:74-78 (project_hidden),
+ *                       decoding/flash_medusa_decoder.py:254-294
+ *   fg_lm_head          decoding/flash_medusa_decoder.py:289-294, 414-433, 1079-1091
+ *   fg_medusa_topk      decoding/medusa_tree.py:239-252 (per-depth torch.topk),
+ *                       decoding/flash_medusa_decoder.py:320-339 (confidences)
+ *   fg_tree_layout      decoding/medusa_tree.py:254-277 (BFS token assembly)
+ *   fg_rope_kv_write    models/qwen_flashgrpo_wrapper.py:172-180 (HF rotary + DynamicCache.update)
+ *   fg_tree_attention   decoding/tree_attention.py:6-67 + the HF attention it feeds
+ *   fg_rmsnorm, fg_swiglu  models/qwen_flashgrpo_wrapper.py:172-180 (HF decoder layer)
+ *   fg_sample_tokens    decoding/acceptance.py:34-130 (sample_from_logits)
+ *   fg_accept_walk      decoding/acceptance.py:179-260 (exact_accept_paths_batch);
+ *                       flashgrpo_b200/decoding/acceptance.py:184-267 (correction tokens)
+ *   fg_accept_finalize  decoding/flash_medusa_decoder.py:899-922;
+ *                       flashgrpo_b200/decoding/flash_medusa_decoder.py:2303-2319
+ *   fg_kv_path_gather   decoding/kv_extraction.py:87-218 (extract_accepted_path_kv)
+ */
+#ifndef FLASHGRPO_AMD_H
+#define FLASHGRPO_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Last error message of the calling thread ("" if none). */
+const char* fg_last_error(void);
+int fg_version(void);
+
+/* Medusa residual block for `heads` heads:
+ *   out[h*batch + b, :] = hidden[b] + SiLU(fc_w[h] . LayerNorm_h(hidden[b]) + fc_b[h])
+ * hidden [batch, H] (row stride ldh), ln_w/ln_b [heads, H] fp32, fc_w [heads, H, H],
+ * fc_b [heads, H] in `dtype`; out [heads*batch, H] in out_dtype.
+ * workspace >= fg_medusa_heads_workspace(batch, H, heads, dtype) bytes. */
+size_t fg_medusa_heads_workspace(int batch, int hidden, int heads, int dtype);
+int fg_medusa_heads(const void* hidden, int dtype, int batch, int H, int64_t ldh, int heads, const float* ln_w,
+                    const float* ln_b, float ln_eps, const void* fc_w, const void* fc_b, void* out, int out_dtype,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Tied LM-head projection: out[m, :] = x[row_index ? row_index[m] : m, :] . w^T
+ * x [*, K] (row stride ldx), w [N, K] (row stride ldw), out [M, N] (row stride ldo).
+ * bf16 requires K % 64 == 0 and 16-byte aligned rows. */
+int fg_lm_head(const void* x, int dtype, int M, int K, int64_t ldx, const int32_t* row_index, const void* w,
+               int64_t ldw, int N, void* out, int out_dtype, int64_t ldo, void* stream);
+
+/* Per-row top-kmax candidates, ranked (value desc, index asc).
+ * logits [rows, vocab] with row stride row_stride (multiple of 8, 32-byte aligned base).
+ * cand_tokens/cand_scores [rows, kmax]; row_stats (optional) [rows, 2] = (max, logsumexp).
+ * workspace >= fg_medusa_topk_workspace(rows, vocab, kmax). */
+size_t fg_medusa_topk_workspace(int rows, int vocab, int kmax);
+int fg_medusa_topk(const void* logits, int dtype, int64_t row_stride, int rows, int vocab, int kmax,
+                   int32_t* cand_tokens, float* cand_scores, float* row_stats, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* Dense-tree tokens: tree_tokens[b, 0] = roots[b]; for n >= 1
+ * tree_tokens[b, n] = cand_tokens[(node_depth[n]-2)*batch + b, node_rank[n]].
+ * node_depth/node_rank [num_nodes] describe the plan's BFS topology. */
+int fg_tree_layout(const int32_t* cand_tokens, const float* cand_scores, int kstride, int batch,
+                   const int32_t* roots, const int32_t* node_depth, const int32_t* node_rank, int num_nodes,
+                   int32_t* tree_tokens, float* tree_scores, int out_stride, void* stream);
+
+/* Rotary embedding of q and k for num_nodes new tokens per sequence, and the
+ * K/V write into cache slots seq_len[b] + n. qkv [batch*num_nodes, (Hq+2Hkv)*d]
+ * (row stride ld_qkv); position = seq_len[b] + pos_offset[n]; inv_freq [d/2] fp32;
+ * q_out [batch, num_nodes, Hq, d]; caches [Bc, Hkv, capacity, d]; row_map maps b to
+ * its cache row (NULL = identity). */
+int fg_rope_kv_write(const void* qkv, int dtype, int64_t ld_qkv, int batch, int num_nodes, int q_heads, int kv_heads,
+                     int head_dim, const int32_t* seq_len, const int32_t* pos_offset, const float* inv_freq,
+                     void* q_out, void* k_cache, void* v_cache, int64_t cache_batch_stride,
+                     int64_t cache_head_stride, const int32_t* row_map, void* stream);
+
+/* Tree attention: node n of sequence b attends to cache keys [0, seq_len[b]) and to
+ * tree keys seq_len[b] + m for every bit m of anc[b*anc_batch_stride + n].
+ * q/out [batch, num_nodes, Hq, d]; num_nodes <= 64; bf16 needs d == 128. */
+int fg_tree_attention(const void* q, void* out, const void* k_cache, const void* v_cache, int dtype, int batch,
+                      int num_nodes, int q_heads, int kv_heads, int head_dim, int64_t cache_batch_stride,
+                      int64_t cache_head_stride, int capacity, const int32_t* seq_len, const int32_t* row_map,
+                      const uint64_t* anc, int64_t anc_batch_stride, float scale, void* stream);
+
+/* y = RMSNorm(x [+ delta]) * weight over rows of `hidden`; with delta, x += delta first. */
+int fg_rmsnorm(void* x, const void* delta, const void* weight, void* y, int dtype, int rows, int hidden, float eps,
+               void* stream);
+/* out[t, i] = SiLU(gate_up[t, i]) * gate_up[t, inter + i] */
+int fg_swiglu(const void* gate_up, void* out, int dtype, int rows, int inter, void* stream);
+
+/* One supplied-noise draw per row (rule documented in csrc/sample.hip).
+ * Row r reads logits row row_index ? row_index[r] : r. forced (optional): a value
+ * >= 0 is emitted instead of sampling. Noise: noise[r*noise_stride + noise_col]
+ * when noise != NULL, else counter noise (seed, step, seq_ids ? seq_ids[r] : r, draw).
+ * greedy or temperature == 0: argmax (first maximum). top_k <= 0: off.
+ * top_p_fixed = floor(top_p * 2^32), 0 = off. */
+int fg_sample_tokens(const void* logits, int dtype, int64_t row_stride, int rows, int vocab,
+                     const int32_t* row_index, const int32_t* forced, const uint32_t* noise, int noise_stride,
+                     int noise_col, uint64_t seed, uint64_t step, const int32_t* seq_ids, int draw,
+                     float temperature, int greedy, int top_k, uint32_t top_p_fixed, int32_t* out_tokens,
+                     void* stream);
+
+/* exact_target acceptance walk over `batch` trees (one launch per walk step).
+ * Node n of tree b: tree_tokens/parents[b*nmax + n], n < n_nodes[b], root = node 0.
+ * Logits of node n: row slot_map[b*nmax + n] of tree_logits (packed internal nodes),
+ * or row b*nmax + n when slot_map is NULL (dense). Walk step t (0-based) draws
+ * noise[b*noise_stride + noise_col0 + t] or counter noise with draw index draw0 + t.
+ * Outputs: acc_tokens/acc_nodes [batch, acc_stride], acc_len, last_node, correction
+ * (the unmatched sample, -1 if none). workspace: 2*batch int32. err_flag bits:
+ * 2 = a walked node had no logits row, 4 = acc_stride too small. */
+int fg_accept_walk(const void* tree_logits, int dtype, int64_t row_stride, int vocab, const int32_t* slot_map,
+                   const int32_t* tree_tokens, const int32_t* parents, const int32_t* n_nodes, int nmax, int batch,
+                   int max_walk_steps, const uint32_t* noise, int noise_stride, int noise_col0, uint64_t seed,
+                   uint64_t step, const int32_t* seq_ids, int draw0, float temperature, int greedy, int top_k,
+                   uint32_t top_p_fixed, int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len,
+                   int32_t* last_node, int32_t* correction, int32_t* workspace, int32_t* err_flag, void* stream);
+
+/* Length clamp (max(1, max_length - old_len)), EOS cut (eos_token_id < 0: none),
+ * finished flags and, when pending_root != NULL, the next round's forced root
+ * (the correction token if the whole raw path was kept and the row continues). */
+int fg_accept_finalize(const int32_t* acc_tokens, const int32_t* acc_nodes, int acc_stride, int32_t* acc_len,
+                       int32_t* last_node, const int32_t* correction, const int32_t* old_len, int max_length,
+                       int eos_token_id, int32_t* finished, int32_t* pending_root, int batch, void* stream);
+
+/* Accepted-path compaction for all layers in one launch: for each of num_tensors
+ * cache tensors (device array tensor_ptrs, e.g. K0,V0,K1,V1,...) laid out
+ * [Bc, kv_heads, capacity, head_dim] with the given element strides, moves rows
+ * seq_len[b] + acc_nodes[b, j] to seq_len[b] + j for j < acc_len[b]. All sources
+ * are read before any destination is written. Does not modify seq_len.
+ * err_flag bit 1: a node index was outside [0, tree_nodes) (that row is skipped). */
+int fg_kv_path_gather(const uint64_t* tensor_ptrs, int num_tensors, int batch, int kv_heads, int head_dim,
+                      int elem_bytes, int64_t batch_stride, int64_t head_stride, int64_t row_stride, int capacity,
+                      const int32_t* seq_len, const int32_t* row_map, const int32_t* acc_nodes, int acc_stride,
+                      const int32_t* acc_len, int tree_nodes, int32_t* err_flag, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHGRPO_AMD_H */

@@ -118,7 +118,7 @@ def sample_row(x, u32, *, do_sample=True, temperature=1.0, top_p=1.0, top_k=None
     qk = np.where(keep, q, np.uint64(0))
     total = int(qk.sum(dtype=np.uint64))
     if total == 0:
-        return int(np.argmax(s))
+        return int(np.argmax(np.asarray(x, F32)))
     target = (total * (int(u32) & 0xFFFFFFFF)) >> 32
     cum = np.cumsum(qk, dtype=np.uint64)
     return int(np.argmax(cum > np.uint64(target)))

@@ -1,0 +1,294 @@
+// Tree-verify attention over the cached prefix plus the candidate tree.
+//
+// Query node n of sequence b (all q heads of one KV head, GQA) attends to the
+// committed prefix keys [0, seq_len[b]) and to tree keys seq_len[b] + m for
+// every node m whose bit is set in the node's 64-bit ancestor-or-self mask.
+// The mask is applied to the scores in registers; no [B, 1, N, P+N] float mask
+// is built (replaces flashgrpo/decoding/tree_attention.py:6-67 feeding the HF
+// decoder's eager/SDPA attention, flashgrpo/models/qwen_flashgrpo_wrapper.py:172-180).
+//
+// bf16 path, one workgroup per (sequence, kv head, 256-row query tile):
+//  * the query tile is the G*N rows (n-major, G = q heads per kv head) of one
+//    KV head, so every K/V tile loaded from HBM serves all of them;
+//  * 8 waves, 32 query rows each; S^T = K Q^T with v_mfma_f32_32x32x16_bf16
+//    (keys on the M side) puts one query per lane, so the online-softmax row
+//    max / sum are per-lane values plus one exchange with lane^32;
+//  * O^T += V^T P^T: P^T is fed straight from the S^T accumulators (bf16) as
+//    the B operand, V is transposed into LDS while staging so the A operand
+//    reads two 8-byte runs per lane in the same key order as P^T.
+// fp32 path: one wave per query row, exact online softmax in fp32.
+#include "fg_common.h"
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+struct AttnArgs {
+  const void* q;          // [B, N, Hq, d]
+  void* out;              // [B, N, Hq, d]
+  const void* k;          // layer K cache base [Bc, Hkv, Smax, d]
+  const void* v;
+  int64_t cache_batch;    // elements
+  int64_t cache_head;
+  int capacity;           // Smax
+  const int32_t* seq_len;
+  const int32_t* row_map;
+  const uint64_t* anc;    // [anc_batch_stride * B + N] ancestor masks
+  int64_t anc_stride;     // 0 when all rows share one topology
+  int N, Hq, Hkv, d;
+  float scale;
+};
+
+constexpr int kD = 128;       // head dim of the MFMA path
+constexpr int kKT = 64;       // keys per tile
+constexpr int kWavesA = 8;
+constexpr int kRowsTile = kWavesA * 32;
+constexpr int kKPitch = kD + 8;    // bf16 elements per K row in LDS
+constexpr int kVPitch = kKT + 8;   // bf16 elements per V^T row in LDS
+constexpr float kNegBig = -1.0e30f;
+
+FG_DEVICE int c_row32(int i, int lane) { return (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3); }
+
+__global__ void __launch_bounds__(kWavesA * 64) tree_attn_bf16_kernel(AttnArgs a, int m_tiles) {
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kKT * kKPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[kD * kVPitch];
+
+  const int mt = blockIdx.x % m_tiles;
+  const int hkv = (blockIdx.x / m_tiles) % a.Hkv;
+  const int b = blockIdx.x / (m_tiles * a.Hkv);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5;
+  const int G = a.Hq / a.Hkv;
+  const int M = G * a.N;
+  const int s0 = a.seq_len[b];
+  const int total = s0 + a.N;
+  const int cb = a.row_map ? a.row_map[b] : b;
+  const uint16_t* kbase = (const uint16_t*)a.k + (int64_t)cb * a.cache_batch + (int64_t)hkv * a.cache_head;
+  const uint16_t* vbase = (const uint16_t*)a.v + (int64_t)cb * a.cache_batch + (int64_t)hkv * a.cache_head;
+
+  // This lane's query row (column of S^T).
+  const int r = mt * kRowsTile + wave * 32 + (lane & 31);
+  const bool row_ok = r < M;
+  const int qn = row_ok ? r / G : 0;
+  const int qh = hkv * G + (row_ok ? r % G : 0);
+  const uint64_t anc = row_ok ? a.anc[(int64_t)b * a.anc_stride + qn] : 1ull;
+
+  // Q^T fragments: step s covers d = s*16 + g*8 .. +8.
+  bf16x8 qf[kD / 16];
+  {
+    const uint16_t* qrow = (const uint16_t*)a.q + (((int64_t)b * a.N + qn) * a.Hq + qh) * kD;
+#pragma unroll
+    for (int s = 0; s < kD / 16; ++s) {
+      uint4 w = row_ok ? *(const uint4*)(qrow + s * 16 + g * 8) : make_uint4(0, 0, 0, 0);
+      qf[s] = __builtin_bit_cast(bf16x8, w);
+    }
+  }
+
+  floatx16 o[kD / 32];
+#pragma unroll
+  for (int db = 0; db < kD / 32; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
+  float m_run = kNegBig, l_run = 0.0f;
+  const float sl2 = a.scale * 1.44269504088896341f;
+
+  // Staging: 512 threads, K tile 64 x 128 bf16 = 1024 chunks of 16 B (2 per
+  // thread), same for V.
+  auto load_tile = [&](int key0, uint4 (&rk)[2], uint4 (&rv)[2]) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      int idx = tid + c * 512;
+      int kr = idx >> 4, col = (idx & 15) * 8;
+      int key = min(key0 + kr, total - 1);
+      key = min(key, a.capacity - 1);
+      rk[c] = *(const uint4*)(kbase + (int64_t)key * kD + col);
+      rv[c] = *(const uint4*)(vbase + (int64_t)key * kD + col);
+    }
+  };
+  auto store_tile = [&](const uint4 (&rk)[2], const uint4 (&rv)[2]) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      int idx = tid + c * 512;
+      int kr = idx >> 4, col = (idx & 15) * 8;
+      *(uint4*)&Ks[kr * kKPitch + col] = rk[c];
+      uint32_t w[4] = {rv[c].x, rv[c].y, rv[c].z, rv[c].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        Vt[(col + 2 * e) * kVPitch + kr] = (uint16_t)(w[e] & 0xffffu);
+        Vt[(col + 2 * e + 1) * kVPitch + kr] = (uint16_t)(w[e] >> 16);
+      }
+    }
+  };
+
+  uint4 rk[2], rv[2];
+  load_tile(0, rk, rv);
+  const int ntiles = (total + kKT - 1) / kKT;
+  for (int t = 0; t < ntiles; ++t) {
+    const int key0 = t * kKT;
+    __syncthreads();
+    store_tile(rk, rv);
+    __syncthreads();
+    if (t + 1 < ntiles) load_tile(key0 + kKT, rk, rv);
+
+    // S^T for two 32-key blocks.
+    floatx16 st[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) st[kb][i] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < kD / 16; ++s) {
+        bf16x8 kf = *(const bf16x8*)&Ks[(kb * 32 + (lane & 31)) * kKPitch + s * 16 + g * 8];
+        st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], st[kb], 0, 0, 0);
+      }
+    }
+    // Mask and scale (log2 domain), tile max.
+    float tmax = kNegBig;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        int key = key0 + kb * 32 + c_row32(i, lane);
+        bool ok;
+        if (key < s0) {
+          ok = true;
+        } else {
+          int m = key - s0;
+          ok = m < a.N && ((anc >> m) & 1ull);
+        }
+        float x = ok ? st[kb][i] * sl2 : kNegBig;
+        st[kb][i] = x;
+        tmax = fmaxf(tmax, x);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float m_new = fmaxf(m_run, tmax);
+    const float alpha = exp2f(m_run - m_new);
+    float psum = 0.0f;
+    bf16x8 pf[2][2];  // [kb][ks] B operand of P^T
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        uint32_t packed[4];
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          float p0 = st[kb][ks * 8 + j] <= kNegBig ? 0.0f : exp2f(st[kb][ks * 8 + j] - m_new);
+          float p1 = st[kb][ks * 8 + j + 1] <= kNegBig ? 0.0f : exp2f(st[kb][ks * 8 + j + 1] - m_new);
+          uint16_t h0 = fg::f32_to_bf16(p0), h1 = fg::f32_to_bf16(p1);
+          psum += fg::bf16_to_f32(h0) + fg::bf16_to_f32(h1);
+          packed[j / 2] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+        }
+        pf[kb][ks] = __builtin_bit_cast(bf16x8, make_uint4(packed[0], packed[1], packed[2], packed[3]));
+      }
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int db = 0; db < kD / 32; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+    // O^T += V^T P^T. Slot j of lane (g) holds key kb*32 + ks*16 + (j/4)*8 + g*4 + j%4.
+#pragma unroll
+    for (int db = 0; db < kD / 32; ++db) {
+      const uint16_t* vrow = &Vt[(db * 32 + (lane & 31)) * kVPitch];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          int kk = kb * 32 + ks * 16 + g * 4;
+          uint2 lo = *(const uint2*)(vrow + kk);
+          uint2 hi = *(const uint2*)(vrow + kk + 8);
+          bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[kb][ks], o[db], 0, 0, 0);
+        }
+    }
+  }
+  // Combine the two half-lanes' sums and write.
+  l_run += __shfl_xor(l_run, 32, 64);
+  const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+  if (row_ok) {
+    uint16_t* orow = (uint16_t*)a.out + (((int64_t)b * a.N + qn) * a.Hq + qh) * kD;
+#pragma unroll
+    for (int db = 0; db < kD / 32; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; i += 4) {
+        int d0 = db * 32 + c_row32(i, lane);
+        uint32_t w0 = (uint32_t)fg::f32_to_bf16(o[db][i] * inv) | ((uint32_t)fg::f32_to_bf16(o[db][i + 1] * inv) << 16);
+        uint32_t w1 = (uint32_t)fg::f32_to_bf16(o[db][i + 2] * inv) | ((uint32_t)fg::f32_to_bf16(o[db][i + 3] * inv) << 16);
+        *(uint2*)(orow + d0) = make_uint2(w0, w1);
+      }
+  }
+}
+
+// fp32: one wave per (sequence, node, q head); lane owns head dims lane, lane+64.
+__global__ void __launch_bounds__(64) tree_attn_f32_kernel(AttnArgs a) {
+  const int qh = blockIdx.x % a.Hq;
+  const int n = (blockIdx.x / a.Hq) % a.N;
+  const int b = blockIdx.x / (a.Hq * a.N);
+  const int lane = threadIdx.x;
+  const int G = a.Hq / a.Hkv, hkv = qh / G;
+  const int s0 = a.seq_len[b];
+  const int cb = a.row_map ? a.row_map[b] : b;
+  const float* kbase = (const float*)a.k + (int64_t)cb * a.cache_batch + (int64_t)hkv * a.cache_head;
+  const float* vbase = (const float*)a.v + (int64_t)cb * a.cache_batch + (int64_t)hkv * a.cache_head;
+  const float* qrow = (const float*)a.q + (((int64_t)b * a.N + n) * a.Hq + qh) * a.d;
+  const uint64_t anc = a.anc[(int64_t)b * a.anc_stride + n];
+  float q0 = lane < a.d ? qrow[lane] : 0.0f;
+  float q1 = lane + 64 < a.d ? qrow[lane + 64] : 0.0f;
+  float m = -INFINITY, l = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  const int total = s0 + a.N;
+  for (int key = 0; key < total; ++key) {
+    if (key >= s0) {
+      int mm = key - s0;
+      if (!((anc >> mm) & 1ull)) continue;
+    }
+    const float* kr = kbase + (int64_t)key * a.d;
+    float part = (lane < a.d ? q0 * kr[lane] : 0.0f) + (lane + 64 < a.d ? q1 * kr[lane + 64] : 0.0f);
+    float s = fg::wave_sum(part) * a.scale;
+    float m_new = fmaxf(m, s);
+    float alpha = expf(m - m_new);
+    float p = expf(s - m_new);
+    const float* vr = vbase + (int64_t)key * a.d;
+    l = l * alpha + p;
+    o0 = o0 * alpha + (lane < a.d ? p * vr[lane] : 0.0f);
+    o1 = o1 * alpha + (lane + 64 < a.d ? p * vr[lane + 64] : 0.0f);
+    m = m_new;
+  }
+  float* orow = (float*)a.out + (((int64_t)b * a.N + n) * a.Hq + qh) * a.d;
+  if (lane < a.d) orow[lane] = o0 / l;
+  if (lane + 64 < a.d) orow[lane + 64] = o1 / l;
+}
+
+}  // namespace
+
+extern "C" int fg_tree_attention(const void* q, void* out, const void* k_cache, const void* v_cache, int dtype,
+                                 int batch, int num_nodes, int q_heads, int kv_heads, int head_dim,
+                                 int64_t cache_batch_stride, int64_t cache_head_stride, int capacity,
+                                 const int32_t* seq_len, const int32_t* row_map, const uint64_t* anc,
+                                 int64_t anc_batch_stride, float scale, void* stream) {
+  FG_REQUIRE(q && out && k_cache && v_cache && seq_len && anc, "fg_tree_attention: null pointer");
+  FG_REQUIRE(batch > 0 && num_nodes > 0 && num_nodes <= 64, "fg_tree_attention: num_nodes must be in [1, 64]");
+  FG_REQUIRE(q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0, "fg_tree_attention: heads");
+  FG_REQUIRE(capacity >= num_nodes, "fg_tree_attention: capacity");
+  AttnArgs a;
+  a.q = q; a.out = out; a.k = k_cache; a.v = v_cache;
+  a.cache_batch = cache_batch_stride; a.cache_head = cache_head_stride; a.capacity = capacity;
+  a.seq_len = seq_len; a.row_map = row_map; a.anc = anc; a.anc_stride = anc_batch_stride;
+  a.N = num_nodes; a.Hq = q_heads; a.Hkv = kv_heads; a.d = head_dim; a.scale = scale;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == fg::kBF16) {
+    FG_REQUIRE(head_dim == kD, "fg_tree_attention: bf16 path supports head_dim 128");
+    FG_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)k_cache & 15) == 0 && ((uintptr_t)v_cache & 15) == 0 &&
+                   cache_head_stride % 8 == 0 && cache_batch_stride % 8 == 0,
+               "fg_tree_attention: 16-byte alignment");
+    int M = (q_heads / kv_heads) * num_nodes;
+    int m_tiles = (M + kRowsTile - 1) / kRowsTile;
+    hipLaunchKernelGGL(tree_attn_bf16_kernel, dim3(batch * kv_heads * m_tiles), dim3(kWavesA * 64), 0, s, a,
+                       m_tiles);
+  } else if (dtype == fg::kF32) {
+    FG_REQUIRE(head_dim <= 128, "fg_tree_attention: fp32 path supports head_dim <= 128");
+    hipLaunchKernelGGL(tree_attn_f32_kernel, dim3(batch * num_nodes * q_heads), dim3(64), 0, s, a);
+  } else {
+    return fg::fail("fg_tree_attention: dtype");
+  }
+  return fg::check_launch("fg_tree_attention");
+}

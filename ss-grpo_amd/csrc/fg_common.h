@@ -1,0 +1,212 @@
+// Shared device helpers for the flashgrpo_amd HIP kernels (gfx950 / CDNA4).
+//
+// bf16 storage is raw uint16_t; conversions use round-to-nearest-even, the
+// rounding torch applies when it casts fp32 to bf16.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#define FG_DEVICE __device__ __forceinline__
+
+namespace fg {
+
+enum Dtype : int { kF32 = 0, kBF16 = 1 };
+
+// ------------------------------------------------------------------ errors
+// Host-side error state (thread-local message, returned by fg_last_error).
+void set_error(const std::string& msg);
+int fail(const std::string& msg);          // sets the message, returns -1
+int check_launch(const char* what);        // hipGetLastError -> code
+
+#define FG_REQUIRE(cond, msg)              \
+  do {                                     \
+    if (!(cond)) return ::fg::fail(msg);   \
+  } while (0)
+
+inline int elem_bytes(int dtype) { return dtype == kBF16 ? 2 : 4; }
+
+// ------------------------------------------------------------------ bf16
+FG_DEVICE float bf16_to_f32(uint16_t u) { return __uint_as_float(((uint32_t)u) << 16); }
+
+FG_DEVICE uint16_t f32_to_bf16(float f) {
+  uint32_t b = __float_as_uint(f);
+  if ((b & 0x7f800000u) == 0x7f800000u && (b & 0x007fffffu)) return (uint16_t)((b >> 16) | 0x40);
+  b += 0x7fffu + ((b >> 16) & 1u);
+  return (uint16_t)(b >> 16);
+}
+
+template <int DT>
+FG_DEVICE float load_elem(const void* p, int64_t i) {
+  if constexpr (DT == kBF16)
+    return bf16_to_f32(((const uint16_t*)p)[i]);
+  else
+    return ((const float*)p)[i];
+}
+
+template <int DT>
+FG_DEVICE void store_elem(void* p, int64_t i, float v) {
+  if constexpr (DT == kBF16)
+    ((uint16_t*)p)[i] = f32_to_bf16(v);
+  else
+    ((float*)p)[i] = v;
+}
+
+// Load 8 consecutive elements starting at i (i a multiple of 8 and the row
+// base 16-byte aligned for bf16 / 32-byte aligned for fp32).
+template <int DT>
+FG_DEVICE void load8(const void* p, int64_t i, float (&v)[8]) {
+  if constexpr (DT == kBF16) {
+    uint4 r = *(const uint4*)((const uint16_t*)p + i);
+    uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[2 * j] = __uint_as_float(w[j] << 16);
+      v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+    }
+  } else {
+    float4 a = *(const float4*)((const float*)p + i);
+    float4 b = *(const float4*)((const float*)p + i + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+}
+
+// ------------------------------------------------------------------ ordering keys
+// Order-preserving uint32 key of a float: -0 maps to +0's key and every NaN to
+// the largest key, so (key desc, index asc) is a total order agreeing with <.
+FG_DEVICE uint32_t sort_key32(float f) {
+  if (f != f) return 0xffffffffu;
+  if (f == 0.0f) return 0x80000000u;
+  uint32_t b = __float_as_uint(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// Composite rank key: larger is better; unique per index.
+FG_DEVICE uint64_t rank_key(float f, uint32_t idx) {
+  return ((uint64_t)sort_key32(f) << 32) | (uint64_t)(0xffffffffu - idx);
+}
+FG_DEVICE uint32_t rank_key_index(uint64_t k) { return 0xffffffffu - (uint32_t)(k & 0xffffffffu); }
+FG_DEVICE float rank_key_value(uint64_t k) {
+  uint32_t key = (uint32_t)(k >> 32);
+  uint32_t b = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
+  return __uint_as_float(b);
+}
+
+// ------------------------------------------------------------------ exp_fg
+// Deterministic fp32 exp for t <= 0: Cody-Waite reduction with a split ln2 and
+// the Cephes expf minimax polynomial (S. L. Moshier, Cephes Math Library,
+// single/expf.c), evaluated with separately rounded multiplies and adds so that
+// the CPU oracle (numpy float32) reproduces every bit. Inputs below -64 (and
+// NaN) give 0.
+FG_DEVICE float exp_fg(float t) {
+#pragma clang fp contract(off)
+  if (!(t >= -64.0f)) return 0.0f;
+  float kf = rintf(t * 1.44269504088896341f);
+  float r = t - kf * 0.693359375f;
+  r = r - kf * -2.12194440e-4f;
+  float z = r * r;
+  float p = 1.9875691500e-4f;
+  p = p * r;
+  p = p + 1.3981999507e-3f;
+  p = p * r;
+  p = p + 8.3334519073e-3f;
+  p = p * r;
+  p = p + 4.1665795894e-2f;
+  p = p * r;
+  p = p + 1.6666665459e-1f;
+  p = p * r;
+  p = p + 5.0000001201e-1f;
+  float y = p * z;
+  y = y + r;
+  y = y + 1.0f;
+  int ki = (int)kf;
+  float scale = __uint_as_float((uint32_t)(ki + 127) << 23);
+  return y * scale;
+}
+
+// trunc(e * 2^40) as uint64, by exponent/mantissa arithmetic (exact).
+FG_DEVICE uint64_t quantize_q40(float e) {
+  uint32_t b = __float_as_uint(e);
+  int ex = (int)((b >> 23) & 0xff);
+  if (ex == 0) return 0;  // zero (exp_fg never returns subnormals)
+  uint64_t m = (uint64_t)((b & 0x7fffffu) | 0x800000u);
+  int sh = ex - 127 + 40 - 23;  // value = m * 2^sh
+  if (sh >= 0) return m << sh;
+  if (sh <= -24) return 0;
+  return m >> (-sh);
+}
+
+// floor(a * u / 2^32) for a < 2^64, u < 2^32.
+FG_DEVICE uint64_t mulhi_u64_u32(uint64_t a, uint32_t u) {
+  uint64_t hi = (a >> 32) * (uint64_t)u;
+  uint64_t lo = ((a & 0xffffffffull) * (uint64_t)u) >> 32;
+  return hi + lo;
+}
+
+// ------------------------------------------------------------------ counter noise
+// SplitMix64 output finalizer (Steele, Lea, Flood 2014).
+FG_DEVICE uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+// u32 noise keyed by (seed, step, sequence id, draw index).
+FG_DEVICE uint32_t counter_noise(uint64_t seed, uint64_t step, uint32_t seq, uint32_t draw) {
+  uint64_t key = ((step & 0xffffffffull) << 32) | ((uint64_t)(seq & 0xffffffu) << 8) | (draw & 0xffu);
+  return (uint32_t)(mix64(mix64(seed + 0x9E3779B97F4A7C15ull) ^ key) >> 32);
+}
+
+// ------------------------------------------------------------------ wave reductions
+FG_DEVICE float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+FG_DEVICE float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+FG_DEVICE uint64_t shfl_xor_u64(uint64_t v, int o) {
+  uint32_t lo = __shfl_xor((unsigned)(v & 0xffffffffu), o, 64);
+  uint32_t hi = __shfl_xor((unsigned)(v >> 32), o, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+FG_DEVICE uint64_t shfl_up_u64(uint64_t v, int o) {
+  uint32_t lo = __shfl_up((unsigned)(v & 0xffffffffu), o, 64);
+  uint32_t hi = __shfl_up((unsigned)(v >> 32), o, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+FG_DEVICE uint64_t shfl_u64(uint64_t v, int src) {
+  uint32_t lo = __shfl((unsigned)(v & 0xffffffffu), src, 64);
+  uint32_t hi = __shfl((unsigned)(v >> 32), src, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+FG_DEVICE uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += shfl_xor_u64(v, o);
+  return v;
+}
+FG_DEVICE uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint64_t w = shfl_xor_u64(v, o);
+    v = w > v ? w : v;
+  }
+  return v;
+}
+// Inclusive prefix sum across the 64 lanes.
+FG_DEVICE uint64_t wave_incl_scan_u64(uint64_t v) {
+  int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    uint64_t w = shfl_up_u64(v, o);
+    if (lane >= o) v += w;
+  }
+  return v;
+}
+
+}  // namespace fg

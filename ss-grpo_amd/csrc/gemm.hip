@@ -1,0 +1,348 @@
+// Dense contractions of the rollout step: the tied LM-head projection and the
+// Medusa residual block.
+//
+//   C[M, N] = epilogue(A[M, K] . B[N, K]^T)      (both operands K-contiguous)
+//
+// bf16 path: MFMA v_mfma_f32_32x32x16_bf16 tiles, LDS double buffering, fp32
+// accumulation, XCD-aware block order (consecutive tiles of one N column
+// stripe land on the same XCD so the weight stripe is read from HBM once and
+// reused from that XCD's L2 across the M tiles). fp32 path: LDS-tiled FMA
+// kernel used by the fp32 configuration.
+//
+// Replaces the lm_head calls of flashgrpo/decoding/flash_medusa_decoder.py:289-294,
+// 414-433, 1079-1091 and MedusaPredictionHead.project_hidden
+// (flashgrpo/models/medusa_heads.py:74-78).
+#include "fg_common.h"
+
+#include <algorithm>
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+enum Epilogue : int { kEpiNone = 0, kEpiMedusa = 1 };
+
+struct GemmArgs {
+  const void* A;
+  int64_t lda;
+  int64_t a_batch;
+  const int32_t* a_rows;  // optional row gather for A
+  const void* B;
+  int64_t ldb;
+  int64_t b_batch;
+  void* C;
+  int64_t ldc;
+  int64_t c_batch;
+  const void* bias;       // medusa: [N] per batch (dtype of B)
+  int64_t bias_batch;
+  const void* R;          // medusa residual [M, N] (dtype r_dtype)
+  int64_t ldr;
+  int64_t r_batch;
+  int r_dtype;
+  int M, N, K;
+};
+
+FG_DEVICE float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+template <int CDT, int BDT>
+FG_DEVICE void epilogue_store(const GemmArgs& g, int z, int m, int n, float acc, int epi) {
+  if (m >= g.M || n >= g.N) return;
+  float v = acc;
+  if (epi == kEpiMedusa) {
+    float b = fg::load_elem<BDT>(g.bias, z * g.bias_batch + n);
+    float r = g.r_dtype == fg::kBF16 ? fg::load_elem<fg::kBF16>(g.R, z * g.r_batch + (int64_t)m * g.ldr + n)
+                                     : fg::load_elem<fg::kF32>(g.R, z * g.r_batch + (int64_t)m * g.ldr + n);
+    v = r + silu(v + b);
+  }
+  fg::store_elem<CDT>(g.C, z * g.c_batch + (int64_t)m * g.ldc + n, v);
+}
+
+// ----------------------------------------------------------------- bf16 MFMA
+constexpr int kBK = 64;
+constexpr int kPad = 8;  // bf16 elements of padding per LDS row (16 bytes)
+constexpr int kLdsRow = kBK + kPad;
+
+// Row of accumulator element i held by `lane` in a 32x32 MFMA output tile.
+FG_DEVICE int c_row32(int i, int lane) { return (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3); }
+
+template <int BM, int BN, int WM, int WN, int CDT>
+__global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs g, int epi, int tiles_m, int tiles_n) {
+  constexpr int WAVES_N = BN / WN;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int A_CHUNKS = BM * kBK / 8 / 256;  // 16-byte chunks per thread
+  constexpr int B_CHUNKS = BN * kBK / 8 / 256;
+  static_assert((BM / WM) * (BN / WN) == 4, "4 waves");
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kLdsRow];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * kLdsRow];
+
+  // XCD-aware tile order: blocks are dispatched round-robin over 8 XCDs; give
+  // each XCD a contiguous range of tiles, M fastest, so an N stripe of the
+  // weight is shared by tiles resident on one XCD.
+  const int nblocks = tiles_m * tiles_n;
+  const int bid = blockIdx.x;
+  const int q = nblocks / 8, rem = nblocks % 8;
+  const int xcd = bid % 8, local = bid / 8;
+  const int t = xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
+  const int tm = t % tiles_m, tn = t / tiles_m;
+  const int z = blockIdx.z;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+
+  const uint16_t* Ab = (const uint16_t*)g.A + z * g.a_batch;
+  const uint16_t* Bb = (const uint16_t*)g.B + z * g.b_batch;
+
+  // Per-thread global source rows (fixed across k tiles).
+  const uint16_t* a_src[A_CHUNKS];
+  int a_dst[A_CHUNKS];
+#pragma unroll
+  for (int c = 0; c < A_CHUNKS; ++c) {
+    int idx = tid + c * 256;
+    int r = idx / (kBK / 8), col = (idx % (kBK / 8)) * 8;
+    int m = min(m0 + r, g.M - 1);
+    int src_row = g.a_rows ? g.a_rows[m] : m;
+    a_src[c] = Ab + (int64_t)src_row * g.lda + col;
+    a_dst[c] = r * kLdsRow + col;
+  }
+  const uint16_t* b_src[B_CHUNKS];
+  int b_dst[B_CHUNKS];
+#pragma unroll
+  for (int c = 0; c < B_CHUNKS; ++c) {
+    int idx = tid + c * 256;
+    int r = idx / (kBK / 8), col = (idx % (kBK / 8)) * 8;
+    int n = min(n0 + r, g.N - 1);
+    b_src[c] = Bb + (int64_t)n * g.ldb + col;
+    b_dst[c] = r * kLdsRow + col;
+  }
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  uint4 ra[A_CHUNKS], rb[B_CHUNKS];
+  const int ktiles = g.K / kBK;
+  // prologue
+#pragma unroll
+  for (int c = 0; c < A_CHUNKS; ++c) ra[c] = *(const uint4*)(a_src[c]);
+#pragma unroll
+  for (int c = 0; c < B_CHUNKS; ++c) rb[c] = *(const uint4*)(b_src[c]);
+#pragma unroll
+  for (int c = 0; c < A_CHUNKS; ++c) *(uint4*)&As[0][a_dst[c]] = ra[c];
+#pragma unroll
+  for (int c = 0; c < B_CHUNKS; ++c) *(uint4*)&Bs[0][b_dst[c]] = rb[c];
+  __syncthreads();
+
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < ktiles;
+    if (more) {
+      const int koff = (kt + 1) * kBK;
+#pragma unroll
+      for (int c = 0; c < A_CHUNKS; ++c) ra[c] = *(const uint4*)(a_src[c] + koff);
+#pragma unroll
+      for (int c = 0; c < B_CHUNKS; ++c) rb[c] = *(const uint4*)(b_src[c] + koff);
+    }
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk) {
+      bf16x8 af[TM], bfr[TN];
+      const int kcol = kk * 16 + (lane >> 5) * 8;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        int r = wm * WM + i * 32 + (lane & 31);
+        af[i] = *(const bf16x8*)&As[cur][r * kLdsRow + kcol];
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        int r = wn * WN + j * 32 + (lane & 31);
+        bfr[j] = *(const bf16x8*)&Bs[cur][r * kLdsRow + kcol];
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) {
+#pragma unroll
+      for (int c = 0; c < A_CHUNKS; ++c) *(uint4*)&As[cur ^ 1][a_dst[c]] = ra[c];
+#pragma unroll
+      for (int c = 0; c < B_CHUNKS; ++c) *(uint4*)&Bs[cur ^ 1][b_dst[c]] = rb[c];
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        int m = m0 + wm * WM + i * 32 + c_row32(v, lane);
+        int n = n0 + wn * WN + j * 32 + (lane & 31);
+        epilogue_store<CDT, fg::kBF16>(g, z, m, n, acc[i][j][v], epi);
+      }
+}
+
+// ----------------------------------------------------------------- fp32 FMA
+template <int CDT>
+__global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs g, int epi) {
+  constexpr int T = 64, BKf = 16;
+  __shared__ float As[BKf][T + 1];
+  __shared__ float Bs[BKf][T + 1];
+  const int z = blockIdx.z;
+  const int m0 = blockIdx.y * T, n0 = blockIdx.x * T;
+  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+  const float* Ab = (const float*)g.A + z * g.a_batch;
+  const float* Bb = (const float*)g.B + z * g.b_batch;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < g.K; k0 += BKf) {
+    for (int e = threadIdx.x; e < T * BKf; e += 256) {
+      int r = e / BKf, kk = e % BKf;
+      int m = m0 + r, n = n0 + r, k = k0 + kk;
+      float av = 0.0f, bv = 0.0f;
+      if (m < g.M && k < g.K) {
+        int src = g.a_rows ? g.a_rows[m] : m;
+        av = Ab[(int64_t)src * g.lda + k];
+      }
+      if (n < g.N && k < g.K) bv = Bb[(int64_t)n * g.ldb + k];
+      As[kk][r] = av;
+      Bs[kk][r] = bv;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < BKf; ++kk) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = As[kk][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) epilogue_store<CDT, fg::kF32>(g, z, m0 + ty * 4 + i, n0 + tx * 4 + j, acc[i][j], epi);
+}
+
+int launch_gemm(const GemmArgs& g, int dtype, int out_dtype, int epi, int batch, hipStream_t s) {
+  FG_REQUIRE(g.M > 0 && g.N > 0 && g.K > 0 && batch > 0, "gemm: empty shape");
+  if (dtype == fg::kBF16) {
+    FG_REQUIRE(g.K % kBK == 0, "gemm: bf16 path needs K % 64 == 0");
+    FG_REQUIRE(g.lda % 8 == 0 && g.ldb % 8 == 0 && ((uintptr_t)g.A & 15) == 0 && ((uintptr_t)g.B & 15) == 0,
+               "gemm: bf16 operands need 16-byte aligned rows");
+    if (g.M <= 64) {
+      constexpr int BM = 64, BN = 128;
+      int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+      dim3 grid(tm * tn, 1, batch);
+      if (out_dtype == fg::kBF16)
+        hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, 32, 64, fg::kBF16>), grid, dim3(256), 0, s, g, epi, tm, tn);
+      else
+        hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, 32, 64, fg::kF32>), grid, dim3(256), 0, s, g, epi, tm, tn);
+    } else {
+      constexpr int BM = 128, BN = 128;
+      int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+      dim3 grid(tm * tn, 1, batch);
+      if (out_dtype == fg::kBF16)
+        hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, 64, 64, fg::kBF16>), grid, dim3(256), 0, s, g, epi, tm, tn);
+      else
+        hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, 64, 64, fg::kF32>), grid, dim3(256), 0, s, g, epi, tm, tn);
+    }
+  } else {
+    dim3 grid((g.N + 63) / 64, (g.M + 63) / 64, batch);
+    if (out_dtype == fg::kBF16)
+      hipLaunchKernelGGL(gemm_f32_kernel<fg::kBF16>, grid, dim3(256), 0, s, g, epi);
+    else
+      hipLaunchKernelGGL(gemm_f32_kernel<fg::kF32>, grid, dim3(256), 0, s, g, epi);
+  }
+  return fg::check_launch("gemm");
+}
+
+// LayerNorm of each row of h, once per Medusa head (affine per head).
+template <int HDT, int ODT>
+__global__ void __launch_bounds__(256) medusa_ln_kernel(const void* __restrict__ h, int64_t ldh, int H, int heads,
+                                                        int batch, const float* __restrict__ ln_w,
+                                                        const float* __restrict__ ln_b, float eps,
+                                                        void* __restrict__ out) {
+  const int b = blockIdx.x;
+  __shared__ float red[8];
+  float s = 0.0f;
+  for (int i = threadIdx.x; i < H; i += 256) s += fg::load_elem<HDT>(h, (int64_t)b * ldh + i);
+  s = fg::wave_sum(s);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  const float mean = (red[0] + red[1] + red[2] + red[3]) / (float)H;
+  __syncthreads();
+  float v = 0.0f;
+  for (int i = threadIdx.x; i < H; i += 256) {
+    float d = fg::load_elem<HDT>(h, (int64_t)b * ldh + i) - mean;
+    v += d * d;
+  }
+  v = fg::wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[4 + (threadIdx.x >> 6)] = v;
+  __syncthreads();
+  const float rstd = rsqrtf((red[4] + red[5] + red[6] + red[7]) / (float)H + eps);
+  for (int hd = 0; hd < heads; ++hd)
+    for (int i = threadIdx.x; i < H; i += 256) {
+      float x = (fg::load_elem<HDT>(h, (int64_t)b * ldh + i) - mean) * rstd;
+      fg::store_elem<ODT>(out, ((int64_t)hd * batch + b) * H + i, x * ln_w[hd * H + i] + ln_b[hd * H + i]);
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int fg_lm_head(const void* x, int dtype, int M, int K, int64_t ldx, const int32_t* row_index, const void* w,
+               int64_t ldw, int N, void* out, int out_dtype, int64_t ldo, void* stream) {
+  FG_REQUIRE(x && w && out, "fg_lm_head: null pointer");
+  FG_REQUIRE(dtype == fg::kF32 || dtype == fg::kBF16, "fg_lm_head: dtype");
+  GemmArgs g{};
+  g.A = x; g.lda = ldx; g.a_rows = row_index;
+  g.B = w; g.ldb = ldw;
+  g.C = out; g.ldc = ldo;
+  g.M = M; g.N = N; g.K = K;
+  return launch_gemm(g, dtype, out_dtype, kEpiNone, 1, (hipStream_t)stream);
+}
+
+size_t fg_medusa_heads_workspace(int batch, int hidden, int heads, int dtype) {
+  return (size_t)batch * hidden * heads * fg::elem_bytes(dtype) + 256;
+}
+
+// out[h*B + b, :] = hidden[b] + SiLU(fc_h(LayerNorm_h(hidden[b]))) for each head h.
+int fg_medusa_heads(const void* hidden, int dtype, int batch, int H, int64_t ldh, int heads, const float* ln_w,
+                    const float* ln_b, float ln_eps, const void* fc_w, const void* fc_b, void* out, int out_dtype,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  FG_REQUIRE(hidden && ln_w && ln_b && fc_w && fc_b && out && workspace, "fg_medusa_heads: null pointer");
+  FG_REQUIRE(batch > 0 && H > 0 && heads > 0, "fg_medusa_heads: empty shape");
+  FG_REQUIRE(dtype == fg::kF32 || dtype == fg::kBF16, "fg_medusa_heads: dtype");
+  FG_REQUIRE(workspace_bytes >= (size_t)batch * H * heads * fg::elem_bytes(dtype), "fg_medusa_heads: workspace");
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == fg::kBF16)
+    hipLaunchKernelGGL((medusa_ln_kernel<fg::kBF16, fg::kBF16>), dim3(batch), dim3(256), 0, s, hidden, ldh, H, heads,
+                       batch, ln_w, ln_b, ln_eps, workspace);
+  else
+    hipLaunchKernelGGL((medusa_ln_kernel<fg::kF32, fg::kF32>), dim3(batch), dim3(256), 0, s, hidden, ldh, H, heads,
+                       batch, ln_w, ln_b, ln_eps, workspace);
+  int rc = fg::check_launch("fg_medusa_heads(ln)");
+  if (rc) return rc;
+  GemmArgs g{};
+  g.A = workspace; g.lda = H; g.a_batch = (int64_t)batch * H;
+  g.B = fc_w; g.ldb = H; g.b_batch = (int64_t)H * H;
+  g.C = out; g.ldc = H; g.c_batch = (int64_t)batch * H;
+  g.bias = fc_b; g.bias_batch = H;
+  g.R = hidden; g.ldr = ldh; g.r_batch = 0; g.r_dtype = dtype;
+  g.M = batch; g.N = H; g.K = H;
+  return launch_gemm(g, dtype, out_dtype, kEpiMedusa, heads, s);
+}
+
+}  // extern "C"

@@ -1,0 +1,500 @@
+// Supplied-noise target sampling and the exact_target acceptance walk.
+//
+// Replaces sample_from_logits / exact_accept_paths_batch
+// (flashgrpo/decoding/acceptance.py:34-130, 179-260; correction tokens as in
+// flashgrpo_b200/decoding/acceptance.py:184-267). torch.multinomial cannot take
+// caller noise, so the draw follows one integer inverse-CDF rule that the CPU
+// oracle reproduces bit for bit:
+//   s_i = x_i / T (correctly rounded), m = max s, q_i = trunc(exp_fg(s_i - m) * 2^40)
+//   candidate order (key(s) desc, index asc); top_k keeps the first k; top_p
+//   keeps position j while the preceding kept mass <= floor(total * tp32 / 2^32)
+//   target = floor(total_kept * u32 / 2^32); token = first kept index (vocab
+//   order) whose inclusive q prefix exceeds target.
+// Integer sums make every result independent of reduction order.
+//
+// One 1024-thread workgroup per sampled row. The row is split into 16
+// contiguous wave segments; a wave walks its segment 512 elements (8 per lane,
+// 16-byte loads) per step. Top-k / top-p use an MSB-first 4 x 8-bit radix
+// select over the keys with count or q-weighted histograms in LDS.
+#include "fg_common.h"
+
+namespace {
+
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / 64;
+constexpr int kStep = 512;  // elements per wave step
+
+struct Shared {
+  uint64_t wsum[kWaves];
+  uint64_t hist[256];
+  uint64_t wkey[kWaves];
+  float wmax[kWaves];
+  uint64_t u64b[2];
+  int32_t i32b[2];
+};
+
+template <int DT>
+struct Row {
+  const char* p;
+  int V;
+  int seg;
+  float T;
+  bool scale;
+  float m;  // max scaled logit
+
+  FG_DEVICE int load(int i0, float (&x)[8]) const {
+    if (i0 + 8 <= V) {
+      fg::load8<DT>(p, i0, x);
+      return 8;
+    }
+    int n = V - i0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = j < n ? fg::load_elem<DT>(p, i0 + j) : 0.0f;
+    return n < 0 ? 0 : n;
+  }
+  FG_DEVICE float scaled(float x) const { return scale ? __fdiv_rn(x, T) : x; }
+  FG_DEVICE uint64_t weight(float s) const { return fg::quantize_q40(fg::exp_fg(s - m)); }
+};
+
+// Candidate-set predicate: key > kappa, or key == kappa and index <= last.
+struct KeyCut {
+  uint32_t kappa;
+  uint32_t last;
+  FG_DEVICE bool operator()(uint32_t key, uint32_t i) const { return key > kappa || (key == kappa && i <= last); }
+};
+constexpr KeyCut kAll{0u, 0xffffffffu};
+
+// Calls f(i, s, key) for each element of this wave's segment, 8 per lane per step.
+template <int DT, class F>
+FG_DEVICE void for_wave_segment(const Row<DT>& r, F&& f) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int lo = wave * r.seg;
+  const int hi = min(r.V, lo + r.seg);
+  for (int base = lo; base < hi; base += kStep) {
+    int i0 = base + lane * 8;
+    float x[8];
+    int n = r.load(i0, x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j < n) {
+        float s = r.scaled(x[j]);
+        f(i0 + j, s, fg::sort_key32(s));
+      }
+  }
+}
+
+// Elements equal to kappa inside a candidate cut.
+struct TiePred {
+  KeyCut within;
+  uint32_t kappa;
+  FG_DEVICE bool operator()(uint32_t key, uint32_t i) const { return key == kappa && within(key, i); }
+};
+
+// Block sum over pred-elements of w (1 or q); per-wave partials land in sh.wsum.
+template <bool WEIGHTED, int DT, class Pred>
+FG_DEVICE uint64_t block_sum(const Row<DT>& r, Pred pred, Shared& sh) {
+  __syncthreads();
+  uint64_t acc = 0;
+  for_wave_segment(r, [&](int i, float s, uint32_t key) {
+    if (pred(key, (uint32_t)i)) acc += WEIGHTED ? r.weight(s) : 1ull;
+  });
+  acc = fg::wave_sum_u64(acc);
+  if ((threadIdx.x & 63) == 0) sh.wsum[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  uint64_t tot = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) tot += sh.wsum[w];
+  return tot;
+}
+
+// First index (vocabulary order) among pred-elements whose inclusive running
+// sum of w exceeds target (-1 if none). sh.wsum must hold the per-wave sums of
+// the same (pred, w), as left by block_sum.
+template <bool WEIGHTED, int DT, class Pred>
+FG_DEVICE int block_locate(const Row<DT>& r, Pred pred, uint64_t target, Shared& sh) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  uint64_t before = 0;
+  int win = -1;
+  for (int w = 0; w < kWaves; ++w) {
+    if (before + sh.wsum[w] > target) {
+      win = w;
+      break;
+    }
+    before += sh.wsum[w];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) sh.i32b[0] = -1;
+  __syncthreads();
+  if (wave == win) {
+    uint64_t run = before;
+    const int lo = wave * r.seg;
+    const int hi = min(r.V, lo + r.seg);
+    for (int base = lo; base < hi; base += kStep) {
+      int i0 = base + lane * 8;
+      float x[8];
+      int n = r.load(i0, x);
+      uint64_t w8[8];
+      uint64_t mine = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        w8[j] = 0;
+        if (j < n) {
+          float s = r.scaled(x[j]);
+          if (pred(fg::sort_key32(s), (uint32_t)(i0 + j))) w8[j] = WEIGHTED ? r.weight(s) : 1ull;
+        }
+        mine += w8[j];
+      }
+      uint64_t incl = fg::wave_incl_scan_u64(mine);
+      uint64_t step_total = fg::shfl_u64(incl, 63);
+      if (run + step_total > target) {
+        uint64_t excl = run + incl - mine;
+        if (excl <= target && target < run + incl) {
+          uint64_t c = excl;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            c += w8[j];
+            if (c > target) {
+              sh.i32b[0] = i0 + j;
+              break;
+            }
+          }
+        }
+        break;
+      }
+      run += step_total;
+    }
+  }
+  __syncthreads();
+  return sh.i32b[0];
+}
+
+// MSB-first radix select over `within`-elements in candidate order
+// (key desc, index asc): returns the cut that keeps every position up to and
+// including the first one where the running count / q-mass exceeds target.
+template <bool WEIGHTED, int DT>
+FG_DEVICE KeyCut radix_select(const Row<DT>& r, KeyCut within, uint64_t target, Shared& sh) {
+  uint32_t prefix = 0, pmask = 0;
+  uint64_t above = 0;  // mass of within-elements whose key is above the current range
+  const int lane = threadIdx.x & 63;
+  for (int level = 0; level < 4; ++level) {
+    const int shift = 24 - 8 * level;
+    __syncthreads();
+    for (int d = threadIdx.x; d < 256; d += kThreads) sh.hist[d] = 0;
+    __syncthreads();
+    for_wave_segment(r, [&](int i, float s, uint32_t key) {
+      if (within(key, (uint32_t)i) && (key & pmask) == prefix)
+        atomicAdd((unsigned long long*)&sh.hist[(key >> shift) & 255u],
+                  (unsigned long long)(WEIGHTED ? r.weight(s) : 1ull));
+    });
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      // lane l owns digits 255-4l .. 252-4l, scanned from the largest digit down
+      uint64_t h[4], mine = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        h[j] = sh.hist[255 - 4 * lane - j];
+        mine += h[j];
+      }
+      uint64_t incl = fg::wave_incl_scan_u64(mine);
+      uint64_t excl = incl - mine;
+      if (above + excl <= target && target < above + incl) {
+        uint64_t c = above + excl;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (c + h[j] > target) {
+            sh.i32b[1] = 255 - 4 * lane - j;
+            sh.u64b[1] = c;
+            break;
+          }
+          c += h[j];
+        }
+      }
+    }
+    __syncthreads();
+    prefix |= (uint32_t)sh.i32b[1] << shift;
+    above = sh.u64b[1];
+    pmask |= 255u << shift;
+  }
+  // Ties on the selected key resolve in index order.
+  TiePred tie{within, prefix};
+  block_sum<WEIGHTED, DT>(r, tie, sh);
+  int last = block_locate<WEIGHTED, DT>(r, tie, target - above, sh);
+  return KeyCut{prefix, (uint32_t)last};
+}
+
+// First maximum of the raw logits (rank keys: value desc, index asc).
+template <int DT>
+FG_DEVICE int block_argmax(const Row<DT>& r0, Shared& sh) {
+  Row<DT> raw = r0;
+  raw.scale = false;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  uint64_t best = 0;
+  for_wave_segment(raw, [&](int i, float, uint32_t key) {
+    uint64_t k = ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+    best = k > best ? k : best;
+  });
+  best = fg::wave_max_u64(best);
+  __syncthreads();
+  if (lane == 0) sh.wkey[wave] = best;
+  __syncthreads();
+  uint64_t b = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) b = sh.wkey[w] > b ? sh.wkey[w] : b;
+  return (int)fg::rank_key_index(b);
+}
+
+struct SampleParams {
+  float temperature;
+  int greedy;
+  int top_k;      // 0 = off
+  uint32_t tp32;  // 0 = off
+};
+
+// One draw from one row by the whole block. Returns the token (all threads).
+template <int DT>
+FG_DEVICE int block_sample(const void* rowp, int V, const SampleParams& sp, uint32_t u, Shared& sh) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  Row<DT> r;
+  r.p = (const char*)rowp;
+  r.V = V;
+  r.seg = (((V + kWaves - 1) / kWaves) + kStep - 1) / kStep * kStep;
+  r.scale = sp.temperature > 0.0f && sp.temperature != 1.0f;
+  r.T = sp.temperature;
+  r.m = 0.0f;
+  if (sp.greedy) return block_argmax<DT>(r, sh);
+  // Row max of raw logits; division by T > 0 is monotone, so max(x/T) = max(x)/T.
+  float mx = -INFINITY;
+  {
+    Row<DT> raw = r;
+    raw.scale = false;
+    for_wave_segment(raw, [&](int, float s, uint32_t) { mx = fmaxf(mx, s); });
+  }
+  mx = fg::wave_max(mx);
+  __syncthreads();
+  if (lane == 0) sh.wmax[wave] = mx;
+  __syncthreads();
+  mx = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, sh.wmax[w]);
+  r.m = r.scale ? __fdiv_rn(mx, r.T) : mx;
+
+  KeyCut keep = kAll;
+  if (sp.top_k > 0) keep = radix_select<false, DT>(r, kAll, (uint64_t)(sp.top_k - 1), sh);
+  if (sp.tp32) {
+    uint64_t tot = block_sum<true, DT>(r, keep, sh);
+    keep = radix_select<true, DT>(r, keep, fg::mulhi_u64_u32(tot, sp.tp32), sh);
+  }
+  uint64_t total = block_sum<true, DT>(r, keep, sh);
+  if (total == 0) return block_argmax<DT>(r, sh);
+  return block_locate<true, DT>(r, keep, fg::mulhi_u64_u32(total, u), sh);
+}
+
+FG_DEVICE uint32_t noise_value(const uint32_t* noise, int64_t noise_index, uint64_t seed, uint64_t step,
+                               uint32_t seq, uint32_t draw) {
+  if (noise) return noise[noise_index];
+  return fg::counter_noise(seed, step, seq, draw);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) sample_rows_kernel(
+    const void* __restrict__ logits, int64_t row_stride, int vocab, const int32_t* __restrict__ row_index,
+    const int32_t* __restrict__ forced, const uint32_t* __restrict__ noise, int noise_stride, int noise_col,
+    uint64_t seed, uint64_t step, const int32_t* __restrict__ seq_ids, int draw, SampleParams sp,
+    int32_t* __restrict__ out) {
+  __shared__ Shared sh;
+  const int rrow = blockIdx.x;
+  if (forced && forced[rrow] >= 0) {
+    if (threadIdx.x == 0) out[rrow] = forced[rrow];
+    return;
+  }
+  const int src = row_index ? row_index[rrow] : rrow;
+  const char* rowp = (const char*)logits + (int64_t)src * row_stride * (DT == fg::kBF16 ? 2 : 4);
+  uint32_t seq = seq_ids ? (uint32_t)seq_ids[rrow] : (uint32_t)rrow;
+  uint32_t u = noise_value(noise, (int64_t)rrow * noise_stride + noise_col, seed, step, seq, (uint32_t)draw);
+  int tok = block_sample<DT>(rowp, vocab, sp, u, sh);
+  if (threadIdx.x == 0) out[rrow] = tok;
+}
+
+// Walk state lives in the caller's workspace: parent[B], active[B].
+__global__ void walk_init_kernel(const int32_t* __restrict__ tree_tokens, const int32_t* __restrict__ parents,
+                                 const int32_t* __restrict__ n_nodes, int nmax, int batch, int32_t* acc_tokens,
+                                 int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
+                                 int32_t* correction, int32_t* state) {
+  int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  acc_tokens[(int64_t)b * acc_stride] = tree_tokens[(int64_t)b * nmax];
+  acc_nodes[(int64_t)b * acc_stride] = 0;
+  acc_len[b] = 1;
+  last_node[b] = 0;
+  correction[b] = -1;
+  int has_child = 0;
+  for (int c = 1; c < n_nodes[b]; ++c) has_child |= parents[(int64_t)b * nmax + c] == 0;
+  state[b] = 0;              // parent
+  state[batch + b] = has_child;  // active
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) walk_step_kernel(
+    const void* __restrict__ logits, int64_t row_stride, int vocab, const int32_t* __restrict__ slot_map,
+    const int32_t* __restrict__ tree_tokens, const int32_t* __restrict__ parents, const int32_t* __restrict__ n_nodes,
+    int nmax, int batch, int walk_step, const uint32_t* __restrict__ noise, int noise_stride, int noise_col0,
+    uint64_t seed, uint64_t step, const int32_t* __restrict__ seq_ids, int draw0, SampleParams sp,
+    int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
+    int32_t* correction, int32_t* state, int32_t* err_flag) {
+  __shared__ Shared sh;
+  const int b = blockIdx.x;
+  if (!state[batch + b]) return;
+  const int parent = state[b];
+  const int64_t slot = slot_map ? (int64_t)slot_map[(int64_t)b * nmax + parent] : (int64_t)b * nmax + parent;
+  if (slot < 0) {
+    if (threadIdx.x == 0) {
+      if (err_flag) atomicOr(err_flag, 2);
+      state[batch + b] = 0;
+    }
+    return;
+  }
+  const char* rowp = (const char*)logits + slot * row_stride * (DT == fg::kBF16 ? 2 : 4);
+  uint32_t seq = seq_ids ? (uint32_t)seq_ids[b] : (uint32_t)b;
+  uint32_t u = noise_value(noise, (int64_t)b * noise_stride + noise_col0 + walk_step, seed, step, seq,
+                           (uint32_t)(draw0 + walk_step));
+  int tok = block_sample<DT>(rowp, vocab, sp, u, sh);
+  if (threadIdx.x == 0) {
+    const int nn = n_nodes[b];
+    const int32_t* pb = parents + (int64_t)b * nmax;
+    const int32_t* tb = tree_tokens + (int64_t)b * nmax;
+    int match = -1;
+    for (int c = 1; c < nn; ++c)
+      if (pb[c] == parent && tb[c] == tok) {
+        match = c;
+        break;
+      }
+    if (match < 0) {
+      correction[b] = tok;
+      state[batch + b] = 0;
+    } else {
+      int len = acc_len[b];
+      if (len < acc_stride) {
+        acc_tokens[(int64_t)b * acc_stride + len] = tok;
+        acc_nodes[(int64_t)b * acc_stride + len] = match;
+        acc_len[b] = len + 1;
+      } else if (err_flag) {
+        atomicOr(err_flag, 4);
+      }
+      last_node[b] = match;
+      state[b] = match;
+      int has_child = 0;
+      for (int c = match + 1; c < nn; ++c) has_child |= pb[c] == match;
+      state[batch + b] = has_child;
+    }
+  }
+}
+
+// Length clamp, EOS cut, finished flag and the b200 pending root.
+// Follows flashgrpo/decoding/flash_medusa_decoder.py:899-922 and
+// flashgrpo_b200/decoding/flash_medusa_decoder.py:2303-2319.
+__global__ void accept_finalize_kernel(const int32_t* __restrict__ acc_tokens, const int32_t* __restrict__ acc_nodes,
+                                       int acc_stride, int32_t* acc_len, int32_t* last_node,
+                                       const int32_t* __restrict__ correction, const int32_t* __restrict__ old_len,
+                                       int max_length, int eos_token_id, int32_t* finished, int32_t* pending_root,
+                                       int batch) {
+  int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  const int raw = acc_len[b];
+  int keep = max(1, max_length - old_len[b]);
+  int len = min(raw, keep);
+  int eos = 0;
+  if (eos_token_id >= 0) {
+    for (int j = 0; j < len; ++j)
+      if (acc_tokens[(int64_t)b * acc_stride + j] == eos_token_id) {
+        len = j + 1;
+        eos = 1;
+        break;
+      }
+  }
+  acc_len[b] = len;
+  last_node[b] = acc_nodes[(int64_t)b * acc_stride + len - 1];
+  int fin = eos || old_len[b] + len >= max_length;
+  finished[b] = fin;
+  if (pending_root) pending_root[b] = (correction[b] >= 0 && len == raw && !fin) ? correction[b] : -1;
+}
+
+SampleParams make_params(float temperature, int greedy, int top_k, int vocab, uint32_t tp32) {
+  SampleParams sp;
+  sp.temperature = temperature;
+  sp.greedy = greedy || temperature == 0.0f;
+  sp.top_k = (top_k > 0 && top_k < vocab) ? top_k : 0;
+  sp.tp32 = tp32;
+  return sp;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fg_sample_tokens(const void* logits, int dtype, int64_t row_stride, int rows, int vocab,
+                     const int32_t* row_index, const int32_t* forced, const uint32_t* noise, int noise_stride,
+                     int noise_col, uint64_t seed, uint64_t step, const int32_t* seq_ids, int draw,
+                     float temperature, int greedy, int top_k, uint32_t top_p_fixed, int32_t* out_tokens,
+                     void* stream) {
+  FG_REQUIRE(logits && out_tokens, "fg_sample_tokens: null pointer");
+  FG_REQUIRE(rows > 0 && vocab > 0 && vocab < (1 << 23), "fg_sample_tokens: vocab must be in [1, 2^23)");
+  FG_REQUIRE(dtype == fg::kF32 || dtype == fg::kBF16, "fg_sample_tokens: dtype");
+  FG_REQUIRE(row_stride >= vocab && row_stride % 8 == 0 && ((uintptr_t)logits & 31) == 0,
+             "fg_sample_tokens: rows must be 32-byte aligned (row_stride % 8 == 0)");
+  SampleParams sp = make_params(temperature, greedy, top_k, vocab, top_p_fixed);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == fg::kBF16)
+    hipLaunchKernelGGL(sample_rows_kernel<fg::kBF16>, dim3(rows), dim3(kThreads), 0, s, logits, row_stride, vocab,
+                       row_index, forced, noise, noise_stride, noise_col, seed, step, seq_ids, draw, sp, out_tokens);
+  else
+    hipLaunchKernelGGL(sample_rows_kernel<fg::kF32>, dim3(rows), dim3(kThreads), 0, s, logits, row_stride, vocab,
+                       row_index, forced, noise, noise_stride, noise_col, seed, step, seq_ids, draw, sp, out_tokens);
+  return fg::check_launch("fg_sample_tokens");
+}
+
+int fg_accept_walk(const void* tree_logits, int dtype, int64_t row_stride, int vocab, const int32_t* slot_map,
+                   const int32_t* tree_tokens, const int32_t* parents, const int32_t* n_nodes, int nmax, int batch,
+                   int max_walk_steps, const uint32_t* noise, int noise_stride, int noise_col0, uint64_t seed,
+                   uint64_t step, const int32_t* seq_ids, int draw0, float temperature, int greedy, int top_k,
+                   uint32_t top_p_fixed, int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len,
+                   int32_t* last_node, int32_t* correction, int32_t* workspace, int32_t* err_flag, void* stream) {
+  FG_REQUIRE(tree_logits && tree_tokens && parents && n_nodes && acc_tokens && acc_nodes && acc_len && last_node &&
+                 correction && workspace,
+             "fg_accept_walk: null pointer");
+  FG_REQUIRE(batch > 0 && nmax > 0 && nmax <= 64 && vocab > 0 && vocab < (1 << 23), "fg_accept_walk: bad shape");
+  FG_REQUIRE(acc_stride >= 1 && max_walk_steps >= 0, "fg_accept_walk: bad acc_stride / steps");
+  FG_REQUIRE(dtype == fg::kF32 || dtype == fg::kBF16, "fg_accept_walk: dtype");
+  FG_REQUIRE(row_stride >= vocab && row_stride % 8 == 0 && ((uintptr_t)tree_logits & 31) == 0,
+             "fg_accept_walk: rows must be 32-byte aligned (row_stride % 8 == 0)");
+  SampleParams sp = make_params(temperature, greedy, top_k, vocab, top_p_fixed);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(walk_init_kernel, dim3((batch + 63) / 64), dim3(64), 0, s, tree_tokens, parents, n_nodes, nmax,
+                     batch, acc_tokens, acc_nodes, acc_stride, acc_len, last_node, correction, workspace);
+  for (int t = 0; t < max_walk_steps; ++t) {
+    if (dtype == fg::kBF16)
+      hipLaunchKernelGGL(walk_step_kernel<fg::kBF16>, dim3(batch), dim3(kThreads), 0, s, tree_logits, row_stride,
+                         vocab, slot_map, tree_tokens, parents, n_nodes, nmax, batch, t, noise, noise_stride,
+                         noise_col0, seed, step, seq_ids, draw0, sp, acc_tokens, acc_nodes, acc_stride, acc_len,
+                         last_node, correction, workspace, err_flag);
+    else
+      hipLaunchKernelGGL(walk_step_kernel<fg::kF32>, dim3(batch), dim3(kThreads), 0, s, tree_logits, row_stride,
+                         vocab, slot_map, tree_tokens, parents, n_nodes, nmax, batch, t, noise, noise_stride,
+                         noise_col0, seed, step, seq_ids, draw0, sp, acc_tokens, acc_nodes, acc_stride, acc_len,
+                         last_node, correction, workspace, err_flag);
+  }
+  return fg::check_launch("fg_accept_walk");
+}
+
+int fg_accept_finalize(const int32_t* acc_tokens, const int32_t* acc_nodes, int acc_stride, int32_t* acc_len,
+                       int32_t* last_node, const int32_t* correction, const int32_t* old_len, int max_length,
+                       int eos_token_id, int32_t* finished, int32_t* pending_root, int batch, void* stream) {
+  FG_REQUIRE(acc_tokens && acc_nodes && acc_len && last_node && correction && old_len && finished,
+             "fg_accept_finalize: null pointer");
+  FG_REQUIRE(batch > 0 && acc_stride >= 1, "fg_accept_finalize: bad shape");
+  hipLaunchKernelGGL(accept_finalize_kernel, dim3((batch + 63) / 64), dim3(64), 0, (hipStream_t)stream, acc_tokens,
+                     acc_nodes, acc_stride, acc_len, last_node, correction, old_len, max_length, eos_token_id,
+                     finished, pending_root, batch);
+  return fg::check_launch("fg_accept_finalize");
+}
+
+}  // extern "C"

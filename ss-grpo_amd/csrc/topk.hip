@@ -1,0 +1,295 @@
+// Per-depth Medusa top-k candidate selection and dense-tree token layout.
+//
+// Replaces the per-depth torch.topk + .cpu() + Python BFS of
+// flashgrpo/decoding/medusa_tree.py:228-278. Candidates are ranked by
+// (value desc, index asc) so ties resolve the same way on every run; the
+// tree topology (parent, depth, candidate rank of each node) depends only on
+// the plan and is supplied by the host, the kernel fills in the tokens.
+//
+// Phase 1: grid (rows, chunks). Each thread keeps a sorted top-K of 64-bit
+// rank keys over its strided elements (and, optionally, a running max and
+// sum of exp for the row's log-sum-exp); lists merge across the wave with the
+// bitonic "max(A[i], B[K-1-i]) then sort" step, then across waves in LDS.
+// Phase 2: one wave per row merges the chunk lists.
+#include "fg_common.h"
+
+#include <algorithm>
+
+namespace {
+
+constexpr int kThreads = 256;
+
+template <int K>
+FG_DEVICE void insert_key(uint64_t (&top)[K], uint64_t k) {
+  if (k <= top[K - 1]) return;
+  top[K - 1] = k;
+#pragma unroll
+  for (int i = K - 1; i > 0; --i) {
+    if (top[i] > top[i - 1]) {
+      uint64_t t = top[i];
+      top[i] = top[i - 1];
+      top[i - 1] = t;
+    }
+  }
+}
+
+// Sort a bitonic sequence of K keys into descending order.
+template <int K>
+FG_DEVICE void bitonic_sort_desc(uint64_t (&v)[K]) {
+#pragma unroll
+  for (int len = K / 2; len > 0; len >>= 1) {
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      if ((i & len) == 0) {
+        int j = i | len;
+        if (v[j] > v[i]) {
+          uint64_t t = v[i];
+          v[i] = v[j];
+          v[j] = t;
+        }
+      }
+    }
+  }
+}
+
+// top-K of two descending lists, result descending in `a`.
+template <int K>
+FG_DEVICE void merge_desc(uint64_t (&a)[K], const uint64_t (&b)[K]) {
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    uint64_t o = b[K - 1 - i];
+    a[i] = o > a[i] ? o : a[i];
+  }
+  bitonic_sort_desc<K>(a);
+}
+
+template <int K>
+FG_DEVICE void wave_merge(uint64_t (&top)[K]) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint64_t other[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) other[i] = fg::shfl_xor_u64(top[i], o);
+    merge_desc<K>(top, other);
+  }
+}
+
+struct LseAcc {
+  float m, s;
+};
+
+FG_DEVICE LseAcc lse_combine(LseAcc a, LseAcc b) {
+  float m = fmaxf(a.m, b.m);
+  if (m == -INFINITY) return {m, 0.0f};
+  return {m, a.s * __expf(a.m - m) + b.s * __expf(b.m - m)};
+}
+
+template <int DT, int K, bool STATS>
+__global__ void __launch_bounds__(kThreads) topk_phase1(const void* __restrict__ logits, int64_t row_stride,
+                                                        int vocab, int chunk, uint64_t* __restrict__ part_keys,
+                                                        float2* __restrict__ part_lse) {
+  const int row = blockIdx.x;
+  const int c = blockIdx.y;
+  const int nchunks = gridDim.y;
+  const char* rowp = (const char*)logits + (int64_t)row * row_stride * (DT == fg::kBF16 ? 2 : 4);
+  const int lo = c * chunk;
+  const int hi = min(vocab, lo + chunk);
+  uint64_t top[K];
+#pragma unroll
+  for (int i = 0; i < K; ++i) top[i] = 0;
+  LseAcc acc{-INFINITY, 0.0f};
+  // Vector body: 8 elements per thread per step; chunk starts are multiples of 8.
+  const int vec_hi = lo + ((hi - lo) & ~7);
+  for (int i = lo + threadIdx.x * 8; i < vec_hi; i += kThreads * 8) {
+    float v[8];
+    fg::load8<DT>(rowp, i, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) insert_key<K>(top, fg::rank_key(v[j], (uint32_t)(i + j)));
+    if constexpr (STATS) {
+      float m8 = v[0];
+#pragma unroll
+      for (int j = 1; j < 8; ++j) m8 = fmaxf(m8, v[j]);
+      float m = fmaxf(acc.m, m8);
+      float s = (acc.m == -INFINITY) ? 0.0f : acc.s * __expf(acc.m - m);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += __expf(v[j] - m);
+      acc = {m, s};
+    }
+  }
+  for (int i = vec_hi + threadIdx.x; i < hi; i += kThreads) {
+    float v = fg::load_elem<DT>(rowp, i);
+    insert_key<K>(top, fg::rank_key(v, (uint32_t)i));
+    if constexpr (STATS) acc = lse_combine(acc, LseAcc{v, 1.0f});
+  }
+  wave_merge<K>(top);
+  __shared__ uint64_t s_top[kThreads / 64][K];
+  __shared__ float2 s_lse[kThreads / 64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if constexpr (STATS) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      LseAcc other{__shfl_xor(acc.m, o, 64), __shfl_xor(acc.s, o, 64)};
+      acc = lse_combine(acc, other);
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < K; ++i) s_top[wave][i] = top[i];
+    s_lse[wave] = make_float2(acc.m, acc.s);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) {
+      uint64_t other[K];
+#pragma unroll
+      for (int i = 0; i < K; ++i) other[i] = s_top[w][i];
+      merge_desc<K>(top, other);
+      if constexpr (STATS) acc = lse_combine(acc, LseAcc{s_lse[w].x, s_lse[w].y});
+    }
+    uint64_t* out = part_keys + ((int64_t)row * nchunks + c) * K;
+#pragma unroll
+    for (int i = 0; i < K; ++i) out[i] = top[i];
+    if constexpr (STATS) part_lse[(int64_t)row * nchunks + c] = make_float2(acc.m, acc.s);
+  }
+}
+
+template <int K, bool STATS>
+__global__ void __launch_bounds__(64) topk_phase2(const uint64_t* __restrict__ part_keys,
+                                                  const float2* __restrict__ part_lse, int nchunks, int kout,
+                                                  int32_t* __restrict__ cand_tokens, float* __restrict__ cand_scores,
+                                                  float* __restrict__ row_stats) {
+  const int row = blockIdx.x;
+  const int lane = threadIdx.x;
+  uint64_t top[K];
+  LseAcc acc{-INFINITY, 0.0f};
+#pragma unroll
+  for (int i = 0; i < K; ++i) top[i] = 0;
+  for (int c = lane; c < nchunks; c += 64) {
+    uint64_t other[K];
+    const uint64_t* in = part_keys + ((int64_t)row * nchunks + c) * K;
+#pragma unroll
+    for (int i = 0; i < K; ++i) other[i] = in[i];
+    merge_desc<K>(top, other);
+    if constexpr (STATS) {
+      float2 p = part_lse[(int64_t)row * nchunks + c];
+      acc = lse_combine(acc, LseAcc{p.x, p.y});
+    }
+  }
+  wave_merge<K>(top);
+  if constexpr (STATS) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      LseAcc other{__shfl_xor(acc.m, o, 64), __shfl_xor(acc.s, o, 64)};
+      acc = lse_combine(acc, other);
+    }
+  }
+  if (lane == 0) {
+    for (int i = 0; i < kout; ++i) {
+      cand_tokens[(int64_t)row * kout + i] = (int32_t)fg::rank_key_index(top[i]);
+      cand_scores[(int64_t)row * kout + i] = fg::rank_key_value(top[i]);
+    }
+    if constexpr (STATS) {
+      row_stats[2 * row] = acc.m;
+      row_stats[2 * row + 1] = acc.m + __logf(acc.s);
+    }
+  }
+}
+
+template <int DT, int K, bool STATS>
+void launch_topk(const void* logits, int64_t row_stride, int rows, int vocab, int chunks, int chunk, int kout,
+                 uint64_t* part_keys, float2* part_lse, int32_t* tok, float* score, float* stats,
+                 hipStream_t stream) {
+  hipLaunchKernelGGL((topk_phase1<DT, K, STATS>), dim3(rows, chunks), dim3(kThreads), 0, stream, logits, row_stride,
+                     vocab, chunk, part_keys, part_lse);
+  hipLaunchKernelGGL((topk_phase2<K, STATS>), dim3(rows), dim3(64), 0, stream, part_keys, part_lse, chunks, kout, tok,
+                     score, stats);
+}
+
+template <int DT, bool STATS>
+void dispatch_k(int K, const void* logits, int64_t row_stride, int rows, int vocab, int chunks, int chunk, int kout,
+                uint64_t* pk, float2* pl, int32_t* tok, float* score, float* stats, hipStream_t s) {
+  switch (K) {
+    case 1: launch_topk<DT, 1, STATS>(logits, row_stride, rows, vocab, chunks, chunk, kout, pk, pl, tok, score, stats, s); break;
+    case 2: launch_topk<DT, 2, STATS>(logits, row_stride, rows, vocab, chunks, chunk, kout, pk, pl, tok, score, stats, s); break;
+    case 4: launch_topk<DT, 4, STATS>(logits, row_stride, rows, vocab, chunks, chunk, kout, pk, pl, tok, score, stats, s); break;
+    case 8: launch_topk<DT, 8, STATS>(logits, row_stride, rows, vocab, chunks, chunk, kout, pk, pl, tok, score, stats, s); break;
+    default: launch_topk<DT, 16, STATS>(logits, row_stride, rows, vocab, chunks, chunk, kout, pk, pl, tok, score, stats, s); break;
+  }
+}
+
+__global__ void tree_layout_kernel(const int32_t* __restrict__ cand_tokens, const float* __restrict__ cand_scores,
+                                   int kstride, int batch, const int32_t* __restrict__ roots,
+                                   const int32_t* __restrict__ node_depth, const int32_t* __restrict__ node_rank,
+                                   int num_nodes, int32_t* __restrict__ tree_tokens, float* __restrict__ tree_scores,
+                                   int out_stride) {
+  const int b = blockIdx.x;
+  for (int n = threadIdx.x; n < num_nodes; n += blockDim.x) {
+    int32_t tok;
+    float sc;
+    if (n == 0) {
+      tok = roots[b];
+      sc = 0.0f;
+    } else {
+      int64_t r = (int64_t)(node_depth[n] - 2) * batch + b;
+      tok = cand_tokens[r * kstride + node_rank[n]];
+      sc = cand_scores[r * kstride + node_rank[n]];
+    }
+    tree_tokens[(int64_t)b * out_stride + n] = tok;
+    if (tree_scores) tree_scores[(int64_t)b * out_stride + n] = sc;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+// Workspace bytes fg_medusa_topk needs for `rows` rows.
+size_t fg_medusa_topk_workspace(int rows, int vocab, int kmax) {
+  int chunks = 64;
+  return (size_t)rows * chunks * (16 * sizeof(uint64_t) + sizeof(float2)) + 256;
+}
+
+int fg_medusa_topk(const void* logits, int dtype, int64_t row_stride, int rows, int vocab, int kmax,
+                   int32_t* cand_tokens, float* cand_scores, float* row_stats, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  FG_REQUIRE(logits && cand_tokens && cand_scores && workspace, "fg_medusa_topk: null pointer");
+  FG_REQUIRE(rows > 0 && vocab > 0 && vocab < (1 << 30), "fg_medusa_topk: bad shape");
+  FG_REQUIRE(kmax >= 1 && kmax <= 16 && kmax <= vocab, "fg_medusa_topk: kmax must be in [1, min(16, vocab)]");
+  FG_REQUIRE(dtype == fg::kF32 || dtype == fg::kBF16, "fg_medusa_topk: dtype");
+  FG_REQUIRE(row_stride >= vocab && row_stride % 8 == 0, "fg_medusa_topk: row_stride must be >= vocab and a multiple of 8");
+  FG_REQUIRE(((uintptr_t)logits & 31) == 0, "fg_medusa_topk: logits must be 32-byte aligned");
+  int K = kmax <= 1 ? 1 : kmax <= 2 ? 2 : kmax <= 4 ? 4 : kmax <= 8 ? 8 : 16;
+  // Enough workgroups to cover the chip: ~2048 in total, chunks of >= 2048 elements.
+  int chunks = (2048 + rows - 1) / rows;
+  chunks = std::max(1, std::min(chunks, std::min(64, (vocab + 2047) / 2048)));
+  int chunk = ((vocab + chunks - 1) / chunks + 7) & ~7;
+  chunks = (vocab + chunk - 1) / chunk;
+  size_t need = (size_t)rows * chunks * (K * sizeof(uint64_t) + sizeof(float2));
+  FG_REQUIRE(workspace_bytes >= need, "fg_medusa_topk: workspace too small");
+  uint64_t* pk = (uint64_t*)workspace;
+  float2* pl = (float2*)(pk + (size_t)rows * chunks * K);
+  hipStream_t s = (hipStream_t)stream;
+  bool stats = row_stats != nullptr;
+  if (dtype == fg::kBF16) {
+    if (stats) dispatch_k<fg::kBF16, true>(K, logits, row_stride, rows, vocab, chunks, chunk, kmax, pk, pl, cand_tokens, cand_scores, row_stats, s);
+    else dispatch_k<fg::kBF16, false>(K, logits, row_stride, rows, vocab, chunks, chunk, kmax, pk, pl, cand_tokens, cand_scores, row_stats, s);
+  } else {
+    if (stats) dispatch_k<fg::kF32, true>(K, logits, row_stride, rows, vocab, chunks, chunk, kmax, pk, pl, cand_tokens, cand_scores, row_stats, s);
+    else dispatch_k<fg::kF32, false>(K, logits, row_stride, rows, vocab, chunks, chunk, kmax, pk, pl, cand_tokens, cand_scores, row_stats, s);
+  }
+  return fg::check_launch("fg_medusa_topk");
+}
+
+int fg_tree_layout(const int32_t* cand_tokens, const float* cand_scores, int kstride, int batch,
+                   const int32_t* roots, const int32_t* node_depth, const int32_t* node_rank, int num_nodes,
+                   int32_t* tree_tokens, float* tree_scores, int out_stride, void* stream) {
+  FG_REQUIRE(roots && node_depth && node_rank && tree_tokens, "fg_tree_layout: null pointer");
+  FG_REQUIRE(batch > 0 && num_nodes > 0 && out_stride >= num_nodes, "fg_tree_layout: bad shape");
+  FG_REQUIRE(num_nodes == 1 || (cand_tokens && cand_scores && kstride > 0), "fg_tree_layout: candidates missing");
+  hipLaunchKernelGGL(tree_layout_kernel, dim3(batch), dim3(64), 0, (hipStream_t)stream, cand_tokens, cand_scores,
+                     kstride, batch, roots, node_depth, node_rank, num_nodes, tree_tokens, tree_scores, out_stride);
+  return fg::check_launch("fg_tree_layout");
+}
+
+}  // extern "C"

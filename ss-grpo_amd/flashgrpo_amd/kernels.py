@@ -1,0 +1,279 @@
+"""Torch-facing wrappers over the C ABI (one function per entry point).
+
+Each wrapper checks devices, dtypes and shapes on the host, passes raw
+pointers plus torch's current HIP stream, and raises on any error code. All
+device work happens in the HIP kernels of ``ss-grpo_amd/csrc``.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+F32, BF16 = 0, 1
+_DT = {torch.float32: F32, torch.bfloat16: BF16}
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}; expected float32 or bfloat16") from None
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _dev(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("flashgrpo_amd kernels take device tensors (got a CPU tensor)")
+
+
+def _i32(t, name):
+    if t is not None and t.dtype != torch.int32:
+        raise TypeError(f"{name} must be int32")
+
+
+def aligned_rows(x: torch.Tensor) -> torch.Tensor:
+    """x itself when its rows start 32-byte aligned with a stride that is a
+    multiple of 8 elements (what the row kernels load with 16-byte vectors),
+    otherwise a padded copy viewed back to x's shape."""
+    x2 = x.reshape(-1, x.shape[-1]) if x.dim() != 2 else x
+    if x2.stride(-1) == 1 and x2.stride(0) % 8 == 0 and x2.data_ptr() % 32 == 0:
+        return x2
+    V = x2.shape[-1]
+    pad = torch.empty(x2.shape[0], (V + 7) // 8 * 8, dtype=x2.dtype, device=x2.device)
+    pad[:, :V].copy_(x2)
+    return pad[:, :V]
+
+
+def top_p_fixed(top_p) -> int:
+    """floor(top_p * 2^32) for 0 < top_p < 1, else 0 (no nucleus cut)."""
+    if top_p is None or not (0.0 < float(top_p) < 1.0):
+        return 0
+    return int(float(top_p) * 4294967296.0)
+
+
+# ------------------------------------------------------------------ contractions
+def medusa_heads(hidden, ln_w, ln_b, fc_w, fc_b, *, eps=1e-5, out=None, out_dtype=None, workspace=None):
+    """[heads*B, H] = hidden + SiLU(fc(LayerNorm(hidden))) per head (heads stacked)."""
+    _dev(hidden, ln_w, ln_b, fc_w, fc_b)
+    B, H = hidden.shape
+    heads = fc_w.shape[0]
+    if hidden.stride(1) != 1 or fc_w.shape[1:] != (H, H) or not fc_w.is_contiguous() or not fc_b.is_contiguous():
+        raise ValueError("medusa_heads: expected hidden [B,H] row-major, fc_w [heads,H,H], fc_b [heads,H]")
+    if fc_w.dtype != hidden.dtype or fc_b.dtype != hidden.dtype:
+        raise TypeError("medusa_heads: fc weights must share the hidden dtype")
+    ln_w = ln_w.float().contiguous()
+    ln_b = ln_b.float().contiguous()
+    od = out_dtype or hidden.dtype
+    if out is None:
+        out = torch.empty(heads * B, H, dtype=od, device=hidden.device)
+    need = _lib.load().fg_medusa_heads_workspace(B, H, heads, dtype_code(hidden))
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=hidden.device)
+    _lib.call("fg_medusa_heads", _ptr(hidden), dtype_code(hidden), B, H, hidden.stride(0), heads, _ptr(ln_w),
+              _ptr(ln_b), float(eps), _ptr(fc_w), _ptr(fc_b), _ptr(out), dtype_code(out), _ptr(workspace),
+              workspace.numel() * workspace.element_size(), _stream())
+    return out
+
+
+def lm_head(x, weight, *, row_index=None, out=None, out_dtype=None):
+    """out[m] = x[row_index[m] if row_index is given else m] @ weight.T"""
+    _dev(x, weight, row_index)
+    _i32(row_index, "row_index")
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    if x2.stride(1) != 1 or weight.stride(1) != 1 or weight.shape[1] != K:
+        raise ValueError("lm_head: operands must be K-contiguous with matching K")
+    if x.dtype != weight.dtype:
+        raise TypeError("lm_head: x and weight dtypes differ")
+    M = row_index.numel() if row_index is not None else x2.shape[0]
+    N = weight.shape[0]
+    od = out_dtype or x.dtype
+    if out is None:
+        out = torch.empty(M, N, dtype=od, device=x.device)
+    if M == 0:
+        return out
+    _lib.call("fg_lm_head", _ptr(x2), dtype_code(x), M, K, x2.stride(0), _ptr(row_index), _ptr(weight),
+              weight.stride(0), N, _ptr(out), dtype_code(out), out.stride(0), _stream())
+    return out
+
+
+# ------------------------------------------------------------------ tree construction
+def medusa_topk(logits, kmax, *, stats=False, workspace=None):
+    """Top-kmax candidates per row ranked (value desc, index asc).
+
+    Returns (tokens int32 [R, kmax], scores fp32 [R, kmax], stats fp32 [R, 2] or None)
+    where stats holds (row max, row logsumexp).
+    """
+    _dev(logits)
+    logits = aligned_rows(logits)
+    R, V = logits.shape
+    tok = torch.empty(R, kmax, dtype=torch.int32, device=logits.device)
+    sc = torch.empty(R, kmax, dtype=torch.float32, device=logits.device)
+    st = torch.empty(R, 2, dtype=torch.float32, device=logits.device) if stats else None
+    need = _lib.load().fg_medusa_topk_workspace(R, V, kmax)
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=logits.device)
+    _lib.call("fg_medusa_topk", _ptr(logits), dtype_code(logits), logits.stride(0), R, V, kmax, _ptr(tok), _ptr(sc),
+              _ptr(st), _ptr(workspace), workspace.numel() * workspace.element_size(), _stream())
+    return tok, sc, st
+
+
+def tree_layout(cand_tokens, cand_scores, batch, roots, node_depth, node_rank, num_nodes, *, out_tokens=None,
+                out_scores=None):
+    _dev(cand_tokens, cand_scores, roots, node_depth, node_rank)
+    for t, n in ((cand_tokens, "cand_tokens"), (roots, "roots"), (node_depth, "node_depth"), (node_rank, "node_rank")):
+        _i32(t, n)
+    dev = roots.device
+    if out_tokens is None:
+        out_tokens = torch.empty(batch, num_nodes, dtype=torch.int32, device=dev)
+    if out_scores is None:
+        out_scores = torch.empty(batch, num_nodes, dtype=torch.float32, device=dev)
+    kstride = cand_tokens.shape[-1] if cand_tokens is not None else 0
+    _lib.call("fg_tree_layout", _ptr(cand_tokens), _ptr(cand_scores), kstride, batch, _ptr(roots), _ptr(node_depth),
+              _ptr(node_rank), num_nodes, _ptr(out_tokens), _ptr(out_scores), out_tokens.stride(0), _stream())
+    return out_tokens, out_scores
+
+
+# ------------------------------------------------------------------ verify forward pieces
+def rope_kv_write(qkv, *, batch, num_nodes, q_heads, kv_heads, head_dim, seq_len, pos_offset, inv_freq, q_out,
+                  k_cache, v_cache, row_map=None):
+    _dev(qkv, seq_len, pos_offset, inv_freq, q_out, k_cache, v_cache, row_map)
+    _i32(seq_len, "seq_len")
+    _i32(pos_offset, "pos_offset")
+    _i32(row_map, "row_map")
+    if k_cache.stride(-1) != 1 or k_cache.stride(-2) != head_dim:
+        raise ValueError("rope_kv_write: cache rows must be contiguous [.., capacity, d]")
+    _lib.call("fg_rope_kv_write", _ptr(qkv), dtype_code(qkv), qkv.stride(0), batch, num_nodes, q_heads, kv_heads,
+              head_dim, _ptr(seq_len), _ptr(pos_offset), _ptr(inv_freq), _ptr(q_out), _ptr(k_cache), _ptr(v_cache),
+              k_cache.stride(0), k_cache.stride(1), _ptr(row_map), _stream())
+
+
+def tree_attention(q, k_cache, v_cache, *, seq_len, anc, num_nodes, q_heads, kv_heads, head_dim, out=None,
+                   row_map=None, scale=None):
+    """q [B, N, Hq, d]; caches [Bc, Hkv, S, d]; anc uint64 as int64 [B, N] or [N]."""
+    _dev(q, k_cache, v_cache, seq_len, anc, row_map)
+    _i32(seq_len, "seq_len")
+    if anc.dtype != torch.int64:
+        raise TypeError("anc must be int64 (bit pattern of the uint64 masks)")
+    B = q.shape[0]
+    if out is None:
+        out = torch.empty_like(q)
+    anc_stride = 0 if anc.dim() == 1 else anc.stride(0)
+    scale = 1.0 / math.sqrt(head_dim) if scale is None else scale
+    _lib.call("fg_tree_attention", _ptr(q), _ptr(out), _ptr(k_cache), _ptr(v_cache), dtype_code(q), B, num_nodes,
+              q_heads, kv_heads, head_dim, k_cache.stride(0), k_cache.stride(1), k_cache.shape[2], _ptr(seq_len),
+              _ptr(row_map), _ptr(anc), anc_stride, float(scale), _stream())
+    return out
+
+
+def rmsnorm(x, weight, eps, *, delta=None, out=None):
+    _dev(x, weight, delta)
+    H = x.shape[-1]
+    rows = x.numel() // H
+    if out is None:
+        out = torch.empty_like(x)
+    _lib.call("fg_rmsnorm", _ptr(x), _ptr(delta), _ptr(weight), _ptr(out), dtype_code(x), rows, H, float(eps),
+              _stream())
+    return out
+
+
+def swiglu(gate_up, *, out=None):
+    _dev(gate_up)
+    rows, two_f = gate_up.shape
+    F = two_f // 2
+    if out is None:
+        out = torch.empty(rows, F, dtype=gate_up.dtype, device=gate_up.device)
+    _lib.call("fg_swiglu", _ptr(gate_up), _ptr(out), dtype_code(gate_up), rows, F, _stream())
+    return out
+
+
+# ------------------------------------------------------------------ sampling / acceptance
+def sample_tokens(logits, *, noise=None, noise_col=0, seed=0, step=0, seq_ids=None, draw=0, row_index=None,
+                  forced=None, temperature=1.0, greedy=False, top_k=None, top_p=1.0, out=None):
+    """One token per row (see the rule in csrc/sample.hip). noise: uint32 bits as int32 [R, C]."""
+    _dev(logits, noise, seq_ids, row_index, forced)
+    for t, n in ((seq_ids, "seq_ids"), (row_index, "row_index"), (forced, "forced")):
+        _i32(t, n)
+    if noise is not None and noise.dtype != torch.int32:
+        raise TypeError("noise must be int32 holding uint32 bit patterns")
+    logits = aligned_rows(logits)
+    V = logits.shape[-1]
+    rows = row_index.numel() if row_index is not None else logits.shape[0]
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int32, device=logits.device)
+    T = 0.0 if temperature is None else float(temperature)
+    use_T = T if T > 0 else (-1.0 if T < 0 or temperature is None else 0.0)
+    g = bool(greedy) or (temperature is not None and T == 0.0)
+    _lib.call("fg_sample_tokens", _ptr(logits), dtype_code(logits), logits.stride(0), rows,
+              V, _ptr(row_index), _ptr(forced), _ptr(noise), noise.stride(0) if noise is not None else 0,
+              int(noise_col), int(seed) & (2 ** 64 - 1), int(step), _ptr(seq_ids), int(draw), use_T, int(g),
+              int(top_k or 0), top_p_fixed(top_p), _ptr(out), _stream())
+    return out
+
+
+def accept_walk(tree_logits, tree_tokens, parents, n_nodes, *, max_walk_steps, slot_map=None, noise=None,
+                noise_col0=0, seed=0, step=0, seq_ids=None, draw0=1, temperature=1.0, greedy=False, top_k=None,
+                top_p=1.0, acc_stride=None, err_flag=None, out=None):
+    """exact_target walk. Returns dict of int32 device tensors (acc_tokens, acc_nodes, acc_len, last_node, correction)."""
+    _dev(tree_logits, tree_tokens, parents, n_nodes, slot_map, noise, seq_ids)
+    for t, n in ((tree_tokens, "tree_tokens"), (parents, "parents"), (n_nodes, "n_nodes"), (slot_map, "slot_map"),
+                 (seq_ids, "seq_ids")):
+        _i32(t, n)
+    B, nmax = tree_tokens.shape
+    V = tree_logits.shape[-1]
+    dev = tree_tokens.device
+    acc_stride = acc_stride or (max_walk_steps + 1)
+    if out is None:
+        out = dict(acc_tokens=torch.empty(B, acc_stride, dtype=torch.int32, device=dev),
+                   acc_nodes=torch.empty(B, acc_stride, dtype=torch.int32, device=dev),
+                   acc_len=torch.empty(B, dtype=torch.int32, device=dev),
+                   last_node=torch.empty(B, dtype=torch.int32, device=dev),
+                   correction=torch.empty(B, dtype=torch.int32, device=dev),
+                   state=torch.empty(2 * B, dtype=torch.int32, device=dev))
+    T = 0.0 if temperature is None else float(temperature)
+    use_T = T if T > 0 else (-1.0 if T < 0 or temperature is None else 0.0)
+    g = bool(greedy) or (temperature is not None and T == 0.0)
+    lg = aligned_rows(tree_logits.reshape(-1, V))
+    _lib.call("fg_accept_walk", _ptr(lg), dtype_code(lg), lg.stride(0), V, _ptr(slot_map), _ptr(tree_tokens),
+              _ptr(parents), _ptr(n_nodes), nmax, B, int(max_walk_steps), _ptr(noise),
+              noise.stride(0) if noise is not None else 0, int(noise_col0), int(seed) & (2 ** 64 - 1), int(step),
+              _ptr(seq_ids), int(draw0), use_T, int(g), int(top_k or 0), top_p_fixed(top_p), _ptr(out["acc_tokens"]),
+              _ptr(out["acc_nodes"]), acc_stride, _ptr(out["acc_len"]), _ptr(out["last_node"]),
+              _ptr(out["correction"]), _ptr(out["state"]), _ptr(err_flag), _stream())
+    return out
+
+
+def accept_finalize(walk, old_len, *, max_length, eos_token_id, finished=None, pending_root=None):
+    _dev(old_len)
+    _i32(old_len, "old_len")
+    B = walk["acc_len"].numel()
+    if finished is None:
+        finished = torch.empty(B, dtype=torch.int32, device=old_len.device)
+    _lib.call("fg_accept_finalize", _ptr(walk["acc_tokens"]), _ptr(walk["acc_nodes"]), walk["acc_tokens"].stride(0),
+              _ptr(walk["acc_len"]), _ptr(walk["last_node"]), _ptr(walk["correction"]), _ptr(old_len),
+              int(max_length), -1 if eos_token_id is None else int(eos_token_id), _ptr(finished),
+              _ptr(pending_root), B, _stream())
+    return finished
+
+
+def kv_path_gather(tensor_ptrs, *, batch, kv_heads, head_dim, elem_bytes, strides, capacity, seq_len, acc_nodes,
+                   acc_len, tree_nodes, row_map=None, err_flag=None):
+    """tensor_ptrs: int64 device tensor of cache base addresses (K0, V0, K1, V1, ...)."""
+    _dev(tensor_ptrs, seq_len, acc_nodes, acc_len, row_map, err_flag)
+    for t, n in ((seq_len, "seq_len"), (acc_nodes, "acc_nodes"), (acc_len, "acc_len"), (row_map, "row_map")):
+        _i32(t, n)
+    bs, hs, rs = strides
+    _lib.call("fg_kv_path_gather", _ptr(tensor_ptrs), tensor_ptrs.numel(), batch, kv_heads, head_dim, elem_bytes, bs,
+              hs, rs, capacity, _ptr(seq_len), _ptr(row_map), _ptr(acc_nodes), acc_nodes.stride(0), _ptr(acc_len),
+              int(tree_nodes), _ptr(err_flag), _stream())

@@ -1,0 +1,48 @@
+"""The C-ABI library loads and exports every symbol include/flashgrpo_amd.h declares (no GPU calls)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "flashgrpo_amd.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(fg_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    from flashgrpo_amd import _lib
+
+    assert _declared() == _lib.exported_symbols()
+
+
+def test_library_exports_every_declared_symbol():
+    from flashgrpo_amd import _lib
+
+    path = _lib.library_path()
+    if not os.path.exists(path):
+        pytest.skip("native library not built (run __graft_entry__.build())")
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True).stdout
+    exported = set(re.findall(r" T (fg_[a-z0-9_]+)", out))
+    missing = [s for s in _declared() if s not in exported]
+    assert not missing, missing
+
+
+def test_library_loads_and_reports_errors_without_gpu_work():
+    from flashgrpo_amd import _lib
+
+    if not os.path.exists(_lib.library_path()):
+        pytest.skip("native library not built")
+    lib = _lib.load()
+    assert lib.fg_version() == 1
+    # A shape error is caught on the host before any launch.
+    rc = lib.fg_kv_path_gather(None, 0, 0, 0, 0, 2, 0, 0, 0, 0, None, None, None, 0, None, 0, None, None)
+    assert rc != 0 and b"null pointer" in lib.fg_last_error()
+    rc = lib.fg_sample_tokens(ctypes.c_void_p(64), 1, 8, 1, 0, None, None, None, 0, 0, 0, 0, None, 0, 1.0, 0, 0, 0,
+                              ctypes.c_void_p(64), None)
+    assert rc != 0 and b"vocab" in lib.fg_last_error()

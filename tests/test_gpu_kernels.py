@@ -1,0 +1,434 @@
+"""Kernel-level parity of the HIP path against the CPU oracle (through the C ABI).
+
+Integer/index work (top-k, tree layout, sampling, acceptance, KV gather) must
+be bit-exact; floating-point contractions are checked with the tolerance the
+north star states: max|a-b|/max|b| <= 2e-2 in bf16 and <= 1e-5 in fp32.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv as OK
+from oracle import sampling as OS
+from oracle import tree as OT
+from oracle import model as OM
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from flashgrpo_amd import _lib
+
+    _lib.load()
+
+
+def K():
+    from flashgrpo_amd import kernels
+
+    return kernels
+
+
+def rel_err(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def to_np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def noise_i32(n_rows, n_cols, seed):
+    rng = np.random.default_rng(seed)
+    u = rng.integers(0, 2 ** 32, size=(n_rows, n_cols), dtype=np.uint64)
+    return u, torch.from_numpy(u.astype(np.uint32).view(np.int32)).to(DEV)
+
+
+# ------------------------------------------------------------------ KV gather
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_kv_path_gather_matches_oracle(dtype):
+    torch.manual_seed(0)
+    L, B, H, S, D = 3, 5, 2, 40, 128 if dtype == torch.bfloat16 else 64
+    caches = [torch.randn(B, H, S, D, device=DEV).to(dtype) for _ in range(2 * L)]
+    before = [to_np(c) for c in caches]
+    seq = np.array([3, 10, 0, 20, 7], np.int32)
+    paths = [[0, 2, 5, 7], [0], [0, 1], [0, 3, 4], [0, 6, 8, 9, 11]]
+    width = 5
+    nodes = np.zeros((B, width), np.int32)
+    for b, p in enumerate(paths):
+        nodes[b, :len(p)] = p
+    lens = np.array([len(p) for p in paths], np.int32)
+    ptrs = torch.tensor([c.data_ptr() for c in caches], dtype=torch.int64, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    c0 = caches[0]
+    K().kv_path_gather(ptrs, batch=B, kv_heads=H, head_dim=D, elem_bytes=c0.element_size(),
+                       strides=(c0.stride(0), c0.stride(1), c0.stride(2)), capacity=S,
+                       seq_len=torch.from_numpy(seq).to(DEV), acc_nodes=torch.from_numpy(nodes).to(DEV),
+                       acc_len=torch.from_numpy(lens).to(DEV), tree_nodes=12, err_flag=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    for c, bef in zip(caches, before):
+        want = OK.compact_rows(bef, seq, nodes, lens)
+        assert np.array_equal(to_np(c), want)
+
+
+def test_kv_path_gather_seed17_golden_and_bounds():
+    import json
+    import os
+
+    gold = os.path.join(os.path.dirname(__file__), "golden")
+    arr = np.load(os.path.join(gold, "reference_arrays.npz"))
+    case = json.load(open(os.path.join(gold, "reference_cases.json")))["seed17_kv"]
+    # head_dim 8 fp32 rows are 32 bytes: multiple of 16, so the kernel accepts them
+    key = torch.from_numpy(arr["seed17_key"]).to(DEV).contiguous()
+    val = torch.from_numpy(arr["seed17_value"]).to(DEV).contiguous()
+    B, H, S, D = key.shape
+    acc = case["accepted"]
+    nodes = torch.tensor([p + [p[-1]] * (3 - len(p)) for p in acc], dtype=torch.int32, device=DEV)
+    lens = torch.tensor([len(p) for p in acc], dtype=torch.int32, device=DEV)
+    seq = torch.full((B,), case["old_len"], dtype=torch.int32, device=DEV)
+    ptrs = torch.tensor([key.data_ptr(), val.data_ptr()], dtype=torch.int64, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    K().kv_path_gather(ptrs, batch=B, kv_heads=H, head_dim=D, elem_bytes=4, strides=(key.stride(0), key.stride(1), D),
+                       capacity=S, seq_len=seq, acc_nodes=nodes, acc_len=lens, tree_nodes=4, err_flag=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    old = case["old_len"]
+    for b, p in enumerate(acc):
+        n = len(p)
+        assert np.array_equal(to_np(key)[b, :, :old + n], arr["seed17_expect_key"][b, :, :old + n])
+        assert np.array_equal(to_np(val)[b, :, :old + n], arr["seed17_expect_value"][b, :, :old + n])
+    # out-of-range node: flagged, row untouched
+    before = to_np(key).copy()
+    bad = torch.tensor([[0, 4, 4], [0, 1, 1]], dtype=torch.int32, device=DEV)
+    K().kv_path_gather(ptrs, batch=B, kv_heads=H, head_dim=D, elem_bytes=4, strides=(key.stride(0), key.stride(1), D),
+                       capacity=S, seq_len=seq, acc_nodes=bad, acc_len=torch.tensor([2, 2], dtype=torch.int32,
+                                                                                    device=DEV),
+                       tree_nodes=4, err_flag=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) & 1
+    assert np.array_equal(to_np(key)[0], before[0])
+
+
+# ------------------------------------------------------------------ top-k / layout
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("V,kmax", [(37, 3), (1000, 4), (32000, 8), (152064, 4), (5000, 16), (9, 1)])
+def test_medusa_topk_matches_canonical_order(dtype, V, kmax):
+    g = torch.Generator(device="cpu").manual_seed(V + kmax)
+    R = 24
+    x = torch.randn(R, V, generator=g)
+    x[:4] = torch.round(x[:4] * 2) / 2          # heavy ties
+    x[4, :] = 0.0
+    x[5, ::3] = -0.0
+    xd = x.to(dtype).to(DEV)
+    tok, sc, st = K().medusa_topk(xd, kmax, stats=True)
+    xs = to_np(xd)
+    for r in range(R):
+        ids, vals = OT.topk_canonical(xs[r], kmax)
+        assert tok[r].tolist() == ids.tolist(), r
+        assert np.array_equal(to_np(sc[r]), vals.astype(np.float32) + 0.0)
+        lse = np.log(np.sum(np.exp(xs[r].astype(np.float64) - xs[r].max()))) + xs[r].max()
+        assert abs(float(st[r, 1]) - lse) < 1e-4 * max(1.0, abs(lse))
+        assert float(st[r, 0]) == float(xs[r].max())
+
+
+def test_tree_layout_matches_oracle_trees():
+    rng = np.random.default_rng(3)
+    for ks, budget, B, V in [([4, 2], 16, 8, 500), ([4, 2, 1, 1], 32, 6, 300), ([4, 3, 2], 16, 3, 64)]:
+        logits = [rng.standard_normal((B, V)).astype(np.float32) for _ in ks]
+        roots = rng.integers(0, V, B)
+        plan = OT.Plan(budget, len(ks), ks, OT.dense_node_count(ks), "fixed", "dense")
+        trees = OT.build_batch_trees(roots, logits, plan)
+        parents, depths, ranks = OT.dense_topology(ks, budget)
+        N = len(parents)
+        lg = torch.from_numpy(np.concatenate(logits)).to(DEV)
+        tok, sc, _ = K().medusa_topk(lg, max(ks))
+        out, scores = K().tree_layout(tok, sc, B, torch.from_numpy(roots.astype(np.int32)).to(DEV),
+                                      torch.tensor(depths, dtype=torch.int32, device=DEV),
+                                      torch.tensor(ranks, dtype=torch.int32, device=DEV), N)
+        for b, t in enumerate(trees):
+            assert out[b].tolist() == t.tokens
+            assert np.allclose(to_np(scores[b]), np.array(t.scores, np.float32))
+
+
+# ------------------------------------------------------------------ sampling
+MODES = [dict(), dict(temperature=0.7), dict(temperature=1.3, top_p=0.95), dict(top_p=0.5), dict(top_k=5),
+         dict(top_k=50, top_p=0.8, temperature=0.9), dict(greedy=True), dict(temperature=0.0),
+         dict(temperature=None), dict(top_p=0.999)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("mode", MODES, ids=[str(m) for m in MODES])
+def test_sample_tokens_bit_exact(dtype, mode):
+    g = torch.Generator(device="cpu").manual_seed(11)
+    rows = []
+    for V, scale in [(4, 1.0), (37, 3.0), (1000, 2.0), (32000, 1.0), (32000, 6.0)]:
+        for r in range(6):
+            x = torch.randn(V, generator=g) * scale
+            if r == 0:
+                x = torch.zeros(V)
+            if r == 1:
+                x = torch.round(x)
+            rows.append(x)
+    for x in rows:
+        V = x.numel()
+        xd = x.to(dtype).to(DEV).reshape(1, V).repeat(8, 1)
+        u, nz = noise_i32(8, 1, V)
+        out = K().sample_tokens(xd, noise=nz, temperature=mode.get("temperature", 1.0),
+                                greedy=mode.get("greedy", False), top_k=mode.get("top_k"),
+                                top_p=mode.get("top_p", 1.0))
+        xs = to_np(xd[0])
+        want = [OS.sample_row(xs, int(u[i, 0]), do_sample=not mode.get("greedy", False),
+                              temperature=mode.get("temperature", 1.0), top_p=mode.get("top_p", 1.0),
+                              top_k=mode.get("top_k")) for i in range(8)]
+        assert out.tolist() == want, (V, mode)
+
+
+def test_sample_tokens_full_vocab_and_counter_noise():
+    g = torch.Generator(device="cpu").manual_seed(5)
+    V = 152064
+    x = (torch.randn(6, V, generator=g) * 2).to(torch.bfloat16).to(DEV)
+    seq = torch.tensor([0, 5, 9, 100, 7, 3], dtype=torch.int32, device=DEV)
+    for kw in [dict(), dict(top_p=0.95), dict(top_k=40, temperature=0.7)]:
+        out = K().sample_tokens(x, seed=1234, step=17, seq_ids=seq, draw=2, **kw)
+        xs = to_np(x)
+        want = [OS.sample_row(xs[i], OS.counter_noise(1234, 17, int(seq[i]), 2), **kw) for i in range(6)]
+        assert out.tolist() == want
+
+
+def test_sampling_law_matches_reference_distribution_tests():
+    # flashgrpo/tests/test_exact_acceptance_distribution.py:17-37 on the device sampler
+    for i, (vals, top_p) in enumerate([([5.0, 4.0, 0.0, -1.0], 0.85), ([0.0, 0.0, 0.0, 0.0], 0.75)]):
+        n = 50000
+        x = torch.tensor(vals, dtype=torch.float32, device=DEV).reshape(1, 4).expand(n, 4).contiguous()
+        # pad rows to a multiple-of-8 stride
+        xp = torch.full((n, 8), -1e30, device=DEV)
+        xp[:, :4] = x
+        out = K().sample_tokens(xp[:, :4], seed=321 + i, temperature=0.8, top_p=top_p)
+        obs = np.bincount(out.cpu().numpy(), minlength=4) / n
+        exp = OS.logits_to_probs(np.array(vals), temperature=0.8, top_p=top_p)
+        assert np.max(np.abs(obs - exp)) < 0.015
+
+
+# ------------------------------------------------------------------ acceptance walk
+def _walk_case(rng, B, ks, budget, V, planted):
+    parents, depths, ranks = OT.dense_topology(ks, budget)
+    N = len(parents)
+    toks = rng.integers(0, V, (B, N)).astype(np.int32)
+    trees = [OT.Tree(toks[b].tolist(), parents, depths) for b in range(B)]
+    _, _, slots = OT.internal_slots(trees)
+    R = sum(1 for s in slots for v in s if v >= 0)
+    packed = rng.standard_normal((R, V)).astype(np.float32)
+    if planted:
+        for b, t in enumerate(trees):
+            for n in range(N):
+                kids = t.children(n)
+                if kids and slots[b][n] >= 0:
+                    packed[slots[b][n], t.tokens[kids[min(b % len(kids), len(kids) - 1)]]] += 12.0
+    return trees, parents, N, slots, packed
+
+
+@pytest.mark.parametrize("planted", [False, True])
+@pytest.mark.parametrize("emit_correction", [False, True])
+@pytest.mark.parametrize("mode", [dict(), dict(top_p=0.9), dict(greedy=True), dict(temperature=0.7, top_k=20)])
+def test_accept_walk_bit_exact(planted, emit_correction, mode):
+    rng = np.random.default_rng(7 + planted)
+    B, ks, budget, V = 16, [4, 2, 1, 1], 32, 64
+    trees, parents, N, slots, packed = _walk_case(rng, B, ks, budget, V, planted)
+    D = len(ks)
+    u, nz = noise_i32(B, D, 99)
+    lg = torch.from_numpy(packed).to(DEV)
+    tt = torch.tensor([t.tokens for t in trees], dtype=torch.int32, device=DEV)
+    pp = torch.tensor([parents] * B, dtype=torch.int32, device=DEV)
+    nn = torch.full((B,), N, dtype=torch.int32, device=DEV)
+    sm = torch.tensor(slots, dtype=torch.int32, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    greedy = mode.get("greedy", False)
+    w = K().accept_walk(lg, tt, pp, nn, max_walk_steps=D, slot_map=sm, noise=nz, temperature=mode.get("temperature", 1.0),
+                        greedy=greedy, top_k=mode.get("top_k"), top_p=mode.get("top_p", 1.0), err_flag=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 0
+    res = OS.accept_walk(trees, packed, u.tolist(), do_sample=not greedy, temperature=mode.get("temperature", 1.0),
+                         top_p=mode.get("top_p", 1.0), top_k=mode.get("top_k"), slots=slots, emit_correction=True)
+    toks, nodes, last, corr = res
+    L = w["acc_len"].tolist()
+    for b in range(B):
+        assert L[b] == len(toks[b])
+        assert w["acc_tokens"][b, :L[b]].tolist() == toks[b]
+        assert w["acc_nodes"][b, :L[b]].tolist() == nodes[b]
+        assert int(w["last_node"][b]) == last[b]
+        assert int(w["correction"][b]) == (-1 if corr[b] is None else corr[b])
+    if planted:
+        assert max(L) == D + 1
+
+
+def test_accept_walk_dense_equals_packed_reference_case():
+    import json
+    import os
+
+    c = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_cases.json")))["acceptance"]["packed"]
+    dense = np.full((2, 4, 16), -10.0, np.float32)
+    for h in c["hot"]:
+        dense[h[0], h[1], h[2]] = 10.0
+    packed = np.stack([dense[0, 0], dense[0, 1], dense[1, 0], dense[1, 2]])
+    tt = torch.tensor([t["tokens"] for t in c["trees"]], dtype=torch.int32, device=DEV)
+    pp = torch.tensor([t["parents"] for t in c["trees"]], dtype=torch.int32, device=DEV)
+    nn = torch.full((2,), 4, dtype=torch.int32, device=DEV)
+    pad = lambda a: torch.from_numpy(np.concatenate([a, np.full(a.shape[:-1] + (0,), 0, np.float32)], -1)).to(DEV)
+    r1 = K().accept_walk(pad(dense.reshape(8, 16)), tt, pp, nn, max_walk_steps=2, greedy=True)
+    r2 = K().accept_walk(pad(packed), tt, pp, nn, max_walk_steps=2, greedy=True,
+                         slot_map=torch.tensor(c["slots"], dtype=torch.int32, device=DEV))
+    for r in (r1, r2):
+        L = r["acc_len"].tolist()
+        assert [r["acc_tokens"][b, :L[b]].tolist() for b in range(2)] == c["expect_tokens"]
+        assert [r["acc_nodes"][b, :L[b]].tolist() for b in range(2)] == c["expect_nodes"]
+        assert r["last_node"].tolist() == c["expect_last"]
+
+
+def test_accept_finalize_matches_oracle_clamp():
+    rng = np.random.default_rng(1)
+    B, W = 12, 5
+    acc = rng.integers(0, 6, (B, W)).astype(np.int32)
+    nodes = np.tile(np.arange(W, dtype=np.int32), (B, 1))
+    lens = rng.integers(1, W + 1, B).astype(np.int32)
+    corr = rng.integers(-1, 6, B).astype(np.int32)
+    old = rng.integers(90, 101, B).astype(np.int32)
+    walk = dict(acc_tokens=torch.from_numpy(acc).to(DEV), acc_nodes=torch.from_numpy(nodes).to(DEV),
+                acc_len=torch.from_numpy(lens.copy()).to(DEV), last_node=torch.zeros(B, dtype=torch.int32, device=DEV),
+                correction=torch.from_numpy(corr).to(DEV))
+    pend = torch.empty(B, dtype=torch.int32, device=DEV)
+    fin = K().accept_finalize(walk, torch.from_numpy(old).to(DEV), max_length=100, eos_token_id=2, pending_root=pend)
+    torch.cuda.synchronize()
+    for b in range(B):
+        t, n, f, _ = OS.clamp_accepted(acc[b, :lens[b]].tolist(), nodes[b, :lens[b]].tolist(), remaining=100 - old[b],
+                                       eos_token_id=2, old_len=old[b], max_length=100)
+        assert int(walk["acc_len"][b]) == len(t) and bool(fin[b]) == f
+        assert int(walk["last_node"][b]) == n[-1]
+        want_p = corr[b] if (corr[b] >= 0 and len(t) == lens[b] and not f) else -1
+        assert int(pend[b]) == want_p
+
+
+# ------------------------------------------------------------------ contractions
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("M,N,Kd", [(1, 1000, 128), (64, 4096, 512), (65, 1024, 256), (200, 3000, 512),
+                                    (300, 512, 1536)])
+def test_lm_head_matches_fp32_reference(dtype, M, N, Kd):
+    torch.manual_seed(M + N)
+    x = (torch.randn(M + 7, Kd, device=DEV) * 0.5).to(dtype)
+    w = (torch.randn(N, Kd, device=DEV) * 0.05).to(dtype)
+    idx = torch.randperm(M + 7, device=DEV)[:M].to(torch.int32)
+    out = K().lm_head(x, w, row_index=idx, out_dtype=torch.float32)
+    ref = x.float()[idx.long()] @ w.float().t()
+    assert rel_err(to_np(out), to_np(ref)) < TOL[dtype]
+    out2 = K().lm_head(x, w)
+    assert rel_err(to_np(out2), to_np(x.float() @ w.float().t())) < TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_medusa_heads_match_oracle(dtype):
+    rng = np.random.default_rng(2)
+    B, H, nh = 16, 512, 3
+    heads = OM.random_medusa(H, nh, seed=4, std=0.05)
+    heads[1]["ln_w"] = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    heads[1]["ln_b"] = (0.1 * rng.standard_normal(H)).astype(np.float32)
+    h = rng.standard_normal((B, H)).astype(np.float32)
+    hd = torch.from_numpy(h).to(DEV).to(dtype)
+    out = K().medusa_heads(hd, torch.from_numpy(np.stack([x["ln_w"] for x in heads])).to(DEV),
+                           torch.from_numpy(np.stack([x["ln_b"] for x in heads])).to(DEV),
+                           torch.from_numpy(np.stack([x["fc_w"] for x in heads])).to(DEV).to(dtype),
+                           torch.from_numpy(np.stack([x["fc_b"] for x in heads])).to(DEV).to(dtype),
+                           out_dtype=torch.float32)
+    hs = to_np(hd)
+    for i, hp in enumerate(heads):
+        hp = dict(hp, fc_w=to_np(torch.from_numpy(hp["fc_w"]).to(dtype)), fc_b=to_np(torch.from_numpy(hp["fc_b"]).to(dtype)))
+        want = OM.medusa_project(hs, hp)
+        assert rel_err(to_np(out[i * B:(i + 1) * B]), want) < TOL[dtype]
+
+
+# ------------------------------------------------------------------ attention and layer pieces
+def _attn_reference(q, kc, vc, seq, anc, N, G):
+    B, _, Hq, d = q.shape
+    out = np.zeros_like(q, dtype=np.float64)
+    for b in range(B):
+        for n in range(N):
+            for hq in range(Hq):
+                hk = hq // G
+                s0 = seq[b]
+                keys = list(range(s0)) + [s0 + m for m in range(N) if (int(anc[b][n]) >> m) & 1]
+                kk = kc[b, hk, keys].astype(np.float64)
+                vv = vc[b, hk, keys].astype(np.float64)
+                s = kk @ q[b, n, hq].astype(np.float64) / np.sqrt(d)
+                p = np.exp(s - s.max())
+                out[b, n, hq] = (p / p.sum()) @ vv
+    return out
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float32, 64), (torch.float32, 128)])
+@pytest.mark.parametrize("ks,budget,Hq,Hkv", [([4, 2, 1, 1], 32, 28, 4), ([4, 2], 16, 8, 2), ([3], 4, 12, 2),
+                                               ([1] * 63, 64, 4, 1)])
+def test_tree_attention_matches_reference(dtype, d, ks, budget, Hq, Hkv):
+    rng = np.random.default_rng(len(ks) + Hq)
+    parents, depths, _ = OT.dense_topology(ks, budget)
+    N = len(parents)
+    B, S = 3, 300
+    seq = np.array([0, 37, 200], np.int32)[:B] if N < 64 else np.array([5, 100, 230], np.int32)
+    anc_bits = OT.ancestor_bits(parents)
+    anc = np.array([anc_bits] * B, dtype=np.uint64)
+    q = rng.standard_normal((B, N, Hq, d)).astype(np.float32)
+    kc = rng.standard_normal((B, Hkv, S, d)).astype(np.float32)
+    vc = rng.standard_normal((B, Hkv, S, d)).astype(np.float32)
+    qt = torch.from_numpy(q).to(DEV).to(dtype)
+    kt = torch.from_numpy(kc).to(DEV).to(dtype)
+    vt = torch.from_numpy(vc).to(DEV).to(dtype)
+    anct = torch.from_numpy(anc.view(np.int64)).to(DEV)
+    out = K().tree_attention(qt, kt, vt, seq_len=torch.from_numpy(seq).to(DEV), anc=anct, num_nodes=N, q_heads=Hq,
+                             kv_heads=Hkv, head_dim=d)
+    want = _attn_reference(to_np(qt), to_np(kt), to_np(vt), seq, anc, N, Hq // Hkv)
+    assert rel_err(to_np(out), want) < TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rope_kv_write_rmsnorm_swiglu(dtype):
+    rng = np.random.default_rng(9)
+    B, N, Hq, Hkv, d, S = 3, 5, 4, 2, 64, 50
+    seq = np.array([0, 7, 30], np.int32)
+    pos_off = np.array([0, 1, 1, 2, 2], np.int32)
+    inv = OM.inv_freq_table(d, 1e6)
+    qkv = rng.standard_normal((B * N, (Hq + 2 * Hkv) * d)).astype(np.float32)
+    qkvd = torch.from_numpy(qkv).to(DEV).to(dtype)
+    qo = torch.empty(B, N, Hq, d, dtype=dtype, device=DEV)
+    kc = torch.zeros(B, Hkv, S, d, dtype=dtype, device=DEV)
+    vc = torch.zeros(B, Hkv, S, d, dtype=dtype, device=DEV)
+    K().rope_kv_write(qkvd, batch=B, num_nodes=N, q_heads=Hq, kv_heads=Hkv, head_dim=d,
+                      seq_len=torch.from_numpy(seq).to(DEV), pos_offset=torch.from_numpy(pos_off).to(DEV),
+                      inv_freq=torch.from_numpy(inv).to(DEV), q_out=qo, k_cache=kc, v_cache=vc)
+    x = to_np(qkvd).reshape(B, N, Hq + 2 * Hkv, d)
+    pos = seq[:, None] + pos_off[None]
+    cos, sin = OM.rope_cos_sin(pos, inv)
+    qr = OM.apply_rope(x[:, :, :Hq], cos[:, :, None], sin[:, :, None])
+    kr = OM.apply_rope(x[:, :, Hq:Hq + Hkv], cos[:, :, None], sin[:, :, None])
+    tol = TOL[dtype] if dtype == torch.bfloat16 else 2e-6
+    assert rel_err(to_np(qo), qr) < tol
+    for b in range(B):
+        for n in range(N):
+            assert rel_err(to_np(kc[b, :, seq[b] + n]), kr[b, n]) < tol
+            assert np.array_equal(to_np(vc[b, :, seq[b] + n]), x[b, n, Hq + Hkv:])
+    # rmsnorm with fused residual add
+    H = 384
+    xr = torch.from_numpy(rng.standard_normal((7, H)).astype(np.float32)).to(DEV).to(dtype)
+    dl = torch.from_numpy(rng.standard_normal((7, H)).astype(np.float32)).to(DEV).to(dtype)
+    w = torch.from_numpy((1 + 0.1 * rng.standard_normal(H)).astype(np.float32)).to(DEV).to(dtype)
+    summed = (xr.float() + dl.float()).to(dtype)
+    y = K().rmsnorm(xr, w, 1e-6, delta=dl)
+    assert torch.equal(xr, summed)
+    assert rel_err(to_np(y), OM.rmsnorm(to_np(summed), to_np(w), 1e-6)) < TOL[dtype]
+    gu = torch.from_numpy(rng.standard_normal((5, 2 * 96)).astype(np.float32)).to(DEV).to(dtype)
+    sg = K().swiglu(gu)
+    g_ = to_np(gu)
+    assert rel_err(to_np(sg), OM.silu(g_[:, :96].astype(np.float64)) * g_[:, 96:]) < TOL[dtype]
