@@ -1,0 +1,298 @@
+#!/usr/bin/env python
+"""Rollout benchmark of the FlashGRPO speculative verify step on one MI355X.
+
+A step is one verify round of FlashMedusaDecoder over every active sequence:
+root draw, Medusa heads + tied LM head, top-k tree, tree-attention verify
+forward, packed internal-node LM head, exact_target walk and accepted-path KV
+compaction. Default workload: the Qwen2.5-7B shape (28 layers, hidden 3584,
+28/4 heads, MLP 18944, vocab 152064, bf16), 64 sequences (8 prompts x 8 GRPO
+repeats) with a 2048-token uniform-random prefix, 4 tied Medusa heads, adaptive
+concurrency-aware tree (cpeak 2048 -> 32-node budget), temperature 1.0.
+Weights are seeded random init; the prefix is really prefilled (untimed).
+
+Prints one JSON line: rollout tok/s (emitted tokens over the timed verify
+rounds), per-step latency, the roofline of the dominant hand-written kernel
+(HIP events on the launch stream) and the CPU oracle baseline on a bounded
+sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "ss-grpo_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
+
+WORKLOADS = {
+    "7b": dict(target="qwen25_7b", prompts=8, repeats=8, prefix=2048, heads=4, tree_mode="concurrency_aware",
+               cpeak=2048, max_nodes=32, max_depth=5, topk=(4, 3, 2), adaptive=True, temperature=1.0,
+               name="qwen2.5-7b-shape B64 P2048 4 Medusa heads adaptive 32-node tree"),
+    "1.5b": dict(target="qwen25_1p5b", prompts=4, repeats=8, prefix=512, heads=3, tree_mode="concurrency_aware",
+                 cpeak=512, max_nodes=16, max_depth=4, topk=(4, 3, 2), adaptive=False, temperature=1.0,
+                 name="qwen2.5-1.5b-shape B32 P512 3 Medusa heads 16-node tree"),
+    "14b": dict(target="qwen25_14b", prompts=16, repeats=8, prefix=4096, heads=4, tree_mode="concurrency_aware",
+                cpeak=8192, max_nodes=64, max_depth=5, topk=(4, 3, 2), adaptive=False, temperature=1.0,
+                name="qwen2.5-14b-shape B128 P4096 4 Medusa heads 64-node tree"),
+    "tiny": dict(target="tiny", prompts=4, repeats=2, prefix=256, heads=3, tree_mode="fixed", cpeak=64,
+                 max_nodes=16, max_depth=4, topk=(4, 3, 2), adaptive=False, temperature=1.0,
+                 name="tiny-qwen2 B8 P256 3 Medusa heads fixed 16-node tree"),
+}
+
+
+class _NoEosTokenizer:
+    pad_token_id = 0
+    eos_token_id = -1  # synthetic ids: no end-of-sequence token, rows run to max_length
+
+
+def build(work, dtype, seed=0):
+    import torch
+
+    from flashgrpo_amd.decoding import FlashMedusaConfig, FlashMedusaDecoder
+    from flashgrpo_amd.models import MedusaHeads, TargetConfig, TargetModel
+
+    cfg = getattr(TargetConfig, work["target"])()
+    model = TargetModel.random(cfg, seed=seed, dtype=dtype, device="cuda")
+    heads = MedusaHeads.random(cfg.hidden, cfg.vocab, work["heads"], seed=seed + 1, device="cuda")
+    dcfg = FlashMedusaConfig(num_medusa_heads=work["heads"], tree_mode=work["tree_mode"], cpeak_nodes=work["cpeak"],
+                             max_tree_nodes_per_seq=work["max_nodes"], max_tree_depth=work["max_depth"],
+                             fixed_tree_topk_by_depth=tuple(work["topk"]), adaptive_tree_enabled=work["adaptive"],
+                             adaptive_min_topk_by_depth=(1, 1, 1), temperature=work["temperature"], top_p=work["top_p"],
+                             noise_seed=seed + 2)
+    return cfg, model, heads, FlashMedusaDecoder(model, heads, _NoEosTokenizer(), dcfg)
+
+
+def algorithmic_work(cfg, rnd, seq_before, elem):
+    """Per-kernel algorithmic bytes / flops of one verify round (the roofline numerators)."""
+    B, N, I, nh = rnd["batch"], rnd["num_nodes"], rnd["internal"], rnd["heads"]
+    H, V, d, Hq, Hkv, L = cfg.hidden, cfg.vocab, cfg.head_dim, cfg.q_heads, cfg.kv_heads, cfg.num_layers
+    keys = sum(int(s) + N for s in seq_before)
+    attn_bytes = 2 * Hkv * keys * d * elem + 2 * B * N * Hq * d * elem       # per layer launch
+    attn_flops = 4 * Hq * N * d * keys                                          # per layer launch
+    M = B * I
+    w = {
+        "fg_tree_attention": dict(bytes=attn_bytes, flops=attn_flops, launches=L),
+        "fg_lm_head:tree": dict(flops=2 * M * H * V, bytes=H * V * elem + M * H * elem + M * V * elem, launches=1),
+        "fg_lm_head:medusa": dict(flops=2 * nh * B * H * V, bytes=H * V * elem + nh * B * (H + V) * elem, launches=1),
+        "fg_medusa_heads": dict(flops=2 * nh * B * H * H, bytes=nh * H * H * elem, launches=1),
+        "fg_medusa_topk": dict(bytes=nh * B * V * elem, launches=1),
+        "fg_sample_tokens": dict(bytes=B * V * elem, launches=1),
+        "fg_accept_walk": dict(bytes=int(rnd["walk_draws"].sum()) * V * elem, launches=1),
+        "fg_kv_path_gather": dict(bytes=2 * L * 2 * Hkv * int(rnd["acc_len"].sum()) * d * elem, launches=1),
+    }
+    return w
+
+
+def cpu_baseline(model, heads, r, work, seed, layers=2):
+    """Oracle (numpy fp32) verify round on the host: same shapes, decoder stack cut to
+    `layers` of L layers and its forward time scaled back to L layers."""
+    import numpy as np
+    import torch
+
+    from oracle import decode as OD
+    from oracle import model as OM
+
+    cfg = model.cfg
+    nl = min(layers, cfg.num_layers)
+    f = lambda t: t.detach().float().cpu().numpy()
+    qd, kd = cfg.q_heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    W = {"embed": f(model.w["embed"]), "final_norm": f(model.w["final_norm"]), "layers": [],
+         "inv_freq": model.inv_freq.cpu().numpy()}
+    W["lm_head"] = W["embed"] if cfg.tie_word_embeddings else f(model.w["lm_head"])
+    for lw in model.w["layers"][:nl]:
+        qkv = f(lw["qkv_w"])
+        b = f(lw["qkv_b"]) if lw["qkv_b"] is not None else None
+        gu = f(lw["gate_up_w"])
+        W["layers"].append({"input_norm": f(lw["input_norm"]), "q_w": qkv[:qd], "k_w": qkv[qd:qd + kd],
+                            "v_w": qkv[qd + kd:], "q_b": None if b is None else b[:qd],
+                            "k_b": None if b is None else b[qd:qd + kd], "v_b": None if b is None else b[qd + kd:],
+                            "o_w": f(lw["o_w"]), "post_norm": f(lw["post_norm"]), "gate_w": gu[:cfg.intermediate],
+                            "up_w": gu[cfg.intermediate:], "down_w": f(lw["down_w"])})
+    hd = [{"ln_w": f(h.norm.weight), "ln_b": f(h.norm.bias),
+           "fc_w": f(h.fc.weight.to(model.dtype)), "fc_b": f(h.fc.bias.to(model.dtype))} for h in heads.heads]
+    ocfg = OM.ModelConfig(nl, cfg.hidden, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.intermediate, cfg.vocab,
+                          cfg.rope_theta, cfg.rms_eps, cfg.qkv_bias, cfg.tie_word_embeddings)
+    cap = int(r.seq_h.max()) + 72
+    rows = r.row_map.long()
+    st = OD.State([f(r.cache.kv[l, 0].index_select(0, rows)[:, :, :cap]) for l in range(nl)],
+                  [f(r.cache.kv[l, 1].index_select(0, rows)[:, :, :cap]) for l in range(nl)],
+                  r.seq_h.copy(), f(r.hidden), f(r.logits), rows.cpu().numpy(),
+                  np.full(len(r.active), -1, np.int64))
+    spec = OD.DecodeSpec(num_medusa_heads=work["heads"], tree_mode=work["tree_mode"], cpeak_nodes=work["cpeak"],
+                         max_tree_nodes_per_seq=work["max_nodes"], max_tree_depth=work["max_depth"],
+                         fixed_tree_topk_by_depth=tuple(work["topk"]), adaptive_tree_enabled=work["adaptive"],
+                         temperature=work["temperature"], top_p=work["top_p"])
+    threads = len(os.sched_getaffinity(0))
+    try:
+        from threadpoolctl import threadpool_info
+
+        blas = [p["num_threads"] for p in threadpool_info() if p.get("user_api") == "blas"]
+        threads = max(blas) if blas else threads
+    except Exception:
+        pass
+    t0 = time.perf_counter()
+    out = OD.verify_round(ocfg, W, hd, st, spec, seed, 0, 10 ** 9, dtype=np.float32)
+    t_round = time.perf_counter() - t0
+    tree = out["trees"][0]
+    B, N = len(r.active), tree.node_count
+    allowed = np.zeros((B, N, N), bool)
+    for n in range(N):
+        for a in tree.ancestors_including_self(n):
+            allowed[:, n, a] = True
+    valid = np.arange(st.k[0].shape[2])[None, :] < st.seq_len[:, None]
+    toks = np.array([t.tokens for t in out["trees"]])
+    t1 = time.perf_counter()
+    OM.forward(ocfg, W, toks, st.seq_len[:, None] + np.asarray(tree.depths)[None] - 1, st.k, st.v, valid, allowed,
+               dtype=np.float32)
+    t_fwd = time.perf_counter() - t1
+    t_est = t_round + (cfg.num_layers / nl - 1.0) * t_fwd
+    tokens = sum(len(t) for t in out["acc_tokens"])
+    return {"value": round(tokens / t_est, 3), "unit": "tok/s", "cores": int(threads), "kind": "port",
+            "sample": (f"one verify round of the same workload (B={B}, N={N}, vocab {cfg.vocab}) through the numpy "
+                       f"oracle in fp32 with the decoder stack cut to {nl} of {cfg.num_layers} layers; measured "
+                       f"{t_round:.2f} s round + {t_fwd:.2f} s {nl}-layer forward, scaled to {cfg.num_layers} layers "
+                       f"= {t_est:.2f} s for {tokens} tokens"),
+            "seconds": round(t_est, 3)}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=16)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="7b", choices=sorted(WORKLOADS))
+    ap.add_argument("--top-p", type=float, default=1.0, help="1.0 for throughput; 0.95 is the reference default")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-layers", type=int, default=2)
+    ap.add_argument("--seed", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (sequences shard by data "
+              "parallelism with no exchange inside the verify step; run one process per GPU)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from flashgrpo_amd import timing
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    work = dict(WORKLOADS[args.config], top_p=args.top_p)
+    dtype = torch.float32 if args.config == "tiny" else torch.bfloat16
+    elem = 4 if dtype == torch.float32 else 2
+    log = lambda msg: print(f"bench: {msg}", file=sys.stderr, flush=True)
+    cfg, model, heads, dec = build(work, dtype, seed=args.seed)
+    log(f"built {work['name']} ({dtype})")
+    g = torch.Generator().manual_seed(args.seed + 3)
+    prompts = torch.randint(0, cfg.vocab, (work["prompts"], work["prefix"]), generator=g)
+    # long enough that no row reaches max_length inside the benchmark
+    max_length = work["prefix"] + 8 * (args.warmup + args.steps + 4) + 64
+    t_pre = time.perf_counter()
+    r = dec.start(prompts, torch.ones_like(prompts), repeated_generate_nums=work["repeats"], max_length=max_length)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t_pre
+    log(f"prefill {prefill_s:.1f} s")
+    for _ in range(args.warmup):
+        dec.step(r)
+    log("warmup done")
+    timer = timing.KernelTimer()
+    rounds, seqs = [], []
+    tokens = 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    with timing.active(timer):
+        for _ in range(args.steps):
+            seqs.append(r.seq_h.copy())
+            tokens += dec.step(r)
+            rounds.append(r.last_round)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    kstats = timer.summary()
+    log(f"timed {args.steps} steps in {elapsed:.3f} s")
+
+    # roofline per kernel family: algorithmic work over the measured launch time
+    totals = {}
+    for rnd, sq in zip(rounds, seqs):
+        for name, w in algorithmic_work(cfg, rnd, sq, elem).items():
+            t = totals.setdefault(name, dict(bytes=0, flops=0, launches=0))
+            t["bytes"] += w.get("bytes", 0)
+            t["flops"] += w.get("flops", 0)
+            t["launches"] += w["launches"]
+    kernels = {}
+    for name, t in totals.items():
+        ks = kstats.get(name)
+        if not ks or ks["total_ms"] <= 0:
+            continue
+        sec = ks["total_ms"] / 1e3
+        gbs = t["bytes"] / sec / 1e9
+        tfl = t["flops"] / sec / 1e12
+        peak_f = BF16_PEAK_TFLOPS if dtype == torch.bfloat16 else FP32_PEAK_TFLOPS
+        frac = max(gbs / HBM_PEAK_GBS, tfl / peak_f)
+        kernels[name] = dict(avg_us=round(ks["avg_ms"] * 1e3, 2), launches=ks["count"],
+                             total_ms=round(ks["total_ms"], 3), GBps=round(gbs, 1), TFLOPs=round(tfl, 2),
+                             roofline_frac=round(frac, 4))
+    mine_ms = sum(v["total_ms"] for k, v in kstats.items())
+    dominant = max(kernels, key=lambda k: kernels[k]["total_ms"])
+    t = totals[dominant]
+    ks = kstats[dominant]
+    per_launch_s = ks["avg_ms"] / 1e3
+    n_launch = max(t["launches"], 1)
+    peak_f = BF16_PEAK_TFLOPS if dtype == torch.bfloat16 else FP32_PEAK_TFLOPS
+    bound = "mfma" if t["flops"] / max(t["bytes"], 1) > (peak_f * 1e12) / (HBM_PEAK_GBS * 1e9) else "hbm"
+    if bound == "hbm":
+        achieved = t["bytes"] / n_launch / per_launch_s / 1e9
+        roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                        frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None, kernel=dominant,
+                        bytes_per_launch=int(t["bytes"] / n_launch), avg_launch_us=round(ks["avg_ms"] * 1e3, 2))
+    else:
+        achieved = t["flops"] / n_launch / per_launch_s / 1e12
+        roofline = dict(bound="mfma", achieved=round(achieved, 2), peak=peak_f, unit="TFLOP/s",
+                        frac=round(achieved / peak_f, 4), traffic=None, kernel=dominant,
+                        flops_per_launch=int(t["flops"] / n_launch), avg_launch_us=round(ks["avg_ms"] * 1e3, 2))
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline ...")
+        cpu = cpu_baseline(model, heads, r, work, seed=args.seed + 2, layers=args.cpu_layers)
+        log(f"cpu baseline {cpu['seconds']} s")
+    res = {
+        "metric": "rollout tok/s per MI355X (Qwen2.5-7B shape); verify-step latency; % roofline",
+        "value": round(tokens / elapsed, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if dtype == torch.bfloat16 else "fp32",
+        "data": "synthetic (uniform-random prefix tokens, seeded random-init weights and Medusa heads, counter noise)",
+        "config": {"workload": work["name"], "sequences": len(r.active), "prefix": work["prefix"],
+                   "tree_nodes": rounds[-1]["num_nodes"], "internal_nodes": rounds[-1]["internal"],
+                   "topk_by_depth": r.plan_last.get("topk_by_depth"), "temperature": work["temperature"],
+                   "top_p": work["top_p"], "parallelism": "single GPU"},
+        "tokens": int(tokens),
+        "accept_len_mean": round(tokens / max(sum(x["batch"] for x in rounds), 1), 4),
+        "prefill_s": round(prefill_s, 2),
+        "hand_kernels_ms_per_step": round(mine_ms / args.steps, 3),
+        "roofline": roofline,
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -77,11 +77,13 @@ int fg_tree_layout(const int32_t* cand_tokens, const float* cand_scores, int kst
  * K/V write into cache slots seq_len[b] + n. qkv [batch*num_nodes, (Hq+2Hkv)*d]
  * (row stride ld_qkv); position = seq_len[b] + pos_offset[n]; inv_freq [d/2] fp32;
  * q_out [batch, num_nodes, Hq, d]; caches [Bc, Hkv, capacity, d]; row_map maps b to
- * its cache row (NULL = identity). */
+ * its cache row (NULL = identity). A slot outside [0, capacity) is not written and
+ * sets err_flag bit 8 (err_flag may be NULL). */
 int fg_rope_kv_write(const void* qkv, int dtype, int64_t ld_qkv, int batch, int num_nodes, int q_heads, int kv_heads,
                      int head_dim, const int32_t* seq_len, const int32_t* pos_offset, const float* inv_freq,
                      void* q_out, void* k_cache, void* v_cache, int64_t cache_batch_stride,
-                     int64_t cache_head_stride, const int32_t* row_map, void* stream);
+                     int64_t cache_head_stride, int capacity, const int32_t* row_map, int32_t* err_flag,
+                     void* stream);
 
 /* Tree attention: node n of sequence b attends to cache keys [0, seq_len[b]) and to
  * tree keys seq_len[b] + m for every bit m of anc[b*anc_batch_stride + n].

@@ -123,51 +123,54 @@ def apply_rope(x, cos, sin):
     return x * cos + rot * sin
 
 
-def medusa_project(hidden, head):
+def medusa_project(hidden, head, dtype=F64):
     """h + SiLU(fc(LayerNorm(h))). Follows ``flashgrpo/models/medusa_heads.py:74-78``."""
-    h = np.asarray(hidden, F64)
-    z = layernorm(h, head["ln_w"], head["ln_b"], 1e-5) @ np.asarray(head["fc_w"], F64).T + np.asarray(head["fc_b"], F64)
+    h = np.asarray(hidden, dtype)
+    ln = layernorm(h, head["ln_w"], head["ln_b"], 1e-5).astype(dtype)
+    z = ln @ np.asarray(head["fc_w"], dtype).T + np.asarray(head["fc_b"], dtype)
     return h + silu(z)
 
 
-def medusa_logits(hidden, heads, lm_head, max_heads=None):
+def medusa_logits(hidden, heads, lm_head, max_heads=None, dtype=F64):
     """Per-head logits through the tied LM head.
 
     Follows ``flashgrpo/decoding/flash_medusa_decoder.py:254-294`` (one shared
     vocabulary projection of the concatenated head outputs).
     """
     n = len(heads) if max_heads is None else min(max_heads, len(heads))
-    W = np.asarray(lm_head, F64)
-    return [medusa_project(hidden, heads[i]) @ W.T for i in range(n)]
+    W = np.asarray(lm_head, dtype)
+    return [medusa_project(hidden, heads[i], dtype) @ W.T for i in range(n)]
 
 
 # --------------------------------------------------------------------------- decoder
 def forward(cfg: ModelConfig, W: dict, tokens, positions, past_k, past_v, past_valid, self_allowed,
-            fp32_angles=True):
+            fp32_angles=True, dtype=F64):
     """Decoder forward of N new tokens per row against a cached prefix.
 
     tokens/positions [B, N]; past_k/past_v: per layer [B, Hkv, P, d] (P may be 0);
     past_valid [B, P] bool; self_allowed [B, N, N] bool (query n may see new key m).
     Returns (final-normed hidden [B, N, H], new K list, new V list), new K/V
-    per layer [B, Hkv, N, d] after rotary embedding.
+    per layer [B, Hkv, N, d] after rotary embedding. ``dtype`` is the compute
+    type (float64 for parity checks; float32 for the timed CPU baseline, with
+    weights already in float32 so that no weight copy is made).
     """
     tokens = np.asarray(tokens)
     B, N = tokens.shape
     Hq, Hkv, d, G = cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.group
-    x = np.asarray(W["embed"], F64)[tokens]
+    x = np.asarray(W["embed"], dtype)[tokens]
     cos, sin = rope_cos_sin(positions, W["inv_freq"], fp32_angles)
-    cos, sin = cos[:, :, None, :], sin[:, :, None, :]
+    cos, sin = cos[:, :, None, :].astype(dtype), sin[:, :, None, :].astype(dtype)
     P = 0 if past_k is None or len(past_k) == 0 else past_k[0].shape[2]
     allowed = np.concatenate([np.broadcast_to(np.asarray(past_valid, bool)[:, None, :], (B, N, P)),
                               np.asarray(self_allowed, bool)], axis=-1)
     scale = 1.0 / np.sqrt(d)
     new_k, new_v = [], []
     for li, lw in enumerate(W["layers"]):
-        h = rmsnorm(x, lw["input_norm"], cfg.rms_eps)
+        h = rmsnorm(x, lw["input_norm"], cfg.rms_eps).astype(dtype)
 
         def proj(w, b):
-            y = h @ np.asarray(w, F64).T
-            return y + np.asarray(b, F64) if b is not None else y
+            y = h @ np.asarray(w, dtype).T
+            return y + np.asarray(b, dtype) if b is not None else y
 
         q = apply_rope(proj(lw["q_w"], lw["q_b"]).reshape(B, N, Hq, d), cos, sin)
         k = apply_rope(proj(lw["k_w"], lw["k_b"]).reshape(B, N, Hkv, d), cos, sin)
@@ -175,39 +178,39 @@ def forward(cfg: ModelConfig, W: dict, tokens, positions, past_k, past_v, past_v
         k = k.transpose(0, 2, 1, 3)
         v = v.transpose(0, 2, 1, 3)
         if P:
-            keys = np.concatenate([np.asarray(past_k[li], F64), k], axis=2)
-            vals = np.concatenate([np.asarray(past_v[li], F64), v], axis=2)
+            keys = np.concatenate([np.asarray(past_k[li], dtype), k], axis=2)
+            vals = np.concatenate([np.asarray(past_v[li], dtype), v], axis=2)
         else:
             keys, vals = k, v
-        out = np.empty((B, N, Hq, d))
+        out = np.empty((B, N, Hq, d), dtype=x.dtype)
         for hq in range(Hq):
             kv = hq // G
-            s = np.einsum("bnd,bsd->bns", q[:, :, hq], keys[:, kv]) * scale
+            s = np.matmul(q[:, :, hq], keys[:, kv].transpose(0, 2, 1)) * scale
             s = np.where(allowed, s, -np.inf)
             s = s - s.max(axis=-1, keepdims=True)
             p = np.exp(s)
             p = p / p.sum(axis=-1, keepdims=True)
-            out[:, :, hq] = np.einsum("bns,bsd->bnd", p, vals[:, kv])
-        x = x + out.reshape(B, N, Hq * d) @ np.asarray(lw["o_w"], F64).T
-        h2 = rmsnorm(x, lw["post_norm"], cfg.rms_eps)
-        g = h2 @ np.asarray(lw["gate_w"], F64).T
-        u = h2 @ np.asarray(lw["up_w"], F64).T
-        x = x + (silu(g) * u) @ np.asarray(lw["down_w"], F64).T
+            out[:, :, hq] = np.matmul(p, vals[:, kv])
+        x = x + out.reshape(B, N, Hq * d) @ np.asarray(lw["o_w"], dtype).T
+        h2 = rmsnorm(x, lw["post_norm"], cfg.rms_eps).astype(dtype)
+        g = h2 @ np.asarray(lw["gate_w"], dtype).T
+        u = h2 @ np.asarray(lw["up_w"], dtype).T
+        x = x + ((silu(g) * u) @ np.asarray(lw["down_w"], dtype).T).astype(dtype)
         new_k.append(k)
         new_v.append(v)
-    return rmsnorm(x, W["final_norm"], cfg.rms_eps), new_k, new_v
+    return rmsnorm(x, W["final_norm"], cfg.rms_eps).astype(dtype), new_k, new_v
 
 
-def prefill(cfg, W, tokens, fp32_angles=True):
+def prefill(cfg, W, tokens, fp32_angles=True, dtype=F64):
     """Causal forward of full-length prompts [B, P]; returns (hidden, K list, V list)."""
     tokens = np.asarray(tokens)
     B, P = tokens.shape
     pos = np.broadcast_to(np.arange(P), (B, P))
     causal = np.broadcast_to(np.tril(np.ones((P, P), bool)), (B, P, P))
-    return forward(cfg, W, tokens, pos, None, None, np.zeros((B, 0), bool), causal, fp32_angles)
+    return forward(cfg, W, tokens, pos, None, None, np.zeros((B, 0), bool), causal, fp32_angles, dtype)
 
 
-def tree_verify(cfg, W, tree_tokens, depths, parents, past_k, past_v, seq_len):
+def tree_verify(cfg, W, tree_tokens, depths, parents, past_k, past_v, seq_len, dtype=F64):
     """Tree forward: node n at position seq_len + depth - 1, seeing prefix + ancestors.
 
     Follows the mask/position construction of ``flashgrpo/decoding/tree_attention.py:6-67``
@@ -225,8 +228,8 @@ def tree_verify(cfg, W, tree_tokens, depths, parents, past_k, past_v, seq_len):
                 a = parents[b][a]
     pos = np.asarray(seq_len)[:, None] + np.asarray(depths) - 1
     P = past_k[0].shape[2]
-    return forward(cfg, W, tree_tokens, pos, past_k, past_v, np.ones((B, P), bool), allowed)
+    return forward(cfg, W, tree_tokens, pos, past_k, past_v, np.ones((B, P), bool), allowed, dtype=dtype)
 
 
-def logits(hidden, lm_head):
-    return np.asarray(hidden, F64) @ np.asarray(lm_head, F64).T
+def logits(hidden, lm_head, dtype=F64):
+    return np.asarray(hidden, dtype) @ np.asarray(lm_head, dtype).T

@@ -13,8 +13,8 @@ template <int DT>
 __global__ void __launch_bounds__(256) rope_kv_write_kernel(
     const void* __restrict__ qkv, int64_t ld_qkv, int N, int Hq, int Hkv, int d, const int32_t* __restrict__ seq_len,
     const int32_t* __restrict__ pos_offset, const float* __restrict__ inv_freq, void* __restrict__ q_out,
-    void* __restrict__ k_cache, void* __restrict__ v_cache, int64_t cache_batch, int64_t cache_head,
-    const int32_t* __restrict__ row_map) {
+    void* __restrict__ k_cache, void* __restrict__ v_cache, int64_t cache_batch, int64_t cache_head, int capacity,
+    const int32_t* __restrict__ row_map, int32_t* __restrict__ err_flag) {
   const int tok = blockIdx.x;
   const int b = tok / N, n = tok % N;
   const int s = seq_len[b];
@@ -22,6 +22,8 @@ __global__ void __launch_bounds__(256) rope_kv_write_kernel(
   const int slot = s + n;
   const int cb = row_map ? row_map[b] : b;
   const int half = d / 2;
+  const bool slot_ok = slot >= 0 && slot < capacity;
+  if (!slot_ok && threadIdx.x == 0 && err_flag) atomicOr(err_flag, 8);
   const int64_t row = (int64_t)tok * ld_qkv;
   // q and k heads: rotate pairs (i, i + d/2)
   for (int e = threadIdx.x; e < (Hq + Hkv) * half; e += blockDim.x) {
@@ -37,14 +39,14 @@ __global__ void __launch_bounds__(256) rope_kv_write_kernel(
       int64_t dst = ((int64_t)tok * Hq + h) * d;
       fg::store_elem<DT>(q_out, dst + i, y1);
       fg::store_elem<DT>(q_out, dst + i + half, y2);
-    } else {
+    } else if (slot_ok) {
       int hk = h - Hq;
       int64_t dst = (int64_t)cb * cache_batch + (int64_t)hk * cache_head + (int64_t)slot * d;
       fg::store_elem<DT>(k_cache, dst + i, y1);
       fg::store_elem<DT>(k_cache, dst + i + half, y2);
     }
   }
-  for (int e = threadIdx.x; e < Hkv * d; e += blockDim.x) {
+  for (int e = threadIdx.x; slot_ok && e < Hkv * d; e += blockDim.x) {
     int hk = e / d, i = e % d;
     float x = fg::load_elem<DT>(qkv, row + (int64_t)(Hq + Hkv + hk) * d + i);
     fg::store_elem<DT>(v_cache, (int64_t)cb * cache_batch + (int64_t)hk * cache_head + (int64_t)slot * d + i, x);
@@ -96,7 +98,8 @@ extern "C" {
 int fg_rope_kv_write(const void* qkv, int dtype, int64_t ld_qkv, int batch, int num_nodes, int q_heads, int kv_heads,
                      int head_dim, const int32_t* seq_len, const int32_t* pos_offset, const float* inv_freq,
                      void* q_out, void* k_cache, void* v_cache, int64_t cache_batch_stride,
-                     int64_t cache_head_stride, const int32_t* row_map, void* stream) {
+                     int64_t cache_head_stride, int capacity, const int32_t* row_map, int32_t* err_flag,
+                     void* stream) {
   FG_REQUIRE(qkv && seq_len && pos_offset && inv_freq && q_out && k_cache && v_cache, "fg_rope_kv_write: null pointer");
   FG_REQUIRE(batch > 0 && num_nodes > 0 && q_heads > 0 && kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0,
              "fg_rope_kv_write: bad shape");
@@ -105,11 +108,11 @@ int fg_rope_kv_write(const void* qkv, int dtype, int64_t ld_qkv, int batch, int 
   if (dtype == fg::kBF16)
     hipLaunchKernelGGL(rope_kv_write_kernel<fg::kBF16>, grid, dim3(256), 0, s, qkv, ld_qkv, num_nodes, q_heads,
                        kv_heads, head_dim, seq_len, pos_offset, inv_freq, q_out, k_cache, v_cache,
-                       cache_batch_stride, cache_head_stride, row_map);
+                       cache_batch_stride, cache_head_stride, capacity, row_map, err_flag);
   else
     hipLaunchKernelGGL(rope_kv_write_kernel<fg::kF32>, grid, dim3(256), 0, s, qkv, ld_qkv, num_nodes, q_heads,
                        kv_heads, head_dim, seq_len, pos_offset, inv_freq, q_out, k_cache, v_cache,
-                       cache_batch_stride, cache_head_stride, row_map);
+                       cache_batch_stride, cache_head_stride, capacity, row_map, err_flag);
   return fg::check_launch("fg_rope_kv_write");
 }
 

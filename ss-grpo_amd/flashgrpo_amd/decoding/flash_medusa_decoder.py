@@ -1,0 +1,541 @@
+"""FlashMedusaDecoder: the speculative rollout loop on the device.
+
+Same configuration dataclass, constructor and ``generate`` contract as
+``flashgrpo/decoding/flash_medusa_decoder.py:41-134,550-1229`` (result keys
+included). One verify round, per active sequence:
+
+  root draw            fg_sample_tokens (draw 0; b200 mode: pending correction forced)
+  Medusa proposals     fg_medusa_heads -> fg_lm_head -> fg_medusa_topk (+ row stats)
+  plan / tree          plan_tree (host), adaptive refit from per-head confidence
+                       quantiles, cached TreeTopology, fg_tree_layout
+  tree verify          TargetModel.forward (tree attention with ancestor bit masks)
+  packed LM head       fg_lm_head over internal nodes only
+  acceptance           fg_accept_walk (draws 1..D) + fg_accept_finalize (clamp, EOS)
+  cache update         fg_kv_path_gather (extract_path) or a chain re-forward
+                       (recompute_accepted)
+  next state           hidden at the last accepted node; its packed logits row,
+                       or a fresh LM-head row when it is a leaf
+
+There is one device-to-host copy per round (accepted tokens, lengths, flags),
+plus one for the adaptive-plan confidences when that mode is on. Draws use
+counter noise keyed by (seed, round, sequence id, draw index), so results do
+not depend on batch composition or on which rows finished earlier.
+
+Not built here (rejected at construction): reflex fast-state proposals
+(``reflex_enabled``) and chain proposals (``proposal_mode="chain"``).
+"""
+from __future__ import annotations
+
+import math
+import time
+import warnings
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from .. import kernels as K
+from .. import timing
+from ..models.target import TargetModel, as_mask_tensor, chain_bits
+from .medusa_tree import TreePlan, TreeTopology, dense_node_count, fit_topk_to_budget, plan_tree
+
+
+@dataclass
+class FlashMedusaConfig:
+    num_medusa_heads: int = 3
+    tree_mode: str = "concurrency_aware"
+    tree_layout: str = "dense"
+    acceptance: str = "exact_target"
+    cache_update_mode: str = "extract_path"
+    allow_recompute_fallback: bool = True
+    cpeak_nodes: int = 64
+    min_tree_nodes_per_seq: int = 1
+    max_tree_nodes_per_seq: int = 16
+    max_tree_depth: int = 4
+    fixed_tree_topk_by_depth: tuple = (4, 3, 2)
+    do_sample: bool = True
+    temperature: float = 1.0
+    top_p: float = 0.95
+    top_k: int | None = None
+    clone_tree_cache: bool = True
+    oom_shrink_factor: float = 0.5
+    enable_medusa_spec_after: int = 0
+    proposal_mode: str = "medusa"
+    chain_enable_after: int = 0
+    chain_bootstrap_from_medusa: bool = True
+    adaptive_tree_enabled: bool = False
+    adaptive_confidence_metric: str = "top1_prob"
+    adaptive_confidence_quantile: float = 0.25
+    adaptive_confidence_low: float = 0.15
+    adaptive_confidence_high: float = 0.45
+    adaptive_min_topk_by_depth: tuple = (1, 1, 1)
+    adaptive_depth_weight_decay: float = 0.5
+    head_inference_autocast: bool = True
+    project_internal_tree_logits_only: bool = True
+    inplace_kv_compaction: bool = True
+    reflex_enabled: bool = False
+    # build additions
+    emit_correction_token: bool = False  # flashgrpo_b200 acceptance semantics
+    noise_seed: int | None = None        # None: drawn from torch's default generator per generate()
+
+
+def _quantile(values: np.ndarray, q: float) -> float:
+    """Linear-interpolation quantile (torch.quantile's default)."""
+    v = np.sort(values.astype(np.float64))
+    pos = q * (v.size - 1)
+    lo = int(math.floor(pos))
+    hi = min(lo + 1, v.size - 1)
+    return float(v[lo] + (v[hi] - v[lo]) * (pos - lo))
+
+
+class FlashMedusaDecoder:
+    def __init__(self, target_model, medusa_heads, tokenizer, config: FlashMedusaConfig):
+        if config.acceptance != "exact_target":
+            raise NotImplementedError("Only exact_target acceptance is implemented in the main FlashGRPO path")
+        if config.cache_update_mode not in {"extract_path", "recompute_accepted"}:
+            raise ValueError(f"Unsupported cache_update_mode={config.cache_update_mode}")
+        if config.proposal_mode not in {"medusa", "chain"}:
+            raise ValueError(f"Unsupported proposal_mode={config.proposal_mode}")
+        if config.proposal_mode == "chain":
+            raise NotImplementedError("chain proposals are not built in flashgrpo_amd yet")
+        if config.reflex_enabled:
+            raise NotImplementedError("reflex fast-state proposals are not built in flashgrpo_amd")
+        self.target_model = target_model
+        self.model = target_model if isinstance(target_model, TargetModel) else TargetModel.from_hf(target_model)
+        self.medusa_heads = medusa_heads
+        self.tokenizer = tokenizer
+        self.config = config
+
+    # ------------------------------------------------------------------ helpers
+    def _token_ids(self):
+        tok = self.tokenizer
+        pad = getattr(tok, "pad_token_id", None)
+        eos = getattr(tok, "eos_token_id", None)
+        if pad is None:
+            pad = eos
+        if pad is None:
+            pad = 0
+        if eos is None:
+            eos = pad
+        return int(pad), int(eos)
+
+    def _plan(self, active_bsz: int) -> TreePlan:
+        cfg = self.config
+        return plan_tree(active_batch_size=active_bsz,
+                         num_medusa_heads=min(cfg.num_medusa_heads, self.medusa_heads.num_heads),
+                         tree_mode=cfg.tree_mode, tree_layout=cfg.tree_layout, cpeak_nodes=cfg.cpeak_nodes,
+                         min_tree_nodes_per_seq=cfg.min_tree_nodes_per_seq,
+                         max_tree_nodes_per_seq=cfg.max_tree_nodes_per_seq, max_tree_depth=cfg.max_tree_depth,
+                         fixed_tree_topk_by_depth=list(cfg.fixed_tree_topk_by_depth),
+                         adaptive_tree_enabled=bool(cfg.adaptive_tree_enabled),
+                         adaptive_min_topk_by_depth=list(cfg.adaptive_min_topk_by_depth))
+
+    def _topk_from_confidence(self, confidence: float, base_k: int, depth_idx: int) -> int:
+        """``flash_medusa_decoder.py:341-360``."""
+        cfg = self.config
+        base_k = max(1, int(base_k))
+        mins = list(cfg.adaptive_min_topk_by_depth) or [1]
+        min_k = max(1, min(base_k, int(mins[min(depth_idx, len(mins) - 1)])))
+        if (not cfg.adaptive_tree_enabled) or base_k <= min_k:
+            return base_k
+        if not math.isfinite(float(confidence)):
+            return min_k
+        low, high = float(cfg.adaptive_confidence_low), float(cfg.adaptive_confidence_high)
+        if high <= low:
+            return min_k if confidence >= high else base_k
+        if confidence <= low:
+            return base_k
+        if confidence >= high:
+            return min_k
+        ratio = (confidence - low) / (high - low)
+        return max(min_k, min(base_k, int(round(base_k - ratio * (base_k - min_k)))))
+
+    def _adapt_plan(self, plan: TreePlan, stats: np.ndarray, cand_scores: np.ndarray, batch: int):
+        """Confidence quantile per head -> branching -> budget refit (``flash_medusa_decoder.py:320-389``).
+
+        top1_prob confidence = exp(max - logsumexp) of each head's logits row;
+        margin = top1 - top2 of the candidate scores.
+        """
+        cfg = self.config
+        heads = min(len(plan.topk_by_depth), plan.active_heads)
+        q = min(1.0, max(0.0, float(cfg.adaptive_confidence_quantile)))
+        confs = []
+        for d in range(heads):
+            rows = slice(d * batch, (d + 1) * batch)
+            if cfg.adaptive_confidence_metric == "margin":
+                sc = cand_scores[rows]
+                score = sc[:, 0] - sc[:, 1] if sc.shape[1] > 1 else sc[:, 0]
+            else:
+                st = stats[rows].astype(np.float64)
+                score = np.exp(st[:, 0] - st[:, 1])
+            confs.append(_quantile(np.nan_to_num(score, nan=0.0, posinf=0.0, neginf=0.0), q))
+        adapted = [self._topk_from_confidence(c, int(k), d) for d, (k, c) in
+                   enumerate(zip(plan.topk_by_depth, confs))]
+        if adapted:
+            adapted = fit_topk_to_budget(adapted, plan.node_budget_per_seq,
+                                         min_topk_by_depth=list(cfg.adaptive_min_topk_by_depth)[:len(adapted)],
+                                         depth_weight_decay=float(cfg.adaptive_depth_weight_decay))
+        new = TreePlan(plan.node_budget_per_seq, len(adapted), [max(1, int(k)) for k in adapted],
+                       dense_node_count(adapted), plan.mode, plan.layout)
+        return new, {"confidence": confs, "topk": list(adapted)}
+
+    # ------------------------------------------------------------------ rollout
+    @torch.no_grad()
+    def start(self, input_ids: torch.Tensor, attention_mask: torch.Tensor, *, repeated_generate_nums=None,
+              max_length: int = 2048, statistical_time: bool = False, generation_step: int = 0) -> "Rollout":
+        """Prefill the prompts (left padding compacted away), repeat rows for GRPO
+        groups and return the rollout state before the first verify round."""
+        cfg = self.config
+        model = self.model
+        dev = model.device
+        V = model.cfg.vocab
+        repeats = max(1, int(repeated_generate_nums or 1))
+        if cfg.noise_seed is None:
+            seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+        else:
+            seed = (int(cfg.noise_seed) * 1000003 + int(generation_step)) & (2 ** 64 - 1)
+        r = Rollout(seed=seed, max_length=int(max_length), statistical_time=bool(statistical_time),
+                    generation_step=int(generation_step), device=dev)
+        r.total_start = time.time()
+        ids_h = input_ids.detach().cpu()
+        mask_h = attention_mask.detach().cpu().bool()
+        B0 = ids_h.shape[0]
+        lens = mask_h.sum(-1).numpy().astype(np.int64)
+        if lens.min() < 1:
+            raise ValueError("every prompt needs at least one unmasked token")
+        valid_ids = ids_h[mask_h]
+        if int(valid_ids.min()) < 0 or int(valid_ids.max()) >= V:
+            raise ValueError(f"input token ids must lie in [0, {V})")
+        pmax = int(lens.max())
+        # Slots past a row's length are never attended; fill them with token 0.
+        packed = torch.zeros((B0, pmax), dtype=torch.int32)
+        for b in range(B0):
+            packed[b, :lens[b]] = ids_h[b][mask_h[b]].to(torch.int32)
+        B = B0 * repeats
+        capacity = max(int(max_length), pmax + 1) + 80
+        r.cache = model.new_cache(B, capacity)
+        first_rows = torch.arange(B0, dtype=torch.int32, device=dev) * repeats
+        r.sync()
+        t0 = time.time()
+        last_hidden = model.prefill(packed.to(dev), r.cache, lengths=lens, row_map=first_rows)
+        first_logits = model.logits(last_hidden)
+        r.sync()
+        r.prefill_time = time.time() - t0
+        if repeats > 1:
+            src = torch.arange(B0, device=dev).repeat_interleave(repeats) * repeats
+            dst = torch.arange(B, device=dev)
+            dup = (dst % repeats) != 0
+            r.cache.repeat_rows(src[dup].to(torch.int32), dst[dup].to(torch.int32))
+            r.hidden = last_hidden.repeat_interleave(repeats, dim=0).contiguous()
+            r.logits = first_logits.repeat_interleave(repeats, dim=0).contiguous()
+        else:
+            r.hidden, r.logits = last_hidden, first_logits
+        r.active = list(range(B))
+        r.row_map = torch.arange(B, dtype=torch.int32, device=dev)
+        r.seq = r.cache.seq_len.clone()
+        r.seq_h = np.repeat(lens, repeats).astype(np.int64)
+        r.pending = torch.full((B,), -1, dtype=torch.int32, device=dev) if cfg.emit_correction_token else None
+        r.generated = [[] for _ in range(B)]
+        r.err = torch.zeros(1, dtype=torch.int32, device=dev)
+        return r
+
+    @torch.no_grad()
+    def step(self, r: "Rollout", trace: list | None = None) -> int:
+        """One verify round over the active rows; returns the tokens it emitted."""
+        cfg = self.config
+        model = self.model
+        dev = r.device
+        m = r.m
+        greedy = (not cfg.do_sample) or cfg.temperature == 0
+        b200 = bool(cfg.emit_correction_token)
+        _, eos_id = self._token_ids()
+        Bc = len(r.active)
+        rnd = m["rounds"]
+        roots = K.sample_tokens(r.logits, seed=r.seed, step=rnd, seq_ids=r.row_map, draw=0, forced=r.pending,
+                                temperature=cfg.temperature, greedy=greedy, top_k=cfg.top_k, top_p=cfg.top_p)
+        use_tree = r.generation_step >= int(cfg.enable_medusa_spec_after)
+        plan = self._plan(Bc) if use_tree else TreePlan(1, 0, [], 1, cfg.tree_mode, cfg.tree_layout)
+        cand = score = mlog = None
+        adaptive_stats = {}
+        if plan.active_heads > 0:
+            r.sync()
+            t0 = time.time()
+            proj = self.medusa_heads.project_all(r.hidden, plan.active_heads)
+            with timing.label("medusa"):
+                mlog = model.logits(proj)
+            cand, score, stats = K.medusa_topk(mlog, max(plan.topk_by_depth), stats=bool(cfg.adaptive_tree_enabled))
+            r.sync()
+            m["medusa_time"] += time.time() - t0
+            if cfg.adaptive_tree_enabled:
+                plan, adaptive_stats = self._adapt_plan(plan, stats.cpu().numpy(), score.cpu().numpy(), Bc)
+        topo = TreeTopology.for_plan(plan)
+        N = topo.num_nodes
+        r.plan_last = {"B_cur": Bc, "node_budget_per_seq": plan.node_budget_per_seq,
+                       "active_heads": plan.active_heads, "topk_by_depth": plan.topk_by_depth,
+                       "actual_nodes": plan.actual_nodes, "proposal_mode": "medusa" if use_tree else "target_only",
+                       "adaptive_tree": adaptive_stats}
+        m["active_sum"] += Bc
+        m["node_sum"] += N
+        m["samples"] += 1
+        for dpt in topo.depths[1:]:
+            r.proposed_by_depth[dpt] = r.proposed_by_depth.get(dpt, 0) + Bc
+        dshared = topo.device(dev)
+        dmap = topo.device(dev, Bc)
+        if N > 1:
+            tree_tokens, _ = K.tree_layout(cand, score, Bc, roots, dshared["depth"], dshared["rank"], N)
+        else:
+            tree_tokens = roots.view(Bc, 1)
+        # ---------------- verify forward + packed LM head
+        tree_logits = slot_map = hidden_t = None
+        if int(r.seq_h.max()) + N > r.cache.capacity:
+            raise RuntimeError("KV cache capacity exceeded")  # unreachable: rows finish at max_length
+        r.sync()
+        t0 = time.time()
+        try:
+            hidden_t = model.forward(tree_tokens, r.cache, pos_offset=dshared["pos_offset"], anc=dshared["anc"],
+                                     seq_len=r.seq, row_map=r.row_map, err_flag=r.err)
+            if N > 1:
+                m["tree_query_rows"] += Bc * N
+                with timing.label("tree"):
+                    if cfg.project_internal_tree_logits_only:
+                        tree_logits = model.logits(hidden_t, row_index=dmap["internal_rows"])
+                        slot_map = dmap["slot_map"]
+                    else:
+                        tree_logits = model.logits(hidden_t)
+                m["tree_lm_head_rows"] += tree_logits.shape[0]
+        except RuntimeError as exc:
+            if "out of memory" not in str(exc).lower():
+                raise
+            m["oom"] += 1
+            torch.cuda.empty_cache()
+            hidden_t = tree_logits = None
+        r.sync()
+        m["verify_time"] += time.time() - t0
+        # ---------------- acceptance
+        if tree_logits is not None:
+            walk = K.accept_walk(tree_logits, tree_tokens, dmap["parents"], dmap["n_nodes"],
+                                 max_walk_steps=topo.max_depth, slot_map=slot_map, seed=r.seed, step=rnd,
+                                 seq_ids=r.row_map, draw0=1, temperature=cfg.temperature, greedy=greedy,
+                                 top_k=cfg.top_k, top_p=cfg.top_p, err_flag=r.err)
+        else:
+            zeros = torch.zeros(Bc, dtype=torch.int32, device=dev)
+            walk = dict(acc_tokens=roots.view(Bc, 1).clone(), acc_nodes=zeros.view(Bc, 1).clone(),
+                        acc_len=torch.ones(Bc, dtype=torch.int32, device=dev), last_node=zeros.clone(),
+                        correction=torch.full((Bc,), -1, dtype=torch.int32, device=dev))
+        new_pending = torch.empty(Bc, dtype=torch.int32, device=dev) if b200 else None
+        finished_d = K.accept_finalize(walk, r.seq, max_length=r.max_length, eos_token_id=eos_id,
+                                       pending_root=new_pending)
+        # ---------------- the one host sync of the round
+        W = walk["acc_tokens"].shape[1]
+        cols = [walk["acc_tokens"], walk["acc_len"].view(-1, 1), finished_d.view(-1, 1),
+                walk["last_node"].view(-1, 1), r.err.expand(Bc).view(-1, 1)]
+        if b200:
+            cols.append(new_pending.view(-1, 1))
+        pack = torch.cat(cols, dim=1).cpu().numpy()
+        acc_tok_h, acc_len_h = pack[:, :W], pack[:, W]
+        fin_h, last_h = pack[:, W + 1].astype(bool), pack[:, W + 2]
+        if int(pack[0, W + 3]):
+            raise RuntimeError(f"flashgrpo_amd kernel reported an index error (flag {int(pack[0, W + 3])})")
+        if b200:
+            m["corrections"] += int(np.count_nonzero(pack[:, W + 4] >= 0))
+        if trace is not None:
+            rec = dict(round=rnd, active=list(r.active), plan=list(plan.topk_by_depth),
+                       budget=plan.node_budget_per_seq, seq_len=r.seq.cpu().numpy().copy(),
+                       logits_in=r.logits.float().cpu().numpy(), hidden_in=r.hidden.float().cpu().numpy(),
+                       roots=roots.cpu().numpy(), tree_tokens=tree_tokens.cpu().numpy(), acc_tokens=acc_tok_h.copy(),
+                       acc_len=acc_len_h.copy(), finished=fin_h.copy(), last_node=last_h.copy(), seed=r.seed)
+            if mlog is not None:
+                rec["medusa_logits"] = mlog.float().cpu().numpy()
+                rec["cand"] = cand.cpu().numpy()
+            if tree_logits is not None:
+                rec["tree_logits"] = tree_logits.float().cpu().numpy()
+                rec["slot_map"] = None if slot_map is None else slot_map.cpu().numpy()
+                rec["tree_hidden"] = hidden_t.float().cpu().numpy()
+            if b200:
+                rec["pending"] = pack[:, W + 4].copy()
+            trace.append(rec)
+        # ---------------- cache update + next state
+        extracted = False
+        if cfg.cache_update_mode == "extract_path" and tree_logits is not None:
+            r.sync()
+            t0 = time.time()
+            r.cache.gather_path(r.seq, walk["acc_nodes"], walk["acc_len"], N, row_map=r.row_map, err_flag=r.err)
+            ar = torch.arange(Bc, device=dev)
+            last = walk["last_node"].long()
+            r.hidden = hidden_t[ar, last].contiguous()
+            if slot_map is not None:
+                slots = slot_map[ar, last]
+                r.logits = tree_logits.index_select(0, slots.clamp_min(0).long())
+                leaf = np.nonzero(np.array([topo.slot_of[int(n)] < 0 for n in last_h]))[0]
+                if leaf.size:
+                    li = torch.from_numpy(leaf).to(dev)
+                    with timing.label("leaf"):
+                        r.logits.index_copy_(0, li, model.logits(r.hidden.index_select(0, li)))
+                    m["tree_lm_head_rows"] += int(leaf.size)
+            else:
+                r.logits = tree_logits.index_select(0, ar * N + last)
+            r.sync()
+            dt_ = time.time() - t0
+            m["extract_time"] += dt_
+            m["cache_time"] += dt_
+            m["extract_ok"] += 1
+            extracted = True
+        elif cfg.cache_update_mode == "extract_path" and plan.active_heads > 0:
+            m["extract_fallback"] += 1
+            if not cfg.allow_recompute_fallback:
+                raise RuntimeError("KV extraction was requested but no tree cache was available")
+        if not extracted:
+            r.sync()
+            t0 = time.time()
+            if N == 1 and hidden_t is not None:
+                # root-only round: the forward already wrote the root's K/V at slot seq_len
+                r.hidden = hidden_t[:, 0].contiguous()
+            else:
+                wmax = int(acc_len_h.max())
+                cols_ = torch.arange(wmax, device=dev)[None, :]
+                # entries past a row's accepted length are padding: use token 0
+                chain = torch.where(cols_ < walk["acc_len"][:, None], walk["acc_tokens"][:, :wmax],
+                                    torch.zeros((), dtype=torch.int32, device=dev)).contiguous()
+                h = model.forward(chain, r.cache, pos_offset=torch.arange(wmax, dtype=torch.int32, device=dev),
+                                  anc=as_mask_tensor(chain_bits(wmax), dev), seq_len=r.seq, row_map=r.row_map,
+                                  err_flag=r.err)
+                r.hidden = h[torch.arange(Bc, device=dev), (walk["acc_len"] - 1).long()].contiguous()
+            with timing.label("next"):
+                r.logits = model.logits(r.hidden)
+            r.sync()
+            dt_ = time.time() - t0
+            m["cache_time"] += dt_
+            if cfg.cache_update_mode == "extract_path" and plan.active_heads > 0:
+                m["recompute_time"] += dt_
+        r.seq = r.seq + walk["acc_len"]
+        r.seq_h = r.seq_h + acc_len_h
+        r.last_round = dict(num_nodes=N, internal=len(topo.internal), acc_len=acc_len_h.copy(),
+                            last_node=last_h.copy(), walk_draws=np.array(
+                                [int(a) - (1 if topo.slot_of[int(n)] < 0 else 0) for a, n in zip(acc_len_h, last_h)])
+                            if N > 1 else np.zeros(Bc, dtype=np.int64), heads=plan.active_heads, batch=Bc)
+        if b200:
+            r.pending = new_pending
+        # ---------------- bookkeeping
+        m["rounds"] += 1
+        emitted = 0
+        for i in range(Bc):
+            L = int(acc_len_h[i])
+            emitted += L
+            r.generated[r.active[i]].extend(int(t) for t in acc_tok_h[i, :L])
+            r.accept_hist[L] = r.accept_hist.get(L, 0) + 1
+            for dpt in range(2, L + 1):
+                r.accept_by_depth[dpt] = r.accept_by_depth.get(dpt, 0) + 1
+            m["total_acc_length"] += L
+            m["total_decoded_steps"] += 1
+            m["accepted"] += max(L - 1, 0)
+            m["proposed"] += max(N - 1, 0)
+        if fin_h.any():
+            keep = np.nonzero(~fin_h)[0]
+            if keep.size == 0:
+                r.active = []
+            else:
+                kt = torch.from_numpy(keep).to(dev)
+                r.active = [r.active[i] for i in keep]
+                r.row_map = r.row_map.index_select(0, kt)
+                r.seq = r.seq.index_select(0, kt)
+                r.seq_h = r.seq_h[keep]
+                r.hidden = r.hidden.index_select(0, kt)
+                r.logits = r.logits.index_select(0, kt)
+                if b200:
+                    r.pending = r.pending.index_select(0, kt)
+        return emitted
+
+    def finish(self, r: "Rollout") -> dict:
+        """Result dict with the keys of ``flash_medusa_decoder.py:1189-1229``."""
+        cfg = self.config
+        m = r.m
+        total_time = time.time() - r.total_start
+        accept_rate = m["accepted"] / max(m["proposed"], 1)
+        avg_accept = m["total_acc_length"] / max(m["total_decoded_steps"], 1)
+        reflex = {"enabled": False, "feedback_enabled": False, "proposal_injection_enabled": False,
+                  "fast_state_norm_mean": 0.0, "fast_state_norm_p95": 0.0}
+        return {
+            "generated_token_ids": r.generated,
+            "max_sequence_length": max((len(s) for s in r.generated), default=0),
+            "total_acc_length": int(m["total_acc_length"]),
+            "average_accept_length": float(avg_accept),
+            "accepted_tokens_per_medusa_step": float(avg_accept),
+            "total_decoded_token_num": int(m["total_decoded_steps"]),
+            "total_accepted_draft_tokens": int(m["accepted"]),
+            "total_proposed_draft_tokens": int(m["proposed"]),
+            "total_accepted_medusa_tokens": int(m["accepted"]),
+            "total_proposed_medusa_tokens": int(m["proposed"]),
+            "draft_acceptance_rate": float(accept_rate),
+            "medusa_acceptance_rate": float(accept_rate),
+            "total_verify_rounds": int(m["rounds"]),
+            "average_active_batch_size": m["active_sum"] / max(m["rounds"], 1),
+            "average_tree_nodes_per_seq": m["node_sum"] / max(m["samples"], 1),
+            "tree_query_rows": int(m["tree_query_rows"]),
+            "tree_lm_head_rows": int(m["tree_lm_head_rows"]),
+            "tree_lm_head_row_ratio": m["tree_lm_head_rows"] / max(m["tree_query_rows"], 1),
+            "accept_length_histogram": r.accept_hist,
+            "medusa_accept_by_depth": r.accept_by_depth,
+            "medusa_proposed_by_depth": r.proposed_by_depth,
+            "last_tree_plan": r.plan_last,
+            "cache_update_mode": cfg.cache_update_mode,
+            "kv_extraction_success_count": int(m["extract_ok"]),
+            "kv_extraction_fallback_count": int(m["extract_fallback"]),
+            "kv_extraction_time": m["extract_time"],
+            "recompute_fallback_time": m["recompute_time"],
+            "oom_count": int(m["oom"]),
+            "total_time_cost": total_time,
+            "prefill_time_cost": r.prefill_time,
+            "target_time_cost": r.prefill_time + m["verify_time"] + m["cache_time"],
+            "tree_verify_time_cost": m["verify_time"],
+            "cache_update_time_cost": m["cache_time"],
+            "medusa_head_time_cost": m["medusa_time"],
+            "draft_time_cost": m["medusa_time"],
+            "check_time_cost": 0.0,
+            "noise_seed": r.seed,
+            "total_correction_tokens": int(m["corrections"]),
+            "reflex_metrics": reflex,
+            "reflex_head_metrics": {},
+            "reflex_aux_records": {},
+        }
+
+    @torch.no_grad()
+    def generate(self, input_ids: torch.Tensor, attention_mask: torch.Tensor, *, repeated_generate_nums=None,
+                 max_length: int = 2048, statistical_time: bool = False, generation_step: int = 0,
+                 collect_reflex_aux_cache=None, trace: list | None = None) -> dict:
+        """Reference contract of ``flash_medusa_decoder.py:550-1229``. ``trace``
+        (optional list) receives one dict of host copies per verify round; it adds
+        copies and synchronisation and is meant for parity tests."""
+        del collect_reflex_aux_cache
+        r = self.start(input_ids, attention_mask, repeated_generate_nums=repeated_generate_nums,
+                       max_length=max_length, statistical_time=statistical_time, generation_step=generation_step)
+        while r.active:
+            self.step(r, trace)
+        return self.finish(r)
+
+
+class Rollout:
+    """Device state of one generate() call between verify rounds (compact over active rows)."""
+
+    def __init__(self, *, seed, max_length, statistical_time, generation_step, device):
+        self.seed = seed
+        self.max_length = max_length
+        self.statistical_time = statistical_time
+        self.generation_step = generation_step
+        self.device = device
+        self.cache = None
+        self.active = []
+        self.row_map = self.seq = self.hidden = self.logits = self.pending = self.err = None
+        self.seq_h = None
+        self.generated = []
+        self.prefill_time = 0.0
+        self.total_start = time.time()
+        self.m = dict(total_acc_length=0, total_decoded_steps=0, accepted=0, proposed=0, rounds=0, active_sum=0,
+                      node_sum=0.0, samples=0, tree_query_rows=0, tree_lm_head_rows=0, medusa_time=0.0,
+                      verify_time=0.0, cache_time=0.0, extract_time=0.0, recompute_time=0.0, extract_ok=0,
+                      extract_fallback=0, oom=0, corrections=0)
+        self.accept_hist, self.accept_by_depth, self.proposed_by_depth = {}, {}, {}
+        self.plan_last = {}
+
+    def sync(self):
+        if self.statistical_time:
+            torch.cuda.synchronize(self.device)

@@ -1,0 +1,285 @@
+"""Tree planner, dense candidate trees and their device topology.
+
+Same public names and behaviour as ``flashgrpo/decoding/medusa_tree.py``:
+``CandidateTree``, ``TreePlan``, ``dense_node_count``, ``fit_topk_to_budget``,
+``plan_tree``, ``build_dense_tree``, ``build_batch_trees``. Candidate ties are
+resolved (value desc, index asc), which ``torch.topk`` leaves unspecified.
+
+``TreeTopology`` is the build's device form of a plan: in a dense tree the
+parent/depth/candidate-rank of every node depends only on the plan, so it is
+computed once per plan on the host (cached) and every row shares it; only the
+tokens differ per row and come from ``fg_medusa_topk`` + ``fg_tree_layout``.
+"""
+from __future__ import annotations
+
+import math
+import warnings
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from .. import kernels as K
+
+
+@dataclass
+class CandidateTree:
+    tokens: list
+    parents: list
+    depths: list
+    scores: list = field(default_factory=list)
+
+    def __post_init__(self) -> None:
+        self.children: dict = {}
+        for idx, parent in enumerate(self.parents):
+            if parent >= 0:
+                self.children.setdefault(parent, []).append(idx)
+
+    def ancestors_including_self(self, node_idx: int) -> list:
+        path = [node_idx]
+        p = self.parents[node_idx]
+        while p >= 0:
+            path.append(p)
+            p = self.parents[p]
+        return path[::-1]
+
+    @property
+    def node_count(self) -> int:
+        return len(self.tokens)
+
+
+@dataclass
+class TreePlan:
+    node_budget_per_seq: int
+    active_heads: int
+    topk_by_depth: list
+    actual_nodes: int
+    mode: str
+    layout: str
+
+
+def dense_node_count(topk_by_depth) -> int:
+    """1 + sum over depths of the product of branching factors (``medusa_tree.py:46-52``)."""
+    total, width = 1, 1
+    for k in topk_by_depth:
+        width *= int(k)
+        total += width
+    return total
+
+
+def fit_topk_to_budget(topk_by_depth, node_budget, *, min_topk_by_depth=None, depth_weight_decay=0.5):
+    """Greedy budget fit of ``medusa_tree.py:55-99``: shrink the depth with the best
+    nodes-saved per discounted log-utility lost; drop the deepest horizon when no
+    depth can shrink further."""
+    budget = max(1, int(node_budget))
+    ks = [max(1, int(k)) for k in topk_by_depth]
+    mins = list(min_topk_by_depth or [])
+    floor = [max(1, min(ks[i], int(mins[i]) if i < len(mins) else 1)) for i in range(len(ks))]
+    base = max(float(depth_weight_decay), 1e-3)
+    while ks and dense_node_count(ks) > budget:
+        now = dense_node_count(ks)
+        best = None
+        for d, k in enumerate(ks):
+            if k <= floor[d]:
+                continue
+            saved = now - dense_node_count(ks[:d] + [k - 1] + ks[d + 1:])
+            lost = base ** d * (math.log1p(k) - math.log(k))
+            cand = (saved / max(lost, 1e-9), saved, d)
+            best = cand if best is None or cand > best else best
+        if best is None:
+            ks.pop()
+            floor.pop()
+        else:
+            ks[best[2]] -= 1
+    return ks
+
+
+def plan_tree(*, active_batch_size, num_medusa_heads, tree_mode, tree_layout, cpeak_nodes, min_tree_nodes_per_seq,
+              max_tree_nodes_per_seq, max_tree_depth, fixed_tree_topk_by_depth, adaptive_tree_enabled=False,
+              adaptive_min_topk_by_depth=None) -> TreePlan:
+    """Per-step plan (``medusa_tree.py:102-178``): fixed, or concurrency-aware with a
+    ``floor(cpeak_nodes / B)`` node budget clamped to [min, max] nodes per sequence."""
+    if tree_layout not in {"dense", "sparse"}:
+        raise ValueError(f"Unsupported tree_layout={tree_layout}")
+    if tree_layout == "sparse":
+        warnings.warn("flashgrpo tree_layout='sparse' is a v1 skeleton; falling back to dense.", RuntimeWarning)
+        tree_layout = "dense"
+    bsz = max(1, int(active_batch_size))
+    if tree_mode == "fixed":
+        budget = int(max_tree_nodes_per_seq)
+        ks = [max(1, int(k)) for k in list(fixed_tree_topk_by_depth)[:num_medusa_heads]]
+        while ks and dense_node_count(ks) > budget:
+            ks[-1] -= 1
+            if ks[-1] <= 0:
+                ks.pop()
+        ks = ks[:min(len(ks), max(0, int(max_tree_depth) - 1))]
+    elif tree_mode == "concurrency_aware":
+        budget = max(int(min_tree_nodes_per_seq), min(int(max_tree_nodes_per_seq), int(cpeak_nodes) // bsz))
+        max_heads = min(int(num_medusa_heads), max(0, int(max_tree_depth) - 1))
+        defaults = list(fixed_tree_topk_by_depth) or [4, 3, 2, 1, 1]
+        ks = []
+        if adaptive_tree_enabled:
+            mins = list(adaptive_min_topk_by_depth or [])
+            chain = []
+            for d in range(max_heads):
+                mk = max(1, int(mins[d]) if d < len(mins) else 1)
+                if dense_node_count(chain + [mk]) > budget:
+                    break
+                chain.append(mk)
+                ks.append(max(mk, int(defaults[min(d, len(defaults) - 1)])))
+        else:
+            paths, used = 1, 1
+            for d in range(max_heads):
+                room = budget - used
+                if room <= 0:
+                    break
+                k = min(max(1, int(defaults[min(d, len(defaults) - 1)])), max(1, room // paths))
+                if used + paths * k > budget:
+                    k = room // paths
+                if k <= 0:
+                    break
+                ks.append(int(k))
+                paths *= int(k)
+                used += paths
+    else:
+        raise ValueError(f"Unsupported tree_mode={tree_mode}")
+    return TreePlan(budget, len(ks), ks, dense_node_count(ks), tree_mode, tree_layout)
+
+
+# ------------------------------------------------------------------ device topology
+class TreeTopology:
+    """Dense-tree structure of one plan, truncated at its node budget.
+
+    Host lists (``parents``, ``depths``, ``ranks``, ``internal``) plus cached
+    device tensors: node depth/rank/position offset [N], ancestor-or-self bit
+    masks [N] (int64 bit patterns), and per-batch-size parent/slot maps.
+    """
+
+    _cache: dict = {}
+
+    def __init__(self, topk_by_depth, budget):
+        parents, depths, ranks = [-1], [1], [0]
+        frontier = [0]
+        for d, k in enumerate(topk_by_depth):
+            if int(k) <= 0:
+                break
+            nxt, full = [], False
+            for p in frontier:
+                for r in range(int(k)):
+                    parents.append(p)
+                    depths.append(d + 2)
+                    ranks.append(r)
+                    nxt.append(len(parents) - 1)
+                    if len(parents) >= budget:
+                        full = True
+                        break
+                if full:
+                    break
+            frontier = nxt
+            if not frontier or len(parents) >= budget:
+                break
+        self.topk_by_depth = [int(k) for k in topk_by_depth]
+        self.parents, self.depths, self.ranks = parents, depths, ranks
+        self.num_nodes = len(parents)
+        if self.num_nodes > 64:
+            raise ValueError("tree nodes exceed the 64-node limit of the ancestor bit masks")
+        has_child = [False] * self.num_nodes
+        for p in parents[1:]:
+            has_child[p] = True
+        self.internal = [n for n in range(self.num_nodes) if has_child[n]]
+        self.slot_of = [-1] * self.num_nodes
+        for i, n in enumerate(self.internal):
+            self.slot_of[n] = i
+        self.max_depth = max(depths) - 1  # walk steps
+        bits = []
+        for n in range(self.num_nodes):
+            m, p = 1 << n, parents[n]
+            while p >= 0:
+                m |= 1 << p
+                p = parents[p]
+            bits.append(m)
+        self.anc_bits = bits
+        self._dev = {}
+
+    @classmethod
+    def for_plan(cls, plan: TreePlan) -> "TreeTopology":
+        key = (tuple(int(k) for k in plan.topk_by_depth[: plan.active_heads]), int(plan.node_budget_per_seq))
+        topo = cls._cache.get(key)
+        if topo is None:
+            topo = cls(list(key[0]), key[1])
+            cls._cache[key] = topo
+        return topo
+
+    def device(self, device, batch: int | None = None) -> dict:
+        """Device tensors; batch-sized maps are cached per batch size."""
+        key = (str(device), batch)
+        d = self._dev.get(key)
+        if d is None:
+            i32 = dict(dtype=torch.int32, device=device)
+            arr = np.array([b & 0xFFFFFFFFFFFFFFFF for b in self.anc_bits], dtype=np.uint64).view(np.int64)
+            d = dict(depth=torch.tensor(self.depths, **i32), rank=torch.tensor(self.ranks, **i32),
+                     pos_offset=torch.tensor([x - 1 for x in self.depths], **i32),
+                     anc=torch.from_numpy(arr).to(device))
+            if batch is not None:
+                N, I = self.num_nodes, len(self.internal)
+                d["parents"] = torch.tensor([self.parents] * batch, **i32)
+                d["n_nodes"] = torch.full((batch,), N, **i32)
+                slots = np.full((batch, N), -1, dtype=np.int32)
+                rows = np.zeros(batch * I, dtype=np.int32)
+                for b in range(batch):
+                    for i, n in enumerate(self.internal):
+                        slots[b, n] = b * I + i
+                        rows[b * I + i] = b * N + n
+                d["slot_map"] = torch.from_numpy(slots).to(device)
+                d["internal_rows"] = torch.from_numpy(rows).to(device)
+            self._dev[key] = d
+        return d
+
+
+# ------------------------------------------------------------------ tree builders
+def build_tree_tokens(roots: torch.Tensor, cand_tokens: torch.Tensor, cand_scores: torch.Tensor,
+                      topo: TreeTopology, batch: int):
+    """Device tokens [B, N] (int32) and scores [B, N] of a dense tree."""
+    d = topo.device(roots.device)
+    return K.tree_layout(cand_tokens, cand_scores, batch, roots.to(torch.int32), d["depth"], d["rank"],
+                         topo.num_nodes)
+
+
+def _trees_from_device(tokens: torch.Tensor, scores: torch.Tensor, topo: TreeTopology) -> list:
+    toks = tokens.cpu().tolist()
+    scs = scores.cpu().tolist()
+    return [CandidateTree(tokens=t, parents=list(topo.parents), depths=list(topo.depths), scores=s)
+            for t, s in zip(toks, scs)]
+
+
+def build_batch_trees(root_tokens: torch.Tensor, medusa_logits: list, plan: TreePlan) -> list:
+    """Dense Medusa trees for a batch (``medusa_tree.py:228-278``): one device top-k
+    over all depths, one layout launch, then the CandidateTree objects."""
+    batch = int(root_tokens.shape[0])
+    depths = []
+    for d, k in enumerate(plan.topk_by_depth[: plan.active_heads]):
+        if d >= len(medusa_logits):
+            break
+        k = min(max(0, int(k)), int(medusa_logits[d].shape[-1]))
+        if k <= 0:
+            break
+        depths.append(k)
+    topo = TreeTopology(depths, plan.node_budget_per_seq)
+    device = root_tokens.device
+    if not depths:
+        t = root_tokens.reshape(batch, 1).to(torch.int32)
+        return _trees_from_device(t, torch.zeros(batch, 1), topo)
+    if device.type != "cuda":
+        raise ValueError("build_batch_trees: device tensors required (HIP path)")
+    stacked = torch.cat([medusa_logits[d] for d in range(len(depths))], dim=0)
+    cand, score, _ = K.medusa_topk(stacked, max(depths))
+    tokens, scores = build_tree_tokens(root_tokens, cand, score, topo, batch)
+    return _trees_from_device(tokens, scores, topo)
+
+
+def build_dense_tree(root_token: int, medusa_logits: list, plan: TreePlan) -> CandidateTree:
+    """Single-row tree (``medusa_tree.py:200-225``)."""
+    rows = [lg.reshape(1, -1) for lg in medusa_logits]
+    device = rows[0].device if rows else torch.device("cuda")
+    root = torch.tensor([int(root_token)], dtype=torch.int32, device=device)
+    return build_batch_trees(root, rows, plan)[0]

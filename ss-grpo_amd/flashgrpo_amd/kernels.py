@@ -10,9 +10,14 @@ import math
 
 import torch
 
-from . import _lib
+from . import _lib, timing
 
 F32, BF16 = 0, 1
+
+
+def _call(name: str, *args) -> None:
+    with timing.launch(name):
+        _lib.call(name, *args)
 _DT = {torch.float32: F32, torch.bfloat16: BF16}
 
 
@@ -80,7 +85,7 @@ def medusa_heads(hidden, ln_w, ln_b, fc_w, fc_b, *, eps=1e-5, out=None, out_dtyp
     need = _lib.load().fg_medusa_heads_workspace(B, H, heads, dtype_code(hidden))
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(need, dtype=torch.uint8, device=hidden.device)
-    _lib.call("fg_medusa_heads", _ptr(hidden), dtype_code(hidden), B, H, hidden.stride(0), heads, _ptr(ln_w),
+    _call("fg_medusa_heads", _ptr(hidden), dtype_code(hidden), B, H, hidden.stride(0), heads, _ptr(ln_w),
               _ptr(ln_b), float(eps), _ptr(fc_w), _ptr(fc_b), _ptr(out), dtype_code(out), _ptr(workspace),
               workspace.numel() * workspace.element_size(), _stream())
     return out
@@ -103,7 +108,7 @@ def lm_head(x, weight, *, row_index=None, out=None, out_dtype=None):
         out = torch.empty(M, N, dtype=od, device=x.device)
     if M == 0:
         return out
-    _lib.call("fg_lm_head", _ptr(x2), dtype_code(x), M, K, x2.stride(0), _ptr(row_index), _ptr(weight),
+    _call("fg_lm_head", _ptr(x2), dtype_code(x), M, K, x2.stride(0), _ptr(row_index), _ptr(weight),
               weight.stride(0), N, _ptr(out), dtype_code(out), out.stride(0), _stream())
     return out
 
@@ -124,7 +129,7 @@ def medusa_topk(logits, kmax, *, stats=False, workspace=None):
     need = _lib.load().fg_medusa_topk_workspace(R, V, kmax)
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(need, dtype=torch.uint8, device=logits.device)
-    _lib.call("fg_medusa_topk", _ptr(logits), dtype_code(logits), logits.stride(0), R, V, kmax, _ptr(tok), _ptr(sc),
+    _call("fg_medusa_topk", _ptr(logits), dtype_code(logits), logits.stride(0), R, V, kmax, _ptr(tok), _ptr(sc),
               _ptr(st), _ptr(workspace), workspace.numel() * workspace.element_size(), _stream())
     return tok, sc, st
 
@@ -140,23 +145,23 @@ def tree_layout(cand_tokens, cand_scores, batch, roots, node_depth, node_rank, n
     if out_scores is None:
         out_scores = torch.empty(batch, num_nodes, dtype=torch.float32, device=dev)
     kstride = cand_tokens.shape[-1] if cand_tokens is not None else 0
-    _lib.call("fg_tree_layout", _ptr(cand_tokens), _ptr(cand_scores), kstride, batch, _ptr(roots), _ptr(node_depth),
+    _call("fg_tree_layout", _ptr(cand_tokens), _ptr(cand_scores), kstride, batch, _ptr(roots), _ptr(node_depth),
               _ptr(node_rank), num_nodes, _ptr(out_tokens), _ptr(out_scores), out_tokens.stride(0), _stream())
     return out_tokens, out_scores
 
 
 # ------------------------------------------------------------------ verify forward pieces
 def rope_kv_write(qkv, *, batch, num_nodes, q_heads, kv_heads, head_dim, seq_len, pos_offset, inv_freq, q_out,
-                  k_cache, v_cache, row_map=None):
+                  k_cache, v_cache, row_map=None, err_flag=None):
     _dev(qkv, seq_len, pos_offset, inv_freq, q_out, k_cache, v_cache, row_map)
     _i32(seq_len, "seq_len")
     _i32(pos_offset, "pos_offset")
     _i32(row_map, "row_map")
     if k_cache.stride(-1) != 1 or k_cache.stride(-2) != head_dim:
         raise ValueError("rope_kv_write: cache rows must be contiguous [.., capacity, d]")
-    _lib.call("fg_rope_kv_write", _ptr(qkv), dtype_code(qkv), qkv.stride(0), batch, num_nodes, q_heads, kv_heads,
+    _call("fg_rope_kv_write", _ptr(qkv), dtype_code(qkv), qkv.stride(0), batch, num_nodes, q_heads, kv_heads,
               head_dim, _ptr(seq_len), _ptr(pos_offset), _ptr(inv_freq), _ptr(q_out), _ptr(k_cache), _ptr(v_cache),
-              k_cache.stride(0), k_cache.stride(1), _ptr(row_map), _stream())
+              k_cache.stride(0), k_cache.stride(1), k_cache.shape[-2], _ptr(row_map), _ptr(err_flag), _stream())
 
 
 def tree_attention(q, k_cache, v_cache, *, seq_len, anc, num_nodes, q_heads, kv_heads, head_dim, out=None,
@@ -171,7 +176,7 @@ def tree_attention(q, k_cache, v_cache, *, seq_len, anc, num_nodes, q_heads, kv_
         out = torch.empty_like(q)
     anc_stride = 0 if anc.dim() == 1 else anc.stride(0)
     scale = 1.0 / math.sqrt(head_dim) if scale is None else scale
-    _lib.call("fg_tree_attention", _ptr(q), _ptr(out), _ptr(k_cache), _ptr(v_cache), dtype_code(q), B, num_nodes,
+    _call("fg_tree_attention", _ptr(q), _ptr(out), _ptr(k_cache), _ptr(v_cache), dtype_code(q), B, num_nodes,
               q_heads, kv_heads, head_dim, k_cache.stride(0), k_cache.stride(1), k_cache.shape[2], _ptr(seq_len),
               _ptr(row_map), _ptr(anc), anc_stride, float(scale), _stream())
     return out
@@ -183,7 +188,7 @@ def rmsnorm(x, weight, eps, *, delta=None, out=None):
     rows = x.numel() // H
     if out is None:
         out = torch.empty_like(x)
-    _lib.call("fg_rmsnorm", _ptr(x), _ptr(delta), _ptr(weight), _ptr(out), dtype_code(x), rows, H, float(eps),
+    _call("fg_rmsnorm", _ptr(x), _ptr(delta), _ptr(weight), _ptr(out), dtype_code(x), rows, H, float(eps),
               _stream())
     return out
 
@@ -194,7 +199,7 @@ def swiglu(gate_up, *, out=None):
     F = two_f // 2
     if out is None:
         out = torch.empty(rows, F, dtype=gate_up.dtype, device=gate_up.device)
-    _lib.call("fg_swiglu", _ptr(gate_up), _ptr(out), dtype_code(gate_up), rows, F, _stream())
+    _call("fg_swiglu", _ptr(gate_up), _ptr(out), dtype_code(gate_up), rows, F, _stream())
     return out
 
 
@@ -215,7 +220,7 @@ def sample_tokens(logits, *, noise=None, noise_col=0, seed=0, step=0, seq_ids=No
     T = 0.0 if temperature is None else float(temperature)
     use_T = T if T > 0 else (-1.0 if T < 0 or temperature is None else 0.0)
     g = bool(greedy) or (temperature is not None and T == 0.0)
-    _lib.call("fg_sample_tokens", _ptr(logits), dtype_code(logits), logits.stride(0), rows,
+    _call("fg_sample_tokens", _ptr(logits), dtype_code(logits), logits.stride(0), rows,
               V, _ptr(row_index), _ptr(forced), _ptr(noise), noise.stride(0) if noise is not None else 0,
               int(noise_col), int(seed) & (2 ** 64 - 1), int(step), _ptr(seq_ids), int(draw), use_T, int(g),
               int(top_k or 0), top_p_fixed(top_p), _ptr(out), _stream())
@@ -235,8 +240,8 @@ def accept_walk(tree_logits, tree_tokens, parents, n_nodes, *, max_walk_steps, s
     dev = tree_tokens.device
     acc_stride = acc_stride or (max_walk_steps + 1)
     if out is None:
-        out = dict(acc_tokens=torch.empty(B, acc_stride, dtype=torch.int32, device=dev),
-                   acc_nodes=torch.empty(B, acc_stride, dtype=torch.int32, device=dev),
+        out = dict(acc_tokens=torch.zeros(B, acc_stride, dtype=torch.int32, device=dev),
+                   acc_nodes=torch.zeros(B, acc_stride, dtype=torch.int32, device=dev),
                    acc_len=torch.empty(B, dtype=torch.int32, device=dev),
                    last_node=torch.empty(B, dtype=torch.int32, device=dev),
                    correction=torch.empty(B, dtype=torch.int32, device=dev),
@@ -245,7 +250,7 @@ def accept_walk(tree_logits, tree_tokens, parents, n_nodes, *, max_walk_steps, s
     use_T = T if T > 0 else (-1.0 if T < 0 or temperature is None else 0.0)
     g = bool(greedy) or (temperature is not None and T == 0.0)
     lg = aligned_rows(tree_logits.reshape(-1, V))
-    _lib.call("fg_accept_walk", _ptr(lg), dtype_code(lg), lg.stride(0), V, _ptr(slot_map), _ptr(tree_tokens),
+    _call("fg_accept_walk", _ptr(lg), dtype_code(lg), lg.stride(0), V, _ptr(slot_map), _ptr(tree_tokens),
               _ptr(parents), _ptr(n_nodes), nmax, B, int(max_walk_steps), _ptr(noise),
               noise.stride(0) if noise is not None else 0, int(noise_col0), int(seed) & (2 ** 64 - 1), int(step),
               _ptr(seq_ids), int(draw0), use_T, int(g), int(top_k or 0), top_p_fixed(top_p), _ptr(out["acc_tokens"]),
@@ -260,7 +265,7 @@ def accept_finalize(walk, old_len, *, max_length, eos_token_id, finished=None, p
     B = walk["acc_len"].numel()
     if finished is None:
         finished = torch.empty(B, dtype=torch.int32, device=old_len.device)
-    _lib.call("fg_accept_finalize", _ptr(walk["acc_tokens"]), _ptr(walk["acc_nodes"]), walk["acc_tokens"].stride(0),
+    _call("fg_accept_finalize", _ptr(walk["acc_tokens"]), _ptr(walk["acc_nodes"]), walk["acc_tokens"].stride(0),
               _ptr(walk["acc_len"]), _ptr(walk["last_node"]), _ptr(walk["correction"]), _ptr(old_len),
               int(max_length), -1 if eos_token_id is None else int(eos_token_id), _ptr(finished),
               _ptr(pending_root), B, _stream())
@@ -274,6 +279,6 @@ def kv_path_gather(tensor_ptrs, *, batch, kv_heads, head_dim, elem_bytes, stride
     for t, n in ((seq_len, "seq_len"), (acc_nodes, "acc_nodes"), (acc_len, "acc_len"), (row_map, "row_map")):
         _i32(t, n)
     bs, hs, rs = strides
-    _lib.call("fg_kv_path_gather", _ptr(tensor_ptrs), tensor_ptrs.numel(), batch, kv_heads, head_dim, elem_bytes, bs,
+    _call("fg_kv_path_gather", _ptr(tensor_ptrs), tensor_ptrs.numel(), batch, kv_heads, head_dim, elem_bytes, bs,
               hs, rs, capacity, _ptr(seq_len), _ptr(row_map), _ptr(acc_nodes), acc_nodes.stride(0), _ptr(acc_len),
               int(tree_nodes), _ptr(err_flag), _stream())

@@ -1,0 +1,5 @@
+"""Model adapters (mirrors ``flashgrpo.models``): Medusa heads and the native target model."""
+from .medusa_heads import ChainDraftCell, MedusaHeads, MedusaPredictionHead
+from .target import KVCache, TargetConfig, TargetModel
+
+__all__ = ["ChainDraftCell", "MedusaHeads", "MedusaPredictionHead", "KVCache", "TargetConfig", "TargetModel"]

@@ -1,0 +1,341 @@
+"""Qwen2/Llama-architecture target model with a per-sequence contiguous KV cache.
+
+Replaces the Hugging Face decoder the reference drives through
+``flashgrpo/models/qwen_flashgrpo_wrapper.py:150-239`` (``prefill``,
+``forward_tokens``, ``forward_tree``) and its ``DynamicCache``:
+
+* the cache is preallocated once, ``[L, 2, B, Hkv, capacity, d]``, with a
+  device ``seq_len[B]``; the tree's K/V go straight into slots
+  ``seq_len[b] + n`` (no per-step ``torch.cat`` of the prefix) and the
+  accepted path is compacted in place by ``fg_kv_path_gather``;
+* attention is ``fg_tree_attention`` (ancestor bitmask in registers) for the
+  tree verify and for prefill, which runs as causal 64-token chains;
+* RMSNorm (+ residual add), rotary + cache write and SwiGLU are HIP kernels;
+  the dense projections are plain library GEMMs (``F.linear``, hipBLASLt).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from .. import kernels as K
+
+MAX_TREE_NODES = 64
+
+
+@dataclass
+class TargetConfig:
+    num_layers: int
+    hidden: int
+    q_heads: int
+    kv_heads: int
+    head_dim: int
+    intermediate: int
+    vocab: int
+    rope_theta: float = 1.0e6
+    rms_eps: float = 1.0e-6
+    qkv_bias: bool = True
+    tie_word_embeddings: bool = False
+    name: str = "custom"
+
+    @property
+    def group(self) -> int:
+        return self.q_heads // self.kv_heads
+
+    # Shapes named by the benchmark configurations.
+    @staticmethod
+    def tiny():
+        return TargetConfig(4, 512, 8, 2, 64, 1408, 32000, 1.0e6, 1e-6, True, True, "tiny-qwen2")
+
+    @staticmethod
+    def qwen25_1p5b():
+        return TargetConfig(28, 1536, 12, 2, 128, 8960, 151936, 1.0e6, 1e-6, True, True, "qwen2.5-1.5b")
+
+    @staticmethod
+    def qwen25_7b():
+        return TargetConfig(28, 3584, 28, 4, 128, 18944, 152064, 1.0e6, 1e-6, True, False, "qwen2.5-7b")
+
+    @staticmethod
+    def llama31_8b():
+        return TargetConfig(32, 4096, 32, 8, 128, 14336, 128256, 5.0e5, 1e-5, False, False, "llama-3.1-8b")
+
+    @staticmethod
+    def qwen25_14b():
+        return TargetConfig(48, 5120, 40, 8, 128, 13824, 152064, 1.0e6, 1e-6, True, False, "qwen2.5-14b")
+
+
+def inv_freq_table(head_dim: int, theta: float) -> torch.Tensor:
+    """fp32 theta^(-2i/d), computed in float64 then rounded once."""
+    i = np.arange(0, head_dim, 2, dtype=np.float64)
+    return torch.from_numpy((1.0 / theta ** (i / head_dim)).astype(np.float32))
+
+
+def chain_bits(n: int) -> list:
+    """Ancestor-or-self masks of a causal chain of n nodes."""
+    return [(1 << (i + 1)) - 1 if i < 63 else -1 for i in range(n)]
+
+
+def as_mask_tensor(bits, device) -> torch.Tensor:
+    """uint64 bit masks -> int64 tensor with the same bit patterns."""
+    arr = np.array([int(b) & 0xFFFFFFFFFFFFFFFF for b in bits], dtype=np.uint64).view(np.int64)
+    return torch.from_numpy(arr).to(device)
+
+
+class KVCache:
+    """Contiguous per-sequence KV cache: kv[L, 2, B, Hkv, capacity, d] + seq_len[B].
+
+    ``seq_len`` counts committed (accepted) tokens of each cache row. Tree
+    verification writes its nodes after them without advancing ``seq_len``.
+    """
+
+    def __init__(self, cfg: TargetConfig, batch: int, capacity: int, *, dtype, device):
+        self.cfg = cfg
+        self.batch = int(batch)
+        self.capacity = int(capacity)
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self.kv = torch.zeros(cfg.num_layers, 2, batch, cfg.kv_heads, capacity, cfg.head_dim, dtype=dtype,
+                              device=device)
+        self.seq_len = torch.zeros(batch, dtype=torch.int32, device=device)
+        ptrs = [self.kv[l, j].data_ptr() for l in range(cfg.num_layers) for j in range(2)]
+        self.tensor_ptrs = torch.tensor(ptrs, dtype=torch.int64, device=device)
+
+    def k(self, layer: int) -> torch.Tensor:
+        return self.kv[layer, 0]
+
+    def v(self, layer: int) -> torch.Tensor:
+        return self.kv[layer, 1]
+
+    @property
+    def strides(self):
+        t = self.kv[0, 0]
+        return t.stride(0), t.stride(1), t.stride(2)
+
+    def gather_path(self, seq_len, acc_nodes, acc_len, tree_nodes, *, row_map=None, err_flag=None):
+        K.kv_path_gather(self.tensor_ptrs, batch=seq_len.numel(), kv_heads=self.cfg.kv_heads,
+                         head_dim=self.cfg.head_dim, elem_bytes=self.kv.element_size(), strides=self.strides,
+                         capacity=self.capacity, seq_len=seq_len, acc_nodes=acc_nodes, acc_len=acc_len,
+                         tree_nodes=tree_nodes, row_map=row_map, err_flag=err_flag)
+
+    def repeat_rows(self, src_rows: torch.Tensor, dst_rows: torch.Tensor) -> None:
+        """Copy cache rows src -> dst (all layers), e.g. GRPO repeats of one prompt."""
+        self.kv.index_copy_(2, dst_rows.long(), self.kv.index_select(2, src_rows.long()))
+        self.seq_len.index_copy_(0, dst_rows.long(), self.seq_len.index_select(0, src_rows.long()))
+
+
+class TargetModel:
+    """Decoder weights on the device plus the verify / prefill forward."""
+
+    def __init__(self, cfg: TargetConfig, weights: dict, *, dtype, device):
+        self.cfg = cfg
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self.w = weights
+        self.inv_freq = inv_freq_table(cfg.head_dim, cfg.rope_theta).to(device)
+        self._bufs = {}
+
+    # -------------------------------------------------------------- construction
+    @classmethod
+    def random(cls, cfg: TargetConfig, *, seed: int = 0, std: float = 0.02, dtype=torch.bfloat16, device="cuda"):
+        """Seeded N(0, std) weights generated on the device; norms 1, biases 0."""
+        g = torch.Generator(device=device).manual_seed(int(seed))
+        H, d, Fi = cfg.hidden, cfg.head_dim, cfg.intermediate
+        qkv_rows = (cfg.q_heads + 2 * cfg.kv_heads) * d
+
+        def n(*shape):
+            t = torch.empty(*shape, dtype=dtype, device=device)
+            t.normal_(0.0, std, generator=g)
+            return t
+
+        w = {"embed": n(cfg.vocab, H), "final_norm": torch.ones(H, dtype=dtype, device=device), "layers": []}
+        for _ in range(cfg.num_layers):
+            w["layers"].append({
+                "input_norm": torch.ones(H, dtype=dtype, device=device),
+                "qkv_w": n(qkv_rows, H),
+                "qkv_b": torch.zeros(qkv_rows, dtype=dtype, device=device) if cfg.qkv_bias else None,
+                "o_w": n(H, cfg.q_heads * d),
+                "post_norm": torch.ones(H, dtype=dtype, device=device),
+                "gate_up_w": n(2 * Fi, H),
+                "down_w": n(H, Fi),
+            })
+        w["lm_head"] = w["embed"] if cfg.tie_word_embeddings else n(cfg.vocab, H)
+        return cls(cfg, w, dtype=dtype, device=device)
+
+    @classmethod
+    def from_numpy(cls, cfg: TargetConfig, W: dict, *, dtype=torch.float32, device="cuda"):
+        """From a dict of numpy arrays with per-projection keys (q_w, k_w, ... gate_w, up_w)."""
+
+        def t(a):
+            return None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(device=device, dtype=dtype)
+
+        w = {"embed": t(W["embed"]), "final_norm": t(W["final_norm"]), "layers": []}
+        for lw in W["layers"]:
+            bias = None
+            if lw.get("q_b") is not None:
+                bias = t(np.concatenate([lw["q_b"], lw["k_b"], lw["v_b"]]))
+            w["layers"].append({
+                "input_norm": t(lw["input_norm"]),
+                "qkv_w": t(np.concatenate([lw["q_w"], lw["k_w"], lw["v_w"]])),
+                "qkv_b": bias,
+                "o_w": t(lw["o_w"]),
+                "post_norm": t(lw["post_norm"]),
+                "gate_up_w": t(np.concatenate([lw["gate_w"], lw["up_w"]])),
+                "down_w": t(lw["down_w"]),
+            })
+        w["lm_head"] = w["embed"] if cfg.tie_word_embeddings else t(W["lm_head"])
+        m = cls(cfg, w, dtype=dtype, device=device)
+        if "inv_freq" in W:
+            m.inv_freq = torch.from_numpy(np.asarray(W["inv_freq"], np.float32)).to(device)
+        return m
+
+    @classmethod
+    def from_hf(cls, hf_model, *, dtype=None, device=None):
+        """Convert a transformers Qwen2/Llama causal LM (optionally PEFT-wrapped)."""
+        base = hf_model
+        if hasattr(base, "get_base_model"):
+            base = base.get_base_model()
+        c = base.config
+        cfg = TargetConfig(
+            num_layers=c.num_hidden_layers, hidden=c.hidden_size, q_heads=c.num_attention_heads,
+            kv_heads=getattr(c, "num_key_value_heads", c.num_attention_heads),
+            head_dim=getattr(c, "head_dim", None) or c.hidden_size // c.num_attention_heads,
+            intermediate=c.intermediate_size, vocab=c.vocab_size,
+            rope_theta=float(getattr(c, "rope_theta", None) or (getattr(c, "rope_parameters", None) or {}).get(
+                "rope_theta", 1e4)),
+            rms_eps=float(c.rms_norm_eps), qkv_bias=bool(getattr(c, "attention_bias", False) or
+                                                         c.model_type == "qwen2"),
+            tie_word_embeddings=bool(getattr(c, "tie_word_embeddings", False)), name=c.model_type)
+        sd = base.state_dict()
+        dev = device or next(base.parameters()).device
+        dt = dtype or next(base.parameters()).dtype
+
+        def g(k):
+            return sd[k].to(device=dev, dtype=dt).contiguous()
+
+        w = {"embed": g("model.embed_tokens.weight"), "final_norm": g("model.norm.weight"), "layers": []}
+        for i in range(cfg.num_layers):
+            p = f"model.layers.{i}."
+            qkv_b = None
+            if p + "self_attn.q_proj.bias" in sd:
+                qkv_b = torch.cat([g(p + "self_attn.q_proj.bias"), g(p + "self_attn.k_proj.bias"),
+                                   g(p + "self_attn.v_proj.bias")])
+            w["layers"].append({
+                "input_norm": g(p + "input_layernorm.weight"),
+                "qkv_w": torch.cat([g(p + "self_attn.q_proj.weight"), g(p + "self_attn.k_proj.weight"),
+                                    g(p + "self_attn.v_proj.weight")]),
+                "qkv_b": qkv_b,
+                "o_w": g(p + "self_attn.o_proj.weight"),
+                "post_norm": g(p + "post_attention_layernorm.weight"),
+                "gate_up_w": torch.cat([g(p + "mlp.gate_proj.weight"), g(p + "mlp.up_proj.weight")]),
+                "down_w": g(p + "mlp.down_proj.weight"),
+            })
+        w["lm_head"] = g("lm_head.weight") if "lm_head.weight" in sd else w["embed"]
+        cfg.qkv_bias = w["layers"][0]["qkv_b"] is not None
+        m = cls(cfg, w, dtype=dt, device=dev)
+        rot = getattr(base.model, "rotary_emb", None)
+        if rot is not None and hasattr(rot, "inv_freq"):
+            m.inv_freq = rot.inv_freq.detach().to(device=dev, dtype=torch.float32)
+        return m
+
+    @property
+    def lm_head_weight(self) -> torch.Tensor:
+        return self.w["lm_head"]
+
+    @property
+    def embed_weight(self) -> torch.Tensor:
+        return self.w["embed"]
+
+    def new_cache(self, batch: int, capacity: int) -> KVCache:
+        return KVCache(self.cfg, batch, capacity, dtype=self.dtype, device=self.device)
+
+    # -------------------------------------------------------------- forward
+    def _buf(self, name, shape, dtype=None):
+        dtype = dtype or self.dtype
+        numel = int(np.prod(shape))
+        b = self._bufs.get(name)
+        if b is None or b.numel() < numel or b.dtype != dtype:
+            b = torch.empty(max(numel, 1), dtype=dtype, device=self.device)
+            self._bufs[name] = b
+        return b[:numel].view(*shape)
+
+    def forward(self, tokens: torch.Tensor, cache: KVCache, *, pos_offset: torch.Tensor, anc: torch.Tensor,
+                seq_len: torch.Tensor | None = None, row_map: torch.Tensor | None = None,
+                err_flag: torch.Tensor | None = None) -> torch.Tensor:
+        """Forward N new tokens per row after each row's committed prefix.
+
+        tokens [B, N] int (device); pos_offset [N] int32: position = seq_len[b] + pos_offset[n];
+        anc: int64 bit masks [N] (shared) or [B, N]; node n's K/V land in cache slot
+        seq_len[b] + n of cache row row_map[b]. Returns final-normed hidden [B, N, H].
+        ``seq_len`` defaults to ``cache.seq_len`` and is not advanced here.
+        """
+        cfg = self.cfg
+        B, N = tokens.shape
+        if N > MAX_TREE_NODES:
+            raise ValueError(f"at most {MAX_TREE_NODES} new tokens per forward")
+        seq_len = cache.seq_len if seq_len is None else seq_len
+        T = B * N
+        H, d = cfg.hidden, cfg.head_dim
+        x = self.w["embed"].index_select(0, tokens.reshape(-1).long())  # [T, H] residual stream
+        q = self._buf("q", (B, N, cfg.q_heads, d))
+        attn = self._buf("attn", (B, N, cfg.q_heads, d))
+        delta = None
+        for l, lw in enumerate(self.w["layers"]):
+            h = K.rmsnorm(x, lw["input_norm"], cfg.rms_eps, delta=delta, out=self._buf("h", (T, H)))
+            qkv = F.linear(h, lw["qkv_w"], lw["qkv_b"])
+            K.rope_kv_write(qkv, batch=B, num_nodes=N, q_heads=cfg.q_heads, kv_heads=cfg.kv_heads, head_dim=d,
+                            seq_len=seq_len, pos_offset=pos_offset, inv_freq=self.inv_freq, q_out=q,
+                            k_cache=cache.k(l), v_cache=cache.v(l), row_map=row_map, err_flag=err_flag)
+            K.tree_attention(q, cache.k(l), cache.v(l), seq_len=seq_len, anc=anc, num_nodes=N, q_heads=cfg.q_heads,
+                             kv_heads=cfg.kv_heads, head_dim=d, out=attn, row_map=row_map)
+            o = F.linear(attn.view(T, cfg.q_heads * d), lw["o_w"])
+            h2 = K.rmsnorm(x, lw["post_norm"], cfg.rms_eps, delta=o, out=self._buf("h", (T, H)))
+            gu = F.linear(h2, lw["gate_up_w"])
+            act = K.swiglu(gu, out=self._buf("act", (T, cfg.intermediate)))
+            delta = F.linear(act, lw["down_w"])
+        out = torch.empty(T, H, dtype=self.dtype, device=self.device)
+        K.rmsnorm(x, self.w["final_norm"], cfg.rms_eps, delta=delta, out=out)
+        return out.view(B, N, H)
+
+    def logits(self, hidden: torch.Tensor, *, row_index=None, out_dtype=None) -> torch.Tensor:
+        return K.lm_head(hidden.reshape(-1, self.cfg.hidden), self.w["lm_head"], row_index=row_index,
+                         out_dtype=out_dtype)
+
+    def prefill(self, input_ids: torch.Tensor, cache: KVCache, *, lengths=None, chunk: int = MAX_TREE_NODES,
+                row_map: torch.Tensor | None = None) -> torch.Tensor:
+        """Causal prefill of left-aligned prompts in 64-token chains.
+
+        input_ids [B, P] (device or host) holds each row's valid tokens left-aligned
+        (row b has ``lengths[b]`` of them, default P). Writes cache slots [0, len) of
+        every row, sets ``cache.seq_len`` and returns the hidden state of each row's
+        last token [B, H].
+        """
+        B, P = input_ids.shape
+        ids = input_ids.to(self.device, dtype=torch.int32)
+        lens = np.full(B, P, dtype=np.int64) if lengths is None else np.asarray(lengths, dtype=np.int64)
+        if lens.min() < 1:
+            raise ValueError("every prompt needs at least one token")
+        seq = torch.zeros(B, dtype=torch.int32, device=self.device)
+        cache.seq_len.zero_()
+        last = torch.empty(B, self.cfg.hidden, dtype=self.dtype, device=self.device)
+        anc_full = as_mask_tensor(chain_bits(chunk), self.device)
+        offs_full = torch.arange(chunk, dtype=torch.int32, device=self.device)
+        for start in range(0, int(lens.max()), chunk):
+            n = min(chunk, P - start)
+            tok = ids[:, start:start + n].contiguous()
+            hid = self.forward(tok, cache, pos_offset=offs_full[:n], anc=anc_full[:n], seq_len=seq, row_map=row_map)
+            adv = np.clip(lens - start, 0, n)
+            ends = np.nonzero((lens > start) & (lens <= start + n))[0]
+            if ends.size:
+                e = torch.from_numpy(ends).to(self.device)
+                pos = torch.from_numpy(lens[ends] - start - 1).to(self.device)
+                last.index_copy_(0, e, hid[e, pos])
+            seq += torch.from_numpy(adv.astype(np.int32)).to(self.device)
+        if row_map is None:
+            cache.seq_len.copy_(seq)
+        else:
+            cache.seq_len.index_copy_(0, row_map.long(), seq)
+        return last

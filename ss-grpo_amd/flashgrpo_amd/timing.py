@@ -1,0 +1,78 @@
+"""Per-kernel HIP-event timing for the benchmark.
+
+When a ``KernelTimer`` is active, every C-ABI launch made through
+``flashgrpo_amd.kernels`` is bracketed by two ``torch.cuda.Event`` records on
+the stream the kernel is launched on (torch's current stream). Labels set with
+``label(...)`` refine the kernel name (e.g. the LM-head GEMM of the packed tree
+rows vs. the Medusa rows). Off by default: no events are recorded.
+"""
+from __future__ import annotations
+
+import contextlib
+import threading
+from collections import defaultdict
+
+import torch
+
+_state = threading.local()
+
+
+class KernelTimer:
+    def __init__(self):
+        self.events = defaultdict(list)
+
+    def summary(self) -> dict:
+        """{name: {"count", "total_ms", "avg_ms"}} after synchronising."""
+        torch.cuda.synchronize()
+        out = {}
+        for name, evs in self.events.items():
+            ms = [s.elapsed_time(e) for s, e in evs]
+            out[name] = {"count": len(ms), "total_ms": float(sum(ms)), "avg_ms": float(sum(ms) / max(len(ms), 1))}
+        return out
+
+
+def _timer():
+    return getattr(_state, "timer", None)
+
+
+def _labels():
+    if not hasattr(_state, "labels"):
+        _state.labels = []
+    return _state.labels
+
+
+@contextlib.contextmanager
+def active(timer: KernelTimer | None):
+    prev = _timer()
+    _state.timer = timer
+    try:
+        yield timer
+    finally:
+        _state.timer = prev
+
+
+@contextlib.contextmanager
+def label(name: str):
+    _labels().append(name)
+    try:
+        yield
+    finally:
+        _labels().pop()
+
+
+@contextlib.contextmanager
+def launch(kernel: str):
+    t = _timer()
+    if t is None:
+        yield
+        return
+    labels = _labels()
+    name = kernel + (":" + labels[-1] if labels else "")
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    try:
+        yield
+    finally:
+        e.record()
+        t.events[name].append((s, e))

@@ -1,0 +1,246 @@
+"""End-to-end rollout parity: FlashMedusaDecoder.generate on the GPU in lockstep
+with the CPU oracle.
+
+Every verify round is replayed on the oracle from the GPU's own inputs to that
+round: decisions (root draw, plan, tree tokens, accepted path and length,
+finish flags, b200 forced roots) must be bit-exact given the GPU's logits;
+floating-point values (hidden states, Medusa logits, tree hidden states, tree
+logits) must be within 1e-5 (fp32) / 2e-2 (bf16) max relative error of an
+independent float64 oracle that recomputes the accepted tokens' KV (so the
+next round also checks extract == recompute).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import decode as OD
+from oracle import model as OM
+from oracle import sampling as OS
+from oracle import tree as OT
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+def rel(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+class Tok:
+    def __init__(self, eos):
+        self.eos_token_id = eos
+        self.pad_token_id = 0
+
+
+def build(ocfg, W, heads, dtype):
+    from flashgrpo_amd.models import MedusaHeads, TargetConfig, TargetModel
+
+    tcfg = TargetConfig(ocfg.num_layers, ocfg.hidden, ocfg.q_heads, ocfg.kv_heads, ocfg.head_dim, ocfg.intermediate,
+                        ocfg.vocab, ocfg.rope_theta, ocfg.rms_eps, ocfg.qkv_bias, ocfg.tie_word_embeddings)
+    model = TargetModel.from_numpy(tcfg, W, dtype=dtype, device=DEV)
+    mh = MedusaHeads(ocfg.hidden, ocfg.vocab, len(heads)).to(DEV)
+    with torch.no_grad():
+        for hd, src in zip(mh.heads, heads):
+            hd.fc.weight.copy_(torch.from_numpy(src["fc_w"]))
+            hd.fc.bias.copy_(torch.from_numpy(src["fc_b"]))
+            hd.norm.weight.copy_(torch.from_numpy(src["ln_w"]))
+            hd.norm.bias.copy_(torch.from_numpy(src["ln_b"]))
+    return model, mh
+
+
+def rounded(W, heads, dtype):
+    if dtype == torch.float32:
+        return W, heads
+    r = lambda a: None if a is None else torch.from_numpy(np.asarray(a)).to(torch.bfloat16).float().numpy()
+    Wr = {k: r(v) for k, v in W.items() if k not in ("layers", "inv_freq")}
+    Wr["inv_freq"] = W["inv_freq"]
+    Wr["layers"] = [{k: r(v) for k, v in lw.items()} for lw in W["layers"]]
+    hr = [dict(h, fc_w=r(h["fc_w"]), fc_b=r(h["fc_b"])) for h in heads]
+    return Wr, hr
+
+
+class OracleRow:
+    """Per-sequence float64 oracle cache, advanced by recomputing accepted tokens."""
+
+    def __init__(self, ocfg, W, prompt):
+        self.cfg, self.W = ocfg, W
+        hid, self.k, self.v = OM.prefill(ocfg, W, np.asarray(prompt)[None])
+        self.hidden = hid[0, -1]
+        self.len = len(prompt)
+
+    def append(self, toks):
+        n = len(toks)
+        hid, nk, nv = OM.forward(self.cfg, self.W, np.asarray(toks)[None], (self.len + np.arange(n))[None], self.k,
+                                 self.v, np.ones((1, self.len), bool), np.tril(np.ones((n, n), bool))[None])
+        self.k = [np.concatenate([a, b], axis=2) for a, b in zip(self.k, nk)]
+        self.v = [np.concatenate([a, b], axis=2) for a, b in zip(self.v, nv)]
+        self.hidden = hid[0, -1]
+        self.len += n
+
+    def tree(self, toks, parents, depths):
+        N = len(toks)
+        allowed = np.zeros((1, N, N), bool)
+        for n in range(N):
+            a = n
+            while a >= 0:
+                allowed[0, n, a] = True
+                a = parents[a]
+        pos = self.len + np.asarray(depths) - 1
+        hid, _, _ = OM.forward(self.cfg, self.W, np.asarray(toks)[None], pos[None], self.k, self.v,
+                               np.ones((1, self.len), bool), allowed)
+        return hid[0]
+
+
+def lockstep(trace, ocfg, Wr, heads_r, spec, prompts, dtype, seed, max_length, emit_correction=False):
+    tol = TOL[dtype]
+    rows = {}
+    for s in range(prompts.shape[0]):
+        rows[s] = OracleRow(ocfg, Wr, prompts[s])
+    kw = dict(do_sample=spec.do_sample and spec.temperature != 0, temperature=spec.temperature, top_p=spec.top_p,
+              top_k=spec.top_k)
+    stats = dict(rounds=0, deep=0, max_acc=1)
+    pending = {}
+    for rec in trace:
+        rnd, active = rec["round"], rec["active"]
+        Bc = len(active)
+        for i, s in enumerate(active):
+            assert rel(rec["hidden_in"][i], rows[s].hidden) < tol, (rnd, s)
+            assert rel(rec["logits_in"][i], OM.logits(rows[s].hidden, Wr["lm_head"])) < tol, (rnd, s)
+        want_roots = [pending[s] if s in pending else
+                      OS.sample_row(rec["logits_in"][i], OS.counter_noise(seed, rnd, s, 0), **kw)
+                      for i, s in enumerate(active)]
+        assert rec["roots"].tolist() == want_roots, rnd
+        plan = OD.plan_for(spec, Bc)
+        if "medusa_logits" in rec:
+            nh = plan.active_heads
+            ml = rec["medusa_logits"].reshape(nh, Bc, -1)
+            want_ml = OM.medusa_logits(rec["hidden_in"], heads_r, Wr["lm_head"], nh)
+            for d in range(nh):
+                assert rel(ml[d], want_ml[d]) < tol
+            plan = OD.adapt_plan(spec, plan, [ml[d] for d in range(nh)])
+        assert rec["plan"] == list(plan.topk_by_depth), rnd
+        heads_logits = []
+        if "medusa_logits" in rec:
+            ml = rec["medusa_logits"]
+            heads_logits = list(ml.reshape(ml.shape[0] // Bc, Bc, -1))
+        trees = OT.build_batch_trees(rec["roots"], heads_logits, plan)
+        assert rec["tree_tokens"].tolist() == [t.tokens for t in trees], rnd
+        N = trees[0].node_count
+        if "tree_logits" in rec:
+            for i, s in enumerate(active):
+                want_h = rows[s].tree(trees[i].tokens, trees[i].parents, trees[i].depths)
+                assert rel(rec["tree_hidden"][i], want_h) < tol, (rnd, s)
+            nz = [[OS.counter_noise(seed, rnd, s, 1 + t) for t in range(N)] for s in active]
+            if rec["slot_map"] is not None:  # packed internal-node rows
+                r_, n_, slots = OT.internal_slots(trees)
+                want_tl = OM.logits(rec["tree_hidden"][r_, n_], Wr["lm_head"])
+                assert rec["slot_map"].tolist() == slots
+                walk_logits = rec["tree_logits"]
+            else:  # every node projected, dense [B, N, V]
+                slots = None
+                want_tl = OM.logits(rec["tree_hidden"].reshape(Bc * N, -1), Wr["lm_head"])
+                walk_logits = rec["tree_logits"].reshape(Bc, N, -1)
+            assert rel(rec["tree_logits"], want_tl) < tol
+            at, an, last, corr = OS.accept_walk(trees, walk_logits, nz, slots=slots, emit_correction=True, **kw)
+        else:
+            at, an, last, corr = [[int(r)] for r in rec["roots"]], [[0]] * Bc, [0] * Bc, [None] * Bc
+        pending = {}
+        for i, s in enumerate(active):
+            raw = len(at[i])
+            t, n, fin, _ = OS.clamp_accepted(at[i], an[i], remaining=max_length - rows[s].len,
+                                             eos_token_id=spec.eos_token_id, old_len=rows[s].len,
+                                             max_length=max_length)
+            L = int(rec["acc_len"][i])
+            assert rec["acc_tokens"][i, :L].tolist() == t, (rnd, s)
+            assert bool(rec["finished"][i]) == fin
+            assert int(rec["last_node"][i]) == n[-1]
+            stats["max_acc"] = max(stats["max_acc"], L)
+            if emit_correction and corr[i] is not None and len(t) == raw and not fin:
+                pending[s] = corr[i]
+            rows[s].append(t)
+        if emit_correction:
+            assert sorted(pending.items()) == sorted((s, int(p)) for s, p in zip(active, rec["pending"]) if p >= 0)
+        stats["rounds"] += 1
+    return stats
+
+
+def _run(ocfg, spec, *, dtype, B0, repeats, P, max_length, seed=123, wseed=0, cache_mode="extract_path",
+         internal_only=True):
+    from flashgrpo_amd.decoding import FlashMedusaConfig, FlashMedusaDecoder
+
+    W = OM.random_weights(ocfg, seed=wseed, std=0.05)
+    heads = OM.random_medusa(ocfg.hidden, spec.num_medusa_heads, seed=wseed + 1, std=0.05)
+    model, mh = build(ocfg, W, heads, dtype)
+    cfg = FlashMedusaConfig(num_medusa_heads=spec.num_medusa_heads, tree_mode=spec.tree_mode,
+                            cpeak_nodes=spec.cpeak_nodes, max_tree_nodes_per_seq=spec.max_tree_nodes_per_seq,
+                            max_tree_depth=spec.max_tree_depth, fixed_tree_topk_by_depth=spec.fixed_tree_topk_by_depth,
+                            adaptive_tree_enabled=spec.adaptive_tree_enabled, do_sample=spec.do_sample,
+                            temperature=spec.temperature, top_p=spec.top_p, top_k=spec.top_k,
+                            emit_correction_token=spec.emit_correction_token, noise_seed=seed,
+                            cache_update_mode=cache_mode, project_internal_tree_logits_only=internal_only)
+    dec = FlashMedusaDecoder(model, mh, Tok(spec.eos_token_id), cfg)
+    rng = np.random.default_rng(wseed + 7)
+    prompts = rng.integers(0, ocfg.vocab, (B0, P))
+    trace = []
+    out = dec.generate(torch.from_numpy(prompts), torch.ones(B0, P, dtype=torch.long), repeated_generate_nums=repeats,
+                       max_length=max_length, trace=trace)
+    Wr, hr = rounded(W, heads, dtype)
+    seed_eff = trace[0]["seed"]
+    stats = lockstep(trace, ocfg, Wr, hr, spec, np.repeat(prompts, repeats, axis=0), dtype, seed_eff, max_length,
+                     emit_correction=spec.emit_correction_token)
+    for s, g in enumerate(out["generated_token_ids"]):
+        assert len(g) >= 1
+    return out, stats
+
+
+SMALL = OM.ModelConfig(num_layers=2, hidden=256, q_heads=4, kv_heads=2, head_dim=64, intermediate=512, vocab=64)
+SMALL16 = OM.ModelConfig(num_layers=2, hidden=256, q_heads=4, kv_heads=2, head_dim=128, intermediate=512, vocab=64)
+
+
+@pytest.mark.parametrize("top_p", [1.0, 0.9])
+def test_lockstep_fp32_fixed_tree_small_vocab(top_p):
+    spec = OD.DecodeSpec(tree_mode="fixed", max_tree_nodes_per_seq=16, fixed_tree_topk_by_depth=(4, 2, 1),
+                         num_medusa_heads=3, max_tree_depth=4, top_p=top_p)
+    out, st = _run(SMALL, spec, dtype=torch.float32, B0=3, repeats=2, P=33, max_length=33 + 24)
+    assert st["max_acc"] >= 2  # a 64-token vocabulary accepts children: the gather moves real paths
+    assert out["kv_extraction_success_count"] == st["rounds"]
+
+
+def test_lockstep_bf16_concurrency_tree():
+    spec = OD.DecodeSpec(tree_mode="concurrency_aware", cpeak_nodes=48, max_tree_nodes_per_seq=16,
+                         fixed_tree_topk_by_depth=(4, 3, 2), num_medusa_heads=3, max_tree_depth=4, top_p=0.95,
+                         eos_token_id=5)
+    _run(SMALL16, spec, dtype=torch.bfloat16, B0=2, repeats=2, P=70, max_length=70 + 20)
+
+
+def test_lockstep_adaptive_b200_greedy_and_recompute():
+    spec = OD.DecodeSpec(tree_mode="concurrency_aware", cpeak_nodes=64, max_tree_nodes_per_seq=32,
+                         fixed_tree_topk_by_depth=(4, 3, 2), num_medusa_heads=4, max_tree_depth=5,
+                         adaptive_tree_enabled=True, top_p=1.0, emit_correction_token=True)
+    out, st = _run(SMALL, spec, dtype=torch.float32, B0=2, repeats=1, P=20, max_length=20 + 16)
+    assert out["total_correction_tokens"] >= 0
+    spec_g = OD.DecodeSpec(tree_mode="fixed", max_tree_nodes_per_seq=12, fixed_tree_topk_by_depth=(3, 2),
+                           num_medusa_heads=2, do_sample=False)
+    _run(SMALL, spec_g, dtype=torch.float32, B0=2, repeats=2, P=17, max_length=17 + 12, cache_mode="recompute_accepted")
+    _run(SMALL, spec_g, dtype=torch.float32, B0=2, repeats=2, P=17, max_length=17 + 12, internal_only=False)
+
+
+def test_tiny_config_32_rounds_fp32():
+    """4 layers, H512, 8/2 heads, d64, F1408, V32000, fixed [4,3,2] in 16 nodes,
+    8 sequences (4 prompts x 2 repeats), 256-token prefix, T=1, 32 verify rounds."""
+    cfg = OM.ModelConfig(num_layers=4, hidden=512, q_heads=8, kv_heads=2, head_dim=64, intermediate=1408,
+                         vocab=32000, rope_theta=1e6, tie_word_embeddings=True)
+    spec = OD.DecodeSpec(tree_mode="fixed", max_tree_nodes_per_seq=16, fixed_tree_topk_by_depth=(4, 3, 2),
+                         num_medusa_heads=3, max_tree_depth=4, top_p=1.0)
+    out, st = _run(cfg, spec, dtype=torch.float32, B0=4, repeats=2, P=256, max_length=256 + 32)
+    # one token per round unless a rare Medusa candidate is accepted
+    assert 28 <= st["rounds"] == out["total_verify_rounds"] <= 32
+    assert out["last_tree_plan"]["topk_by_depth"] == [4, 2]

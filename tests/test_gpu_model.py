@@ -1,0 +1,122 @@
+"""Target-model parity on the GPU: prefill, tree verify and the KV it writes,
+against the float64 oracle decoder (max|a-b|/max|b| <= 1e-5 fp32, 2e-2 bf16)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import model as OM
+from oracle import tree as OT
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+def rel(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def _cfgs(dtype):
+    if dtype == torch.float32:
+        return OM.ModelConfig(num_layers=2, hidden=256, q_heads=4, kv_heads=2, head_dim=64, intermediate=512,
+                              vocab=1000)
+    return OM.ModelConfig(num_layers=2, hidden=512, q_heads=8, kv_heads=2, head_dim=128, intermediate=768,
+                          vocab=1000)
+
+
+def _model(ocfg, W, dtype):
+    from flashgrpo_amd.models.target import TargetConfig, TargetModel
+
+    tcfg = TargetConfig(ocfg.num_layers, ocfg.hidden, ocfg.q_heads, ocfg.kv_heads, ocfg.head_dim, ocfg.intermediate,
+                        ocfg.vocab, ocfg.rope_theta, ocfg.rms_eps, ocfg.qkv_bias, ocfg.tie_word_embeddings)
+    return TargetModel.from_numpy(tcfg, W, dtype=dtype, device=DEV)
+
+
+def _rounded(W, dtype):
+    """Weights as the device holds them (bf16-rounded for the bf16 model)."""
+    if dtype == torch.float32:
+        return W
+    r = lambda a: None if a is None else torch.from_numpy(a).to(torch.bfloat16).float().numpy()
+    out = {k: r(v) for k, v in W.items() if k not in ("layers", "inv_freq")}
+    out["inv_freq"] = W["inv_freq"]
+    out["layers"] = [{k: r(v) for k, v in lw.items()} for lw in W["layers"]]
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_prefill_and_tree_verify_match_oracle(dtype):
+    ocfg = _cfgs(dtype)
+    rng = np.random.default_rng(0)
+    W = OM.random_weights(ocfg, seed=1, std=0.05)
+    for lw in W["layers"]:
+        lw["q_b"] = (rng.standard_normal(lw["q_b"].shape) * 0.1).astype(np.float32)
+        lw["k_b"] = (rng.standard_normal(lw["k_b"].shape) * 0.1).astype(np.float32)
+    m = _model(ocfg, W, dtype)
+    Wr = _rounded(W, dtype)
+    B, P = 3, 150
+    lens = np.array([150, 97, 64])
+    prompts = rng.integers(0, ocfg.vocab, (B, P))
+    cache = m.new_cache(B, 256)
+    last = m.prefill(torch.from_numpy(prompts).to(DEV), cache, lengths=lens)
+    assert cache.seq_len.cpu().tolist() == lens.tolist()
+    for b in range(B):
+        hid, ks, vs = OM.prefill(ocfg, Wr, prompts[b:b + 1, :lens[b]])
+        assert rel(last[b].float().cpu().numpy(), hid[0, -1]) < TOL[dtype]
+        for li in range(ocfg.num_layers):
+            assert rel(cache.k(li)[b, :, :lens[b]].float().cpu().numpy(), ks[li][0]) < TOL[dtype]
+            assert rel(cache.v(li)[b, :, :lens[b]].float().cpu().numpy(), vs[li][0]) < TOL[dtype]
+    # tree verify on top of the ragged prefixes
+    from flashgrpo_amd.decoding.medusa_tree import TreeTopology
+
+    topo = TreeTopology([4, 2, 1], 16)
+    N = topo.num_nodes
+    toks = rng.integers(0, ocfg.vocab, (B, N))
+    d = topo.device(DEV)
+    hid_t = m.forward(torch.from_numpy(toks).to(DEV).to(torch.int32), cache, pos_offset=d["pos_offset"], anc=d["anc"])
+    logits = m.logits(hid_t, out_dtype=torch.float32)
+    for b in range(B):
+        _, ks, vs = OM.prefill(ocfg, Wr, prompts[b:b + 1, :lens[b]])
+        want, tk, tv = OM.tree_verify(ocfg, Wr, toks[b:b + 1], [topo.depths], [topo.parents], ks, vs, [lens[b]])
+        assert rel(hid_t[b].float().cpu().numpy(), want[0]) < TOL[dtype]
+        assert rel(logits[b * N:(b + 1) * N].cpu().numpy(), OM.logits(want[0], Wr["lm_head"])) < TOL[dtype]
+        for li in range(ocfg.num_layers):
+            got = cache.k(li)[b, :, lens[b]:lens[b] + N].float().cpu().numpy()
+            assert rel(got, tk[li][0]) < TOL[dtype]
+
+
+def test_tree_logits_equal_sequential_path_on_device():
+    """The reference's promise (tree_attention.py:14-19): batched tree logits equal
+    each root-to-node path forwarded on its own."""
+    ocfg = _cfgs(torch.float32)
+    W = OM.random_weights(ocfg, seed=4, std=0.05)
+    m = _model(ocfg, W, torch.float32)
+    from flashgrpo_amd.decoding.medusa_tree import TreeTopology
+    from flashgrpo_amd.models.target import as_mask_tensor, chain_bits
+
+    rng = np.random.default_rng(5)
+    B, P = 2, 40
+    prompts = torch.from_numpy(rng.integers(0, ocfg.vocab, (B, P))).to(DEV)
+    topo = TreeTopology([3, 2, 1], 16)
+    toks = torch.from_numpy(rng.integers(0, ocfg.vocab, (B, topo.num_nodes))).to(DEV).to(torch.int32)
+    cache = m.new_cache(B, 128)
+    m.prefill(prompts, cache)
+    d = topo.device(DEV)
+    tree_h = m.forward(toks, cache, pos_offset=d["pos_offset"], anc=d["anc"])
+    from oracle.tree import Tree
+
+    t = Tree(list(range(topo.num_nodes)), topo.parents, topo.depths)
+    for n in range(topo.num_nodes):
+        path = t.ancestors_including_self(n)
+        c2 = m.new_cache(B, 128)
+        m.prefill(prompts, c2)
+        chain = toks[:, path].contiguous()
+        h = m.forward(chain, c2, pos_offset=torch.arange(len(path), dtype=torch.int32, device=DEV),
+                      anc=as_mask_tensor(chain_bits(len(path)), DEV))
+        assert rel(tree_h[:, n].cpu().numpy(), h[:, -1].cpu().numpy()) < 1e-5
