@@ -72,23 +72,33 @@ def build(work, dtype, seed=0):
 
 
 def algorithmic_work(cfg, rnd, seq_before, elem):
-    """Per-kernel algorithmic bytes / flops of one verify round (the roofline numerators)."""
+    """Per-kernel algorithmic bytes / flops of one verify round (the roofline numerators),
+    summed over the round's launches of that kernel."""
     B, N, I, nh = rnd["batch"], rnd["num_nodes"], rnd["internal"], rnd["heads"]
     H, V, d, Hq, Hkv, L = cfg.hidden, cfg.vocab, cfg.head_dim, cfg.q_heads, cfg.kv_heads, cfg.num_layers
     keys = sum(int(s) + N for s in seq_before)
-    attn_bytes = 2 * Hkv * keys * d * elem + 2 * B * N * Hq * d * elem       # per layer launch
-    attn_flops = 4 * Hq * N * d * keys                                          # per layer launch
-    M = B * I
+    attn_bytes = 2 * Hkv * keys * d * elem + 2 * B * N * Hq * d * elem       # one layer: K, V, Q in, O out
+    attn_flops = 4 * Hq * N * d * keys                                          # one layer: QK^T and PV
+    draws = int(rnd["walk_draws"].sum())
     w = {
-        "fg_tree_attention": dict(bytes=attn_bytes, flops=attn_flops, launches=L),
-        "fg_lm_head:tree": dict(flops=2 * M * H * V, bytes=H * V * elem + M * H * elem + M * V * elem, launches=1),
+        "fg_tree_attention": dict(bytes=L * attn_bytes, flops=L * attn_flops, launches=L),
         "fg_lm_head:medusa": dict(flops=2 * nh * B * H * V, bytes=H * V * elem + nh * B * (H + V) * elem, launches=1),
         "fg_medusa_heads": dict(flops=2 * nh * B * H * H, bytes=nh * H * H * elem, launches=1),
         "fg_medusa_topk": dict(bytes=nh * B * V * elem, launches=1),
         "fg_sample_tokens": dict(bytes=B * V * elem, launches=1),
-        "fg_accept_walk": dict(bytes=int(rnd["walk_draws"].sum()) * V * elem, launches=1),
         "fg_kv_path_gather": dict(bytes=2 * L * 2 * Hkv * int(rnd["acc_len"].sum()) * d * elem, launches=1),
     }
+    if rnd.get("lazy"):
+        # one launch per walk step, each streams the whole LM-head weight once for its active rows
+        D = rnd["walk_steps"]
+        w["fg_lm_head:tree"] = dict(flops=2 * draws * H * V, bytes=D * H * V * elem + draws * (H + V) * elem,
+                                    launches=D)
+        w["fg_walk_step"] = dict(bytes=draws * V * elem, launches=D)
+    else:
+        M = B * I
+        w["fg_lm_head:tree"] = dict(flops=2 * M * H * V, bytes=H * V * elem + M * H * elem + M * V * elem,
+                                    launches=1)
+        w["fg_accept_walk"] = dict(bytes=draws * V * elem, launches=1)
     return w
 
 

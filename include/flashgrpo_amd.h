@@ -22,6 +22,7 @@
  *   fg_rmsnorm, fg_swiglu  models/qwen_flashgrpo_wrapper.py:172-180 (HF decoder layer)
  *   fg_sample_tokens    decoding/acceptance.py:34-130 (sample_from_logits)
  *   fg_accept_walk      decoding/acceptance.py:179-260 (exact_accept_paths_batch);
+ *   fg_walk_begin/rows/step  the same walk, one step per call (lazy LM-head rows);
  *                       flashgrpo_b200/decoding/acceptance.py:184-267 (correction tokens)
  *   fg_accept_finalize  decoding/flash_medusa_decoder.py:899-922;
  *                       flashgrpo_b200/decoding/flash_medusa_decoder.py:2303-2319
@@ -53,9 +54,11 @@ int fg_medusa_heads(const void* hidden, int dtype, int batch, int H, int64_t ldh
 
 /* Tied LM-head projection: out[m, :] = x[row_index ? row_index[m] : m, :] . w^T
  * x [*, K] (row stride ldx), w [N, K] (row stride ldw), out [M, N] (row stride ldo).
+ * row_active (optional, [M]): output tiles whose rows are all 0 there are not computed.
  * bf16 requires K % 64 == 0 and 16-byte aligned rows. */
-int fg_lm_head(const void* x, int dtype, int M, int K, int64_t ldx, const int32_t* row_index, const void* w,
-               int64_t ldw, int N, void* out, int out_dtype, int64_t ldo, void* stream);
+int fg_lm_head(const void* x, int dtype, int M, int K, int64_t ldx, const int32_t* row_index,
+               const int32_t* row_active, const void* w, int64_t ldw, int N, void* out, int out_dtype, int64_t ldo,
+               void* stream);
 
 /* Per-row top-kmax candidates, ranked (value desc, index asc).
  * logits [rows, vocab] with row stride row_stride (multiple of 8, 32-byte aligned base).
@@ -117,7 +120,7 @@ int fg_sample_tokens(const void* logits, int dtype, int64_t row_stride, int rows
  * or row b*nmax + n when slot_map is NULL (dense). Walk step t (0-based) draws
  * noise[b*noise_stride + noise_col0 + t] or counter noise with draw index draw0 + t.
  * Outputs: acc_tokens/acc_nodes [batch, acc_stride], acc_len, last_node, correction
- * (the unmatched sample, -1 if none). workspace: 2*batch int32. err_flag bits:
+ * (the unmatched sample, -1 if none). workspace: 3*batch int32 (walk state). err_flag bits:
  * 2 = a walked node had no logits row, 4 = acc_stride too small. */
 int fg_accept_walk(const void* tree_logits, int dtype, int64_t row_stride, int vocab, const int32_t* slot_map,
                    const int32_t* tree_tokens, const int32_t* parents, const int32_t* n_nodes, int nmax, int batch,
@@ -125,6 +128,24 @@ int fg_accept_walk(const void* tree_logits, int dtype, int64_t row_stride, int v
                    uint64_t step, const int32_t* seq_ids, int draw0, float temperature, int greedy, int top_k,
                    uint32_t top_p_fixed, int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len,
                    int32_t* last_node, int32_t* correction, int32_t* workspace, int32_t* err_flag, void* stream);
+
+/* The same walk one step at a time, for callers that compute each step's logits
+ * rows on demand (the LM head of only the nodes the walk actually samples):
+ *   fg_walk_begin  -- initialise outputs and the walk state (3*batch int32);
+ *   fg_walk_rows   -- row_index[b] = b*nmax + current parent of b, row_active[b];
+ *   fg_walk_step   -- draw for every active row b from row b of step_logits
+ *                     (noise column noise_col0 + walk_step, counter draw draw0 + walk_step).
+ * After the walk, state[2*batch + b] is the step whose logits row b last sampled (-1: none). */
+int fg_walk_begin(const int32_t* tree_tokens, const int32_t* parents, const int32_t* n_nodes, int nmax, int batch,
+                  int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
+                  int32_t* correction, int32_t* state, void* stream);
+int fg_walk_rows(const int32_t* state, int batch, int nmax, int32_t* row_index, int32_t* row_active, void* stream);
+int fg_walk_step(const void* step_logits, int dtype, int64_t row_stride, int vocab, const int32_t* tree_tokens,
+                 const int32_t* parents, const int32_t* n_nodes, int nmax, int batch, int walk_step,
+                 const uint32_t* noise, int noise_stride, int noise_col0, uint64_t seed, uint64_t step,
+                 const int32_t* seq_ids, int draw0, float temperature, int greedy, int top_k, uint32_t top_p_fixed,
+                 int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
+                 int32_t* correction, int32_t* state, int32_t* err_flag, void* stream);
 
 /* Length clamp (max(1, max_length - old_len)), EOS cut (eos_token_id < 0: none),
  * finished flags and, when pending_root != NULL, the next round's forced root

@@ -28,6 +28,7 @@ struct GemmArgs {
   int64_t lda;
   int64_t a_batch;
   const int32_t* a_rows;  // optional row gather for A
+  const int32_t* row_active;  // optional: tiles whose rows are all 0 here are skipped
   const void* B;
   int64_t ldb;
   int64_t b_batch;
@@ -44,6 +45,14 @@ struct GemmArgs {
 };
 
 FG_DEVICE float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+// Block-uniform: does any row of [m0, m0 + rows) have a non-zero row_active flag?
+FG_DEVICE bool tile_has_active_row(const GemmArgs& g, int m0, int rows) {
+  int any = 0;
+  for (int r = threadIdx.x; r < rows; r += blockDim.x)
+    if (m0 + r < g.M) any |= g.row_active[m0 + r] != 0;
+  return __syncthreads_or(any) != 0;
+}
 
 template <int CDT, int BDT>
 FG_DEVICE void epilogue_store(const GemmArgs& g, int z, int m, int n, float acc, int epi) {
@@ -88,6 +97,7 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs g, int epi, int
   const int z = blockIdx.z;
   const int m0 = tm * BM, n0 = tn * BN;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (g.row_active && !tile_has_active_row(g, m0, BM)) return;
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
   const uint16_t* Ab = (const uint16_t*)g.A + z * g.a_batch;
@@ -188,6 +198,140 @@ __global__ void __launch_bounds__(256) gemm_bf16_kernel(GemmArgs g, int epi, int
       }
 }
 
+// ----------------------------------------------------------------- bf16 MFMA, 256-wide N tiles
+// Block tile BM x 256 x 64, 4 waves as 2 (M) x 2 (N), wave tile (BM/2) x 128.
+// The MFMA is issued with the B fragment as its first operand, so every
+// 32x32 accumulator is a tile of C^T: lane l holds row m = l % 32 of C and,
+// for each group of 4 accumulator registers, 4 consecutive columns -- the
+// epilogue writes 8-byte (bf16) / 16-byte (fp32) runs instead of scalars.
+// LDS rows are padded to 72 elements (144 B), which keeps the 16-byte
+// fragment reads of 16 consecutive rows on distinct banks.
+template <int BM, int CDT>
+__global__ void __launch_bounds__(256) gemm_bf16_wide_kernel(GemmArgs g, int epi, int tiles_m, int tiles_n) {
+  constexpr int BN = 256;
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int A_CHUNKS = BM * kBK / 8 / 256;
+  constexpr int B_CHUNKS = BN * kBK / 8 / 256;
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kLdsRow];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * kLdsRow];
+
+  const int nblocks = tiles_m * tiles_n;
+  const int bid = blockIdx.x;
+  const int q = nblocks / 8, rem = nblocks % 8;
+  const int xcd = bid % 8, local = bid / 8;
+  const int t = xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
+  const int tm = t % tiles_m, tn = t / tiles_m;
+  const int z = blockIdx.z;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (g.row_active && !tile_has_active_row(g, m0, BM)) return;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const uint16_t* Ab = (const uint16_t*)g.A + z * g.a_batch;
+  const uint16_t* Bb = (const uint16_t*)g.B + z * g.b_batch;
+  const uint16_t* a_src[A_CHUNKS];
+  int a_dst[A_CHUNKS];
+#pragma unroll
+  for (int c = 0; c < A_CHUNKS; ++c) {
+    int idx = tid + c * 256;
+    int r = idx >> 3, col = (idx & 7) * 8;
+    int m = min(m0 + r, g.M - 1);
+    int src_row = g.a_rows ? g.a_rows[m] : m;
+    a_src[c] = Ab + (int64_t)src_row * g.lda + col;
+    a_dst[c] = r * kLdsRow + col;
+  }
+  const uint16_t* b_src[B_CHUNKS];
+  int b_dst[B_CHUNKS];
+#pragma unroll
+  for (int c = 0; c < B_CHUNKS; ++c) {
+    int idx = tid + c * 256;
+    int r = idx >> 3, col = (idx & 7) * 8;
+    int n = min(n0 + r, g.N - 1);
+    b_src[c] = Bb + (int64_t)n * g.ldb + col;
+    b_dst[c] = r * kLdsRow + col;
+  }
+
+  floatx16 acc[TN][TM];
+#pragma unroll
+  for (int j = 0; j < TN; ++j)
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[j][i][v] = 0.0f;
+
+  uint4 ra[A_CHUNKS], rb[B_CHUNKS];
+  const int ktiles = g.K / kBK;
+#pragma unroll
+  for (int c = 0; c < A_CHUNKS; ++c) ra[c] = *(const uint4*)(a_src[c]);
+#pragma unroll
+  for (int c = 0; c < B_CHUNKS; ++c) rb[c] = *(const uint4*)(b_src[c]);
+#pragma unroll
+  for (int c = 0; c < A_CHUNKS; ++c) *(uint4*)&As[0][a_dst[c]] = ra[c];
+#pragma unroll
+  for (int c = 0; c < B_CHUNKS; ++c) *(uint4*)&Bs[0][b_dst[c]] = rb[c];
+  __syncthreads();
+
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < ktiles;
+    if (more) {
+      const int koff = (kt + 1) * kBK;
+#pragma unroll
+      for (int c = 0; c < A_CHUNKS; ++c) ra[c] = *(const uint4*)(a_src[c] + koff);
+#pragma unroll
+      for (int c = 0; c < B_CHUNKS; ++c) rb[c] = *(const uint4*)(b_src[c] + koff);
+    }
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk) {
+      const int kcol = kk * 16 + (lane >> 5) * 8;
+      bf16x8 af[TM], bfr[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = *(const bf16x8*)&As[cur][(wm * WM + i * 32 + (lane & 31)) * kLdsRow + kcol];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bfr[j] = *(const bf16x8*)&Bs[cur][(wn * WN + j * 32 + (lane & 31)) * kLdsRow + kcol];
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[j][i], 0, 0, 0);
+    }
+    if (more) {
+#pragma unroll
+      for (int c = 0; c < A_CHUNKS; ++c) *(uint4*)&As[cur ^ 1][a_dst[c]] = ra[c];
+#pragma unroll
+      for (int c = 0; c < B_CHUNKS; ++c) *(uint4*)&Bs[cur ^ 1][b_dst[c]] = rb[c];
+    }
+    __syncthreads();
+  }
+
+  // Epilogue: acc[j][i] is the C^T tile (n rows, m columns) -> lane owns row m.
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int m = m0 + wm * WM + i * 32 + (lane & 31);
+    if (m >= g.M) continue;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v4 = 0; v4 < 4; ++v4) {
+        const int n = n0 + wn * WN + j * 32 + v4 * 8 + (lane >> 5) * 4;
+        float o[4] = {acc[j][i][4 * v4], acc[j][i][4 * v4 + 1], acc[j][i][4 * v4 + 2], acc[j][i][4 * v4 + 3]};
+        if (epi == kEpiNone && n + 3 < g.N) {
+          if constexpr (CDT == fg::kBF16) {
+            uint32_t w0 = (uint32_t)fg::f32_to_bf16(o[0]) | ((uint32_t)fg::f32_to_bf16(o[1]) << 16);
+            uint32_t w1 = (uint32_t)fg::f32_to_bf16(o[2]) | ((uint32_t)fg::f32_to_bf16(o[3]) << 16);
+            *(uint2*)((uint16_t*)g.C + z * g.c_batch + (int64_t)m * g.ldc + n) = make_uint2(w0, w1);
+          } else {
+            *(float4*)((float*)g.C + z * g.c_batch + (int64_t)m * g.ldc + n) = make_float4(o[0], o[1], o[2], o[3]);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) epilogue_store<CDT, fg::kBF16>(g, z, m, n + e, o[e], epi);
+        }
+      }
+  }
+}
+
 // ----------------------------------------------------------------- fp32 FMA
 template <int CDT>
 __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs g, int epi) {
@@ -196,6 +340,7 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs g, int epi) {
   __shared__ float Bs[BKf][T + 1];
   const int z = blockIdx.z;
   const int m0 = blockIdx.y * T, n0 = blockIdx.x * T;
+  if (g.row_active && !tile_has_active_row(g, m0, T)) return;
   const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
   const float* Ab = (const float*)g.A + z * g.a_batch;
   const float* Bb = (const float*)g.B + z * g.b_batch;
@@ -240,7 +385,30 @@ int launch_gemm(const GemmArgs& g, int dtype, int out_dtype, int epi, int batch,
     FG_REQUIRE(g.K % kBK == 0, "gemm: bf16 path needs K % 64 == 0");
     FG_REQUIRE(g.lda % 8 == 0 && g.ldb % 8 == 0 && ((uintptr_t)g.A & 15) == 0 && ((uintptr_t)g.B & 15) == 0,
                "gemm: bf16 operands need 16-byte aligned rows");
-    if (g.M <= 64) {
+    const bool wide_ok = g.N >= 512 && g.ldc % 4 == 0 && ((uintptr_t)g.C & 15) == 0 && (g.c_batch % 4) == 0;
+    if (wide_ok) {
+      // Pick the M tile that pads M least (larger tile on ties).
+      const int cands[3] = {192, 128, 64};
+      int BM = 256, best = 1 << 30;
+      for (int c : cands) {
+        int waste = (g.M + c - 1) / c * c - g.M;
+        if (waste < best) {
+          best = waste;
+          BM = c;
+        }
+      }
+      int tm = (g.M + BM - 1) / BM, tn = (g.N + 255) / 256;
+      dim3 grid(tm * tn, 1, batch);
+#define FG_WIDE(BMv)                                                                                          \
+  if (out_dtype == fg::kBF16)                                                                                  \
+    hipLaunchKernelGGL((gemm_bf16_wide_kernel<BMv, fg::kBF16>), grid, dim3(256), 0, s, g, epi, tm, tn);        \
+  else                                                                                                         \
+    hipLaunchKernelGGL((gemm_bf16_wide_kernel<BMv, fg::kF32>), grid, dim3(256), 0, s, g, epi, tm, tn);
+      if (BM == 192) { FG_WIDE(192) }
+      else if (BM == 128) { FG_WIDE(128) }
+      else { FG_WIDE(64) }
+#undef FG_WIDE
+    } else if (g.M <= 64) {
       constexpr int BM = 64, BN = 128;
       int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
       dim3 grid(tm * tn, 1, batch);
@@ -302,12 +470,13 @@ __global__ void __launch_bounds__(256) medusa_ln_kernel(const void* __restrict__
 
 extern "C" {
 
-int fg_lm_head(const void* x, int dtype, int M, int K, int64_t ldx, const int32_t* row_index, const void* w,
-               int64_t ldw, int N, void* out, int out_dtype, int64_t ldo, void* stream) {
+int fg_lm_head(const void* x, int dtype, int M, int K, int64_t ldx, const int32_t* row_index,
+               const int32_t* row_active, const void* w, int64_t ldw, int N, void* out, int out_dtype, int64_t ldo,
+               void* stream) {
   FG_REQUIRE(x && w && out, "fg_lm_head: null pointer");
   FG_REQUIRE(dtype == fg::kF32 || dtype == fg::kBF16, "fg_lm_head: dtype");
   GemmArgs g{};
-  g.A = x; g.lda = ldx; g.a_rows = row_index;
+  g.A = x; g.lda = ldx; g.a_rows = row_index; g.row_active = row_active;
   g.B = w; g.ldb = ldw;
   g.C = out; g.ldc = ldo;
   g.M = M; g.N = N; g.K = K;

@@ -315,7 +315,8 @@ __global__ void __launch_bounds__(kThreads) sample_rows_kernel(
   if (threadIdx.x == 0) out[rrow] = tok;
 }
 
-// Walk state lives in the caller's workspace: parent[B], active[B].
+// Walk state lives in the caller's workspace: parent[B], active[B], and the
+// walk step at which each row last sampled (-1 before its first draw) [B].
 __global__ void walk_init_kernel(const int32_t* __restrict__ tree_tokens, const int32_t* __restrict__ parents,
                                  const int32_t* __restrict__ n_nodes, int nmax, int batch, int32_t* acc_tokens,
                                  int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
@@ -329,23 +330,35 @@ __global__ void walk_init_kernel(const int32_t* __restrict__ tree_tokens, const 
   correction[b] = -1;
   int has_child = 0;
   for (int c = 1; c < n_nodes[b]; ++c) has_child |= parents[(int64_t)b * nmax + c] == 0;
-  state[b] = 0;              // parent
+  state[b] = 0;                  // parent
   state[batch + b] = has_child;  // active
+  state[2 * batch + b] = -1;     // last sampling step
+}
+
+// Lazy LM-head rows of a walk step: row b samples from hidden row b*nmax + parent[b].
+__global__ void walk_rows_kernel(const int32_t* __restrict__ state, int batch, int nmax, int32_t* row_index,
+                                 int32_t* row_active) {
+  int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  row_index[b] = b * nmax + state[b];
+  row_active[b] = state[batch + b];
 }
 
 template <int DT>
 __global__ void __launch_bounds__(kThreads) walk_step_kernel(
     const void* __restrict__ logits, int64_t row_stride, int vocab, const int32_t* __restrict__ slot_map,
     const int32_t* __restrict__ tree_tokens, const int32_t* __restrict__ parents, const int32_t* __restrict__ n_nodes,
-    int nmax, int batch, int walk_step, const uint32_t* __restrict__ noise, int noise_stride, int noise_col0,
-    uint64_t seed, uint64_t step, const int32_t* __restrict__ seq_ids, int draw0, SampleParams sp,
+    int nmax, int batch, int walk_step, int rows_by_batch, const uint32_t* __restrict__ noise, int noise_stride,
+    int noise_col0, uint64_t seed, uint64_t step, const int32_t* __restrict__ seq_ids, int draw0, SampleParams sp,
     int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
     int32_t* correction, int32_t* state, int32_t* err_flag) {
   __shared__ Shared sh;
   const int b = blockIdx.x;
   if (!state[batch + b]) return;
   const int parent = state[b];
-  const int64_t slot = slot_map ? (int64_t)slot_map[(int64_t)b * nmax + parent] : (int64_t)b * nmax + parent;
+  const int64_t slot = rows_by_batch ? (int64_t)b
+                       : slot_map    ? (int64_t)slot_map[(int64_t)b * nmax + parent]
+                                     : (int64_t)b * nmax + parent;
   if (slot < 0) {
     if (threadIdx.x == 0) {
       if (err_flag) atomicOr(err_flag, 2);
@@ -359,6 +372,7 @@ __global__ void __launch_bounds__(kThreads) walk_step_kernel(
                            (uint32_t)(draw0 + walk_step));
   int tok = block_sample<DT>(rowp, vocab, sp, u, sh);
   if (threadIdx.x == 0) {
+    state[2 * batch + b] = walk_step;
     const int nn = n_nodes[b];
     const int32_t* pb = parents + (int64_t)b * nmax;
     const int32_t* tb = tree_tokens + (int64_t)b * nmax;
@@ -473,16 +487,65 @@ int fg_accept_walk(const void* tree_logits, int dtype, int64_t row_stride, int v
   for (int t = 0; t < max_walk_steps; ++t) {
     if (dtype == fg::kBF16)
       hipLaunchKernelGGL(walk_step_kernel<fg::kBF16>, dim3(batch), dim3(kThreads), 0, s, tree_logits, row_stride,
-                         vocab, slot_map, tree_tokens, parents, n_nodes, nmax, batch, t, noise, noise_stride,
+                         vocab, slot_map, tree_tokens, parents, n_nodes, nmax, batch, t, 0, noise, noise_stride,
                          noise_col0, seed, step, seq_ids, draw0, sp, acc_tokens, acc_nodes, acc_stride, acc_len,
                          last_node, correction, workspace, err_flag);
     else
       hipLaunchKernelGGL(walk_step_kernel<fg::kF32>, dim3(batch), dim3(kThreads), 0, s, tree_logits, row_stride,
-                         vocab, slot_map, tree_tokens, parents, n_nodes, nmax, batch, t, noise, noise_stride,
+                         vocab, slot_map, tree_tokens, parents, n_nodes, nmax, batch, t, 0, noise, noise_stride,
                          noise_col0, seed, step, seq_ids, draw0, sp, acc_tokens, acc_nodes, acc_stride, acc_len,
                          last_node, correction, workspace, err_flag);
   }
   return fg::check_launch("fg_accept_walk");
+}
+
+int fg_walk_begin(const int32_t* tree_tokens, const int32_t* parents, const int32_t* n_nodes, int nmax, int batch,
+                  int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
+                  int32_t* correction, int32_t* state, void* stream) {
+  FG_REQUIRE(tree_tokens && parents && n_nodes && acc_tokens && acc_nodes && acc_len && last_node && correction &&
+                 state,
+             "fg_walk_begin: null pointer");
+  FG_REQUIRE(batch > 0 && nmax > 0 && nmax <= 64 && acc_stride >= 1, "fg_walk_begin: bad shape");
+  hipLaunchKernelGGL(walk_init_kernel, dim3((batch + 63) / 64), dim3(64), 0, (hipStream_t)stream, tree_tokens,
+                     parents, n_nodes, nmax, batch, acc_tokens, acc_nodes, acc_stride, acc_len, last_node, correction,
+                     state);
+  return fg::check_launch("fg_walk_begin");
+}
+
+int fg_walk_rows(const int32_t* state, int batch, int nmax, int32_t* row_index, int32_t* row_active, void* stream) {
+  FG_REQUIRE(state && row_index && row_active && batch > 0 && nmax > 0, "fg_walk_rows: bad arguments");
+  hipLaunchKernelGGL(walk_rows_kernel, dim3((batch + 63) / 64), dim3(64), 0, (hipStream_t)stream, state, batch, nmax,
+                     row_index, row_active);
+  return fg::check_launch("fg_walk_rows");
+}
+
+int fg_walk_step(const void* step_logits, int dtype, int64_t row_stride, int vocab, const int32_t* tree_tokens,
+                 const int32_t* parents, const int32_t* n_nodes, int nmax, int batch, int walk_step,
+                 const uint32_t* noise, int noise_stride, int noise_col0, uint64_t seed, uint64_t step,
+                 const int32_t* seq_ids, int draw0, float temperature, int greedy, int top_k, uint32_t top_p_fixed,
+                 int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
+                 int32_t* correction, int32_t* state, int32_t* err_flag, void* stream) {
+  FG_REQUIRE(step_logits && tree_tokens && parents && n_nodes && acc_tokens && acc_nodes && acc_len && last_node &&
+                 correction && state,
+             "fg_walk_step: null pointer");
+  FG_REQUIRE(batch > 0 && nmax > 0 && nmax <= 64 && vocab > 0 && vocab < (1 << 23) && walk_step >= 0,
+             "fg_walk_step: bad shape");
+  FG_REQUIRE(dtype == fg::kF32 || dtype == fg::kBF16, "fg_walk_step: dtype");
+  FG_REQUIRE(row_stride >= vocab && row_stride % 8 == 0 && ((uintptr_t)step_logits & 31) == 0,
+             "fg_walk_step: rows must be 32-byte aligned (row_stride % 8 == 0)");
+  SampleParams sp = make_params(temperature, greedy, top_k, vocab, top_p_fixed);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == fg::kBF16)
+    hipLaunchKernelGGL(walk_step_kernel<fg::kBF16>, dim3(batch), dim3(kThreads), 0, s, step_logits, row_stride, vocab,
+                       nullptr, tree_tokens, parents, n_nodes, nmax, batch, walk_step, 1, noise, noise_stride,
+                       noise_col0, seed, step, seq_ids, draw0, sp, acc_tokens, acc_nodes, acc_stride, acc_len,
+                       last_node, correction, state, err_flag);
+  else
+    hipLaunchKernelGGL(walk_step_kernel<fg::kF32>, dim3(batch), dim3(kThreads), 0, s, step_logits, row_stride, vocab,
+                       nullptr, tree_tokens, parents, n_nodes, nmax, batch, walk_step, 1, noise, noise_stride,
+                       noise_col0, seed, step, seq_ids, draw0, sp, acc_tokens, acc_nodes, acc_stride, acc_len,
+                       last_node, correction, state, err_flag);
+  return fg::check_launch("fg_walk_step");
 }
 
 int fg_accept_finalize(const int32_t* acc_tokens, const int32_t* acc_nodes, int acc_stride, int32_t* acc_len,

@@ -26,7 +26,7 @@ SIGNATURES = {
     "fg_version": (_I, []),
     "fg_medusa_heads_workspace": (_SZ, [_I, _I, _I, _I]),
     "fg_medusa_heads": (_I, [_P, _I, _I, _I, _I64, _I, _P, _P, _F, _P, _P, _P, _I, _P, _SZ, _P]),
-    "fg_lm_head": (_I, [_P, _I, _I, _I, _I64, _P, _P, _I64, _I, _P, _I, _I64, _P]),
+    "fg_lm_head": (_I, [_P, _I, _I, _I, _I64, _P, _P, _P, _I64, _I, _P, _I, _I64, _P]),
     "fg_medusa_topk_workspace": (_SZ, [_I, _I, _I]),
     "fg_medusa_topk": (_I, [_P, _I, _I64, _I, _I, _I, _P, _P, _P, _P, _SZ, _P]),
     "fg_tree_layout": (_I, [_P, _P, _I, _I, _P, _P, _P, _I, _P, _P, _I, _P]),
@@ -39,6 +39,10 @@ SIGNATURES = {
                               _P]),
     "fg_accept_walk": (_I, [_P, _I, _I64, _I, _P, _P, _P, _P, _I, _I, _I, _P, _I, _I, _U64, _U64, _P, _I, _F, _I, _I,
                             _U32, _P, _P, _I, _P, _P, _P, _P, _P, _P]),
+    "fg_walk_begin": (_I, [_P, _P, _P, _I, _I, _P, _P, _I, _P, _P, _P, _P, _P]),
+    "fg_walk_rows": (_I, [_P, _I, _I, _P, _P, _P]),
+    "fg_walk_step": (_I, [_P, _I, _I64, _I, _P, _P, _P, _I, _I, _I, _P, _I, _I, _U64, _U64, _P, _I, _F, _I, _I, _U32,
+                          _P, _P, _I, _P, _P, _P, _P, _P, _P]),
     "fg_accept_finalize": (_I, [_P, _P, _I, _P, _P, _P, _P, _I, _I, _P, _P, _I, _P]),
     "fg_kv_path_gather": (_I, [_P, _I, _I, _I, _I, _I, _I64, _I64, _I64, _I, _P, _P, _P, _I, _P, _I, _P, _P]),
 }

@@ -9,12 +9,15 @@ included). One verify round, per active sequence:
   plan / tree          plan_tree (host), adaptive refit from per-head confidence
                        quantiles, cached TreeTopology, fg_tree_layout
   tree verify          TargetModel.forward (tree attention with ancestor bit masks)
-  packed LM head       fg_lm_head over internal nodes only
-  acceptance           fg_accept_walk (draws 1..D) + fg_accept_finalize (clamp, EOS)
+  acceptance           lazy (default): per walk step t, fg_walk_rows -> fg_lm_head over
+                       the node each row samples from -> fg_walk_step (draw 1+t);
+                       packed: fg_lm_head over internal nodes + fg_accept_walk;
+                       then fg_accept_finalize (clamp, EOS)
   cache update         fg_kv_path_gather (extract_path) or a chain re-forward
                        (recompute_accepted)
-  next state           hidden at the last accepted node; its packed logits row,
-                       or a fresh LM-head row when it is a leaf
+  next state           hidden at the last accepted node; its logits row from the
+                       walk (lazy) or the packed projection, or a fresh LM-head row
+                       when it is a leaf
 
 There is one device-to-host copy per round (accepted tokens, lengths, flags),
 plus one for the adaptive-plan confidences when that mode is on. Draws use
@@ -77,6 +80,11 @@ class FlashMedusaConfig:
     # build additions
     emit_correction_token: bool = False  # flashgrpo_b200 acceptance semantics
     noise_seed: int | None = None        # None: drawn from torch's default generator per generate()
+    # Project tree LM-head rows lazily, one walk step at a time, for the node each
+    # row's walk samples from (at most batch rows per step). Draws, accepted paths
+    # and next-round logits are identical to the packed projection; only nodes the
+    # walk never reaches are skipped.
+    lazy_walk_lm_head: bool = True
 
 
 def _quantile(values: np.ndarray, q: float) -> float:
@@ -285,8 +293,10 @@ class FlashMedusaDecoder:
             tree_tokens, _ = K.tree_layout(cand, score, Bc, roots, dshared["depth"], dshared["rank"], N)
         else:
             tree_tokens = roots.view(Bc, 1)
-        # ---------------- verify forward + packed LM head
-        tree_logits = slot_map = hidden_t = None
+        # ---------------- verify forward + tree LM head
+        tree_logits = slot_map = hidden_t = walk_logits = walk = None
+        lazy = bool(cfg.lazy_walk_lm_head) and N > 1
+        D = topo.max_depth
         if int(r.seq_h.max()) + N > r.cache.capacity:
             raise RuntimeError("KV cache capacity exceeded")  # unreachable: rows finish at max_length
         r.sync()
@@ -296,27 +306,41 @@ class FlashMedusaDecoder:
                                      seq_len=r.seq, row_map=r.row_map, err_flag=r.err)
             if N > 1:
                 m["tree_query_rows"] += Bc * N
-                with timing.label("tree"):
-                    if cfg.project_internal_tree_logits_only:
-                        tree_logits = model.logits(hidden_t, row_index=dmap["internal_rows"])
-                        slot_map = dmap["slot_map"]
-                    else:
-                        tree_logits = model.logits(hidden_t)
-                m["tree_lm_head_rows"] += tree_logits.shape[0]
+                if lazy:
+                    walk_logits = torch.empty((D, Bc, model.cfg.vocab), dtype=model.dtype, device=dev)
+                else:
+                    with timing.label("tree"):
+                        if cfg.project_internal_tree_logits_only:
+                            tree_logits = model.logits(hidden_t, row_index=dmap["internal_rows"])
+                            slot_map = dmap["slot_map"]
+                        else:
+                            tree_logits = model.logits(hidden_t)
+                    m["tree_lm_head_rows"] += tree_logits.shape[0]
         except RuntimeError as exc:
             if "out of memory" not in str(exc).lower():
                 raise
             m["oom"] += 1
             torch.cuda.empty_cache()
-            hidden_t = tree_logits = None
+            hidden_t = tree_logits = walk_logits = None
         r.sync()
         m["verify_time"] += time.time() - t0
         # ---------------- acceptance
-        if tree_logits is not None:
-            walk = K.accept_walk(tree_logits, tree_tokens, dmap["parents"], dmap["n_nodes"],
-                                 max_walk_steps=topo.max_depth, slot_map=slot_map, seed=r.seed, step=rnd,
-                                 seq_ids=r.row_map, draw0=1, temperature=cfg.temperature, greedy=greedy,
-                                 top_k=cfg.top_k, top_p=cfg.top_p, err_flag=r.err)
+        walk_kw = dict(seed=r.seed, step=rnd, seq_ids=r.row_map, draw0=1, temperature=cfg.temperature, greedy=greedy,
+                       top_k=cfg.top_k, top_p=cfg.top_p, err_flag=r.err)
+        if walk_logits is not None:
+            # Walk step t samples row b from the node its walk stands on; only those
+            # rows are projected (inactive rows' tiles are skipped).
+            walk = K.walk_begin(tree_tokens, dmap["parents"], dmap["n_nodes"], acc_stride=D + 1)
+            for t in range(D):
+                K.walk_rows(walk, N)
+                with timing.label("tree"):
+                    model.logits(hidden_t, row_index=walk["row_index"], row_active=walk["row_active"],
+                                 out=walk_logits[t])
+                K.walk_step(walk, walk_logits[t], tree_tokens, dmap["parents"], dmap["n_nodes"], walk_step=t,
+                            **walk_kw)
+        elif tree_logits is not None:
+            walk = K.accept_walk(tree_logits, tree_tokens, dmap["parents"], dmap["n_nodes"], max_walk_steps=D,
+                                 slot_map=slot_map, **walk_kw)
         else:
             zeros = torch.zeros(Bc, dtype=torch.int32, device=dev)
             walk = dict(acc_tokens=roots.view(Bc, 1).clone(), acc_nodes=zeros.view(Bc, 1).clone(),
@@ -329,6 +353,8 @@ class FlashMedusaDecoder:
         W = walk["acc_tokens"].shape[1]
         cols = [walk["acc_tokens"], walk["acc_len"].view(-1, 1), finished_d.view(-1, 1),
                 walk["last_node"].view(-1, 1), r.err.expand(Bc).view(-1, 1)]
+        if walk_logits is not None:
+            cols += [walk["state"][2 * Bc:].view(-1, 1), walk["acc_nodes"]]
         if b200:
             cols.append(new_pending.view(-1, 1))
         pack = torch.cat(cols, dim=1).cpu().numpy()
@@ -336,8 +362,14 @@ class FlashMedusaDecoder:
         fin_h, last_h = pack[:, W + 1].astype(bool), pack[:, W + 2]
         if int(pack[0, W + 3]):
             raise RuntimeError(f"flashgrpo_amd kernel reported an index error (flag {int(pack[0, W + 3])})")
+        col = W + 4
+        walk_last_h = acc_nodes_h = None
+        if walk_logits is not None:
+            walk_last_h, acc_nodes_h = pack[:, col], pack[:, col + 1:col + 1 + W]
+            col += 1 + W
+            m["tree_lm_head_rows"] += int(np.sum(walk_last_h + 1))
         if b200:
-            m["corrections"] += int(np.count_nonzero(pack[:, W + 4] >= 0))
+            m["corrections"] += int(np.count_nonzero(pack[:, col] >= 0))
         if trace is not None:
             rec = dict(round=rnd, active=list(r.active), plan=list(plan.topk_by_depth),
                        budget=plan.node_budget_per_seq, seq_len=r.seq.cpu().numpy().copy(),
@@ -350,30 +382,42 @@ class FlashMedusaDecoder:
             if tree_logits is not None:
                 rec["tree_logits"] = tree_logits.float().cpu().numpy()
                 rec["slot_map"] = None if slot_map is None else slot_map.cpu().numpy()
+            if walk_logits is not None:
+                # rows[t, b] is valid for t <= walk_last[b]; it is the node acc_nodes[b, t]
+                rec["walk_logits"] = walk_logits.float().cpu().numpy()
+                rec["walk_last"] = walk_last_h.copy()
+                rec["acc_nodes"] = acc_nodes_h.copy()
+            if hidden_t is not None and N > 1:
                 rec["tree_hidden"] = hidden_t.float().cpu().numpy()
             if b200:
-                rec["pending"] = pack[:, W + 4].copy()
+                rec["pending"] = pack[:, col].copy()
             trace.append(rec)
         # ---------------- cache update + next state
         extracted = False
-        if cfg.cache_update_mode == "extract_path" and tree_logits is not None:
+        if cfg.cache_update_mode == "extract_path" and (tree_logits is not None or walk_logits is not None):
             r.sync()
             t0 = time.time()
             r.cache.gather_path(r.seq, walk["acc_nodes"], walk["acc_len"], N, row_map=r.row_map, err_flag=r.err)
             ar = torch.arange(Bc, device=dev)
             last = walk["last_node"].long()
             r.hidden = hidden_t[ar, last].contiguous()
-            if slot_map is not None:
-                slots = slot_map[ar, last]
-                r.logits = tree_logits.index_select(0, slots.clamp_min(0).long())
+            if walk_logits is None and slot_map is None:
+                r.logits = tree_logits.index_select(0, ar * N + last)
+            else:
+                if walk_logits is not None:
+                    # the last accepted node at position acc_len-1 was sampled from at that
+                    # walk step unless it is a leaf (then it has no projected row)
+                    tpos = (walk["acc_len"].long() - 1).clamp(0, D - 1)
+                    r.logits = walk_logits[tpos, ar]
+                else:
+                    slots = slot_map[ar, last]
+                    r.logits = tree_logits.index_select(0, slots.clamp_min(0).long())
                 leaf = np.nonzero(np.array([topo.slot_of[int(n)] < 0 for n in last_h]))[0]
                 if leaf.size:
                     li = torch.from_numpy(leaf).to(dev)
                     with timing.label("leaf"):
                         r.logits.index_copy_(0, li, model.logits(r.hidden.index_select(0, li)))
                     m["tree_lm_head_rows"] += int(leaf.size)
-            else:
-                r.logits = tree_logits.index_select(0, ar * N + last)
             r.sync()
             dt_ = time.time() - t0
             m["extract_time"] += dt_
@@ -409,10 +453,15 @@ class FlashMedusaDecoder:
                 m["recompute_time"] += dt_
         r.seq = r.seq + walk["acc_len"]
         r.seq_h = r.seq_h + acc_len_h
+        if walk_last_h is not None:
+            draws = walk_last_h.astype(np.int64) + 1
+        elif N > 1:
+            draws = np.array([int(a) - (1 if topo.slot_of[int(n)] < 0 else 0) for a, n in zip(acc_len_h, last_h)])
+        else:
+            draws = np.zeros(Bc, dtype=np.int64)
         r.last_round = dict(num_nodes=N, internal=len(topo.internal), acc_len=acc_len_h.copy(),
-                            last_node=last_h.copy(), walk_draws=np.array(
-                                [int(a) - (1 if topo.slot_of[int(n)] < 0 else 0) for a, n in zip(acc_len_h, last_h)])
-                            if N > 1 else np.zeros(Bc, dtype=np.int64), heads=plan.active_heads, batch=Bc)
+                            last_node=last_h.copy(), walk_draws=draws, heads=plan.active_heads, batch=Bc,
+                            lazy=walk_last_h is not None, walk_steps=D if walk_last_h is not None else 0)
         if b200:
             r.pending = new_pending
         # ---------------- bookkeeping

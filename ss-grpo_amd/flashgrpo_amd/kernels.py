@@ -91,10 +91,13 @@ def medusa_heads(hidden, ln_w, ln_b, fc_w, fc_b, *, eps=1e-5, out=None, out_dtyp
     return out
 
 
-def lm_head(x, weight, *, row_index=None, out=None, out_dtype=None):
-    """out[m] = x[row_index[m] if row_index is given else m] @ weight.T"""
-    _dev(x, weight, row_index)
+def lm_head(x, weight, *, row_index=None, row_active=None, out=None, out_dtype=None):
+    """out[m] = x[row_index[m] if row_index is given else m] @ weight.T
+
+    row_active (int32 [M], optional): output tiles whose rows are all 0 are skipped."""
+    _dev(x, weight, row_index, row_active)
     _i32(row_index, "row_index")
+    _i32(row_active, "row_active")
     K = x.shape[-1]
     x2 = x.reshape(-1, K)
     if x2.stride(1) != 1 or weight.stride(1) != 1 or weight.shape[1] != K:
@@ -108,8 +111,8 @@ def lm_head(x, weight, *, row_index=None, out=None, out_dtype=None):
         out = torch.empty(M, N, dtype=od, device=x.device)
     if M == 0:
         return out
-    _call("fg_lm_head", _ptr(x2), dtype_code(x), M, K, x2.stride(0), _ptr(row_index), _ptr(weight),
-              weight.stride(0), N, _ptr(out), dtype_code(out), out.stride(0), _stream())
+    _call("fg_lm_head", _ptr(x2), dtype_code(x), M, K, x2.stride(0), _ptr(row_index), _ptr(row_active),
+          _ptr(weight), weight.stride(0), N, _ptr(out), dtype_code(out), out.stride(0), _stream())
     return out
 
 
@@ -245,7 +248,7 @@ def accept_walk(tree_logits, tree_tokens, parents, n_nodes, *, max_walk_steps, s
                    acc_len=torch.empty(B, dtype=torch.int32, device=dev),
                    last_node=torch.empty(B, dtype=torch.int32, device=dev),
                    correction=torch.empty(B, dtype=torch.int32, device=dev),
-                   state=torch.empty(2 * B, dtype=torch.int32, device=dev))
+                   state=torch.empty(3 * B, dtype=torch.int32, device=dev))
     T = 0.0 if temperature is None else float(temperature)
     use_T = T if T > 0 else (-1.0 if T < 0 or temperature is None else 0.0)
     g = bool(greedy) or (temperature is not None and T == 0.0)
@@ -257,6 +260,49 @@ def accept_walk(tree_logits, tree_tokens, parents, n_nodes, *, max_walk_steps, s
               _ptr(out["acc_nodes"]), acc_stride, _ptr(out["acc_len"]), _ptr(out["last_node"]),
               _ptr(out["correction"]), _ptr(out["state"]), _ptr(err_flag), _stream())
     return out
+
+
+def walk_begin(tree_tokens, parents, n_nodes, *, acc_stride):
+    """Initialise a step-at-a-time walk; returns the walk dict (outputs + state)."""
+    _dev(tree_tokens, parents, n_nodes)
+    B, nmax = tree_tokens.shape
+    dev = tree_tokens.device
+    w = dict(acc_tokens=torch.zeros(B, acc_stride, dtype=torch.int32, device=dev),
+             acc_nodes=torch.zeros(B, acc_stride, dtype=torch.int32, device=dev),
+             acc_len=torch.empty(B, dtype=torch.int32, device=dev),
+             last_node=torch.empty(B, dtype=torch.int32, device=dev),
+             correction=torch.empty(B, dtype=torch.int32, device=dev),
+             state=torch.empty(3 * B, dtype=torch.int32, device=dev),
+             row_index=torch.empty(B, dtype=torch.int32, device=dev),
+             row_active=torch.empty(B, dtype=torch.int32, device=dev))
+    _call("fg_walk_begin", _ptr(tree_tokens), _ptr(parents), _ptr(n_nodes), nmax, B, _ptr(w["acc_tokens"]),
+          _ptr(w["acc_nodes"]), acc_stride, _ptr(w["acc_len"]), _ptr(w["last_node"]), _ptr(w["correction"]),
+          _ptr(w["state"]), _stream())
+    return w
+
+
+def walk_rows(walk, nmax):
+    """Fill walk['row_index'] (b*nmax + parent) and walk['row_active'] for the next step."""
+    B = walk["acc_len"].numel()
+    _call("fg_walk_rows", _ptr(walk["state"]), B, nmax, _ptr(walk["row_index"]), _ptr(walk["row_active"]), _stream())
+
+
+def walk_step(walk, step_logits, tree_tokens, parents, n_nodes, *, walk_step, noise=None, noise_col0=0, seed=0,
+              step=0, seq_ids=None, draw0=1, temperature=1.0, greedy=False, top_k=None, top_p=1.0, err_flag=None):
+    """One walk step: active row b draws from row b of step_logits."""
+    _dev(step_logits, tree_tokens, parents, n_nodes, noise, seq_ids)
+    B, nmax = tree_tokens.shape
+    lg = aligned_rows(step_logits)
+    V = lg.shape[-1]
+    T = 0.0 if temperature is None else float(temperature)
+    use_T = T if T > 0 else (-1.0 if T < 0 or temperature is None else 0.0)
+    g = bool(greedy) or (temperature is not None and T == 0.0)
+    _call("fg_walk_step", _ptr(lg), dtype_code(lg), lg.stride(0), V, _ptr(tree_tokens), _ptr(parents), _ptr(n_nodes),
+          nmax, B, int(walk_step), _ptr(noise), noise.stride(0) if noise is not None else 0, int(noise_col0),
+          int(seed) & (2 ** 64 - 1), int(step), _ptr(seq_ids), int(draw0), use_T, int(g), int(top_k or 0),
+          top_p_fixed(top_p), _ptr(walk["acc_tokens"]), _ptr(walk["acc_nodes"]), walk["acc_tokens"].stride(0),
+          _ptr(walk["acc_len"]), _ptr(walk["last_node"]), _ptr(walk["correction"]), _ptr(walk["state"]),
+          _ptr(err_flag), _stream())
 
 
 def accept_finalize(walk, old_len, *, max_length, eos_token_id, finished=None, pending_root=None):

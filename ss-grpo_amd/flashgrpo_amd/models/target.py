@@ -300,9 +300,12 @@ class TargetModel:
         K.rmsnorm(x, self.w["final_norm"], cfg.rms_eps, delta=delta, out=out)
         return out.view(B, N, H)
 
-    def logits(self, hidden: torch.Tensor, *, row_index=None, out_dtype=None) -> torch.Tensor:
+    def logits(self, hidden: torch.Tensor, *, row_index=None, row_active=None, out=None,
+               out_dtype=None) -> torch.Tensor:
+        """LM-head rows: hidden rows (optionally gathered by row_index); rows with
+        row_active == 0 may be left unwritten."""
         return K.lm_head(hidden.reshape(-1, self.cfg.hidden), self.w["lm_head"], row_index=row_index,
-                         out_dtype=out_dtype)
+                         row_active=row_active, out=out, out_dtype=out_dtype)
 
     def prefill(self, input_ids: torch.Tensor, cache: KVCache, *, lengths=None, chunk: int = MAX_TREE_NODES,
                 row_map: torch.Tensor | None = None) -> torch.Tensor:

@@ -134,11 +134,25 @@ def lockstep(trace, ocfg, Wr, heads_r, spec, prompts, dtype, seed, max_length, e
         trees = OT.build_batch_trees(rec["roots"], heads_logits, plan)
         assert rec["tree_tokens"].tolist() == [t.tokens for t in trees], rnd
         N = trees[0].node_count
-        if "tree_logits" in rec:
+        if "tree_hidden" in rec:
             for i, s in enumerate(active):
                 want_h = rows[s].tree(trees[i].tokens, trees[i].parents, trees[i].depths)
                 assert rel(rec["tree_hidden"][i], want_h) < tol, (rnd, s)
             nz = [[OS.counter_noise(seed, rnd, s, 1 + t) for t in range(N)] for s in active]
+        if "walk_logits" in rec:  # lazy: one projected row per walk step and sequence
+            slots = None
+            want_all = OM.logits(rec["tree_hidden"].reshape(Bc * N, -1), Wr["lm_head"]).reshape(Bc, N, -1)
+            walk_logits = want_all.copy()
+            for i in range(Bc):
+                for t in range(int(rec["walk_last"][i]) + 1):
+                    node = int(rec["acc_nodes"][i, t])
+                    assert rel(rec["walk_logits"][t, i], want_all[i, node]) < tol, (rnd, i, t)
+                    walk_logits[i, node] = rec["walk_logits"][t, i]
+            at, an, last, corr = OS.accept_walk(trees, walk_logits, nz, slots=slots, emit_correction=True, **kw)
+            for i in range(Bc):  # draws made: one per step until a mismatch or a leaf
+                assert int(rec["walk_last"][i]) + 1 == len(at[i]) - (corr[i] is None), (rnd, i)
+                assert rec["acc_nodes"][i, :len(an[i])].tolist() == an[i], (rnd, i)
+        elif "tree_logits" in rec:
             if rec["slot_map"] is not None:  # packed internal-node rows
                 r_, n_, slots = OT.internal_slots(trees)
                 want_tl = OM.logits(rec["tree_hidden"][r_, n_], Wr["lm_head"])
@@ -173,7 +187,7 @@ def lockstep(trace, ocfg, Wr, heads_r, spec, prompts, dtype, seed, max_length, e
 
 
 def _run(ocfg, spec, *, dtype, B0, repeats, P, max_length, seed=123, wseed=0, cache_mode="extract_path",
-         internal_only=True):
+         internal_only=True, lazy=True):
     from flashgrpo_amd.decoding import FlashMedusaConfig, FlashMedusaDecoder
 
     W = OM.random_weights(ocfg, seed=wseed, std=0.05)
@@ -185,7 +199,8 @@ def _run(ocfg, spec, *, dtype, B0, repeats, P, max_length, seed=123, wseed=0, ca
                             adaptive_tree_enabled=spec.adaptive_tree_enabled, do_sample=spec.do_sample,
                             temperature=spec.temperature, top_p=spec.top_p, top_k=spec.top_k,
                             emit_correction_token=spec.emit_correction_token, noise_seed=seed,
-                            cache_update_mode=cache_mode, project_internal_tree_logits_only=internal_only)
+                            cache_update_mode=cache_mode, project_internal_tree_logits_only=internal_only,
+                            lazy_walk_lm_head=lazy)
     dec = FlashMedusaDecoder(model, mh, Tok(spec.eos_token_id), cfg)
     rng = np.random.default_rng(wseed + 7)
     prompts = rng.integers(0, ocfg.vocab, (B0, P))
@@ -205,11 +220,11 @@ SMALL = OM.ModelConfig(num_layers=2, hidden=256, q_heads=4, kv_heads=2, head_dim
 SMALL16 = OM.ModelConfig(num_layers=2, hidden=256, q_heads=4, kv_heads=2, head_dim=128, intermediate=512, vocab=64)
 
 
-@pytest.mark.parametrize("top_p", [1.0, 0.9])
-def test_lockstep_fp32_fixed_tree_small_vocab(top_p):
+@pytest.mark.parametrize("top_p,lazy", [(1.0, True), (0.9, True), (0.9, False)])
+def test_lockstep_fp32_fixed_tree_small_vocab(top_p, lazy):
     spec = OD.DecodeSpec(tree_mode="fixed", max_tree_nodes_per_seq=16, fixed_tree_topk_by_depth=(4, 2, 1),
                          num_medusa_heads=3, max_tree_depth=4, top_p=top_p)
-    out, st = _run(SMALL, spec, dtype=torch.float32, B0=3, repeats=2, P=33, max_length=33 + 24)
+    out, st = _run(SMALL, spec, dtype=torch.float32, B0=3, repeats=2, P=33, max_length=33 + 24, lazy=lazy)
     assert st["max_acc"] >= 2  # a 64-token vocabulary accepts children: the gather moves real paths
     assert out["kv_extraction_success_count"] == st["rounds"]
 
@@ -230,7 +245,9 @@ def test_lockstep_adaptive_b200_greedy_and_recompute():
     spec_g = OD.DecodeSpec(tree_mode="fixed", max_tree_nodes_per_seq=12, fixed_tree_topk_by_depth=(3, 2),
                            num_medusa_heads=2, do_sample=False)
     _run(SMALL, spec_g, dtype=torch.float32, B0=2, repeats=2, P=17, max_length=17 + 12, cache_mode="recompute_accepted")
-    _run(SMALL, spec_g, dtype=torch.float32, B0=2, repeats=2, P=17, max_length=17 + 12, internal_only=False)
+    _run(SMALL, spec_g, dtype=torch.float32, B0=2, repeats=2, P=17, max_length=17 + 12, internal_only=False,
+         lazy=False)
+    _run(SMALL, spec, dtype=torch.float32, B0=2, repeats=1, P=20, max_length=20 + 16, lazy=False)
 
 
 def test_tiny_config_32_rounds_fp32():
