@@ -3,7 +3,7 @@
 
 A step is one verify round of FlashMedusaDecoder over every active sequence:
 root draw, Medusa heads + tied LM head, top-k tree, tree-attention verify
-forward, packed internal-node LM head, exact_target walk and accepted-path KV
+forward, lazy walk LM head + exact_target walk and accepted-path KV
 compaction. Default workload: the Qwen2.5-7B shape (28 layers, hidden 3584,
 28/4 heads, MLP 18944, vocab 152064, bf16), 64 sequences (8 prompts x 8 GRPO
 repeats) with a 2048-token uniform-random prefix, 4 tied Medusa heads, adaptive
@@ -14,6 +14,11 @@ Prints one JSON line: rollout tok/s (emitted tokens over the timed verify
 rounds), per-step latency, the roofline of the dominant hand-written kernel
 (HIP events on the launch stream) and the CPU oracle baseline on a bounded
 sample of the same workload.
+
+The timed rounds are bracketed by two short spin kernels (outside the timed
+region) so a rocprofv3 kernel trace of this command can be cut to exactly those
+rounds: `python bench.py --summarize-trace <run>_kernel_trace.csv` prints the
+per-kernel table of the dispatches between the markers.
 """
 from __future__ import annotations
 
@@ -89,9 +94,11 @@ def algorithmic_work(cfg, rnd, seq_before, elem):
         "fg_kv_path_gather": dict(bytes=2 * L * 2 * Hkv * int(rnd["acc_len"].sum()) * d * elem, launches=1),
     }
     if rnd.get("lazy"):
-        # one launch per walk step, each streams the whole LM-head weight once for its active rows
+        # one launch per walk step; a step with an active row streams the whole LM-head
+        # weight once, a step with none skips every tile
         D = rnd["walk_steps"]
-        w["fg_lm_head:tree"] = dict(flops=2 * draws * H * V, bytes=D * H * V * elem + draws * (H + V) * elem,
+        busy = int(rnd["walk_draws"].max()) if draws else 0
+        w["fg_lm_head:tree"] = dict(flops=2 * draws * H * V, bytes=busy * H * V * elem + draws * (H + V) * elem,
                                     launches=D)
         w["fg_walk_step"] = dict(bytes=draws * V * elem, launches=D)
     else:
@@ -174,6 +181,37 @@ def cpu_baseline(model, heads, r, work, seed, layers=2):
             "seconds": round(t_est, 3)}
 
 
+def summarize_trace(path, top=30):
+    """Per-kernel table of a rocprofv3 kernel-trace CSV, restricted to the dispatches
+    between the last two spin-kernel markers that bracket the timed rounds."""
+    import csv
+
+    with open(path, newline="") as fh:
+        rows = sorted(csv.DictReader(fh), key=lambda r: int(r["Start_Timestamp"]))
+    marks = [i for i, r in enumerate(rows) if "spin_kernel" in r["Kernel_Name"]]
+    if len(marks) < 2:
+        raise SystemExit(f"{path}: no pair of spin_kernel markers around the timed rounds")
+    sel = rows[marks[-2] + 1:marks[-1]]
+    agg = {}
+    for r in sel:
+        name = r["Kernel_Name"]
+        dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        a = agg.setdefault(name, [0, 0.0, float("inf"), 0.0])
+        a[0] += 1
+        a[1] += dur
+        a[2] = min(a[2], dur)
+        a[3] = max(a[3], dur)
+    total = sum(a[1] for a in agg.values())
+    span = (int(sel[-1]["End_Timestamp"]) - int(sel[0]["Start_Timestamp"])) / 1e3
+    print(f"dispatches between the markers: {len(sel)}; kernel time {total / 1e3:.3f} ms; "
+          f"first start to last end {span / 1e3:.3f} ms")
+    print("| total ms | % | calls | avg us | min us | max us | kernel |")
+    print("|---:|---:|---:|---:|---:|---:|---|")
+    for name, (c, t, lo, hi) in sorted(agg.items(), key=lambda kv: -kv[1][1])[:top]:
+        short = name if len(name) <= 100 else name[:97] + "..."
+        print(f"| {t / 1e3:.3f} | {100 * t / total:.1f} | {c} | {t / c:.1f} | {lo:.1f} | {hi:.1f} | `{short}` |")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -184,7 +222,11 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=2)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--summarize-trace", metavar="CSV", help="summarise a rocprofv3 kernel trace of this command")
     args = ap.parse_args()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (sequences shard by data "
               "parallelism with no exchange inside the verify step; run one process per GPU)", file=sys.stderr)
@@ -219,6 +261,7 @@ def main():
     timer = timing.KernelTimer()
     rounds, seqs = [], []
     tokens = 0
+    torch.cuda._sleep(1000)  # trace marker: the timed rounds start after this kernel
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     with timing.active(timer):
@@ -228,6 +271,8 @@ def main():
             rounds.append(r.last_round)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    torch.cuda._sleep(1000)  # trace marker: end of the timed rounds
+    torch.cuda.synchronize()
     kstats = timer.summary()
     log(f"timed {args.steps} steps in {elapsed:.3f} s")
 
