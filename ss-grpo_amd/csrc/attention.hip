@@ -7,15 +7,25 @@
 // is built (replaces flashgrpo/decoding/tree_attention.py:6-67 feeding the HF
 // decoder's eager/SDPA attention, flashgrpo/models/qwen_flashgrpo_wrapper.py:172-180).
 //
-// bf16 path, one workgroup per (sequence, kv head, 256-row query tile):
+// bf16 path, one workgroup of 8 waves per (sequence, kv head, 256-row query tile):
 //  * the query tile is the G*N rows (n-major, G = q heads per kv head) of one
 //    KV head, so every K/V tile loaded from HBM serves all of them;
-//  * 8 waves, 32 query rows each; S^T = K Q^T with v_mfma_f32_32x32x16_bf16
-//    (keys on the M side) puts one query per lane, so the online-softmax row
-//    max / sum are per-lane values plus one exchange with lane^32;
-//  * O^T += V^T P^T: P^T is fed straight from the S^T accumulators (bf16) as
-//    the B operand, V is transposed into LDS while staging so the A operand
-//    reads two 8-byte runs per lane in the same key order as P^T.
+//  * each wave owns 32 query rows; two waves share a SIMD, so one wave's MFMAs
+//    overlap the other's softmax arithmetic; a wave whose rows are all past the
+//    tile only stages K/V;
+//  * S^T = K Q^T (keys on the M side) puts one query per lane: the online
+//    softmax row max / sum are per-lane values plus one exchange with lane^32;
+//  * O^T += V^T P^T: P^T is fed straight from the S^T accumulators (bf16) as the
+//    B operand; V is transposed into LDS while staging (2 keys x 8 dims per
+//    thread) so the A operand reads two 8-byte runs per lane in the key order
+//    of the accumulators; 4-key groups of V^T row d are stored XOR-swizzled by
+//    (d >> 3) & 15, which keeps the staging writes and the fragment reads free
+//    of bank conflicts;
+//  * K/V tiles are double-buffered in LDS and the next tile's global loads are
+//    in flight during the current tile's MFMAs: one barrier per 64-key tile;
+//  * the ancestor mask is evaluated only on tiles that reach the tree keys, and
+//    the running max (and the O rescale) only moves when a lane's max grows by
+//    more than 2^8, so after the first keys the rescale is almost never taken.
 // fp32 path: one wave per query row, exact online softmax in fp32.
 #include "fg_common.h"
 
@@ -40,19 +50,32 @@ struct AttnArgs {
   float scale;
 };
 
-constexpr int kD = 128;       // head dim of the MFMA path
-constexpr int kKT = 64;       // keys per tile
-constexpr int kWavesA = 8;
-constexpr int kRowsTile = kWavesA * 32;
+constexpr int kD = 128;            // head dim of the MFMA path
+constexpr int kKT = 64;            // keys per tile
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+constexpr int kRowsTile = kWaves * 32;
 constexpr int kKPitch = kD + 8;    // bf16 elements per K row in LDS
 constexpr int kVPitch = kKT + 8;   // bf16 elements per V^T row in LDS
-constexpr float kNegBig = -1.0e30f;
+constexpr float kRescaleSlack = 8.0f;  // log2 units
+static_assert(kKT * kD / 8 == 2 * kThreads, "staging: two 16-byte K and V chunks per thread");
 
 FG_DEVICE int c_row32(int i, int lane) { return (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3); }
 
-__global__ void __launch_bounds__(kWavesA * 64) tree_attn_bf16_kernel(AttnArgs a, int m_tiles) {
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kKT * kKPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[kD * kVPitch];
+FG_DEVICE uint32_t u4_word(const uint4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+
+// Keys key0 .. key0+63 of one row: key0 + j is allowed when it is a prefix key
+// (j < sh, sh = seq_len - key0) or tree node j - sh with its bit set in tree_bits.
+// Shift amounts are kept in [0, 63].
+FG_DEVICE uint64_t tile_allowed_mask(int sh, uint64_t tree_bits) {
+  const uint64_t prefix = sh <= 0 ? 0ull : sh >= 64 ? ~0ull : ((1ull << sh) - 1ull);
+  const uint64_t tree = sh >= 64 ? 0ull : sh >= 0 ? (tree_bits << sh) : sh <= -64 ? 0ull : (tree_bits >> -sh);
+  return prefix | tree;
+}
+
+__global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, int m_tiles) {
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kKT * kKPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][kD * kVPitch];
 
   const int mt = blockIdx.x % m_tiles;
   const int hkv = (blockIdx.x / m_tiles) % a.Hkv;
@@ -62,16 +85,20 @@ __global__ void __launch_bounds__(kWavesA * 64) tree_attn_bf16_kernel(AttnArgs a
   const int M = G * a.N;
   const int s0 = a.seq_len[b];
   const int total = s0 + a.N;
+  const int last_key = min(total, a.capacity) - 1;
   const int cb = a.row_map ? a.row_map[b] : b;
   const uint16_t* kbase = (const uint16_t*)a.k + (int64_t)cb * a.cache_batch + (int64_t)hkv * a.cache_head;
   const uint16_t* vbase = (const uint16_t*)a.v + (int64_t)cb * a.cache_batch + (int64_t)hkv * a.cache_head;
 
   // This lane's query row (column of S^T).
-  const int r = mt * kRowsTile + wave * 32 + (lane & 31);
+  const int row0 = mt * kRowsTile + wave * 32;
+  const bool computes = row0 < M;   // wave-uniform
+  const int r = row0 + (lane & 31);
   const bool row_ok = r < M;
   const int qn = row_ok ? r / G : 0;
   const int qh = hkv * G + (row_ok ? r % G : 0);
   const uint64_t anc = row_ok ? a.anc[(int64_t)b * a.anc_stride + qn] : 1ull;
+  const uint64_t tree_bits = a.N >= 64 ? anc : anc & ((1ull << a.N) - 1);  // allowed tree nodes
 
   // Q^T fragments: step s covers d = s*16 + g*8 .. +8.
   bf16x8 qf[kD / 16];
@@ -89,122 +116,135 @@ __global__ void __launch_bounds__(kWavesA * 64) tree_attn_bf16_kernel(AttnArgs a
   for (int db = 0; db < kD / 32; ++db)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
-  float m_run = kNegBig, l_run = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f;
   const float sl2 = a.scale * 1.44269504088896341f;
 
-  // Staging: 512 threads, K tile 64 x 128 bf16 = 1024 chunks of 16 B (2 per
-  // thread), same for V.
-  auto load_tile = [&](int key0, uint4 (&rk)[2], uint4 (&rv)[2]) {
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      int idx = tid + c * 512;
-      int kr = idx >> 4, col = (idx & 15) * 8;
-      int key = min(key0 + kr, total - 1);
-      key = min(key, a.capacity - 1);
-      rk[c] = *(const uint4*)(kbase + (int64_t)key * kD + col);
-      rv[c] = *(const uint4*)(vbase + (int64_t)key * kD + col);
-    }
+  // Staging. K: chunk c of thread t is row t/16 + 32c, dims (t%16)*8..+8.
+  // V: thread t holds keys 2*(t/16) and 2*(t/16)+1 of dims (t%16)*8..+8 and
+  // writes each V^T row as one 4-byte key pair.
+  const int st_col = (tid & 15) * 8;
+  const int st_row = tid >> 4;
+  // Named registers (not arrays) so the prefetch stays in VGPRs.
+  uint4 rk0, rk1, rv0, rv1;
+  auto load_tile = [&](int key0) {
+    const uint16_t* kp = kbase + st_col;
+    const uint16_t* vp = vbase + st_col;
+    rk0 = *(const uint4*)(kp + (int64_t)min(key0 + st_row, last_key) * kD);
+    rk1 = *(const uint4*)(kp + (int64_t)min(key0 + st_row + 32, last_key) * kD);
+    rv0 = *(const uint4*)(vp + (int64_t)min(key0 + 2 * st_row, last_key) * kD);
+    rv1 = *(const uint4*)(vp + (int64_t)min(key0 + 2 * st_row + 1, last_key) * kD);
   };
-  auto store_tile = [&](const uint4 (&rk)[2], const uint4 (&rv)[2]) {
+  // V^T row d, key pair p (keys 2p, 2p+1) lives at word 2*((p >> 1) ^ ((d >> 3) & 15)) + (p & 1).
+  const int vsw_word = 2 * ((st_row >> 1) ^ ((st_col >> 3) & 15)) + (st_row & 1);
+  auto store_tile = [&](int buf) {
+    uint16_t* kd = &Ks[buf][st_row * kKPitch + st_col];
+    *(uint4*)(kd) = rk0;
+    *(uint4*)(kd + 32 * kKPitch) = rk1;
+    uint32_t* vt = (uint32_t*)&Vt[buf][st_col * kVPitch] + vsw_word;
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      int idx = tid + c * 512;
-      int kr = idx >> 4, col = (idx & 15) * 8;
-      *(uint4*)&Ks[kr * kKPitch + col] = rk[c];
-      uint32_t w[4] = {rv[c].x, rv[c].y, rv[c].z, rv[c].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        Vt[(col + 2 * e) * kVPitch + kr] = (uint16_t)(w[e] & 0xffffu);
-        Vt[(col + 2 * e + 1) * kVPitch + kr] = (uint16_t)(w[e] >> 16);
-      }
+    for (int e2 = 0; e2 < 4; ++e2) {
+      const uint32_t w0 = u4_word(rv0, e2), w1 = u4_word(rv1, e2);
+      vt[(2 * e2) * (kVPitch / 2)] = __builtin_amdgcn_perm(w1, w0, 0x05040100u);      // element 2*e2
+      vt[(2 * e2 + 1) * (kVPitch / 2)] = __builtin_amdgcn_perm(w1, w0, 0x07060302u);  // element 2*e2+1
     }
   };
 
-  uint4 rk[2], rv[2];
-  load_tile(0, rk, rv);
   const int ntiles = (total + kKT - 1) / kKT;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
     const int key0 = t * kKT;
-    __syncthreads();
-    store_tile(rk, rv);
-    __syncthreads();
-    if (t + 1 < ntiles) load_tile(key0 + kKT, rk, rv);
+    if (t + 1 < ntiles) load_tile(key0 + kKT);
 
-    // S^T for two 32-key blocks.
-    floatx16 st[2];
+    if (computes) {
+      // S^T for two 32-key blocks.
+      floatx16 st[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+      for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) st[kb][i] = 0.0f;
+        for (int i = 0; i < 16; ++i) st[kb][i] = 0.0f;
 #pragma unroll
-      for (int s = 0; s < kD / 16; ++s) {
-        bf16x8 kf = *(const bf16x8*)&Ks[(kb * 32 + (lane & 31)) * kKPitch + s * 16 + g * 8];
-        st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], st[kb], 0, 0, 0);
-      }
-    }
-    // Mask and scale (log2 domain), tile max.
-    float tmax = kNegBig;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        int key = key0 + kb * 32 + c_row32(i, lane);
-        bool ok;
-        if (key < s0) {
-          ok = true;
-        } else {
-          int m = key - s0;
-          ok = m < a.N && ((anc >> m) & 1ull);
+        for (int s = 0; s < kD / 16; ++s) {
+          bf16x8 kf = *(const bf16x8*)&Ks[buf][(kb * 32 + (lane & 31)) * kKPitch + s * 16 + g * 8];
+          st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], st[kb], 0, 0, 0);
         }
-        float x = ok ? st[kb][i] * sl2 : kNegBig;
-        st[kb][i] = x;
-        tmax = fmaxf(tmax, x);
       }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float m_new = fmaxf(m_run, tmax);
-    const float alpha = exp2f(m_run - m_new);
-    float psum = 0.0f;
-    bf16x8 pf[2][2];  // [kb][ks] B operand of P^T
+      if (key0 + kKT > s0) {  // tile reaches the tree keys (or the end)
+        // Allowed keys of this tile as a 64-bit mask (bit j = key key0 + j), shifted
+        // to this half-wave's first key; element i sits at bit kb*32 + c_row32(i, 0).
+        const uint64_t allowed = tile_allowed_mask(s0 - key0, tree_bits) >> (g * 4);
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        uint32_t packed[4];
-#pragma unroll
-        for (int j = 0; j < 8; j += 2) {
-          float p0 = st[kb][ks * 8 + j] <= kNegBig ? 0.0f : exp2f(st[kb][ks * 8 + j] - m_new);
-          float p1 = st[kb][ks * 8 + j + 1] <= kNegBig ? 0.0f : exp2f(st[kb][ks * 8 + j + 1] - m_new);
-          uint16_t h0 = fg::f32_to_bf16(p0), h1 = fg::f32_to_bf16(p1);
-          psum += fg::bf16_to_f32(h0) + fg::bf16_to_f32(h1);
-          packed[j / 2] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-        }
-        pf[kb][ks] = __builtin_bit_cast(bf16x8, make_uint4(packed[0], packed[1], packed[2], packed[3]));
+          for (int i = 0; i < 16; ++i) {
+            const bool ok = (allowed >> (kb * 32 + c_row32(i, 0))) & 1ull;
+            st[kb][i] = ok ? st[kb][i] : -INFINITY;
+          }
       }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
+      float tmax = -INFINITY;
 #pragma unroll
-    for (int db = 0; db < kD / 32; ++db)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
-    // O^T += V^T P^T. Slot j of lane (g) holds key kb*32 + ks*16 + (j/4)*8 + g*4 + j%4.
+        for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, st[kb][i]);
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      // Lazy rescale: the reference max only moves when some lane's max grew by
+      // more than 2^kRescaleSlack, so p <= 2^kRescaleSlack and O / l is unchanged.
+      const float m_new = fmaxf(m_run, tmax * sl2);
+      if (__any(m_new > m_run + kRescaleSlack)) {
+        const float m_sub = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_sub);
+        l_run *= alpha;
 #pragma unroll
-    for (int db = 0; db < kD / 32; ++db) {
-      const uint16_t* vrow = &Vt[(db * 32 + (lane & 31)) * kVPitch];
+        for (int db = 0; db < kD / 32; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+        m_run = m_new;
+      }
+      const float m_sub = m_run == -INFINITY ? 0.0f : m_run;
+      float psum = 0.0f;
+      bf16x8 pf[2][2];  // [kb][ks] B operand of P^T
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          int kk = kb * 32 + ks * 16 + g * 4;
-          uint2 lo = *(const uint2*)(vrow + kk);
-          uint2 hi = *(const uint2*)(vrow + kk + 8);
-          bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[kb][ks], o[db], 0, 0, 0);
+          uint32_t packed[4];
+#pragma unroll
+          for (int j = 0; j < 8; j += 2) {
+            float p0 = __builtin_amdgcn_exp2f(fmaf(st[kb][ks * 8 + j], sl2, -m_sub));
+            float p1 = __builtin_amdgcn_exp2f(fmaf(st[kb][ks * 8 + j + 1], sl2, -m_sub));
+            psum += p0 + p1;
+            packed[j / 2] = fg::pack_bf16x2(p0, p1);
+          }
+          pf[kb][ks] = __builtin_bit_cast(bf16x8, make_uint4(packed[0], packed[1], packed[2], packed[3]));
         }
+      l_run += psum;
+      // O^T += V^T P^T. Slot j of lane (g) holds key kb*32 + ks*16 + (j/4)*8 + g*4 + j%4.
+#pragma unroll
+      for (int db = 0; db < kD / 32; ++db) {
+        const int dv = db * 32 + (lane & 31);
+        const uint16_t* vrow = &Vt[buf][dv * kVPitch];
+        const int sw = (dv >> 3) & 15;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            int kg = kb * 8 + ks * 4 + g;  // 4-key group of slots 0..3; slots 4..7 are group kg + 2
+            uint2 lo = *(const uint2*)(vrow + 4 * (kg ^ sw));
+            uint2 hi = *(const uint2*)(vrow + 4 * ((kg + 2) ^ sw));
+            bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+            o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[kb][ks], o[db], 0, 0, 0);
+          }
+      }
     }
+    if (t + 1 < ntiles) store_tile(buf ^ 1);
+    __syncthreads();
   }
+
   // Combine the two half-lanes' sums and write.
-  l_run += __shfl_xor(l_run, 32, 64);
-  const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+  float l = l_run + __shfl_xor(l_run, 32, 64);
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   if (row_ok) {
     uint16_t* orow = (uint16_t*)a.out + (((int64_t)b * a.N + qn) * a.Hq + qh) * kD;
 #pragma unroll
@@ -212,8 +252,8 @@ __global__ void __launch_bounds__(kWavesA * 64) tree_attn_bf16_kernel(AttnArgs a
 #pragma unroll
       for (int i = 0; i < 16; i += 4) {
         int d0 = db * 32 + c_row32(i, lane);
-        uint32_t w0 = (uint32_t)fg::f32_to_bf16(o[db][i] * inv) | ((uint32_t)fg::f32_to_bf16(o[db][i + 1] * inv) << 16);
-        uint32_t w1 = (uint32_t)fg::f32_to_bf16(o[db][i + 2] * inv) | ((uint32_t)fg::f32_to_bf16(o[db][i + 3] * inv) << 16);
+        uint32_t w0 = fg::pack_bf16x2(o[db][i] * inv, o[db][i + 1] * inv);
+        uint32_t w1 = fg::pack_bf16x2(o[db][i + 2] * inv, o[db][i + 3] * inv);
         *(uint2*)(orow + d0) = make_uint2(w0, w1);
       }
   }
@@ -282,8 +322,7 @@ extern "C" int fg_tree_attention(const void* q, void* out, const void* k_cache, 
                "fg_tree_attention: 16-byte alignment");
     int M = (q_heads / kv_heads) * num_nodes;
     int m_tiles = (M + kRowsTile - 1) / kRowsTile;
-    hipLaunchKernelGGL(tree_attn_bf16_kernel, dim3(batch * kv_heads * m_tiles), dim3(kWavesA * 64), 0, s, a,
-                       m_tiles);
+    hipLaunchKernelGGL(tree_attn_bf16_kernel, dim3(batch * kv_heads * m_tiles), dim3(kThreads), 0, s, a, m_tiles);
   } else if (dtype == fg::kF32) {
     FG_REQUIRE(head_dim <= 128, "fg_tree_attention: fp32 path supports head_dim <= 128");
     hipLaunchKernelGGL(tree_attn_f32_kernel, dim3(batch * num_nodes * q_heads), dim3(64), 0, s, a);

@@ -38,6 +38,16 @@ FG_DEVICE uint16_t f32_to_bf16(float f) {
   return (uint16_t)(b >> 16);
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats to packed bf16 (lo = a, hi = b), round-to-nearest-even: one
+// v_cvt_pk_bf16_f32 on gfx950. Equals f32_to_bf16 on finite inputs.
+FG_DEVICE uint32_t pack_bf16x2(float a, float b) {
+  f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
 template <int DT>
 FG_DEVICE float load_elem(const void* p, int64_t i) {
   if constexpr (DT == kBF16)

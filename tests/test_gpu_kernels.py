@@ -371,7 +371,7 @@ def _attn_reference(q, kc, vc, seq, anc, N, G):
 
 @pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float32, 64), (torch.float32, 128)])
 @pytest.mark.parametrize("ks,budget,Hq,Hkv", [([4, 2, 1, 1], 32, 28, 4), ([4, 2], 16, 8, 2), ([3], 4, 12, 2),
-                                               ([1] * 63, 64, 4, 1)])
+                                               ([1] * 63, 64, 4, 1), ([2] * 5, 48, 28, 4)])
 def test_tree_attention_matches_reference(dtype, d, ks, budget, Hq, Hkv):
     rng = np.random.default_rng(len(ks) + Hq)
     parents, depths, _ = OT.dense_topology(ks, budget)
