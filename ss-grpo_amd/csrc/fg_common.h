@@ -84,6 +84,17 @@ FG_DEVICE void load8(const void* p, int64_t i, float (&v)[8]) {
   }
 }
 
+template <int DT>
+FG_DEVICE void store8(void* p, int64_t i, const float (&v)[8]) {
+  if constexpr (DT == kBF16) {
+    *(uint4*)((uint16_t*)p + i) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                             pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+  } else {
+    *(float4*)((float*)p + i) = make_float4(v[0], v[1], v[2], v[3]);
+    *(float4*)((float*)p + i + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
 // ------------------------------------------------------------------ ordering keys
 // Order-preserving uint32 key of a float: -0 maps to +0's key and every NaN to
 // the largest key, so (key desc, index asc) is a total order agreeing with <.

@@ -7,14 +7,41 @@
 
 namespace {
 
+// 4 consecutive elements as floats (8 bytes bf16 / 16 bytes fp32).
+template <int DT>
+FG_DEVICE void load4(const void* p, int64_t i, float (&v)[4]) {
+  if constexpr (DT == fg::kBF16) {
+    uint2 r = *(const uint2*)((const uint16_t*)p + i);
+    v[0] = __uint_as_float(r.x << 16);
+    v[1] = __uint_as_float(r.x & 0xffff0000u);
+    v[2] = __uint_as_float(r.y << 16);
+    v[3] = __uint_as_float(r.y & 0xffff0000u);
+  } else {
+    float4 a = *(const float4*)((const float*)p + i);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  }
+}
+
+template <int DT>
+FG_DEVICE void store4(void* p, int64_t i, const float (&v)[4]) {
+  if constexpr (DT == fg::kBF16)
+    *(uint2*)((uint16_t*)p + i) = make_uint2(fg::pack_bf16x2(v[0], v[1]), fg::pack_bf16x2(v[2], v[3]));
+  else
+    *(float4*)((float*)p + i) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
 // One workgroup per token (b, n). qkv row = [q heads | k heads | v heads] x d.
 // Position = seq_len[b] + pos_offset[n]; cache slot = seq_len[b] + n.
+// cos/sin of the token's d/2 angles are computed once into LDS; each thread then
+// rotates 4 consecutive pairs (i, i + d/2) of one head with 8/16-byte accesses.
+// Requires d % 8 == 0 and d <= 256.
 template <int DT>
 __global__ void __launch_bounds__(256) rope_kv_write_kernel(
     const void* __restrict__ qkv, int64_t ld_qkv, int N, int Hq, int Hkv, int d, const int32_t* __restrict__ seq_len,
     const int32_t* __restrict__ pos_offset, const float* __restrict__ inv_freq, void* __restrict__ q_out,
     void* __restrict__ k_cache, void* __restrict__ v_cache, int64_t cache_batch, int64_t cache_head, int capacity,
     const int32_t* __restrict__ row_map, int32_t* __restrict__ err_flag) {
+  __shared__ float cs[128], sn[128];
   const int tok = blockIdx.x;
   const int b = tok / N, n = tok % N;
   const int s = seq_len[b];
@@ -24,71 +51,111 @@ __global__ void __launch_bounds__(256) rope_kv_write_kernel(
   const int half = d / 2;
   const bool slot_ok = slot >= 0 && slot < capacity;
   if (!slot_ok && threadIdx.x == 0 && err_flag) atomicOr(err_flag, 8);
+  for (int i = threadIdx.x; i < half; i += blockDim.x) {
+    const float ang = (float)pos * inv_freq[i];
+    cs[i] = cosf(ang);
+    sn[i] = sinf(ang);
+  }
+  __syncthreads();
   const int64_t row = (int64_t)tok * ld_qkv;
-  // q and k heads: rotate pairs (i, i + d/2)
-  for (int e = threadIdx.x; e < (Hq + Hkv) * half; e += blockDim.x) {
-    int h = e / half, i = e % half;
-    float ang = (float)pos * inv_freq[i];
-    float c = cosf(ang), sn = sinf(ang);
-    int64_t src = row + (int64_t)h * d;
-    float x1 = fg::load_elem<DT>(qkv, src + i);
-    float x2 = fg::load_elem<DT>(qkv, src + i + half);
-    float y1 = x1 * c - x2 * sn;
-    float y2 = x2 * c + x1 * sn;
+  const int quads = half / 4;
+  // q and k heads: rotate pairs (i, i + d/2), 4 pairs per item
+  for (int e = threadIdx.x; e < (Hq + Hkv) * quads; e += blockDim.x) {
+    const int h = e / quads, i0 = (e % quads) * 4;
+    const int64_t src = row + (int64_t)h * d;
+    float x1[4], x2[4], y1[4], y2[4];
+    load4<DT>(qkv, src + i0, x1);
+    load4<DT>(qkv, src + i0 + half, x2);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float c = cs[i0 + j], sv = sn[i0 + j];
+      y1[j] = x1[j] * c - x2[j] * sv;
+      y2[j] = x2[j] * c + x1[j] * sv;
+    }
     if (h < Hq) {
-      int64_t dst = ((int64_t)tok * Hq + h) * d;
-      fg::store_elem<DT>(q_out, dst + i, y1);
-      fg::store_elem<DT>(q_out, dst + i + half, y2);
+      const int64_t dst = ((int64_t)tok * Hq + h) * d;
+      store4<DT>(q_out, dst + i0, y1);
+      store4<DT>(q_out, dst + i0 + half, y2);
     } else if (slot_ok) {
-      int hk = h - Hq;
-      int64_t dst = (int64_t)cb * cache_batch + (int64_t)hk * cache_head + (int64_t)slot * d;
-      fg::store_elem<DT>(k_cache, dst + i, y1);
-      fg::store_elem<DT>(k_cache, dst + i + half, y2);
+      const int64_t dst = (int64_t)cb * cache_batch + (int64_t)(h - Hq) * cache_head + (int64_t)slot * d;
+      store4<DT>(k_cache, dst + i0, y1);
+      store4<DT>(k_cache, dst + i0 + half, y2);
     }
   }
-  for (int e = threadIdx.x; slot_ok && e < Hkv * d; e += blockDim.x) {
-    int hk = e / d, i = e % d;
-    float x = fg::load_elem<DT>(qkv, row + (int64_t)(Hq + Hkv + hk) * d + i);
-    fg::store_elem<DT>(v_cache, (int64_t)cb * cache_batch + (int64_t)hk * cache_head + (int64_t)slot * d + i, x);
+  const int oct = d / 8;
+  for (int e = threadIdx.x; slot_ok && e < Hkv * oct; e += blockDim.x) {
+    const int hk = e / oct, i0 = (e % oct) * 8;
+    float x[8];
+    fg::load8<DT>(qkv, row + (int64_t)(Hq + Hkv + hk) * d + i0, x);
+    fg::store8<DT>(v_cache, (int64_t)cb * cache_batch + (int64_t)hk * cache_head + (int64_t)slot * d + i0, x);
   }
 }
 
-// y = RMSNorm(x [+ delta]) * w; with delta the sum is written back to x first.
+// y = RMSNorm(x [+ delta]) * w; with delta the sum is written back to x first and
+// the stored (rounded) residual feeds the norm. One workgroup per row, 8
+// elements per access; the row stays in registers between the two passes.
+// Requires H % 8 == 0 and H <= 8 * 256 * kNormChunks.
+constexpr int kNormChunks = 4;
+
 template <int DT>
 __global__ void __launch_bounds__(256) rmsnorm_kernel(void* __restrict__ x, const void* __restrict__ delta,
                                                       const void* __restrict__ w, void* __restrict__ y, int H,
                                                       float eps) {
   const int64_t base = (int64_t)blockIdx.x * H;
+  const int nch = H / 8;
   __shared__ float red[4];
+  float v[kNormChunks][8];
   float ss = 0.0f;
-  for (int i = threadIdx.x; i < H; i += 256) {
-    float v = fg::load_elem<DT>(x, base + i);
-    if (delta) {
-      v += fg::load_elem<DT>(delta, base + i);
-      fg::store_elem<DT>(x, base + i, v);
-      v = fg::load_elem<DT>(x, base + i);  // the stored (rounded) residual feeds the norm
+#pragma unroll
+  for (int c = 0; c < kNormChunks; ++c) {
+    const int ch = threadIdx.x + c * 256;
+    if (ch < nch) {
+      fg::load8<DT>(x, base + ch * 8, v[c]);
+      if (delta) {
+        float dv[8];
+        fg::load8<DT>(delta, base + ch * 8, dv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[c][j] += dv[j];
+        fg::store8<DT>(x, base + ch * 8, v[c]);
+        if constexpr (DT == fg::kBF16) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[c][j] = fg::bf16_to_f32(fg::f32_to_bf16(v[c][j]));
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += v[c][j] * v[c][j];
     }
-    ss += v * v;
   }
   ss = fg::wave_sum(ss);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
   __syncthreads();
   const float rs = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + eps);
-  for (int i = threadIdx.x; i < H; i += 256) {
-    float v = fg::load_elem<DT>(x, base + i);
-    fg::store_elem<DT>(y, base + i, v * rs * fg::load_elem<DT>(w, i));
+#pragma unroll
+  for (int c = 0; c < kNormChunks; ++c) {
+    const int ch = threadIdx.x + c * 256;
+    if (ch < nch) {
+      float wv[8], o[8];
+      fg::load8<DT>(w, ch * 8, wv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = v[c][j] * rs * wv[j];
+      fg::store8<DT>(y, base + ch * 8, o);
+    }
   }
 }
 
-// out[t, i] = silu(gu[t, i]) * gu[t, F + i]
+// out[t, i] = silu(gu[t, i]) * gu[t, F + i]; 8 elements per thread, one grid row
+// per token. Requires F % 8 == 0.
 template <int DT>
-__global__ void swiglu_kernel(const void* __restrict__ gu, void* __restrict__ out, int F, int64_t total) {
-  int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= total) return;
-  int64_t t = e / F, i = e % F;
-  float gt = fg::load_elem<DT>(gu, t * 2 * F + i);
-  float up = fg::load_elem<DT>(gu, t * 2 * F + F + i);
-  fg::store_elem<DT>(out, e, gt / (1.0f + __expf(-gt)) * up);
+__global__ void __launch_bounds__(256) swiglu_kernel(const void* __restrict__ gu, void* __restrict__ out, int F) {
+  const int ch = blockIdx.x * 256 + threadIdx.x;
+  if (ch * 8 >= F) return;
+  const int64_t t = blockIdx.y;
+  float g[8], u[8], o[8];
+  fg::load8<DT>(gu, t * 2 * F + ch * 8, g);
+  fg::load8<DT>(gu, t * 2 * F + F + ch * 8, u);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = g[j] / (1.0f + __expf(-g[j])) * u[j];
+  fg::store8<DT>(out, t * F + ch * 8, o);
 }
 
 }  // namespace
@@ -101,8 +168,12 @@ int fg_rope_kv_write(const void* qkv, int dtype, int64_t ld_qkv, int batch, int 
                      int64_t cache_head_stride, int capacity, const int32_t* row_map, int32_t* err_flag,
                      void* stream) {
   FG_REQUIRE(qkv && seq_len && pos_offset && inv_freq && q_out && k_cache && v_cache, "fg_rope_kv_write: null pointer");
-  FG_REQUIRE(batch > 0 && num_nodes > 0 && q_heads > 0 && kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0,
-             "fg_rope_kv_write: bad shape");
+  FG_REQUIRE(batch > 0 && num_nodes > 0 && q_heads > 0 && kv_heads > 0, "fg_rope_kv_write: bad shape");
+  FG_REQUIRE(head_dim > 0 && head_dim % 8 == 0 && head_dim <= 256, "fg_rope_kv_write: head_dim must be a multiple of 8 in [8, 256]");
+  FG_REQUIRE(ld_qkv % 8 == 0 && ((uintptr_t)qkv & 15) == 0 && ((uintptr_t)q_out & 15) == 0 &&
+                 ((uintptr_t)k_cache & 15) == 0 && ((uintptr_t)v_cache & 15) == 0 && cache_batch_stride % 8 == 0 &&
+                 cache_head_stride % 8 == 0,
+             "fg_rope_kv_write: rows must be 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
   dim3 grid(batch * num_nodes);
   if (dtype == fg::kBF16)
@@ -119,6 +190,10 @@ int fg_rope_kv_write(const void* qkv, int dtype, int64_t ld_qkv, int batch, int 
 int fg_rmsnorm(void* x, const void* delta, const void* weight, void* y, int dtype, int rows, int hidden, float eps,
                void* stream) {
   FG_REQUIRE(x && weight && y && rows > 0 && hidden > 0, "fg_rmsnorm: bad arguments");
+  FG_REQUIRE(hidden % 8 == 0 && hidden <= 8 * 256 * kNormChunks, "fg_rmsnorm: hidden must be a multiple of 8, at most 8192");
+  FG_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)weight & 15) == 0 && ((uintptr_t)y & 15) == 0 &&
+                 (!delta || ((uintptr_t)delta & 15) == 0),
+             "fg_rmsnorm: 16-byte alignment");
   hipStream_t s = (hipStream_t)stream;
   if (dtype == fg::kBF16)
     hipLaunchKernelGGL(rmsnorm_kernel<fg::kBF16>, dim3(rows), dim3(256), 0, s, x, delta, weight, y, hidden, eps);
@@ -129,13 +204,15 @@ int fg_rmsnorm(void* x, const void* delta, const void* weight, void* y, int dtyp
 
 int fg_swiglu(const void* gate_up, void* out, int dtype, int rows, int inter, void* stream) {
   FG_REQUIRE(gate_up && out && rows > 0 && inter > 0, "fg_swiglu: bad arguments");
-  int64_t total = (int64_t)rows * inter;
-  dim3 grid((unsigned)((total + 255) / 256));
+  FG_REQUIRE(inter % 8 == 0 && ((uintptr_t)gate_up & 15) == 0 && ((uintptr_t)out & 15) == 0,
+             "fg_swiglu: intermediate size must be a multiple of 8 with 16-byte aligned rows");
+  FG_REQUIRE(rows <= 65535, "fg_swiglu: at most 65535 rows per call");
+  dim3 grid((unsigned)((inter / 8 + 255) / 256), (unsigned)rows);
   hipStream_t s = (hipStream_t)stream;
   if (dtype == fg::kBF16)
-    hipLaunchKernelGGL(swiglu_kernel<fg::kBF16>, grid, dim3(256), 0, s, gate_up, out, inter, total);
+    hipLaunchKernelGGL(swiglu_kernel<fg::kBF16>, grid, dim3(256), 0, s, gate_up, out, inter);
   else
-    hipLaunchKernelGGL(swiglu_kernel<fg::kF32>, grid, dim3(256), 0, s, gate_up, out, inter, total);
+    hipLaunchKernelGGL(swiglu_kernel<fg::kF32>, grid, dim3(256), 0, s, gate_up, out, inter);
   return fg::check_launch("fg_swiglu");
 }
 
