@@ -11,7 +11,8 @@ Replaces the Hugging Face decoder the reference drives through
 * attention is ``fg_tree_attention`` (ancestor bitmask in registers) for the
   tree verify and for prefill, which runs as causal 64-token chains;
 * RMSNorm (+ residual add), rotary + cache write and SwiGLU are HIP kernels;
-  the dense projections are plain library GEMMs (``F.linear``, hipBLASLt).
+  the dense projections are plain library GEMMs (``F.linear``: hipBLASLt or
+  rocBLAS, with the per-shape solution table of ``flashgrpo_amd.tuning``).
 """
 from __future__ import annotations
 
@@ -23,6 +24,7 @@ import torch
 import torch.nn.functional as F
 
 from .. import kernels as K
+from ..tuning import use_tuned_gemms
 
 MAX_TREE_NODES = 64
 
@@ -137,6 +139,8 @@ class TargetModel:
         self.w = weights
         self.inv_freq = inv_freq_table(cfg.head_dim, cfg.rope_theta).to(device)
         self._bufs = {}
+        if self.device.type == "cuda":
+            use_tuned_gemms()
 
     # -------------------------------------------------------------- construction
     @classmethod
