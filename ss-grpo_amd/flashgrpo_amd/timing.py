@@ -18,8 +18,12 @@ _state = threading.local()
 
 
 class KernelTimer:
-    def __init__(self):
+    """Collects (start, end) event pairs per kernel name. ``only``: a set of C-ABI
+    entry-point names to time (None: every launch)."""
+
+    def __init__(self, only=None):
         self.events = defaultdict(list)
+        self.only = None if only is None else set(only)
 
     def summary(self) -> dict:
         """{name: {"count", "total_ms", "avg_ms"}} after synchronising."""
@@ -63,7 +67,7 @@ def label(name: str):
 @contextlib.contextmanager
 def launch(kernel: str):
     t = _timer()
-    if t is None:
+    if t is None or (t.only is not None and kernel not in t.only):
         yield
         return
     labels = _labels()
