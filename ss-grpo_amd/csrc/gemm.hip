@@ -20,6 +20,8 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));  // 16-byte register value (no struct copies)
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 enum Epilogue : int { kEpiNone = 0, kEpiMedusa = 1 };
 
@@ -332,6 +334,289 @@ __global__ void __launch_bounds__(256) gemm_bf16_wide_kernel(GemmArgs g, int epi
   }
 }
 
+// ----------------------------------------------------------------- bf16 weight streaming, M <= 256
+// For the skinny products of the rollout (LM head over <= 256 rows, Medusa fc
+// over the batch) the weight matrix B is read exactly once and dominates the
+// bytes, so B never goes through LDS: every wave owns 16 rows of B and streams
+// them from global memory straight into registers with v_mfma_f32_16x16x32_bf16
+// operand layout. Per 128-wide k-tile, lane (n, q) = (l % 16, l / 16) holds the
+// 64 contiguous bytes B[n][k0 + q*32 .. +32]: each row is read as 256-byte runs
+// by four lanes (the access pattern that measured fastest for this stream).
+// A (<= 256 rows) is staged per k-tile in LDS (double-buffered) and shared by
+// all waves of the workgroup; its 16-byte pieces are XOR-swizzled by row & 15,
+// which keeps the fragment reads free of bank conflicts without padding.
+//
+// Loads run PF k-tiles ahead in register rings (A staging chunks first, then
+// the W pieces of the same tile). Every load is issued unconditionally (past the
+// last k-tile they re-read one fixed line) so the wait counts stay static:
+// consuming tile kt waits only for the loads of tile kt, not for younger ones.
+//
+// k order inside a k-tile: MFMA step s uses piece s (8 k) of each lane's 32-k
+// run, i.e. k = k0 + q*32 + s*8 + j for the lane group q; the A fragments read
+// the same k's, so the products sum the same terms as the natural order. Each
+// 16x16 accumulator is a tile of C^T (lane owns column m = l % 16 and rows
+// n = 4*(l/16) .. +4), so the epilogue writes 4 consecutive n per store.
+constexpr int kST = 128;  // k-tile of the streaming kernel
+FG_DEVICE int a_swz16(int row, int piece) { return row * kST + ((piece ^ (row & 15)) << 3); }
+
+// Up to 32 rows of A the kernel fits in 128 VGPRs, so two workgroups share a CU
+// (more loads in flight per CU).
+constexpr int stream_occupancy(int mb) { return mb <= 2 ? 2 : 1; }
+
+template <int MB, int WAVES, int PF, int CDT>
+__global__ void __launch_bounds__(WAVES * 64, stream_occupancy(MB) * WAVES / 4) gemm_bf16_stream_kernel(GemmArgs g,
+                                                                                                       int epi) {
+  constexpr int NT = WAVES * 64;
+  constexpr int MROWS = MB * 16;
+  constexpr int AC = MROWS * (kST / 8) / NT;  // A staging chunks per thread
+  static_assert(AC >= 1 && MROWS * (kST / 8) % NT == 0, "A staging split");
+  static_assert(PF == 4 || PF == 2, "the ring below is written out for four or two slots");
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][MROWS * kST];
+  // (kST-wide k-tiles, MROWS <= 128)
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q4 = lane >> 4;
+  const int z = blockIdx.y;
+  const int n_base = blockIdx.x * (WAVES * 16) + wave * 16;
+  if (g.row_active && !tile_has_active_row(g, 0, g.M)) return;
+
+  const uint16_t* Ab = (const uint16_t*)g.A + z * g.a_batch;
+  const uint16_t* Bb = (const uint16_t*)g.B + z * g.b_batch;
+  const v4u* dummy = (const v4u*)Bb;  // target of the loads past the last k-tile
+  // This lane's B row (clamped for loads; rows >= N are not stored).
+  const int nb = min(n_base + (lane & 15), g.N - 1);
+  const uint16_t* bsrc = Bb + (int64_t)nb * g.ldb + q4 * 32;
+  // A staging: chunk c of thread t is row (t + c*NT) / 16, 16-byte piece (t % 16).
+  const uint16_t* a_src = Ab + (tid & 15) * 8;
+  int64_t a_off[AC];
+  int a_dst[AC];
+#pragma unroll
+  for (int c = 0; c < AC; ++c) {
+    int idx = tid + c * NT;
+    int r = idx >> 4;
+    int m = min(r, g.M - 1);
+    int src_row = g.a_rows ? g.a_rows[m] : m;
+    a_off[c] = (int64_t)src_row * g.lda;
+    a_dst[c] = a_swz16(r, idx & 15);
+  }
+
+  floatx4 acc[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) acc[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const int ktiles = g.K / kST;  // a multiple of PF (host check)
+  // Ring slots as separate named arrays (constant indices only) so they stay in VGPRs.
+  v4u w0[4], w1[4], w2[4], w3[4], a0[AC], a1[AC], a2[AC], a3[AC];
+#define FG_ISSUE(W, A, KT)                                                                                  \
+  {                                                                                                         \
+    const int kt_ = (KT);                                                                                   \
+    const bool live_ = kt_ < ktiles;                                                                        \
+    _Pragma("unroll") for (int c = 0; c < AC; ++c) A[c] = live_ ? *(const v4u*)(a_src + a_off[c] + kt_ * kST) : *dummy; \
+    _Pragma("unroll") for (int p = 0; p < 4; ++p) W[p] = live_ ? *(const v4u*)(bsrc + kt_ * kST + p * 8) : *dummy; \
+  }
+#define FG_STEP(W, A_NEXT, U)                                                                               \
+  {                                                                                                         \
+    const int cur = (kt0 + (U)) & 1;                                                                        \
+    _Pragma("unroll") for (int st = 0; st < 4; ++st) {                                                      \
+      const bf16x8 wf = __builtin_bit_cast(bf16x8, W[st]);                                                  \
+      _Pragma("unroll") for (int i = 0; i < MB; ++i) {                                                      \
+        const bf16x8 af = *(const bf16x8*)&As[cur][a_swz16(i * 16 + (lane & 15), q4 * 4 + st)];             \
+        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, af, acc[i], 0, 0, 0);                          \
+      }                                                                                                     \
+    }                                                                                                       \
+    _Pragma("unroll") for (int c = 0; c < AC; ++c) *(v4u*)&As[cur ^ 1][a_dst[c]] = A_NEXT[c];             \
+  }
+  FG_ISSUE(w0, a0, 0)
+  FG_ISSUE(w1, a1, 1)
+  if constexpr (PF == 4) {
+    FG_ISSUE(w2, a2, 2)
+    FG_ISSUE(w3, a3, 3)
+  }
+#pragma unroll
+  for (int c = 0; c < AC; ++c) *(v4u*)&As[0][a_dst[c]] = a0[c];
+  __syncthreads();
+
+  for (int kt0 = 0; kt0 < ktiles; kt0 += PF) {
+    // step u consumes slot u, stores the A tile of slot u+1, refills slot u with tile kt0+u+PF
+    if constexpr (PF == 4) {
+      FG_STEP(w0, a1, 0) FG_ISSUE(w0, a0, kt0 + 4) __syncthreads();
+      FG_STEP(w1, a2, 1) FG_ISSUE(w1, a1, kt0 + 5) __syncthreads();
+      FG_STEP(w2, a3, 2) FG_ISSUE(w2, a2, kt0 + 6) __syncthreads();
+      FG_STEP(w3, a0, 3) FG_ISSUE(w3, a3, kt0 + 7) __syncthreads();
+    } else {
+      FG_STEP(w0, a1, 0) FG_ISSUE(w0, a0, kt0 + 2) __syncthreads();
+      FG_STEP(w1, a0, 1) FG_ISSUE(w1, a1, kt0 + 3) __syncthreads();
+    }
+  }
+#undef FG_ISSUE
+#undef FG_STEP
+
+  // Epilogue: acc[i] is the C^T tile (16 n rows, 16 m columns) -> lane owns column m.
+  const int n = n_base + q4 * 4;
+#pragma unroll
+  for (int i = 0; i < MB; ++i) {
+    const int m = i * 16 + (lane & 15);
+    if (m >= g.M) continue;
+    float o[4] = {acc[i][0], acc[i][1], acc[i][2], acc[i][3]};
+    if (epi == kEpiNone && n + 3 < g.N && (g.ldc & 3) == 0) {
+      if constexpr (CDT == fg::kBF16) {
+        *(uint2*)((uint16_t*)g.C + z * g.c_batch + (int64_t)m * g.ldc + n) =
+            make_uint2(fg::pack_bf16x2(o[0], o[1]), fg::pack_bf16x2(o[2], o[3]));
+      } else {
+        *(float4*)((float*)g.C + z * g.c_batch + (int64_t)m * g.ldc + n) = make_float4(o[0], o[1], o[2], o[3]);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) epilogue_store<CDT, fg::kBF16>(g, z, m, n + e, o[e], epi);
+    }
+  }
+}
+
+// 129..256 rows of A: the same stream with v_mfma_f32_32x32x16_bf16 and 32 rows
+// of B per wave, which halves the LDS reads of A per byte of B (at this M the
+// A fragment reads, not HBM, would otherwise bound the kernel). 64-wide k-tiles,
+// two in flight; lane (n, g) = (l % 32, l / 32) holds B[n][k0 + g*32 .. +32] and
+// feeds 16-byte piece kk to MFMA step kk. A rows in LDS are 128 B, pieces
+// XOR-swizzled by (row >> 1) & 7.
+FG_DEVICE int a_swz32(int row, int piece) { return row * kBK + ((piece ^ ((row >> 1) & 7)) << 3); }
+
+template <int CDT>
+__global__ void __launch_bounds__(512) gemm_bf16_stream32_kernel(GemmArgs g, int epi) {
+  constexpr int WAVES = 8, NT = 512, MB = 8, MROWS = 256;
+  constexpr int AC = MROWS * (kBK / 8) / NT;  // 4
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][MROWS * kBK];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g2 = lane >> 5;
+  const int z = blockIdx.y;
+  const int n_base = blockIdx.x * (WAVES * 32) + wave * 32;
+  if (g.row_active && !tile_has_active_row(g, 0, g.M)) return;
+
+  const uint16_t* Ab = (const uint16_t*)g.A + z * g.a_batch;
+  const uint16_t* Bb = (const uint16_t*)g.B + z * g.b_batch;
+  const v4u* dummy = (const v4u*)Bb;
+  const int nb = min(n_base + (lane & 31), g.N - 1);
+  const uint16_t* bsrc = Bb + (int64_t)nb * g.ldb + g2 * 32;
+  const uint16_t* a_src = Ab + (tid & 7) * 8;
+  int64_t a_off[AC];
+  int a_dst[AC];
+#pragma unroll
+  for (int c = 0; c < AC; ++c) {
+    int idx = tid + c * NT;
+    int r = idx >> 3;
+    int m = min(r, g.M - 1);
+    int src_row = g.a_rows ? g.a_rows[m] : m;
+    a_off[c] = (int64_t)src_row * g.lda;
+    a_dst[c] = a_swz32(r, idx & 7);
+  }
+  floatx16 acc[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
+
+  const int ktiles = g.K / kBK;  // even (host check)
+  v4u w0[4], w1[4], a0[AC], a1[AC];
+#define FG_ISSUE(W, A, KT)                                                                                  \
+  {                                                                                                         \
+    const int kt_ = (KT);                                                                                   \
+    const bool live_ = kt_ < ktiles;                                                                        \
+    _Pragma("unroll") for (int c = 0; c < AC; ++c) A[c] = live_ ? *(const v4u*)(a_src + a_off[c] + kt_ * kBK) : *dummy; \
+    _Pragma("unroll") for (int q = 0; q < 4; ++q) W[q] = live_ ? *(const v4u*)(bsrc + kt_ * kBK + q * 8) : *dummy; \
+  }
+#define FG_STEP(W, A_NEXT, U)                                                                               \
+  {                                                                                                         \
+    const int cur = (kt0 + (U)) & 1;                                                                        \
+    _Pragma("unroll") for (int kk = 0; kk < 4; ++kk) {                                                      \
+      const bf16x8 wf = __builtin_bit_cast(bf16x8, W[kk]);                                                  \
+      _Pragma("unroll") for (int i = 0; i < MB; ++i) {                                                      \
+        const bf16x8 af = *(const bf16x8*)&As[cur][a_swz32(i * 32 + (lane & 31), g2 * 4 + kk)];             \
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf, af, acc[i], 0, 0, 0);                          \
+      }                                                                                                     \
+    }                                                                                                       \
+    _Pragma("unroll") for (int c = 0; c < AC; ++c) *(v4u*)&As[cur ^ 1][a_dst[c]] = A_NEXT[c];             \
+  }
+  FG_ISSUE(w0, a0, 0)
+  FG_ISSUE(w1, a1, 1)
+#pragma unroll
+  for (int c = 0; c < AC; ++c) *(v4u*)&As[0][a_dst[c]] = a0[c];
+  __syncthreads();
+  for (int kt0 = 0; kt0 < ktiles; kt0 += 2) {
+    FG_STEP(w0, a1, 0) FG_ISSUE(w0, a0, kt0 + 2) __syncthreads();
+    FG_STEP(w1, a0, 1) FG_ISSUE(w1, a1, kt0 + 3) __syncthreads();
+  }
+#undef FG_ISSUE
+#undef FG_STEP
+
+  // Epilogue: acc[i] is the C^T tile (n rows, m columns) -> lane owns column m.
+#pragma unroll
+  for (int i = 0; i < MB; ++i) {
+    const int m = i * 32 + (lane & 31);
+    if (m >= g.M) continue;
+#pragma unroll
+    for (int v4 = 0; v4 < 4; ++v4) {
+      const int n = n_base + v4 * 8 + g2 * 4;
+      float o[4] = {acc[i][4 * v4], acc[i][4 * v4 + 1], acc[i][4 * v4 + 2], acc[i][4 * v4 + 3]};
+      if (epi == kEpiNone && n + 3 < g.N && (g.ldc & 3) == 0) {
+        if constexpr (CDT == fg::kBF16) {
+          *(uint2*)((uint16_t*)g.C + z * g.c_batch + (int64_t)m * g.ldc + n) =
+              make_uint2(fg::pack_bf16x2(o[0], o[1]), fg::pack_bf16x2(o[2], o[3]));
+        } else {
+          *(float4*)((float*)g.C + z * g.c_batch + (int64_t)m * g.ldc + n) = make_float4(o[0], o[1], o[2], o[3]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) epilogue_store<CDT, fg::kBF16>(g, z, m, n + e, o[e], epi);
+      }
+    }
+  }
+}
+
+template <int MB, int WAVES, int PF>
+void launch_stream(const GemmArgs& g, int out_dtype, int epi, int batch, hipStream_t s) {
+  dim3 grid((g.N + WAVES * 16 - 1) / (WAVES * 16), batch);
+  if (out_dtype == fg::kBF16)
+    hipLaunchKernelGGL((gemm_bf16_stream_kernel<MB, WAVES, PF, fg::kBF16>), grid, dim3(WAVES * 64), 0, s, g, epi);
+  else
+    hipLaunchKernelGGL((gemm_bf16_stream_kernel<MB, WAVES, PF, fg::kF32>), grid, dim3(WAVES * 64), 0, s, g, epi);
+}
+
+// 16-row blocks of A: 1, 2, 4 or 8 (M <= 128; above that the 32x32 variant runs).
+constexpr int stream_mb(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8; }
+constexpr int stream_pf(int) { return 4; }  // k-tiles in flight
+
+// Can a weight-streaming kernel run this product? (bf16, M <= 256; K a multiple
+// of 4 * 128 up to 128 rows, of 2 * 64 above.)
+bool stream_gemm_ok(const GemmArgs& g) {
+  if (g.M <= 128) return g.K % (kST * 4) == 0;
+  return g.M <= 256 && g.K % (kBK * 2) == 0;
+}
+
+// The most waves per workgroup (<= 8) that still give >= 2 workgroups per CU
+// (256 CUs) over the whole product. A staging needs MB*16*16 >= waves*64, and
+// with more than 64 rows of A fewer than 4 waves leave too many staging chunks
+// per thread.
+void launch_stream_gemm(const GemmArgs& g, int out_dtype, int epi, int batch, hipStream_t s) {
+  if (g.M > 128) {
+    dim3 grid((g.N + 255) / 256, batch);
+    if (out_dtype == fg::kBF16)
+      hipLaunchKernelGGL(gemm_bf16_stream32_kernel<fg::kBF16>, grid, dim3(512), 0, s, g, epi);
+    else
+      hipLaunchKernelGGL(gemm_bf16_stream32_kernel<fg::kF32>, grid, dim3(512), 0, s, g, epi);
+    return;
+  }
+  const int mb = stream_mb(g.M);
+  auto wgs = [&](int waves) { return (long)((g.N + waves * 16 - 1) / (waves * 16)) * batch; };
+  const int min_waves = mb >= 8 ? 4 : 2;
+  int waves = std::min(8, mb * 4);
+  while (waves > min_waves && wgs(waves) < 512) waves /= 2;
+#define FG_STREAM(MBv, Wv) \
+  if (mb == MBv && waves == Wv) { launch_stream<MBv, Wv, stream_pf(MBv)>(g, out_dtype, epi, batch, s); return; }
+  FG_STREAM(1, 2) FG_STREAM(1, 4)
+  FG_STREAM(2, 2) FG_STREAM(2, 4) FG_STREAM(2, 8)
+  FG_STREAM(4, 2) FG_STREAM(4, 4) FG_STREAM(4, 8)
+  FG_STREAM(8, 4) FG_STREAM(8, 8)
+#undef FG_STREAM
+}
+
 // ----------------------------------------------------------------- fp32 FMA
 template <int CDT>
 __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs g, int epi) {
@@ -386,7 +671,9 @@ int launch_gemm(const GemmArgs& g, int dtype, int out_dtype, int epi, int batch,
     FG_REQUIRE(g.lda % 8 == 0 && g.ldb % 8 == 0 && ((uintptr_t)g.A & 15) == 0 && ((uintptr_t)g.B & 15) == 0,
                "gemm: bf16 operands need 16-byte aligned rows");
     const bool wide_ok = g.N >= 512 && g.ldc % 4 == 0 && ((uintptr_t)g.C & 15) == 0 && (g.c_batch % 4) == 0;
-    if (wide_ok) {
+    if (stream_gemm_ok(g)) {
+      launch_stream_gemm(g, out_dtype, epi, batch, s);
+    } else if (wide_ok) {
       // Pick the M tile that pads M least (larger tile on ties).
       const int cands[3] = {192, 128, 64};
       int BM = 256, best = 1 << 30;
