@@ -275,7 +275,8 @@ class FlashMedusaDecoder:
             r.sync()
             m["medusa_time"] += time.time() - t0
             if cfg.adaptive_tree_enabled:
-                plan, adaptive_stats = self._adapt_plan(plan, stats.cpu().numpy(), score.cpu().numpy(), Bc)
+                both = torch.cat([stats.view(stats.shape[0], -1), score.view(score.shape[0], -1)], 1).cpu().numpy()
+                plan, adaptive_stats = self._adapt_plan(plan, both[:, :2], both[:, 2:], Bc)
         topo = TreeTopology.for_plan(plan)
         N = topo.num_nodes
         r.plan_last = {"B_cur": Bc, "node_budget_per_seq": plan.node_budget_per_seq,
@@ -285,8 +286,8 @@ class FlashMedusaDecoder:
         m["active_sum"] += Bc
         m["node_sum"] += N
         m["samples"] += 1
-        for dpt in topo.depths[1:]:
-            r.proposed_by_depth[dpt] = r.proposed_by_depth.get(dpt, 0) + Bc
+        for dpt, c in topo.depth_counts.items():
+            r.proposed_by_depth[dpt] = r.proposed_by_depth.get(dpt, 0) + c * Bc
         dshared = topo.device(dev)
         dmap = topo.device(dev, Bc)
         if N > 1:
@@ -466,18 +467,20 @@ class FlashMedusaDecoder:
             r.pending = new_pending
         # ---------------- bookkeeping
         m["rounds"] += 1
-        emitted = 0
-        for i in range(Bc):
-            L = int(acc_len_h[i])
-            emitted += L
-            r.generated[r.active[i]].extend(int(t) for t in acc_tok_h[i, :L])
-            r.accept_hist[L] = r.accept_hist.get(L, 0) + 1
-            for dpt in range(2, L + 1):
-                r.accept_by_depth[dpt] = r.accept_by_depth.get(dpt, 0) + 1
-            m["total_acc_length"] += L
-            m["total_decoded_steps"] += 1
-            m["accepted"] += max(L - 1, 0)
-            m["proposed"] += max(N - 1, 0)
+        lens = acc_len_h.astype(np.int64)
+        emitted = int(lens.sum())
+        toks = acc_tok_h.tolist()
+        for i, L in enumerate(lens.tolist()):
+            r.generated[r.active[i]].extend(toks[i][:L])
+        for L, c in enumerate(np.bincount(lens).tolist()):
+            if c:
+                r.accept_hist[L] = r.accept_hist.get(L, 0) + c
+        for dpt in range(2, int(lens.max()) + 1):
+            r.accept_by_depth[dpt] = r.accept_by_depth.get(dpt, 0) + int(np.count_nonzero(lens >= dpt))
+        m["total_acc_length"] += emitted
+        m["total_decoded_steps"] += Bc
+        m["accepted"] += int(np.maximum(lens - 1, 0).sum())
+        m["proposed"] += max(N - 1, 0) * Bc
         if fin_h.any():
             keep = np.nonzero(~fin_h)[0]
             if keep.size == 0:

@@ -191,6 +191,9 @@ class TreeTopology:
         for i, n in enumerate(self.internal):
             self.slot_of[n] = i
         self.max_depth = max(depths) - 1  # walk steps
+        self.depth_counts = {}  # non-root nodes per depth
+        for dpt in depths[1:]:
+            self.depth_counts[dpt] = self.depth_counts.get(dpt, 0) + 1
         bits = []
         for n in range(self.num_nodes):
             m, p = 1 << n, parents[n]

@@ -21,9 +21,11 @@ class KernelTimer:
     """Collects (start, end) event pairs per kernel name. ``only``: a set of C-ABI
     entry-point names to time (None: every launch)."""
 
-    def __init__(self, only=None):
+    def __init__(self, only=None, every: int = 1):
         self.events = defaultdict(list)
         self.only = None if only is None else set(only)
+        self.every = max(1, int(every))  # time one launch in `every` of each name
+        self.seen = defaultdict(int)
 
     def summary(self) -> dict:
         """{name: {"count", "total_ms", "avg_ms"}} after synchronising."""
@@ -72,6 +74,11 @@ def launch(kernel: str):
         return
     labels = _labels()
     name = kernel + (":" + labels[-1] if labels else "")
+    n = t.seen[name]
+    t.seen[name] = n + 1
+    if n % t.every:
+        yield
+        return
     s = torch.cuda.Event(enable_timing=True)
     e = torch.cuda.Event(enable_timing=True)
     s.record()
