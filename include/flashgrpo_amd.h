@@ -102,17 +102,23 @@ int fg_rmsnorm(void* x, const void* delta, const void* weight, void* y, int dtyp
 /* out[t, i] = SiLU(gate_up[t, i]) * gate_up[t, inter + i] */
 int fg_swiglu(const void* gate_up, void* out, int dtype, int rows, int inter, void* stream);
 
+/* Workspace (bytes) that lets fg_sample_tokens / fg_walk_step split each row of an
+ * unrestricted (no top-k, no top-p) or greedy draw over several workgroups. */
+size_t fg_sample_workspace(int rows);
+
 /* One supplied-noise draw per row (rule documented in csrc/sample.hip).
  * Row r reads logits row row_index ? row_index[r] : r. forced (optional): a value
  * >= 0 is emitted instead of sampling. Noise: noise[r*noise_stride + noise_col]
  * when noise != NULL, else counter noise (seed, step, seq_ids ? seq_ids[r] : r, draw).
  * greedy or temperature == 0: argmax (first maximum). top_k <= 0: off.
- * top_p_fixed = floor(top_p * 2^32), 0 = off. */
+ * top_p_fixed = floor(top_p * 2^32), 0 = off. workspace (optional, >= fg_sample_workspace(rows)
+ * bytes): unrestricted and greedy draws then run split over several workgroups per row;
+ * results are identical either way. */
 int fg_sample_tokens(const void* logits, int dtype, int64_t row_stride, int rows, int vocab,
                      const int32_t* row_index, const int32_t* forced, const uint32_t* noise, int noise_stride,
                      int noise_col, uint64_t seed, uint64_t step, const int32_t* seq_ids, int draw,
                      float temperature, int greedy, int top_k, uint32_t top_p_fixed, int32_t* out_tokens,
-                     void* stream);
+                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* exact_target acceptance walk over `batch` trees (one launch per walk step).
  * Node n of tree b: tree_tokens/parents[b*nmax + n], n < n_nodes[b], root = node 0.
@@ -135,7 +141,8 @@ int fg_accept_walk(const void* tree_logits, int dtype, int64_t row_stride, int v
  *   fg_walk_rows   -- row_index[b] = b*nmax + current parent of b, row_active[b];
  *   fg_walk_step   -- draw for every active row b from row b of step_logits
  *                     (noise column noise_col0 + walk_step, counter draw draw0 + walk_step).
- * After the walk, state[2*batch + b] is the step whose logits row b last sampled (-1: none). */
+ * After the walk, state[2*batch + b] is the step whose logits row b last sampled (-1: none).
+ * fg_walk_step's workspace is optional, as for fg_sample_tokens (rows = batch). */
 int fg_walk_begin(const int32_t* tree_tokens, const int32_t* parents, const int32_t* n_nodes, int nmax, int batch,
                   int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
                   int32_t* correction, int32_t* state, void* stream);
@@ -145,7 +152,8 @@ int fg_walk_step(const void* step_logits, int dtype, int64_t row_stride, int voc
                  const uint32_t* noise, int noise_stride, int noise_col0, uint64_t seed, uint64_t step,
                  const int32_t* seq_ids, int draw0, float temperature, int greedy, int top_k, uint32_t top_p_fixed,
                  int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
-                 int32_t* correction, int32_t* state, int32_t* err_flag, void* stream);
+                 int32_t* correction, int32_t* state, int32_t* err_flag, void* workspace, size_t workspace_bytes,
+                 void* stream);
 
 /* Length clamp (max(1, max_length - old_len)), EOS cut (eos_token_id < 0: none),
  * finished flags and, when pending_root != NULL, the next round's forced root

@@ -12,7 +12,9 @@
 //   order) whose inclusive q prefix exceeds target.
 // Integer sums make every result independent of reduction order.
 //
-// One 1024-thread workgroup per sampled row. The row is split into 16
+// Unrestricted and greedy draws with a workspace run split over 16 chunks per
+// row (three launches, see "split sampling"). Otherwise: one 1024-thread
+// workgroup per sampled row. The row is split into 16
 // contiguous wave segments; a wave walks its segment 512 elements (8 per lane,
 // 16-byte loads) per step. Top-k / top-p use an MSB-first 4 x 8-bit radix
 // select over the keys with count or q-weighted histograms in LDS.
@@ -344,6 +346,41 @@ __global__ void walk_rows_kernel(const int32_t* __restrict__ state, int batch, i
   row_active[b] = state[batch + b];
 }
 
+// Walk update of tree b after its draw `tok` at `parent` (one thread).
+FG_DEVICE void walk_apply(int b, int tok, int parent, const int32_t* tree_tokens, const int32_t* parents,
+                          const int32_t* n_nodes, int nmax, int batch, int walk_step, int32_t* acc_tokens,
+                          int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
+                          int32_t* correction, int32_t* state, int32_t* err_flag) {
+  state[2 * batch + b] = walk_step;
+  const int nn = n_nodes[b];
+  const int32_t* pb = parents + (int64_t)b * nmax;
+  const int32_t* tb = tree_tokens + (int64_t)b * nmax;
+  int match = -1;
+  for (int c = 1; c < nn; ++c)
+    if (pb[c] == parent && tb[c] == tok) {
+      match = c;
+      break;
+    }
+  if (match < 0) {
+    correction[b] = tok;
+    state[batch + b] = 0;
+  } else {
+    int len = acc_len[b];
+    if (len < acc_stride) {
+      acc_tokens[(int64_t)b * acc_stride + len] = tok;
+      acc_nodes[(int64_t)b * acc_stride + len] = match;
+      acc_len[b] = len + 1;
+    } else if (err_flag) {
+      atomicOr(err_flag, 4);
+    }
+    last_node[b] = match;
+    state[b] = match;
+    int has_child = 0;
+    for (int c = match + 1; c < nn; ++c) has_child |= pb[c] == match;
+    state[batch + b] = has_child;
+  }
+}
+
 template <int DT>
 __global__ void __launch_bounds__(kThreads) walk_step_kernel(
     const void* __restrict__ logits, int64_t row_stride, int vocab, const int32_t* __restrict__ slot_map,
@@ -371,36 +408,235 @@ __global__ void __launch_bounds__(kThreads) walk_step_kernel(
   uint32_t u = noise_value(noise, (int64_t)b * noise_stride + noise_col0 + walk_step, seed, step, seq,
                            (uint32_t)(draw0 + walk_step));
   int tok = block_sample<DT>(rowp, vocab, sp, u, sh);
-  if (threadIdx.x == 0) {
-    state[2 * batch + b] = walk_step;
-    const int nn = n_nodes[b];
-    const int32_t* pb = parents + (int64_t)b * nmax;
-    const int32_t* tb = tree_tokens + (int64_t)b * nmax;
-    int match = -1;
-    for (int c = 1; c < nn; ++c)
-      if (pb[c] == parent && tb[c] == tok) {
-        match = c;
-        break;
-      }
-    if (match < 0) {
-      correction[b] = tok;
-      state[batch + b] = 0;
+  if (threadIdx.x == 0)
+    walk_apply(b, tok, parent, tree_tokens, parents, n_nodes, nmax, batch, walk_step, acc_tokens, acc_nodes, acc_stride,
+               acc_len, last_node, correction, state, err_flag);
+}
+
+// ------------------------------------------------------------------ split sampling
+// Unrestricted draws (no top-k / top-p) and greedy draws spread one row over
+// kSplitChunks workgroups instead of one: (1) per chunk, the raw maximum and the
+// first-maximum rank key; (2) per chunk, the q-mass sum against the row maximum;
+// (3) per row, the chunk whose running mass crosses the target, then the index
+// inside it -- the same integer rule as block_sample, so the token is identical.
+constexpr int kSplitChunks = 16;
+constexpr int kSplitThreads = 256;
+
+struct SplitArgs {
+  const void* logits;
+  int64_t row_stride;
+  int vocab;
+  int chunk;                 // elements per chunk (multiple of 8)
+  const int32_t* row_index;  // logits row of sampled row r (NULL: r)
+  const int32_t* forced;     // rows with forced[r] >= 0 are not sampled
+  const int32_t* active;     // rows with active[r] == 0 are not sampled (NULL: all)
+  float temperature;
+  int scale;
+  int greedy;
+  float* part_max;           // [rows, kSplitChunks]
+  uint64_t* part_key;
+  uint64_t* part_sum;
+};
+
+template <int DT>
+FG_DEVICE const char* split_row(const SplitArgs& a, int r) {
+  const int64_t src = a.row_index ? a.row_index[r] : r;
+  return (const char*)a.logits + src * a.row_stride * (DT == fg::kBF16 ? 2 : 4);
+}
+
+FG_DEVICE bool split_skip(const SplitArgs& a, int r) {
+  return (a.forced && a.forced[r] >= 0) || (a.active && !a.active[r]);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kSplitThreads) split_max_kernel(SplitArgs a) {
+  const int c = blockIdx.x, r = blockIdx.y;
+  if (split_skip(a, r)) return;
+  __shared__ float smax[kSplitThreads / 64];
+  __shared__ uint64_t skey[kSplitThreads / 64];
+  const char* p = split_row<DT>(a, r);
+  const int lo = c * a.chunk, hi = min(a.vocab, lo + a.chunk);
+  float mx = -INFINITY;
+  uint64_t best = 0;
+  for (int i0 = lo + threadIdx.x * 8; i0 < hi; i0 += kSplitThreads * 8) {
+    float x[8];
+    if (i0 + 8 <= hi) {
+      fg::load8<DT>(p, i0, x);
     } else {
-      int len = acc_len[b];
-      if (len < acc_stride) {
-        acc_tokens[(int64_t)b * acc_stride + len] = tok;
-        acc_nodes[(int64_t)b * acc_stride + len] = match;
-        acc_len[b] = len + 1;
-      } else if (err_flag) {
-        atomicOr(err_flag, 4);
-      }
-      last_node[b] = match;
-      state[b] = match;
-      int has_child = 0;
-      for (int c = match + 1; c < nn; ++c) has_child |= pb[c] == match;
-      state[batch + b] = has_child;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = i0 + j < hi ? fg::load_elem<DT>(p, i0 + j) : -INFINITY;
     }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (i0 + j < hi) {
+        mx = fmaxf(mx, x[j]);
+        uint64_t k = ((uint64_t)fg::sort_key32(x[j]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)(i0 + j));
+        best = k > best ? k : best;
+      }
   }
+  mx = fg::wave_max(mx);
+  best = fg::wave_max_u64(best);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    smax[wave] = mx;
+    skey[wave] = best;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 1; w < kSplitThreads / 64; ++w) {
+      mx = fmaxf(mx, smax[w]);
+      best = skey[w] > best ? skey[w] : best;
+    }
+    a.part_max[r * kSplitChunks + c] = fmaxf(smax[0], mx);
+    a.part_key[r * kSplitChunks + c] = skey[0] > best ? skey[0] : best;
+  }
+}
+
+// Row maximum of the scaled logits from the chunk maxima (x / T is monotone).
+FG_DEVICE float split_row_max(const SplitArgs& a, int r) {
+  float mx = -INFINITY;
+  for (int c = 0; c < kSplitChunks; ++c) mx = fmaxf(mx, a.part_max[r * kSplitChunks + c]);
+  return a.scale ? __fdiv_rn(mx, a.temperature) : mx;
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kSplitThreads) split_sum_kernel(SplitArgs a) {
+  const int c = blockIdx.x, r = blockIdx.y;
+  if (a.greedy || split_skip(a, r)) return;
+  __shared__ uint64_t ssum[kSplitThreads / 64];
+  const char* p = split_row<DT>(a, r);
+  const float m = split_row_max(a, r);
+  const int lo = c * a.chunk, hi = min(a.vocab, lo + a.chunk);
+  uint64_t acc = 0;
+  for (int i0 = lo + threadIdx.x * 8; i0 < hi; i0 += kSplitThreads * 8) {
+    float x[8];
+    if (i0 + 8 <= hi) {
+      fg::load8<DT>(p, i0, x);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = i0 + j < hi ? fg::load_elem<DT>(p, i0 + j) : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (i0 + j < hi) {
+        const float sv = a.scale ? __fdiv_rn(x[j], a.temperature) : x[j];
+        acc += fg::quantize_q40(fg::exp_fg(sv - m));
+      }
+  }
+  acc = fg::wave_sum_u64(acc);
+  if ((threadIdx.x & 63) == 0) ssum[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t t = 0;
+#pragma unroll
+    for (int w = 0; w < kSplitThreads / 64; ++w) t += ssum[w];
+    a.part_sum[r * kSplitChunks + c] = t;
+  }
+}
+
+// The token of row r from the chunk partials (whole block; every thread returns it).
+template <int DT>
+FG_DEVICE int split_pick(const SplitArgs& a, int r, uint32_t u, Shared& sh) {
+  uint64_t best = 0;
+  for (int c = 0; c < kSplitChunks; ++c) {
+    uint64_t k = a.part_key[r * kSplitChunks + c];
+    best = k > best ? k : best;
+  }
+  if (a.greedy) return (int)fg::rank_key_index(best);
+  uint64_t total = 0;
+  for (int c = 0; c < kSplitChunks; ++c) total += a.part_sum[r * kSplitChunks + c];
+  if (total == 0) return (int)fg::rank_key_index(best);
+  const uint64_t target = fg::mulhi_u64_u32(total, u);
+  uint64_t before = 0;
+  int cs = kSplitChunks - 1;
+  for (int c = 0; c < kSplitChunks; ++c) {
+    const uint64_t ps = a.part_sum[r * kSplitChunks + c];
+    if (before + ps > target) {
+      cs = c;
+      break;
+    }
+    before += ps;
+  }
+  const int lo = cs * a.chunk;
+  Row<DT> rr;
+  rr.p = split_row<DT>(a, r) + (int64_t)lo * (DT == fg::kBF16 ? 2 : 4);
+  rr.V = min(a.vocab, lo + a.chunk) - lo;
+  rr.seg = (((rr.V + kWaves - 1) / kWaves) + kStep - 1) / kStep * kStep;
+  rr.scale = a.scale;
+  rr.T = a.temperature;
+  rr.m = split_row_max(a, r);
+  block_sum<true, DT>(rr, kAll, sh);
+  const int idx = block_locate<true, DT>(rr, kAll, target - before, sh);
+  return idx >= 0 ? lo + idx : (int)fg::rank_key_index(best);  // idx < 0 cannot happen: the chunk holds the target
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) split_sample_kernel(SplitArgs a, const uint32_t* __restrict__ noise,
+                                                                int noise_stride, int noise_col, uint64_t seed,
+                                                                uint64_t step, const int32_t* __restrict__ seq_ids,
+                                                                int draw, int32_t* __restrict__ out) {
+  __shared__ Shared sh;
+  const int r = blockIdx.x;
+  if (a.forced && a.forced[r] >= 0) {
+    if (threadIdx.x == 0) out[r] = a.forced[r];
+    return;
+  }
+  const uint32_t seq = seq_ids ? (uint32_t)seq_ids[r] : (uint32_t)r;
+  const uint32_t u = noise_value(noise, (int64_t)r * noise_stride + noise_col, seed, step, seq, (uint32_t)draw);
+  const int tok = split_pick<DT>(a, r, u, sh);
+  if (threadIdx.x == 0) out[r] = tok;
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) split_walk_kernel(
+    SplitArgs a, const int32_t* __restrict__ tree_tokens, const int32_t* __restrict__ parents,
+    const int32_t* __restrict__ n_nodes, int nmax, int batch, int walk_step, const uint32_t* __restrict__ noise,
+    int noise_stride, int noise_col0, uint64_t seed, uint64_t step, const int32_t* __restrict__ seq_ids, int draw0,
+    int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
+    int32_t* correction, int32_t* state, int32_t* err_flag) {
+  __shared__ Shared sh;
+  const int b = blockIdx.x;
+  if (!state[batch + b]) return;
+  const int parent = state[b];
+  const uint32_t seq = seq_ids ? (uint32_t)seq_ids[b] : (uint32_t)b;
+  const uint32_t u = noise_value(noise, (int64_t)b * noise_stride + noise_col0 + walk_step, seed, step, seq,
+                                 (uint32_t)(draw0 + walk_step));
+  const int tok = split_pick<DT>(a, b, u, sh);
+  if (threadIdx.x == 0)
+    walk_apply(b, tok, parent, tree_tokens, parents, n_nodes, nmax, batch, walk_step, acc_tokens, acc_nodes,
+               acc_stride, acc_len, last_node, correction, state, err_flag);
+}
+
+// Chunk partials of the split path: fills a.part_* (2 launches).
+template <int DT>
+void split_partials(const SplitArgs& a, int rows, hipStream_t s) {
+  dim3 grid(kSplitChunks, rows);
+  hipLaunchKernelGGL(split_max_kernel<DT>, grid, dim3(kSplitThreads), 0, s, a);
+  if (!a.greedy) hipLaunchKernelGGL(split_sum_kernel<DT>, grid, dim3(kSplitThreads), 0, s, a);
+}
+
+size_t split_workspace_bytes(int rows) { return (size_t)rows * kSplitChunks * (4 + 8 + 8) + 64; }
+
+// Carves the split partials out of a caller workspace; false when it is too small.
+bool split_setup(SplitArgs& a, void* workspace, size_t bytes, int rows, const void* logits, int64_t row_stride,
+                 int vocab, float temperature, int greedy) {
+  if (!workspace || bytes < split_workspace_bytes(rows)) return false;
+  char* w = (char*)(((uintptr_t)workspace + 15) & ~(uintptr_t)15);
+  a.part_key = (uint64_t*)w;
+  a.part_sum = a.part_key + (size_t)rows * kSplitChunks;
+  a.part_max = (float*)(a.part_sum + (size_t)rows * kSplitChunks);
+  a.logits = logits;
+  a.row_stride = row_stride;
+  a.vocab = vocab;
+  a.chunk = ((vocab + kSplitChunks - 1) / kSplitChunks + 7) / 8 * 8;
+  a.temperature = temperature;
+  a.greedy = greedy || temperature == 0.0f;
+  a.scale = !a.greedy && temperature > 0.0f && temperature != 1.0f;
+  a.row_index = nullptr;
+  a.forced = nullptr;
+  a.active = nullptr;
+  return true;
 }
 
 // Length clamp, EOS cut, finished flag and the b200 pending root.
@@ -445,11 +681,13 @@ SampleParams make_params(float temperature, int greedy, int top_k, int vocab, ui
 
 extern "C" {
 
+size_t fg_sample_workspace(int rows) { return rows > 0 ? split_workspace_bytes(rows) : 0; }
+
 int fg_sample_tokens(const void* logits, int dtype, int64_t row_stride, int rows, int vocab,
                      const int32_t* row_index, const int32_t* forced, const uint32_t* noise, int noise_stride,
                      int noise_col, uint64_t seed, uint64_t step, const int32_t* seq_ids, int draw,
                      float temperature, int greedy, int top_k, uint32_t top_p_fixed, int32_t* out_tokens,
-                     void* stream) {
+                     void* workspace, size_t workspace_bytes, void* stream) {
   FG_REQUIRE(logits && out_tokens, "fg_sample_tokens: null pointer");
   FG_REQUIRE(rows > 0 && vocab > 0 && vocab < (1 << 23), "fg_sample_tokens: vocab must be in [1, 2^23)");
   FG_REQUIRE(dtype == fg::kF32 || dtype == fg::kBF16, "fg_sample_tokens: dtype");
@@ -457,6 +695,22 @@ int fg_sample_tokens(const void* logits, int dtype, int64_t row_stride, int rows
              "fg_sample_tokens: rows must be 32-byte aligned (row_stride % 8 == 0)");
   SampleParams sp = make_params(temperature, greedy, top_k, vocab, top_p_fixed);
   hipStream_t s = (hipStream_t)stream;
+  SplitArgs a;
+  if ((sp.greedy || (sp.top_k == 0 && sp.tp32 == 0)) &&
+      split_setup(a, workspace, workspace_bytes, rows, logits, row_stride, vocab, temperature, sp.greedy)) {
+    a.row_index = row_index;
+    a.forced = forced;
+    if (dtype == fg::kBF16) {
+      split_partials<fg::kBF16>(a, rows, s);
+      hipLaunchKernelGGL(split_sample_kernel<fg::kBF16>, dim3(rows), dim3(kThreads), 0, s, a, noise, noise_stride,
+                         noise_col, seed, step, seq_ids, draw, out_tokens);
+    } else {
+      split_partials<fg::kF32>(a, rows, s);
+      hipLaunchKernelGGL(split_sample_kernel<fg::kF32>, dim3(rows), dim3(kThreads), 0, s, a, noise, noise_stride,
+                         noise_col, seed, step, seq_ids, draw, out_tokens);
+    }
+    return fg::check_launch("fg_sample_tokens");
+  }
   if (dtype == fg::kBF16)
     hipLaunchKernelGGL(sample_rows_kernel<fg::kBF16>, dim3(rows), dim3(kThreads), 0, s, logits, row_stride, vocab,
                        row_index, forced, noise, noise_stride, noise_col, seed, step, seq_ids, draw, sp, out_tokens);
@@ -524,7 +778,8 @@ int fg_walk_step(const void* step_logits, int dtype, int64_t row_stride, int voc
                  const uint32_t* noise, int noise_stride, int noise_col0, uint64_t seed, uint64_t step,
                  const int32_t* seq_ids, int draw0, float temperature, int greedy, int top_k, uint32_t top_p_fixed,
                  int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
-                 int32_t* correction, int32_t* state, int32_t* err_flag, void* stream) {
+                 int32_t* correction, int32_t* state, int32_t* err_flag, void* workspace, size_t workspace_bytes,
+                 void* stream) {
   FG_REQUIRE(step_logits && tree_tokens && parents && n_nodes && acc_tokens && acc_nodes && acc_len && last_node &&
                  correction && state,
              "fg_walk_step: null pointer");
@@ -535,6 +790,23 @@ int fg_walk_step(const void* step_logits, int dtype, int64_t row_stride, int voc
              "fg_walk_step: rows must be 32-byte aligned (row_stride % 8 == 0)");
   SampleParams sp = make_params(temperature, greedy, top_k, vocab, top_p_fixed);
   hipStream_t s = (hipStream_t)stream;
+  SplitArgs a;
+  if ((sp.greedy || (sp.top_k == 0 && sp.tp32 == 0)) &&
+      split_setup(a, workspace, workspace_bytes, batch, step_logits, row_stride, vocab, temperature, sp.greedy)) {
+    a.active = state + batch;
+    if (dtype == fg::kBF16) {
+      split_partials<fg::kBF16>(a, batch, s);
+      hipLaunchKernelGGL(split_walk_kernel<fg::kBF16>, dim3(batch), dim3(kThreads), 0, s, a, tree_tokens, parents,
+                         n_nodes, nmax, batch, walk_step, noise, noise_stride, noise_col0, seed, step, seq_ids, draw0,
+                         acc_tokens, acc_nodes, acc_stride, acc_len, last_node, correction, state, err_flag);
+    } else {
+      split_partials<fg::kF32>(a, batch, s);
+      hipLaunchKernelGGL(split_walk_kernel<fg::kF32>, dim3(batch), dim3(kThreads), 0, s, a, tree_tokens, parents,
+                         n_nodes, nmax, batch, walk_step, noise, noise_stride, noise_col0, seed, step, seq_ids, draw0,
+                         acc_tokens, acc_nodes, acc_stride, acc_len, last_node, correction, state, err_flag);
+    }
+    return fg::check_launch("fg_walk_step");
+  }
   if (dtype == fg::kBF16)
     hipLaunchKernelGGL(walk_step_kernel<fg::kBF16>, dim3(batch), dim3(kThreads), 0, s, step_logits, row_stride, vocab,
                        nullptr, tree_tokens, parents, n_nodes, nmax, batch, walk_step, 1, noise, noise_stride,

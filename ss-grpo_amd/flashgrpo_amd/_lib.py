@@ -35,14 +35,15 @@ SIGNATURES = {
     "fg_tree_attention": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I64, _I64, _I, _P, _P, _P, _I64, _F, _P]),
     "fg_rmsnorm": (_I, [_P, _P, _P, _P, _I, _I, _I, _F, _P]),
     "fg_swiglu": (_I, [_P, _P, _I, _I, _I, _P]),
+    "fg_sample_workspace": (_SZ, [_I]),
     "fg_sample_tokens": (_I, [_P, _I, _I64, _I, _I, _P, _P, _P, _I, _I, _U64, _U64, _P, _I, _F, _I, _I, _U32, _P,
-                              _P]),
+                              _P, _SZ, _P]),
     "fg_accept_walk": (_I, [_P, _I, _I64, _I, _P, _P, _P, _P, _I, _I, _I, _P, _I, _I, _U64, _U64, _P, _I, _F, _I, _I,
                             _U32, _P, _P, _I, _P, _P, _P, _P, _P, _P]),
     "fg_walk_begin": (_I, [_P, _P, _P, _I, _I, _P, _P, _I, _P, _P, _P, _P, _P]),
     "fg_walk_rows": (_I, [_P, _I, _I, _P, _P, _P]),
     "fg_walk_step": (_I, [_P, _I, _I64, _I, _P, _P, _P, _I, _I, _I, _P, _I, _I, _U64, _U64, _P, _I, _F, _I, _I, _U32,
-                          _P, _P, _I, _P, _P, _P, _P, _P, _P]),
+                          _P, _P, _I, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "fg_accept_finalize": (_I, [_P, _P, _I, _P, _P, _P, _P, _I, _I, _P, _P, _I, _P]),
     "fg_kv_path_gather": (_I, [_P, _I, _I, _I, _I, _I, _I64, _I64, _I64, _I, _P, _P, _P, _I, _P, _I, _P, _P]),
 }

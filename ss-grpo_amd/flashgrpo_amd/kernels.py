@@ -207,9 +207,16 @@ def swiglu(gate_up, *, out=None):
 
 
 # ------------------------------------------------------------------ sampling / acceptance
+def sample_workspace(rows, device):
+    """Scratch that lets unrestricted / greedy draws run split over several workgroups per row."""
+    n = _lib.load().fg_sample_workspace(int(rows))
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
 def sample_tokens(logits, *, noise=None, noise_col=0, seed=0, step=0, seq_ids=None, draw=0, row_index=None,
-                  forced=None, temperature=1.0, greedy=False, top_k=None, top_p=1.0, out=None):
-    """One token per row (see the rule in csrc/sample.hip). noise: uint32 bits as int32 [R, C]."""
+                  forced=None, temperature=1.0, greedy=False, top_k=None, top_p=1.0, out=None, split=True):
+    """One token per row (see the rule in csrc/sample.hip). noise: uint32 bits as int32 [R, C].
+    split=False keeps every row in one workgroup (same tokens; used to cross-check)."""
     _dev(logits, noise, seq_ids, row_index, forced)
     for t, n in ((seq_ids, "seq_ids"), (row_index, "row_index"), (forced, "forced")):
         _i32(t, n)
@@ -223,10 +230,11 @@ def sample_tokens(logits, *, noise=None, noise_col=0, seed=0, step=0, seq_ids=No
     T = 0.0 if temperature is None else float(temperature)
     use_T = T if T > 0 else (-1.0 if T < 0 or temperature is None else 0.0)
     g = bool(greedy) or (temperature is not None and T == 0.0)
+    ws = sample_workspace(rows, logits.device) if split else None
     _call("fg_sample_tokens", _ptr(logits), dtype_code(logits), logits.stride(0), rows,
               V, _ptr(row_index), _ptr(forced), _ptr(noise), noise.stride(0) if noise is not None else 0,
               int(noise_col), int(seed) & (2 ** 64 - 1), int(step), _ptr(seq_ids), int(draw), use_T, int(g),
-              int(top_k or 0), top_p_fixed(top_p), _ptr(out), _stream())
+              int(top_k or 0), top_p_fixed(top_p), _ptr(out), _ptr(ws), 0 if ws is None else ws.numel(), _stream())
     return out
 
 
@@ -274,7 +282,8 @@ def walk_begin(tree_tokens, parents, n_nodes, *, acc_stride):
              correction=torch.empty(B, dtype=torch.int32, device=dev),
              state=torch.empty(3 * B, dtype=torch.int32, device=dev),
              row_index=torch.empty(B, dtype=torch.int32, device=dev),
-             row_active=torch.empty(B, dtype=torch.int32, device=dev))
+             row_active=torch.empty(B, dtype=torch.int32, device=dev),
+             workspace=sample_workspace(B, dev))
     _call("fg_walk_begin", _ptr(tree_tokens), _ptr(parents), _ptr(n_nodes), nmax, B, _ptr(w["acc_tokens"]),
           _ptr(w["acc_nodes"]), acc_stride, _ptr(w["acc_len"]), _ptr(w["last_node"]), _ptr(w["correction"]),
           _ptr(w["state"]), _stream())
@@ -288,7 +297,8 @@ def walk_rows(walk, nmax):
 
 
 def walk_step(walk, step_logits, tree_tokens, parents, n_nodes, *, walk_step, noise=None, noise_col0=0, seed=0,
-              step=0, seq_ids=None, draw0=1, temperature=1.0, greedy=False, top_k=None, top_p=1.0, err_flag=None):
+              step=0, seq_ids=None, draw0=1, temperature=1.0, greedy=False, top_k=None, top_p=1.0, err_flag=None,
+              split=True):
     """One walk step: active row b draws from row b of step_logits."""
     _dev(step_logits, tree_tokens, parents, n_nodes, noise, seq_ids)
     B, nmax = tree_tokens.shape
@@ -302,7 +312,8 @@ def walk_step(walk, step_logits, tree_tokens, parents, n_nodes, *, walk_step, no
           int(seed) & (2 ** 64 - 1), int(step), _ptr(seq_ids), int(draw0), use_T, int(g), int(top_k or 0),
           top_p_fixed(top_p), _ptr(walk["acc_tokens"]), _ptr(walk["acc_nodes"]), walk["acc_tokens"].stride(0),
           _ptr(walk["acc_len"]), _ptr(walk["last_node"]), _ptr(walk["correction"]), _ptr(walk["state"]),
-          _ptr(err_flag), _stream())
+          _ptr(err_flag), _ptr(walk["workspace"]) if split else None, walk["workspace"].numel() if split else 0,
+          _stream())
 
 
 def accept_finalize(walk, old_len, *, max_length, eos_token_id, finished=None, pending_root=None):

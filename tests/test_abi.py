@@ -44,5 +44,6 @@ def test_library_loads_and_reports_errors_without_gpu_work():
     rc = lib.fg_kv_path_gather(None, 0, 0, 0, 0, 2, 0, 0, 0, 0, None, None, None, 0, None, 0, None, None)
     assert rc != 0 and b"null pointer" in lib.fg_last_error()
     rc = lib.fg_sample_tokens(ctypes.c_void_p(64), 1, 8, 1, 0, None, None, None, 0, 0, 0, 0, None, 0, 1.0, 0, 0, 0,
-                              ctypes.c_void_p(64), None)
+                              ctypes.c_void_p(64), None, 0, None)
     assert rc != 0 and b"vocab" in lib.fg_last_error()
+    assert lib.fg_sample_workspace(64) >= 64 * 16 * 20 and lib.fg_sample_workspace(0) == 0

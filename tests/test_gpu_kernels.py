@@ -190,6 +190,26 @@ def test_sample_tokens_bit_exact(dtype, mode):
         assert out.tolist() == want, (V, mode)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("mode", [{}, {"temperature": 0.7}, {"greedy": True}, {"temperature": 1.3}])
+def test_split_sampling_equals_single_workgroup(dtype, mode):
+    """Rows split over 16 workgroups (unrestricted / greedy draws) give the tokens of
+    the one-workgroup-per-row kernel, including flat rows, ties and short vocabularies."""
+    g = torch.Generator(device="cpu").manual_seed(23)
+    for V in (5, 37, 1000, 32000, 152064):
+        x = torch.randn(48, V, generator=g) * 2.0
+        x[0] = 0.0
+        x[1] = torch.round(x[1])
+        x[2, V // 3] = 30.0
+        xd = x.to(dtype).to(DEV)
+        for draw in range(3):
+            kw = dict(seed=99, step=draw, draw=draw, temperature=mode.get("temperature", 1.0),
+                      greedy=mode.get("greedy", False))
+            a = K().sample_tokens(xd, split=True, **kw)
+            b = K().sample_tokens(xd, split=False, **kw)
+            assert a.tolist() == b.tolist(), (V, mode, draw)
+
+
 def test_sample_tokens_full_vocab_and_counter_noise():
     g = torch.Generator(device="cpu").manual_seed(5)
     V = 152064
