@@ -21,8 +21,9 @@
 //    of the accumulators; 4-key groups of V^T row d are stored XOR-swizzled by
 //    (d >> 3) & 15, which keeps the staging writes and the fragment reads free
 //    of bank conflicts;
-//  * K/V tiles are double-buffered in LDS and the next tile's global loads are
-//    in flight during the current tile's MFMAs: one barrier per 64-key tile;
+//  * K/V tiles are double-buffered in LDS and staged through two register
+//    stages: the global loads of tile t+2 are issued before tile t is computed
+//    (two tiles in flight per workgroup), one barrier per 64-key tile;
 //  * the ancestor mask is evaluated only on tiles that reach the tree keys, and
 //    the running max (and the O rescale) only moves when a lane's max grows by
 //    more than 2^8, so after the first keys the rescale is almost never taken.
@@ -61,8 +62,6 @@ constexpr float kRescaleSlack = 8.0f;  // log2 units
 static_assert(kKT * kD / 8 == 2 * kThreads, "staging: two 16-byte K and V chunks per thread");
 
 FG_DEVICE int c_row32(int i, int lane) { return (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3); }
-
-FG_DEVICE uint32_t u4_word(const uint4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 
 // Keys key0 .. key0+63 of one row: key0 + j is allowed when it is a prefix key
 // (j < sh, sh = seq_len - key0) or tree node j - sh with its bit set in tree_bits.
@@ -124,39 +123,49 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
   // writes each V^T row as one 4-byte key pair.
   const int st_col = (tid & 15) * 8;
   const int st_row = tid >> 4;
-  // Named registers (not arrays) so the prefetch stays in VGPRs.
-  uint4 rk0, rk1, rv0, rv1;
-  auto load_tile = [&](int key0) {
-    const uint16_t* kp = kbase + st_col;
-    const uint16_t* vp = vbase + st_col;
-    rk0 = *(const uint4*)(kp + (int64_t)min(key0 + st_row, last_key) * kD);
-    rk1 = *(const uint4*)(kp + (int64_t)min(key0 + st_row + 32, last_key) * kD);
-    rv0 = *(const uint4*)(vp + (int64_t)min(key0 + 2 * st_row, last_key) * kD);
-    rv1 = *(const uint4*)(vp + (int64_t)min(key0 + 2 * st_row + 1, last_key) * kD);
-  };
+  // Two register stages (named 16-byte vectors, not arrays, so they stay in VGPRs):
+  // the loads of tile t+2 are issued before tile t is computed, so every tile's
+  // loads are in flight across two tile computations.
+  typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+  v4u ka0, ka1, va0, va1, kb0, kb1, vb0, vb1;
+#define FG_LOAD(K0, K1, V0, V1, KEY0)                                                      \
+  {                                                                                        \
+    const int key0_ = (KEY0);                                                              \
+    const uint16_t* kp_ = kbase + st_col;                                                  \
+    const uint16_t* vp_ = vbase + st_col;                                                  \
+    K0 = *(const v4u*)(kp_ + (int64_t)min(key0_ + st_row, last_key) * kD);                 \
+    K1 = *(const v4u*)(kp_ + (int64_t)min(key0_ + st_row + 32, last_key) * kD);            \
+    V0 = *(const v4u*)(vp_ + (int64_t)min(key0_ + 2 * st_row, last_key) * kD);             \
+    V1 = *(const v4u*)(vp_ + (int64_t)min(key0_ + 2 * st_row + 1, last_key) * kD);         \
+  }
   // V^T row d, key pair p (keys 2p, 2p+1) lives at word 2*((p >> 1) ^ ((d >> 3) & 15)) + (p & 1).
   const int vsw_word = 2 * ((st_row >> 1) ^ ((st_col >> 3) & 15)) + (st_row & 1);
-  auto store_tile = [&](int buf) {
-    uint16_t* kd = &Ks[buf][st_row * kKPitch + st_col];
-    *(uint4*)(kd) = rk0;
-    *(uint4*)(kd + 32 * kKPitch) = rk1;
-    uint32_t* vt = (uint32_t*)&Vt[buf][st_col * kVPitch] + vsw_word;
-#pragma unroll
-    for (int e2 = 0; e2 < 4; ++e2) {
-      const uint32_t w0 = u4_word(rv0, e2), w1 = u4_word(rv1, e2);
-      vt[(2 * e2) * (kVPitch / 2)] = __builtin_amdgcn_perm(w1, w0, 0x05040100u);      // element 2*e2
-      vt[(2 * e2 + 1) * (kVPitch / 2)] = __builtin_amdgcn_perm(w1, w0, 0x07060302u);  // element 2*e2+1
-    }
-  };
+#define FG_STORE(K0, K1, V0, V1, BUF)                                                      \
+  {                                                                                        \
+    uint16_t* kd_ = &Ks[BUF][st_row * kKPitch + st_col];                                   \
+    *(v4u*)(kd_) = K0;                                                                     \
+    *(v4u*)(kd_ + 32 * kKPitch) = K1;                                                      \
+    uint32_t* vt_ = (uint32_t*)&Vt[BUF][st_col * kVPitch] + vsw_word;                      \
+    _Pragma("unroll") for (int e2 = 0; e2 < 4; ++e2) {                                     \
+      vt_[(2 * e2) * (kVPitch / 2)] = __builtin_amdgcn_perm(V1[e2], V0[e2], 0x05040100u);     \
+      vt_[(2 * e2 + 1) * (kVPitch / 2)] = __builtin_amdgcn_perm(V1[e2], V0[e2], 0x07060302u); \
+    }                                                                                      \
+  }
 
-  const int ntiles = (total + kKT - 1) / kKT;
-  load_tile(0);
-  store_tile(0);
+  // An even number of tiles: a padding tile past the keys is fully masked (its
+  // loads re-read the last key) and leaves O and l unchanged.
+  const int ntiles = ((total + kKT - 1) / kKT + 1) & ~1;
+  FG_LOAD(ka0, ka1, va0, va1, 0)
+  FG_LOAD(kb0, kb1, vb0, vb1, kKT)
+  FG_STORE(ka0, ka1, va0, va1, 0)
   __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    const int key0 = t * kKT;
-    if (t + 1 < ntiles) load_tile(key0 + kKT);
+  for (int t0 = 0; t0 < ntiles; t0 += 2)
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int buf = h;
+    const int key0 = (t0 + h) * kKT;
+    if (h == 0) FG_LOAD(ka0, ka1, va0, va1, key0 + 2 * kKT)
+    else FG_LOAD(kb0, kb1, vb0, vb1, key0 + 2 * kKT)
 
     if (computes) {
       // S^T for two 32-key blocks.
@@ -238,9 +247,12 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
           }
       }
     }
-    if (t + 1 < ntiles) store_tile(buf ^ 1);
+    if (h == 0) FG_STORE(kb0, kb1, vb0, vb1, 1)
+    else FG_STORE(ka0, ka1, va0, va1, 0)
     __syncthreads();
   }
+#undef FG_LOAD
+#undef FG_STORE
 
   // Combine the two half-lanes' sums and write.
   float l = l_run + __shfl_xor(l_run, 32, 64);
