@@ -214,6 +214,30 @@ def summarize_trace(path, top=30):
         print(f"| {t / 1e3:.3f} | {100 * t / total:.1f} | {c} | {t / c:.1f} | {lo:.1f} | {hi:.1f} | `{short}` |")
 
 
+# Device symbol of each C-ABI entry point whose launches the roofline can name.
+KERNEL_SYMBOLS = {"fg_tree_attention": "tree_attn_bf16_kernel", "fg_lm_head": "gemm_bf16_stream",
+                  "fg_sample_tokens": "split_", "fg_kv_path_gather": "kv_path_gather_kernel"}
+
+
+def pmc_traffic(fetch_csv, write_csv, symbol, scale):
+    """Mean HBM bytes per dispatch of `symbol` from FETCH_SIZE / WRITE_SIZE counter CSVs
+    (KiB per dispatch, each scaled by what the counter reads for a copy of known size)."""
+    import csv
+
+    total = 0.0
+    for path, counter, k in ((fetch_csv, "FETCH_SIZE", scale[0]), (write_csv, "WRITE_SIZE", scale[1])):
+        with open(path, newline="") as fh:
+            rows = sorted(csv.DictReader(fh), key=lambda r: int(r["Dispatch_Id"]))
+        marks = [int(r["Dispatch_Id"]) for r in rows if "spin_kernel" in r["Kernel_Name"]]
+        lo, hi = (marks[-2], marks[-1]) if len(marks) >= 2 else (-1, 1 << 62)  # the timed rounds
+        vals = [float(r["Counter_Value"]) for r in rows
+                if lo < int(r["Dispatch_Id"]) < hi and symbol in r["Kernel_Name"] and r["Counter_Name"] == counter]
+        if not vals:
+            return None
+        total += sum(vals) / len(vals) * 1024.0 * k
+    return int(total)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -228,6 +252,10 @@ def main():
                     help="C-ABI entry point whose launches are event-timed in the timed rounds")
     ap.add_argument("--roofline-every", type=int, default=7,
                     help="event-time one launch in this many of the roofline kernel in the timed rounds")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE counter_collection CSVs of the roofline kernel")
+    ap.add_argument("--traffic-scale", nargs=2, type=float, default=(2.0, 1.0), metavar=("FETCH", "WRITE"),
+                    help="copy KiB per counter KiB, measured on a plain copy of known size (FETCH_SIZE, WRITE_SIZE)")
     ap.add_argument("--summarize-trace", metavar="CSV", help="summarise a rocprofv3 kernel trace of this command")
     args = ap.parse_args()
     if args.summarize_trace:
@@ -345,6 +373,9 @@ def main():
                         flops_per_launch=int(t["flops"] / n_launch), avg_launch_us=round(ks["avg_ms"] * 1e3, 2),
                         timed_launches=ks["count"], launches=t["launches"])
 
+    if args.traffic_from:
+        roofline["traffic"] = pmc_traffic(args.traffic_from[0], args.traffic_from[1],
+                                          KERNEL_SYMBOLS.get(name, name), args.traffic_scale)
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
