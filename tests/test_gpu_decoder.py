@@ -261,3 +261,18 @@ def test_tiny_config_32_rounds_fp32():
     # one token per round unless a rare Medusa candidate is accepted
     assert 28 <= st["rounds"] == out["total_verify_rounds"] <= 32
     assert out["last_tree_plan"]["topk_by_depth"] == [4, 2]
+
+
+def test_lockstep_bf16_7b_geometry():
+    """The 7B config's attention and vocabulary geometry (28/4 heads of 128, GQA 7,
+    vocab 152064, 4 Medusa heads, adaptive concurrency-aware plan with a 32-node
+    budget -> 29-node tree) on a 2-layer, 512-wide stack: 4 sequences in lockstep
+    with the oracle, bf16."""
+    cfg = OM.ModelConfig(num_layers=2, hidden=512, q_heads=28, kv_heads=4, head_dim=128, intermediate=1024,
+                         vocab=152064, rope_theta=1e6)
+    spec = OD.DecodeSpec(tree_mode="concurrency_aware", cpeak_nodes=128, max_tree_nodes_per_seq=32,
+                         fixed_tree_topk_by_depth=(4, 3, 2), num_medusa_heads=4, max_tree_depth=5,
+                         adaptive_tree_enabled=True, top_p=1.0)
+    out, st = _run(cfg, spec, dtype=torch.bfloat16, B0=2, repeats=2, P=40, max_length=40 + 6)
+    assert st["rounds"] == out["total_verify_rounds"] >= 3
+    assert out["last_tree_plan"]["node_budget_per_seq"] == 32
