@@ -671,8 +671,22 @@ int launch_gemm(const GemmArgs& g, int dtype, int out_dtype, int epi, int batch,
     FG_REQUIRE(g.lda % 8 == 0 && g.ldb % 8 == 0 && ((uintptr_t)g.A & 15) == 0 && ((uintptr_t)g.B & 15) == 0,
                "gemm: bf16 operands need 16-byte aligned rows");
     const bool wide_ok = g.N >= 512 && g.ldc % 4 == 0 && ((uintptr_t)g.C & 15) == 0 && (g.c_batch % 4) == 0;
-    if (stream_gemm_ok(g)) {
-      launch_stream_gemm(g, out_dtype, epi, batch, s);
+    GemmArgs head = g;
+    head.M = std::min(g.M, 256);
+    if (stream_gemm_ok(head) && g.M <= 4096) {
+      // 256-row slices, each streaming B once (the skinny kernel beats the
+      // square-tile one here even when the product is compute-bound).
+      const int es = out_dtype == fg::kBF16 ? 2 : 4;
+      for (int m0 = 0; m0 < g.M; m0 += 256) {
+        GemmArgs gc = g;
+        gc.M = std::min(256, g.M - m0);
+        if (g.a_rows) gc.a_rows = g.a_rows + m0;
+        else gc.A = (const uint16_t*)g.A + (int64_t)m0 * g.lda;
+        if (g.row_active) gc.row_active = g.row_active + m0;
+        gc.C = (char*)g.C + (int64_t)m0 * g.ldc * es;
+        if (g.R) gc.R = (const char*)g.R + (int64_t)m0 * g.ldr * (g.r_dtype == fg::kBF16 ? 2 : 4);
+        launch_stream_gemm(gc, out_dtype, epi, batch, s);
+      }
     } else if (wide_ok) {
       // Pick the M tile that pads M least (larger tile on ties).
       const int cands[3] = {192, 128, 64};
