@@ -50,6 +50,10 @@ WORKLOADS = {
     "14b": dict(target="qwen25_14b", prompts=16, repeats=8, prefix=4096, heads=4, tree_mode="concurrency_aware",
                 cpeak=8192, max_nodes=64, max_depth=5, topk=(4, 3, 2), adaptive=False, temperature=1.0,
                 name="qwen2.5-14b-shape B128 P4096 4 Medusa heads 64-node tree"),
+    "8b": dict(target="llama31_8b", prompts=12, repeats=8, prefix=1024, heads=4, tree_mode="concurrency_aware",
+               cpeak=4608, max_nodes=48, max_depth=5, topk=(4, 3, 2), adaptive=True, temperature=0.7,
+               proposal="chain", conf_low=0.20, conf_high=0.70,
+               name="llama-3.1-8b-shape B96 P1024 chain proposals (Medusa head 1 + ChainDraftCell) 48-node tree"),
     "tiny": dict(target="tiny", prompts=4, repeats=2, prefix=256, heads=3, tree_mode="fixed", cpeak=64,
                  max_nodes=16, max_depth=4, topk=(4, 3, 2), adaptive=False, temperature=1.0,
                  name="tiny-qwen2 B8 P256 3 Medusa heads fixed 16-node tree"),
@@ -74,7 +78,9 @@ def build(work, dtype, seed=0):
                              max_tree_nodes_per_seq=work["max_nodes"], max_tree_depth=work["max_depth"],
                              fixed_tree_topk_by_depth=tuple(work["topk"]), adaptive_tree_enabled=work["adaptive"],
                              adaptive_min_topk_by_depth=(1, 1, 1), temperature=work["temperature"], top_p=work["top_p"],
-                             noise_seed=seed + 2)
+                             noise_seed=seed + 2, proposal_mode=work.get("proposal", "medusa"),
+                             adaptive_confidence_low=work.get("conf_low", 0.15),
+                             adaptive_confidence_high=work.get("conf_high", 0.45))
     return cfg, model, heads, FlashMedusaDecoder(model, heads, _NoEosTokenizer(), dcfg)
 
 
@@ -87,6 +93,7 @@ def algorithmic_work(cfg, rnd, seq_before, elem):
     attn_bytes = 2 * Hkv * keys * d * elem + 2 * B * N * Hq * d * elem       # one layer: K, V, Q in, O out
     attn_flops = 4 * Hq * N * d * keys                                          # one layer: QK^T and PV
     draws = int(rnd["walk_draws"].sum())
+    chain = rnd.get("chain_rows") or []
     w = {
         "fg_tree_attention": dict(bytes=L * attn_bytes, flops=L * attn_flops, launches=L),
         "fg_lm_head:medusa": dict(flops=2 * nh * B * H * V, bytes=H * V * elem + nh * B * (H + V) * elem, launches=1),
@@ -95,6 +102,15 @@ def algorithmic_work(cfg, rnd, seq_before, elem):
         "fg_sample_tokens": dict(bytes=B * V * elem, launches=1),
         "fg_kv_path_gather": dict(bytes=2 * L * 2 * Hkv * int(rnd["acc_len"].sum()) * d * elem, launches=1),
     }
+    if chain:
+        # chain proposals: one LM-head launch and one top-k launch per depth over every
+        # parent state; the bootstrap state is Medusa head 0 alone
+        R = sum(chain)
+        del w["fg_lm_head:medusa"]
+        w["fg_lm_head:chain"] = dict(flops=2 * R * H * V, bytes=len(chain) * H * V * elem + R * (H + V) * elem,
+                                     launches=len(chain))
+        w["fg_medusa_heads"] = dict(flops=2 * B * H * H, bytes=H * H * elem, launches=1)
+        w["fg_medusa_topk"] = dict(bytes=R * V * elem, launches=len(chain))
     if rnd.get("lazy"):
         # one launch per walk step; a step with an active row streams the whole LM-head
         # weight once, a step with none skips every tile
@@ -138,6 +154,11 @@ def cpu_baseline(model, heads, r, work, seed, layers=2):
                             "up_w": gu[cfg.intermediate:], "down_w": f(lw["down_w"])})
     hd = [{"ln_w": f(h.norm.weight), "ln_b": f(h.norm.bias),
            "fc_w": f(h.fc.weight.to(model.dtype)), "fc_b": f(h.fc.bias.to(model.dtype))} for h in heads.heads]
+    cc = heads.chain_cell
+    g = lambda t: f(t.to(model.dtype))
+    cell = {"sn_w": g(cc.state_norm.weight), "sn_b": g(cc.state_norm.bias), "tn_w": g(cc.token_norm.weight),
+            "tn_b": g(cc.token_norm.bias), "sp_w": g(cc.state_proj.weight), "tp_w": g(cc.token_proj.weight),
+            "op_w": g(cc.out_proj.weight), "op_b": g(cc.out_proj.bias), "gate": float(cc.gate.detach())}
     ocfg = OM.ModelConfig(nl, cfg.hidden, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.intermediate, cfg.vocab,
                           cfg.rope_theta, cfg.rms_eps, cfg.qkv_bias, cfg.tie_word_embeddings)
     cap = int(r.seq_h.max()) + 72
@@ -149,7 +170,10 @@ def cpu_baseline(model, heads, r, work, seed, layers=2):
     spec = OD.DecodeSpec(num_medusa_heads=work["heads"], tree_mode=work["tree_mode"], cpeak_nodes=work["cpeak"],
                          max_tree_nodes_per_seq=work["max_nodes"], max_tree_depth=work["max_depth"],
                          fixed_tree_topk_by_depth=tuple(work["topk"]), adaptive_tree_enabled=work["adaptive"],
-                         temperature=work["temperature"], top_p=work["top_p"])
+                         temperature=work["temperature"], top_p=work["top_p"],
+                         proposal_mode=work.get("proposal", "medusa"),
+                         adaptive_confidence_low=work.get("conf_low", 0.15),
+                         adaptive_confidence_high=work.get("conf_high", 0.45))
     threads = len(os.sched_getaffinity(0))
     try:
         from threadpoolctl import threadpool_info
@@ -159,7 +183,7 @@ def cpu_baseline(model, heads, r, work, seed, layers=2):
     except Exception:
         pass
     t0 = time.perf_counter()
-    out = OD.verify_round(ocfg, W, hd, st, spec, seed, 0, 10 ** 9, dtype=np.float32)
+    out = OD.verify_round(ocfg, W, hd, st, spec, seed, 0, 10 ** 9, dtype=np.float32, cell=cell)
     t_round = time.perf_counter() - t0
     tree = out["trees"][0]
     B, N = len(r.active), tree.node_count

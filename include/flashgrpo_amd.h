@@ -63,9 +63,12 @@ int fg_lm_head(const void* x, int dtype, int M, int K, int64_t ldx, const int32_
 /* Per-row top-kmax candidates, ranked (value desc, index asc).
  * logits [rows, vocab] with row stride row_stride (multiple of 8, 32-byte aligned base).
  * cand_tokens/cand_scores [rows, kmax]; row_stats (optional) [rows, 2] = (max, logsumexp).
+ * sanitize != 0 ranks (and scores) nan_to_num(x, nan=-1e9, posinf=1e9, neginf=-1e9), the
+ * chain builder's logits (decoding/flash_medusa_decoder.py:477-482); 0 ranks NaN first,
+ * as torch.topk does (the Medusa path, decoding/medusa_tree.py:239-252).
  * workspace >= fg_medusa_topk_workspace(rows, vocab, kmax). */
 size_t fg_medusa_topk_workspace(int rows, int vocab, int kmax);
-int fg_medusa_topk(const void* logits, int dtype, int64_t row_stride, int rows, int vocab, int kmax,
+int fg_medusa_topk(const void* logits, int dtype, int64_t row_stride, int rows, int vocab, int kmax, int sanitize,
                    int32_t* cand_tokens, float* cand_scores, float* row_stats, void* workspace,
                    size_t workspace_bytes, void* stream);
 

@@ -43,6 +43,9 @@ class DecodeSpec:
     top_k: int | None = None
     emit_correction_token: bool = False
     eos_token_id: int = -1
+    adaptive_confidence_metric: str = "top1_prob"
+    proposal_mode: str = "medusa"
+    chain_bootstrap_from_medusa: bool = True
 
 
 def plan_for(spec: DecodeSpec, batch: int) -> OT.Plan:
@@ -75,6 +78,71 @@ def adapt_plan(spec: DecodeSpec, plan: OT.Plan, medusa_logits) -> OT.Plan:
     return OT.Plan(plan.node_budget_per_seq, len(ks), ks, OT.dense_node_count(ks), plan.mode, plan.layout)
 
 
+def chain_confidence(logits, metric="top1_prob"):
+    """Per-row confidence of sanitised logits (``flash_medusa_decoder.py:317-339``):
+    exp(max - logsumexp) or top1 - top2; non-finite scores become 0."""
+    x = OT.nan_to_num_logits(logits).astype(np.float64)
+    if metric == "margin":
+        if x.shape[-1] == 1:
+            score = x[:, 0]
+        else:
+            top2 = -np.sort(-x, axis=-1)[:, :2]
+            score = top2[:, 0] - top2[:, 1]
+    else:
+        m = x.max(axis=-1)
+        lse = m + np.log(np.exp(x - m[:, None]).sum(axis=-1))
+        score = np.exp(m - lse)
+    return np.nan_to_num(score, nan=0.0, posinf=0.0, neginf=0.0)
+
+
+def chain_proposals(spec: DecodeSpec, plan: OT.Plan, hidden, roots, heads, cell, embed, lm_head, dtype=np.float64,
+                    logits_hook=None):
+    """Chain-mode trees (``flash_medusa_decoder.py:435-539``).
+
+    The first parent state is Medusa head 0's residual output of the hidden state
+    (``chain_bootstrap_from_medusa``) or the chain cell applied to (hidden, root
+    embedding). Depth d projects every parent state through the LM head, takes the
+    confidence quantile over all of them, maps it to k_d (no budget refit), adds the
+    children and advances each child's state with the chain cell on its token's
+    embedding. ``logits_hook(d, states)`` may replace the logits computed for depth d
+    (the lockstep tests feed in the device's values). Returns
+    (trees, chain plan, confidences, per-depth records of states, logits, k,
+    parent_index, tokens).
+    """
+    B = len(roots)
+    if spec.chain_bootstrap_from_medusa and heads:
+        states = OM.medusa_project(hidden, heads[0], dtype)
+    else:
+        states = OM.chain_cell(hidden, np.asarray(embed)[np.asarray(roots)], cell, dtype)
+    trees = [OT.Tree([int(r)], [-1], [1], [0.0]) for r in roots]
+    cur = [[0] for _ in range(B)]
+    adapted, confs, recs = [], [], []
+    for d, base_k in enumerate(plan.topk_by_depth):
+        if states.shape[0] == 0:
+            break
+        lg = OM.logits(states, lm_head, dtype).astype(np.float32) if logits_hook is None else logits_hook(d, states)
+        conf = OT.quantile_linear(chain_confidence(lg, spec.adaptive_confidence_metric),
+                                  min(1.0, max(0.0, spec.adaptive_confidence_quantile)))
+        confs.append(conf)
+        k = OT.topk_from_confidence(conf, base_k, d, enabled=spec.adaptive_tree_enabled,
+                                    min_topk_by_depth=spec.adaptive_min_topk_by_depth,
+                                    low=spec.adaptive_confidence_low, high=spec.adaptive_confidence_high)
+        rec = dict(states=states, logits=lg, k=k)
+        recs.append(rec)
+        if k <= 0:
+            break
+        adapted.append(k)
+        cur, pidx, toks = OT.chain_add_children(trees, cur, lg, k, d, plan.node_budget_per_seq)
+        rec.update(parent_index=pidx, tokens=toks)
+        if not toks:
+            break
+        states = OM.chain_cell(np.asarray(states)[pidx], np.asarray(embed)[toks], cell, dtype)
+    ks = [max(1, int(k)) for k in adapted]
+    chain_plan = OT.Plan(plan.node_budget_per_seq, len(ks), ks, max(t.node_count for t in trees), plan.mode,
+                         plan.layout)
+    return trees, chain_plan, confs, recs
+
+
 @dataclass
 class State:
     k: list                  # per layer [B, Hkv, capacity, d]
@@ -101,8 +169,9 @@ def prefill_state(cfg, W, prompts, capacity, dtype=np.float64) -> State:
 
 
 def verify_round(cfg, W, heads, st: State, spec: DecodeSpec, seed: int, rnd: int, max_length: int,
-                 dtype=np.float64) -> dict:
-    """One round; mutates ``st`` and returns what it decided."""
+                 dtype=np.float64, cell=None) -> dict:
+    """One round; mutates ``st`` and returns what it decided. ``cell`` holds the chain
+    cell weights when ``spec.proposal_mode == "chain"``."""
     B = st.seq_len.shape[0]
     L = cfg.num_layers
     greedy = (not spec.do_sample) or spec.temperature == 0
@@ -111,10 +180,16 @@ def verify_round(cfg, W, heads, st: State, spec: DecodeSpec, seed: int, rnd: int
                       OS.sample_row(st.logits[b], OS.counter_noise(seed, rnd, int(st.seq_ids[b]), 0), **kw)
                       for b in range(B)], np.int64)
     plan = plan_for(spec, B)
-    mlog = OM.medusa_logits(st.hidden, heads, W["lm_head"], plan.active_heads, dtype) if plan.active_heads else []
-    mlog = [np.asarray(x, np.float32) for x in mlog]
-    plan = adapt_plan(spec, plan, mlog)
-    trees = OT.build_batch_trees(roots, mlog, plan)
+    if spec.proposal_mode == "chain" and plan.active_heads:
+        mlog = []
+        trees, plan, _, chain = chain_proposals(spec, plan, st.hidden, roots, heads, cell, W["embed"], W["lm_head"],
+                                                dtype)
+    else:
+        chain = None
+        mlog = OM.medusa_logits(st.hidden, heads, W["lm_head"], plan.active_heads, dtype) if plan.active_heads else []
+        mlog = [np.asarray(x, np.float32) for x in mlog]
+        plan = adapt_plan(spec, plan, mlog)
+        trees = OT.build_batch_trees(roots, mlog, plan)
     N = trees[0].node_count
     parents = trees[0].parents
     depths = trees[0].depths
@@ -131,7 +206,7 @@ def verify_round(cfg, W, heads, st: State, spec: DecodeSpec, seed: int, rnd: int
             s = int(st.seq_len[b])
             st.k[li][b, :, s:s + N] = nk[li][b]
             st.v[li][b, :, s:s + N] = nv[li][b]
-    out = dict(roots=roots, plan=plan, trees=trees, tree_hidden=hid, medusa_logits=mlog)
+    out = dict(roots=roots, plan=plan, trees=trees, tree_hidden=hid, medusa_logits=mlog, chain=chain)
     if N > 1:
         rows, nodes, slots = OT.internal_slots(trees)
         packed = OM.logits(hid[rows, nodes], W["lm_head"], dtype).astype(np.float32)
@@ -166,7 +241,7 @@ def verify_round(cfg, W, heads, st: State, spec: DecodeSpec, seed: int, rnd: int
     return out
 
 
-def generate(cfg, W, heads, prompts, spec: DecodeSpec, *, max_length, seed, repeats=1, dtype=np.float64):
+def generate(cfg, W, heads, prompts, spec: DecodeSpec, *, max_length, seed, repeats=1, dtype=np.float64, cell=None):
     """Whole loop for full-length prompts; returns the generated token lists."""
     prompts = np.repeat(np.asarray(prompts), repeats, axis=0)
     B = prompts.shape[0]
@@ -176,7 +251,7 @@ def generate(cfg, W, heads, prompts, spec: DecodeSpec, *, max_length, seed, repe
     active = np.arange(B)
     rnd = 0
     while active.size:
-        out = verify_round(cfg, W, heads, st, spec, seed, rnd, max_length, dtype)
+        out = verify_round(cfg, W, heads, st, spec, seed, rnd, max_length, dtype, cell=cell)
         for i, b in enumerate(active):
             gen[b].extend(out["acc_tokens"][i])
         keep = ~out["finished"]

@@ -142,6 +142,29 @@ def medusa_logits(hidden, heads, lm_head, max_heads=None, dtype=F64):
     return [medusa_project(hidden, heads[i], dtype) @ W.T for i in range(n)]
 
 
+def random_chain_cell(hidden: int, seed: int, std: float = 0.02, bottleneck_ratio: int = 8, gate_init: float = -3.0,
+                      dtype=np.float32) -> dict:
+    """ChainDraftCell weights (``flashgrpo/models/medusa_heads.py:12-35``): LayerNorms identity,
+    projections ~ N(0, std). The reference zero-initialises out_proj, which makes the
+    cell the identity; synthetic runs draw it ~ N(0, std) as well."""
+    rng = np.random.default_rng(seed)
+    bott = max(64, hidden // max(1, bottleneck_ratio))
+    n = lambda *shape: (rng.standard_normal(shape, dtype=np.float32) * std).astype(dtype)
+    return {"sn_w": np.ones(hidden, dtype), "sn_b": np.zeros(hidden, dtype), "tn_w": np.ones(hidden, dtype),
+            "tn_b": np.zeros(hidden, dtype), "sp_w": n(bott, hidden), "tp_w": n(bott, hidden), "op_w": n(hidden, bott),
+            "op_b": n(hidden), "gate": np.float32(gate_init)}
+
+
+def chain_cell(state, token_embedding, cell, dtype=F64):
+    """state + sigmoid(gate) * out(SiLU(Ps . LN(state) + Pt . LN(emb))).
+    Follows ``flashgrpo/models/medusa_heads.py:37-42`` (LayerNorm eps 1e-5)."""
+    s = np.asarray(state, dtype)
+    mixed = (layernorm(s, cell["sn_w"], cell["sn_b"]).astype(dtype) @ np.asarray(cell["sp_w"], dtype).T
+             + layernorm(token_embedding, cell["tn_w"], cell["tn_b"]).astype(dtype) @ np.asarray(cell["tp_w"], dtype).T)
+    delta = silu(mixed) @ np.asarray(cell["op_w"], dtype).T + np.asarray(cell["op_b"], dtype)
+    return s + (1.0 / (1.0 + np.exp(-np.float64(cell["gate"])))) * delta
+
+
 # --------------------------------------------------------------------------- decoder
 def forward(cfg: ModelConfig, W: dict, tokens, positions, past_k, past_v, past_valid, self_allowed,
             fp32_angles=True, dtype=F64):

@@ -350,3 +350,62 @@ def ancestor_bits(parents):
             p = parents[p]
         out.append(m)
     return out
+
+
+def nan_to_num_logits(x):
+    """The chain-mode sanitising of ``flash_medusa_decoder.py:477-482`` (fp32; NaN -> -1e9,
+    +inf -> 1e9, -inf -> -1e9)."""
+    return np.nan_to_num(np.asarray(x, np.float32), nan=-1.0e9, posinf=1.0e9, neginf=-1.0e9)
+
+
+def chain_add_children(trees, cur, logits, k, depth_idx, budget):
+    """One depth of the chain builder (``flash_medusa_decoder.py:488-521``).
+
+    cur[b] lists the node ids of row b's current parents; logits[b * n_d + j] is the
+    (unsanitised) logits row of parent j of row b, n_d = len(cur[b]). Each parent in
+    order receives its top-k children (canonical order) while its row holds fewer than
+    `budget` nodes. Returns (next cur, parent_index, tokens): parent_index and tokens
+    list the new nodes in creation order (row-major), parent_index as rows of logits.
+    """
+    lg = nan_to_num_logits(logits)
+    B = len(trees)
+    n_d = len(cur[0]) if B else 0
+    nxt = [[] for _ in range(B)]
+    pidx, toks = [], []
+    for b in range(B):
+        t = trees[b]
+        for j, pn in enumerate(cur[b]):
+            if t.node_count >= budget:
+                break
+            ids, vals = topk_canonical(lg[b * n_d + j], min(int(k), lg.shape[-1]))
+            for tok, val in zip(ids, vals):
+                if t.node_count >= budget:
+                    break
+                t.tokens.append(int(tok))
+                t.parents.append(pn)
+                t.depths.append(depth_idx + 2)
+                t.scores.append(float(val))
+                nxt[b].append(t.node_count - 1)
+                pidx.append(b * n_d + j)
+                toks.append(int(tok))
+    return nxt, pidx, toks
+
+
+def build_chain_trees(roots, chain_logits, topk_by_depth, budget):
+    """Chain-mode candidate trees (``flash_medusa_decoder.py:435-539``) from given
+    per-depth logits: chain_logits[d] is [B * n_d, V], the parent states of depth d in
+    creation order (row-major over sequences, then node order). Returns
+    (trees, parent_index, tokens) with the per-depth lists of chain_add_children.
+    """
+    trees = [Tree([int(r)], [-1], [1], [0.0]) for r in roots]
+    cur = [[0] for _ in roots]
+    parent_index, tokens = [], []
+    for d, k in enumerate(topk_by_depth):
+        if d >= len(chain_logits) or int(k) <= 0:
+            break
+        cur, pidx, toks = chain_add_children(trees, cur, chain_logits[d], k, d, budget)
+        if not pidx:
+            break
+        parent_index.append(pidx)
+        tokens.append(toks)
+    return trees, parent_index, tokens

@@ -11,6 +11,11 @@
 // sum of exp for the row's log-sum-exp); lists merge across the wave with the
 // bitonic "max(A[i], B[K-1-i]) then sort" step, then across waves in LDS.
 // Phase 2: one wave per row merges the chunk lists.
+//
+// With `sanitize` the values are first mapped as torch.nan_to_num(x.float(),
+// nan=-1e9, posinf=1e9, neginf=-1e9) does before the chain builder's top-k
+// (flashgrpo/decoding/flash_medusa_decoder.py:477-482); without it NaN ranks
+// above every number, as in torch.topk.
 #include "fg_common.h"
 
 #include <algorithm>
@@ -74,6 +79,16 @@ FG_DEVICE void wave_merge(uint64_t (&top)[K]) {
   }
 }
 
+template <bool SAN>
+FG_DEVICE float sanitize(float v) {
+  if constexpr (SAN) {
+    if (v != v) return -1.0e9f;
+    if (v == INFINITY) return 1.0e9f;
+    if (v == -INFINITY) return -1.0e9f;
+  }
+  return v;
+}
+
 struct LseAcc {
   float m, s;
 };
@@ -84,7 +99,7 @@ FG_DEVICE LseAcc lse_combine(LseAcc a, LseAcc b) {
   return {m, a.s * __expf(a.m - m) + b.s * __expf(b.m - m)};
 }
 
-template <int DT, int K, bool STATS>
+template <int DT, int K, bool STATS, bool SAN>
 __global__ void __launch_bounds__(kThreads) topk_phase1(const void* __restrict__ logits, int64_t row_stride,
                                                         int vocab, int chunk, uint64_t* __restrict__ part_keys,
                                                         float2* __restrict__ part_lse) {
@@ -104,6 +119,8 @@ __global__ void __launch_bounds__(kThreads) topk_phase1(const void* __restrict__
     float v[8];
     fg::load8<DT>(rowp, i, v);
 #pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = sanitize<SAN>(v[j]);
+#pragma unroll
     for (int j = 0; j < 8; ++j) insert_key<K>(top, fg::rank_key(v[j], (uint32_t)(i + j)));
     if constexpr (STATS) {
       float m8 = v[0];
@@ -117,7 +134,7 @@ __global__ void __launch_bounds__(kThreads) topk_phase1(const void* __restrict__
     }
   }
   for (int i = vec_hi + threadIdx.x; i < hi; i += kThreads) {
-    float v = fg::load_elem<DT>(rowp, i);
+    float v = sanitize<SAN>(fg::load_elem<DT>(rowp, i));
     insert_key<K>(top, fg::rank_key(v, (uint32_t)i));
     if constexpr (STATS) acc = lse_combine(acc, LseAcc{v, 1.0f});
   }
@@ -198,9 +215,13 @@ __global__ void __launch_bounds__(64) topk_phase2(const uint64_t* __restrict__ p
 
 template <int DT, int K, bool STATS>
 void launch_topk(const void* logits, int64_t row_stride, int rows, int vocab, int chunks, int chunk, int kout,
-                 uint64_t* part_keys, float2* part_lse, int32_t* tok, float* score, float* stats,
+                 uint64_t* part_keys, float2* part_lse, int32_t* tok, float* score, float* stats, bool san,
                  hipStream_t stream) {
-  hipLaunchKernelGGL((topk_phase1<DT, K, STATS>), dim3(rows, chunks), dim3(kThreads), 0, stream, logits, row_stride,
+  if (san)
+    hipLaunchKernelGGL((topk_phase1<DT, K, STATS, true>), dim3(rows, chunks), dim3(kThreads), 0, stream, logits,
+                       row_stride, vocab, chunk, part_keys, part_lse);
+  else
+    hipLaunchKernelGGL((topk_phase1<DT, K, STATS, false>), dim3(rows, chunks), dim3(kThreads), 0, stream, logits, row_stride,
                      vocab, chunk, part_keys, part_lse);
   hipLaunchKernelGGL((topk_phase2<K, STATS>), dim3(rows), dim3(64), 0, stream, part_keys, part_lse, chunks, kout, tok,
                      score, stats);
@@ -208,13 +229,13 @@ void launch_topk(const void* logits, int64_t row_stride, int rows, int vocab, in
 
 template <int DT, bool STATS>
 void dispatch_k(int K, const void* logits, int64_t row_stride, int rows, int vocab, int chunks, int chunk, int kout,
-                uint64_t* pk, float2* pl, int32_t* tok, float* score, float* stats, hipStream_t s) {
+                uint64_t* pk, float2* pl, int32_t* tok, float* score, float* stats, bool san, hipStream_t s) {
   switch (K) {
-    case 1: launch_topk<DT, 1, STATS>(logits, row_stride, rows, vocab, chunks, chunk, kout, pk, pl, tok, score, stats, s); break;
-    case 2: launch_topk<DT, 2, STATS>(logits, row_stride, rows, vocab, chunks, chunk, kout, pk, pl, tok, score, stats, s); break;
-    case 4: launch_topk<DT, 4, STATS>(logits, row_stride, rows, vocab, chunks, chunk, kout, pk, pl, tok, score, stats, s); break;
-    case 8: launch_topk<DT, 8, STATS>(logits, row_stride, rows, vocab, chunks, chunk, kout, pk, pl, tok, score, stats, s); break;
-    default: launch_topk<DT, 16, STATS>(logits, row_stride, rows, vocab, chunks, chunk, kout, pk, pl, tok, score, stats, s); break;
+    case 1: launch_topk<DT, 1, STATS>(logits, row_stride, rows, vocab, chunks, chunk, kout, pk, pl, tok, score, stats, san, s); break;
+    case 2: launch_topk<DT, 2, STATS>(logits, row_stride, rows, vocab, chunks, chunk, kout, pk, pl, tok, score, stats, san, s); break;
+    case 4: launch_topk<DT, 4, STATS>(logits, row_stride, rows, vocab, chunks, chunk, kout, pk, pl, tok, score, stats, san, s); break;
+    case 8: launch_topk<DT, 8, STATS>(logits, row_stride, rows, vocab, chunks, chunk, kout, pk, pl, tok, score, stats, san, s); break;
+    default: launch_topk<DT, 16, STATS>(logits, row_stride, rows, vocab, chunks, chunk, kout, pk, pl, tok, score, stats, san, s); break;
   }
 }
 
@@ -250,7 +271,7 @@ size_t fg_medusa_topk_workspace(int rows, int vocab, int kmax) {
   return (size_t)rows * chunks * (16 * sizeof(uint64_t) + sizeof(float2)) + 256;
 }
 
-int fg_medusa_topk(const void* logits, int dtype, int64_t row_stride, int rows, int vocab, int kmax,
+int fg_medusa_topk(const void* logits, int dtype, int64_t row_stride, int rows, int vocab, int kmax, int sanitize,
                    int32_t* cand_tokens, float* cand_scores, float* row_stats, void* workspace,
                    size_t workspace_bytes, void* stream) {
   FG_REQUIRE(logits && cand_tokens && cand_scores && workspace, "fg_medusa_topk: null pointer");
@@ -272,11 +293,11 @@ int fg_medusa_topk(const void* logits, int dtype, int64_t row_stride, int rows, 
   hipStream_t s = (hipStream_t)stream;
   bool stats = row_stats != nullptr;
   if (dtype == fg::kBF16) {
-    if (stats) dispatch_k<fg::kBF16, true>(K, logits, row_stride, rows, vocab, chunks, chunk, kmax, pk, pl, cand_tokens, cand_scores, row_stats, s);
-    else dispatch_k<fg::kBF16, false>(K, logits, row_stride, rows, vocab, chunks, chunk, kmax, pk, pl, cand_tokens, cand_scores, row_stats, s);
+    if (stats) dispatch_k<fg::kBF16, true>(K, logits, row_stride, rows, vocab, chunks, chunk, kmax, pk, pl, cand_tokens, cand_scores, row_stats, sanitize != 0, s);
+    else dispatch_k<fg::kBF16, false>(K, logits, row_stride, rows, vocab, chunks, chunk, kmax, pk, pl, cand_tokens, cand_scores, row_stats, sanitize != 0, s);
   } else {
-    if (stats) dispatch_k<fg::kF32, true>(K, logits, row_stride, rows, vocab, chunks, chunk, kmax, pk, pl, cand_tokens, cand_scores, row_stats, s);
-    else dispatch_k<fg::kF32, false>(K, logits, row_stride, rows, vocab, chunks, chunk, kmax, pk, pl, cand_tokens, cand_scores, row_stats, s);
+    if (stats) dispatch_k<fg::kF32, true>(K, logits, row_stride, rows, vocab, chunks, chunk, kmax, pk, pl, cand_tokens, cand_scores, row_stats, sanitize != 0, s);
+    else dispatch_k<fg::kF32, false>(K, logits, row_stride, rows, vocab, chunks, chunk, kmax, pk, pl, cand_tokens, cand_scores, row_stats, sanitize != 0, s);
   }
   return fg::check_launch("fg_medusa_topk");
 }

@@ -8,6 +8,9 @@ included). One verify round, per active sequence:
   Medusa proposals     fg_medusa_heads -> fg_lm_head -> fg_medusa_topk (+ row stats)
   plan / tree          plan_tree (host), adaptive refit from per-head confidence
                        quantiles, cached TreeTopology, fg_tree_layout
+  chain proposals      (proposal_mode="chain") per depth: fg_lm_head over every parent
+                       state -> fg_medusa_topk (sanitised, + row stats) -> children
+                       in dense-BFS order under the budget -> ChainDraftCell step
   tree verify          TargetModel.forward (tree attention with ancestor bit masks)
   acceptance           lazy (default): per walk step t, fg_walk_rows -> fg_lm_head over
                        the node each row samples from -> fg_walk_step (draw 1+t);
@@ -20,12 +23,13 @@ included). One verify round, per active sequence:
                        when it is a leaf
 
 There is one device-to-host copy per round (accepted tokens, lengths, flags),
-plus one for the adaptive-plan confidences when that mode is on. Draws use
-counter noise keyed by (seed, round, sequence id, draw index), so results do
-not depend on batch composition or on which rows finished earlier.
+plus one for the adaptive-plan confidences when that mode is on (one per
+depth in chain mode). Draws use counter noise keyed by (seed, round, sequence
+id, draw index), so results do not depend on batch composition or on which
+rows finished earlier.
 
 Not built here (rejected at construction): reflex fast-state proposals
-(``reflex_enabled``) and chain proposals (``proposal_mode="chain"``).
+(``reflex_enabled``).
 """
 from __future__ import annotations
 
@@ -104,8 +108,6 @@ class FlashMedusaDecoder:
             raise ValueError(f"Unsupported cache_update_mode={config.cache_update_mode}")
         if config.proposal_mode not in {"medusa", "chain"}:
             raise ValueError(f"Unsupported proposal_mode={config.proposal_mode}")
-        if config.proposal_mode == "chain":
-            raise NotImplementedError("chain proposals are not built in flashgrpo_amd yet")
         if config.reflex_enabled:
             raise NotImplementedError("reflex fast-state proposals are not built in flashgrpo_amd")
         self.target_model = target_model
@@ -187,6 +189,92 @@ class FlashMedusaDecoder:
                        dense_node_count(adapted), plan.mode, plan.layout)
         return new, {"confidence": confs, "topk": list(adapted)}
 
+    def _chain_trees(self, r: "Rollout", roots: torch.Tensor, plan: TreePlan, Bc: int, record: bool):
+        """Chain proposals (``flash_medusa_decoder.py:435-539``).
+
+        The first parent state is Medusa head 0's residual output of the hidden state
+        (``chain_bootstrap_from_medusa``), else the chain cell on (hidden, root
+        embedding). Depth d projects every parent state through the LM head, ranks
+        nan_to_num'd logits (value desc, index asc), takes the confidence quantile over
+        all parent rows, maps it to k_d (no budget refit) and gives each parent in order
+        its top-k_d children while its row holds fewer than the node budget. All rows
+        share one topology (the dense BFS of the adapted k list cut at the budget), so
+        child c of depth d+1 is rank c % k_d of parent c // k_d and every step is a
+        batched gather. Each child's state is the cell applied to its parent's state
+        and its token's embedding; the states after the last depth are not computed
+        (nothing reads them).
+
+        Returns (tree_tokens [Bc, N] int32, chain plan, info) where info holds the
+        adaptive stats, the device confidences still to be read (non-adaptive), the
+        LM-head rows of each depth and the per-depth trace records.
+        """
+        cfg = self.config
+        model, heads = self.model, self.medusa_heads
+        dev = r.device
+        H, V = model.cfg.hidden, model.cfg.vocab
+        emb = model.embed_weight
+        adaptive = bool(cfg.adaptive_tree_enabled)
+        margin = cfg.adaptive_confidence_metric == "margin"
+        q = min(1.0, max(0.0, float(cfg.adaptive_confidence_quantile)))
+        if cfg.chain_bootstrap_from_medusa and heads.num_heads > 0:
+            states = heads.heads[0].project_hidden(r.hidden)
+        else:
+            states = heads.chain_next_state(r.hidden, roots, emb)
+        budget = int(plan.node_budget_per_seq)
+        ks = list(plan.topk_by_depth)
+        cols = [roots.view(Bc, 1)]
+        nodes, n_d = 1, 1
+        adapted, confs_host, confs_dev, recs, rows = [], [], [], [], []
+        for d, base_k in enumerate(ks):
+            base_k = max(1, int(base_k))
+            if nodes >= budget and not adaptive:
+                # the reference projects these states only to report k_d, which is
+                # base_k without adaptation; the tree gets no nodes at this depth
+                adapted.append(base_k)
+                break
+            with timing.label("chain"):
+                lg = model.logits(states.to(model.dtype))
+            rows.append(int(lg.shape[0]))
+            kq = min(max(base_k, 2 if margin else 1), V)
+            cand, score, st = K.medusa_topk(lg, kq, stats=not margin, sanitize=True)
+            if margin:
+                row_conf = score[:, 0] - score[:, 1] if kq > 1 else score[:, 0]
+            else:
+                row_conf = torch.exp(st[:, 0] - st[:, 1])
+            conf_d = torch.quantile(torch.nan_to_num(row_conf, nan=0.0, posinf=0.0, neginf=0.0), q)
+            if adaptive:
+                conf = float(conf_d)  # k_d decides the next depth's width: one sync per depth
+                confs_host.append(conf)
+                k = self._topk_from_confidence(conf, base_k, d)
+            else:
+                confs_dev.append(conf_d)
+                k = base_k
+            adapted.append(k)
+            kk = min(k, V)
+            n_next = min(n_d * kk, budget - nodes)
+            rec = dict(k=k, states=states, logits=lg, cand=cand) if record else None
+            if n_next <= 0:
+                if record:
+                    recs.append(rec)
+                break
+            j = torch.arange(n_next, device=dev)
+            par, rank = j // kk, j % kk
+            tok = cand.view(Bc, n_d, kq)[:, par, rank]
+            cols.append(tok)
+            if record:
+                rec.update(parent_local=par.cpu().numpy(), rank=rank.cpu().numpy())
+                recs.append(rec)
+            nodes += n_next
+            if d + 1 < len(ks) and (nodes < budget or adaptive):
+                ps = states.view(Bc, n_d, H)[:, par].reshape(Bc * n_next, H)
+                states = heads.chain_next_state(ps, tok.reshape(-1), emb)
+            n_d = n_next
+        ks_out = [max(1, int(k)) for k in adapted]
+        chain_plan = TreePlan(budget, len(ks_out), ks_out, nodes, plan.mode, plan.layout)
+        info = dict(stats={"confidence": confs_host, "topk": list(adapted)}, rows=rows, recs=recs,
+                    conf=torch.stack(confs_dev).float() if confs_dev else None)
+        return torch.cat(cols, dim=1).contiguous(), chain_plan, info
+
     # ------------------------------------------------------------------ rollout
     @torch.no_grad()
     def start(self, input_ids: torch.Tensor, attention_mask: torch.Tensor, *, repeated_generate_nums=None,
@@ -263,9 +351,23 @@ class FlashMedusaDecoder:
                                 temperature=cfg.temperature, greedy=greedy, top_k=cfg.top_k, top_p=cfg.top_p)
         use_tree = r.generation_step >= int(cfg.enable_medusa_spec_after)
         plan = self._plan(Bc) if use_tree else TreePlan(1, 0, [], 1, cfg.tree_mode, cfg.tree_layout)
-        cand = score = mlog = None
+        use_chain = use_tree and cfg.proposal_mode == "chain" and r.generation_step >= int(cfg.chain_enable_after)
+        cand = score = mlog = tree_tokens = chain_conf = None
+        chain_recs, chain_rows = [], []
         adaptive_stats = {}
-        if plan.active_heads > 0:
+        if plan.active_heads > 0 and use_chain:
+            r.sync()
+            t0 = time.time()
+            tree_tokens, plan, info = self._chain_trees(r, roots, plan, Bc, trace is not None)
+            adaptive_stats, chain_conf = info["stats"], info["conf"]
+            chain_recs, chain_rows = info["recs"], info["rows"]
+            if chain_conf is not None:
+                # confidences reported without adaptation: read after the round's one sync
+                conf_h = torch.empty(chain_conf.shape, dtype=torch.float32, pin_memory=True)
+                conf_h.copy_(chain_conf, non_blocking=True)
+            r.sync()
+            m["medusa_time"] += time.time() - t0
+        elif plan.active_heads > 0:
             r.sync()
             t0 = time.time()
             proj = self.medusa_heads.project_all(r.hidden, plan.active_heads)
@@ -281,7 +383,8 @@ class FlashMedusaDecoder:
         N = topo.num_nodes
         r.plan_last = {"B_cur": Bc, "node_budget_per_seq": plan.node_budget_per_seq,
                        "active_heads": plan.active_heads, "topk_by_depth": plan.topk_by_depth,
-                       "actual_nodes": plan.actual_nodes, "proposal_mode": "medusa" if use_tree else "target_only",
+                       "actual_nodes": plan.actual_nodes,
+                       "proposal_mode": ("chain" if use_chain else "medusa") if use_tree else "target_only",
                        "adaptive_tree": adaptive_stats}
         m["active_sum"] += Bc
         m["node_sum"] += N
@@ -290,7 +393,9 @@ class FlashMedusaDecoder:
             r.proposed_by_depth[dpt] = r.proposed_by_depth.get(dpt, 0) + c * Bc
         dshared = topo.device(dev)
         dmap = topo.device(dev, Bc)
-        if N > 1:
+        if tree_tokens is not None:
+            assert tree_tokens.shape[1] == N, (tree_tokens.shape, N)
+        elif N > 1:
             tree_tokens, _ = K.tree_layout(cand, score, Bc, roots, dshared["depth"], dshared["rank"], N)
         else:
             tree_tokens = roots.view(Bc, 1)
@@ -359,6 +464,8 @@ class FlashMedusaDecoder:
         if b200:
             cols.append(new_pending.view(-1, 1))
         pack = torch.cat(cols, dim=1).cpu().numpy()
+        if chain_conf is not None:
+            adaptive_stats["confidence"] = conf_h.tolist()
         acc_tok_h, acc_len_h = pack[:, :W], pack[:, W]
         fin_h, last_h = pack[:, W + 1].astype(bool), pack[:, W + 2]
         if int(pack[0, W + 3]):
@@ -380,6 +487,11 @@ class FlashMedusaDecoder:
             if mlog is not None:
                 rec["medusa_logits"] = mlog.float().cpu().numpy()
                 rec["cand"] = cand.cpu().numpy()
+            if chain_recs:
+                rec["chain"] = [dict(k=c["k"], states=c["states"].float().cpu().numpy(),
+                                     logits=c["logits"].float().cpu().numpy(), cand=c["cand"].cpu().numpy(),
+                                     parent_local=c.get("parent_local"), rank=c.get("rank")) for c in chain_recs]
+                rec["chain_budget"] = plan.node_budget_per_seq
             if tree_logits is not None:
                 rec["tree_logits"] = tree_logits.float().cpu().numpy()
                 rec["slot_map"] = None if slot_map is None else slot_map.cpu().numpy()
@@ -462,7 +574,8 @@ class FlashMedusaDecoder:
             draws = np.zeros(Bc, dtype=np.int64)
         r.last_round = dict(num_nodes=N, internal=len(topo.internal), acc_len=acc_len_h.copy(),
                             last_node=last_h.copy(), walk_draws=draws, heads=plan.active_heads, batch=Bc,
-                            lazy=walk_last_h is not None, walk_steps=D if walk_last_h is not None else 0)
+                            lazy=walk_last_h is not None, walk_steps=D if walk_last_h is not None else 0,
+                            chain_rows=list(chain_rows))
         if b200:
             r.pending = new_pending
         # ---------------- bookkeeping

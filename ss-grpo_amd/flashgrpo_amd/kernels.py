@@ -117,11 +117,12 @@ def lm_head(x, weight, *, row_index=None, row_active=None, out=None, out_dtype=N
 
 
 # ------------------------------------------------------------------ tree construction
-def medusa_topk(logits, kmax, *, stats=False, workspace=None):
+def medusa_topk(logits, kmax, *, stats=False, sanitize=False, workspace=None):
     """Top-kmax candidates per row ranked (value desc, index asc).
 
     Returns (tokens int32 [R, kmax], scores fp32 [R, kmax], stats fp32 [R, 2] or None)
-    where stats holds (row max, row logsumexp).
+    where stats holds (row max, row logsumexp). ``sanitize`` ranks
+    nan_to_num(logits, nan=-1e9, posinf=1e9, neginf=-1e9) (chain proposals).
     """
     _dev(logits)
     logits = aligned_rows(logits)
@@ -132,8 +133,8 @@ def medusa_topk(logits, kmax, *, stats=False, workspace=None):
     need = _lib.load().fg_medusa_topk_workspace(R, V, kmax)
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(need, dtype=torch.uint8, device=logits.device)
-    _call("fg_medusa_topk", _ptr(logits), dtype_code(logits), logits.stride(0), R, V, kmax, _ptr(tok), _ptr(sc),
-              _ptr(st), _ptr(workspace), workspace.numel() * workspace.element_size(), _stream())
+    _call("fg_medusa_topk", _ptr(logits), dtype_code(logits), logits.stride(0), R, V, kmax, int(bool(sanitize)),
+          _ptr(tok), _ptr(sc), _ptr(st), _ptr(workspace), workspace.numel() * workspace.element_size(), _stream())
     return tok, sc, st
 
 

@@ -14,6 +14,7 @@ from pathlib import Path
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from .. import kernels as K
 
@@ -33,12 +34,42 @@ class ChainDraftCell(nn.Module):
         self.gate = nn.Parameter(torch.tensor(float(gate_init), dtype=dtype or torch.float32))
         nn.init.zeros_(self.out_proj.weight)
         nn.init.zeros_(self.out_proj.bias)
+        self._cast = None
+        self._cast_key = None
 
     def forward(self, state, token_embedding):
         dt = self.state_norm.weight.dtype
         s = state.to(dt)
         mixed = self.state_proj(self.state_norm(s)) + self.token_proj(self.token_norm(token_embedding.to(dt)))
         return s + torch.sigmoid(self.gate) * self.out_proj(self.act(mixed))
+
+    def _weights(self, dtype, device):
+        params = list(self.parameters())
+        key = (dtype, str(device), tuple(p._version for p in params), tuple(p.data_ptr() for p in params))
+        if self._cast_key != key:
+            with torch.no_grad():
+                c = lambda t: t.detach().to(device=device, dtype=dtype).contiguous()
+                self._cast = dict(
+                    sn_w=c(self.state_norm.weight), sn_b=c(self.state_norm.bias),
+                    tn_w=c(self.token_norm.weight), tn_b=c(self.token_norm.bias),
+                    # [bottleneck, 2H]: state_proj and token_proj side by side, one GEMM over
+                    # the concatenated normalised inputs gives their sum
+                    proj=c(torch.cat([self.state_proj.weight, self.token_proj.weight], dim=1)),
+                    out_w=c(self.out_proj.weight), out_b=c(self.out_proj.bias),
+                    gate=torch.sigmoid(self.gate.detach().float()).to(device=device, dtype=dtype),
+                    eps=float(self.state_norm.eps))
+            self._cast_key = key
+        return self._cast
+
+    def step(self, state, token_embedding):
+        """The cell in the state's dtype (weights cast once and cached), as the rollout
+        runs the Medusa heads in the target's dtype."""
+        w = self._weights(state.dtype, state.device)
+        H = state.shape[-1]
+        x = torch.cat([F.layer_norm(state, (H,), w["sn_w"], w["sn_b"], w["eps"]),
+                       F.layer_norm(token_embedding.to(state.dtype), (H,), w["tn_w"], w["tn_b"], w["eps"])], dim=-1)
+        delta = F.linear(F.silu(F.linear(x, w["proj"])), w["out_w"], w["out_b"])
+        return torch.addcmul(state, delta, w["gate"])
 
 
 class MedusaPredictionHead(nn.Module):
@@ -130,8 +161,10 @@ class MedusaHeads(nn.Module):
         return list(logits.split(B, dim=0))
 
     def chain_next_state(self, state, token_ids, embedding_weight):
+        """Next chain state from the parent state and the path token's embedding
+        (``medusa_heads.py:279-286``), computed in the state's dtype."""
         emb = embedding_weight.index_select(0, token_ids.to(embedding_weight.device).long())
-        return self.chain_cell(state, emb)
+        return self.chain_cell.step(state, emb)
 
     # -------------------------------------------------------------- checkpoint I/O
     def _config(self):
@@ -178,4 +211,9 @@ class MedusaHeads(nn.Module):
             for hd in m.heads:
                 hd.fc.weight.normal_(0.0, std, generator=g)
                 hd.fc.bias.normal_(0.0, std, generator=g)
+            # the reference zero-initialises out_proj (the cell starts as the identity);
+            # synthetic runs draw it too so that chain depths differ
+            cc = m.chain_cell
+            for p in (cc.state_proj.weight, cc.token_proj.weight, cc.out_proj.weight, cc.out_proj.bias):
+                p.normal_(0.0, std, generator=g)
         return m

@@ -40,7 +40,7 @@ class Tok:
         self.pad_token_id = 0
 
 
-def build(ocfg, W, heads, dtype):
+def build(ocfg, W, heads, dtype, cell=None):
     from flashgrpo_amd.models import MedusaHeads, TargetConfig, TargetModel
 
     tcfg = TargetConfig(ocfg.num_layers, ocfg.hidden, ocfg.q_heads, ocfg.kv_heads, ocfg.head_dim, ocfg.intermediate,
@@ -53,18 +53,72 @@ def build(ocfg, W, heads, dtype):
             hd.fc.bias.copy_(torch.from_numpy(src["fc_b"]))
             hd.norm.weight.copy_(torch.from_numpy(src["ln_w"]))
             hd.norm.bias.copy_(torch.from_numpy(src["ln_b"]))
+        if cell is not None:
+            cc = mh.chain_cell
+            for mod_p, key in ((cc.state_norm.weight, "sn_w"), (cc.state_norm.bias, "sn_b"),
+                               (cc.token_norm.weight, "tn_w"), (cc.token_norm.bias, "tn_b"),
+                               (cc.state_proj.weight, "sp_w"), (cc.token_proj.weight, "tp_w"),
+                               (cc.out_proj.weight, "op_w"), (cc.out_proj.bias, "op_b")):
+                mod_p.copy_(torch.from_numpy(np.asarray(cell[key], np.float32)))
+            cc.gate.fill_(float(cell["gate"]))
     return model, mh
 
 
-def rounded(W, heads, dtype):
+def rounded(W, heads, dtype, cell=None):
     if dtype == torch.float32:
-        return W, heads
+        return W, heads, cell
     r = lambda a: None if a is None else torch.from_numpy(np.asarray(a)).to(torch.bfloat16).float().numpy()
     Wr = {k: r(v) for k, v in W.items() if k not in ("layers", "inv_freq")}
     Wr["inv_freq"] = W["inv_freq"]
     Wr["layers"] = [{k: r(v) for k, v in lw.items()} for lw in W["layers"]]
     hr = [dict(h, fc_w=r(h["fc_w"]), fc_b=r(h["fc_b"])) for h in heads]
-    return Wr, hr
+    # the device runs the chain cell in the target's dtype
+    cr = None if cell is None else {k: (v if k == "gate" else r(v)) for k, v in cell.items()}
+    return Wr, hr, cr
+
+
+def _k_near(conf, base_k, d, spec):
+    """Branching factors within 1e-6 of a confidence (device and oracle confidences
+    differ by rounding; a value on a rounding edge of k may go either way)."""
+    return {OT.topk_from_confidence(c, base_k, d, enabled=spec.adaptive_tree_enabled,
+                                    min_topk_by_depth=spec.adaptive_min_topk_by_depth,
+                                    low=spec.adaptive_confidence_low, high=spec.adaptive_confidence_high)
+            for c in (conf - 1e-6, conf, conf + 1e-6)}
+
+
+def check_chain(rec, spec, Wr, heads_r, cell_r, tol, Bc):
+    """Chain proposals of one round from the device's own per-depth states and logits:
+    bootstrap state, logits of every state, adapted k, tree tokens (exact given the
+    logits) and each next state (cell on the device's parent state)."""
+    ch = rec["chain"]
+    roots = rec["roots"]
+    if spec.chain_bootstrap_from_medusa:
+        boot = OM.medusa_project(rec["hidden_in"], heads_r[0])
+    else:
+        boot = OM.chain_cell(rec["hidden_in"], Wr["embed"][roots], cell_r)
+    assert rel(ch[0]["states"], boot) < tol
+    base = OD.plan_for(spec, Bc).topk_by_depth
+    budget = rec["chain_budget"]
+    trees = [OT.Tree([int(x)], [-1], [1], [0.0]) for x in roots]
+    cur = [[0] for _ in range(Bc)]
+    ks = []
+    for d, c in enumerate(ch):
+        assert rel(c["logits"], OM.logits(c["states"], Wr["lm_head"])) < tol, d
+        conf = OT.quantile_linear(OD.chain_confidence(c["logits"], spec.adaptive_confidence_metric),
+                                  spec.adaptive_confidence_quantile)
+        assert c["k"] in _k_near(conf, base[d], d, spec), (d, conf, c["k"])
+        ks.append(c["k"])
+        cur, pidx, toks = OT.chain_add_children(trees, cur, c["logits"], c["k"], d, budget)
+        if not toks:
+            break
+        if d + 1 < len(ch):
+            want = OM.chain_cell(c["states"][pidx], Wr["embed"][toks], cell_r)
+            assert rel(ch[d + 1]["states"], want) < tol, d
+    assert rec["tree_tokens"].tolist() == [t.tokens for t in trees]
+    assert rec["plan"][:len(ks)] == ks
+    # a depth reached with the budget already full reports base k (no adaptation)
+    assert rec["plan"][len(ks):] == list(base[len(ks):len(rec["plan"])])
+    return trees
 
 
 class OracleRow:
@@ -99,7 +153,7 @@ class OracleRow:
         return hid[0]
 
 
-def lockstep(trace, ocfg, Wr, heads_r, spec, prompts, dtype, seed, max_length, emit_correction=False):
+def lockstep(trace, ocfg, Wr, heads_r, spec, prompts, dtype, seed, max_length, emit_correction=False, cell_r=None):
     tol = TOL[dtype]
     rows = {}
     for s in range(prompts.shape[0]):
@@ -119,20 +173,24 @@ def lockstep(trace, ocfg, Wr, heads_r, spec, prompts, dtype, seed, max_length, e
                       for i, s in enumerate(active)]
         assert rec["roots"].tolist() == want_roots, rnd
         plan = OD.plan_for(spec, Bc)
-        if "medusa_logits" in rec:
-            nh = plan.active_heads
-            ml = rec["medusa_logits"].reshape(nh, Bc, -1)
-            want_ml = OM.medusa_logits(rec["hidden_in"], heads_r, Wr["lm_head"], nh)
-            for d in range(nh):
-                assert rel(ml[d], want_ml[d]) < tol
-            plan = OD.adapt_plan(spec, plan, [ml[d] for d in range(nh)])
-        assert rec["plan"] == list(plan.topk_by_depth), rnd
-        heads_logits = []
-        if "medusa_logits" in rec:
-            ml = rec["medusa_logits"]
-            heads_logits = list(ml.reshape(ml.shape[0] // Bc, Bc, -1))
-        trees = OT.build_batch_trees(rec["roots"], heads_logits, plan)
-        assert rec["tree_tokens"].tolist() == [t.tokens for t in trees], rnd
+        if "chain" in rec:
+            trees = check_chain(rec, spec, Wr, heads_r, cell_r, tol, Bc)
+            stats["chain_rounds"] = stats.get("chain_rounds", 0) + 1
+        else:
+            if "medusa_logits" in rec:
+                nh = plan.active_heads
+                ml = rec["medusa_logits"].reshape(nh, Bc, -1)
+                want_ml = OM.medusa_logits(rec["hidden_in"], heads_r, Wr["lm_head"], nh)
+                for d in range(nh):
+                    assert rel(ml[d], want_ml[d]) < tol
+                plan = OD.adapt_plan(spec, plan, [ml[d] for d in range(nh)])
+            assert rec["plan"] == list(plan.topk_by_depth), rnd
+            heads_logits = []
+            if "medusa_logits" in rec:
+                ml = rec["medusa_logits"]
+                heads_logits = list(ml.reshape(ml.shape[0] // Bc, Bc, -1))
+            trees = OT.build_batch_trees(rec["roots"], heads_logits, plan)
+            assert rec["tree_tokens"].tolist() == [t.tokens for t in trees], rnd
         N = trees[0].node_count
         if "tree_hidden" in rec:
             for i, s in enumerate(active):
@@ -192,7 +250,9 @@ def _run(ocfg, spec, *, dtype, B0, repeats, P, max_length, seed=123, wseed=0, ca
 
     W = OM.random_weights(ocfg, seed=wseed, std=0.05)
     heads = OM.random_medusa(ocfg.hidden, spec.num_medusa_heads, seed=wseed + 1, std=0.05)
-    model, mh = build(ocfg, W, heads, dtype)
+    cell = OM.random_chain_cell(ocfg.hidden, seed=wseed + 2, std=0.05, gate_init=-1.0) \
+        if spec.proposal_mode == "chain" else None
+    model, mh = build(ocfg, W, heads, dtype, cell)
     cfg = FlashMedusaConfig(num_medusa_heads=spec.num_medusa_heads, tree_mode=spec.tree_mode,
                             cpeak_nodes=spec.cpeak_nodes, max_tree_nodes_per_seq=spec.max_tree_nodes_per_seq,
                             max_tree_depth=spec.max_tree_depth, fixed_tree_topk_by_depth=spec.fixed_tree_topk_by_depth,
@@ -200,17 +260,23 @@ def _run(ocfg, spec, *, dtype, B0, repeats, P, max_length, seed=123, wseed=0, ca
                             temperature=spec.temperature, top_p=spec.top_p, top_k=spec.top_k,
                             emit_correction_token=spec.emit_correction_token, noise_seed=seed,
                             cache_update_mode=cache_mode, project_internal_tree_logits_only=internal_only,
-                            lazy_walk_lm_head=lazy)
+                            lazy_walk_lm_head=lazy, proposal_mode=spec.proposal_mode,
+                            chain_bootstrap_from_medusa=spec.chain_bootstrap_from_medusa,
+                            adaptive_confidence_metric=spec.adaptive_confidence_metric,
+                            adaptive_confidence_quantile=spec.adaptive_confidence_quantile,
+                            adaptive_confidence_low=spec.adaptive_confidence_low,
+                            adaptive_confidence_high=spec.adaptive_confidence_high,
+                            adaptive_min_topk_by_depth=spec.adaptive_min_topk_by_depth)
     dec = FlashMedusaDecoder(model, mh, Tok(spec.eos_token_id), cfg)
     rng = np.random.default_rng(wseed + 7)
     prompts = rng.integers(0, ocfg.vocab, (B0, P))
     trace = []
     out = dec.generate(torch.from_numpy(prompts), torch.ones(B0, P, dtype=torch.long), repeated_generate_nums=repeats,
                        max_length=max_length, trace=trace)
-    Wr, hr = rounded(W, heads, dtype)
+    Wr, hr, cr = rounded(W, heads, dtype, cell)
     seed_eff = trace[0]["seed"]
     stats = lockstep(trace, ocfg, Wr, hr, spec, np.repeat(prompts, repeats, axis=0), dtype, seed_eff, max_length,
-                     emit_correction=spec.emit_correction_token)
+                     emit_correction=spec.emit_correction_token, cell_r=cr)
     for s, g in enumerate(out["generated_token_ids"]):
         assert len(g) >= 1
     return out, stats
@@ -276,3 +342,45 @@ def test_lockstep_bf16_7b_geometry():
     out, st = _run(cfg, spec, dtype=torch.bfloat16, B0=2, repeats=2, P=40, max_length=40 + 6)
     assert st["rounds"] == out["total_verify_rounds"] >= 3
     assert out["last_tree_plan"]["node_budget_per_seq"] == 32
+
+
+@pytest.mark.parametrize("dtype,boot,metric", [(torch.float32, True, "top1_prob"), (torch.float32, False, "margin"),
+                                               (torch.bfloat16, True, "top1_prob")])
+def test_lockstep_chain_proposals(dtype, boot, metric):
+    """proposal_mode="chain": per-depth LM head over every parent state, sanitised
+    top-k, adapted k, dense-BFS children under the budget, ChainDraftCell steps."""
+    spec = OD.DecodeSpec(tree_mode="concurrency_aware", cpeak_nodes=64, max_tree_nodes_per_seq=16,
+                         fixed_tree_topk_by_depth=(4, 3, 2), num_medusa_heads=3, max_tree_depth=4, top_p=1.0,
+                         proposal_mode="chain", chain_bootstrap_from_medusa=boot, adaptive_tree_enabled=True,
+                         adaptive_confidence_metric=metric,
+                         adaptive_confidence_low=0.005 if metric == "top1_prob" else 0.01,
+                         adaptive_confidence_high=0.05 if metric == "top1_prob" else 0.3)
+    cfg = SMALL if dtype == torch.float32 else SMALL16
+    out, st = _run(cfg, spec, dtype=dtype, B0=2, repeats=2, P=24, max_length=24 + 16)
+    assert st["chain_rounds"] == st["rounds"] == out["total_verify_rounds"]
+    assert out["last_tree_plan"]["proposal_mode"] == "chain"
+
+
+def test_lockstep_chain_fixed_tree():
+    """Non-adaptive chain proposals on a fixed plan ([4, 1] in 12 nodes), top-p 0.9.
+    (The adaptive cases above cut their trees inside a depth: a [4, 3, 2] plan in 16
+    nodes.)"""
+    spec = OD.DecodeSpec(tree_mode="fixed", max_tree_nodes_per_seq=12, fixed_tree_topk_by_depth=(4, 2, 1),
+                         num_medusa_heads=3, max_tree_depth=4, top_p=0.9, proposal_mode="chain")
+    out, st = _run(SMALL, spec, dtype=torch.float32, B0=2, repeats=2, P=20, max_length=20 + 16)
+    assert st["chain_rounds"] == st["rounds"]
+
+
+def test_lockstep_bf16_8b_chain_geometry():
+    """The 8B chain config's geometry (32/8 heads of 128, vocab 128256, theta 5e5, no
+    QKV bias, 4 heads, chain proposals, adaptive concurrency-aware plan with a 48-node
+    budget) on a 2-layer, 512-wide stack: 4 sequences in lockstep, bf16."""
+    cfg = OM.ModelConfig(num_layers=2, hidden=512, q_heads=32, kv_heads=8, head_dim=128, intermediate=1024,
+                         vocab=128256, rope_theta=5e5, qkv_bias=False)
+    spec = OD.DecodeSpec(tree_mode="concurrency_aware", cpeak_nodes=192, max_tree_nodes_per_seq=48,
+                         fixed_tree_topk_by_depth=(4, 3, 2), num_medusa_heads=4, max_tree_depth=5,
+                         adaptive_tree_enabled=True, adaptive_confidence_low=0.2, adaptive_confidence_high=0.7,
+                         temperature=0.7, top_p=1.0, proposal_mode="chain")
+    out, st = _run(cfg, spec, dtype=torch.bfloat16, B0=2, repeats=2, P=40, max_length=40 + 6)
+    assert st["chain_rounds"] == st["rounds"] >= 3
+    assert out["last_tree_plan"]["node_budget_per_seq"] == 48

@@ -138,6 +138,35 @@ def test_medusa_topk_matches_canonical_order(dtype, V, kmax):
         assert float(st[r, 0]) == float(xs[r].max())
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_medusa_topk_sanitize_nan_inf(dtype):
+    """sanitize=1 ranks nan_to_num(x, -1e9, 1e9, -1e9) (chain builder); sanitize=0 ranks
+    NaN above every number (torch.topk)."""
+    g = torch.Generator(device="cpu").manual_seed(12)
+    R, V, k = 6, 4099, 4
+    x = torch.randn(R, V, generator=g)
+    x[0, [5, 77, 4000]] = float("nan")
+    x[1, [3, 9]] = float("inf")
+    x[2, :] = float("-inf")
+    x[3, :] = float("nan")
+    x[4, ::2] = float("-inf")
+    x[5, [10, 11]] = float("nan")
+    x[5, [12]] = float("inf")
+    xd = x.to(dtype).to(DEV)
+    xs = to_np(xd)
+    tok, sc, st = K().medusa_topk(xd, k, stats=True, sanitize=True)
+    raw, _, _ = K().medusa_topk(xd, k)
+    for r in range(R):
+        clean = OT.nan_to_num_logits(xs[r])
+        ids, vals = OT.topk_canonical(clean, k)
+        assert tok[r].tolist() == ids.tolist(), r
+        assert np.array_equal(to_np(sc[r]), vals.astype(np.float32) + 0.0), r
+        m = float(clean.max())
+        lse = np.log(np.sum(np.exp(clean.astype(np.float64) - m))) + m
+        assert float(st[r, 0]) == m and abs(float(st[r, 1]) - lse) < 1e-4 * max(1.0, abs(lse)), r
+        assert raw[r].tolist() == OT.topk_canonical(xs[r], k)[0].tolist(), r
+
+
 def test_tree_layout_matches_oracle_trees():
     rng = np.random.default_rng(3)
     for ks, budget, B, V in [([4, 2], 16, 8, 500), ([4, 2, 1, 1], 32, 6, 300), ([4, 3, 2], 16, 3, 64)]:

@@ -81,3 +81,57 @@ def test_b200_correction_becomes_next_root():
             assert st.pending[b] == (-1 if c is None else c)
     assert seen > 0
     assert OS.counter_noise(9, 0, 0, 0) != OS.counter_noise(9, 0, 0, 1)
+
+
+def _greedy_reference(W, prompts, steps):
+    """Plain autoregressive greedy decoding (first maximum) by full re-forwards."""
+    out = []
+    for p in prompts:
+        seq = list(p)
+        for _ in range(steps):
+            hid, _, _ = OM.prefill(CFG, W, np.array([seq]))
+            lg = OM.logits(hid[0, -1], W["lm_head"]).astype(np.float32)
+            seq.append(int(np.argmax(lg)))
+        out.append(seq[len(p):])
+    return out
+
+
+def test_greedy_speculation_equals_greedy_decoding_medusa_and_chain():
+    """exact_target acceptance is lossless: with greedy draws, any proposal mode
+    emits the target's own greedy continuation."""
+    W, heads = _setup(5)
+    cell = OM.random_chain_cell(CFG.hidden, seed=6, std=0.3, gate_init=-1.0)
+    prompts = np.random.default_rng(4).integers(0, CFG.vocab, (2, 5))
+    ref = _greedy_reference(W, prompts, 12)
+    for mode, boot in [("medusa", True), ("chain", True), ("chain", False)]:
+        spec = OD.DecodeSpec(tree_mode="fixed", max_tree_nodes_per_seq=12, fixed_tree_topk_by_depth=(3, 2, 1),
+                             do_sample=False, proposal_mode=mode, chain_bootstrap_from_medusa=boot)
+        gen = OD.generate(CFG, W, heads, prompts, spec, max_length=17, seed=3, cell=cell)
+        assert gen == ref, mode
+
+
+def test_chain_round_extract_equals_recompute_and_trees():
+    W, heads = _setup(6)
+    cell = OM.random_chain_cell(CFG.hidden, seed=7, std=0.3, gate_init=-1.0)
+    prompts = np.random.default_rng(5).integers(0, CFG.vocab, (3, 6))
+    spec = OD.DecodeSpec(tree_mode="fixed", max_tree_nodes_per_seq=10, fixed_tree_topk_by_depth=(3, 2, 2),
+                         proposal_mode="chain", adaptive_tree_enabled=True, adaptive_confidence_low=0.05,
+                         adaptive_confidence_high=0.3)
+    st = OD.prefill_state(CFG, W, prompts, 64)
+    hist = [list(p) for p in prompts]
+    for rnd in range(4):
+        h_in = st.hidden.copy()
+        out = OD.verify_round(CFG, W, heads, st, spec, seed=2, rnd=rnd, max_length=60, cell=cell)
+        recs = out["chain"]
+        plan = out["plan"]
+        assert plan.topk_by_depth == [r["k"] for r in recs][:len(plan.topk_by_depth)]
+        assert np.array_equal(recs[0]["states"], OM.medusa_project(h_in, heads[0]))
+        for b in range(3):
+            hist[b].extend(out["acc_tokens"][b])
+            full = np.array([hist[b]])
+            hid, ks, _ = OM.prefill(CFG, W, full)
+            assert np.allclose(st.hidden[b], hid[0, -1], atol=1e-10)
+            assert np.allclose(st.k[0][b, :, :len(hist[b])], ks[0][0], atol=1e-10)
+        trees = out["trees"]
+        assert all(t.parents == trees[0].parents for t in trees)
+        assert trees[0].node_count <= 10

@@ -113,3 +113,44 @@ def test_medusa_block_matches_torch_modules():
             th = torch.from_numpy(h)
             ref = (th + torch.nn.functional.silu(fc(ln(th)))).numpy()
         assert np.allclose(M.medusa_project(h, hd), ref, rtol=0, atol=1e-12)
+
+
+def _torch_chain_cell(cell, H):
+    """The cell's published structure from torch modules (double): LayerNorm ->
+    Linear for state and token, SiLU, Linear with bias, sigmoid-gated residual."""
+    mods = dict(sn=torch.nn.LayerNorm(H, eps=1e-5).double(), tn=torch.nn.LayerNorm(H, eps=1e-5).double(),
+                sp=torch.nn.Linear(H, cell["sp_w"].shape[0], bias=False).double(),
+                tp=torch.nn.Linear(H, cell["tp_w"].shape[0], bias=False).double(),
+                op=torch.nn.Linear(cell["op_w"].shape[1], H).double())
+    t = lambda a: torch.from_numpy(np.asarray(a, np.float64))
+    with torch.no_grad():
+        mods["sn"].weight.copy_(t(cell["sn_w"])); mods["sn"].bias.copy_(t(cell["sn_b"]))
+        mods["tn"].weight.copy_(t(cell["tn_w"])); mods["tn"].bias.copy_(t(cell["tn_b"]))
+        mods["sp"].weight.copy_(t(cell["sp_w"])); mods["tp"].weight.copy_(t(cell["tp_w"]))
+        mods["op"].weight.copy_(t(cell["op_w"])); mods["op"].bias.copy_(t(cell["op_b"]))
+
+    def run(s, e):
+        with torch.no_grad():
+            mixed = mods["sp"](mods["sn"](t(s))) + mods["tp"](mods["tn"](t(e)))
+            delta = mods["op"](torch.nn.functional.silu(mixed))
+            return (t(s) + torch.sigmoid(torch.tensor(float(cell["gate"]), dtype=torch.float64)) * delta).numpy()
+    return run
+
+
+def test_chain_cell_matches_torch_modules():
+    rng = np.random.default_rng(6)
+    H = 40
+    cell = M.random_chain_cell(H, seed=7, std=0.3, gate_init=-2.0)
+    assert cell["sp_w"].shape == (64, H) and cell["op_w"].shape == (H, 64)  # bottleneck max(64, H // 8)
+    assert M.random_chain_cell(1024, seed=0)["sp_w"].shape == (128, 1024)
+    cell["sn_w"] = (1 + 0.2 * rng.standard_normal(H)).astype(np.float32)
+    cell["tn_b"] = (0.2 * rng.standard_normal(H)).astype(np.float32)
+    s, e = rng.standard_normal((5, H)), rng.standard_normal((5, H))
+    assert np.allclose(M.chain_cell(s, e, cell), _torch_chain_cell(cell, H)(s, e), rtol=0, atol=1e-12)
+    # the reference's zero-initialised out_proj makes the cell the identity
+    zero = dict(cell, op_w=np.zeros_like(cell["op_w"]), op_b=np.zeros_like(cell["op_b"]))
+    assert np.array_equal(M.chain_cell(s, e, zero), s)
+    # gate 0 gives half of delta: the output is linear in sigmoid(gate)
+    g0 = dict(cell, gate=np.float32(0.0))
+    big = dict(cell, gate=np.float32(60.0))
+    assert np.allclose(M.chain_cell(s, e, g0) - s, 0.5 * (M.chain_cell(s, e, big) - s), atol=1e-12)

@@ -158,3 +158,62 @@ def test_adaptive_confidence_mapping():
     assert T.topk_from_confidence(float("nan"), 4, 0, **kw) == 1
     assert T.topk_from_confidence(0.3, 4, 0, **dict(kw, enabled=False)) == 4
     assert T.quantile_linear([0.1, 0.2, 0.3, 0.4], 0.25) == pytest.approx(0.175)
+
+
+def test_chain_trees_known_answer():
+    """Hand-derived chain tree: V=6, k=(2, 2), budget 6. NaN and -inf become -1e9 and
+    rank below every finite logit; equal logits resolve to the lower index."""
+    nan, inf = float("nan"), float("inf")
+    d0 = np.array([[0.1, 0.5, 0.3, nan, -inf, 0.5]], np.float32)           # root -> [1, 5]
+    d1 = np.array([[nan, 0.2, 0.9, 0.9, 0.0, -1.0],                        # node 1 -> [2, 3]
+                   [inf, 0.0, 0.1, 0.2, 0.3, 0.4]], np.float32)            # node 2 -> [0, 5]
+    trees, pidx, toks = T.build_chain_trees([4], [d0, d1], [2, 2], budget=6)
+    t = trees[0]
+    assert t.tokens == [4, 1, 5, 2, 3, 0]
+    assert t.parents == [-1, 0, 0, 1, 1, 2]
+    assert t.depths == [1, 2, 2, 3, 3, 3]
+    assert pidx == [[0, 0], [0, 0, 1]] and toks == [[1, 5], [2, 3, 0]]
+    assert t.scores[5] == 1.0e9  # +inf clamps to 1e9
+    # a NaN row ranks every finite logit first
+    assert T.build_chain_trees([0], [np.array([[nan, -3.0, nan, -2.0]], np.float32)], [3], 9)[0][0].tokens == [0, 3, 1, 0]
+
+
+def test_chain_trees_follow_dense_topology():
+    rng = np.random.default_rng(8)
+    for ks, budget in [([4, 2], 16), ([4, 3, 2], 16), ([2, 2, 2, 2], 12), ([3, 1], 40), ([1, 1, 1], 3)]:
+        B, V = 3, 30
+        logits, n = [], 1
+        for k in ks:
+            logits.append(rng.standard_normal((B * n, V)).astype(np.float32))
+            n *= k
+        trees, pidx, toks = T.build_chain_trees(rng.integers(0, V, B), logits, ks, budget)
+        parents, depths, ranks = T.dense_topology(ks, budget)
+        first = [depths.index(d) if d in depths else len(depths) for d in range(2, len(ks) + 3)]
+        for b, t in enumerate(trees):
+            assert t.parents == parents and t.depths == depths
+            for node in range(1, t.node_count):
+                d = depths[node] - 2
+                par = parents[node]
+                local = par - (first[d - 1] if d else 0)   # parent's index within its depth
+                n_d = first[d] - (first[d - 1] if d else 0)
+                row = logits[d][b * n_d + local]
+                assert t.tokens[node] == T.topk_canonical(row, ks[d])[0][ranks[node]]
+        # creation order is row-major: the parent rows of each depth never decrease
+        for p in pidx:
+            assert p == sorted(p)
+
+
+def test_chain_confidence_matches_torch():
+    import torch
+
+    from oracle import decode as D
+
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((7, 33)).astype(np.float32) * 3
+    x[2, 4] = np.nan
+    x[3, :] = -np.inf
+    sx = torch.nan_to_num(torch.from_numpy(x).double(), nan=-1e9, posinf=1e9, neginf=-1e9)
+    top1 = torch.exp(sx.max(-1).values - torch.logsumexp(sx, -1)).numpy()
+    assert np.allclose(D.chain_confidence(x), top1, rtol=1e-12, atol=0)
+    v = torch.topk(sx, 2, dim=-1).values
+    assert np.allclose(D.chain_confidence(x, "margin"), (v[:, 0] - v[:, 1]).numpy(), rtol=0, atol=0)
