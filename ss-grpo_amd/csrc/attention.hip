@@ -10,17 +10,23 @@
 // bf16 path, one workgroup of 8 waves per (sequence, kv head, 256-row query tile):
 //  * the query tile is the G*N rows (n-major, G = q heads per kv head) of one
 //    KV head, so every K/V tile loaded from HBM serves all of them;
-//  * each wave owns 32 query rows; two waves share a SIMD, so one wave's MFMAs
-//    overlap the other's softmax arithmetic; a wave whose rows are all past the
-//    tile only stages K/V;
+//  * each wave owns 32 query rows, two waves per SIMD; a wave whose rows are all
+//    past the tile only stages K/V;
 //  * S^T = K Q^T (keys on the M side) puts one query per lane: the online
-//    softmax row max / sum are per-lane values plus one exchange with lane^32;
+//    softmax row max / sum are per-lane values plus one exchange with the other
+//    half-wave (v_permlane32_swap);
 //  * O^T += V^T P^T: P^T is fed straight from the S^T accumulators (bf16) as the
-//    B operand; V is transposed into LDS while staging (2 keys x 8 dims per
-//    thread) so the A operand reads two 8-byte runs per lane in the key order
-//    of the accumulators; 4-key groups of V^T row d are stored XOR-swizzled by
-//    (d >> 3) & 15, which keeps the staging writes and the fragment reads free
-//    of bank conflicts;
+//    B operand; l is summed from the same bf16 P (v_dot2c_f32_bf16);
+//  * waves 0-3 stage K, waves 4-7 stage V, with buffer loads over the sequence's
+//    keys [0, min(seq_len + N, capacity)) (loads past the end return 0);
+//  * V^T rows hold the 64 keys of a tile in the order 0-3, 8-11, 4-7, 12-15 per
+//    16-key block, so the 8 keys a lane feeds the PV MFMA (4g..4g+3 and
+//    8+4g..8+4g+3 of a block) are one 16-byte read at a compile-time offset; the
+//    staging writes are 4-key runs (8 bytes) with consecutive lanes on consecutive
+//    runs of one row, and a row pitch of 9 16-byte chunks puts 8 consecutive rows
+//    on distinct banks (reads and writes are conflict-free);
+//  * per tile all 16 K fragments are read from LDS before the first MFMA and the
+//    16 V^T fragments are read during the S MFMAs (one LDS latency per phase);
 //  * K/V tiles are double-buffered in LDS and staged through two register
 //    stages: the global loads of tile t+2 are issued before tile t is computed
 //    (two tiles in flight per workgroup), one barrier per 64-key tile;
@@ -57,9 +63,9 @@ constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kRowsTile = kWaves * 32;
 constexpr int kKPitch = kD + 8;    // bf16 elements per K row in LDS
-constexpr int kVPitch = kKT + 8;   // bf16 elements per V^T row in LDS
+constexpr int kVtPitch = kKT + 8;  // bf16 elements per V^T row in LDS (9 16-byte chunks)
 constexpr float kRescaleSlack = 8.0f;  // log2 units
-static_assert(kKT * kD / 8 == 2 * kThreads, "staging: two 16-byte K and V chunks per thread");
+static_assert(kKT * kD / 8 == 4 * (kThreads / 2), "staging: four 16-byte chunks per thread of a half");
 
 FG_DEVICE int c_row32(int i, int lane) { return (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3); }
 
@@ -72,34 +78,50 @@ FG_DEVICE uint64_t tile_allowed_mask(int sh, uint64_t tree_bits) {
   return prefix | tree;
 }
 
+// Position of key k in a V^T row (see the layout notes above).
+FG_DEVICE int vt_pos(int k) {
+  return (k & ~15) | (k & 3) | (((k >> 3) & 1) << 2) | (((k >> 2) & 1) << 3);
+}
+
+// Max / sum of a value with the same lane of the other half-wave.
+FG_DEVICE float xor32_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+FG_DEVICE float xor32_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
 __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, int m_tiles) {
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kKT * kKPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][kD * kVPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][kD * kVtPitch];
+  typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
   const int mt = blockIdx.x % m_tiles;
   const int hkv = (blockIdx.x / m_tiles) % a.Hkv;
   const int b = blockIdx.x / (m_tiles * a.Hkv);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int G = a.Hq / a.Hkv;
   const int M = G * a.N;
   const int s0 = a.seq_len[b];
   const int total = s0 + a.N;
-  const int last_key = min(total, a.capacity) - 1;
+  const int nkeys = min(total, a.capacity);
   const int cb = a.row_map ? a.row_map[b] : b;
   const uint16_t* kbase = (const uint16_t*)a.k + (int64_t)cb * a.cache_batch + (int64_t)hkv * a.cache_head;
   const uint16_t* vbase = (const uint16_t*)a.v + (int64_t)cb * a.cache_batch + (int64_t)hkv * a.cache_head;
 
   // This lane's query row (column of S^T).
   const int row0 = mt * kRowsTile + wave * 32;
-  const bool computes = row0 < M;   // wave-uniform
-  const int r = row0 + (lane & 31);
+  const bool computes = row0 < M;  // wave-uniform
+  const int r = row0 + l32;
   const bool row_ok = r < M;
   const int qn = row_ok ? r / G : 0;
   const int qh = hkv * G + (row_ok ? r % G : 0);
   const uint64_t anc = row_ok ? a.anc[(int64_t)b * a.anc_stride + qn] : 1ull;
-  const uint64_t tree_bits = a.N >= 64 ? anc : anc & ((1ull << a.N) - 1);  // allowed tree nodes
-
-  // Q^T fragments: step s covers d = s*16 + g*8 .. +8.
+  const uint64_t tree_bits = a.N >= 64 ? anc : anc & ((1ull << a.N) - 1);
   bf16x8 qf[kD / 16];
   {
     const uint16_t* qrow = (const uint16_t*)a.q + (((int64_t)b * a.N + qn) * a.Hq + qh) * kD;
@@ -109,7 +131,6 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
       qf[s] = __builtin_bit_cast(bf16x8, w);
     }
   }
-
   floatx16 o[kD / 32];
 #pragma unroll
   for (int db = 0; db < kD / 32; ++db)
@@ -117,90 +138,108 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
     for (int i = 0; i < 16; ++i) o[db][i] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
   const float sl2 = a.scale * 1.44269504088896341f;
+  const bf16x2 ones2 = __builtin_bit_cast(bf16x2, 0x3f803f80u);
 
-  // Staging. K: chunk c of thread t is row t/16 + 32c, dims (t%16)*8..+8.
-  // V: thread t holds keys 2*(t/16) and 2*(t/16)+1 of dims (t%16)*8..+8 and
-  // writes each V^T row as one 4-byte key pair.
-  const int st_col = (tid & 15) * 8;
-  const int st_row = tid >> 4;
-  // Two register stages (named 16-byte vectors, not arrays, so they stay in VGPRs):
-  // the loads of tile t+2 are issued before tile t is computed, so every tile's
-  // loads are in flight across two tile computations.
-  typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-  v4u ka0, ka1, va0, va1, kb0, kb1, vb0, vb1;
-#define FG_LOAD(K0, K1, V0, V1, KEY0)                                                      \
-  {                                                                                        \
-    const int key0_ = (KEY0);                                                              \
-    const uint16_t* kp_ = kbase + st_col;                                                  \
-    const uint16_t* vp_ = vbase + st_col;                                                  \
-    K0 = *(const v4u*)(kp_ + (int64_t)min(key0_ + st_row, last_key) * kD);                 \
-    K1 = *(const v4u*)(kp_ + (int64_t)min(key0_ + st_row + 32, last_key) * kD);            \
-    V0 = *(const v4u*)(vp_ + (int64_t)min(key0_ + 2 * st_row, last_key) * kD);             \
-    V1 = *(const v4u*)(vp_ + (int64_t)min(key0_ + 2 * st_row + 1, last_key) * kD);         \
+  // Staging: waves 0-3 fetch K (thread t: 16-byte chunk t & 15 of keys (t >> 4) + 16 i),
+  // waves 4-7 fetch V (thread t: dims 8 ((t-256) >> 4) .. +8 of keys 4 ((t-256) & 15) + i),
+  // both with buffer loads over the sequence's keys [0, nkeys) (past them: 0).
+  const bool stage_k = __builtin_amdgcn_readfirstlane(wave) < 4;  // wave-uniform
+  const int st = tid & 255;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(stage_k ? kbase : vbase), (short)0, nkeys * (kD * 2), 0x00020000);
+  const uint32_t soff = stage_k ? (uint32_t)((st >> 4) * kD + (st & 15) * 8) * 2u
+                                : (uint32_t)(4 * (st & 15) * kD + (st >> 4) * 8) * 2u;
+  const uint32_t sstep = stage_k ? 16u * kD * 2u : 1u * kD * 2u;  // between the thread's 4 chunks
+  uint16_t* const st_dst = stage_k ? &Ks[0][(st >> 4) * kKPitch + (st & 15) * 8]
+                                   : &Vt[0][(8 * (st >> 4)) * kVtPitch + vt_pos(4 * (st & 15))];
+  v4u xa0, xa1, xa2, xa3, xb0, xb1, xb2, xb3;
+#define FG_LOAD8(X0, X1, X2, X3, KEY0)                                                           \
+  {                                                                                              \
+    const uint32_t o_ = soff + (uint32_t)(KEY0) * (uint32_t)(kD * 2);                            \
+    X0 = __builtin_amdgcn_raw_buffer_load_b128(rsrc, o_, 0, 0);                                  \
+    X1 = __builtin_amdgcn_raw_buffer_load_b128(rsrc, o_ + sstep, 0, 0);                          \
+    X2 = __builtin_amdgcn_raw_buffer_load_b128(rsrc, o_ + 2u * sstep, 0, 0);                     \
+    X3 = __builtin_amdgcn_raw_buffer_load_b128(rsrc, o_ + 3u * sstep, 0, 0);                     \
   }
-  // V^T row d, key pair p (keys 2p, 2p+1) lives at word 2*((p >> 1) ^ ((d >> 3) & 15)) + (p & 1).
-  const int vsw_word = 2 * ((st_row >> 1) ^ ((st_col >> 3) & 15)) + (st_row & 1);
-#define FG_STORE(K0, K1, V0, V1, BUF)                                                      \
-  {                                                                                        \
-    uint16_t* kd_ = &Ks[BUF][st_row * kKPitch + st_col];                                   \
-    *(v4u*)(kd_) = K0;                                                                     \
-    *(v4u*)(kd_ + 32 * kKPitch) = K1;                                                      \
-    uint32_t* vt_ = (uint32_t*)&Vt[BUF][st_col * kVPitch] + vsw_word;                      \
-    _Pragma("unroll") for (int e2 = 0; e2 < 4; ++e2) {                                     \
-      vt_[(2 * e2) * (kVPitch / 2)] = __builtin_amdgcn_perm(V1[e2], V0[e2], 0x05040100u);     \
-      vt_[(2 * e2 + 1) * (kVPitch / 2)] = __builtin_amdgcn_perm(V1[e2], V0[e2], 0x07060302u); \
-    }                                                                                      \
+#define FG_STORE8(X0, X1, X2, X3, BUF)                                                           \
+  {                                                                                              \
+    if (stage_k) {                                                                               \
+      uint16_t* kd_ = st_dst + (BUF) * (kKT * kKPitch);                                          \
+      *(v4u*)(kd_) = X0;                                                                         \
+      *(v4u*)(kd_ + 16 * kKPitch) = X1;                                                          \
+      *(v4u*)(kd_ + 32 * kKPitch) = X2;                                                          \
+      *(v4u*)(kd_ + 48 * kKPitch) = X3;                                                          \
+    } else {                                                                                     \
+      uint16_t* vd_ = st_dst + (BUF) * (kD * kVtPitch);                                          \
+      _Pragma("unroll") for (int e2 = 0; e2 < 4; ++e2) {                                         \
+        *(uint2*)(vd_ + (2 * e2) * kVtPitch) =                                                   \
+            make_uint2(__builtin_amdgcn_perm(X1[e2], X0[e2], 0x05040100u),                       \
+                       __builtin_amdgcn_perm(X3[e2], X2[e2], 0x05040100u));                      \
+        *(uint2*)(vd_ + (2 * e2 + 1) * kVtPitch) =                                               \
+            make_uint2(__builtin_amdgcn_perm(X1[e2], X0[e2], 0x07060302u),                       \
+                       __builtin_amdgcn_perm(X3[e2], X2[e2], 0x07060302u));                      \
+      }                                                                                          \
+    }                                                                                            \
   }
 
-  // An even number of tiles: a padding tile past the keys is fully masked (its
-  // loads re-read the last key) and leaves O and l unchanged.
   const int ntiles = ((total + kKT - 1) / kKT + 1) & ~1;
-  FG_LOAD(ka0, ka1, va0, va1, 0)
-  FG_LOAD(kb0, kb1, vb0, vb1, kKT)
-  FG_STORE(ka0, ka1, va0, va1, 0)
+  FG_LOAD8(xa0, xa1, xa2, xa3, 0)
+  FG_LOAD8(xb0, xb1, xb2, xb3, kKT)
+  FG_STORE8(xa0, xa1, xa2, xa3, 0)
   __syncthreads();
+  const uint16_t* const kf_src = &Ks[0][l32 * kKPitch + g * 8];
+  const uint16_t* const vf_src = &Vt[0][l32 * kVtPitch + g * 8];
   for (int t0 = 0; t0 < ntiles; t0 += 2)
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const int buf = h;
     const int key0 = (t0 + h) * kKT;
-    if (h == 0) FG_LOAD(ka0, ka1, va0, va1, key0 + 2 * kKT)
-    else FG_LOAD(kb0, kb1, vb0, vb1, key0 + 2 * kKT)
+    if (h == 0) FG_LOAD8(xa0, xa1, xa2, xa3, key0 + 2 * kKT)
+    else FG_LOAD8(xb0, xb1, xb2, xb3, key0 + 2 * kKT)
 
     if (computes) {
-      // S^T for two 32-key blocks.
-      floatx16 st[2];
+      const uint16_t* kf_ = kf_src + h * (kKT * kKPitch);
+      const uint16_t* vf_ = vf_src + h * (kD * kVtPitch);
+      // All 16 K fragments of the tile are read before the first MFMA (one LDS
+      // latency per tile instead of one per fragment pair); the same registers then
+      // hold the 16 V^T fragments, read before the exponentials.
+      bf16x8 fr[16];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int s = 0; s < kD / 16; ++s) fr[kb * 8 + s] = *(const bf16x8*)(kf_ + kb * 32 * kKPitch + s * 16);
+      __builtin_amdgcn_sched_barrier(0);
+      floatx16 sc[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) st[kb][i] = 0.0f;
+        for (int i = 0; i < 16; ++i) sc[kb][i] = 0.0f;
 #pragma unroll
-        for (int s = 0; s < kD / 16; ++s) {
-          bf16x8 kf = *(const bf16x8*)&Ks[buf][(kb * 32 + (lane & 31)) * kKPitch + s * 16 + g * 8];
-          st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], st[kb], 0, 0, 0);
-        }
+        for (int s = 0; s < kD / 16; ++s)
+          sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr[kb * 8 + s], qf[s], sc[kb], 0, 0, 0);
       }
+#pragma unroll
+      for (int db = 0; db < kD / 32; ++db)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) fr[db * 4 + c] = *(const bf16x8*)(vf_ + db * 32 * kVtPitch + c * 16);
+      __builtin_amdgcn_sched_barrier(0);
       if (key0 + kKT > s0) {  // tile reaches the tree keys (or the end)
-        // Allowed keys of this tile as a 64-bit mask (bit j = key key0 + j), shifted
-        // to this half-wave's first key; element i sits at bit kb*32 + c_row32(i, 0).
         const uint64_t allowed = tile_allowed_mask(s0 - key0, tree_bits) >> (g * 4);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const bool ok = (allowed >> (kb * 32 + c_row32(i, 0))) & 1ull;
-            st[kb][i] = ok ? st[kb][i] : -INFINITY;
+            sc[kb][i] = ok ? sc[kb][i] : -INFINITY;
           }
       }
       float tmax = -INFINITY;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, st[kb][i]);
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, sc[kb][i]);
+      const float m_new = fmaxf(m_run, xor32_max(tmax) * sl2);
       // Lazy rescale: the reference max only moves when some lane's max grew by
       // more than 2^kRescaleSlack, so p <= 2^kRescaleSlack and O / l is unchanged.
-      const float m_new = fmaxf(m_run, tmax * sl2);
       if (__any(m_new > m_run + kRescaleSlack)) {
         const float m_sub = m_new == -INFINITY ? 0.0f : m_new;
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_sub);
@@ -212,7 +251,7 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
         m_run = m_new;
       }
       const float m_sub = m_run == -INFINITY ? 0.0f : m_run;
-      float psum = 0.0f;
+      float psum = l_run;
       bf16x8 pf[2][2];  // [kb][ks] B operand of P^T
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -221,41 +260,30 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
           uint32_t packed[4];
 #pragma unroll
           for (int j = 0; j < 8; j += 2) {
-            float p0 = __builtin_amdgcn_exp2f(fmaf(st[kb][ks * 8 + j], sl2, -m_sub));
-            float p1 = __builtin_amdgcn_exp2f(fmaf(st[kb][ks * 8 + j + 1], sl2, -m_sub));
-            psum += p0 + p1;
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[kb][ks * 8 + j], sl2, -m_sub));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[kb][ks * 8 + j + 1], sl2, -m_sub));
             packed[j / 2] = fg::pack_bf16x2(p0, p1);
+            psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, packed[j / 2]), ones2, psum, false);
           }
           pf[kb][ks] = __builtin_bit_cast(bf16x8, make_uint4(packed[0], packed[1], packed[2], packed[3]));
         }
-      l_run += psum;
-      // O^T += V^T P^T. Slot j of lane (g) holds key kb*32 + ks*16 + (j/4)*8 + g*4 + j%4.
+      l_run = psum;
 #pragma unroll
-      for (int db = 0; db < kD / 32; ++db) {
-        const int dv = db * 32 + (lane & 31);
-        const uint16_t* vrow = &Vt[buf][dv * kVPitch];
-        const int sw = (dv >> 3) & 15;
+      for (int db = 0; db < kD / 32; ++db)
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int ks = 0; ks < 2; ++ks) {
-            int kg = kb * 8 + ks * 4 + g;  // 4-key group of slots 0..3; slots 4..7 are group kg + 2
-            uint2 lo = *(const uint2*)(vrow + 4 * (kg ^ sw));
-            uint2 hi = *(const uint2*)(vrow + 4 * ((kg + 2) ^ sw));
-            bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-            o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[kb][ks], o[db], 0, 0, 0);
-          }
-      }
+          for (int ks = 0; ks < 2; ++ks)
+            o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr[db * 4 + kb * 2 + ks], pf[kb][ks], o[db], 0, 0, 0);
     }
-    if (h == 0) FG_STORE(kb0, kb1, vb0, vb1, 1)
-    else FG_STORE(ka0, ka1, va0, va1, 0)
+    if (h == 0) FG_STORE8(xb0, xb1, xb2, xb3, 1)
+    else FG_STORE8(xa0, xa1, xa2, xa3, 0)
     __syncthreads();
   }
-#undef FG_LOAD
-#undef FG_STORE
+#undef FG_LOAD8
+#undef FG_STORE8
 
-  // Combine the two half-lanes' sums and write.
-  float l = l_run + __shfl_xor(l_run, 32, 64);
+  const float l = xor32_sum(l_run);
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   if (row_ok) {
     uint16_t* orow = (uint16_t*)a.out + (((int64_t)b * a.N + qn) * a.Hq + qh) * kD;
@@ -263,9 +291,9 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
     for (int db = 0; db < kD / 32; ++db)
 #pragma unroll
       for (int i = 0; i < 16; i += 4) {
-        int d0 = db * 32 + c_row32(i, lane);
-        uint32_t w0 = fg::pack_bf16x2(o[db][i] * inv, o[db][i + 1] * inv);
-        uint32_t w1 = fg::pack_bf16x2(o[db][i + 2] * inv, o[db][i + 3] * inv);
+        const int d0 = db * 32 + c_row32(i, lane);
+        const uint32_t w0 = fg::pack_bf16x2(o[db][i] * inv, o[db][i + 1] * inv);
+        const uint32_t w1 = fg::pack_bf16x2(o[db][i + 2] * inv, o[db][i + 3] * inv);
         *(uint2*)(orow + d0) = make_uint2(w0, w1);
       }
   }
@@ -332,8 +360,9 @@ extern "C" int fg_tree_attention(const void* q, void* out, const void* k_cache, 
     FG_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)k_cache & 15) == 0 && ((uintptr_t)v_cache & 15) == 0 &&
                    cache_head_stride % 8 == 0 && cache_batch_stride % 8 == 0,
                "fg_tree_attention: 16-byte alignment");
-    int M = (q_heads / kv_heads) * num_nodes;
-    int m_tiles = (M + kRowsTile - 1) / kRowsTile;
+    FG_REQUIRE((int64_t)capacity * kD * 2 < (1ll << 31), "fg_tree_attention: capacity too large");
+    const int M = (q_heads / kv_heads) * num_nodes;
+    const int m_tiles = (M + kRowsTile - 1) / kRowsTile;
     hipLaunchKernelGGL(tree_attn_bf16_kernel, dim3(batch * kv_heads * m_tiles), dim3(kThreads), 0, s, a, m_tiles);
   } else if (dtype == fg::kF32) {
     FG_REQUIRE(head_dim <= 128, "fg_tree_attention: fp32 path supports head_dim <= 128");
