@@ -33,7 +33,7 @@
 //  * the ancestor mask is evaluated only on tiles that reach the tree keys, and
 //    the running max (and the O rescale) only moves when a lane's max grows by
 //    more than 2^8, so after the first keys the rescale is almost never taken.
-// fp32 path: one wave per query row, exact online softmax in fp32.
+// fp32 path: one wave per query row, 64 keys per step, exact online softmax in fp32.
 #include "fg_common.h"
 
 namespace {
@@ -299,8 +299,15 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
   }
 }
 
-// fp32: one wave per (sequence, node, q head); lane owns head dims lane, lane+64.
+// fp32: one wave per (sequence, node, q head), 64 keys per step. Lane j scores key
+// key0 + j (dot product over the head dim from float4 loads against q in LDS); the
+// step's max and sum are wave reductions; PV broadcasts each key's p with v_readlane
+// while lane j accumulates dims j and j + 64 of O (exact online softmax, fp32). All
+// loads of a step are independent and unconditional (addresses clamped to the last
+// key), so each step waits for memory about once per phase.
+template <int D>
 __global__ void __launch_bounds__(64) tree_attn_f32_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) float qs[D];
   const int qh = blockIdx.x % a.Hq;
   const int n = (blockIdx.x / a.Hq) % a.N;
   const int b = blockIdx.x / (a.Hq * a.N);
@@ -310,32 +317,49 @@ __global__ void __launch_bounds__(64) tree_attn_f32_kernel(AttnArgs a) {
   const int cb = a.row_map ? a.row_map[b] : b;
   const float* kbase = (const float*)a.k + (int64_t)cb * a.cache_batch + (int64_t)hkv * a.cache_head;
   const float* vbase = (const float*)a.v + (int64_t)cb * a.cache_batch + (int64_t)hkv * a.cache_head;
-  const float* qrow = (const float*)a.q + (((int64_t)b * a.N + n) * a.Hq + qh) * a.d;
+  const float* qrow = (const float*)a.q + (((int64_t)b * a.N + n) * a.Hq + qh) * D;
   const uint64_t anc = a.anc[(int64_t)b * a.anc_stride + n];
-  float q0 = lane < a.d ? qrow[lane] : 0.0f;
-  float q1 = lane + 64 < a.d ? qrow[lane + 64] : 0.0f;
+  for (int j = lane; j < D; j += 64) qs[j] = qrow[j];
+  __syncthreads();
   float m = -INFINITY, l = 0.0f, o0 = 0.0f, o1 = 0.0f;
-  const int total = s0 + a.N;
-  for (int key = 0; key < total; ++key) {
-    if (key >= s0) {
-      int mm = key - s0;
-      if (!((anc >> mm) & 1ull)) continue;
+  const int total = min(s0 + a.N, a.capacity);
+  for (int key0 = 0; key0 < total; key0 += 64) {
+    const int key = key0 + lane;
+    const bool ok = key < total && (key < s0 || ((anc >> (key - s0)) & 1ull));
+    const float* kr = kbase + (int64_t)min(key, total - 1) * D;
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < D; j += 4) {
+      const float4 kv = *(const float4*)(kr + j);
+      const float4 qv = *(const float4*)(qs + j);
+      acc = fmaf(qv.x, kv.x, acc);
+      acc = fmaf(qv.y, kv.y, acc);
+      acc = fmaf(qv.z, kv.z, acc);
+      acc = fmaf(qv.w, kv.w, acc);
     }
-    const float* kr = kbase + (int64_t)key * a.d;
-    float part = (lane < a.d ? q0 * kr[lane] : 0.0f) + (lane + 64 < a.d ? q1 * kr[lane + 64] : 0.0f);
-    float s = fg::wave_sum(part) * a.scale;
-    float m_new = fmaxf(m, s);
-    float alpha = expf(m - m_new);
-    float p = expf(s - m_new);
-    const float* vr = vbase + (int64_t)key * a.d;
-    l = l * alpha + p;
-    o0 = o0 * alpha + (lane < a.d ? p * vr[lane] : 0.0f);
-    o1 = o1 * alpha + (lane + 64 < a.d ? p * vr[lane + 64] : 0.0f);
+    const float s = ok ? acc * a.scale : -INFINITY;
+    const float m_new = fmaxf(m, fg::wave_max(s));
+    if (m_new == -INFINITY) continue;  // wave-uniform: no allowed key yet
+    const float alpha = expf(m - m_new);
+    const float p = ok ? expf(s - m_new) : 0.0f;
+    l = l * alpha + fg::wave_sum(p);
+    o0 *= alpha;
+    o1 *= alpha;
+    // Keys past the end carry p = 0 and read the last key's row, so they add 0.
+    const int last = total - 1 - key0;
+    const float* vr = vbase + (int64_t)key0 * D + lane;
+#pragma unroll
+    for (int j = 0; j < 64; ++j) {
+      const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), j));
+      const float* v_ = vr + (int64_t)min(j, last) * D;
+      if (D > 0) o0 = fmaf(pj, lane < D ? v_[0] : 0.0f, o0);
+      if (D > 64) o1 = fmaf(pj, v_[64], o1);
+    }
     m = m_new;
   }
-  float* orow = (float*)a.out + (((int64_t)b * a.N + n) * a.Hq + qh) * a.d;
-  if (lane < a.d) orow[lane] = o0 / l;
-  if (lane + 64 < a.d) orow[lane + 64] = o1 / l;
+  float* orow = (float*)a.out + (((int64_t)b * a.N + n) * a.Hq + qh) * D;
+  if (lane < D) orow[lane] = o0 / l;
+  if (lane + 64 < D) orow[lane + 64] = o1 / l;
 }
 
 }  // namespace
@@ -365,8 +389,13 @@ extern "C" int fg_tree_attention(const void* q, void* out, const void* k_cache, 
     const int m_tiles = (M + kRowsTile - 1) / kRowsTile;
     hipLaunchKernelGGL(tree_attn_bf16_kernel, dim3(batch * kv_heads * m_tiles), dim3(kThreads), 0, s, a, m_tiles);
   } else if (dtype == fg::kF32) {
-    FG_REQUIRE(head_dim <= 128, "fg_tree_attention: fp32 path supports head_dim <= 128");
-    hipLaunchKernelGGL(tree_attn_f32_kernel, dim3(batch * num_nodes * q_heads), dim3(64), 0, s, a);
+    FG_REQUIRE(head_dim == 64 || head_dim == 128, "fg_tree_attention: fp32 path supports head_dim 64 or 128");
+    FG_REQUIRE(((uintptr_t)k_cache & 15) == 0 && cache_head_stride % 4 == 0 && cache_batch_stride % 4 == 0,
+               "fg_tree_attention: fp32 path needs 16-byte aligned K rows");
+    if (head_dim == 64)
+      hipLaunchKernelGGL(tree_attn_f32_kernel<64>, dim3(batch * num_nodes * q_heads), dim3(64), 0, s, a);
+    else
+      hipLaunchKernelGGL(tree_attn_f32_kernel<128>, dim3(batch * num_nodes * q_heads), dim3(64), 0, s, a);
   } else {
     return fg::fail("fg_tree_attention: dtype");
   }
