@@ -1,6 +1,6 @@
 """Regenerate the GEMM solution table (run on the MI355X it is meant for).
 
-    python -m flashgrpo_amd.tuning.make_gemm_table --out gemm_mi355x.csv [--configs 7b,1.5b,14b]
+    python -m flashgrpo_amd.tuning.make_gemm_table --out gemm_mi355x.csv [--configs 7b,1.5b,14b,8b]
 
 For each workload it builds the random-init target model and runs the verify
 forward at the rollout shape (sequences x tree nodes) and the prefill chunk
@@ -18,13 +18,15 @@ WORKLOADS = {
     "7b": ("qwen25_7b", 64 * 29, 8 * 64),
     "1.5b": ("qwen25_1p5b", 32 * 13, 4 * 64),
     "14b": ("qwen25_14b", 128 * 41, 16 * 64),
+    "8b": ("llama31_8b", 96 * 48, 12 * 64),
 }
+SEQUENCES = {"7b": 64, "1.5b": 32, "14b": 128, "8b": 96}
 
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--out", required=True)
-    ap.add_argument("--configs", default="7b,1.5b,14b")
+    ap.add_argument("--configs", default="7b,1.5b,14b,8b")
     args = ap.parse_args()
     os.environ["FLASHGRPO_AMD_GEMM_TABLE"] = "off"
     import torch
@@ -41,7 +43,7 @@ def main():
         cfg = getattr(TargetConfig, preset)()
         model = TargetModel.random(cfg, seed=0, dtype=torch.bfloat16, device="cuda")
         for rows in (rollout_rows, prefill_rows):
-            n = 64 if rows == prefill_rows else rows // {"7b": 64, "1.5b": 32, "14b": 128}[name]
+            n = 64 if rows == prefill_rows else rows // SEQUENCES[name]
             b = rows // n
             cache = model.new_cache(b, 2 * n + 8)
             seq = torch.zeros(b, dtype=torch.int32, device="cuda")
