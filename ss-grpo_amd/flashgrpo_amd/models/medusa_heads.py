@@ -157,7 +157,7 @@ class MedusaHeads(nn.Module):
         proj = self.project_all(last_hidden, max_heads)
         if proj.numel() == 0:
             return []
-        logits = K.lm_head(proj, lm_head_weight.to(proj.dtype))
+        logits = F.linear(proj, lm_head_weight.to(proj.dtype))
         return list(logits.split(B, dim=0))
 
     def chain_next_state(self, state, token_ids, embedding_weight):

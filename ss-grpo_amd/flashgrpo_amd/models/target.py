@@ -307,9 +307,22 @@ class TargetModel:
     def logits(self, hidden: torch.Tensor, *, row_index=None, row_active=None, out=None,
                out_dtype=None) -> torch.Tensor:
         """LM-head rows: hidden rows (optionally gathered by row_index); rows with
-        row_active == 0 may be left unwritten."""
-        return K.lm_head(hidden.reshape(-1, self.cfg.hidden), self.w["lm_head"], row_index=row_index,
-                         row_active=row_active, out=out, out_dtype=out_dtype)
+        row_active == 0 may be left unwritten.
+
+        Gathered or skippable rows (the lazy walk projection) run the fg_lm_head
+        kernel, which reads only the listed rows and skips tiles with no active row.
+        Contiguous bf16 rows are a plain GEMM and go to hipBLASLt, which measured
+        faster than fg_lm_head at every row count from 96 to 2304 on MI355X.
+        """
+        x = hidden.reshape(-1, self.cfg.hidden)
+        if (row_index is None and row_active is None and self.dtype == torch.bfloat16
+                and (out_dtype is None or out_dtype == self.dtype)):
+            w = self.w["lm_head"]
+            if out is None:
+                return F.linear(x, w)
+            return torch.matmul(x, w.t(), out=out)
+        return K.lm_head(x, self.w["lm_head"], row_index=row_index, row_active=row_active, out=out,
+                         out_dtype=out_dtype)
 
     def prefill(self, input_ids: torch.Tensor, cache: KVCache, *, lengths=None, chunk: int = MAX_TREE_NODES,
                 row_map: torch.Tensor | None = None) -> torch.Tensor:
