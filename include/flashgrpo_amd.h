@@ -93,11 +93,17 @@ int fg_rope_kv_write(const void* qkv, int dtype, int64_t ld_qkv, int batch, int 
 
 /* Tree attention: node n of sequence b attends to cache keys [0, seq_len[b]) and to
  * tree keys seq_len[b] + m for every bit m of anc[b*anc_batch_stride + n].
- * q/out [batch, num_nodes, Hq, d]; num_nodes <= 64; bf16 needs d == 128. */
+ * q/out [batch, num_nodes, Hq, d]; num_nodes <= 64; bf16 needs d == 128, fp32 d 64 or 128.
+ * When batch x kv_heads leaves the chip idle (bf16), each sequence's keys are split over
+ * several workgroups whose partial softmax states are merged by a second launch; that
+ * needs workspace >= fg_tree_attention_workspace(...) (0 when no split is used; a null
+ * or smaller workspace runs unsplit). */
+size_t fg_tree_attention_workspace(int batch, int num_nodes, int q_heads, int kv_heads, int head_dim, int capacity);
 int fg_tree_attention(const void* q, void* out, const void* k_cache, const void* v_cache, int dtype, int batch,
                       int num_nodes, int q_heads, int kv_heads, int head_dim, int64_t cache_batch_stride,
                       int64_t cache_head_stride, int capacity, const int32_t* seq_len, const int32_t* row_map,
-                      const uint64_t* anc, int64_t anc_batch_stride, float scale, void* stream);
+                      const uint64_t* anc, int64_t anc_batch_stride, float scale, void* workspace,
+                      size_t workspace_bytes, void* stream);
 
 /* y = RMSNorm(x [+ delta]) * weight over rows of `hidden`; with delta, x += delta first. */
 int fg_rmsnorm(void* x, const void* delta, const void* weight, void* y, int dtype, int rows, int hidden, float eps,

@@ -36,6 +36,8 @@
 // fp32 path: one wave per query row, 64 keys per step, exact online softmax in fp32.
 #include "fg_common.h"
 
+#include <algorithm>
+
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -55,6 +57,14 @@ struct AttnArgs {
   int64_t anc_stride;     // 0 when all rows share one topology
   int N, Hq, Hkv, d;
   float scale;
+  // Key split: workgroup part `sp` of `splits` covers tiles [sp*tps, (sp+1)*tps) of
+  // its row's keys and writes the unnormalised O (fp32) and (max, sum) of each query
+  // row to o_part / ml_part ([splits, B, N, Hq, d] and [splits, B, N, Hq]); splits == 1
+  // writes the normalised output directly.
+  int splits;
+  int batch;
+  float* o_part;
+  float2* ml_part;
 };
 
 constexpr int kD = 128;            // head dim of the MFMA path
@@ -77,6 +87,8 @@ FG_DEVICE uint64_t tile_allowed_mask(int sh, uint64_t tree_bits) {
   const uint64_t tree = sh >= 64 ? 0ull : sh >= 0 ? (tree_bits << sh) : sh <= -64 ? 0ull : (tree_bits >> -sh);
   return prefix | tree;
 }
+// Bits j < n of a 64-bit mask (n clamped to [0, 64]).
+FG_DEVICE uint64_t low_bits(int n) { return n <= 0 ? 0ull : n >= 64 ? ~0ull : ((1ull << n) - 1ull); }
 
 // Position of key k in a V^T row (see the layout notes above).
 FG_DEVICE int vt_pos(int k) {
@@ -100,9 +112,10 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
   __shared__ __attribute__((aligned(16))) uint16_t Vt[2][kD * kVtPitch];
   typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
-  const int mt = blockIdx.x % m_tiles;
-  const int hkv = (blockIdx.x / m_tiles) % a.Hkv;
-  const int b = blockIdx.x / (m_tiles * a.Hkv);
+  const int sp = blockIdx.x % a.splits;
+  const int mt = (blockIdx.x / a.splits) % m_tiles;
+  const int hkv = (blockIdx.x / (a.splits * m_tiles)) % a.Hkv;
+  const int b = blockIdx.x / (a.splits * m_tiles * a.Hkv);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int G = a.Hq / a.Hkv;
   const int M = G * a.N;
@@ -112,6 +125,12 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
   const int cb = a.row_map ? a.row_map[b] : b;
   const uint16_t* kbase = (const uint16_t*)a.k + (int64_t)cb * a.cache_batch + (int64_t)hkv * a.cache_head;
   const uint16_t* vbase = (const uint16_t*)a.v + (int64_t)cb * a.cache_batch + (int64_t)hkv * a.cache_head;
+  // This workgroup's key tiles [t_begin, t_end) and the key bound they stop at.
+  const int tiles_all = (total + kKT - 1) / kKT;
+  const int tps = (tiles_all + a.splits - 1) / a.splits;
+  const int t_begin = min(sp * tps, tiles_all);
+  const int t_end = min(t_begin + tps, tiles_all);
+  const int key_end = min(total, t_end * kKT);
 
   // This lane's query row (column of S^T).
   const int row0 = mt * kRowsTile + wave * 32;
@@ -182,9 +201,12 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
     }                                                                                            \
   }
 
-  const int ntiles = ((total + kKT - 1) / kKT + 1) & ~1;
-  FG_LOAD8(xa0, xa1, xa2, xa3, 0)
-  FG_LOAD8(xb0, xb1, xb2, xb3, kKT)
+  // An even number of tiles: a padding tile past key_end is fully masked (its loads
+  // read past the keys or into the next part) and leaves O and l unchanged.
+  const int ntiles = (t_end - t_begin + 1) & ~1;
+  const int kbeg = t_begin * kKT;
+  FG_LOAD8(xa0, xa1, xa2, xa3, kbeg)
+  FG_LOAD8(xb0, xb1, xb2, xb3, kbeg + kKT)
   FG_STORE8(xa0, xa1, xa2, xa3, 0)
   __syncthreads();
   const uint16_t* const kf_src = &Ks[0][l32 * kKPitch + g * 8];
@@ -192,7 +214,7 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
   for (int t0 = 0; t0 < ntiles; t0 += 2)
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const int key0 = (t0 + h) * kKT;
+    const int key0 = kbeg + (t0 + h) * kKT;
     if (h == 0) FG_LOAD8(xa0, xa1, xa2, xa3, key0 + 2 * kKT)
     else FG_LOAD8(xb0, xb1, xb2, xb3, key0 + 2 * kKT)
 
@@ -222,8 +244,8 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
 #pragma unroll
         for (int c = 0; c < 4; ++c) fr[db * 4 + c] = *(const bf16x8*)(vf_ + db * 32 * kVtPitch + c * 16);
       __builtin_amdgcn_sched_barrier(0);
-      if (key0 + kKT > s0) {  // tile reaches the tree keys (or the end)
-        const uint64_t allowed = tile_allowed_mask(s0 - key0, tree_bits) >> (g * 4);
+      if (key0 + kKT > s0 || key0 + kKT > key_end) {  // tile reaches the tree keys or the part's end
+        const uint64_t allowed = (tile_allowed_mask(s0 - key0, tree_bits) & low_bits(key_end - key0)) >> (g * 4);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -284,6 +306,19 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
 #undef FG_STORE8
 
   const float l = xor32_sum(l_run);
+  if (a.splits > 1) {  // unnormalised part: O rows (fp32) and (max in log2 units, sum)
+    if (row_ok) {
+      const int64_t prow = (((int64_t)sp * a.batch + b) * a.N + qn) * a.Hq + qh;
+      float* orow = a.o_part + prow * kD;
+#pragma unroll
+      for (int db = 0; db < kD / 32; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; i += 4)
+          *(float4*)(orow + db * 32 + c_row32(i, lane)) = make_float4(o[db][i], o[db][i + 1], o[db][i + 2], o[db][i + 3]);
+      if (g == 0) a.ml_part[prow] = make_float2(m_run, l);
+    }
+    return;
+  }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   if (row_ok) {
     uint16_t* orow = (uint16_t*)a.out + (((int64_t)b * a.N + qn) * a.Hq + qh) * kD;
@@ -297,6 +332,30 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
         *(uint2*)(orow + d0) = make_uint2(w0, w1);
       }
   }
+}
+
+// Key-split combine: one wave per (sequence, node, q head) row; lane j owns dims
+// 2j, 2j+1. O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s (parts with no
+// allowed key have m_s = -inf and weigh 0).
+__global__ void __launch_bounds__(64) tree_attn_combine_kernel(AttnArgs a, int rows) {
+  const int row = blockIdx.x;
+  const int lane = threadIdx.x;
+  float mx = -INFINITY;
+  for (int p = 0; p < a.splits; ++p) mx = fmaxf(mx, a.ml_part[(int64_t)p * rows + row].x);
+  float den = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  if (mx != -INFINITY) {
+    for (int p = 0; p < a.splits; ++p) {
+      const float2 ml = a.ml_part[(int64_t)p * rows + row];
+      if (ml.x == -INFINITY) continue;
+      const float w = __builtin_amdgcn_exp2f(ml.x - mx);
+      const float2 ov = *(const float2*)(a.o_part + ((int64_t)p * rows + row) * kD + 2 * lane);
+      den += w * ml.y;
+      o0 += w * ov.x;
+      o1 += w * ov.y;
+    }
+  }
+  const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+  *(uint32_t*)((uint16_t*)a.out + (int64_t)row * kD + 2 * lane) = fg::pack_bf16x2(o0 * inv, o1 * inv);
 }
 
 // fp32: one wave per (sequence, node, q head), 64 keys per step. Lane j scores key
@@ -362,13 +421,43 @@ __global__ void __launch_bounds__(64) tree_attn_f32_kernel(AttnArgs a) {
   if (lane + 64 < D) orow[lane + 64] = o1 / l;
 }
 
+
+// Key-split policy: when (sequences x kv heads x row tiles) leaves CUs idle, each
+// workgroup's keys are cut into parts of at least 8 tiles (capacity bound); shorter
+// parts measured no faster than one workgroup per row tile.
+constexpr int kSplitTarget = 256;  // workgroups that fill the chip
+constexpr int kMaxSplits = 16;
+
+int attn_splits(int batch, int num_nodes, int q_heads, int kv_heads, int capacity) {
+  const int M = (q_heads / kv_heads) * num_nodes;
+  const int base = batch * kv_heads * ((M + kRowsTile - 1) / kRowsTile);
+  if (base >= kSplitTarget) return 1;
+  const int tiles = (capacity + kKT - 1) / kKT;
+  const int sp = std::min((kSplitTarget + base - 1) / base, std::max(1, tiles / 8));
+  return std::max(1, std::min(sp, kMaxSplits));
+}
+
+size_t attn_workspace_bytes(int splits, int batch, int num_nodes, int q_heads) {
+  if (splits <= 1) return 0;
+  const size_t rows = (size_t)splits * batch * num_nodes * q_heads;
+  return rows * (kD * sizeof(float) + sizeof(float2)) + 256;
+}
+
 }  // namespace
+
+extern "C" size_t fg_tree_attention_workspace(int batch, int num_nodes, int q_heads, int kv_heads, int head_dim,
+                                              int capacity) {
+  if (batch <= 0 || num_nodes <= 0 || q_heads <= 0 || kv_heads <= 0 || head_dim != kD || capacity <= 0) return 0;
+  return attn_workspace_bytes(attn_splits(batch, num_nodes, q_heads, kv_heads, capacity), batch, num_nodes,
+                              q_heads);
+}
 
 extern "C" int fg_tree_attention(const void* q, void* out, const void* k_cache, const void* v_cache, int dtype,
                                  int batch, int num_nodes, int q_heads, int kv_heads, int head_dim,
                                  int64_t cache_batch_stride, int64_t cache_head_stride, int capacity,
                                  const int32_t* seq_len, const int32_t* row_map, const uint64_t* anc,
-                                 int64_t anc_batch_stride, float scale, void* stream) {
+                                 int64_t anc_batch_stride, float scale, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
   FG_REQUIRE(q && out && k_cache && v_cache && seq_len && anc, "fg_tree_attention: null pointer");
   FG_REQUIRE(batch > 0 && num_nodes > 0 && num_nodes <= 64, "fg_tree_attention: num_nodes must be in [1, 64]");
   FG_REQUIRE(q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0, "fg_tree_attention: heads");
@@ -378,6 +467,7 @@ extern "C" int fg_tree_attention(const void* q, void* out, const void* k_cache, 
   a.cache_batch = cache_batch_stride; a.cache_head = cache_head_stride; a.capacity = capacity;
   a.seq_len = seq_len; a.row_map = row_map; a.anc = anc; a.anc_stride = anc_batch_stride;
   a.N = num_nodes; a.Hq = q_heads; a.Hkv = kv_heads; a.d = head_dim; a.scale = scale;
+  a.splits = 1; a.batch = batch; a.o_part = nullptr; a.ml_part = nullptr;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == fg::kBF16) {
     FG_REQUIRE(head_dim == kD, "fg_tree_attention: bf16 path supports head_dim 128");
@@ -387,7 +477,19 @@ extern "C" int fg_tree_attention(const void* q, void* out, const void* k_cache, 
     FG_REQUIRE((int64_t)capacity * kD * 2 < (1ll << 31), "fg_tree_attention: capacity too large");
     const int M = (q_heads / kv_heads) * num_nodes;
     const int m_tiles = (M + kRowsTile - 1) / kRowsTile;
-    hipLaunchKernelGGL(tree_attn_bf16_kernel, dim3(batch * kv_heads * m_tiles), dim3(kThreads), 0, s, a, m_tiles);
+    const int splits = attn_splits(batch, num_nodes, q_heads, kv_heads, capacity);
+    if (splits > 1 && workspace && workspace_bytes >= attn_workspace_bytes(splits, batch, num_nodes, q_heads)) {
+      const size_t rows = (size_t)batch * num_nodes * q_heads;
+      char* w = (char*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+      a.splits = splits;
+      a.o_part = (float*)w;
+      a.ml_part = (float2*)(w + (size_t)splits * rows * kD * sizeof(float));
+      hipLaunchKernelGGL(tree_attn_bf16_kernel, dim3(batch * kv_heads * m_tiles * splits), dim3(kThreads), 0, s, a,
+                         m_tiles);
+      hipLaunchKernelGGL(tree_attn_combine_kernel, dim3((unsigned)rows), dim3(64), 0, s, a, (int)rows);
+    } else {
+      hipLaunchKernelGGL(tree_attn_bf16_kernel, dim3(batch * kv_heads * m_tiles), dim3(kThreads), 0, s, a, m_tiles);
+    }
   } else if (dtype == fg::kF32) {
     FG_REQUIRE(head_dim == 64 || head_dim == 128, "fg_tree_attention: fp32 path supports head_dim 64 or 128");
     FG_REQUIRE(((uintptr_t)k_cache & 15) == 0 && cache_head_stride % 4 == 0 && cache_batch_stride % 4 == 0,

@@ -32,7 +32,9 @@ SIGNATURES = {
     "fg_tree_layout": (_I, [_P, _P, _I, _I, _P, _P, _P, _I, _P, _P, _I, _P]),
     "fg_rope_kv_write": (_I, [_P, _I, _I64, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _P, _P,
                               _P]),
-    "fg_tree_attention": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I64, _I64, _I, _P, _P, _P, _I64, _F, _P]),
+    "fg_tree_attention_workspace": (_SZ, [_I, _I, _I, _I, _I, _I]),
+    "fg_tree_attention": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I64, _I64, _I, _P, _P, _P, _I64, _F, _P,
+                               _SZ, _P]),
     "fg_rmsnorm": (_I, [_P, _P, _P, _P, _I, _I, _I, _F, _P]),
     "fg_swiglu": (_I, [_P, _P, _I, _I, _I, _P]),
     "fg_sample_workspace": (_SZ, [_I]),

@@ -36,6 +36,20 @@ def _stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
+_SCRATCH = {}
+
+
+def _scratch(name: str, nbytes: int, device) -> torch.Tensor:
+    """A cached uint8 device buffer of at least nbytes for one kind of workspace.
+    Launches are ordered on the current stream, so successive calls may share it."""
+    key = (name, str(device))
+    buf = _SCRATCH.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(int(nbytes), dtype=torch.uint8, device=device)
+        _SCRATCH[key] = buf
+    return buf
+
+
 def _dev(*ts):
     for t in ts:
         if t is not None and not t.is_cuda:
@@ -180,9 +194,16 @@ def tree_attention(q, k_cache, v_cache, *, seq_len, anc, num_nodes, q_heads, kv_
         out = torch.empty_like(q)
     anc_stride = 0 if anc.dim() == 1 else anc.stride(0)
     scale = 1.0 / math.sqrt(head_dim) if scale is None else scale
+    capacity = k_cache.shape[2]
+    ws, ws_bytes = None, 0
+    if q.dtype == torch.bfloat16:
+        need = _lib.load().fg_tree_attention_workspace(B, num_nodes, q_heads, kv_heads, head_dim, capacity)
+        if need:
+            ws = _scratch("tree_attention", need, q.device)
+            ws_bytes = ws.numel()
     _call("fg_tree_attention", _ptr(q), _ptr(out), _ptr(k_cache), _ptr(v_cache), dtype_code(q), B, num_nodes,
-              q_heads, kv_heads, head_dim, k_cache.stride(0), k_cache.stride(1), k_cache.shape[2], _ptr(seq_len),
-              _ptr(row_map), _ptr(anc), anc_stride, float(scale), _stream())
+          q_heads, kv_heads, head_dim, k_cache.stride(0), k_cache.stride(1), capacity, _ptr(seq_len),
+          _ptr(row_map), _ptr(anc), anc_stride, float(scale), _ptr(ws), ws_bytes, _stream())
     return out
 
 

@@ -47,3 +47,15 @@ def test_library_loads_and_reports_errors_without_gpu_work():
                               ctypes.c_void_p(64), None, 0, None)
     assert rc != 0 and b"vocab" in lib.fg_last_error()
     assert lib.fg_sample_workspace(64) >= 64 * 16 * 20 and lib.fg_sample_workspace(0) == 0
+
+
+def test_tree_attention_split_policy():
+    """Key split only when sequences x kv heads leave the chip idle (host-side sizing)."""
+    from flashgrpo_amd import _lib
+
+    lib = _lib.load()
+    assert lib.fg_tree_attention_workspace(64, 29, 28, 4, 128, 2640) == 0      # 7B rounds: 256 workgroups
+    small = lib.fg_tree_attention_workspace(16, 29, 28, 4, 128, 2640)          # 16 sequences, 2k keys: 64 workgroups
+    assert small > 16 * 29 * 28 * 128 * 4                                        # at least two parts of fp32 O
+    assert lib.fg_tree_attention_workspace(32, 13, 12, 2, 128, 900) == 0       # parts would be under 8 tiles
+    assert lib.fg_tree_attention_workspace(2, 13, 12, 2, 64, 900) == 0         # fp32-only head dim

@@ -442,6 +442,29 @@ def test_tree_attention_matches_reference(dtype, d, ks, budget, Hq, Hkv):
     assert rel_err(to_np(out), want) < TOL[dtype]
 
 
+@pytest.mark.parametrize("ks,budget,Hq,Hkv", [([4, 2, 1, 1], 32, 28, 4), ([2] * 5, 48, 12, 2), ([1] * 63, 64, 4, 1)])
+def test_tree_attention_key_split(ks, budget, Hq, Hkv):
+    """Few sequences and a long cache: keys are split over several workgroups (with
+    empty parts for short rows) and merged by the combine launch."""
+    from flashgrpo_amd import _lib
+
+    rng = np.random.default_rng(Hq + len(ks))
+    parents, depths, _ = OT.dense_topology(ks, budget)
+    N = len(parents)
+    B, S, d = 3, 1100, 128
+    seq = np.array([0, 333, 1100 - 64], np.int32)
+    assert _lib.load().fg_tree_attention_workspace(B, N, Hq, Hkv, d, S) > 0  # the split path runs
+    anc = np.array([OT.ancestor_bits(parents)] * B, dtype=np.uint64)
+    q = torch.from_numpy(rng.standard_normal((B, N, Hq, d)).astype(np.float32)).to(DEV).to(torch.bfloat16)
+    kt = torch.from_numpy(rng.standard_normal((B, Hkv, S, d)).astype(np.float32)).to(DEV).to(torch.bfloat16)
+    vt = torch.from_numpy(rng.standard_normal((B, Hkv, S, d)).astype(np.float32)).to(DEV).to(torch.bfloat16)
+    anct = torch.from_numpy(anc.view(np.int64)).to(DEV)
+    out = K().tree_attention(q, kt, vt, seq_len=torch.from_numpy(seq).to(DEV), anc=anct, num_nodes=N, q_heads=Hq,
+                             kv_heads=Hkv, head_dim=d)
+    want = _attn_reference(to_np(q), to_np(kt), to_np(vt), seq, anc, N, Hq // Hkv)
+    assert rel_err(to_np(out), want) < TOL[torch.bfloat16]
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_rope_kv_write_rmsnorm_swiglu(dtype):
     rng = np.random.default_rng(9)
