@@ -307,7 +307,7 @@ def main():
     g = torch.Generator().manual_seed(args.seed + 3)
     prompts = torch.randint(0, cfg.vocab, (work["prompts"], work["prefix"]), generator=g)
     # long enough that no row reaches max_length inside the benchmark
-    max_length = work["prefix"] + 8 * (args.warmup + 2 * args.steps + 4) + 64
+    max_length = work["prefix"] + 8 * (args.warmup + 2 * args.steps + 12) + 64
     t_pre = time.perf_counter()
     r = dec.start(prompts, torch.ones_like(prompts), repeated_generate_nums=work["repeats"], max_length=max_length)
     torch.cuda.synchronize()
@@ -350,6 +350,22 @@ def main():
     kstats = timer.summary()
     rstats = rtimer.summary()
     log(f"instrumented {args.steps} steps in {elapsed_i:.3f} s")
+    # Phase rounds (continuing): the decoder's statistical_time mode synchronises
+    # at each phase boundary, so the phases add up to slightly more than a round.
+    phase_keys = ("medusa_time", "verify_time", "accept_time", "cache_time")
+    before = {k: r.m[k] for k in phase_keys}
+    r.statistical_time = True
+    n_phase = max(min(args.steps, 8), 1)
+    t2 = time.perf_counter()
+    for _ in range(n_phase):
+        dec.step(r)
+    torch.cuda.synchronize()
+    elapsed_p = time.perf_counter() - t2
+    r.statistical_time = False
+    phases = {k.replace("_time", ""): round((r.m[k] - before[k]) / n_phase * 1e3, 3) for k in phase_keys}
+    phases["other"] = round(elapsed_p / n_phase * 1e3 - sum(phases.values()), 3)
+    phases["rounds"] = n_phase
+    log(f"phases (ms/round) {phases}")
 
     def work_totals(rnds, sqs):
         totals = {}
@@ -427,6 +443,7 @@ def main():
         "prefill_s": round(prefill_s, 2),
         "hand_kernels_ms_per_step": round(mine_ms / args.steps, 3),
         "ms_per_step_instrumented": round(elapsed_i / args.steps * 1e3, 3),
+        "phases_ms": phases,
         "roofline": roofline,
         "kernels": kernels,
         "cpu_baseline": cpu,

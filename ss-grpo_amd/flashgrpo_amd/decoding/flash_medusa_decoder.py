@@ -430,6 +430,7 @@ class FlashMedusaDecoder:
             hidden_t = tree_logits = walk_logits = None
         r.sync()
         m["verify_time"] += time.time() - t0
+        t_acc = time.time()
         # ---------------- acceptance
         walk_kw = dict(seed=r.seed, step=rnd, seq_ids=r.row_map, draw0=1, temperature=cfg.temperature, greedy=greedy,
                        top_k=cfg.top_k, top_p=cfg.top_p, err_flag=r.err)
@@ -464,6 +465,7 @@ class FlashMedusaDecoder:
         if b200:
             cols.append(new_pending.view(-1, 1))
         pack = torch.cat(cols, dim=1).cpu().numpy()
+        m["accept_time"] += time.time() - t_acc
         if chain_conf is not None:
             adaptive_stats["confidence"] = conf_h.tolist()
         acc_tok_h, acc_len_h = pack[:, :W], pack[:, W]
@@ -656,6 +658,8 @@ class FlashMedusaDecoder:
             "medusa_head_time_cost": m["medusa_time"],
             "draft_time_cost": m["medusa_time"],
             "check_time_cost": 0.0,
+            # walk + finalize + the round's one sync (lazy walks project their LM-head rows here)
+            "accept_time_cost": m["accept_time"],
             "noise_seed": r.seed,
             "total_correction_tokens": int(m["corrections"]),
             "reflex_metrics": reflex,
@@ -696,7 +700,7 @@ class Rollout:
         self.total_start = time.time()
         self.m = dict(total_acc_length=0, total_decoded_steps=0, accepted=0, proposed=0, rounds=0, active_sum=0,
                       node_sum=0.0, samples=0, tree_query_rows=0, tree_lm_head_rows=0, medusa_time=0.0,
-                      verify_time=0.0, cache_time=0.0, extract_time=0.0, recompute_time=0.0, extract_ok=0,
+                      verify_time=0.0, accept_time=0.0, cache_time=0.0, extract_time=0.0, recompute_time=0.0, extract_ok=0,
                       extract_fallback=0, oom=0, corrections=0)
         self.accept_hist, self.accept_by_depth, self.proposed_by_depth = {}, {}, {}
         self.plan_last = {}
