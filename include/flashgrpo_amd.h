@@ -17,6 +17,8 @@
  *   fg_medusa_topk      decoding/medusa_tree.py:239-252 (per-depth torch.topk),
  *                       decoding/flash_medusa_decoder.py:320-339 (confidences)
  *   fg_tree_layout      decoding/medusa_tree.py:254-277 (BFS token assembly)
+ *   fg_sparse_tree_layout  flashgrpo_b200/decoding/medusa_tree.py:509-685
+ *                       (_select_sparse_children + _build_sparse_batch_trees)
  *   fg_rope_kv_write    models/qwen_flashgrpo_wrapper.py:172-180 (HF rotary + DynamicCache.update)
  *   fg_tree_attention   decoding/tree_attention.py:6-67 + the HF attention it feeds
  *   fg_rmsnorm, fg_swiglu  models/qwen_flashgrpo_wrapper.py:172-180 (HF decoder layer)
@@ -79,15 +81,34 @@ int fg_tree_layout(const int32_t* cand_tokens, const float* cand_scores, int kst
                    const int32_t* roots, const int32_t* node_depth, const int32_t* node_rank, int num_nodes,
                    int32_t* tree_tokens, float* tree_scores, int out_stride, void* stream);
 
+/* Sparse asymmetric trees, one per sequence. cand_tokens/cand_scores are the
+ * top-kstride lists of heads 1..heads (row h*batch + b, as fg_medusa_topk writes
+ * them); nodes_by_head [heads] (host) are the per-head node counts; heads beyond
+ * the third are ignored. Node order: root, head-1 nodes, greedily picked head-2
+ * then head-3 (parent, candidate) pairs, leftover head-1 candidates; cut at
+ * `budget`. Candidate score = value / temperature (fp32); pair value =
+ * parent score + candidate score - diversity_penalty * (picks of the parent) in
+ * fp64. head3_gate [batch] u8 (NULL = all rows) switches head 3 off per row, its
+ * nodes then go to head 2. Outputs [batch, num_nodes] (num_nodes <= 64): tokens,
+ * parents (-1 root/padding), depth (root 1, padding 0), pos_offset (depth - 1,
+ * padding 0), anc (ancestor-or-self bits; padding: self), n_children, scores (fp64
+ * path scores, root 0; may be NULL); n_nodes [batch]. */
+int fg_sparse_tree_layout(const int32_t* cand_tokens, const float* cand_scores, int kstride, int batch,
+                          int vocab, const int32_t* roots, const uint8_t* head3_gate, const int32_t* nodes_by_head,
+                          int heads, int budget, float temperature, double diversity_penalty, int num_nodes,
+                          int32_t* tree_tokens, int32_t* parents, int32_t* depth, int32_t* pos_offset,
+                          uint64_t* anc, int32_t* n_children, int32_t* n_nodes, double* scores, void* stream);
+
 /* Rotary embedding of q and k for num_nodes new tokens per sequence, and the
  * K/V write into cache slots seq_len[b] + n. qkv [batch*num_nodes, (Hq+2Hkv)*d]
- * (row stride ld_qkv); position = seq_len[b] + pos_offset[n]; inv_freq [d/2] fp32;
+ * (row stride ld_qkv); position = seq_len[b] + pos_offset[b*pos_batch_stride + n]
+ * (stride 0: one offset list for every sequence); inv_freq [d/2] fp32;
  * q_out [batch, num_nodes, Hq, d]; caches [Bc, Hkv, capacity, d]; row_map maps b to
  * its cache row (NULL = identity). A slot outside [0, capacity) is not written and
  * sets err_flag bit 8 (err_flag may be NULL). */
 int fg_rope_kv_write(const void* qkv, int dtype, int64_t ld_qkv, int batch, int num_nodes, int q_heads, int kv_heads,
-                     int head_dim, const int32_t* seq_len, const int32_t* pos_offset, const float* inv_freq,
-                     void* q_out, void* k_cache, void* v_cache, int64_t cache_batch_stride,
+                     int head_dim, const int32_t* seq_len, const int32_t* pos_offset, int64_t pos_batch_stride,
+                     const float* inv_freq, void* q_out, void* k_cache, void* v_cache, int64_t cache_batch_stride,
                      int64_t cache_head_stride, int capacity, const int32_t* row_map, int32_t* err_flag,
                      void* stream);
 

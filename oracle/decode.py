@@ -46,16 +46,27 @@ class DecodeSpec:
     adaptive_confidence_metric: str = "top1_prob"
     proposal_mode: str = "medusa"
     chain_bootstrap_from_medusa: bool = True
+    tree_layout: str = "dense"
+    sparse_nodes_by_head: tuple = (5, 4, 0)
+    sparse_min_head3_nodes: int = 0
+    sparse_head3_min_budget: int = 8
+    sparse_branch_score_temperature: float = 1.0
+    sparse_diversity_penalty: float = 0.05
 
 
 def plan_for(spec: DecodeSpec, batch: int) -> OT.Plan:
     return OT.plan_tree(active_batch_size=batch, num_medusa_heads=spec.num_medusa_heads, tree_mode=spec.tree_mode,
-                        tree_layout="dense", cpeak_nodes=spec.cpeak_nodes,
+                        tree_layout=spec.tree_layout, cpeak_nodes=spec.cpeak_nodes,
                         min_tree_nodes_per_seq=spec.min_tree_nodes_per_seq,
                         max_tree_nodes_per_seq=spec.max_tree_nodes_per_seq, max_tree_depth=spec.max_tree_depth,
                         fixed_tree_topk_by_depth=list(spec.fixed_tree_topk_by_depth),
                         adaptive_tree_enabled=spec.adaptive_tree_enabled,
-                        adaptive_min_topk_by_depth=list(spec.adaptive_min_topk_by_depth))
+                        adaptive_min_topk_by_depth=list(spec.adaptive_min_topk_by_depth),
+                        sparse_nodes_by_head=list(spec.sparse_nodes_by_head),
+                        sparse_min_head3_nodes=spec.sparse_min_head3_nodes,
+                        sparse_head3_min_budget=spec.sparse_head3_min_budget,
+                        sparse_branch_score_temperature=spec.sparse_branch_score_temperature,
+                        sparse_diversity_penalty=spec.sparse_diversity_penalty)
 
 
 def adapt_plan(spec: DecodeSpec, plan: OT.Plan, medusa_logits) -> OT.Plan:
@@ -75,7 +86,12 @@ def adapt_plan(spec: DecodeSpec, plan: OT.Plan, medusa_logits) -> OT.Plan:
     ks = OT.fit_topk_to_budget(ks, plan.node_budget_per_seq,
                                min_topk_by_depth=list(spec.adaptive_min_topk_by_depth)[: len(ks)],
                                depth_weight_decay=spec.adaptive_depth_weight_decay)
-    return OT.Plan(plan.node_budget_per_seq, len(ks), ks, OT.dense_node_count(ks), plan.mode, plan.layout)
+    # a sparse plan takes the fitted list as its per-head node counts
+    # (flashgrpo_b200/decoding/flash_medusa_decoder.py:1063-1077)
+    sparse = plan.layout == "sparse_asymmetric"
+    return OT.Plan(plan.node_budget_per_seq, len(ks), ks, OT.dense_node_count(ks), plan.mode, plan.layout,
+                   list(ks) if sparse else [], plan.min_head3_nodes, plan.head3_min_budget,
+                   plan.branch_score_temperature, plan.diversity_penalty)
 
 
 def chain_confidence(logits, metric="top1_prob"):
@@ -189,17 +205,26 @@ def verify_round(cfg, W, heads, st: State, spec: DecodeSpec, seed: int, rnd: int
         mlog = OM.medusa_logits(st.hidden, heads, W["lm_head"], plan.active_heads, dtype) if plan.active_heads else []
         mlog = [np.asarray(x, np.float32) for x in mlog]
         plan = adapt_plan(spec, plan, mlog)
-        trees = OT.build_batch_trees(roots, mlog, plan)
-    N = trees[0].node_count
-    parents = trees[0].parents
-    depths = trees[0].depths
-    toks = np.array([t.tokens for t in trees], np.int64)
-    valid = np.arange(st.k[0].shape[2])[None, :] < st.seq_len[:, None]
+        if plan.layout == "sparse_asymmetric":
+            trees = OT.build_sparse_trees(roots, mlog, plan)
+        else:
+            trees = OT.build_batch_trees(roots, mlog, plan)
+    # Rows are padded to the widest tree: a padding node (token 0, position offset 0)
+    # sees only itself (flashgrpo/decoding/tree_attention.py:47-50) and is never walked.
+    N = max(t.node_count for t in trees)
+    toks = np.zeros((B, N), np.int64)
     allowed = np.zeros((B, N, N), bool)
-    for n in range(N):
-        for a in trees[0].ancestors_including_self(n):
-            allowed[:, n, a] = True
-    pos = st.seq_len[:, None] + np.asarray(depths)[None, :] - 1
+    depth_off = np.zeros((B, N), np.int64)
+    for b, t in enumerate(trees):
+        toks[b, :t.node_count] = t.tokens
+        for n in range(N):
+            if n < t.node_count:
+                allowed[b, n, t.ancestors_including_self(n)] = True
+                depth_off[b, n] = t.depths[n] - 1
+            else:
+                allowed[b, n, n] = True
+    valid = np.arange(st.k[0].shape[2])[None, :] < st.seq_len[:, None]
+    pos = st.seq_len[:, None] + depth_off
     hid, nk, nv = OM.forward(cfg, W, toks, pos, st.k, st.v, valid, allowed, dtype=dtype)
     for li in range(L):
         for b in range(B):

@@ -66,14 +66,44 @@ class Plan:
     actual_nodes: int
     mode: str
     layout: str
+    # sparse_asymmetric layout only (flashgrpo_b200/decoding/medusa_tree.py:49-60)
+    nodes_by_head: list = field(default_factory=list)
+    min_head3_nodes: int = 0
+    head3_min_budget: int = 8
+    branch_score_temperature: float = 1.0
+    diversity_penalty: float = 0.0
 
 
 def plan_tree(*, active_batch_size, num_medusa_heads, tree_mode, tree_layout, cpeak_nodes,
               min_tree_nodes_per_seq, max_tree_nodes_per_seq, max_tree_depth,
-              fixed_tree_topk_by_depth, adaptive_tree_enabled=False, adaptive_min_topk_by_depth=None) -> Plan:
-    """Per-step tree plan. Follows ``flashgrpo/decoding/medusa_tree.py:102-178``."""
-    if tree_layout not in ("dense", "sparse"):
+              fixed_tree_topk_by_depth, adaptive_tree_enabled=False, adaptive_min_topk_by_depth=None,
+              sparse_nodes_by_head=None, sparse_min_head3_nodes=1, sparse_head3_min_budget=8,
+              sparse_branch_score_temperature=1.0, sparse_diversity_penalty=0.05) -> Plan:
+    """Per-step tree plan. Follows ``flashgrpo/decoding/medusa_tree.py:102-178``.
+
+    ``tree_layout="sparse"`` is planned as dense (the reference's v1 mapping,
+    ``:118-122``). ``"sparse_asymmetric"`` plans the dense branching first and then
+    replaces it with per-head node counts, following
+    ``flashgrpo_b200/decoding/medusa_tree.py:342-458``.
+    """
+    if tree_layout not in ("dense", "sparse", "sparse_asymmetric"):
         raise ValueError(tree_layout)
+    if tree_layout == "sparse_asymmetric":
+        dense = plan_tree(active_batch_size=active_batch_size, num_medusa_heads=num_medusa_heads,
+                          tree_mode=tree_mode, tree_layout="dense", cpeak_nodes=cpeak_nodes,
+                          min_tree_nodes_per_seq=min_tree_nodes_per_seq,
+                          max_tree_nodes_per_seq=max_tree_nodes_per_seq, max_tree_depth=max_tree_depth,
+                          fixed_tree_topk_by_depth=fixed_tree_topk_by_depth,
+                          adaptive_tree_enabled=adaptive_tree_enabled,
+                          adaptive_min_topk_by_depth=adaptive_min_topk_by_depth)
+        max_heads = min(int(num_medusa_heads), max(0, int(max_tree_depth) - 1))
+        requested = list(sparse_nodes_by_head or fixed_tree_topk_by_depth or [4, 3, 2])
+        alloc = sparse_allocation(dense.node_budget_per_seq, max_heads, requested, sparse_min_head3_nodes,
+                                  sparse_head3_min_budget)
+        return Plan(dense.node_budget_per_seq, len(alloc), list(alloc), 1 + sum(alloc), tree_mode,
+                    "sparse_asymmetric", list(alloc), max(0, int(sparse_min_head3_nodes)),
+                    max(1, int(sparse_head3_min_budget)), max(1e-6, float(sparse_branch_score_temperature)),
+                    max(0.0, float(sparse_diversity_penalty)))
     layout = "dense"
     bsz = max(1, int(active_batch_size))
     if tree_mode == "fixed":
@@ -119,6 +149,34 @@ def plan_tree(*, active_batch_size, num_medusa_heads, tree_mode, tree_layout, cp
     else:
         raise ValueError(tree_mode)
     return Plan(budget, heads, ks, dense_node_count(ks), tree_mode, layout)
+
+
+def sparse_allocation(budget, max_heads, requested, min_head3_nodes, head3_min_budget):
+    """Per-head node counts of a sparse_asymmetric tree.
+
+    Follows ``flashgrpo_b200/decoding/medusa_tree.py:411-444``: heads take their
+    requested counts in order from the ``budget - 1`` non-root slots; when the budget
+    reaches ``head3_min_budget`` and head 3 was requested, heads 2 then 1 each give
+    up all but one node until head 3 holds ``min_head3_nodes``; trailing zero heads
+    are dropped.
+    """
+    alloc = [0] * max_heads
+    remaining = max(0, int(budget) - 1)
+    for h in range(max_heads):
+        want = max(0, int(requested[h]) if h < len(requested) else 0)
+        alloc[h] = min(want, remaining)
+        remaining -= alloc[h]
+    if max_heads >= 3 and budget >= int(head3_min_budget) and len(requested) >= 3 and int(requested[2]) > 0:
+        deficit = max(0, max(1, int(min_head3_nodes)) - alloc[2])
+        for donor in (1, 0):
+            moved = min(deficit, max(0, alloc[donor] - 1))
+            alloc[donor] -= moved
+            alloc[2] += moved
+            deficit -= moved
+            if deficit == 0:
+                break
+    active = max((h + 1 for h, c in enumerate(alloc) if c > 0), default=0)
+    return alloc[:active]
 
 
 def topk_from_confidence(confidence, base_k, depth_idx, *, enabled, min_topk_by_depth, low, high):
@@ -280,6 +338,115 @@ def build_batch_trees(roots, medusa_logits, plan: Plan):
             if not frontier or len(toks) >= plan.node_budget_per_seq:
                 break
         trees.append(Tree(toks, pars, deps, scs))
+    return trees
+
+
+def sparse_widths(nodes_by_head, vocab):
+    """Candidates taken per head for a sparse tree: heads 1 and 2 keep head 3's count
+    in reserve (``flashgrpo_b200/decoding/medusa_tree.py:569-579``)."""
+    realloc = nodes_by_head[2] if len(nodes_by_head) >= 3 else 0
+    out = []
+    for h, c in enumerate(nodes_by_head):
+        w = c + realloc if h < 2 else c
+        out.append(max(1, min(int(w), int(vocab))))
+    return out
+
+
+def select_sparse_children(parent_nodes, parent_scores, token_ids, token_scores, count, diversity_penalty):
+    """Greedy choice of path extensions with a per-parent diversity penalty.
+
+    Follows ``flashgrpo_b200/decoding/medusa_tree.py:509-546``. The pool is every
+    (parent, candidate) pair in parent-major order, valued at parent score +
+    candidate score (float64). Each pick takes the first pair of strictly largest
+    ``cumulative - penalty * picks_of_its_parent`` among the unpicked pairs; a pool
+    with no value above -inf ends the picks. Returns (parent node, token, cumulative).
+    """
+    if count <= 0 or not parent_nodes or len(token_ids) == 0:
+        return []
+    pool = [(float(parent_scores[p]) + float(s), p, int(t))
+            for p in range(len(parent_nodes)) for t, s in zip(token_ids, token_scores)]
+    picked = [False] * len(pool)
+    uses = [0] * len(parent_nodes)
+    pen = float(diversity_penalty)
+    out = []
+    for _ in range(min(int(count), len(pool))):
+        best, best_v = -1, -math.inf
+        for i, (cum, p, _t) in enumerate(pool):
+            if picked[i]:
+                continue
+            v = cum - pen * uses[p]
+            if v > best_v:
+                best_v, best = v, i
+        if best < 0:
+            break
+        cum, p, t = pool[best]
+        picked[best] = True
+        uses[p] += 1
+        out.append((int(parent_nodes[p]), t, cum))
+    return out
+
+
+def build_sparse_trees(roots, medusa_logits, plan: Plan, head3_gate=None):
+    """Sparse asymmetric candidate trees for a batch.
+
+    Follows ``flashgrpo_b200/decoding/medusa_tree.py:549-685``. Per row: the root;
+    head 1's first ``n1`` candidates under the root; head 2's pairs chosen greedily
+    under the head-1 nodes (``n2``, plus head 3's count when head 3 is gated off for
+    the row); head 3's pairs under the head-2 nodes; then the remaining head-1
+    candidates while the budget allows; truncated to the budget. Candidate scores
+    are the top-k logits divided by the branch temperature in float32 (canonical
+    top-k order). ``head3_gate`` is a per-row bool list (None = every row).
+    """
+    B = len(roots)
+    nodes = list(plan.nodes_by_head or plan.topk_by_depth)
+    heads = min(int(plan.active_heads), len(nodes), len(medusa_logits))
+    nodes = nodes[:heads]
+    if heads == 0:
+        return [Tree([int(r)], [-1], [1], [0.0]) for r in roots]
+    V = np.asarray(medusa_logits[0]).shape[-1]
+    widths = sparse_widths(nodes, V)
+    realloc = nodes[2] if len(nodes) >= 3 else 0
+    T = np.float32(max(float(plan.branch_score_temperature), 1e-6))
+    cands = []
+    for h, w in enumerate(widths):
+        lg = np.asarray(medusa_logits[h], dtype=np.float32)
+        rows = []
+        for b in range(B):
+            ids, vals = topk_canonical(lg[b], w)
+            rows.append((ids.tolist(), (vals.astype(np.float32) / T).astype(np.float32).tolist()))
+        cands.append(rows)
+    gate = [True] * B if head3_gate is None else [bool(g) for g in head3_gate]
+    budget = int(plan.node_budget_per_seq)
+    trees = []
+    for b in range(B):
+        toks, pars, deps, scs = [int(roots[b])], [-1], [1], [0.0]
+        n1 = nodes[0]
+        h1_ids, h1_sc = cands[0][b]
+        for t, s in zip(h1_ids[:n1], h1_sc[:n1]):
+            toks.append(int(t)); pars.append(0); deps.append(2); scs.append(float(s))
+        h1_nodes = list(range(1, len(toks)))
+        use3 = len(nodes) >= 3 and nodes[2] > 0 and gate[b]
+        n2 = (nodes[1] if len(nodes) >= 2 else 0) + (0 if use3 else realloc)
+        h2_nodes, h2_sc = [], []
+        if n2 > 0 and len(cands) >= 2:
+            ids, sc = cands[1][b]
+            for p, t, cum in select_sparse_children(h1_nodes, [scs[i] for i in h1_nodes], ids, sc, n2,
+                                                    plan.diversity_penalty):
+                toks.append(t); pars.append(p); deps.append(3); scs.append(cum)
+                h2_nodes.append(len(toks) - 1); h2_sc.append(cum)
+        if use3 and len(cands) >= 3 and h2_nodes:
+            ids, sc = cands[2][b]
+            for p, t, cum in select_sparse_children(h2_nodes, h2_sc, ids, sc, nodes[2], plan.diversity_penalty):
+                toks.append(t); pars.append(p); deps.append(4); scs.append(cum)
+        seen = {toks[i] for i in h1_nodes}
+        for t, s in zip(h1_ids[n1:], h1_sc[n1:]):
+            if len(toks) >= budget:
+                break
+            if int(t) in seen:
+                continue
+            toks.append(int(t)); pars.append(0); deps.append(2); scs.append(float(s))
+            seen.add(int(t))
+        trees.append(Tree(toks[:budget], pars[:budget], deps[:budget], scs[:budget]))
     return trees
 
 

@@ -31,21 +31,22 @@ FG_DEVICE void store4(void* p, int64_t i, const float (&v)[4]) {
 }
 
 // One workgroup per token (b, n). qkv row = [q heads | k heads | v heads] x d.
-// Position = seq_len[b] + pos_offset[n]; cache slot = seq_len[b] + n.
+// Position = seq_len[b] + pos_offset[b * pos_stride + n]; cache slot = seq_len[b] + n.
 // cos/sin of the token's d/2 angles are computed once into LDS; each thread then
 // rotates 4 consecutive pairs (i, i + d/2) of one head with 8/16-byte accesses.
 // Requires d % 8 == 0 and d <= 256.
 template <int DT>
 __global__ void __launch_bounds__(256) rope_kv_write_kernel(
     const void* __restrict__ qkv, int64_t ld_qkv, int N, int Hq, int Hkv, int d, const int32_t* __restrict__ seq_len,
-    const int32_t* __restrict__ pos_offset, const float* __restrict__ inv_freq, void* __restrict__ q_out,
+    const int32_t* __restrict__ pos_offset, int64_t pos_stride, const float* __restrict__ inv_freq,
+    void* __restrict__ q_out,
     void* __restrict__ k_cache, void* __restrict__ v_cache, int64_t cache_batch, int64_t cache_head, int capacity,
     const int32_t* __restrict__ row_map, int32_t* __restrict__ err_flag) {
   __shared__ float cs[128], sn[128];
   const int tok = blockIdx.x;
   const int b = tok / N, n = tok % N;
   const int s = seq_len[b];
-  const int pos = s + pos_offset[n];
+  const int pos = s + pos_offset[(int64_t)b * pos_stride + n];
   const int slot = s + n;
   const int cb = row_map ? row_map[b] : b;
   const int half = d / 2;
@@ -163,12 +164,13 @@ __global__ void __launch_bounds__(256) swiglu_kernel(const void* __restrict__ gu
 extern "C" {
 
 int fg_rope_kv_write(const void* qkv, int dtype, int64_t ld_qkv, int batch, int num_nodes, int q_heads, int kv_heads,
-                     int head_dim, const int32_t* seq_len, const int32_t* pos_offset, const float* inv_freq,
-                     void* q_out, void* k_cache, void* v_cache, int64_t cache_batch_stride,
+                     int head_dim, const int32_t* seq_len, const int32_t* pos_offset, int64_t pos_batch_stride,
+                     const float* inv_freq, void* q_out, void* k_cache, void* v_cache, int64_t cache_batch_stride,
                      int64_t cache_head_stride, int capacity, const int32_t* row_map, int32_t* err_flag,
                      void* stream) {
   FG_REQUIRE(qkv && seq_len && pos_offset && inv_freq && q_out && k_cache && v_cache, "fg_rope_kv_write: null pointer");
   FG_REQUIRE(batch > 0 && num_nodes > 0 && q_heads > 0 && kv_heads > 0, "fg_rope_kv_write: bad shape");
+  FG_REQUIRE(pos_batch_stride == 0 || pos_batch_stride >= num_nodes, "fg_rope_kv_write: pos_batch_stride must be 0 or >= num_nodes");
   FG_REQUIRE(head_dim > 0 && head_dim % 8 == 0 && head_dim <= 256, "fg_rope_kv_write: head_dim must be a multiple of 8 in [8, 256]");
   FG_REQUIRE(ld_qkv % 8 == 0 && ((uintptr_t)qkv & 15) == 0 && ((uintptr_t)q_out & 15) == 0 &&
                  ((uintptr_t)k_cache & 15) == 0 && ((uintptr_t)v_cache & 15) == 0 && cache_batch_stride % 8 == 0 &&
@@ -178,11 +180,11 @@ int fg_rope_kv_write(const void* qkv, int dtype, int64_t ld_qkv, int batch, int 
   dim3 grid(batch * num_nodes);
   if (dtype == fg::kBF16)
     hipLaunchKernelGGL(rope_kv_write_kernel<fg::kBF16>, grid, dim3(256), 0, s, qkv, ld_qkv, num_nodes, q_heads,
-                       kv_heads, head_dim, seq_len, pos_offset, inv_freq, q_out, k_cache, v_cache,
+                       kv_heads, head_dim, seq_len, pos_offset, pos_batch_stride, inv_freq, q_out, k_cache, v_cache,
                        cache_batch_stride, cache_head_stride, capacity, row_map, err_flag);
   else
     hipLaunchKernelGGL(rope_kv_write_kernel<fg::kF32>, grid, dim3(256), 0, s, qkv, ld_qkv, num_nodes, q_heads,
-                       kv_heads, head_dim, seq_len, pos_offset, inv_freq, q_out, k_cache, v_cache,
+                       kv_heads, head_dim, seq_len, pos_offset, pos_batch_stride, inv_freq, q_out, k_cache, v_cache,
                        cache_batch_stride, cache_head_stride, capacity, row_map, err_flag);
   return fg::check_launch("fg_rope_kv_write");
 }

@@ -19,6 +19,8 @@
 #include "fg_common.h"
 
 #include <algorithm>
+#include <climits>
+#include <cmath>
 
 namespace {
 
@@ -261,6 +263,158 @@ __global__ void tree_layout_kernel(const int32_t* __restrict__ cand_tokens, cons
   }
 }
 
+// ---------------------------------------------------------------- sparse asymmetric trees
+// One wave per sequence assembles the tree of
+// flashgrpo_b200/decoding/medusa_tree.py:549-685 from the per-head top-k lists:
+// head-1 nodes under the root, then head-2 and head-3 nodes picked greedily from
+// (parent, candidate) pairs (:509-546), then leftover head-1 candidates. A pick is
+// the pair of largest parent score + candidate score - penalty * (picks of its
+// parent) in float64, the lowest pair index on ties (the reference's first strict
+// maximum in parent-major order); a value that is NaN or -inf is never picked. The
+// lanes hold the pairs (index lane + 64c) and reduce the best one across the wave.
+constexpr int kSpMaxNodes = 128;  // nodes assembled before the budget cut
+constexpr int kSpMaxParents = 64;
+constexpr int kSpMaxPool = 1024;  // (parent, candidate) pairs of one head
+
+struct SparseArgs {
+  const int32_t* cand_tokens;
+  const float* cand_scores;
+  int kstride, batch;
+  const int32_t* roots;
+  const uint8_t* gate;
+  int n1, n2, n3, realloc, w1, w2, w3, heads, budget, num_nodes;
+  float temperature;
+  double penalty;
+  int32_t *tokens, *parents, *depth, *pos_offset, *n_children, *n_nodes;
+  uint64_t* anc;
+  double* scores;
+};
+
+#pragma clang fp contract(off)
+__global__ void __launch_bounds__(64) sparse_tree_kernel(SparseArgs a) {
+  __shared__ int tok[kSpMaxNodes], par[kSpMaxNodes], dep[kSpMaxNodes];
+  __shared__ double sc[kSpMaxNodes];
+  __shared__ int uses[kSpMaxParents];
+  const int b = blockIdx.x, lane = threadIdx.x;
+  auto row = [&](int h) { return ((int64_t)h * a.batch + b) * a.kstride; };
+  auto cand_score = [&](int h, int c) -> double { return (double)(a.cand_scores[row(h) + c] / a.temperature); };
+  int cnt = 1;
+  if (lane == 0) {
+    tok[0] = a.roots[b];
+    par[0] = -1;
+    dep[0] = 1;
+    sc[0] = 0.0;
+  }
+  const int n1 = min(a.n1, a.w1);
+  if (lane < n1) {
+    tok[1 + lane] = a.cand_tokens[row(0) + lane];
+    par[1 + lane] = 0;
+    dep[1 + lane] = 2;
+    sc[1 + lane] = cand_score(0, lane);
+  }
+  cnt += n1;
+  __syncthreads();
+
+  // Greedy picks of `count` pairs from parents [p0, p0 + np) x candidates [0, w) of head h.
+  auto pick = [&](int h, int p0, int np, int w, int count, int depth) {
+    const int P = np * w;
+    uint32_t picked = 0;
+    if (lane < np) uses[lane] = 0;
+    __syncthreads();
+    const int npick = min(count, P);
+    for (int it = 0; it < npick; ++it) {
+      double bv = -INFINITY;
+      int bi = INT_MAX;
+      for (int c = 0; c * 64 < P; ++c) {
+        const int i = lane + 64 * c;
+        if (i < P && !((picked >> c) & 1u)) {
+          const int j = i / w, r = i - j * w;
+          const double cum = sc[p0 + j] + cand_score(h, r);
+          const double v = cum - a.penalty * (double)uses[j];
+          if (v > bv) {
+            bv = v;
+            bi = i;
+          }
+        }
+      }
+      for (int off = 32; off >= 1; off >>= 1) {
+        const double ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        if (ov > bv || (ov == bv && oi < bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      if (bi == INT_MAX) break;  // wave-uniform: nothing left above -inf
+      if (lane == (bi & 63)) picked |= 1u << (bi >> 6);
+      const int j = bi / w, r = bi - j * w;
+      if (lane == 0) {
+        if (cnt < kSpMaxNodes) {
+          tok[cnt] = a.cand_tokens[row(h) + r];
+          par[cnt] = p0 + j;
+          dep[cnt] = depth;
+          sc[cnt] = sc[p0 + j] + cand_score(h, r);
+        }
+        uses[j] += 1;
+      }
+      ++cnt;
+      __syncthreads();
+    }
+  };
+
+  const bool use3 = a.heads >= 3 && a.n3 > 0 && (!a.gate || a.gate[b]);
+  const int n2 = a.n2 + (use3 ? 0 : a.realloc);
+  const int h2_begin = cnt;
+  if (a.heads >= 2 && n2 > 0) pick(1, 1, n1, a.w2, n2, 3);
+  const int h2_end = min(cnt, kSpMaxNodes);
+  if (use3 && h2_end > h2_begin) pick(2, h2_begin, h2_end - h2_begin, a.w3, a.n3, 4);
+  // leftover head-1 candidates while the budget allows (distinct from every head-1 node)
+  if (lane == 0) {
+    const int extra_begin = cnt;
+    for (int c = n1; c < a.w1 && cnt < a.budget && cnt < kSpMaxNodes; ++c) {
+      const int t = a.cand_tokens[row(0) + c];
+      bool seen = false;
+      for (int m = 1; m <= n1; ++m) seen |= tok[m] == t;
+      for (int m = extra_begin; m < cnt; ++m) seen |= tok[m] == t;
+      if (seen) continue;
+      tok[cnt] = t;
+      par[cnt] = 0;
+      dep[cnt] = 2;
+      sc[cnt] = cand_score(0, c);
+      ++cnt;
+    }
+  }
+  __syncthreads();
+  cnt = __shfl(cnt, 0);
+  const int count = min(min(cnt, a.budget), a.num_nodes);
+  const int64_t o = (int64_t)b * a.num_nodes;
+  for (int n = lane; n < a.num_nodes; n += 64) {
+    if (n < count) {
+      uint64_t m = 1ull << n;
+      for (int p = par[n]; p >= 0; p = par[p]) m |= 1ull << p;
+      int kids = 0;
+      for (int c = n + 1; c < count; ++c) kids += par[c] == n;
+      a.tokens[o + n] = tok[n];
+      a.parents[o + n] = par[n];
+      a.depth[o + n] = dep[n];
+      a.pos_offset[o + n] = dep[n] - 1;
+      a.anc[o + n] = m;
+      a.n_children[o + n] = kids;
+      if (a.scores) a.scores[o + n] = sc[n];
+    } else {
+      a.tokens[o + n] = 0;
+      a.parents[o + n] = -1;
+      a.depth[o + n] = 0;
+      a.pos_offset[o + n] = 0;
+      a.anc[o + n] = 1ull << n;
+      a.n_children[o + n] = 0;
+      if (a.scores) a.scores[o + n] = 0.0;
+    }
+  }
+  if (lane == 0) a.n_nodes[b] = count;
+}
+#pragma clang fp contract(on)
+
 }  // namespace
 
 extern "C" {
@@ -311,6 +465,54 @@ int fg_tree_layout(const int32_t* cand_tokens, const float* cand_scores, int kst
   hipLaunchKernelGGL(tree_layout_kernel, dim3(batch), dim3(64), 0, (hipStream_t)stream, cand_tokens, cand_scores,
                      kstride, batch, roots, node_depth, node_rank, num_nodes, tree_tokens, tree_scores, out_stride);
   return fg::check_launch("fg_tree_layout");
+}
+
+int fg_sparse_tree_layout(const int32_t* cand_tokens, const float* cand_scores, int kstride, int batch,
+                          int vocab, const int32_t* roots, const uint8_t* head3_gate, const int32_t* nodes_by_head,
+                          int heads, int budget, float temperature, double diversity_penalty, int num_nodes,
+                          int32_t* tree_tokens, int32_t* parents, int32_t* depth, int32_t* pos_offset,
+                          uint64_t* anc, int32_t* n_children, int32_t* n_nodes, double* scores, void* stream) {
+  FG_REQUIRE(cand_tokens && cand_scores && roots && nodes_by_head && tree_tokens && parents && depth && pos_offset &&
+                 anc && n_children && n_nodes,
+             "fg_sparse_tree_layout: null pointer");
+  FG_REQUIRE(batch > 0 && heads >= 1 && vocab >= 1 && kstride >= 1 && kstride <= 16, "fg_sparse_tree_layout: bad shape");
+  FG_REQUIRE(num_nodes >= 1 && num_nodes <= 64 && budget >= 1, "fg_sparse_tree_layout: num_nodes must be in [1, 64]");
+  FG_REQUIRE(temperature > 0.0f && diversity_penalty >= 0.0, "fg_sparse_tree_layout: temperature must be > 0, penalty >= 0");
+  SparseArgs a{};
+  a.n1 = nodes_by_head[0];
+  a.n2 = heads >= 2 ? nodes_by_head[1] : 0;
+  a.n3 = heads >= 3 ? nodes_by_head[2] : 0;
+  FG_REQUIRE(a.n1 >= 0 && a.n2 >= 0 && a.n3 >= 0, "fg_sparse_tree_layout: negative node count");
+  a.realloc = heads >= 3 ? a.n3 : 0;
+  // candidates per head (flashgrpo_b200/decoding/medusa_tree.py:569-579)
+  a.w1 = std::max(1, std::min(a.n1 + a.realloc, vocab));
+  a.w2 = std::max(1, std::min(a.n2 + a.realloc, vocab));
+  a.w3 = std::max(1, std::min(a.n3, vocab));
+  FG_REQUIRE(a.w1 <= kstride && (heads < 2 || a.w2 <= kstride) && (heads < 3 || a.w3 <= kstride),
+             "fg_sparse_tree_layout: candidate lists (kstride) shorter than the head widths");
+  FG_REQUIRE(a.n2 + a.realloc <= kSpMaxParents && 1 + a.n1 + a.n2 + a.n3 + 2 * a.realloc <= kSpMaxNodes,
+             "fg_sparse_tree_layout: node counts too large");
+  a.cand_tokens = cand_tokens;
+  a.cand_scores = cand_scores;
+  a.kstride = kstride;
+  a.batch = batch;
+  a.roots = roots;
+  a.gate = head3_gate;
+  a.heads = std::min(heads, 3);
+  a.budget = budget;
+  a.num_nodes = num_nodes;
+  a.temperature = temperature;
+  a.penalty = diversity_penalty;
+  a.tokens = tree_tokens;
+  a.parents = parents;
+  a.depth = depth;
+  a.pos_offset = pos_offset;
+  a.anc = anc;
+  a.n_children = n_children;
+  a.n_nodes = n_nodes;
+  a.scores = scores;
+  hipLaunchKernelGGL(sparse_tree_kernel, dim3(batch), dim3(64), 0, (hipStream_t)stream, a);
+  return fg::check_launch("fg_sparse_tree_layout");
 }
 
 }  // extern "C"

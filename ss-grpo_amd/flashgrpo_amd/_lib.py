@@ -30,8 +30,10 @@ SIGNATURES = {
     "fg_medusa_topk_workspace": (_SZ, [_I, _I, _I]),
     "fg_medusa_topk": (_I, [_P, _I, _I64, _I, _I, _I, _I, _P, _P, _P, _P, _SZ, _P]),
     "fg_tree_layout": (_I, [_P, _P, _I, _I, _P, _P, _P, _I, _P, _P, _I, _P]),
-    "fg_rope_kv_write": (_I, [_P, _I, _I64, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I64, _I64, _I, _P, _P,
-                              _P]),
+    "fg_sparse_tree_layout": (_I, [_P, _P, _I, _I, _I, _P, _P, _P, _I, _I, _F, C.c_double, _I, _P, _P, _P, _P, _P,
+                                   _P, _P, _P, _P]),
+    "fg_rope_kv_write": (_I, [_P, _I, _I64, _I, _I, _I, _I, _I, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I, _P,
+                              _P, _P]),
     "fg_tree_attention_workspace": (_SZ, [_I, _I, _I, _I, _I, _I]),
     "fg_tree_attention": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I64, _I64, _I, _P, _P, _P, _I64, _F, _P,
                                _SZ, _P]),

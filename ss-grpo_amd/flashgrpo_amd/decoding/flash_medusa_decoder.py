@@ -44,7 +44,8 @@ import torch
 from .. import kernels as K
 from .. import timing
 from ..models.target import TargetModel, as_mask_tensor, chain_bits
-from .medusa_tree import TreePlan, TreeTopology, dense_node_count, fit_topk_to_budget, plan_tree
+from .medusa_tree import (TreePlan, TreeTopology, dense_node_count, fit_topk_to_budget, plan_tree, sparse_tree_device,
+                          sparse_widths)
 
 
 @dataclass
@@ -89,6 +90,14 @@ class FlashMedusaConfig:
     # and next-round logits are identical to the packed projection; only nodes the
     # walk never reaches are skipped.
     lazy_walk_lm_head: bool = True
+    # tree_layout="sparse_asymmetric" (flashgrpo_b200/decoding/flash_medusa_decoder.py:65-73);
+    # the head-3 quality calibrator and its exploration rounds are not built: every
+    # row keeps head 3 (build_batch_trees accepts an explicit per-row gate).
+    sparse_nodes_by_head: tuple = (5, 4, 0)
+    sparse_min_head3_nodes: int = 0
+    sparse_head3_min_budget: int = 8
+    sparse_branch_score_temperature: float = 1.0
+    sparse_diversity_penalty: float = 0.05
 
 
 def _quantile(values: np.ndarray, q: float) -> float:
@@ -138,7 +147,12 @@ class FlashMedusaDecoder:
                          max_tree_nodes_per_seq=cfg.max_tree_nodes_per_seq, max_tree_depth=cfg.max_tree_depth,
                          fixed_tree_topk_by_depth=list(cfg.fixed_tree_topk_by_depth),
                          adaptive_tree_enabled=bool(cfg.adaptive_tree_enabled),
-                         adaptive_min_topk_by_depth=list(cfg.adaptive_min_topk_by_depth))
+                         adaptive_min_topk_by_depth=list(cfg.adaptive_min_topk_by_depth),
+                         sparse_nodes_by_head=list(cfg.sparse_nodes_by_head),
+                         sparse_min_head3_nodes=int(cfg.sparse_min_head3_nodes),
+                         sparse_head3_min_budget=int(cfg.sparse_head3_min_budget),
+                         sparse_branch_score_temperature=float(cfg.sparse_branch_score_temperature),
+                         sparse_diversity_penalty=float(cfg.sparse_diversity_penalty))
 
     def _topk_from_confidence(self, confidence: float, base_k: int, depth_idx: int) -> int:
         """``flash_medusa_decoder.py:341-360``."""
@@ -185,8 +199,12 @@ class FlashMedusaDecoder:
             adapted = fit_topk_to_budget(adapted, plan.node_budget_per_seq,
                                          min_topk_by_depth=list(cfg.adaptive_min_topk_by_depth)[:len(adapted)],
                                          depth_weight_decay=float(cfg.adaptive_depth_weight_decay))
-        new = TreePlan(plan.node_budget_per_seq, len(adapted), [max(1, int(k)) for k in adapted],
-                       dense_node_count(adapted), plan.mode, plan.layout)
+        ks = [max(1, int(k)) for k in adapted]
+        # a sparse plan takes the fitted list as its per-head node counts
+        # (flashgrpo_b200/decoding/flash_medusa_decoder.py:1063-1077)
+        new = TreePlan(plan.node_budget_per_seq, len(ks), ks, dense_node_count(ks), plan.mode, plan.layout,
+                       list(ks) if plan.layout == "sparse_asymmetric" else [], plan.min_head3_nodes,
+                       plan.head3_min_budget, plan.branch_score_temperature, plan.diversity_penalty)
         return new, {"confidence": confs, "topk": list(adapted)}
 
     def _chain_trees(self, r: "Rollout", roots: torch.Tensor, plan: TreePlan, Bc: int, record: bool):
@@ -352,7 +370,7 @@ class FlashMedusaDecoder:
         use_tree = r.generation_step >= int(cfg.enable_medusa_spec_after)
         plan = self._plan(Bc) if use_tree else TreePlan(1, 0, [], 1, cfg.tree_mode, cfg.tree_layout)
         use_chain = use_tree and cfg.proposal_mode == "chain" and r.generation_step >= int(cfg.chain_enable_after)
-        cand = score = mlog = tree_tokens = chain_conf = None
+        cand = score = mlog = tree_tokens = chain_conf = sparse = None
         chain_recs, chain_rows = [], []
         adaptive_stats = {}
         if plan.active_heads > 0 and use_chain:
@@ -373,42 +391,60 @@ class FlashMedusaDecoder:
             proj = self.medusa_heads.project_all(r.hidden, plan.active_heads)
             with timing.label("medusa"):
                 mlog = model.logits(proj)
-            cand, score, stats = K.medusa_topk(mlog, max(plan.topk_by_depth), stats=bool(cfg.adaptive_tree_enabled))
+            if plan.layout == "sparse_asymmetric":
+                # candidate lists of the sparse widths (adaptation only shrinks them)
+                kc = max(sparse_widths(list(plan.nodes_by_head or plan.topk_by_depth)[:3], mlog.shape[-1]))
+            else:
+                kc = max(plan.topk_by_depth)
+            cand, score, stats = K.medusa_topk(mlog, kc, stats=bool(cfg.adaptive_tree_enabled))
             r.sync()
             m["medusa_time"] += time.time() - t0
             if cfg.adaptive_tree_enabled:
                 both = torch.cat([stats.view(stats.shape[0], -1), score.view(score.shape[0], -1)], 1).cpu().numpy()
                 plan, adaptive_stats = self._adapt_plan(plan, both[:, :2], both[:, 2:], Bc)
-        topo = TreeTopology.for_plan(plan)
-        N = topo.num_nodes
+            if plan.layout == "sparse_asymmetric" and plan.active_heads > 0:
+                sparse = sparse_tree_device(roots, cand, score, plan, Bc, mlog.shape[-1])
+        if sparse is not None:
+            # per-row topology (b200 sparse_asymmetric): rows padded to the widest bound
+            tree_tokens = sparse["tokens"]
+            N = tree_tokens.shape[1]
+            D = min(3, plan.active_heads)
+            tv = dict(pos_offset=sparse["pos_offset"], anc=sparse["anc"], parents=sparse["parents"],
+                      n_nodes=sparse["n_nodes"], internal_rows=None, slot_map=None)
+        else:
+            topo = TreeTopology.for_plan(plan)
+            N = topo.num_nodes
+            D = topo.max_depth
         r.plan_last = {"B_cur": Bc, "node_budget_per_seq": plan.node_budget_per_seq,
                        "active_heads": plan.active_heads, "topk_by_depth": plan.topk_by_depth,
                        "actual_nodes": plan.actual_nodes,
                        "proposal_mode": ("chain" if use_chain else "medusa") if use_tree else "target_only",
                        "adaptive_tree": adaptive_stats}
         m["active_sum"] += Bc
-        m["node_sum"] += N
         m["samples"] += 1
-        for dpt, c in topo.depth_counts.items():
-            r.proposed_by_depth[dpt] = r.proposed_by_depth.get(dpt, 0) + c * Bc
-        dshared = topo.device(dev)
-        dmap = topo.device(dev, Bc)
-        if tree_tokens is not None:
-            assert tree_tokens.shape[1] == N, (tree_tokens.shape, N)
-        elif N > 1:
-            tree_tokens, _ = K.tree_layout(cand, score, Bc, roots, dshared["depth"], dshared["rank"], N)
-        else:
-            tree_tokens = roots.view(Bc, 1)
+        if sparse is None:
+            m["node_sum"] += N
+            for dpt, c in topo.depth_counts.items():
+                r.proposed_by_depth[dpt] = r.proposed_by_depth.get(dpt, 0) + c * Bc
+            dshared = topo.device(dev)
+            dmap = topo.device(dev, Bc)
+            tv = dict(pos_offset=dshared["pos_offset"], anc=dshared["anc"], parents=dmap["parents"],
+                      n_nodes=dmap["n_nodes"], internal_rows=dmap["internal_rows"], slot_map=dmap["slot_map"])
+            if tree_tokens is not None:
+                assert tree_tokens.shape[1] == N, (tree_tokens.shape, N)
+            elif N > 1:
+                tree_tokens, _ = K.tree_layout(cand, score, Bc, roots, dshared["depth"], dshared["rank"], N)
+            else:
+                tree_tokens = roots.view(Bc, 1)
         # ---------------- verify forward + tree LM head
         tree_logits = slot_map = hidden_t = walk_logits = walk = None
         lazy = bool(cfg.lazy_walk_lm_head) and N > 1
-        D = topo.max_depth
         if int(r.seq_h.max()) + N > r.cache.capacity:
             raise RuntimeError("KV cache capacity exceeded")  # unreachable: rows finish at max_length
         r.sync()
         t0 = time.time()
         try:
-            hidden_t = model.forward(tree_tokens, r.cache, pos_offset=dshared["pos_offset"], anc=dshared["anc"],
+            hidden_t = model.forward(tree_tokens, r.cache, pos_offset=tv["pos_offset"], anc=tv["anc"],
                                      seq_len=r.seq, row_map=r.row_map, err_flag=r.err)
             if N > 1:
                 m["tree_query_rows"] += Bc * N
@@ -416,9 +452,9 @@ class FlashMedusaDecoder:
                     walk_logits = torch.empty((D, Bc, model.cfg.vocab), dtype=model.dtype, device=dev)
                 else:
                     with timing.label("tree"):
-                        if cfg.project_internal_tree_logits_only:
-                            tree_logits = model.logits(hidden_t, row_index=dmap["internal_rows"])
-                            slot_map = dmap["slot_map"]
+                        if cfg.project_internal_tree_logits_only and tv["internal_rows"] is not None:
+                            tree_logits = model.logits(hidden_t, row_index=tv["internal_rows"])
+                            slot_map = tv["slot_map"]
                         else:
                             tree_logits = model.logits(hidden_t)
                     m["tree_lm_head_rows"] += tree_logits.shape[0]
@@ -437,16 +473,16 @@ class FlashMedusaDecoder:
         if walk_logits is not None:
             # Walk step t samples row b from the node its walk stands on; only those
             # rows are projected (inactive rows' tiles are skipped).
-            walk = K.walk_begin(tree_tokens, dmap["parents"], dmap["n_nodes"], acc_stride=D + 1)
+            walk = K.walk_begin(tree_tokens, tv["parents"], tv["n_nodes"], acc_stride=D + 1)
             for t in range(D):
                 K.walk_rows(walk, N)
                 with timing.label("tree"):
                     model.logits(hidden_t, row_index=walk["row_index"], row_active=walk["row_active"],
                                  out=walk_logits[t])
-                K.walk_step(walk, walk_logits[t], tree_tokens, dmap["parents"], dmap["n_nodes"], walk_step=t,
+                K.walk_step(walk, walk_logits[t], tree_tokens, tv["parents"], tv["n_nodes"], walk_step=t,
                             **walk_kw)
         elif tree_logits is not None:
-            walk = K.accept_walk(tree_logits, tree_tokens, dmap["parents"], dmap["n_nodes"], max_walk_steps=D,
+            walk = K.accept_walk(tree_logits, tree_tokens, tv["parents"], tv["n_nodes"], max_walk_steps=D,
                                  slot_map=slot_map, **walk_kw)
         else:
             zeros = torch.zeros(Bc, dtype=torch.int32, device=dev)
@@ -464,6 +500,11 @@ class FlashMedusaDecoder:
             cols += [walk["state"][2 * Bc:].view(-1, 1), walk["acc_nodes"]]
         if b200:
             cols.append(new_pending.view(-1, 1))
+        if sparse is not None:
+            # last node is a leaf; nodes per row; non-root nodes per depth 2..D+1
+            leaf_d = sparse["n_children"].gather(1, walk["last_node"].long().view(-1, 1)) == 0
+            per_depth = (sparse["depth"].unsqueeze(2) == torch.arange(2, D + 2, device=dev, dtype=torch.int32)).sum(1)
+            cols += [leaf_d.to(torch.int32), sparse["n_nodes"].view(-1, 1), per_depth.to(torch.int32)]
         pack = torch.cat(cols, dim=1).cpu().numpy()
         m["accept_time"] += time.time() - t_acc
         if chain_conf is not None:
@@ -480,6 +521,14 @@ class FlashMedusaDecoder:
             m["tree_lm_head_rows"] += int(np.sum(walk_last_h + 1))
         if b200:
             m["corrections"] += int(np.count_nonzero(pack[:, col] >= 0))
+        sparse_leaf_h = None
+        proposed_before = sum(r.proposed_by_depth.get(j + 2, 0) for j in range(D))
+        if sparse is not None:
+            c0 = col + (1 if b200 else 0)
+            sparse_leaf_h = pack[:, c0].astype(bool)
+            m["node_sum"] += float(pack[:, c0 + 1].mean())
+            for j in range(D):
+                r.proposed_by_depth[j + 2] = r.proposed_by_depth.get(j + 2, 0) + int(pack[:, c0 + 2 + j].sum())
         if trace is not None:
             rec = dict(round=rnd, active=list(r.active), plan=list(plan.topk_by_depth),
                        budget=plan.node_budget_per_seq, seq_len=r.seq.cpu().numpy().copy(),
@@ -494,6 +543,10 @@ class FlashMedusaDecoder:
                                      logits=c["logits"].float().cpu().numpy(), cand=c["cand"].cpu().numpy(),
                                      parent_local=c.get("parent_local"), rank=c.get("rank")) for c in chain_recs]
                 rec["chain_budget"] = plan.node_budget_per_seq
+            if sparse is not None:
+                rec["sparse"] = {k: sparse[k].cpu().numpy() for k in ("parents", "depth", "n_nodes", "n_children",
+                                                                       "pos_offset", "anc")}
+                rec["sparse_plan"] = list(plan.nodes_by_head)
             if tree_logits is not None:
                 rec["tree_logits"] = tree_logits.float().cpu().numpy()
                 rec["slot_map"] = None if slot_map is None else slot_map.cpu().numpy()
@@ -527,7 +580,10 @@ class FlashMedusaDecoder:
                 else:
                     slots = slot_map[ar, last]
                     r.logits = tree_logits.index_select(0, slots.clamp_min(0).long())
-                leaf = np.nonzero(np.array([topo.slot_of[int(n)] < 0 for n in last_h]))[0]
+                if sparse_leaf_h is not None:
+                    leaf = np.nonzero(sparse_leaf_h)[0]
+                else:
+                    leaf = np.nonzero(np.array([topo.slot_of[int(n)] < 0 for n in last_h]))[0]
                 if leaf.size:
                     li = torch.from_numpy(leaf).to(dev)
                     with timing.label("leaf"):
@@ -570,11 +626,15 @@ class FlashMedusaDecoder:
         r.seq_h = r.seq_h + acc_len_h
         if walk_last_h is not None:
             draws = walk_last_h.astype(np.int64) + 1
+        elif N > 1 and sparse_leaf_h is not None:
+            draws = acc_len_h.astype(np.int64) - sparse_leaf_h.astype(np.int64)
         elif N > 1:
             draws = np.array([int(a) - (1 if topo.slot_of[int(n)] < 0 else 0) for a, n in zip(acc_len_h, last_h)])
         else:
             draws = np.zeros(Bc, dtype=np.int64)
-        r.last_round = dict(num_nodes=N, internal=len(topo.internal), acc_len=acc_len_h.copy(),
+        # internal = LM-head rows per sequence of the packed projection (all N for sparse trees)
+        r.last_round = dict(num_nodes=N, internal=N if sparse is not None else len(topo.internal),
+                            acc_len=acc_len_h.copy(),
                             last_node=last_h.copy(), walk_draws=draws, heads=plan.active_heads, batch=Bc,
                             lazy=walk_last_h is not None, walk_steps=D if walk_last_h is not None else 0,
                             chain_rows=list(chain_rows))
@@ -595,7 +655,10 @@ class FlashMedusaDecoder:
         m["total_acc_length"] += emitted
         m["total_decoded_steps"] += Bc
         m["accepted"] += int(np.maximum(lens - 1, 0).sum())
-        m["proposed"] += max(N - 1, 0) * Bc
+        if sparse is not None:
+            m["proposed"] += sum(r.proposed_by_depth.get(j + 2, 0) for j in range(D)) - proposed_before
+        else:
+            m["proposed"] += max(N - 1, 0) * Bc
         if fin_h.any():
             keep = np.nonzero(~fin_h)[0]
             if keep.size == 0:

@@ -56,6 +56,12 @@ class TreePlan:
     actual_nodes: int
     mode: str
     layout: str
+    # sparse_asymmetric layout (flashgrpo_b200/decoding/medusa_tree.py:49-60)
+    nodes_by_head: list = field(default_factory=list)
+    min_head3_nodes: int = 0
+    head3_min_budget: int = 8
+    branch_score_temperature: float = 1.0
+    diversity_penalty: float = 0.0
 
 
 def dense_node_count(topk_by_depth) -> int:
@@ -96,11 +102,32 @@ def fit_topk_to_budget(topk_by_depth, node_budget, *, min_topk_by_depth=None, de
 
 def plan_tree(*, active_batch_size, num_medusa_heads, tree_mode, tree_layout, cpeak_nodes, min_tree_nodes_per_seq,
               max_tree_nodes_per_seq, max_tree_depth, fixed_tree_topk_by_depth, adaptive_tree_enabled=False,
-              adaptive_min_topk_by_depth=None) -> TreePlan:
+              adaptive_min_topk_by_depth=None, sparse_nodes_by_head=None, sparse_min_head3_nodes=1,
+              sparse_head3_min_budget=8, sparse_branch_score_temperature=1.0,
+              sparse_diversity_penalty=0.05) -> TreePlan:
     """Per-step plan (``medusa_tree.py:102-178``): fixed, or concurrency-aware with a
-    ``floor(cpeak_nodes / B)`` node budget clamped to [min, max] nodes per sequence."""
-    if tree_layout not in {"dense", "sparse"}:
+    ``floor(cpeak_nodes / B)`` node budget clamped to [min, max] nodes per sequence.
+
+    ``tree_layout="sparse_asymmetric"`` (``flashgrpo_b200/decoding/medusa_tree.py:342-458``)
+    keeps the dense plan's budget and replaces its branching by per-head node counts
+    (``sparse_allocation``); ``"sparse"`` stays the v1 mapping to dense."""
+    if tree_layout not in {"dense", "sparse", "sparse_asymmetric"}:
         raise ValueError(f"Unsupported tree_layout={tree_layout}")
+    if tree_layout == "sparse_asymmetric":
+        dense = plan_tree(active_batch_size=active_batch_size, num_medusa_heads=num_medusa_heads,
+                          tree_mode=tree_mode, tree_layout="dense", cpeak_nodes=cpeak_nodes,
+                          min_tree_nodes_per_seq=min_tree_nodes_per_seq, max_tree_nodes_per_seq=max_tree_nodes_per_seq,
+                          max_tree_depth=max_tree_depth, fixed_tree_topk_by_depth=fixed_tree_topk_by_depth,
+                          adaptive_tree_enabled=adaptive_tree_enabled,
+                          adaptive_min_topk_by_depth=adaptive_min_topk_by_depth)
+        max_heads = min(int(num_medusa_heads), max(0, int(max_tree_depth) - 1))
+        requested = list(sparse_nodes_by_head or fixed_tree_topk_by_depth or [4, 3, 2])
+        counts = sparse_allocation(dense.node_budget_per_seq, max_heads, requested, sparse_min_head3_nodes,
+                                   sparse_head3_min_budget)
+        return TreePlan(dense.node_budget_per_seq, len(counts), list(counts), 1 + sum(counts), tree_mode,
+                        "sparse_asymmetric", list(counts), max(0, int(sparse_min_head3_nodes)),
+                        max(1, int(sparse_head3_min_budget)), max(1e-6, float(sparse_branch_score_temperature)),
+                        max(0.0, float(sparse_diversity_penalty)))
     if tree_layout == "sparse":
         warnings.warn("flashgrpo tree_layout='sparse' is a v1 skeleton; falling back to dense.", RuntimeWarning)
         tree_layout = "dense"
@@ -144,6 +171,64 @@ def plan_tree(*, active_batch_size, num_medusa_heads, tree_mode, tree_layout, cp
     else:
         raise ValueError(f"Unsupported tree_mode={tree_mode}")
     return TreePlan(budget, len(ks), ks, dense_node_count(ks), tree_mode, tree_layout)
+
+
+def sparse_allocation(budget, max_heads, requested, min_head3_nodes, head3_min_budget) -> list:
+    """Per-head node counts of a sparse asymmetric tree
+    (``flashgrpo_b200/decoding/medusa_tree.py:411-444``).
+
+    Heads take their requested counts in order out of the ``budget - 1`` non-root
+    slots. If head 3 was requested and the budget reaches ``head3_min_budget``,
+    head 2 and then head 1 hand over nodes (keeping one each) until head 3 holds
+    ``max(1, min_head3_nodes)``. Heads after the last non-empty one are dropped."""
+    counts = []
+    left = max(0, int(budget) - 1)
+    for h in range(max_heads):
+        take = min(max(0, int(requested[h]) if h < len(requested) else 0), left)
+        counts.append(take)
+        left -= take
+    if max_heads >= 3 and budget >= int(head3_min_budget) and len(requested) >= 3 and int(requested[2]) > 0:
+        short = max(0, max(1, int(min_head3_nodes)) - counts[2])
+        for donor in (1, 0):
+            give = min(short, max(0, counts[donor] - 1))
+            counts[donor] -= give
+            counts[2] += give
+            short -= give
+            if short == 0:
+                break
+    last = max((h + 1 for h, c in enumerate(counts) if c > 0), default=0)
+    return counts[:last]
+
+
+def sparse_widths(nodes_by_head, vocab) -> list:
+    """Top-k candidates taken per head: heads 1 and 2 hold head 3's count in reserve
+    (``flashgrpo_b200/decoding/medusa_tree.py:569-579``)."""
+    spare = nodes_by_head[2] if len(nodes_by_head) >= 3 else 0
+    return [max(1, min(int(c) + (spare if h < 2 else 0), int(vocab))) for h, c in enumerate(nodes_by_head)]
+
+
+def sparse_max_nodes(plan: TreePlan) -> int:
+    """Upper bound of a sparse tree's node count (the verify width): root, the head
+    counts of the first three heads, and at most head 3's count of leftover head-1
+    candidates, cut at the budget."""
+    nodes = list(plan.nodes_by_head or plan.topk_by_depth)[: min(3, plan.active_heads)]
+    spare = nodes[2] if len(nodes) >= 3 else 0
+    return max(1, min(int(plan.node_budget_per_seq), 1 + sum(nodes) + spare))
+
+
+def sparse_tree_device(roots: torch.Tensor, cand_tokens: torch.Tensor, cand_scores: torch.Tensor, plan: TreePlan,
+                       batch: int, vocab: int, *, head3_gate=None, scores=False) -> dict:
+    """Device sparse trees of a batch (``fg_sparse_tree_layout``): tokens, parents,
+    depth, pos_offset, anc, n_children [batch, N] and n_nodes [batch] with
+    N = ``sparse_max_nodes(plan)``; rows with fewer nodes are padded."""
+    nodes = list(plan.nodes_by_head or plan.topk_by_depth)[: plan.active_heads]
+    N = sparse_max_nodes(plan)
+    if N > 64:
+        raise ValueError("tree nodes exceed the 64-node limit of the ancestor bit masks")
+    return K.sparse_tree_layout(cand_tokens, cand_scores, batch, roots.to(torch.int32), nodes, vocab=vocab,
+                                budget=plan.node_budget_per_seq, num_nodes=N,
+                                temperature=plan.branch_score_temperature,
+                                diversity_penalty=plan.diversity_penalty, head3_gate=head3_gate, scores=scores)
 
 
 # ------------------------------------------------------------------ device topology
@@ -255,10 +340,17 @@ def _trees_from_device(tokens: torch.Tensor, scores: torch.Tensor, topo: TreeTop
             for t, s in zip(toks, scs)]
 
 
-def build_batch_trees(root_tokens: torch.Tensor, medusa_logits: list, plan: TreePlan) -> list:
+def build_batch_trees(root_tokens: torch.Tensor, medusa_logits: list, plan: TreePlan, *,
+                      head3_gate_mask: torch.Tensor | None = None) -> list:
     """Dense Medusa trees for a batch (``medusa_tree.py:228-278``): one device top-k
-    over all depths, one layout launch, then the CandidateTree objects."""
+    over all depths, one layout launch, then the CandidateTree objects.
+
+    A ``sparse_asymmetric`` plan builds the b200 sparse trees instead
+    (``flashgrpo_b200/decoding/medusa_tree.py:731-749``); ``head3_gate_mask``
+    [batch] bool switches head 3 off per row (None: every row keeps it)."""
     batch = int(root_tokens.shape[0])
+    if plan.layout == "sparse_asymmetric":
+        return _sparse_batch_trees(root_tokens, medusa_logits, plan, head3_gate_mask)
     depths = []
     for d, k in enumerate(plan.topk_by_depth[: plan.active_heads]):
         if d >= len(medusa_logits):
@@ -278,6 +370,30 @@ def build_batch_trees(root_tokens: torch.Tensor, medusa_logits: list, plan: Tree
     cand, score, _ = K.medusa_topk(stacked, max(depths))
     tokens, scores = build_tree_tokens(root_tokens, cand, score, topo, batch)
     return _trees_from_device(tokens, scores, topo)
+
+
+def _sparse_batch_trees(root_tokens, medusa_logits, plan, head3_gate_mask) -> list:
+    batch = int(root_tokens.shape[0])
+    heads = min(int(plan.active_heads), len(plan.nodes_by_head or plan.topk_by_depth), len(medusa_logits))
+    if heads == 0:
+        return [CandidateTree(tokens=[int(t)], parents=[-1], depths=[1], scores=[0.0])
+                for t in root_tokens.reshape(-1).tolist()]
+    if root_tokens.device.type != "cuda":
+        raise ValueError("build_batch_trees: device tensors required (HIP path)")
+    plan_h = TreePlan(plan.node_budget_per_seq, heads, list(plan.topk_by_depth)[:heads], plan.actual_nodes, plan.mode,
+                      plan.layout, list(plan.nodes_by_head or plan.topk_by_depth)[:heads], plan.min_head3_nodes,
+                      plan.head3_min_budget, plan.branch_score_temperature, plan.diversity_penalty)
+    vocab = int(medusa_logits[0].shape[-1])
+    used = min(heads, 3)
+    widths = sparse_widths(plan_h.nodes_by_head, vocab)[:used]
+    stacked = torch.cat([medusa_logits[h] for h in range(used)], dim=0)
+    cand, score, _ = K.medusa_topk(stacked, max(widths))
+    d = sparse_tree_device(root_tokens, cand, score, plan_h, batch, vocab, head3_gate=head3_gate_mask, scores=True)
+    n = d["n_nodes"].cpu().tolist()
+    toks, pars, deps = d["tokens"].cpu().tolist(), d["parents"].cpu().tolist(), d["depth"].cpu().tolist()
+    scs = d["scores"].cpu().tolist()
+    return [CandidateTree(tokens=toks[b][:n[b]], parents=pars[b][:n[b]], depths=deps[b][:n[b]], scores=scs[b][:n[b]])
+            for b in range(batch)]
 
 
 def build_dense_tree(root_token: int, medusa_logits: list, plan: TreePlan) -> CandidateTree:

@@ -6,6 +6,7 @@ device work happens in the HIP kernels of ``ss-grpo_amd/csrc``.
 """
 from __future__ import annotations
 
+import ctypes as C
 import math
 
 import torch
@@ -168,6 +169,45 @@ def tree_layout(cand_tokens, cand_scores, batch, roots, node_depth, node_rank, n
     return out_tokens, out_scores
 
 
+def sparse_tree_layout(cand_tokens, cand_scores, batch, roots, nodes_by_head, *, vocab, budget, num_nodes,
+                       temperature=1.0, diversity_penalty=0.0, head3_gate=None, scores=False):
+    """Sparse asymmetric trees on the device (``fg_sparse_tree_layout``).
+
+    cand_tokens/cand_scores: [heads*batch, kstride] top-k lists (head-major rows).
+    Returns a dict of [batch, num_nodes] int32 ``tokens``, ``parents``, ``depth``,
+    ``pos_offset``, ``n_children``, int64 ``anc`` bit masks, ``n_nodes`` [batch], and
+    with ``scores`` the fp64 path scores [batch, num_nodes].
+    """
+    _dev(cand_tokens, cand_scores, roots, head3_gate)
+    _i32(cand_tokens, "cand_tokens")
+    _i32(roots, "roots")
+    nodes = [int(n) for n in nodes_by_head]
+    if not nodes:
+        raise ValueError("sparse_tree_layout: no heads")
+    if cand_tokens.shape[0] < min(len(nodes), 3) * batch or cand_scores.shape != cand_tokens.shape:
+        raise ValueError("sparse_tree_layout: candidate rows missing")
+    if not (cand_tokens.is_contiguous() and cand_scores.is_contiguous() and cand_scores.dtype == torch.float32):
+        raise ValueError("sparse_tree_layout: contiguous int32 tokens and fp32 scores required")
+    if head3_gate is not None:
+        if head3_gate.dtype not in (torch.bool, torch.uint8) or head3_gate.numel() != batch:
+            raise ValueError("sparse_tree_layout: head3_gate must be bool/uint8 [batch]")
+        head3_gate = head3_gate.contiguous().view(torch.uint8)
+    dev = roots.device
+    i32 = dict(dtype=torch.int32, device=dev)
+    out = dict(tokens=torch.empty(batch, num_nodes, **i32), parents=torch.empty(batch, num_nodes, **i32),
+               depth=torch.empty(batch, num_nodes, **i32), pos_offset=torch.empty(batch, num_nodes, **i32),
+               anc=torch.empty(batch, num_nodes, dtype=torch.int64, device=dev),
+               n_children=torch.empty(batch, num_nodes, **i32), n_nodes=torch.empty(batch, **i32),
+               scores=torch.empty(batch, num_nodes, dtype=torch.float64, device=dev) if scores else None)
+    nodes_arr = (C.c_int32 * len(nodes))(*nodes)
+    _call("fg_sparse_tree_layout", _ptr(cand_tokens), _ptr(cand_scores), cand_tokens.shape[1], batch, int(vocab),
+          _ptr(roots), _ptr(head3_gate), C.cast(nodes_arr, C.c_void_p), len(nodes), int(budget), float(temperature),
+          float(diversity_penalty), num_nodes, _ptr(out["tokens"]), _ptr(out["parents"]), _ptr(out["depth"]),
+          _ptr(out["pos_offset"]), _ptr(out["anc"]), _ptr(out["n_children"]), _ptr(out["n_nodes"]),
+          _ptr(out["scores"]), _stream())
+    return out
+
+
 # ------------------------------------------------------------------ verify forward pieces
 def rope_kv_write(qkv, *, batch, num_nodes, q_heads, kv_heads, head_dim, seq_len, pos_offset, inv_freq, q_out,
                   k_cache, v_cache, row_map=None, err_flag=None):
@@ -177,8 +217,17 @@ def rope_kv_write(qkv, *, batch, num_nodes, q_heads, kv_heads, head_dim, seq_len
     _i32(row_map, "row_map")
     if k_cache.stride(-1) != 1 or k_cache.stride(-2) != head_dim:
         raise ValueError("rope_kv_write: cache rows must be contiguous [.., capacity, d]")
+    if pos_offset.dim() == 2:
+        if tuple(pos_offset.shape) != (batch, num_nodes) or not pos_offset.is_contiguous():
+            raise ValueError("rope_kv_write: per-sequence pos_offset must be contiguous [batch, num_nodes]")
+        pos_stride = num_nodes
+    else:
+        if pos_offset.numel() < num_nodes:
+            raise ValueError("rope_kv_write: pos_offset shorter than num_nodes")
+        pos_stride = 0
     _call("fg_rope_kv_write", _ptr(qkv), dtype_code(qkv), qkv.stride(0), batch, num_nodes, q_heads, kv_heads,
-              head_dim, _ptr(seq_len), _ptr(pos_offset), _ptr(inv_freq), _ptr(q_out), _ptr(k_cache), _ptr(v_cache),
+              head_dim, _ptr(seq_len), _ptr(pos_offset), pos_stride, _ptr(inv_freq), _ptr(q_out), _ptr(k_cache),
+              _ptr(v_cache),
               k_cache.stride(0), k_cache.stride(1), k_cache.shape[-2], _ptr(row_map), _ptr(err_flag), _stream())
 
 

@@ -271,8 +271,8 @@ class TargetModel:
                 err_flag: torch.Tensor | None = None) -> torch.Tensor:
         """Forward N new tokens per row after each row's committed prefix.
 
-        tokens [B, N] int (device); pos_offset [N] int32: position = seq_len[b] + pos_offset[n];
-        anc: int64 bit masks [N] (shared) or [B, N]; node n's K/V land in cache slot
+        tokens [B, N] int (device); pos_offset int32 [N] (shared) or [B, N]: position =
+        seq_len[b] + pos_offset[(b,) n]; anc: int64 bit masks [N] (shared) or [B, N]; node n's K/V land in cache slot
         seq_len[b] + n of cache row row_map[b]. Returns final-normed hidden [B, N, H].
         ``seq_len`` defaults to ``cache.seq_len`` and is not advanced here.
         """

@@ -189,13 +189,26 @@ def lockstep(trace, ocfg, Wr, heads_r, spec, prompts, dtype, seed, max_length, e
             if "medusa_logits" in rec:
                 ml = rec["medusa_logits"]
                 heads_logits = list(ml.reshape(ml.shape[0] // Bc, Bc, -1))
-            trees = OT.build_batch_trees(rec["roots"], heads_logits, plan)
-            assert rec["tree_tokens"].tolist() == [t.tokens for t in trees], rnd
-        N = trees[0].node_count
+            if plan.layout == "sparse_asymmetric" and plan.active_heads:
+                # per-row trees, padded to the widest bound
+                trees = OT.build_sparse_trees(rec["roots"], heads_logits, plan)
+                sp = rec["sparse"]
+                assert rec["sparse_plan"] == list(plan.nodes_by_head), rnd
+                for i, t in enumerate(trees):
+                    n = t.node_count
+                    assert int(sp["n_nodes"][i]) == n, (rnd, i)
+                    assert rec["tree_tokens"][i, :n].tolist() == t.tokens, (rnd, i)
+                    assert sp["parents"][i, :n].tolist() == t.parents, (rnd, i)
+                    assert sp["depth"][i, :n].tolist() == t.depths, (rnd, i)
+                stats["sparse_shapes"] = stats.get("sparse_shapes", set()) | {tuple(t.parents) for t in trees}
+            else:
+                trees = OT.build_batch_trees(rec["roots"], heads_logits, plan)
+                assert rec["tree_tokens"].tolist() == [t.tokens for t in trees], rnd
+        N = rec["tree_tokens"].shape[1]
         if "tree_hidden" in rec:
             for i, s in enumerate(active):
                 want_h = rows[s].tree(trees[i].tokens, trees[i].parents, trees[i].depths)
-                assert rel(rec["tree_hidden"][i], want_h) < tol, (rnd, s)
+                assert rel(rec["tree_hidden"][i][:trees[i].node_count], want_h) < tol, (rnd, s)
             nz = [[OS.counter_noise(seed, rnd, s, 1 + t) for t in range(N)] for s in active]
         if "walk_logits" in rec:  # lazy: one projected row per walk step and sequence
             slots = None
@@ -266,7 +279,12 @@ def _run(ocfg, spec, *, dtype, B0, repeats, P, max_length, seed=123, wseed=0, ca
                             adaptive_confidence_quantile=spec.adaptive_confidence_quantile,
                             adaptive_confidence_low=spec.adaptive_confidence_low,
                             adaptive_confidence_high=spec.adaptive_confidence_high,
-                            adaptive_min_topk_by_depth=spec.adaptive_min_topk_by_depth)
+                            adaptive_min_topk_by_depth=spec.adaptive_min_topk_by_depth,
+                            tree_layout=spec.tree_layout, sparse_nodes_by_head=spec.sparse_nodes_by_head,
+                            sparse_min_head3_nodes=spec.sparse_min_head3_nodes,
+                            sparse_head3_min_budget=spec.sparse_head3_min_budget,
+                            sparse_branch_score_temperature=spec.sparse_branch_score_temperature,
+                            sparse_diversity_penalty=spec.sparse_diversity_penalty)
     dec = FlashMedusaDecoder(model, mh, Tok(spec.eos_token_id), cfg)
     rng = np.random.default_rng(wseed + 7)
     prompts = rng.integers(0, ocfg.vocab, (B0, P))
@@ -384,3 +402,31 @@ def test_lockstep_bf16_8b_chain_geometry():
     out, st = _run(cfg, spec, dtype=torch.bfloat16, B0=2, repeats=2, P=40, max_length=40 + 6)
     assert st["chain_rounds"] == st["rounds"] >= 3
     assert out["last_tree_plan"]["node_budget_per_seq"] == 48
+
+
+@pytest.mark.parametrize("dtype,lazy,b200", [(torch.float32, True, False), (torch.float32, False, True),
+                                             (torch.bfloat16, True, False)])
+def test_lockstep_sparse_asymmetric_tree(dtype, lazy, b200):
+    """b200 sparse_asymmetric trees (per-row parents, rows padded to the widest bound):
+    trees, verify hidden states, walk, extraction and next state against the oracle."""
+    spec = OD.DecodeSpec(tree_mode="fixed", max_tree_nodes_per_seq=14, fixed_tree_topk_by_depth=(4, 3, 2),
+                         num_medusa_heads=3, max_tree_depth=4, top_p=0.95, tree_layout="sparse_asymmetric",
+                         sparse_nodes_by_head=(3, 4, 3), sparse_min_head3_nodes=1, sparse_diversity_penalty=0.3,
+                         sparse_branch_score_temperature=0.8, emit_correction_token=b200)
+    cfg = SMALL16 if dtype == torch.bfloat16 else SMALL  # the bf16 attention takes head_dim 128
+    out, st = _run(cfg, spec, dtype=dtype, B0=3, repeats=2, P=33, max_length=33 + 24, lazy=lazy)
+    assert st["max_acc"] >= 2
+    assert len(st["sparse_shapes"]) > 1  # rows really differ in topology
+    assert out["kv_extraction_success_count"] == st["rounds"]
+    assert out["last_tree_plan"]["topk_by_depth"] == [3, 4, 3]
+
+
+def test_lockstep_sparse_adaptive_concurrency():
+    """Adaptive sparse plan: the confidence-fitted list becomes the per-head node counts
+    (flashgrpo_b200/decoding/flash_medusa_decoder.py:1063-1095)."""
+    spec = OD.DecodeSpec(tree_mode="concurrency_aware", cpeak_nodes=96, max_tree_nodes_per_seq=20,
+                         fixed_tree_topk_by_depth=(4, 3, 2), num_medusa_heads=3, max_tree_depth=4, top_p=1.0,
+                         tree_layout="sparse_asymmetric", sparse_nodes_by_head=(5, 4, 2), sparse_min_head3_nodes=1,
+                         adaptive_tree_enabled=True, adaptive_confidence_low=0.05, adaptive_confidence_high=0.2)
+    out, st = _run(SMALL, spec, dtype=torch.float32, B0=2, repeats=3, P=20, max_length=20 + 24)
+    assert st["rounds"] > 0 and out["kv_extraction_success_count"] == st["rounds"]

@@ -186,6 +186,73 @@ def test_tree_layout_matches_oracle_trees():
             assert np.allclose(to_np(scores[b]), np.array(t.scores, np.float32))
 
 
+SPARSE_CASES = [  # nodes_by_head, budget, vocab, temperature, penalty, gate
+    ([4, 3, 2], 10, 17, 1.0, 0.05, None),
+    ([4, 3, 2], 32, 300, 0.7, 0.05, "random"),
+    ([5, 4], 16, 500, 1.0, 0.0, None),
+    ([3, 4, 3], 14, 64, 1.0, 0.3, "random"),
+    ([6, 0, 3], 12, 40, 1.3, 0.05, None),
+    ([2, 2, 2, 2], 9, 50, 1.0, 0.05, "random"),
+    ([4, 3, 2], 8, 5, 1.0, 0.05, None),
+    ([3], 8, 100, 1.0, 0.05, None),
+    ([8, 8, 8], 40, 1000, 0.5, 0.01, "random"),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("case", range(len(SPARSE_CASES)))
+def test_sparse_tree_layout_matches_oracle(dtype, case):
+    """fg_sparse_tree_layout (flashgrpo_b200/decoding/medusa_tree.py:509-685) against the
+    oracle's greedy builder: tokens, parents, depths, node counts and fp64 path scores
+    bit-exact, including ties, NaN rows, a per-row head-3 gate and vocabularies
+    narrower than the head widths."""
+    from flashgrpo_amd.decoding.medusa_tree import TreePlan, sparse_max_nodes, sparse_tree_device, sparse_widths
+
+    nodes, budget, V, temp, pen, gate = SPARSE_CASES[case]
+    B = 11
+    rng = np.random.default_rng(100 + case)
+    heads = min(len(nodes), 3)
+    x = rng.standard_normal((heads * B, V)).astype(np.float32)
+    x[:3] = np.round(x[:3] * 2) / 2          # ties inside a row and across parents
+    if heads >= 2:
+        x[B + 1, : V // 2] = np.nan          # a head-2 row with NaN candidates
+    x[4] = 0.0                               # an all-equal row
+    xd = torch.from_numpy(x).to(dtype).to(DEV)
+    xs = to_np(xd).astype(np.float32)
+    roots = rng.integers(0, V, B)
+    g = rng.random(B) < 0.5 if gate == "random" else None
+    plan = TreePlan(budget, len(nodes), list(nodes), 1 + sum(nodes), "fixed", "sparse_asymmetric", list(nodes), 1, 8,
+                    temp, pen)
+    oplan = OT.Plan(budget, len(nodes), list(nodes), 1 + sum(nodes), "fixed", "sparse_asymmetric", list(nodes), 1, 8,
+                    temp, pen)
+    want = OT.build_sparse_trees(roots, [xs[h * B:(h + 1) * B] for h in range(heads)], oplan,
+                                 None if g is None else g.tolist())
+    kc = max(sparse_widths(nodes[:3], V))
+    tok, sc, _ = K().medusa_topk(xd, kc)
+    gd = None if g is None else torch.from_numpy(g).to(DEV)
+    d = sparse_tree_device(torch.from_numpy(roots.astype(np.int32)).to(DEV), tok, sc, plan, B, V, head3_gate=gd,
+                           scores=True)
+    N = sparse_max_nodes(plan)
+    assert d["tokens"].shape == (B, N)
+    got = {k: v.cpu().numpy() for k, v in d.items()}
+    for b, t in enumerate(want):
+        n = t.node_count
+        assert n <= N
+        assert int(got["n_nodes"][b]) == n, b
+        assert got["tokens"][b, :n].tolist() == t.tokens, b
+        assert got["parents"][b, :n].tolist() == t.parents, b
+        assert got["depth"][b, :n].tolist() == t.depths, b
+        assert got["scores"][b, :n].tolist() == t.scores, b
+        assert got["pos_offset"][b, :n].tolist() == [x - 1 for x in t.depths]
+        bits = OT.ancestor_bits(t.parents)
+        assert [int(v) & 0xFFFFFFFFFFFFFFFF for v in got["anc"][b, :n]] == bits, b
+        assert got["n_children"][b, :n].tolist() == [len(t.children(i)) for i in range(n)]
+        # padding: self-only mask, never a child, offset 0
+        assert got["parents"][b, n:].tolist() == [-1] * (N - n)
+        assert [int(v) & 0xFFFFFFFFFFFFFFFF for v in got["anc"][b, n:]] == [1 << i for i in range(n, N)]
+        assert not got["pos_offset"][b, n:].any()
+
+
 # ------------------------------------------------------------------ sampling
 MODES = [dict(), dict(temperature=0.7), dict(temperature=1.3, top_p=0.95), dict(top_p=0.5), dict(top_k=5),
          dict(top_k=50, top_p=0.8, temperature=0.9), dict(greedy=True), dict(temperature=0.0),

@@ -103,11 +103,43 @@ def test_greedy_speculation_equals_greedy_decoding_medusa_and_chain():
     cell = OM.random_chain_cell(CFG.hidden, seed=6, std=0.3, gate_init=-1.0)
     prompts = np.random.default_rng(4).integers(0, CFG.vocab, (2, 5))
     ref = _greedy_reference(W, prompts, 12)
-    for mode, boot in [("medusa", True), ("chain", True), ("chain", False)]:
+    for mode, boot, layout in [("medusa", True, "dense"), ("chain", True, "dense"), ("chain", False, "dense"),
+                               ("medusa", True, "sparse_asymmetric")]:
         spec = OD.DecodeSpec(tree_mode="fixed", max_tree_nodes_per_seq=12, fixed_tree_topk_by_depth=(3, 2, 1),
-                             do_sample=False, proposal_mode=mode, chain_bootstrap_from_medusa=boot)
+                             do_sample=False, proposal_mode=mode, chain_bootstrap_from_medusa=boot,
+                             tree_layout=layout, sparse_nodes_by_head=(3, 4, 2), sparse_min_head3_nodes=1)
         gen = OD.generate(CFG, W, heads, prompts, spec, max_length=17, seed=3, cell=cell)
-        assert gen == ref, mode
+        assert gen == ref, (mode, layout)
+
+
+def test_sparse_round_extract_equals_recompute_with_row_topologies():
+    """Sparse trees differ per row (greedy parent choice, leftover head-1 nodes), so rows
+    are padded to the widest tree; extraction must still equal a recompute."""
+    W, heads = _setup(8)
+    prompts = np.random.default_rng(9).integers(0, CFG.vocab, (4, 6))
+    spec = OD.DecodeSpec(tree_mode="fixed", max_tree_nodes_per_seq=14, fixed_tree_topk_by_depth=(4, 3, 2),
+                         tree_layout="sparse_asymmetric", sparse_nodes_by_head=(3, 4, 3), sparse_min_head3_nodes=1,
+                         sparse_diversity_penalty=0.3, top_p=1.0)
+    st = OD.prefill_state(CFG, W, prompts, 96)
+    hist = [list(p) for p in prompts]
+    shapes, deep = set(), 0
+    for rnd in range(5):
+        out = OD.verify_round(CFG, W, heads, st, spec, seed=4, rnd=rnd, max_length=90)
+        assert out["plan"].nodes_by_head == [3, 4, 3]
+        for t in out["trees"]:
+            shapes.add(tuple(t.parents))
+            assert t.node_count <= 14 and all(0 <= p < n for n, p in enumerate(t.parents) if n)
+        for b in range(4):
+            hist[b].extend(out["acc_tokens"][b])
+            deep = max(deep, len(out["acc_tokens"][b]))
+            hid, ks, vs = OM.prefill(CFG, W, np.array([hist[b]]))
+            L = len(hist[b])
+            assert st.seq_len[b] == L
+            assert np.allclose(st.hidden[b], hid[0, -1], atol=1e-10)
+            for li in range(CFG.num_layers):
+                assert np.allclose(st.k[li][b, :, :L], ks[li][0], atol=1e-10)
+                assert np.allclose(st.v[li][b, :, :L], vs[li][0], atol=1e-10)
+    assert len(shapes) > 1 and deep >= 2
 
 
 def test_chain_round_extract_equals_recompute_and_trees():

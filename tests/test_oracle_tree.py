@@ -217,3 +217,107 @@ def test_chain_confidence_matches_torch():
     assert np.allclose(D.chain_confidence(x), top1, rtol=1e-12, atol=0)
     v = torch.topk(sx, 2, dim=-1).values
     assert np.allclose(D.chain_confidence(x, "margin"), (v[:, 0] - v[:, 1]).numpy(), rtol=0, atol=0)
+
+
+# --------------------------------------------------------------------------- sparse asymmetric (b200)
+def _sparse_plan(nodes=(4, 3, 2), budget=10, heads=3, min3=1, mode="fixed", **kw):
+    """The plan of flashgrpo_b200/tests/test_sparse_asymmetric_hrdcr.py:28-41."""
+    return T.plan_tree(active_batch_size=1, num_medusa_heads=heads, tree_mode=mode, tree_layout="sparse_asymmetric",
+                       cpeak_nodes=budget, min_tree_nodes_per_seq=1, max_tree_nodes_per_seq=budget,
+                       max_tree_depth=4, fixed_tree_topk_by_depth=[4, 3, 2], sparse_nodes_by_head=list(nodes),
+                       sparse_min_head3_nodes=min3, sparse_head3_min_budget=8, **kw)
+
+
+def _proposal_logits(batch=1, vocab=17):
+    """flashgrpo_b200/tests/test_sparse_asymmetric_hrdcr.py:44-46: descending logits,
+    head i shifted by -0.1 i (float32)."""
+    base = np.arange(vocab, dtype=np.float32)[::-1]
+    return [np.tile(base - np.float32(i * 0.1), (batch, 1)).astype(np.float32) for i in range(3)]
+
+
+def test_sparse_allocation_hand_derived():
+    """Budget split of flashgrpo_b200/decoding/medusa_tree.py:411-444, worked by hand."""
+    assert T.sparse_allocation(10, 3, [4, 3, 2], 1, 8) == [4, 3, 2]      # the reference test's plan
+    assert T.sparse_allocation(32, 3, [5, 4, 0], 0, 8) == [5, 4]          # b200 defaults: head 3 dropped
+    assert T.sparse_allocation(12, 3, [8, 8, 2], 1, 8) == [8, 2, 1]       # head 2 gives one node to head 3
+    assert T.sparse_allocation(12, 3, [8, 8, 2], 3, 8) == [7, 1, 3]       # head 2 keeps one, head 1 gives the rest
+    assert T.sparse_allocation(10, 3, [9, 9, 2], 3, 8) == [6, 0, 3]       # an empty head 2 stays in the list
+    assert T.sparse_allocation(6, 3, [4, 3, 2], 1, 8) == [4, 1]           # budget below head3_min_budget
+    assert T.sparse_allocation(1, 3, [4, 3, 2], 1, 8) == []
+    p = _sparse_plan()
+    assert (p.active_heads, p.topk_by_depth, p.nodes_by_head, p.actual_nodes, p.layout) == \
+        (3, [4, 3, 2], [4, 3, 2], 10, "sparse_asymmetric")
+    assert p.diversity_penalty == 0.05 and p.branch_score_temperature == 1.0
+    # concurrency-aware: the dense planner's budget floor(cpeak / B), then the split
+    q = T.plan_tree(active_batch_size=4, num_medusa_heads=3, tree_mode="concurrency_aware",
+                    tree_layout="sparse_asymmetric", cpeak_nodes=64, min_tree_nodes_per_seq=1,
+                    max_tree_nodes_per_seq=32, max_tree_depth=4, fixed_tree_topk_by_depth=[4, 3, 2],
+                    sparse_nodes_by_head=[8, 6, 4])
+    assert q.node_budget_per_seq == 16 and q.nodes_by_head == [8, 6, 1]
+
+
+def test_sparse_tree_reference_invariants_and_known_answer():
+    """flashgrpo_b200/tests/test_sparse_asymmetric_hrdcr.py:50-80, plus the exact trees
+    worked by hand from the greedy rule (parent score + candidate score - 0.05 x picks)."""
+    plan = _sparse_plan()
+    t = T.build_sparse_trees([7], _proposal_logits(), plan, [True])[0]
+    assert t.node_count == 10
+    assert len({(p, k) for p, k in zip(t.parents, t.tokens)}) == 10
+    for n, (p, d) in enumerate(zip(t.parents, t.depths)):
+        assert (p == -1) if n == 0 else (0 <= p < n and t.depths[p] == d - 1)
+    # head 1: tokens 0..3 (scores 16..13); head 2 picks (node1, 0) 31.9, (node2, 0) 30.9 over
+    # (node1, 1) 30.9 - 0.05, then (node1, 1); head 3 picks (node5, 0), then (node6, 0) 46.7
+    # over (node5, 1) 46.7 - 0.05.
+    assert t.tokens == [7, 0, 1, 2, 3, 0, 0, 1, 0, 0]
+    assert t.parents == [-1, 0, 0, 0, 0, 1, 2, 1, 5, 6]
+    assert t.depths == [1, 2, 2, 2, 2, 3, 3, 3, 4, 4]
+    assert abs(t.scores[8] - (16.0 + 15.9 + 15.8)) < 1e-5
+    # head 3 gated off: its two nodes go to head 2 (reference: nodes_by_head + [0] == [4, 5, 0])
+    r = T.build_sparse_trees([7], _proposal_logits(), plan, [False])[0]
+    assert r.node_count == 10 and [r.depths.count(d) for d in (2, 3, 4)] == [4, 5, 0]
+    assert r.parents[5:] == [1, 2, 1, 3, 2] and r.tokens[5:] == [0, 0, 1, 0, 1]
+
+
+def test_sparse_greedy_without_penalty_is_a_sorted_pool():
+    """With no penalty the greedy picks are the pool sorted by (cumulative desc, pair
+    index asc): an independent formulation, checked on random tied scores."""
+    rng = np.random.default_rng(11)
+    for trial in range(200):
+        npar, w = int(rng.integers(1, 6)), int(rng.integers(1, 7))
+        ps = (rng.integers(-3, 3, npar) / 2).tolist()
+        ts = (rng.integers(-3, 3, w) / 2).astype(np.float32).tolist()
+        toks = rng.permutation(50)[:w].tolist()
+        count = int(rng.integers(0, npar * w + 2))
+        got = T.select_sparse_children(list(range(10, 10 + npar)), ps, toks, ts, count, 0.0)
+        pool = [(ps[p] + ts[j], p * w + j) for p in range(npar) for j in range(w)]
+        want = sorted(pool, key=lambda x: (-x[0], x[1]))[:count]
+        assert [(10 + i // w, toks[i % w], c) for c, i in want] == got, trial
+
+
+def test_sparse_greedy_penalty_spreads_parents_and_skips_nan():
+    # equal pools: the penalty alternates parents instead of draining the first one
+    got = T.select_sparse_children([1, 2], [0.0, 0.0], [5, 6, 7], [3.0, 2.99, 2.98], 4, 0.05)
+    assert [(p, t) for p, t, _ in got] == [(1, 5), (2, 5), (1, 6), (2, 6)]
+    # large penalty: every parent gets its best candidate first
+    got = T.select_sparse_children([1, 2, 3], [1.0, 0.5, 0.0], [5, 6], [1.0, 0.9], 3, 10.0)
+    assert [p for p, _, _ in got] == [1, 2, 3]
+    # NaN and -inf values are never picked; an exhausted pool ends the picks
+    got = T.select_sparse_children([1], [0.0], [5, 6, 7], [float("nan"), 1.0, float("-inf")], 3, 0.0)
+    assert [(p, t) for p, t, _ in got] == [(1, 6)]
+    assert T.select_sparse_children([1], [0.0], [5], [1.0], 0, 0.0) == []
+
+
+def test_sparse_tree_extras_budget_and_widths():
+    """Leftover head-1 candidates fill the budget (medusa_tree.py:658-671); heads past
+    the third are ignored; widths keep head 3's count in reserve (:569-579)."""
+    assert T.sparse_widths([4, 3, 2], 100) == [6, 5, 2] and T.sparse_widths([5, 4], 3) == [3, 3]
+    plan = T.Plan(32, 3, [4, 3, 2], 10, "fixed", "sparse_asymmetric", [4, 3, 2], 1, 8, 1.0, 0.05)
+    t = T.build_sparse_trees([7], _proposal_logits(), plan)[0]
+    assert t.node_count == 12 and t.tokens[10:] == [4, 5] and t.parents[10:] == [0, 0] and t.depths[10:] == [2, 2]
+    plan = T.Plan(11, 3, [4, 3, 2], 10, "fixed", "sparse_asymmetric", [4, 3, 2], 1, 8, 1.0, 0.05)
+    assert T.build_sparse_trees([7], _proposal_logits(), plan)[0].tokens[10:] == [4]
+    plan = T.Plan(8, 3, [4, 3, 2], 10, "fixed", "sparse_asymmetric", [4, 3, 2], 1, 8, 1.0, 0.05)
+    t = T.build_sparse_trees([7], _proposal_logits(), plan)[0]
+    assert t.node_count == 8 and t.depths == [1, 2, 2, 2, 2, 3, 3, 3]  # cut at the budget
+    plan = T.Plan(10, 0, [], 1, "fixed", "sparse_asymmetric", [], 1, 8, 1.0, 0.05)
+    assert T.build_sparse_trees([3, 4], _proposal_logits(2), plan)[1].tokens == [4]
