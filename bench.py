@@ -127,6 +127,74 @@ def algorithmic_work(cfg, rnd, seq_before, elem):
     return w
 
 
+def planted_walk_gather(cfg, r, work, elem, reps=5):
+    """Walk and KV gather at their worst-case bytes.
+
+    With random-init weights no candidate is accepted, so the measured rounds walk
+    one step and gather one row. Here the walk's logits rows are planted (the first
+    child's token is raised by 60) so every sequence accepts a full-depth path of the
+    last round's tree shape: D draws over B rows, then D + 1 rows moved per layer,
+    K/V and KV head. Runs on the bench's cache after the measured rounds (the gather
+    only rewrites tree slots past each committed length, and repeats are idempotent).
+    """
+    import torch
+
+    from flashgrpo_amd import kernels as K
+    from flashgrpo_amd.decoding.medusa_tree import TreeTopology
+
+    plan = r.plan_last
+    topo = TreeTopology(list(plan["topk_by_depth"]), int(plan["node_budget_per_seq"]))
+    N, D, B, V = topo.num_nodes, topo.max_depth, len(r.active), cfg.vocab
+    if N < 2:
+        return None
+    dev = r.device
+    i32 = dict(dtype=torch.int32, device=dev)
+    tokens = ((torch.arange(B, **i32)[:, None] * 1009 + torch.arange(N, **i32)[None, :] * 37) % V).contiguous()
+    parents = torch.tensor([topo.parents] * B, **i32)
+    n_nodes = torch.full((B,), N, **i32)
+    path = [0]
+    while True:
+        kids = [c for c, p in enumerate(topo.parents) if p == path[-1]]
+        if not kids:
+            break
+        path.append(kids[0])
+    g = torch.Generator(device="cpu").manual_seed(5)
+    logits = torch.randn(D, B, V, generator=g).to(dev, torch.bfloat16 if elem == 2 else torch.float32)
+    ar = torch.arange(B, device=dev)
+    for t in range(D):
+        logits[t, ar, tokens[:, path[t + 1]].long()] += 60.0
+    kw = dict(seed=7, step=0, seq_ids=r.row_map, draw0=1, temperature=work["temperature"], greedy=False,
+              top_p=work["top_p"], err_flag=r.err)
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    walk_ms, gather_ms = [], []
+    for _ in range(reps):
+        walk = K.walk_begin(tokens, parents, n_nodes, acc_stride=D + 1)
+        for t in range(D):
+            K.walk_rows(walk, N)
+            e0, e1 = ev(), ev()
+            e0.record()
+            K.walk_step(walk, logits[t], tokens, parents, n_nodes, walk_step=t, **kw)
+            e1.record()
+            walk_ms.append((e0, e1))
+        e0, e1 = ev(), ev()
+        e0.record()
+        r.cache.gather_path(r.seq, walk["acc_nodes"], walk["acc_len"], N, row_map=r.row_map, err_flag=r.err)
+        e1.record()
+        gather_ms.append((e0, e1))
+    torch.cuda.synchronize()
+    if not bool((walk["acc_len"] == D + 1).all()) or int(r.err.max()) != 0:
+        raise RuntimeError("planted walk did not accept the full depth")
+    w_us = sum(a.elapsed_time(b) for a, b in walk_ms) / len(walk_ms) * 1e3
+    g_us = sum(a.elapsed_time(b) for a, b in gather_ms) / len(gather_ms) * 1e3
+    w_bytes = B * V * elem
+    g_bytes = 2 * cfg.num_layers * 2 * B * cfg.kv_heads * (D + 1) * cfg.head_dim * elem
+    return {"depth": D, "sequences": B,
+            "walk_step": {"avg_us": round(w_us, 2), "bytes": w_bytes, "GBps": round(w_bytes / w_us / 1e3, 1),
+                          "hbm_frac": round(w_bytes / w_us / 1e3 / HBM_PEAK_GBS, 4)},
+            "kv_path_gather": {"avg_us": round(g_us, 2), "bytes": g_bytes, "GBps": round(g_bytes / g_us / 1e3, 1),
+                               "hbm_frac": round(g_bytes / g_us / 1e3 / HBM_PEAK_GBS, 4)}}
+
+
 def cpu_baseline(model, heads, r, work, seed, layers=2):
     """Oracle (numpy fp32) verify round on the host: same shapes, decoder stack cut to
     `layers` of L layers and its forward time scaled back to L layers."""
@@ -307,7 +375,7 @@ def main():
     g = torch.Generator().manual_seed(args.seed + 3)
     prompts = torch.randint(0, cfg.vocab, (work["prompts"], work["prefix"]), generator=g)
     # long enough that no row reaches max_length inside the benchmark
-    max_length = work["prefix"] + 8 * (args.warmup + 2 * args.steps + 12) + 64
+    max_length = work["prefix"] + 8 * (args.warmup + 2 * args.steps + 20) + 64
     t_pre = time.perf_counter()
     r = dec.start(prompts, torch.ones_like(prompts), repeated_generate_nums=work["repeats"], max_length=max_length)
     torch.cuda.synchronize()
@@ -350,6 +418,14 @@ def main():
     kstats = timer.summary()
     rstats = rtimer.summary()
     log(f"instrumented {args.steps} steps in {elapsed_i:.3f} s")
+    # Latency rounds (continuing): HIP events on the stream around each round's verify
+    # step, kept out of the timed rounds.
+    r.event_log = []
+    for _ in range(max(min(args.steps, 8), 1)):
+        dec.step(r)
+    torch.cuda.synchronize()
+    step_ms = np.array([a.elapsed_time(b) for a, b in r.event_log])
+    r.event_log = None
     # Phase rounds (continuing): the decoder's statistical_time mode synchronises
     # at each phase boundary, so the phases add up to slightly more than a round.
     phase_keys = ("medusa_time", "verify_time", "accept_time", "cache_time")
@@ -366,6 +442,8 @@ def main():
     phases["other"] = round(elapsed_p / n_phase * 1e3 - sum(phases.values()), 3)
     phases["rounds"] = n_phase
     log(f"phases (ms/round) {phases}")
+    planted = planted_walk_gather(cfg, r, work, elem)
+    log(f"planted {planted}")
 
     def work_totals(rnds, sqs):
         totals = {}
@@ -444,6 +522,10 @@ def main():
         "hand_kernels_ms_per_step": round(mine_ms / args.steps, 3),
         "ms_per_step_instrumented": round(elapsed_i / args.steps * 1e3, 3),
         "phases_ms": phases,
+        # HIP events on the stream: verify forward + tree LM head + walk + KV extraction
+        "verify_step_ms": {"median": round(float(np.median(step_ms)), 3),
+                           "p90": round(float(np.percentile(step_ms, 90)), 3), "rounds": int(step_ms.size)},
+        "planted": planted,
         "roofline": roofline,
         "kernels": kernels,
         "cpu_baseline": cpu,

@@ -205,9 +205,14 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
   // read past the keys or into the next part) and leaves O and l unchanged.
   const int ntiles = (t_end - t_begin + 1) & ~1;
   const int kbeg = t_begin * kKT;
+  // Pipeline: while tile t is computed from LDS buffer t % 2, tile t + 1 is already
+  // in the other buffer (stored at the top of the iteration, so the store and its
+  // wait on the loads overlap the compute) and tiles t + 2, t + 3 are in flight in
+  // the two register sets.
   FG_LOAD8(xa0, xa1, xa2, xa3, kbeg)
   FG_LOAD8(xb0, xb1, xb2, xb3, kbeg + kKT)
   FG_STORE8(xa0, xa1, xa2, xa3, 0)
+  FG_LOAD8(xa0, xa1, xa2, xa3, kbeg + 2 * kKT)
   __syncthreads();
   const uint16_t* const kf_src = &Ks[0][l32 * kKPitch + g * 8];
   const uint16_t* const vf_src = &Vt[0][l32 * kVtPitch + g * 8];
@@ -215,8 +220,13 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int key0 = kbeg + (t0 + h) * kKT;
-    if (h == 0) FG_LOAD8(xa0, xa1, xa2, xa3, key0 + 2 * kKT)
-    else FG_LOAD8(xb0, xb1, xb2, xb3, key0 + 2 * kKT)
+    if (h == 0) {
+      FG_STORE8(xb0, xb1, xb2, xb3, 1)
+      FG_LOAD8(xb0, xb1, xb2, xb3, key0 + 3 * kKT)
+    } else {
+      FG_STORE8(xa0, xa1, xa2, xa3, 0)
+      FG_LOAD8(xa0, xa1, xa2, xa3, key0 + 3 * kKT)
+    }
 
     if (computes) {
       const uint16_t* kf_ = kf_src + h * (kKT * kKPitch);
@@ -298,8 +308,6 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
           for (int ks = 0; ks < 2; ++ks)
             o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr[db * 4 + kb * 2 + ks], pf[kb][ks], o[db], 0, 0, 0);
     }
-    if (h == 0) FG_STORE8(xb0, xb1, xb2, xb3, 1)
-    else FG_STORE8(xa0, xa1, xa2, xa3, 0)
     __syncthreads();
   }
 #undef FG_LOAD8

@@ -443,6 +443,10 @@ class FlashMedusaDecoder:
             raise RuntimeError("KV cache capacity exceeded")  # unreachable: rows finish at max_length
         r.sync()
         t0 = time.time()
+        ev_start = None
+        if r.event_log is not None:
+            ev_start = torch.cuda.Event(enable_timing=True)
+            ev_start.record()
         try:
             hidden_t = model.forward(tree_tokens, r.cache, pos_offset=tv["pos_offset"], anc=tv["anc"],
                                      seq_len=r.seq, row_map=r.row_map, err_flag=r.err)
@@ -622,6 +626,10 @@ class FlashMedusaDecoder:
             m["cache_time"] += dt_
             if cfg.cache_update_mode == "extract_path" and plan.active_heads > 0:
                 m["recompute_time"] += dt_
+        if ev_start is not None:
+            ev_end = torch.cuda.Event(enable_timing=True)
+            ev_end.record()
+            r.event_log.append((ev_start, ev_end))
         r.seq = r.seq + walk["acc_len"]
         r.seq_h = r.seq_h + acc_len_h
         if walk_last_h is not None:
@@ -754,6 +762,9 @@ class Rollout:
         self.statistical_time = statistical_time
         self.generation_step = generation_step
         self.device = device
+        # when a list: (start, end) HIP events of each round's verify step (verify
+        # forward + tree LM head + walk + KV extraction), recorded on the stream
+        self.event_log = None
         self.cache = None
         self.active = []
         self.row_map = self.seq = self.hidden = self.logits = self.pending = self.err = None
