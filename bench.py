@@ -168,6 +168,9 @@ def planted_walk_gather(cfg, r, work, elem, reps=5):
     ev = lambda: torch.cuda.Event(enable_timing=True)
     walk_ms, gather_ms = [], []
     for _ in range(reps):
+        # a spin kernel first, so the host has queued the launches below before they
+        # run and the events time the GPU, not the launch rate
+        torch.cuda._sleep(4_000_000)
         walk = K.walk_begin(tokens, parents, n_nodes, acc_stride=D + 1)
         for t in range(D):
             K.walk_rows(walk, N)
@@ -277,7 +280,8 @@ def cpu_baseline(model, heads, r, work, seed, layers=2):
 
 def summarize_trace(path, top=30):
     """Per-kernel table of a rocprofv3 kernel-trace CSV, restricted to the dispatches
-    between the last two spin-kernel markers that bracket the timed rounds."""
+    between the first two spin-kernel markers, which bracket the timed rounds (later
+    spin kernels belong to the planted measurement)."""
     import csv
 
     with open(path, newline="") as fh:
@@ -285,7 +289,7 @@ def summarize_trace(path, top=30):
     marks = [i for i, r in enumerate(rows) if "spin_kernel" in r["Kernel_Name"]]
     if len(marks) < 2:
         raise SystemExit(f"{path}: no pair of spin_kernel markers around the timed rounds")
-    sel = rows[marks[-2] + 1:marks[-1]]
+    sel = rows[marks[0] + 1:marks[1]]
     agg = {}
     for r in sel:
         name = r["Kernel_Name"]
@@ -321,13 +325,33 @@ def pmc_traffic(fetch_csv, write_csv, symbol, scale):
         with open(path, newline="") as fh:
             rows = sorted(csv.DictReader(fh), key=lambda r: int(r["Dispatch_Id"]))
         marks = [int(r["Dispatch_Id"]) for r in rows if "spin_kernel" in r["Kernel_Name"]]
-        lo, hi = (marks[-2], marks[-1]) if len(marks) >= 2 else (-1, 1 << 62)  # the timed rounds
+        lo, hi = (marks[0], marks[1]) if len(marks) >= 2 else (-1, 1 << 62)  # the timed rounds
         vals = [float(r["Counter_Value"]) for r in rows
                 if lo < int(r["Dispatch_Id"]) < hi and symbol in r["Kernel_Name"] and r["Counter_Name"] == counter]
         if not vals:
             return None
         total += sum(vals) / len(vals) * 1024.0 * k
     return int(total)
+
+
+def summarize_pmc(path, symbol):
+    """Mean value per dispatch of every counter in a rocprofv3 --pmc CSV, over the
+    dispatches of kernels whose name contains `symbol` between the timed-round markers."""
+    import csv
+
+    with open(path, newline="") as fh:
+        rows = sorted(csv.DictReader(fh), key=lambda r: int(r["Dispatch_Id"]))
+    marks = [int(r["Dispatch_Id"]) for r in rows if "spin_kernel" in r["Kernel_Name"]]
+    lo, hi = (marks[0], marks[1]) if len(marks) >= 2 else (-1, 1 << 62)
+    acc = {}
+    for r in rows:
+        if lo < int(r["Dispatch_Id"]) < hi and symbol in r["Kernel_Name"]:
+            acc.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    print(f"{path}: kernels matching {symbol!r} between the timed-round markers")
+    print("| counter | dispatches | mean per dispatch |")
+    print("|---|---:|---:|")
+    for name, v in sorted(acc.items()):
+        print(f"| {name} | {len(v)} | {sum(v) / len(v):.6g} |")
 
 
 def main():
@@ -349,9 +373,14 @@ def main():
     ap.add_argument("--traffic-scale", nargs=2, type=float, default=(2.0, 1.0), metavar=("FETCH", "WRITE"),
                     help="copy KiB per counter KiB, measured on a plain copy of known size (FETCH_SIZE, WRITE_SIZE)")
     ap.add_argument("--summarize-trace", metavar="CSV", help="summarise a rocprofv3 kernel trace of this command")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("CSV", "KERNEL"),
+                    help="per-dispatch counter means of one kernel from a rocprofv3 --pmc run of this command")
     args = ap.parse_args()
     if args.summarize_trace:
         summarize_trace(args.summarize_trace)
+        return
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc)
         return
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (sequences shard by data "
