@@ -69,17 +69,30 @@ def plan_for(spec: DecodeSpec, batch: int) -> OT.Plan:
                         sparse_diversity_penalty=spec.sparse_diversity_penalty)
 
 
+def confidences(spec: DecodeSpec, medusa_logits) -> list:
+    """Per-head confidence quantile over the batch (``flash_medusa_decoder.py:320-339``):
+    top-1 probability, or the top-1 minus top-2 margin."""
+    confs = []
+    for lg in medusa_logits:
+        x = np.asarray(lg, np.float64)
+        if spec.adaptive_confidence_metric == "margin":
+            # top-1 minus top-2 value (flash_medusa_decoder.py:326-331)
+            part = -np.sort(-x, axis=-1)[:, :2]
+            score = part[:, 0] - part[:, 1] if part.shape[1] > 1 else part[:, 0]
+        else:
+            m = x.max(axis=-1)
+            lse = m + np.log(np.exp(x - m[:, None]).sum(axis=-1))
+            score = np.exp(m - lse)
+        score = np.nan_to_num(score, nan=0.0, posinf=0.0, neginf=0.0)
+        confs.append(OT.quantile_linear(score, spec.adaptive_confidence_quantile))
+    return confs
+
+
 def adapt_plan(spec: DecodeSpec, plan: OT.Plan, medusa_logits) -> OT.Plan:
-    """Top-1-probability confidence quantile -> branching -> budget fit
-    (``flash_medusa_decoder.py:320-389``)."""
+    """Confidence quantile -> branching -> budget fit (``flash_medusa_decoder.py:320-389``)."""
     if not spec.adaptive_tree_enabled or not plan.topk_by_depth:
         return plan
-    confs = []
-    for lg in medusa_logits[: len(plan.topk_by_depth)]:
-        x = np.asarray(lg, np.float64)
-        m = x.max(axis=-1)
-        lse = m + np.log(np.exp(x - m[:, None]).sum(axis=-1))
-        confs.append(OT.quantile_linear(np.exp(m - lse), spec.adaptive_confidence_quantile))
+    confs = confidences(spec, medusa_logits[: len(plan.topk_by_depth)])
     ks = [OT.topk_from_confidence(c, k, d, enabled=True, min_topk_by_depth=spec.adaptive_min_topk_by_depth,
                                   low=spec.adaptive_confidence_low, high=spec.adaptive_confidence_high)
           for d, (k, c) in enumerate(zip(plan.topk_by_depth, confs))]

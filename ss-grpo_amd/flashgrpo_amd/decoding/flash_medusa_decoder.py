@@ -396,6 +396,8 @@ class FlashMedusaDecoder:
                 kc = max(sparse_widths(list(plan.nodes_by_head or plan.topk_by_depth)[:3], mlog.shape[-1]))
             else:
                 kc = max(plan.topk_by_depth)
+            if cfg.adaptive_tree_enabled and cfg.adaptive_confidence_metric == "margin":
+                kc = max(kc, min(2, mlog.shape[-1]))  # margin = top-1 - top-2 (flash_medusa_decoder.py:327-331)
             cand, score, stats = K.medusa_topk(mlog, kc, stats=bool(cfg.adaptive_tree_enabled))
             r.sync()
             m["medusa_time"] += time.time() - t0

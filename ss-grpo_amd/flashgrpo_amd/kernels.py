@@ -17,6 +17,9 @@ F32, BF16 = 0, 1
 
 
 def _call(name: str, *args) -> None:
+    if timing.idle():  # no timer installed: launch directly (the context manager costs ~3 us)
+        _lib.call(name, *args)
+        return
     with timing.launch(name):
         _lib.call(name, *args)
 _DT = {torch.float32: F32, torch.bfloat16: BF16}
@@ -33,8 +36,14 @@ def _ptr(t):
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = torch._C._cuda_getCurrentRawStream
+_cur_device = torch._C._cuda_getDevice
+
+
 def _stream() -> int:
-    return torch.cuda.current_stream().cuda_stream
+    """hipStream_t of torch's current stream on the current device (the two direct
+    C calls cost ~1 us; torch.cuda.current_stream() costs ~9 us per launch)."""
+    return _raw_stream(_cur_device())
 
 
 _SCRATCH = {}

@@ -259,7 +259,7 @@ class TargetModel:
     # -------------------------------------------------------------- forward
     def _buf(self, name, shape, dtype=None):
         dtype = dtype or self.dtype
-        numel = int(np.prod(shape))
+        numel = math.prod(shape)
         b = self._bufs.get(name)
         if b is None or b.numel() < numel or b.dtype != dtype:
             b = torch.empty(max(numel, 1), dtype=dtype, device=self.device)

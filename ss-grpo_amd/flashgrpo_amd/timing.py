@@ -41,6 +41,11 @@ def _timer():
     return getattr(_state, "timer", None)
 
 
+def idle() -> bool:
+    """True when no KernelTimer is active on this thread."""
+    return getattr(_state, "timer", None) is None
+
+
 def _labels():
     if not hasattr(_state, "labels"):
         _state.labels = []

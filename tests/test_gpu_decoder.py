@@ -183,6 +183,8 @@ def lockstep(trace, ocfg, Wr, heads_r, spec, prompts, dtype, seed, max_length, e
                 want_ml = OM.medusa_logits(rec["hidden_in"], heads_r, Wr["lm_head"], nh)
                 for d in range(nh):
                     assert rel(ml[d], want_ml[d]) < tol
+                if spec.adaptive_tree_enabled:
+                    stats["conf"] = OD.confidences(spec, [ml[d] for d in range(min(nh, len(plan.topk_by_depth)))])
                 plan = OD.adapt_plan(spec, plan, [ml[d] for d in range(nh)])
             assert rec["plan"] == list(plan.topk_by_depth), rnd
             heads_logits = []
@@ -318,6 +320,21 @@ def test_lockstep_bf16_concurrency_tree():
                          fixed_tree_topk_by_depth=(4, 3, 2), num_medusa_heads=3, max_tree_depth=4, top_p=0.95,
                          eos_token_id=5)
     _run(SMALL16, spec, dtype=torch.bfloat16, B0=2, repeats=2, P=70, max_length=70 + 20)
+
+
+def test_lockstep_adaptive_margin_confidence():
+    """Adaptive plan from the top-1 minus top-2 margin of each head
+    (flash_medusa_decoder.py:326-331), including a plan whose base branching is 1."""
+    for ks, low, high in [((3, 2, 2), 0.05, 0.6), ((1, 1, 1), 0.0, 0.1)]:
+        spec = OD.DecodeSpec(tree_mode="concurrency_aware", cpeak_nodes=64, max_tree_nodes_per_seq=16,
+                             fixed_tree_topk_by_depth=ks, num_medusa_heads=3, max_tree_depth=4,
+                             adaptive_tree_enabled=True, adaptive_confidence_metric="margin",
+                             adaptive_confidence_low=low, adaptive_confidence_high=high, top_p=1.0)
+        out, st = _run(SMALL, spec, dtype=torch.float32, B0=2, repeats=2, P=20, max_length=20 + 16)
+        assert st["rounds"] > 0
+        conf = out["last_tree_plan"]["adaptive_tree"]["confidence"]
+        assert np.allclose(conf, st["conf"], rtol=1e-6, atol=1e-7), (ks, conf, st["conf"])
+        assert all(c > 0 for c in conf)  # a real margin, not a top-1 value or 0
 
 
 def test_lockstep_adaptive_b200_greedy_and_recompute():
