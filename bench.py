@@ -25,6 +25,7 @@ per-kernel table of the dispatches between the markers.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -367,7 +368,8 @@ def main():
     ap.add_argument("--roofline-kernel", default="fg_tree_attention",
                     help="C-ABI entry point whose launches are event-timed in the timed rounds")
     ap.add_argument("--roofline-every", type=int, default=7,
-                    help="event-time one launch in this many of the roofline kernel in the timed rounds")
+                    help="event-time every launch of the roofline kernel in one timed round in this many "
+                         "(those rounds run the verify forward eagerly, the others replay its HIP graph)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE counter_collection CSVs of the roofline kernel")
     ap.add_argument("--traffic-scale", nargs=2, type=float, default=(2.0, 1.0), metavar=("FETCH", "WRITE"),
@@ -410,31 +412,50 @@ def main():
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t_pre
     log(f"prefill {prefill_s:.1f} s")
-    for _ in range(args.warmup):
-        dec.step(r)
+    for i in range(args.warmup):
+        # the last warm-up round runs like a roofline-timed round (eager forward,
+        # events on the roofline kernel): the first such round of a process has cost
+        # ~40 ms more than the others
+        last = i == args.warmup - 1
+        with timing.active(timing.KernelTimer(only={args.roofline_kernel}) if last else None):
+            dec.step(r)
+    torch.cuda.synchronize()
     log("warmup done")
-    # Timed rounds: only the roofline kernel is bracketed by HIP events, and only
-    # one launch in --roofline-every (a few per round), so the event cost stays
-    # out of `value`.
-    rtimer = timing.KernelTimer(only={args.roofline_kernel}, every=args.roofline_every)
+    # Timed rounds: in one round of every --roofline-every, each launch of the
+    # roofline kernel is bracketed by HIP events on its stream (that round runs the
+    # verify forward launch by launch); the other rounds replay the forward's HIP
+    # graph, as the decoder does by default. Nothing else is timed inside.
+    every = max(args.roofline_every, 1)
+    rtimer = timing.KernelTimer(only={args.roofline_kernel},
+                                reserve=cfg.num_layers * ((args.steps + every - 1) // every) + 8)
+    torch.cuda.synchronize()
     rounds, seqs = [], []
     tokens = 0
+    # Python's cyclic collector is run before and paused during the timed rounds, as
+    # timeit does: a full collection inside them has cost ~40 ms of one round.
+    gc.collect()
+    gc.disable()
     torch.cuda._sleep(1000)  # trace marker: the timed rounds start after this kernel
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    with timing.active(rtimer):
-        for _ in range(args.steps):
+    marks = []
+    for i in range(args.steps):
+        with timing.active(rtimer if i % every == 0 else None):
             seqs.append(r.seq_h.copy())
             tokens += dec.step(r)
             rounds.append(r.last_round)
+        marks.append(time.perf_counter())
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    gc.enable()
+    log("timed rounds (host ms, each ends at the round's sync): "
+        + " ".join(f"{(b - a) * 1e3:.2f}" for a, b in zip([t0] + marks[:-1], marks)))
     torch.cuda._sleep(1000)  # trace marker: end of the timed rounds
     torch.cuda.synchronize()
     log(f"timed {args.steps} steps in {elapsed:.3f} s")
     # Instrumented rounds (same workload, continuing): every hand-written launch
     # timed, for the per-kernel table.
-    timer = timing.KernelTimer()
+    timer = timing.KernelTimer(reserve=2048)
     rounds_i, seqs_i = [], []
     t1 = time.perf_counter()
     with timing.active(timer):
@@ -544,7 +565,8 @@ def main():
         "config": {"workload": work["name"], "sequences": len(r.active), "prefix": work["prefix"],
                    "tree_nodes": rounds[-1]["num_nodes"], "internal_nodes": rounds[-1]["internal"],
                    "topk_by_depth": r.plan_last.get("topk_by_depth"), "temperature": work["temperature"],
-                   "top_p": work["top_p"], "parallelism": "single GPU"},
+                   "top_p": work["top_p"], "parallelism": "single GPU",
+                   "verify_forward": "HIP graph replay (eager in the roofline-timed rounds)"},
         "tokens": int(tokens),
         "accept_len_mean": round(tokens / max(sum(x["batch"] for x in rounds), 1), 4),
         "prefill_s": round(prefill_s, 2),

@@ -90,6 +90,9 @@ class FlashMedusaConfig:
     # and next-round logits are identical to the packed projection; only nodes the
     # walk never reaches are skipped.
     lazy_walk_lm_head: bool = True
+    # Replay the verify forward as one HIP graph per (batch, tree width) once that shape
+    # repeats; identical results, one launch instead of ~9 per layer.
+    graph_verify_forward: bool = True
     # tree_layout="sparse_asymmetric" (flashgrpo_b200/decoding/flash_medusa_decoder.py:65-73);
     # the head-3 quality calibrator and its exploration rounds are not built: every
     # row keeps head 3 (build_batch_trees accepts an explicit per-row gate).
@@ -451,7 +454,8 @@ class FlashMedusaDecoder:
             ev_start.record()
         try:
             hidden_t = model.forward(tree_tokens, r.cache, pos_offset=tv["pos_offset"], anc=tv["anc"],
-                                     seq_len=r.seq, row_map=r.row_map, err_flag=r.err)
+                                     seq_len=r.seq, row_map=r.row_map, err_flag=r.err,
+                                     graph=bool(cfg.graph_verify_forward))
             if N > 1:
                 m["tree_query_rows"] += Bc * N
                 if lazy:
@@ -689,6 +693,8 @@ class FlashMedusaDecoder:
         """Result dict with the keys of ``flash_medusa_decoder.py:1189-1229``."""
         cfg = self.config
         m = r.m
+        if r.cache is not None:
+            self.model.drop_graphs(r.cache)  # the rollout's cache goes with it
         total_time = time.time() - r.total_start
         accept_rate = m["accepted"] / max(m["proposed"], 1)
         avg_accept = m["total_acc_length"] / max(m["total_decoded_steps"], 1)

@@ -47,14 +47,18 @@ def _stream() -> int:
 
 
 _SCRATCH = {}
+_SCRATCH_RETIRED = []
 
 
 def _scratch(name: str, nbytes: int, device) -> torch.Tensor:
     """A cached uint8 device buffer of at least nbytes for one kind of workspace.
-    Launches are ordered on the current stream, so successive calls may share it."""
+    Launches are ordered on the current stream, so successive calls may share it.
+    A buffer outgrown is kept alive: a captured graph may still address it."""
     key = (name, str(device))
     buf = _SCRATCH.get(key)
     if buf is None or buf.numel() < nbytes:
+        if buf is not None:
+            _SCRATCH_RETIRED.append(buf)
         buf = torch.empty(int(nbytes), dtype=torch.uint8, device=device)
         _SCRATCH[key] = buf
     return buf

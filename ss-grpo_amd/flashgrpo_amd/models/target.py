@@ -24,6 +24,7 @@ import torch
 import torch.nn.functional as F
 
 from .. import kernels as K
+from .. import timing
 from ..tuning import use_tuned_gemms
 
 MAX_TREE_NODES = 64
@@ -129,6 +130,76 @@ class KVCache:
         self.seq_len.index_copy_(0, dst_rows.long(), self.seq_len.index_select(0, src_rows.long()))
 
 
+_HIP = None
+
+
+def _graph_memset_nodes(graph: torch.cuda.CUDAGraph) -> int:
+    """Memset nodes of a captured (not yet instantiated) graph, counted through the
+    HIP runtime torch already loaded. A library call may record a hipMemsetAsync; such
+    nodes have given wrong results on replays after the first, so a graph holding one
+    is not used."""
+    global _HIP
+    import ctypes
+
+    if _HIP is None:
+        _HIP = ctypes.CDLL("libamdhip64.so.7")
+    raw = ctypes.c_void_p(graph.raw_cuda_graph())
+    n = ctypes.c_size_t(0)
+    if _HIP.hipGraphGetNodes(raw, None, ctypes.byref(n)) != 0:
+        raise RuntimeError("hipGraphGetNodes failed")
+    nodes = (ctypes.c_void_p * max(n.value, 1))()
+    if _HIP.hipGraphGetNodes(raw, nodes, ctypes.byref(n)) != 0:
+        raise RuntimeError("hipGraphGetNodes failed")
+    kind = ctypes.c_int(0)
+    count = 0
+    for i in range(n.value):
+        if _HIP.hipGraphNodeGetType(ctypes.c_void_p(nodes[i]), ctypes.byref(kind)) != 0:
+            raise RuntimeError("hipGraphNodeGetType failed")
+        count += kind.value == 2  # hipGraphNodeTypeMemset
+    return count
+
+
+class _ForwardGraph:
+    """One captured verify forward: static input buffers, the graph, its output."""
+
+    def __init__(self, graph, inputs, out):
+        self.graph, self.inputs, self.out = graph, inputs, out
+
+    @classmethod
+    def capture(cls, model, tokens, cache, pos_offset, anc, seq_len, row_map, err_flag):
+        inputs = dict(tokens=tokens.clone(), pos=pos_offset.clone(), anc=anc.clone(), seq=seq_len.clone(),
+                      row_map=None if row_map is None else row_map.clone())
+
+        def run_eager():
+            return model._forward_eager(inputs["tokens"], cache, pos_offset=inputs["pos"], anc=inputs["anc"],
+                                        seq_len=inputs["seq"], row_map=inputs["row_map"], err_flag=err_flag)
+
+        # A warm-up on the current stream allocates every buffer and workspace the
+        # launches use outside the graph's pool (it rewrites the same tree slots the
+        # caller's forward writes).
+        run_eager()
+        if model._graph_pool is None:
+            model._graph_pool = torch.cuda.graph_pool_handle()
+        g = torch.cuda.CUDAGraph(keep_graph=True)
+        with torch.cuda.graph(g, pool=model._graph_pool):
+            out = run_eager()
+        if _graph_memset_nodes(g):
+            return None
+        g.instantiate()
+        return cls(g, inputs, out)
+
+    def run(self, tokens, pos_offset, anc, seq_len, row_map):
+        st = self.inputs
+        st["tokens"].copy_(tokens)
+        st["pos"].copy_(pos_offset)
+        st["anc"].copy_(anc)
+        st["seq"].copy_(seq_len)
+        if row_map is not None:
+            st["row_map"].copy_(row_map)
+        self.graph.replay()
+        return self.out
+
+
 class TargetModel:
     """Decoder weights on the device plus the verify / prefill forward."""
 
@@ -139,6 +210,10 @@ class TargetModel:
         self.w = weights
         self.inv_freq = inv_freq_table(cfg.head_dim, cfg.rope_theta).to(device)
         self._bufs = {}
+        self._graphs = {}       # graph key -> _ForwardGraph, or None when the key stays eager
+        self._graph_seen = {}   # graph key -> eager calls so far
+        self._graph_pool = None
+        self._retired = []      # buffers replaced while graphs that address them exist
         if self.device.type == "cuda":
             use_tuned_gemms()
 
@@ -262,25 +337,63 @@ class TargetModel:
         numel = math.prod(shape)
         b = self._bufs.get(name)
         if b is None or b.numel() < numel or b.dtype != dtype:
+            if b is not None and self._graphs:
+                self._retired.append(b)  # a captured graph may still address it
             b = torch.empty(max(numel, 1), dtype=dtype, device=self.device)
             self._bufs[name] = b
         return b[:numel].view(*shape)
 
+    def drop_graphs(self, cache: "KVCache | None" = None) -> None:
+        """Forget the captured forwards of one cache (None: all of them)."""
+        if cache is None:
+            self._graphs.clear()
+            self._graph_seen.clear()
+        else:
+            ptr = cache.kv.data_ptr()
+            for d in (self._graphs, self._graph_seen):
+                for k in [k for k in d if k[4] == ptr]:
+                    del d[k]
+        if not self._graphs:
+            self._retired.clear()
+
     def forward(self, tokens: torch.Tensor, cache: KVCache, *, pos_offset: torch.Tensor, anc: torch.Tensor,
                 seq_len: torch.Tensor | None = None, row_map: torch.Tensor | None = None,
-                err_flag: torch.Tensor | None = None) -> torch.Tensor:
+                err_flag: torch.Tensor | None = None, graph: bool = False) -> torch.Tensor:
         """Forward N new tokens per row after each row's committed prefix.
 
         tokens [B, N] int (device); pos_offset int32 [N] (shared) or [B, N]: position =
         seq_len[b] + pos_offset[(b,) n]; anc: int64 bit masks [N] (shared) or [B, N]; node n's K/V land in cache slot
         seq_len[b] + n of cache row row_map[b]. Returns final-normed hidden [B, N, H].
         ``seq_len`` defaults to ``cache.seq_len`` and is not advanced here.
+
+        ``graph=True`` replays a HIP graph of the whole forward (captured on the second
+        call with the same shapes, cache and error word): one launch instead of ~9 per
+        layer. The returned tensor is then the graph's output buffer, overwritten by
+        the next replay of that graph. Calls made while a kernel timer is installed run
+        eagerly so every launch stays visible to it.
         """
+        seq_len = cache.seq_len if seq_len is None else seq_len
+        if graph and timing.idle() and not torch.cuda.is_current_stream_capturing():
+            key = (tuple(tokens.shape), tokens.dtype, tuple(pos_offset.shape), tuple(anc.shape), cache.kv.data_ptr(),
+                   tuple(cache.kv.shape), tuple(seq_len.shape), None if row_map is None else tuple(row_map.shape),
+                   None if err_flag is None else err_flag.data_ptr())
+            g = self._graphs.get(key, False)
+            if g is False:
+                seen = self._graph_seen.get(key, 0)
+                self._graph_seen[key] = seen + 1
+                if seen >= 1:  # a shape seen twice is worth a capture
+                    g = self._graphs[key] = _ForwardGraph.capture(self, tokens, cache, pos_offset, anc, seq_len,
+                                                                  row_map, err_flag)
+            if g:
+                return g.run(tokens, pos_offset, anc, seq_len, row_map)
+        return self._forward_eager(tokens, cache, pos_offset=pos_offset, anc=anc, seq_len=seq_len, row_map=row_map,
+                                   err_flag=err_flag)
+
+    def _forward_eager(self, tokens, cache, *, pos_offset, anc, seq_len, row_map, err_flag):
         cfg = self.cfg
         B, N = tokens.shape
         if N > MAX_TREE_NODES:
             raise ValueError(f"at most {MAX_TREE_NODES} new tokens per forward")
-        seq_len = cache.seq_len if seq_len is None else seq_len
         T = B * N
         H, d = cfg.hidden, cfg.head_dim
         x = self.w["embed"].index_select(0, tokens.reshape(-1).long())  # [T, H] residual stream

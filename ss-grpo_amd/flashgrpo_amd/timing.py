@@ -21,11 +21,25 @@ class KernelTimer:
     """Collects (start, end) event pairs per kernel name. ``only``: a set of C-ABI
     entry-point names to time (None: every launch)."""
 
-    def __init__(self, only=None, every: int = 1):
+    def __init__(self, only=None, every: int = 1, reserve: int = 0):
         self.events = defaultdict(list)
         self.only = None if only is None else set(only)
         self.every = max(1, int(every))  # time one launch in `every` of each name
         self.seen = defaultdict(int)
+        # Event pairs created up front (each recorded once so the runtime object
+        # exists): creating events inside a timed region has cost tens of ms when
+        # the runtime grows its signal pool.
+        self.pool = []
+        for _ in range(max(0, int(reserve))):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            e.record()
+            self.pool.append((s, e))
+
+    def pair(self):
+        if self.pool:
+            return self.pool.pop()
+        return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
     def summary(self) -> dict:
         """{name: {"count", "total_ms", "avg_ms"}} after synchronising."""
@@ -84,8 +98,7 @@ def launch(kernel: str):
     if n % t.every:
         yield
         return
-    s = torch.cuda.Event(enable_timing=True)
-    e = torch.cuda.Event(enable_timing=True)
+    s, e = t.pair()
     s.record()
     try:
         yield

@@ -120,3 +120,46 @@ def test_tree_logits_equal_sequential_path_on_device():
         h = m.forward(chain, c2, pos_offset=torch.arange(len(path), dtype=torch.int32, device=DEV),
                       anc=as_mask_tensor(chain_bits(len(path)), DEV))
         assert rel(tree_h[:, n].cpu().numpy(), h[:, -1].cpu().numpy()) < 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_graph_forward_replays_match_eager(dtype):
+    """The verify forward replayed as a HIP graph: every replay (new tokens, lengths,
+    row map, shared and per-row offsets/masks) equals the eager forward bit for bit,
+    with eager work of other shapes and host syncs between the replays."""
+    from flashgrpo_amd.decoding.medusa_tree import TreeTopology
+
+    ocfg = _cfgs(dtype)
+    rng = np.random.default_rng(4)
+    m = _model(ocfg, OM.random_weights(ocfg, seed=2, std=0.05), dtype)
+    B, P = 4, 96
+    cache = m.new_cache(B + 1, 200)
+    prompts = torch.from_numpy(rng.integers(0, ocfg.vocab, (B + 1, P))).to(DEV)
+    m.prefill(prompts, cache)
+    topo = TreeTopology([3, 2, 1], 12)
+    N = topo.num_nodes
+    d = topo.device(DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    i32 = dict(dtype=torch.int32, device=DEV)
+    for it in range(5):
+        toks = torch.from_numpy(rng.integers(0, ocfg.vocab, (B, N))).to(**i32)
+        seq = torch.from_numpy(rng.integers(P - 20, P, B)).to(**i32)
+        row_map = torch.from_numpy(rng.permutation(B + 1)[:B]).to(**i32)
+        if it % 2:  # per-row offsets and masks (sparse trees)
+            pos = d["pos_offset"].repeat(B, 1).contiguous()
+            anc = d["anc"].repeat(B, 1).contiguous()
+        else:
+            pos, anc = d["pos_offset"], d["anc"]
+        got = m.forward(toks, cache, pos_offset=pos, anc=anc, seq_len=seq, row_map=row_map, err_flag=err,
+                        graph=True).clone()
+        # eager work of another shape in between, then the eager reference
+        m.forward(toks[:2, :5].contiguous(), cache, pos_offset=d["pos_offset"][:5], anc=d["anc"][:5],
+                  seq_len=seq[:2], row_map=row_map[:2], err_flag=err)
+        torch.cuda.synchronize()
+        want = m.forward(toks, cache, pos_offset=pos, anc=anc, seq_len=seq, row_map=row_map, err_flag=err)
+        assert torch.equal(got, want), it
+    assert int(err.item()) == 0
+    graphs = [g for g in m._graphs.values() if g]
+    assert len(graphs) == 2  # the shared-mask and the per-row-mask shapes, each replayed
+    m.drop_graphs(cache)
+    assert not m._graphs
