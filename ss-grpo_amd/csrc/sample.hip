@@ -13,8 +13,9 @@
 // Integer sums make every result independent of reduction order.
 //
 // Unrestricted and greedy draws with a workspace run split over 16 chunks per
-// row (three launches, see "split sampling"). Otherwise: one 1024-thread
-// workgroup per sampled row. The row is split into 16
+// row (three launches, see "split sampling"), top-p draws without top-k too
+// (seven launches, see "split top-p"). Otherwise: one 1024-thread workgroup per
+// sampled row. The row is split into 16
 // contiguous wave segments; a wave walks its segment 512 elements (8 per lane,
 // 16-byte loads) per step. Top-k / top-p use an MSB-first 4 x 8-bit radix
 // select over the keys with count or q-weighted histograms in LDS.
@@ -436,6 +437,19 @@ struct SplitArgs {
   float* part_max;           // [rows, kSplitChunks]
   uint64_t* part_key;
   uint64_t* part_sum;
+  // split top-p (see "split top-p")
+  uint32_t tp32;
+  uint64_t* hist;            // [rows, kSplitChunks, 256] chunk histograms of one radix level
+  struct SelState* sel;      // [rows, 2] select state, double-buffered across levels
+  uint64_t* part_a;          // [rows, kSplitChunks] q-mass of keys above the cut key
+  uint64_t* part_t;          // [rows, kSplitChunks] q-mass of keys equal to it
+};
+
+// Radix select state of one row: the selected key bits so far, the q-mass of
+// keys above them, and the top-p target mass.
+struct SelState {
+  uint32_t prefix, pmask;
+  uint64_t above, target;
 };
 
 template <int DT>
@@ -608,6 +622,287 @@ __global__ void __launch_bounds__(kThreads) split_walk_kernel(
                acc_stride, acc_len, last_node, correction, state, err_flag);
 }
 
+// ------------------------------------------------------------------ split top-p
+// Top-p draws (no top-k) over kSplitChunks workgroups per row, the same integer
+// rule as block_sample / radix_select: (1) chunk maxima (split_max_kernel);
+// (2) four launches of one 8-bit radix level each over the scaled-logit keys: every
+// chunk workgroup first merges the previous level's 16 chunk histograms (all of a
+// row's workgroups reach the same digit; chunk 0 records the state) and then
+// histograms its chunk's q-mass under the new prefix -- the first merge also yields
+// the row's q total and the target floor(total * tp32 / 2^32); (3) the last merge
+// fixes the cut key; each chunk sums the q-mass above it and tied with it;
+// (4) one workgroup per row resolves the ties in index order, then locates the
+// draw among the kept tokens in vocabulary order (chunk by chunk partial sums).
+
+// Calls f(i, s, key) for the elements of chunk c of row r (8 per thread per step).
+template <int DT, class F>
+FG_DEVICE void for_chunk(const SplitArgs& a, int r, int c, F&& f) {
+  const char* p = split_row<DT>(a, r);
+  const int lo = c * a.chunk, hi = min(a.vocab, lo + a.chunk);
+  for (int i0 = lo + threadIdx.x * 8; i0 < hi; i0 += kSplitThreads * 8) {
+    float x[8];
+    if (i0 + 8 <= hi) {
+      fg::load8<DT>(p, i0, x);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = i0 + j < hi ? fg::load_elem<DT>(p, i0 + j) : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (i0 + j < hi) {
+        const float sv = a.scale ? __fdiv_rn(x[j], a.temperature) : x[j];
+        f(i0 + j, sv, fg::sort_key32(sv));
+      }
+  }
+}
+
+// Sum of v over the workgroup (kSplitThreads threads).
+FG_DEVICE uint64_t split_block_sum(uint64_t v, uint64_t* red) {
+  v = fg::wave_sum_u64(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  uint64_t t = 0;
+#pragma unroll
+  for (int w = 0; w < kSplitThreads / 64; ++w) t += red[w];
+  return t;
+}
+
+// Merges the 16 chunk histograms of the level at `shift` into st (radix_select's
+// digit rule); level 0's merge first sets the top-p target from the row total.
+FG_DEVICE void split_merge_level(const SplitArgs& a, int r, int shift, bool first, SelState& st, uint64_t* hs,
+                                 uint64_t* red, int* sdig, uint64_t* sabove) {
+  const uint64_t* hp = a.hist + (size_t)r * kSplitChunks * 256;
+  uint64_t v = 0;
+  for (int c = 0; c < kSplitChunks; ++c) v += hp[c * 256 + threadIdx.x];
+  hs[threadIdx.x] = v;
+  if (first) st.target = fg::mulhi_u64_u32(split_block_sum(v, red), a.tp32);
+  if (threadIdx.x == 0) {
+    *sdig = 0;  // no digit holds the target only when the row total is 0 (then the draw is the argmax)
+    *sabove = st.above;
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    uint64_t h[4], mine = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      h[j] = hs[255 - 4 * lane - j];
+      mine += h[j];
+    }
+    const uint64_t incl = fg::wave_incl_scan_u64(mine);
+    const uint64_t excl = incl - mine;
+    if (st.above + excl <= st.target && st.target < st.above + incl) {
+      uint64_t c = st.above + excl;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (c + h[j] > st.target) {
+          *sdig = 255 - 4 * lane - j;
+          *sabove = c;
+          break;
+        }
+        c += h[j];
+      }
+    }
+  }
+  __syncthreads();
+  st.prefix |= (uint32_t)*sdig << shift;
+  st.pmask |= 255u << shift;
+  st.above = *sabove;
+}
+
+// One radix level (level 0..3, digit bits 31-8l .. 24-8l): merge the previous
+// level, then this chunk's q-mass histogram under the prefix.
+template <int DT>
+__global__ void __launch_bounds__(kSplitThreads) split_topp_level_kernel(SplitArgs a, int level) {
+  const int c = blockIdx.x, r = blockIdx.y;
+  if (split_skip(a, r)) return;
+  __shared__ uint64_t hs[256];
+  __shared__ uint64_t red[kSplitThreads / 64];
+  __shared__ int sdig;
+  __shared__ uint64_t sabove;
+  SelState st{0u, 0u, 0ull, 0ull};
+  if (level >= 2) st = a.sel[r * 2 + ((level - 2) & 1)];
+  if (level >= 1) {
+    split_merge_level(a, r, 24 - 8 * (level - 1), level == 1, st, hs, red, &sdig, &sabove);
+    if (c == 0 && threadIdx.x == 0) a.sel[r * 2 + ((level - 1) & 1)] = st;
+  }
+  const float m = split_row_max(a, r);
+  const int shift = 24 - 8 * level;
+  __syncthreads();
+  hs[threadIdx.x] = 0;
+  __syncthreads();
+  for_chunk<DT>(a, r, c, [&](int, float sv, uint32_t key) {
+    if ((key & st.pmask) == st.prefix)
+      atomicAdd((unsigned long long*)&hs[(key >> shift) & 255u],
+                (unsigned long long)fg::quantize_q40(fg::exp_fg(sv - m)));
+  });
+  __syncthreads();
+  a.hist[((size_t)r * kSplitChunks + c) * 256 + threadIdx.x] = hs[threadIdx.x];
+}
+
+// Last merge (the cut key), then this chunk's q-mass above the cut key and tied with it.
+template <int DT>
+__global__ void __launch_bounds__(kSplitThreads) split_topp_cut_kernel(SplitArgs a) {
+  const int c = blockIdx.x, r = blockIdx.y;
+  if (split_skip(a, r)) return;
+  __shared__ uint64_t hs[256];
+  __shared__ uint64_t red[kSplitThreads / 64];
+  __shared__ int sdig;
+  __shared__ uint64_t sabove;
+  SelState st = a.sel[r * 2 + 0];  // after level 2
+  split_merge_level(a, r, 0, false, st, hs, red, &sdig, &sabove);
+  if (c == 0 && threadIdx.x == 0) a.sel[r * 2 + 1] = st;
+  const float m = split_row_max(a, r);
+  const uint32_t kappa = st.prefix;
+  uint64_t above = 0, tie = 0;
+  for_chunk<DT>(a, r, c, [&](int, float sv, uint32_t key) {
+    if (key >= kappa) {
+      const uint64_t w = fg::quantize_q40(fg::exp_fg(sv - m));
+      if (key > kappa) above += w;
+      else tie += w;
+    }
+  });
+  above = split_block_sum(above, red);
+  tie = split_block_sum(tie, red);
+  if (threadIdx.x == 0) {
+    a.part_a[r * kSplitChunks + c] = above;
+    a.part_t[r * kSplitChunks + c] = tie;
+  }
+}
+
+// Chunk-relative predicates for the pick (element index i is relative to chunk start lo).
+struct TieAt {
+  uint32_t kappa;
+  FG_DEVICE bool operator()(uint32_t key, uint32_t) const { return key == kappa; }
+};
+struct TieUpTo {
+  uint32_t kappa, last_rel;
+  FG_DEVICE bool operator()(uint32_t key, uint32_t i) const { return key == kappa && i <= last_rel; }
+};
+struct KeptIn {
+  uint32_t kappa, last, lo;
+  FG_DEVICE bool operator()(uint32_t key, uint32_t i) const { return key > kappa || (key == kappa && lo + i <= last); }
+};
+
+template <int DT>
+FG_DEVICE Row<DT> chunk_row(const SplitArgs& a, int r, int c) {
+  const int lo = c * a.chunk;
+  Row<DT> rr;
+  rr.p = split_row<DT>(a, r) + (int64_t)lo * (DT == fg::kBF16 ? 2 : 4);
+  rr.V = max(0, min(a.vocab, lo + a.chunk) - lo);
+  rr.seg = (((rr.V + kWaves - 1) / kWaves) + kStep - 1) / kStep * kStep;
+  rr.scale = a.scale;
+  rr.T = a.temperature;
+  rr.m = split_row_max(a, r);
+  return rr;
+}
+
+// The token of row r (whole block; every thread returns it).
+template <int DT>
+FG_DEVICE int split_topp_pick(const SplitArgs& a, int r, uint32_t u, Shared& sh) {
+  const SelState st = a.sel[r * 2 + 1];
+  const uint32_t kappa = st.prefix;
+  const uint64_t* pa = a.part_a + r * kSplitChunks;
+  const uint64_t* pt = a.part_t + r * kSplitChunks;
+  const uint64_t need = st.target - st.above;
+  // ties on the cut key are kept in index order up to the one whose running mass exceeds `need`
+  uint64_t tb = 0;
+  int cs = -1;
+  for (int c = 0; c < kSplitChunks; ++c) {
+    if (tb + pt[c] > need) {
+      cs = c;
+      break;
+    }
+    tb += pt[c];
+  }
+  uint32_t last = 0xffffffffu;
+  uint64_t tie_cs = 0;  // tie mass kept in chunk cs
+  if (cs >= 0) {
+    const Row<DT> rr = chunk_row<DT>(a, r, cs);
+    block_sum<true, DT>(rr, TieAt{kappa}, sh);
+    const int idx = block_locate<true, DT>(rr, TieAt{kappa}, need - tb, sh);
+    if (idx >= 0) {
+      last = (uint32_t)(cs * a.chunk + idx);
+      tie_cs = block_sum<true, DT>(rr, TieUpTo{kappa, (uint32_t)idx}, sh);
+    } else {
+      cs = -1;  // cannot happen: chunk cs holds the crossing tie
+    }
+  }
+  uint64_t total = 0;
+  for (int c = 0; c < kSplitChunks; ++c)
+    total += pa[c] + (cs < 0 || c < cs ? pt[c] : (c == cs ? tie_cs : 0ull));
+  uint64_t best = 0;
+  for (int c = 0; c < kSplitChunks; ++c) {
+    const uint64_t k = a.part_key[r * kSplitChunks + c];
+    best = k > best ? k : best;
+  }
+  if (total == 0) return (int)fg::rank_key_index(best);
+  const uint64_t target = fg::mulhi_u64_u32(total, u);
+  uint64_t before = 0;
+  int c2 = kSplitChunks - 1;
+  for (int c = 0; c < kSplitChunks; ++c) {
+    const uint64_t kc = pa[c] + (cs < 0 || c < cs ? pt[c] : (c == cs ? tie_cs : 0ull));
+    if (before + kc > target) {
+      c2 = c;
+      break;
+    }
+    before += kc;
+  }
+  const Row<DT> r2 = chunk_row<DT>(a, r, c2);
+  const KeptIn kept{kappa, last, (uint32_t)(c2 * a.chunk)};
+  block_sum<true, DT>(r2, kept, sh);
+  const int idx = block_locate<true, DT>(r2, kept, target - before, sh);
+  return idx >= 0 ? c2 * a.chunk + idx : (int)fg::rank_key_index(best);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) split_topp_sample_kernel(SplitArgs a, const uint32_t* __restrict__ noise,
+                                                                     int noise_stride, int noise_col, uint64_t seed,
+                                                                     uint64_t step, const int32_t* __restrict__ seq_ids,
+                                                                     int draw, int32_t* __restrict__ out) {
+  __shared__ Shared sh;
+  const int r = blockIdx.x;
+  if (a.forced && a.forced[r] >= 0) {
+    if (threadIdx.x == 0) out[r] = a.forced[r];
+    return;
+  }
+  const uint32_t seq = seq_ids ? (uint32_t)seq_ids[r] : (uint32_t)r;
+  const uint32_t u = noise_value(noise, (int64_t)r * noise_stride + noise_col, seed, step, seq, (uint32_t)draw);
+  const int tok = split_topp_pick<DT>(a, r, u, sh);
+  if (threadIdx.x == 0) out[r] = tok;
+}
+
+template <int DT>
+__global__ void __launch_bounds__(kThreads) split_topp_walk_kernel(
+    SplitArgs a, const int32_t* __restrict__ tree_tokens, const int32_t* __restrict__ parents,
+    const int32_t* __restrict__ n_nodes, int nmax, int batch, int walk_step, const uint32_t* __restrict__ noise,
+    int noise_stride, int noise_col0, uint64_t seed, uint64_t step, const int32_t* __restrict__ seq_ids, int draw0,
+    int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
+    int32_t* correction, int32_t* state, int32_t* err_flag) {
+  __shared__ Shared sh;
+  const int b = blockIdx.x;
+  if (!state[batch + b]) return;
+  const int parent = state[b];
+  const uint32_t seq = seq_ids ? (uint32_t)seq_ids[b] : (uint32_t)b;
+  const uint32_t u = noise_value(noise, (int64_t)b * noise_stride + noise_col0 + walk_step, seed, step, seq,
+                                 (uint32_t)(draw0 + walk_step));
+  const int tok = split_topp_pick<DT>(a, b, u, sh);
+  if (threadIdx.x == 0)
+    walk_apply(b, tok, parent, tree_tokens, parents, n_nodes, nmax, batch, walk_step, acc_tokens, acc_nodes,
+               acc_stride, acc_len, last_node, correction, state, err_flag);
+}
+
+// Chunk partials of the split top-p path: max, four radix levels, the cut (6 launches).
+template <int DT>
+void split_topp_partials(const SplitArgs& a, int rows, hipStream_t s) {
+  dim3 grid(kSplitChunks, rows);
+  hipLaunchKernelGGL(split_max_kernel<DT>, grid, dim3(kSplitThreads), 0, s, a);
+  for (int level = 0; level < 4; ++level)
+    hipLaunchKernelGGL(split_topp_level_kernel<DT>, grid, dim3(kSplitThreads), 0, s, a, level);
+  hipLaunchKernelGGL(split_topp_cut_kernel<DT>, grid, dim3(kSplitThreads), 0, s, a);
+}
+
 // Chunk partials of the split path: fills a.part_* (2 launches).
 template <int DT>
 void split_partials(const SplitArgs& a, int rows, hipStream_t s) {
@@ -616,7 +911,10 @@ void split_partials(const SplitArgs& a, int rows, hipStream_t s) {
   if (!a.greedy) hipLaunchKernelGGL(split_sum_kernel<DT>, grid, dim3(kSplitThreads), 0, s, a);
 }
 
-size_t split_workspace_bytes(int rows) { return (size_t)rows * kSplitChunks * (4 + 8 + 8) + 64; }
+size_t split_workspace_bytes(int rows) {
+  return (size_t)rows * kSplitChunks * (4 + 8 + 8) + (size_t)rows * kSplitChunks * 256 * 8 +
+         (size_t)rows * 2 * sizeof(SelState) + (size_t)rows * kSplitChunks * 16 + 256;
+}
 
 // Carves the split partials out of a caller workspace; false when it is too small.
 bool split_setup(SplitArgs& a, void* workspace, size_t bytes, int rows, const void* logits, int64_t row_stride,
@@ -625,7 +923,12 @@ bool split_setup(SplitArgs& a, void* workspace, size_t bytes, int rows, const vo
   char* w = (char*)(((uintptr_t)workspace + 15) & ~(uintptr_t)15);
   a.part_key = (uint64_t*)w;
   a.part_sum = a.part_key + (size_t)rows * kSplitChunks;
-  a.part_max = (float*)(a.part_sum + (size_t)rows * kSplitChunks);
+  a.hist = a.part_sum + (size_t)rows * kSplitChunks;
+  a.part_a = a.hist + (size_t)rows * kSplitChunks * 256;
+  a.part_t = a.part_a + (size_t)rows * kSplitChunks;
+  a.sel = (SelState*)(a.part_t + (size_t)rows * kSplitChunks);
+  a.part_max = (float*)(a.sel + (size_t)rows * 2);
+  a.tp32 = 0;
   a.logits = logits;
   a.row_stride = row_stride;
   a.vocab = vocab;
@@ -708,6 +1011,22 @@ int fg_sample_tokens(const void* logits, int dtype, int64_t row_stride, int rows
       split_partials<fg::kF32>(a, rows, s);
       hipLaunchKernelGGL(split_sample_kernel<fg::kF32>, dim3(rows), dim3(kThreads), 0, s, a, noise, noise_stride,
                          noise_col, seed, step, seq_ids, draw, out_tokens);
+    }
+    return fg::check_launch("fg_sample_tokens");
+  }
+  if (!sp.greedy && sp.top_k == 0 && sp.tp32 != 0 &&
+      split_setup(a, workspace, workspace_bytes, rows, logits, row_stride, vocab, temperature, 0)) {
+    a.row_index = row_index;
+    a.forced = forced;
+    a.tp32 = sp.tp32;
+    if (dtype == fg::kBF16) {
+      split_topp_partials<fg::kBF16>(a, rows, s);
+      hipLaunchKernelGGL(split_topp_sample_kernel<fg::kBF16>, dim3(rows), dim3(kThreads), 0, s, a, noise,
+                         noise_stride, noise_col, seed, step, seq_ids, draw, out_tokens);
+    } else {
+      split_topp_partials<fg::kF32>(a, rows, s);
+      hipLaunchKernelGGL(split_topp_sample_kernel<fg::kF32>, dim3(rows), dim3(kThreads), 0, s, a, noise,
+                         noise_stride, noise_col, seed, step, seq_ids, draw, out_tokens);
     }
     return fg::check_launch("fg_sample_tokens");
   }
@@ -802,6 +1121,23 @@ int fg_walk_step(const void* step_logits, int dtype, int64_t row_stride, int voc
     } else {
       split_partials<fg::kF32>(a, batch, s);
       hipLaunchKernelGGL(split_walk_kernel<fg::kF32>, dim3(batch), dim3(kThreads), 0, s, a, tree_tokens, parents,
+                         n_nodes, nmax, batch, walk_step, noise, noise_stride, noise_col0, seed, step, seq_ids, draw0,
+                         acc_tokens, acc_nodes, acc_stride, acc_len, last_node, correction, state, err_flag);
+    }
+    return fg::check_launch("fg_walk_step");
+  }
+  if (!sp.greedy && sp.top_k == 0 && sp.tp32 != 0 &&
+      split_setup(a, workspace, workspace_bytes, batch, step_logits, row_stride, vocab, temperature, 0)) {
+    a.active = state + batch;
+    a.tp32 = sp.tp32;
+    if (dtype == fg::kBF16) {
+      split_topp_partials<fg::kBF16>(a, batch, s);
+      hipLaunchKernelGGL(split_topp_walk_kernel<fg::kBF16>, dim3(batch), dim3(kThreads), 0, s, a, tree_tokens, parents,
+                         n_nodes, nmax, batch, walk_step, noise, noise_stride, noise_col0, seed, step, seq_ids, draw0,
+                         acc_tokens, acc_nodes, acc_stride, acc_len, last_node, correction, state, err_flag);
+    } else {
+      split_topp_partials<fg::kF32>(a, batch, s);
+      hipLaunchKernelGGL(split_topp_walk_kernel<fg::kF32>, dim3(batch), dim3(kThreads), 0, s, a, tree_tokens, parents,
                          n_nodes, nmax, batch, walk_step, noise, noise_stride, noise_col0, seed, step, seq_ids, draw0,
                          acc_tokens, acc_nodes, acc_stride, acc_len, last_node, correction, state, err_flag);
     }

@@ -262,12 +262,15 @@ class FlashMedusaDecoder:
                 row_conf = score[:, 0] - score[:, 1] if kq > 1 else score[:, 0]
             else:
                 row_conf = torch.exp(st[:, 0] - st[:, 1])
-            conf_d = torch.quantile(torch.nan_to_num(row_conf, nan=0.0, posinf=0.0, neginf=0.0), q)
             if adaptive:
-                conf = float(conf_d)  # k_d decides the next depth's width: one sync per depth
+                # k_d decides the next depth's width: one sync per depth, with the
+                # quantile taken on the host (torch.quantile's linear rule)
+                rc = row_conf.float().cpu().numpy()
+                conf = _quantile(np.nan_to_num(rc, nan=0.0, posinf=0.0, neginf=0.0), q)
                 confs_host.append(conf)
                 k = self._topk_from_confidence(conf, base_k, d)
             else:
+                conf_d = torch.quantile(torch.nan_to_num(row_conf, nan=0.0, posinf=0.0, neginf=0.0), q)
                 confs_dev.append(conf_d)
                 k = base_k
             adapted.append(k)

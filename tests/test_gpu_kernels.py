@@ -306,6 +306,64 @@ def test_split_sampling_equals_single_workgroup(dtype, mode):
             assert a.tolist() == b.tolist(), (V, mode, draw)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("mode", [{"top_p": 0.95}, {"top_p": 0.5, "temperature": 0.7}, {"top_p": 0.999},
+                                  {"top_p": 0.9, "temperature": 1.3}])
+def test_split_top_p_equals_single_workgroup(dtype, mode):
+    """Top-p draws split over 16 workgroups (seven launches: max, four radix levels,
+    cut, pick) give the tokens of the one-workgroup radix select, on flat rows, heavy
+    ties, a dominant token, -inf / NaN entries and vocabularies shorter than the
+    chunk count; a few rows are also checked against the oracle."""
+    g = torch.Generator(device="cpu").manual_seed(31)
+    for V in (5, 37, 1000, 32000, 152064):
+        x = torch.randn(40, V, generator=g) * 2.0
+        x[0] = 0.0
+        x[1] = torch.round(x[1])
+        x[2, V // 3] = 30.0
+        x[3, : V // 2] = float("-inf")
+        x[4] = torch.round(x[4] * 4) / 4
+        if V > 8:
+            x[5, 3] = float("nan")
+        xd = x.to(dtype).to(DEV)
+        for draw in range(2):
+            kw = dict(seed=77, step=draw, draw=draw, temperature=mode.get("temperature", 1.0), top_p=mode["top_p"])
+            a = K().sample_tokens(xd, split=True, **kw)
+            b = K().sample_tokens(xd, split=False, **kw)
+            assert a.tolist() == b.tolist(), (V, mode, draw)
+        xs = to_np(xd)
+        for i in (0, 1, 2, 4, 7):
+            want = OS.sample_row(xs[i], OS.counter_noise(77, 1, i, 1), temperature=mode.get("temperature", 1.0),
+                                 top_p=mode["top_p"])
+            assert int(a[i]) == want, (V, mode, i)
+
+
+def test_split_top_p_walk_step_equals_single_workgroup():
+    """The lazy walk's top-p draws (active rows only) through the split path equal the
+    one-workgroup walk step, step by step."""
+    rng = np.random.default_rng(12)
+    B, ks, budget, V = 16, [4, 2, 1], 16, 3000
+    trees, parents, N, slots, packed = _walk_case(rng, B, ks, budget, V, True)
+    tt = torch.tensor([t.tokens for t in trees], dtype=torch.int32, device=DEV)
+    pp = torch.tensor([parents] * B, dtype=torch.int32, device=DEV)
+    nn = torch.full((B,), N, dtype=torch.int32, device=DEV)
+    D = len(ks)
+    walks = []
+    for split in (True, False):
+        w = K().walk_begin(tt, pp, nn, acc_stride=D + 1)
+        for t in range(D):
+            K().walk_rows(w, N)
+            rows = torch.from_numpy(packed[np.minimum(np.arange(B), packed.shape[0] - 1)]).to(DEV)
+            lg = (rows + torch.from_numpy(rng.standard_normal((B, V)).astype(np.float32) * 0.1).to(DEV)
+                  if t == 0 else rows)
+            K().walk_step(w, lg.contiguous(), tt, pp, nn, walk_step=t, seed=5, step=3, top_p=0.9, temperature=0.8,
+                          split=split)
+        walks.append(w)
+        rng = np.random.default_rng(12)  # same perturbation for the second pass
+        _walk_case(rng, B, ks, budget, V, True)
+    for k in ("acc_tokens", "acc_nodes", "acc_len", "last_node", "correction"):
+        assert torch.equal(walks[0][k], walks[1][k]), k
+
+
 def test_sample_tokens_full_vocab_and_counter_noise():
     g = torch.Generator(device="cpu").manual_seed(5)
     V = 152064
