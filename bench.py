@@ -414,9 +414,12 @@ def main():
     log(f"prefill {prefill_s:.1f} s")
     for i in range(args.warmup):
         # the last warm-up round runs like a roofline-timed round (eager forward,
-        # events on the roofline kernel): the first such round of a process has cost
-        # ~40 ms more than the others
+        # events on the roofline kernel), after a full collection of Python's cyclic
+        # garbage (the collector is then paused for the timed rounds, as timeit does)
         last = i == args.warmup - 1
+        if last:
+            gc.collect()
+            gc.disable()
         with timing.active(timing.KernelTimer(only={args.roofline_kernel}) if last else None):
             dec.step(r)
     torch.cuda.synchronize()
@@ -431,10 +434,7 @@ def main():
     torch.cuda.synchronize()
     rounds, seqs = [], []
     tokens = 0
-    # Python's cyclic collector is run before and paused during the timed rounds, as
-    # timeit does: a full collection inside them has cost ~40 ms of one round.
-    gc.collect()
-    gc.disable()
+    # (a full collection inside the timed rounds has cost ~40 ms of one round)
     torch.cuda._sleep(1000)  # trace marker: the timed rounds start after this kernel
     torch.cuda.synchronize()
     t0 = time.perf_counter()

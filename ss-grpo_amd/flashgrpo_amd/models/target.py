@@ -355,6 +355,7 @@ class TargetModel:
                     del d[k]
         if not self._graphs:
             self._retired.clear()
+            self._graph_pool = None  # the pool is released with its last graph; the next capture opens a new one
 
     def forward(self, tokens: torch.Tensor, cache: KVCache, *, pos_offset: torch.Tensor, anc: torch.Tensor,
                 seq_len: torch.Tensor | None = None, row_map: torch.Tensor | None = None,

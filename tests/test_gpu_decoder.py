@@ -447,3 +447,32 @@ def test_lockstep_sparse_adaptive_concurrency():
                          adaptive_tree_enabled=True, adaptive_confidence_low=0.05, adaptive_confidence_high=0.2)
     out, st = _run(SMALL, spec, dtype=torch.float32, B0=2, repeats=3, P=20, max_length=20 + 24)
     assert st["rounds"] > 0 and out["kv_extraction_success_count"] == st["rounds"]
+
+
+def test_graph_replayed_rollouts_equal_eager_rollouts():
+    """Two rollouts in a row on one decoder (graphs captured, replayed, dropped with the
+    first rollout's cache, captured again for the second) emit exactly the tokens of
+    the same rollouts with the eager forward; rows finish at different rounds."""
+    from flashgrpo_amd.decoding import FlashMedusaConfig, FlashMedusaDecoder
+
+    W = OM.random_weights(SMALL16, seed=3, std=0.05)
+    heads = OM.random_medusa(SMALL16.hidden, 3, seed=4, std=0.05)
+    model, mh = build(SMALL16, W, heads, torch.bfloat16)
+    rng = np.random.default_rng(9)
+    outs = {}
+    for graphs in (True, False):
+        cfg = FlashMedusaConfig(num_medusa_heads=3, tree_mode="concurrency_aware", cpeak_nodes=48,
+                                max_tree_nodes_per_seq=16, fixed_tree_topk_by_depth=(4, 2, 1), top_p=0.9,
+                                noise_seed=11, graph_verify_forward=graphs)
+        dec = FlashMedusaDecoder(model, mh, Tok(7), cfg)
+        res = []
+        for P, B, L in ((24, 3, 40), (31, 2, 50)):
+            prompts = np.random.default_rng(P).integers(0, SMALL16.vocab, (B, P))
+            out = dec.generate(torch.from_numpy(prompts), torch.ones(B, P, dtype=torch.long),
+                               repeated_generate_nums=2, max_length=L)
+            res.append(out["generated_token_ids"])
+        outs[graphs] = res
+        assert not model._graphs  # dropped with each rollout
+    assert outs[True] == outs[False]
+    lens = [len(g) for g in outs[True][0]]
+    assert len(set(lens)) > 1 or 7 in sum(outs[True][0], [])  # rows finish apart (EOS) or at max_length
