@@ -325,7 +325,7 @@ def pmc_traffic(fetch_csv, write_csv, symbol, scale):
     for path, counter, k in ((fetch_csv, "FETCH_SIZE", scale[0]), (write_csv, "WRITE_SIZE", scale[1])):
         with open(path, newline="") as fh:
             rows = sorted(csv.DictReader(fh), key=lambda r: int(r["Dispatch_Id"]))
-        marks = [int(r["Dispatch_Id"]) for r in rows if "spin_kernel" in r["Kernel_Name"]]
+        marks = sorted({int(r["Dispatch_Id"]) for r in rows if "spin_kernel" in r["Kernel_Name"]})
         lo, hi = (marks[0], marks[1]) if len(marks) >= 2 else (-1, 1 << 62)  # the timed rounds
         vals = [float(r["Counter_Value"]) for r in rows
                 if lo < int(r["Dispatch_Id"]) < hi and symbol in r["Kernel_Name"] and r["Counter_Name"] == counter]
@@ -342,7 +342,8 @@ def summarize_pmc(path, symbol):
 
     with open(path, newline="") as fh:
         rows = sorted(csv.DictReader(fh), key=lambda r: int(r["Dispatch_Id"]))
-    marks = [int(r["Dispatch_Id"]) for r in rows if "spin_kernel" in r["Kernel_Name"]]
+    # one row per (dispatch, counter): markers are distinct dispatch ids
+    marks = sorted({int(r["Dispatch_Id"]) for r in rows if "spin_kernel" in r["Kernel_Name"]})
     lo, hi = (marks[0], marks[1]) if len(marks) >= 2 else (-1, 1 << 62)
     acc = {}
     for r in rows:
