@@ -113,8 +113,9 @@ int fg_rope_kv_write(const void* qkv, int dtype, int64_t ld_qkv, int batch, int 
                      void* stream);
 
 /* Tree attention: node n of sequence b attends to cache keys [0, seq_len[b]) and to
- * tree keys seq_len[b] + m for every bit m of anc[b*anc_batch_stride + n].
- * q/out [batch, num_nodes, Hq, d]; num_nodes <= 64; bf16 needs d == 128, fp32 d 64 or 128.
+ * tree keys seq_len[b] + m for every bit m of anc[b*anc_batch_stride + n] (num_nodes <= 64).
+ * anc == NULL: the new keys form a causal chain, node n sees new keys 0..n (prefill;
+ * num_nodes <= 8192). q/out [batch, num_nodes, Hq, d]; bf16 needs d == 128, fp32 d 64 or 128.
  * When batch x kv_heads leaves the chip idle (bf16), each sequence's keys are split over
  * several workgroups whose partial softmax states are merged by a second launch; that
  * needs workspace >= fg_tree_attention_workspace(...) (0 when no split is used; a null

@@ -2,8 +2,10 @@
 //
 // Query node n of sequence b (all q heads of one KV head, GQA) attends to the
 // committed prefix keys [0, seq_len[b]) and to tree keys seq_len[b] + m for
-// every node m whose bit is set in the node's 64-bit ancestor-or-self mask.
-// The mask is applied to the scores in registers; no [B, 1, N, P+N] float mask
+// every node m whose bit is set in the node's 64-bit ancestor-or-self mask
+// (with no masks, node n sees new keys 0..n: a causal chain, used by prefill,
+// with up to 8192 new keys). The mask is applied to the scores in registers; no
+// [B, 1, N, P+N] float mask
 // is built (replaces flashgrpo/decoding/tree_attention.py:6-67 feeding the HF
 // decoder's eager/SDPA attention, flashgrpo/models/qwen_flashgrpo_wrapper.py:172-180).
 //
@@ -28,8 +30,9 @@
 //  * per tile all 16 K fragments are read from LDS before the first MFMA and the
 //    16 V^T fragments are read during the S MFMAs (one LDS latency per phase);
 //  * K/V tiles are double-buffered in LDS and staged through two register
-//    stages: the global loads of tile t+2 are issued before tile t is computed
-//    (two tiles in flight per workgroup), one barrier per 64-key tile;
+//    sets: at the top of iteration t the registers of tile t+1 are stored to the
+//    other LDS buffer and the loads of tile t+3 are issued, so tiles t+2 and t+3
+//    are in flight while tile t is computed; one barrier per 64-key tile;
 //  * the ancestor mask is evaluated only on tiles that reach the tree keys, and
 //    the running max (and the O rescale) only moves when a lane's max grows by
 //    more than 2^8, so after the first keys the rescale is almost never taken.
@@ -139,7 +142,8 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
   const bool row_ok = r < M;
   const int qn = row_ok ? r / G : 0;
   const int qh = hkv * G + (row_ok ? r % G : 0);
-  const uint64_t anc = row_ok ? a.anc[(int64_t)b * a.anc_stride + qn] : 1ull;
+  // anc == NULL: the new keys form a chain (prefill), node qn sees new keys 0..qn
+  const uint64_t anc = (row_ok && a.anc) ? a.anc[(int64_t)b * a.anc_stride + qn] : 1ull;
   const uint64_t tree_bits = a.N >= 64 ? anc : anc & ((1ull << a.N) - 1);
   bf16x8 qf[kD / 16];
   {
@@ -255,7 +259,8 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
         for (int c = 0; c < 4; ++c) fr[db * 4 + c] = *(const bf16x8*)(vf_ + db * 32 * kVtPitch + c * 16);
       __builtin_amdgcn_sched_barrier(0);
       if (key0 + kKT > s0 || key0 + kKT > key_end) {  // tile reaches the tree keys or the part's end
-        const uint64_t allowed = (tile_allowed_mask(s0 - key0, tree_bits) & low_bits(key_end - key0)) >> (g * 4);
+        const uint64_t visible = a.anc ? tile_allowed_mask(s0 - key0, tree_bits) : low_bits(s0 + qn + 1 - key0);
+        const uint64_t allowed = (visible & low_bits(key_end - key0)) >> (g * 4);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -385,14 +390,14 @@ __global__ void __launch_bounds__(64) tree_attn_f32_kernel(AttnArgs a) {
   const float* kbase = (const float*)a.k + (int64_t)cb * a.cache_batch + (int64_t)hkv * a.cache_head;
   const float* vbase = (const float*)a.v + (int64_t)cb * a.cache_batch + (int64_t)hkv * a.cache_head;
   const float* qrow = (const float*)a.q + (((int64_t)b * a.N + n) * a.Hq + qh) * D;
-  const uint64_t anc = a.anc[(int64_t)b * a.anc_stride + n];
+  const uint64_t anc = a.anc ? a.anc[(int64_t)b * a.anc_stride + n] : 0ull;
   for (int j = lane; j < D; j += 64) qs[j] = qrow[j];
   __syncthreads();
   float m = -INFINITY, l = 0.0f, o0 = 0.0f, o1 = 0.0f;
   const int total = min(s0 + a.N, a.capacity);
   for (int key0 = 0; key0 < total; key0 += 64) {
     const int key = key0 + lane;
-    const bool ok = key < total && (key < s0 || ((anc >> (key - s0)) & 1ull));
+    const bool ok = key < total && (key < s0 || (a.anc ? ((anc >> (key - s0)) & 1ull) != 0 : key <= s0 + n));
     const float* kr = kbase + (int64_t)min(key, total - 1) * D;
     float acc = 0.0f;
 #pragma unroll
@@ -466,8 +471,9 @@ extern "C" int fg_tree_attention(const void* q, void* out, const void* k_cache, 
                                  const int32_t* seq_len, const int32_t* row_map, const uint64_t* anc,
                                  int64_t anc_batch_stride, float scale, void* workspace, size_t workspace_bytes,
                                  void* stream) {
-  FG_REQUIRE(q && out && k_cache && v_cache && seq_len && anc, "fg_tree_attention: null pointer");
-  FG_REQUIRE(batch > 0 && num_nodes > 0 && num_nodes <= 64, "fg_tree_attention: num_nodes must be in [1, 64]");
+  FG_REQUIRE(q && out && k_cache && v_cache && seq_len, "fg_tree_attention: null pointer");
+  FG_REQUIRE(batch > 0 && num_nodes > 0 && (anc ? num_nodes <= 64 : num_nodes <= 8192),
+             "fg_tree_attention: num_nodes must be in [1, 64] with masks, [1, 8192] for a chain");
   FG_REQUIRE(q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0, "fg_tree_attention: heads");
   FG_REQUIRE(capacity >= num_nodes, "fg_tree_attention: capacity");
   AttnArgs a;

@@ -246,15 +246,16 @@ def rope_kv_write(qkv, *, batch, num_nodes, q_heads, kv_heads, head_dim, seq_len
 
 def tree_attention(q, k_cache, v_cache, *, seq_len, anc, num_nodes, q_heads, kv_heads, head_dim, out=None,
                    row_map=None, scale=None):
-    """q [B, N, Hq, d]; caches [Bc, Hkv, S, d]; anc uint64 as int64 [B, N] or [N]."""
+    """q [B, N, Hq, d]; caches [Bc, Hkv, S, d]; anc uint64 as int64 [B, N] or [N], or None for a
+    causal chain of new keys (node n sees new keys 0..n)."""
     _dev(q, k_cache, v_cache, seq_len, anc, row_map)
     _i32(seq_len, "seq_len")
-    if anc.dtype != torch.int64:
+    if anc is not None and anc.dtype != torch.int64:
         raise TypeError("anc must be int64 (bit pattern of the uint64 masks)")
     B = q.shape[0]
     if out is None:
         out = torch.empty_like(q)
-    anc_stride = 0 if anc.dim() == 1 else anc.stride(0)
+    anc_stride = 0 if anc is None or anc.dim() == 1 else anc.stride(0)
     scale = 1.0 / math.sqrt(head_dim) if scale is None else scale
     capacity = k_cache.shape[2]
     ws, ws_bytes = None, 0

@@ -27,7 +27,9 @@ from .. import kernels as K
 from .. import timing
 from ..tuning import use_tuned_gemms
 
-MAX_TREE_NODES = 64
+MAX_TREE_NODES = 64      # tree nodes per forward (64-bit ancestor masks)
+MAX_CHAIN_TOKENS = 8192  # new tokens per forward without masks (a causal chain)
+PREFILL_CHUNK = 1024     # prompt tokens per prefill forward
 
 
 @dataclass
@@ -363,7 +365,8 @@ class TargetModel:
         """Forward N new tokens per row after each row's committed prefix.
 
         tokens [B, N] int (device); pos_offset int32 [N] (shared) or [B, N]: position =
-        seq_len[b] + pos_offset[(b,) n]; anc: int64 bit masks [N] (shared) or [B, N]; node n's K/V land in cache slot
+        seq_len[b] + pos_offset[(b,) n]; anc: int64 bit masks [N] (shared) or [B, N], or None for a causal
+        chain (node n sees new tokens 0..n; up to MAX_CHAIN_TOKENS); node n's K/V land in cache slot
         seq_len[b] + n of cache row row_map[b]. Returns final-normed hidden [B, N, H].
         ``seq_len`` defaults to ``cache.seq_len`` and is not advanced here.
 
@@ -374,7 +377,7 @@ class TargetModel:
         eagerly so every launch stays visible to it.
         """
         seq_len = cache.seq_len if seq_len is None else seq_len
-        if graph and timing.idle() and not torch.cuda.is_current_stream_capturing():
+        if graph and anc is not None and timing.idle() and not torch.cuda.is_current_stream_capturing():
             key = (tuple(tokens.shape), tokens.dtype, tuple(pos_offset.shape), tuple(anc.shape), cache.kv.data_ptr(),
                    tuple(cache.kv.shape), tuple(seq_len.shape), None if row_map is None else tuple(row_map.shape),
                    None if err_flag is None else err_flag.data_ptr())
@@ -393,8 +396,10 @@ class TargetModel:
     def _forward_eager(self, tokens, cache, *, pos_offset, anc, seq_len, row_map, err_flag):
         cfg = self.cfg
         B, N = tokens.shape
-        if N > MAX_TREE_NODES:
-            raise ValueError(f"at most {MAX_TREE_NODES} new tokens per forward")
+        if anc is not None and N > MAX_TREE_NODES:
+            raise ValueError(f"at most {MAX_TREE_NODES} tree nodes per forward")
+        if N > MAX_CHAIN_TOKENS:
+            raise ValueError(f"at most {MAX_CHAIN_TOKENS} new tokens per forward")
         T = B * N
         H, d = cfg.hidden, cfg.head_dim
         x = self.w["embed"].index_select(0, tokens.reshape(-1).long())  # [T, H] residual stream
@@ -438,9 +443,11 @@ class TargetModel:
         return K.lm_head(x, self.w["lm_head"], row_index=row_index, row_active=row_active, out=out,
                          out_dtype=out_dtype)
 
-    def prefill(self, input_ids: torch.Tensor, cache: KVCache, *, lengths=None, chunk: int = MAX_TREE_NODES,
+    def prefill(self, input_ids: torch.Tensor, cache: KVCache, *, lengths=None, chunk: int = PREFILL_CHUNK,
                 row_map: torch.Tensor | None = None) -> torch.Tensor:
-        """Causal prefill of left-aligned prompts in 64-token chains.
+        """Causal prefill of left-aligned prompts in chains of ``chunk`` tokens (the
+        attention runs without masks: each new token sees the prefix and the chunk's
+        tokens before it).
 
         input_ids [B, P] (device or host) holds each row's valid tokens left-aligned
         (row b has ``lengths[b]`` of them, default P). Writes cache slots [0, len) of
@@ -455,12 +462,12 @@ class TargetModel:
         seq = torch.zeros(B, dtype=torch.int32, device=self.device)
         cache.seq_len.zero_()
         last = torch.empty(B, self.cfg.hidden, dtype=self.dtype, device=self.device)
-        anc_full = as_mask_tensor(chain_bits(chunk), self.device)
+        chunk = max(1, min(int(chunk), MAX_CHAIN_TOKENS))
         offs_full = torch.arange(chunk, dtype=torch.int32, device=self.device)
         for start in range(0, int(lens.max()), chunk):
             n = min(chunk, P - start)
             tok = ids[:, start:start + n].contiguous()
-            hid = self.forward(tok, cache, pos_offset=offs_full[:n], anc=anc_full[:n], seq_len=seq, row_map=row_map)
+            hid = self.forward(tok, cache, pos_offset=offs_full[:n], anc=None, seq_len=seq, row_map=row_map)
             adv = np.clip(lens - start, 0, n)
             ends = np.nonzero((lens > start) & (lens <= start + n))[0]
             if ends.size:

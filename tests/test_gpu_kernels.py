@@ -567,6 +567,40 @@ def test_tree_attention_matches_reference(dtype, d, ks, budget, Hq, Hkv):
     assert rel_err(to_np(out), want) < TOL[dtype]
 
 
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 128), (torch.float32, 64)])
+def test_tree_attention_causal_chain(dtype, d):
+    """No masks (anc None): new token n sees the prefix and new tokens 0..n. Equals the
+    explicit chain masks bit for bit at 64 tokens, and the reference beyond 64 (prefill
+    chunks), with ragged prefixes and GQA."""
+    rng = np.random.default_rng(17)
+    Hq, Hkv = 8, 2
+    for N, seq in ((64, [0, 40, 150]), (300, [0, 77, 5]), (257, [130, 0, 64])):
+        B, S = 3, 520
+        seq = np.array(seq, np.int32)
+        q = torch.from_numpy(rng.standard_normal((B, N, Hq, d)).astype(np.float32)).to(DEV).to(dtype)
+        kt = torch.from_numpy(rng.standard_normal((B, Hkv, S, d)).astype(np.float32)).to(DEV).to(dtype)
+        vt = torch.from_numpy(rng.standard_normal((B, Hkv, S, d)).astype(np.float32)).to(DEV).to(dtype)
+        sl = torch.from_numpy(seq).to(DEV)
+        out = K().tree_attention(q, kt, vt, seq_len=sl, anc=None, num_nodes=N, q_heads=Hq, kv_heads=Hkv, head_dim=d)
+        if N <= 64:
+            bits = [(1 << (n + 1)) - 1 for n in range(N)]
+            anc = torch.from_numpy(np.array(bits, dtype=np.uint64).view(np.int64)).to(DEV)
+            masked = K().tree_attention(q, kt, vt, seq_len=sl, anc=anc, num_nodes=N, q_heads=Hq, kv_heads=Hkv,
+                                        head_dim=d)
+            assert torch.equal(out, masked)
+        qs, ks_, vs = to_np(q), to_np(kt), to_np(vt)
+        for b in range(B):
+            for n in (0, 1, N // 2, N - 1):
+                for hq in (0, 5):
+                    keys = list(range(seq[b] + n + 1))
+                    kk = ks_[b, hq // (Hq // Hkv), keys].astype(np.float64)
+                    vv = vs[b, hq // (Hq // Hkv), keys].astype(np.float64)
+                    sc = kk @ qs[b, n, hq].astype(np.float64) / np.sqrt(d)
+                    p = np.exp(sc - sc.max())
+                    want = (p / p.sum()) @ vv
+                    assert rel_err(to_np(out[b, n, hq]), want) < TOL[dtype], (N, b, n, hq)
+
+
 @pytest.mark.parametrize("ks,budget,Hq,Hkv", [([4, 2, 1, 1], 32, 28, 4), ([2] * 5, 48, 12, 2), ([1] * 63, 64, 4, 1)])
 def test_tree_attention_key_split(ks, budget, Hq, Hkv):
     """Few sequences and a long cache: keys are split over several workgroups (with
