@@ -9,9 +9,12 @@
 // is built (replaces flashgrpo/decoding/tree_attention.py:6-67 feeding the HF
 // decoder's eager/SDPA attention, flashgrpo/models/qwen_flashgrpo_wrapper.py:172-180).
 //
-// bf16 path, one workgroup of 8 waves per (sequence, kv head, 256-row query tile):
+// bf16 path, one workgroup of W waves per (sequence, kv head, 32W-row query tile),
+// W = 8 (one workgroup per CU) when the row tiles fill the chip, else W = 4 (two
+// workgroups per CU, more workgroups for the key split):
 //  * the query tile is the G*N rows (n-major, G = q heads per kv head) of one
-//    KV head, so every K/V tile loaded from HBM serves all of them;
+//    KV head, so every K/V tile loaded from HBM serves all of them; the row tiles
+//    of one KV head run on one XCD and share its L2;
 //  * each wave owns 32 query rows, two waves per SIMD; a wave whose rows are all
 //    past the tile only stages K/V;
 //  * S^T = K Q^T (keys on the M side) puts one query per lane: the online
@@ -19,8 +22,8 @@
 //    half-wave (v_permlane32_swap);
 //  * O^T += V^T P^T: P^T is fed straight from the S^T accumulators (bf16) as the
 //    B operand; l is summed from the same bf16 P (v_dot2c_f32_bf16);
-//  * waves 0-3 stage K, waves 4-7 stage V, with buffer loads over the sequence's
-//    keys [0, min(seq_len + N, capacity)) (loads past the end return 0);
+//  * the first W/2 waves stage K, the others V, with buffer loads over the
+//    sequence's keys [0, min(seq_len + N, capacity)) (loads past the end return 0);
 //  * V^T rows hold the 64 keys of a tile in the order 0-3, 8-11, 4-7, 12-15 per
 //    16-key block, so the 8 keys a lane feeds the PV MFMA (4g..4g+3 and
 //    8+4g..8+4g+3 of a block) are one 16-byte read at a compile-time offset; the
@@ -29,10 +32,10 @@
 //    on distinct banks (reads and writes are conflict-free);
 //  * per tile all 16 K fragments are read from LDS before the first MFMA and the
 //    16 V^T fragments are read during the S MFMAs (one LDS latency per phase);
-//  * K/V tiles are double-buffered in LDS and staged through two register
-//    sets: at the top of iteration t the registers of tile t+1 are stored to the
-//    other LDS buffer and the loads of tile t+3 are issued, so tiles t+2 and t+3
-//    are in flight while tile t is computed; one barrier per 64-key tile;
+//  * K/V tiles are double-buffered in LDS; at the top of iteration t the
+//    registers of tile t+1 are stored to the other LDS buffer and the loads of the
+//    next tile are issued (W = 8: two register sets, tiles t+2 and t+3 in flight;
+//    W = 4: one set, tile t+2); one barrier per 64-key tile;
 //  * the ancestor mask is evaluated only on tiles that reach the tree keys, and
 //    the running max (and the O rescale) only moves when a lane's max grows by
 //    more than 2^8, so after the first keys the rescale is almost never taken.
@@ -72,13 +75,10 @@ struct AttnArgs {
 
 constexpr int kD = 128;            // head dim of the MFMA path
 constexpr int kKT = 64;            // keys per tile
-constexpr int kWaves = 8;
-constexpr int kThreads = kWaves * 64;
-constexpr int kRowsTile = kWaves * 32;
 constexpr int kKPitch = kD + 8;    // bf16 elements per K row in LDS
 constexpr int kVtPitch = kKT + 8;  // bf16 elements per V^T row in LDS (9 16-byte chunks)
 constexpr float kRescaleSlack = 8.0f;  // log2 units
-static_assert(kKT * kD / 8 == 4 * (kThreads / 2), "staging: four 16-byte chunks per thread of a half");
+constexpr int rows_tile(int w) { return w * 32; }
 
 FG_DEVICE int c_row32(int i, int lane) { return (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3); }
 
@@ -110,15 +110,27 @@ FG_DEVICE float xor32_sum(float x) {
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-__global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, int m_tiles) {
+template <int W>
+__global__ void __launch_bounds__(W * 64, 2) tree_attn_bf16_kernel(AttnArgs a, int m_tiles) {
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kKT * kKPitch];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[2][kD * kVtPitch];
   typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+  constexpr int kRowsTile = rows_tile(W);
 
-  const int sp = blockIdx.x % a.splits;
-  const int mt = (blockIdx.x / a.splits) % m_tiles;
-  const int hkv = (blockIdx.x / (a.splits * m_tiles)) % a.Hkv;
-  const int b = blockIdx.x / (a.splits * m_tiles * a.Hkv);
+  // A unit is one (sequence, kv head, key part); its m_tiles row tiles read the same
+  // K/V tiles. Blocks are dispatched round-robin over the 8 XCDs, so the row tiles
+  // of a unit are placed 8 blocks apart: one XCD, dispatched together, the second
+  // read of each K/V tile served from that XCD's L2.
+  int unit = blockIdx.x, mt = 0;
+  if (m_tiles > 1) {
+    const int grp = blockIdx.x / (8 * m_tiles), rem = blockIdx.x % (8 * m_tiles);
+    mt = rem / 8;
+    unit = grp * 8 + rem % 8;
+    if (unit >= a.batch * a.Hkv * a.splits) return;  // grid padded to whole groups of 8 units
+  }
+  const int sp = unit % a.splits;
+  const int hkv = (unit / a.splits) % a.Hkv;
+  const int b = unit / (a.splits * a.Hkv);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
   const int G = a.Hq / a.Hkv;
   const int M = G * a.N;
@@ -163,73 +175,90 @@ __global__ void __launch_bounds__(kThreads) tree_attn_bf16_kernel(AttnArgs a, in
   const float sl2 = a.scale * 1.44269504088896341f;
   const bf16x2 ones2 = __builtin_bit_cast(bf16x2, 0x3f803f80u);
 
-  // Staging: waves 0-3 fetch K (thread t: 16-byte chunk t & 15 of keys (t >> 4) + 16 i),
-  // waves 4-7 fetch V (thread t: dims 8 ((t-256) >> 4) .. +8 of keys 4 ((t-256) & 15) + i),
-  // both with buffer loads over the sequence's keys [0, nkeys) (past them: 0).
-  const bool stage_k = __builtin_amdgcn_readfirstlane(wave) < 4;  // wave-uniform
-  const int st = tid & 255;
+  // Staging: the first W/2 waves fetch K (thread t: 16-byte chunk t & 15 of keys
+  // (t >> 4) + 2W i), the others V (thread t: dims 8 (t >> 4) + 64 u .. +8 of keys
+  // 4 (t & 15) + i), both with buffer loads over the sequence's keys [0, nkeys)
+  // (past them: 0). CH 16-byte chunks per thread and tile.
+  constexpr int CH = 4 * (8 / W);
+  constexpr int KROWS = 2 * W;  // K rows between a thread's chunks
+  const bool stage_k = __builtin_amdgcn_readfirstlane(wave) < W / 2;  // wave-uniform
+  const int st = tid & (W * 32 - 1);
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(stage_k ? kbase : vbase), (short)0, nkeys * (kD * 2), 0x00020000);
   const uint32_t soff = stage_k ? (uint32_t)((st >> 4) * kD + (st & 15) * 8) * 2u
                                 : (uint32_t)(4 * (st & 15) * kD + (st >> 4) * 8) * 2u;
-  const uint32_t sstep = stage_k ? 16u * kD * 2u : 1u * kD * 2u;  // between the thread's 4 chunks
   uint16_t* const st_dst = stage_k ? &Ks[0][(st >> 4) * kKPitch + (st & 15) * 8]
                                    : &Vt[0][(8 * (st >> 4)) * kVtPitch + vt_pos(4 * (st & 15))];
-  v4u xa0, xa1, xa2, xa3, xb0, xb1, xb2, xb3;
-#define FG_LOAD8(X0, X1, X2, X3, KEY0)                                                           \
-  {                                                                                              \
-    const uint32_t o_ = soff + (uint32_t)(KEY0) * (uint32_t)(kD * 2);                            \
-    X0 = __builtin_amdgcn_raw_buffer_load_b128(rsrc, o_, 0, 0);                                  \
-    X1 = __builtin_amdgcn_raw_buffer_load_b128(rsrc, o_ + sstep, 0, 0);                          \
-    X2 = __builtin_amdgcn_raw_buffer_load_b128(rsrc, o_ + 2u * sstep, 0, 0);                     \
-    X3 = __builtin_amdgcn_raw_buffer_load_b128(rsrc, o_ + 3u * sstep, 0, 0);                     \
+  // Byte offset of chunk c from the thread's first chunk.
+  auto chunk_off = [&](int c) -> uint32_t {
+    return stage_k ? (uint32_t)(c * KROWS * kD * 2) : (uint32_t)((c & 3) * kD * 2 + (c >> 2) * 64 * 2);
+  };
+  v4u xa[CH], xb[CH];
+#define FG_LOAD8(X, KEY0)                                                                         \
+  {                                                                                               \
+    const uint32_t o_ = soff + (uint32_t)(KEY0) * (uint32_t)(kD * 2);                             \
+    _Pragma("unroll") for (int c_ = 0; c_ < CH; ++c_) X[c_] =                                     \
+        __builtin_amdgcn_raw_buffer_load_b128(rsrc, o_ + chunk_off(c_), 0, 0);                    \
   }
-#define FG_STORE8(X0, X1, X2, X3, BUF)                                                           \
-  {                                                                                              \
-    if (stage_k) {                                                                               \
-      uint16_t* kd_ = st_dst + (BUF) * (kKT * kKPitch);                                          \
-      *(v4u*)(kd_) = X0;                                                                         \
-      *(v4u*)(kd_ + 16 * kKPitch) = X1;                                                          \
-      *(v4u*)(kd_ + 32 * kKPitch) = X2;                                                          \
-      *(v4u*)(kd_ + 48 * kKPitch) = X3;                                                          \
-    } else {                                                                                     \
-      uint16_t* vd_ = st_dst + (BUF) * (kD * kVtPitch);                                          \
-      _Pragma("unroll") for (int e2 = 0; e2 < 4; ++e2) {                                         \
-        *(uint2*)(vd_ + (2 * e2) * kVtPitch) =                                                   \
-            make_uint2(__builtin_amdgcn_perm(X1[e2], X0[e2], 0x05040100u),                       \
-                       __builtin_amdgcn_perm(X3[e2], X2[e2], 0x05040100u));                      \
-        *(uint2*)(vd_ + (2 * e2 + 1) * kVtPitch) =                                               \
-            make_uint2(__builtin_amdgcn_perm(X1[e2], X0[e2], 0x07060302u),                       \
-                       __builtin_amdgcn_perm(X3[e2], X2[e2], 0x07060302u));                      \
-      }                                                                                          \
-    }                                                                                            \
+#define FG_STORE8(X, BUF)                                                                         \
+  {                                                                                               \
+    if (stage_k) {                                                                                \
+      uint16_t* kd_ = st_dst + (BUF) * (kKT * kKPitch);                                           \
+      _Pragma("unroll") for (int c_ = 0; c_ < CH; ++c_) *(v4u*)(kd_ + c_ * KROWS * kKPitch) = X[c_]; \
+    } else {                                                                                      \
+      _Pragma("unroll") for (int u_ = 0; u_ < CH / 4; ++u_) {                                     \
+        uint16_t* vd_ = st_dst + (BUF) * (kD * kVtPitch) + u_ * 64 * kVtPitch;                    \
+        const v4u* y_ = &X[4 * u_];                                                               \
+        _Pragma("unroll") for (int e2 = 0; e2 < 4; ++e2) {                                        \
+          *(uint2*)(vd_ + (2 * e2) * kVtPitch) =                                                  \
+              make_uint2(__builtin_amdgcn_perm(y_[1][e2], y_[0][e2], 0x05040100u),                \
+                         __builtin_amdgcn_perm(y_[3][e2], y_[2][e2], 0x05040100u));               \
+          *(uint2*)(vd_ + (2 * e2 + 1) * kVtPitch) =                                              \
+              make_uint2(__builtin_amdgcn_perm(y_[1][e2], y_[0][e2], 0x07060302u),                \
+                         __builtin_amdgcn_perm(y_[3][e2], y_[2][e2], 0x07060302u));               \
+        }                                                                                         \
+      }                                                                                           \
+    }                                                                                             \
   }
 
-  // An even number of tiles: a padding tile past key_end is fully masked (its loads
-  // read past the keys or into the next part) and leaves O and l unchanged.
-  const int ntiles = (t_end - t_begin + 1) & ~1;
+  // Tiles are processed in pairs (LDS buffer 0, then 1); when the count is odd the
+  // loop leaves after the first tile of the last pair.
+  const int ntiles = t_end - t_begin;
   const int kbeg = t_begin * kKT;
   // Pipeline: while tile t is computed from LDS buffer t % 2, tile t + 1 is already
   // in the other buffer (stored at the top of the iteration, so the store and its
-  // wait on the loads overlap the compute) and tiles t + 2, t + 3 are in flight in
-  // the two register sets.
-  FG_LOAD8(xa0, xa1, xa2, xa3, kbeg)
-  FG_LOAD8(xb0, xb1, xb2, xb3, kbeg + kKT)
-  FG_STORE8(xa0, xa1, xa2, xa3, 0)
-  FG_LOAD8(xa0, xa1, xa2, xa3, kbeg + 2 * kKT)
+  // wait on the loads overlap the compute). With 8 waves tiles t + 2 and t + 3 are
+  // in flight in two register sets; with 4 waves (twice the chunks per thread, two
+  // workgroups per CU) tile t + 2 is in flight in one.
+  if constexpr (W == 8) {
+    FG_LOAD8(xa, kbeg)
+    FG_LOAD8(xb, kbeg + kKT)
+    FG_STORE8(xa, 0)
+    FG_LOAD8(xa, kbeg + 2 * kKT)
+  } else {
+    FG_LOAD8(xa, kbeg)
+    FG_STORE8(xa, 0)
+    FG_LOAD8(xa, kbeg + kKT)
+  }
   __syncthreads();
   const uint16_t* const kf_src = &Ks[0][l32 * kKPitch + g * 8];
   const uint16_t* const vf_src = &Vt[0][l32 * kVtPitch + g * 8];
   for (int t0 = 0; t0 < ntiles; t0 += 2)
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
+    if (h == 1 && t0 + 1 >= ntiles) break;  // uniform over the workgroup
     const int key0 = kbeg + (t0 + h) * kKT;
-    if (h == 0) {
-      FG_STORE8(xb0, xb1, xb2, xb3, 1)
-      FG_LOAD8(xb0, xb1, xb2, xb3, key0 + 3 * kKT)
+    if constexpr (W == 8) {
+      if (h == 0) {
+        FG_STORE8(xb, 1)
+        FG_LOAD8(xb, key0 + 3 * kKT)
+      } else {
+        FG_STORE8(xa, 0)
+        FG_LOAD8(xa, key0 + 3 * kKT)
+      }
     } else {
-      FG_STORE8(xa0, xa1, xa2, xa3, 0)
-      FG_LOAD8(xa0, xa1, xa2, xa3, key0 + 3 * kKT)
+      FG_STORE8(xa, h ^ 1)
+      FG_LOAD8(xa, key0 + 2 * kKT)
     }
 
     if (computes) {
@@ -435,18 +464,28 @@ __global__ void __launch_bounds__(64) tree_attn_f32_kernel(AttnArgs a) {
 }
 
 
-// Key-split policy: when (sequences x kv heads x row tiles) leaves CUs idle, each
-// workgroup's keys are cut into parts of at least 8 tiles (capacity bound); shorter
-// parts measured no faster than one workgroup per row tile.
-constexpr int kSplitTarget = 256;  // workgroups that fill the chip
+// Waves per workgroup of the bf16 kernel: 8 (one workgroup per CU, every K/V tile
+// staged once per CU) when the row tiles fill the 256 CUs; otherwise 4 (two
+// workgroups per CU, twice as many workgroups for the key split). Measured at the
+// 7B tree shape: 64 sequences 85 us with 8 waves vs 96 with 4; 4 sequences 28 vs 23.5.
+int attn_waves(int batch, int num_nodes, int q_heads, int kv_heads) {
+  const int M = (q_heads / kv_heads) * num_nodes;
+  return batch * kv_heads * ((M + rows_tile(8) - 1) / rows_tile(8)) >= 256 ? 8 : 4;
+}
+
+// Key-split policy: when (sequences x kv heads x row tiles) leaves workgroup slots
+// idle, each workgroup's keys are cut into parts of at least 8 tiles (capacity
+// bound); shorter parts measured no faster than one workgroup per row tile.
 constexpr int kMaxSplits = 16;
 
 int attn_splits(int batch, int num_nodes, int q_heads, int kv_heads, int capacity) {
+  const int w = attn_waves(batch, num_nodes, q_heads, kv_heads);
+  const int target = 256 * (8 / w);  // workgroups that fill the chip
   const int M = (q_heads / kv_heads) * num_nodes;
-  const int base = batch * kv_heads * ((M + kRowsTile - 1) / kRowsTile);
-  if (base >= kSplitTarget) return 1;
+  const int base = batch * kv_heads * ((M + rows_tile(w) - 1) / rows_tile(w));
+  if (base >= target) return 1;
   const int tiles = (capacity + kKT - 1) / kKT;
-  const int sp = std::min((kSplitTarget + base - 1) / base, std::max(1, tiles / 8));
+  const int sp = std::min((target + base - 1) / base, std::max(1, tiles / 8));
   return std::max(1, std::min(sp, kMaxSplits));
 }
 
@@ -454,6 +493,14 @@ size_t attn_workspace_bytes(int splits, int batch, int num_nodes, int q_heads) {
   if (splits <= 1) return 0;
   const size_t rows = (size_t)splits * batch * num_nodes * q_heads;
   return rows * (kD * sizeof(float) + sizeof(float2)) + 256;
+}
+
+template <int W>
+void launch_attn_bf16(const AttnArgs& a, int M, hipStream_t s) {
+  const int m_tiles = (M + rows_tile(W) - 1) / rows_tile(W);
+  const int units = a.batch * a.Hkv * a.splits;
+  const int blocks = m_tiles > 1 ? (units + 7) / 8 * 8 * m_tiles : units;
+  hipLaunchKernelGGL(tree_attn_bf16_kernel<W>, dim3(blocks), dim3(W * 64), 0, s, a, m_tiles);
 }
 
 }  // namespace
@@ -490,20 +537,21 @@ extern "C" int fg_tree_attention(const void* q, void* out, const void* k_cache, 
                "fg_tree_attention: 16-byte alignment");
     FG_REQUIRE((int64_t)capacity * kD * 2 < (1ll << 31), "fg_tree_attention: capacity too large");
     const int M = (q_heads / kv_heads) * num_nodes;
-    const int m_tiles = (M + kRowsTile - 1) / kRowsTile;
     const int splits = attn_splits(batch, num_nodes, q_heads, kv_heads, capacity);
-    if (splits > 1 && workspace && workspace_bytes >= attn_workspace_bytes(splits, batch, num_nodes, q_heads)) {
-      const size_t rows = (size_t)batch * num_nodes * q_heads;
+    const bool split = splits > 1 && workspace &&
+                       workspace_bytes >= attn_workspace_bytes(splits, batch, num_nodes, q_heads);
+    const size_t rows = (size_t)batch * num_nodes * q_heads;
+    if (split) {
       char* w = (char*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
       a.splits = splits;
       a.o_part = (float*)w;
       a.ml_part = (float2*)(w + (size_t)splits * rows * kD * sizeof(float));
-      hipLaunchKernelGGL(tree_attn_bf16_kernel, dim3(batch * kv_heads * m_tiles * splits), dim3(kThreads), 0, s, a,
-                         m_tiles);
-      hipLaunchKernelGGL(tree_attn_combine_kernel, dim3((unsigned)rows), dim3(64), 0, s, a, (int)rows);
-    } else {
-      hipLaunchKernelGGL(tree_attn_bf16_kernel, dim3(batch * kv_heads * m_tiles), dim3(kThreads), 0, s, a, m_tiles);
     }
+    if (attn_waves(batch, num_nodes, q_heads, kv_heads) == 8)
+      launch_attn_bf16<8>(a, M, s);
+    else
+      launch_attn_bf16<4>(a, M, s);
+    if (split) hipLaunchKernelGGL(tree_attn_combine_kernel, dim3((unsigned)rows), dim3(64), 0, s, a, (int)rows);
   } else if (dtype == fg::kF32) {
     FG_REQUIRE(head_dim == 64 || head_dim == 128, "fg_tree_attention: fp32 path supports head_dim 64 or 128");
     FG_REQUIRE(((uintptr_t)k_cache & 15) == 0 && cache_head_stride % 4 == 0 && cache_batch_stride % 4 == 0,

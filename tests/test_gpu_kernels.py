@@ -624,6 +624,48 @@ def test_tree_attention_key_split(ks, budget, Hq, Hkv):
     assert rel_err(to_np(out), want) < TOL[torch.bfloat16]
 
 
+@pytest.mark.parametrize("B,half,ks,budget,Hq,Hkv,S", [(64, 32, [4, 2, 1, 1], 32, 28, 4, 900),
+                                                       (16, 8, [4, 3, 2, 1], 64, 40, 8, 300)])
+def test_tree_attention_wave_layouts_agree(B, half, ks, budget, Hq, Hkv, S):
+    """A batch that fills the chip runs 8-wave workgroups (one or two row tiles per KV
+    head); half of it runs 4-wave workgroups, two per CU (two or three row tiles). Neither
+    splits the keys, so every row sums the same terms in the same order: the half batch
+    equals the first rows of the full batch bit for bit, and sampled rows match the
+    reference."""
+    from flashgrpo_amd import _lib
+
+    rng = np.random.default_rng(B + Hq)
+    parents, depths, _ = OT.dense_topology(ks, budget)
+    N = len(parents)
+    lib = _lib.load()
+    assert lib.fg_tree_attention_workspace(B, N, Hq, Hkv, 128, S) == 0
+    assert lib.fg_tree_attention_workspace(half, N, Hq, Hkv, 128, S) == 0
+    seq = rng.integers(0, S - N + 1, B).astype(np.int32)
+    seq[:3] = [0, S - N, 1]
+    anc = np.array([OT.ancestor_bits(parents)] * B, dtype=np.uint64)
+    q = torch.from_numpy(rng.standard_normal((B, N, Hq, 128)).astype(np.float32)).to(DEV).to(torch.bfloat16)
+    kt = torch.from_numpy(rng.standard_normal((B, Hkv, S, 128)).astype(np.float32)).to(DEV).to(torch.bfloat16)
+    vt = torch.from_numpy(rng.standard_normal((B, Hkv, S, 128)).astype(np.float32)).to(DEV).to(torch.bfloat16)
+    anct = torch.from_numpy(anc.view(np.int64)).to(DEV)
+    sl = torch.from_numpy(seq).to(DEV)
+    kw = dict(num_nodes=N, q_heads=Hq, kv_heads=Hkv, head_dim=128)
+    full = K().tree_attention(q, kt, vt, seq_len=sl, anc=anct, **kw)
+    part = K().tree_attention(q[:half].contiguous(), kt[:half].contiguous(), vt[:half].contiguous(),
+                              seq_len=sl[:half].contiguous(), anc=anct[:half].contiguous(), **kw)
+    assert torch.equal(full[:half], part)
+    qs, ks_, vs = to_np(q), to_np(kt), to_np(vt)
+    G = Hq // Hkv
+    for b in (0, 1, 2, half, B - 1):
+        for n in (0, N // 2, N - 1):
+            for hq in (0, Hq - 1):
+                keys = list(range(seq[b])) + [seq[b] + m for m in range(N) if (int(anc[b][n]) >> m) & 1]
+                kk = ks_[b, hq // G, keys].astype(np.float64)
+                vv = vs[b, hq // G, keys].astype(np.float64)
+                sc = kk @ qs[b, n, hq].astype(np.float64) / np.sqrt(128)
+                p = np.exp(sc - sc.max())
+                assert rel_err(to_np(full[b, n, hq]), (p / p.sum()) @ vv) < TOL[torch.bfloat16], (b, n, hq)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_rope_kv_write_rmsnorm_swiglu(dtype):
     rng = np.random.default_rng(9)
