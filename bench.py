@@ -44,20 +44,20 @@ FP32_PEAK_TFLOPS = 157.3
 WORKLOADS = {
     "7b": dict(target="qwen25_7b", prompts=8, repeats=8, prefix=2048, heads=4, tree_mode="concurrency_aware",
                cpeak=2048, max_nodes=32, max_depth=5, topk=(4, 3, 2), adaptive=True, temperature=1.0,
-               name="qwen2.5-7b-shape B64 P2048 4 Medusa heads adaptive 32-node tree"),
+               rollout_rounds=512, name="qwen2.5-7b-shape B64 P2048 4 Medusa heads adaptive 32-node tree"),
     "1.5b": dict(target="qwen25_1p5b", prompts=4, repeats=8, prefix=512, heads=3, tree_mode="concurrency_aware",
                  cpeak=512, max_nodes=16, max_depth=4, topk=(4, 3, 2), adaptive=False, temperature=1.0,
-                 name="qwen2.5-1.5b-shape B32 P512 3 Medusa heads 16-node tree"),
+                 rollout_rounds=256, name="qwen2.5-1.5b-shape B32 P512 3 Medusa heads 16-node tree"),
     "14b": dict(target="qwen25_14b", prompts=16, repeats=8, prefix=4096, heads=4, tree_mode="concurrency_aware",
                 cpeak=8192, max_nodes=64, max_depth=5, topk=(4, 3, 2), adaptive=False, temperature=1.0,
-                name="qwen2.5-14b-shape B128 P4096 4 Medusa heads 64-node tree"),
+                rollout_rounds=256, name="qwen2.5-14b-shape B128 P4096 4 Medusa heads 64-node tree"),
     "8b": dict(target="llama31_8b", prompts=12, repeats=8, prefix=1024, heads=4, tree_mode="concurrency_aware",
                cpeak=4608, max_nodes=48, max_depth=5, topk=(4, 3, 2), adaptive=True, temperature=0.7,
                proposal="chain", conf_low=0.20, conf_high=0.70,
-               name="llama-3.1-8b-shape B96 P1024 chain proposals (Medusa head 1 + ChainDraftCell) 48-node tree"),
+               rollout_rounds=256, name="llama-3.1-8b-shape B96 P1024 chain proposals (Medusa head 1 + ChainDraftCell) 48-node tree"),
     "tiny": dict(target="tiny", prompts=4, repeats=2, prefix=256, heads=3, tree_mode="fixed", cpeak=64,
                  max_nodes=16, max_depth=4, topk=(4, 3, 2), adaptive=False, temperature=1.0,
-                 name="tiny-qwen2 B8 P256 3 Medusa heads fixed 16-node tree"),
+                 rollout_rounds=32, name="tiny-qwen2 B8 P256 3 Medusa heads fixed 16-node tree"),
 }
 
 
@@ -550,6 +550,7 @@ def main():
         log("cpu baseline ...")
         cpu = cpu_baseline(model, heads, r, work, seed=args.seed + 2, layers=args.cpu_layers)
         log(f"cpu baseline {cpu['seconds']} s")
+    R = int(work["rollout_rounds"])
     res = {
         "metric": "rollout tok/s per MI355X (Qwen2.5-7B shape); verify-step latency; % roofline",
         "value": round(tokens / elapsed, 2),
@@ -571,6 +572,11 @@ def main():
         "tokens": int(tokens),
         "accept_len_mean": round(tokens / max(sum(x["batch"] for x in rounds), 1), 4),
         "prefill_s": round(prefill_s, 2),
+        # The reference's own rate (generated tokens over generation time including the
+        # prefill, flashgrpo_trainer.py:1117) for a rollout of the config's decode rounds,
+        # from the measured prefill and the measured per-round time and tokens.
+        "with_prefill": {"tok_s": round(tokens / args.steps * R / (prefill_s + elapsed / args.steps * R), 2),
+                         "decode_rounds": R},
         "hand_kernels_ms_per_step": round(mine_ms / args.steps, 3),
         "ms_per_step_instrumented": round(elapsed_i / args.steps * 1e3, 3),
         "phases_ms": phases,
