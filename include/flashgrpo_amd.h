@@ -198,7 +198,9 @@ int fg_accept_finalize(const int32_t* acc_tokens, const int32_t* acc_nodes, int 
  * [Bc, kv_heads, capacity, head_dim] with the given element strides, moves rows
  * seq_len[b] + acc_nodes[b, j] to seq_len[b] + j for j < acc_len[b]. All sources
  * are read before any destination is written. Does not modify seq_len.
- * err_flag bit 1: a node index was outside [0, tree_nodes) (that row is skipped). */
+ * acc_stride (the longest accepted path) is at most 32.
+ * err_flag bit 1: a node index was outside [0, tree_nodes) or a path was longer than the
+ * tree (that row is skipped). */
 int fg_kv_path_gather(const uint64_t* tensor_ptrs, int num_tensors, int batch, int kv_heads, int head_dim,
                       int elem_bytes, int64_t batch_stride, int64_t head_stride, int64_t row_stride, int capacity,
                       const int32_t* seq_len, const int32_t* row_map, const int32_t* acc_nodes, int acc_stride,

@@ -51,15 +51,18 @@ def noise_i32(n_rows, n_cols, seed):
 
 
 # ------------------------------------------------------------------ KV gather
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_kv_path_gather_matches_oracle(dtype):
+@pytest.mark.parametrize("dtype,width", [(torch.bfloat16, 5), (torch.float32, 5), (torch.bfloat16, 12)])
+def test_kv_path_gather_matches_oracle(dtype, width):
+    """Paths with self-copies, crossing rows (a destination that is an earlier row's
+    source, and a swap) and, at width 12, the long-path kernel."""
     torch.manual_seed(0)
     L, B, H, S, D = 3, 5, 2, 40, 128 if dtype == torch.bfloat16 else 64
     caches = [torch.randn(B, H, S, D, device=DEV).to(dtype) for _ in range(2 * L)]
     before = [to_np(c) for c in caches]
     seq = np.array([3, 10, 0, 20, 7], np.int32)
-    paths = [[0, 2, 5, 7], [0], [0, 1], [0, 3, 4], [0, 6, 8, 9, 11]]
-    width = 5
+    paths = [[0, 2, 5, 7], [0], [0, 2, 1], [0, 3, 4], [0, 6, 8, 9, 11]]
+    if width > 8:
+        paths[3] = [0, 2, 5, 7, 9, 10, 13, 14, 15, 16, 17, 19]
     nodes = np.zeros((B, width), np.int32)
     for b, p in enumerate(paths):
         nodes[b, :len(p)] = p
@@ -70,7 +73,7 @@ def test_kv_path_gather_matches_oracle(dtype):
     K().kv_path_gather(ptrs, batch=B, kv_heads=H, head_dim=D, elem_bytes=c0.element_size(),
                        strides=(c0.stride(0), c0.stride(1), c0.stride(2)), capacity=S,
                        seq_len=torch.from_numpy(seq).to(DEV), acc_nodes=torch.from_numpy(nodes).to(DEV),
-                       acc_len=torch.from_numpy(lens).to(DEV), tree_nodes=12, err_flag=err)
+                       acc_len=torch.from_numpy(lens).to(DEV), tree_nodes=20, err_flag=err)
     torch.cuda.synchronize()
     assert int(err.item()) == 0
     for c, bef in zip(caches, before):
@@ -114,6 +117,16 @@ def test_kv_path_gather_seed17_golden_and_bounds():
     torch.cuda.synchronize()
     assert int(err.item()) & 1
     assert np.array_equal(to_np(key)[0], before[0])
+    # a path longer than the tree (3 accepted rows, 2 tree nodes): flagged, rows untouched
+    err.zero_()
+    before = to_np(key).copy()
+    K().kv_path_gather(ptrs, batch=B, kv_heads=H, head_dim=D, elem_bytes=4, strides=(key.stride(0), key.stride(1), D),
+                       capacity=S, seq_len=seq, acc_nodes=torch.tensor([[0, 1, 1], [0, 1, 1]], dtype=torch.int32,
+                                                                       device=DEV),
+                       acc_len=torch.tensor([3, 1], dtype=torch.int32, device=DEV), tree_nodes=2, err_flag=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) & 1
+    assert np.array_equal(to_np(key), before)
 
 
 # ------------------------------------------------------------------ top-k / layout
