@@ -480,3 +480,34 @@ class TargetModel:
         else:
             cache.seq_len.index_copy_(0, row_map.long(), seq)
         return last
+
+
+def forward_tree(causal_lm: TargetModel, ids: torch.Tensor, mask4d: torch.Tensor, pkv: KVCache, pos: torch.Tensor, *,
+                 clone_past: bool = True, compute_logits: bool = True) -> dict:
+    """Tree-verify forward with the reference's call shape
+    (``flashgrpo/models/qwen_flashgrpo_wrapper.py:220-239``).
+
+    ``ids`` [B, N], ``mask4d`` [B, 1, N, P + N] and ``pos`` [B, N] are the outputs of
+    ``decoding.tree_attention.build_tree_attention_inputs``. The tree block of the
+    additive mask (its last N columns) becomes one ancestor-or-self bit word per node,
+    applied in registers by the tree-attention kernel; the prefix a node sees is the
+    cache row's committed tokens ``[0, pkv.seq_len[b])`` (the valid prefix slots the
+    reference's mask marks), and positions become offsets from ``pkv.seq_len``. Node
+    n's K/V land in slot ``seq_len[b] + n`` of the cache, past the committed tokens,
+    so the past is never modified and ``clone_past`` needs no copy. Returns
+    ``{"hidden_states": [B, N, H], "logits": [B, N, V] or None, "past_key_values": pkv}``.
+    """
+    B, N = ids.shape
+    if mask4d.dim() != 4 or mask4d.shape[0] != B or mask4d.shape[2] != N or mask4d.shape[3] < N:
+        raise ValueError(f"forward_tree: mask4d {tuple(mask4d.shape)} does not match ids {tuple(ids.shape)}")
+    if N > 64:
+        raise ValueError("forward_tree: trees larger than 64 nodes are not supported")
+    dev = causal_lm.device
+    allowed = mask4d[:, 0, :, -N:] > torch.finfo(mask4d.dtype).min / 2           # [B, N, N]
+    shifts = torch.arange(N, dtype=torch.int64, device=allowed.device)
+    anc = (allowed.to(torch.int64) << shifts).sum(-1).to(dev)                      # distinct bits: sum == or
+    offset = (pos.to(device=dev, dtype=torch.int64) - pkv.seq_len.to(torch.int64)[:, None]).to(torch.int32)
+    hidden = causal_lm.forward(ids.to(device=dev, dtype=torch.int32), pkv, pos_offset=offset.contiguous(),
+                               anc=anc.contiguous())
+    logits = causal_lm.logits(hidden.reshape(B * N, -1)).view(B, N, -1) if compute_logits else None
+    return {"hidden_states": hidden, "logits": logits, "past_key_values": pkv}

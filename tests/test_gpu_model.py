@@ -163,3 +163,48 @@ def test_graph_forward_replays_match_eager(dtype):
     assert len(graphs) == 2  # the shared-mask and the per-row-mask shapes, each replayed
     m.drop_graphs(cache)
     assert not m._graphs
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_forward_tree_reference_call_shape(dtype):
+    """forward_tree(causal_lm, ids, mask4d, pkv, pos) on the outputs of
+    build_tree_attention_inputs (ragged trees, padded nodes): hidden states equal the
+    native forward with the trees' ancestor words bit for bit and match the oracle on
+    every real node; logits are the LM head of those hidden states."""
+    from flashgrpo_amd.decoding.medusa_tree import CandidateTree, TreeTopology
+    from flashgrpo_amd.decoding.tree_attention import build_tree_attention_inputs, tree_ancestor_bits
+    from flashgrpo_amd.models import forward_tree
+
+    ocfg = _cfgs(dtype)
+    W = OM.random_weights(ocfg, seed=8, std=0.05)
+    m = _model(ocfg, W, dtype)
+    Wr = _rounded(W, dtype)
+    rng = np.random.default_rng(9)
+    B, P = 3, 80
+    lens = np.array([80, 33, 51])
+    prompts = rng.integers(0, ocfg.vocab, (B, P))
+    cache = m.new_cache(B, 160)
+    m.prefill(torch.from_numpy(prompts).to(DEV), cache, lengths=lens)
+    topo = TreeTopology([4, 2, 1], 16)
+    sizes = [topo.num_nodes, 7, 1]
+    trees = [CandidateTree([int(x) for x in rng.integers(0, ocfg.vocab, n)], list(topo.parents[:n]),
+                           list(topo.depths[:n])) for n in sizes]
+    full_mask = torch.zeros(B, P, dtype=torch.long)
+    for b in range(B):
+        full_mask[b, :lens[b]] = 1
+    ids, mask4d, pos, valid = build_tree_attention_inputs(trees, full_mask.to(DEV), cache.seq_len.long(),
+                                                          pad_token_id=0, dtype=m.dtype)
+    out = forward_tree(m, ids, mask4d, cache, pos, clone_past=True, compute_logits=True)
+    N = ids.shape[1]
+    assert out["past_key_values"] is cache and cache.seq_len.cpu().tolist() == lens.tolist()
+    anc = tree_ancestor_bits(trees, N).to(DEV)
+    offset = (pos - cache.seq_len.long()[:, None]).to(torch.int32)
+    direct = m.forward(ids.to(torch.int32), cache, pos_offset=offset, anc=anc)
+    assert torch.equal(out["hidden_states"], direct)
+    assert torch.equal(out["logits"], m.logits(direct.reshape(B * N, -1)).view(B, N, -1))
+    for b in range(B):
+        n = sizes[b]
+        _, ks, vs = OM.prefill(ocfg, Wr, prompts[b:b + 1, :lens[b]])
+        want, _, _ = OM.tree_verify(ocfg, Wr, np.array([trees[b].tokens]), [trees[b].depths], [trees[b].parents],
+                                    ks, vs, [lens[b]])
+        assert rel(out["hidden_states"][b, :n].float().cpu().numpy(), want[0]) < TOL[dtype]
