@@ -399,6 +399,13 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     work = dict(WORKLOADS[args.config], top_p=args.top_p)
+    if args.warmup < 3:
+        # the verify forward's HIP graph is captured on its second graph round and the last
+        # warm-up round runs eagerly under the kernel timer, so fewer than three warm-up
+        # rounds would leave the capture inside the timed rounds
+        print(f"bench: warmup raised from {args.warmup} to 3 (graph capture before the timed rounds)",
+              file=sys.stderr, flush=True)
+        args.warmup = 3
     dtype = torch.float32 if args.config == "tiny" else torch.bfloat16
     elem = 4 if dtype == torch.float32 else 2
     log = lambda msg: print(f"bench: {msg}", file=sys.stderr, flush=True)
