@@ -767,6 +767,64 @@ __global__ void __launch_bounds__(256) medusa_ln_kernel(const void* __restrict__
     }
 }
 
+// LayerNorm of the Medusa block with one workgroup per (row, head): the row is held in
+// registers (16-byte loads, H a multiple of 8, at most 8192), its mean and variance reduced
+// over the workgroup, and the head's affine output written with 16-byte stores.
+template <int HDT, int ODT>
+__global__ void __launch_bounds__(256) medusa_ln_vec_kernel(const void* __restrict__ h, int64_t ldh, int H, int batch,
+                                                            const float* __restrict__ ln_w,
+                                                            const float* __restrict__ ln_b, float eps,
+                                                            void* __restrict__ out) {
+  constexpr int KMAX = 4;
+  const int b = blockIdx.x, hd = blockIdx.y, tid = threadIdx.x;
+  const int nchunk = H >> 3;
+  const void* row = (const char*)h + (int64_t)b * ldh * (HDT == fg::kBF16 ? 2 : 4);
+  __shared__ float red[8];
+  float x[KMAX][8];
+  float s = 0.0f;
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    const int c = tid + k * 256;
+    if (c < nchunk) {
+      fg::load8<HDT>(row, (int64_t)c * 8, x[k]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += x[k][j];
+    }
+  }
+  s = fg::wave_sum(s);
+  if ((tid & 63) == 0) red[tid >> 6] = s;
+  __syncthreads();
+  const float mean = (red[0] + red[1] + red[2] + red[3]) / (float)H;
+  float v = 0.0f;
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k)
+    if (tid + k * 256 < nchunk) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float d = x[k][j] - mean;
+        v += d * d;
+      }
+    }
+  v = fg::wave_sum(v);
+  if ((tid & 63) == 0) red[4 + (tid >> 6)] = v;
+  __syncthreads();
+  const float rstd = rsqrtf((red[4] + red[5] + red[6] + red[7]) / (float)H + eps);
+  const float* w = ln_w + (int64_t)hd * H;
+  const float* bb = ln_b + (int64_t)hd * H;
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    const int c = tid + k * 256;
+    if (c < nchunk) {
+      float wv[8], bv[8], y[8];
+      fg::load8<fg::kF32>(w, (int64_t)c * 8, wv);
+      fg::load8<fg::kF32>(bb, (int64_t)c * 8, bv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = (x[k][j] - mean) * rstd * wv[j] + bv[j];
+      fg::store8<ODT>(out, ((int64_t)hd * batch + b) * H + (int64_t)c * 8, y);
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -797,7 +855,15 @@ int fg_medusa_heads(const void* hidden, int dtype, int batch, int H, int64_t ldh
   FG_REQUIRE(dtype == fg::kF32 || dtype == fg::kBF16, "fg_medusa_heads: dtype");
   FG_REQUIRE(workspace_bytes >= (size_t)batch * H * heads * fg::elem_bytes(dtype), "fg_medusa_heads: workspace");
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == fg::kBF16)
+  const bool vec = H % 8 == 0 && H <= 8 * 256 * 4 && ldh % 8 == 0 && ((uintptr_t)hidden & 15) == 0 &&
+                   ((uintptr_t)workspace & 15) == 0 && ((uintptr_t)ln_w & 15) == 0 && ((uintptr_t)ln_b & 15) == 0;
+  if (vec && dtype == fg::kBF16)
+    hipLaunchKernelGGL((medusa_ln_vec_kernel<fg::kBF16, fg::kBF16>), dim3(batch, heads), dim3(256), 0, s, hidden, ldh,
+                       H, batch, ln_w, ln_b, ln_eps, workspace);
+  else if (vec)
+    hipLaunchKernelGGL((medusa_ln_vec_kernel<fg::kF32, fg::kF32>), dim3(batch, heads), dim3(256), 0, s, hidden, ldh,
+                       H, batch, ln_w, ln_b, ln_eps, workspace);
+  else if (dtype == fg::kBF16)
     hipLaunchKernelGGL((medusa_ln_kernel<fg::kBF16, fg::kBF16>), dim3(batch), dim3(256), 0, s, hidden, ldh, H, heads,
                        batch, ln_w, ln_b, ln_eps, workspace);
   else
