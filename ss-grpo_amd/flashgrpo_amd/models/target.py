@@ -482,6 +482,20 @@ class TargetModel:
         return last
 
 
+def native_tree_inputs(mask4d: torch.Tensor, pos: torch.Tensor, seq_len: torch.Tensor):
+    """(anc int64 [B, N], pos_offset int32 [B, N]) of the native verify forward from the
+    reference's additive mask [B, 1, N, P + N] and position ids [B, N]: bit m of node n's
+    word is set where the mask's tree block lets n see node m; offsets are positions
+    minus each row's committed length. On the device of ``mask4d``."""
+    N = mask4d.shape[2]
+    allowed = mask4d[:, 0, :, -N:] > torch.finfo(mask4d.dtype).min / 2           # [B, N, N]
+    shifts = torch.arange(N, dtype=torch.int64, device=allowed.device)
+    anc = (allowed.to(torch.int64) << shifts).sum(-1)                              # distinct bits: sum == or
+    offset = pos.to(device=allowed.device, dtype=torch.int64) - seq_len.to(device=allowed.device,
+                                                                            dtype=torch.int64)[:, None]
+    return anc.contiguous(), offset.to(torch.int32).contiguous()
+
+
 def forward_tree(causal_lm: TargetModel, ids: torch.Tensor, mask4d: torch.Tensor, pkv: KVCache, pos: torch.Tensor, *,
                  clone_past: bool = True, compute_logits: bool = True) -> dict:
     """Tree-verify forward with the reference's call shape
@@ -503,11 +517,8 @@ def forward_tree(causal_lm: TargetModel, ids: torch.Tensor, mask4d: torch.Tensor
     if N > 64:
         raise ValueError("forward_tree: trees larger than 64 nodes are not supported")
     dev = causal_lm.device
-    allowed = mask4d[:, 0, :, -N:] > torch.finfo(mask4d.dtype).min / 2           # [B, N, N]
-    shifts = torch.arange(N, dtype=torch.int64, device=allowed.device)
-    anc = (allowed.to(torch.int64) << shifts).sum(-1).to(dev)                      # distinct bits: sum == or
-    offset = (pos.to(device=dev, dtype=torch.int64) - pkv.seq_len.to(torch.int64)[:, None]).to(torch.int32)
-    hidden = causal_lm.forward(ids.to(device=dev, dtype=torch.int32), pkv, pos_offset=offset.contiguous(),
-                               anc=anc.contiguous())
+    anc, offset = native_tree_inputs(mask4d, pos, pkv.seq_len)
+    hidden = causal_lm.forward(ids.to(device=dev, dtype=torch.int32), pkv, pos_offset=offset.to(dev),
+                               anc=anc.to(dev))
     logits = causal_lm.logits(hidden.reshape(B * N, -1)).view(B, N, -1) if compute_logits else None
     return {"hidden_states": hidden, "logits": logits, "past_key_values": pkv}

@@ -321,3 +321,29 @@ def test_sparse_tree_extras_budget_and_widths():
     assert t.node_count == 8 and t.depths == [1, 2, 2, 2, 2, 3, 3, 3]  # cut at the budget
     plan = T.Plan(10, 0, [], 1, "fixed", "sparse_asymmetric", [], 1, 8, 1.0, 0.05)
     assert T.build_sparse_trees([3, 4], _proposal_logits(2), plan)[1].tokens == [4]
+
+
+def test_native_tree_inputs_from_reference_mask():
+    """forward_tree's conversion: the tree block of build_tree_attention_inputs' additive
+    mask gives each node its ancestor-or-self word (padded nodes: themselves only), and
+    positions become offsets from the committed lengths (depth - 1 on real nodes)."""
+    import torch
+
+    from flashgrpo_amd.decoding.medusa_tree import CandidateTree, TreeTopology
+    from flashgrpo_amd.decoding.tree_attention import build_tree_attention_inputs, tree_ancestor_bits
+    from flashgrpo_amd.models.target import native_tree_inputs
+
+    topo = TreeTopology([4, 3, 2], 40)
+    sizes = [topo.num_nodes, 9, 1]
+    trees = [CandidateTree(list(range(n)), list(topo.parents[:n]), list(topo.depths[:n])) for n in sizes]
+    lens = torch.tensor([50, 7, 0])
+    full = torch.zeros(3, 60, dtype=torch.long)
+    for b, L in enumerate(lens.tolist()):
+        full[b, :L] = 1
+    for dtype in (torch.float32, torch.bfloat16):
+        ids, mask, pos, valid = build_tree_attention_inputs(trees, full, lens, pad_token_id=0, dtype=dtype)
+        anc, off = native_tree_inputs(mask, pos, lens.to(torch.int32))
+        assert torch.equal(anc, tree_ancestor_bits(trees, ids.shape[1]))
+        depth = torch.tensor([list(t.depths) + [1] * (ids.shape[1] - t.node_count) for t in trees])
+        want = torch.where(valid, depth - 1, -lens[:, None])
+        assert off.dtype == torch.int32 and torch.equal(off.long(), want)
