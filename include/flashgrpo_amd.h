@@ -151,6 +151,22 @@ int fg_sample_tokens(const void* logits, int dtype, int64_t row_stride, int rows
                      float temperature, int greedy, int top_k, uint32_t top_p_fixed, int32_t* out_tokens,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* fg_sample_tokens without a workspace argument and without any allocation. No
+ * counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The split partials live in a static device array of the library (8.6 MB per GPU,
+ * held until the process ends) that holds rows <= fg_sample_tokens_noalloc_max_rows()
+ * (256); more rows are rejected with an error. Same arguments, rule and tokens as
+ * fg_sample_tokens with a large enough workspace. Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (on different streams, or from several
+ * threads) race and must be ordered by the caller. */
+size_t fg_sample_tokens_noalloc_max_rows(void);
+int fg_sample_tokens_noalloc(const void* logits, int dtype, int64_t row_stride, int rows, int vocab,
+                             const int32_t* row_index, const int32_t* forced, const uint32_t* noise,
+                             int noise_stride, int noise_col, uint64_t seed, uint64_t step, const int32_t* seq_ids,
+                             int draw, float temperature, int greedy, int top_k, uint32_t top_p_fixed,
+                             int32_t* out_tokens, void* stream);
+
 /* exact_target acceptance walk over `batch` trees (one launch per walk step).
  * Node n of tree b: tree_tokens/parents[b*nmax + n], n < n_nodes[b], root = node 0.
  * Logits of node n: row slot_map[b*nmax + n] of tree_logits (packed internal nodes),

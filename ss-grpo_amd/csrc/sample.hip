@@ -19,6 +19,8 @@
 // contiguous wave segments; a wave walks its segment 512 elements (8 per lane,
 // 16-byte loads) per step. Top-k / top-p use an MSB-first 4 x 8-bit radix
 // select over the keys with count or q-weighted histograms in LDS.
+#include <mutex>
+
 #include "fg_common.h"
 
 namespace {
@@ -911,9 +913,41 @@ void split_partials(const SplitArgs& a, int rows, hipStream_t s) {
   if (!a.greedy) hipLaunchKernelGGL(split_sum_kernel<DT>, grid, dim3(kSplitThreads), 0, s, a);
 }
 
-size_t split_workspace_bytes(int rows) {
+constexpr size_t split_workspace_bytes(int rows) {
   return (size_t)rows * kSplitChunks * (4 + 8 + 8) + (size_t)rows * kSplitChunks * 256 * 8 +
          (size_t)rows * 2 * sizeof(SelState) + (size_t)rows * kSplitChunks * 16 + 256;
+}
+
+// Scratch of fg_sample_tokens_noalloc: the split partials of up to
+// kNoAllocMaxRows rows (8.6 MB per device, held until the process ends). Each
+// kernel of the split paths writes every partial it owns before a later launch
+// reads it, so nothing in it has to start at zero. Host code never hands
+// `scratch` itself to a kernel (in host code the name is only a stand-in): it
+// passes the per-device address that hipGetSymbolAddress returns.
+constexpr int kNoAllocMaxRows = 256;
+constexpr size_t kScratchBytes = split_workspace_bytes(kNoAllocMaxRows);
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per device.
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fg::fail("fg_sample_tokens_noalloc: no current HIP device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fg::fail(std::string("fg_sample_tokens_noalloc: hipGetSymbolAddress(scratch) failed: ") +
+                      hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
 }
 
 // Carves the split partials out of a caller workspace; false when it is too small.
@@ -980,22 +1014,17 @@ SampleParams make_params(float temperature, int greedy, int top_k, int vocab, ui
   return sp;
 }
 
-}  // namespace
-
-extern "C" {
-
-size_t fg_sample_workspace(int rows) { return rows > 0 ? split_workspace_bytes(rows) : 0; }
-
-int fg_sample_tokens(const void* logits, int dtype, int64_t row_stride, int rows, int vocab,
-                     const int32_t* row_index, const int32_t* forced, const uint32_t* noise, int noise_stride,
-                     int noise_col, uint64_t seed, uint64_t step, const int32_t* seq_ids, int draw,
-                     float temperature, int greedy, int top_k, uint32_t top_p_fixed, int32_t* out_tokens,
-                     void* workspace, size_t workspace_bytes, void* stream) {
-  FG_REQUIRE(logits && out_tokens, "fg_sample_tokens: null pointer");
-  FG_REQUIRE(rows > 0 && vocab > 0 && vocab < (1 << 23), "fg_sample_tokens: vocab must be in [1, 2^23)");
-  FG_REQUIRE(dtype == fg::kF32 || dtype == fg::kBF16, "fg_sample_tokens: dtype");
+int sample_tokens_impl(const char* who, const void* logits, int dtype, int64_t row_stride, int rows, int vocab,
+                       const int32_t* row_index, const int32_t* forced, const uint32_t* noise,
+                       int noise_stride, int noise_col, uint64_t seed, uint64_t step,
+                       const int32_t* seq_ids, int draw, float temperature, int greedy, int top_k,
+                       uint32_t top_p_fixed, int32_t* out_tokens, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  FG_REQUIRE(logits && out_tokens, std::string(who) + ": null pointer");
+  FG_REQUIRE(rows > 0 && vocab > 0 && vocab < (1 << 23), std::string(who) + ": vocab must be in [1, 2^23)");
+  FG_REQUIRE(dtype == fg::kF32 || dtype == fg::kBF16, std::string(who) + ": dtype");
   FG_REQUIRE(row_stride >= vocab && row_stride % 8 == 0 && ((uintptr_t)logits & 31) == 0,
-             "fg_sample_tokens: rows must be 32-byte aligned (row_stride % 8 == 0)");
+             std::string(who) + ": rows must be 32-byte aligned (row_stride % 8 == 0)");
   SampleParams sp = make_params(temperature, greedy, top_k, vocab, top_p_fixed);
   hipStream_t s = (hipStream_t)stream;
   SplitArgs a;
@@ -1012,7 +1041,7 @@ int fg_sample_tokens(const void* logits, int dtype, int64_t row_stride, int rows
       hipLaunchKernelGGL(split_sample_kernel<fg::kF32>, dim3(rows), dim3(kThreads), 0, s, a, noise, noise_stride,
                          noise_col, seed, step, seq_ids, draw, out_tokens);
     }
-    return fg::check_launch("fg_sample_tokens");
+    return fg::check_launch(who);
   }
   if (!sp.greedy && sp.top_k == 0 && sp.tp32 != 0 &&
       split_setup(a, workspace, workspace_bytes, rows, logits, row_stride, vocab, temperature, 0)) {
@@ -1028,7 +1057,7 @@ int fg_sample_tokens(const void* logits, int dtype, int64_t row_stride, int rows
       hipLaunchKernelGGL(split_topp_sample_kernel<fg::kF32>, dim3(rows), dim3(kThreads), 0, s, a, noise,
                          noise_stride, noise_col, seed, step, seq_ids, draw, out_tokens);
     }
-    return fg::check_launch("fg_sample_tokens");
+    return fg::check_launch(who);
   }
   if (dtype == fg::kBF16)
     hipLaunchKernelGGL(sample_rows_kernel<fg::kBF16>, dim3(rows), dim3(kThreads), 0, s, logits, row_stride, vocab,
@@ -1036,7 +1065,40 @@ int fg_sample_tokens(const void* logits, int dtype, int64_t row_stride, int rows
   else
     hipLaunchKernelGGL(sample_rows_kernel<fg::kF32>, dim3(rows), dim3(kThreads), 0, s, logits, row_stride, vocab,
                        row_index, forced, noise, noise_stride, noise_col, seed, step, seq_ids, draw, sp, out_tokens);
-  return fg::check_launch("fg_sample_tokens");
+  return fg::check_launch(who);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t fg_sample_workspace(int rows) { return rows > 0 ? split_workspace_bytes(rows) : 0; }
+
+int fg_sample_tokens(const void* logits, int dtype, int64_t row_stride, int rows, int vocab,
+                     const int32_t* row_index, const int32_t* forced, const uint32_t* noise, int noise_stride,
+                     int noise_col, uint64_t seed, uint64_t step, const int32_t* seq_ids, int draw,
+                     float temperature, int greedy, int top_k, uint32_t top_p_fixed, int32_t* out_tokens,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+  return sample_tokens_impl("fg_sample_tokens", logits, dtype, row_stride, rows, vocab, row_index, forced, noise,
+                            noise_stride, noise_col, seed, step, seq_ids, draw, temperature, greedy, top_k,
+                            top_p_fixed, out_tokens, workspace, workspace_bytes, stream);
+}
+
+size_t fg_sample_tokens_noalloc_max_rows(void) { return kNoAllocMaxRows; }
+
+int fg_sample_tokens_noalloc(const void* logits, int dtype, int64_t row_stride, int rows, int vocab,
+                             const int32_t* row_index, const int32_t* forced, const uint32_t* noise,
+                             int noise_stride, int noise_col, uint64_t seed, uint64_t step, const int32_t* seq_ids,
+                             int draw, float temperature, int greedy, int top_k, uint32_t top_p_fixed,
+                             int32_t* out_tokens, void* stream) {
+  FG_REQUIRE(rows > 0 && rows <= kNoAllocMaxRows,
+             "fg_sample_tokens_noalloc: rows must be in [1, " + std::to_string(kNoAllocMaxRows) + "] (got " +
+                 std::to_string(rows) + ")");
+  void* ws = nullptr;
+  if (int rc = scratch_for_current_device(&ws)) return rc;
+  return sample_tokens_impl("fg_sample_tokens_noalloc", logits, dtype, row_stride, rows, vocab, row_index, forced,
+                            noise, noise_stride, noise_col, seed, step, seq_ids, draw, temperature, greedy, top_k,
+                            top_p_fixed, out_tokens, ws, kScratchBytes, stream);
 }
 
 int fg_accept_walk(const void* tree_logits, int dtype, int64_t row_stride, int vocab, const int32_t* slot_map,

@@ -42,6 +42,9 @@ SIGNATURES = {
     "fg_sample_workspace": (_SZ, [_I]),
     "fg_sample_tokens": (_I, [_P, _I, _I64, _I, _I, _P, _P, _P, _I, _I, _U64, _U64, _P, _I, _F, _I, _I, _U32, _P,
                               _P, _SZ, _P]),
+    "fg_sample_tokens_noalloc_max_rows": (_SZ, []),
+    "fg_sample_tokens_noalloc": (_I, [_P, _I, _I64, _I, _I, _P, _P, _P, _I, _I, _U64, _U64, _P, _I, _F, _I, _I, _U32,
+                                      _P, _P]),
     "fg_accept_walk": (_I, [_P, _I, _I64, _I, _P, _P, _P, _P, _I, _I, _I, _P, _I, _I, _U64, _U64, _P, _I, _F, _I, _I,
                             _U32, _P, _P, _I, _P, _P, _P, _P, _P, _P]),
     "fg_walk_begin": (_I, [_P, _P, _P, _I, _I, _P, _P, _I, _P, _P, _P, _P, _P]),
