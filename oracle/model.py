@@ -132,14 +132,16 @@ def medusa_project(hidden, head, dtype=F64):
 
 
 def medusa_logits(hidden, heads, lm_head, max_heads=None, dtype=F64):
-    """Per-head logits through the tied LM head.
+    """Per-head logits: through the head's own output projection when it has one
+    (``head["out_w"]``, an untied head), else through the tied LM head.
 
-    Follows ``flashgrpo/decoding/flash_medusa_decoder.py:254-294`` (one shared
-    vocabulary projection of the concatenated head outputs).
+    Follows ``flashgrpo/decoding/flash_medusa_decoder.py:254-304`` and
+    ``flashgrpo/models/medusa_heads.py:266-276``.
     """
     n = len(heads) if max_heads is None else min(max_heads, len(heads))
     W = np.asarray(lm_head, dtype)
-    return [medusa_project(hidden, heads[i], dtype) @ W.T for i in range(n)]
+    return [medusa_project(hidden, heads[i], dtype) @
+            (W if heads[i].get("out_w") is None else np.asarray(heads[i]["out_w"], dtype)).T for i in range(n)]
 
 
 def random_chain_cell(hidden: int, seed: int, std: float = 0.02, bottleneck_ratio: int = 8, gate_init: float = -3.0,

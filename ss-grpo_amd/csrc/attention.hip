@@ -135,8 +135,10 @@ __global__ void __launch_bounds__(W * 64, 2) tree_attn_bf16_kernel(AttnArgs a, i
   const int G = a.Hq / a.Hkv;
   const int M = G * a.N;
   const int s0 = a.seq_len[b];
-  const int total = s0 + a.N;
-  const int nkeys = min(total, a.capacity);
+  // Keys past the cache's capacity were never written (fg_rope_kv_write flags them):
+  // they are not attended, as in the fp32 kernel.
+  const int total = min(s0 + a.N, a.capacity);
+  const int nkeys = total;
   const int cb = a.row_map ? a.row_map[b] : b;
   const uint16_t* kbase = (const uint16_t*)a.k + (int64_t)cb * a.cache_batch + (int64_t)hkv * a.cache_head;
   const uint16_t* vbase = (const uint16_t*)a.v + (int64_t)cb * a.cache_batch + (int64_t)hkv * a.cache_head;

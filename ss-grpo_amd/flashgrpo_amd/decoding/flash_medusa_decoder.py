@@ -82,6 +82,51 @@ class FlashMedusaConfig:
     project_internal_tree_logits_only: bool = True
     inplace_kv_compaction: bool = True
     reflex_enabled: bool = False
+    # Reflex fast-state settings (flash_medusa_decoder.py:74-116). Accepted so that the
+    # trainer's config builder (flashgrpo_trainer.py:555-633) constructs this class
+    # unchanged; reflex proposals themselves are not built (reflex_enabled=True raises).
+    reflex_state_space: str = "projected"
+    reflex_fast_state_dim: int = 128
+    reflex_beta: float = 0.95
+    reflex_eta: float = 0.1
+    reflex_top_m_feedback: int = 64
+    reflex_feedback_stride: int = 1
+    reflex_feedback_stride_min: int = 1
+    reflex_target_topk: int = 32
+    reflex_feedback_union_cap: int = 96
+    reflex_tv_gate_low: float = 0.05
+    reflex_tv_gate_high: float = 0.20
+    reflex_horizon_weight_decay: float = 0.85
+    reflex_half_life_tokens: float = 48.0
+    reflex_feedback_variance_beta: float = 0.99
+    reflex_feedback_rms_clip: float = 3.0
+    reflex_state_rms_clip: float = 2.0
+    reflex_numerical_reset_rms: float = 2.5
+    reflex_relative_rms_delta_base: float = 0.01
+    reflex_warmup_effective_updates: float = 16.0
+    reflex_magnitude_gate_floor: float = 0.25
+    reflex_guard_calibration_rollouts: int = 20
+    reflex_guard_aal_drop_fraction: float = 0.05
+    reflex_guard_patience: int = 2
+    reflex_guard_disable_rollouts: int = 50
+    reflex_feedback_clip_norm: float = 2.0
+    reflex_hidden_feedback_clip_norm: float = 0.0
+    reflex_fast_state_clip_norm: float = 8.0
+    reflex_correction_clip_norm: float = 1.0
+    reflex_normalize_correction: bool = True
+    reflex_feedback_ce_gate: bool = True
+    reflex_feedback_ce_tau: float = 4.0
+    reflex_feedback_ce_threshold: float = 0.4
+    reflex_normalize_feedback: bool = True
+    reflex_feedback_enabled: bool = False
+    reflex_proposal_injection_enabled: bool = False
+    reflex_proposal_injection_scale: float = 0.0
+    reflex_proposal_injection_after: int = 0
+    reflex_proposal_injection_warmup: int = 0
+    reflex_aux_cache_enabled: bool = False
+    reflex_aux_cache_max_records: int = 8192
+    reflex_aux_cache_stride: int = 1
+    reflex_aux_store_fast_state: bool = False
     # build additions
     emit_correction_token: bool = False  # flashgrpo_b200 acceptance semantics
     noise_seed: int | None = None        # None: drawn from torch's default generator per generate()
@@ -123,10 +168,17 @@ class FlashMedusaDecoder:
         if config.reflex_enabled:
             raise NotImplementedError("reflex fast-state proposals are not built in flashgrpo_amd")
         self.target_model = target_model
+        # A Hugging Face target is converted once here and re-read in place at the
+        # start of every rollout whose parameters changed since (start()).
         self.model = target_model if isinstance(target_model, TargetModel) else TargetModel.from_hf(target_model)
         self.medusa_heads = medusa_heads
         self.tokenizer = tokenizer
         self.config = config
+        for i, hd in enumerate(getattr(medusa_heads, "heads", [])):
+            out = getattr(hd, "output", None)
+            if out is not None and tuple(out.weight.shape) != (self.model.cfg.vocab, self.model.cfg.hidden):
+                raise ValueError(f"untied Medusa head {i}: output {tuple(out.weight.shape)} does not match the "
+                                 f"target's (vocab, hidden) = ({self.model.cfg.vocab}, {self.model.cfg.hidden})")
 
     # ------------------------------------------------------------------ helpers
     def _token_ids(self):
@@ -299,6 +351,20 @@ class FlashMedusaDecoder:
                     conf=torch.stack(confs_dev).float() if confs_dev else None)
         return torch.cat(cols, dim=1).contiguous(), chain_plan, info
 
+    def _medusa_logits(self, proj: torch.Tensor, heads: int, batch: int) -> torch.Tensor:
+        """[heads*B, V] proposal logits (``flash_medusa_decoder.py:281-304``): one LM-head
+        GEMM over every head's rows when all heads are tied, otherwise each head's rows
+        through its own ``output`` projection (an untied head) or the LM head."""
+        model = self.model
+        own = self.medusa_heads.output_weights(model.dtype, model.device)[:heads]
+        if all(w is None for w in own):
+            return model.logits(proj)
+        out = torch.empty((heads * batch, model.cfg.vocab), dtype=model.dtype, device=model.device)
+        for h, w in enumerate(own):
+            rows = slice(h * batch, (h + 1) * batch)
+            model.logits(proj[rows], out=out[rows], weight=w)
+        return out
+
     # ------------------------------------------------------------------ rollout
     @torch.no_grad()
     def start(self, input_ids: torch.Tensor, attention_mask: torch.Tensor, *, repeated_generate_nums=None,
@@ -307,6 +373,7 @@ class FlashMedusaDecoder:
         groups and return the rollout state before the first verify round."""
         cfg = self.config
         model = self.model
+        model.sync_from_hf()  # the policy may have stepped since the last rollout
         dev = model.device
         V = model.cfg.vocab
         repeats = max(1, int(repeated_generate_nums or 1))
@@ -396,7 +463,7 @@ class FlashMedusaDecoder:
             t0 = time.time()
             proj = self.medusa_heads.project_all(r.hidden, plan.active_heads)
             with timing.label("medusa"):
-                mlog = model.logits(proj)
+                mlog = self._medusa_logits(proj, plan.active_heads, Bc)
             if plan.layout == "sparse_asymmetric":
                 # candidate lists of the sparse widths (adaptation only shrinks them)
                 kc = max(sparse_widths(list(plan.nodes_by_head or plan.topk_by_depth)[:3], mlog.shape[-1]))

@@ -149,16 +149,33 @@ class MedusaHeads(nn.Module):
         return K.medusa_heads(hidden.contiguous(), fw["ln_w"][:n], fw["ln_b"][:n], fw["fc_w"][:n], fw["fc_b"][:n],
                               eps=fw["eps"], out=out, workspace=workspace)
 
+    def output_weights(self, dtype, device) -> list:
+        """Per head: its own output projection [V, H] (an untied head, cast once to
+        ``dtype`` and cached until the parameter changes) or None (tied to the LM head)."""
+        outs = [hd.output.weight if hd.output is not None else None for hd in self.heads]
+        key = (dtype, str(device), tuple(None if w is None else (w._version, w.data_ptr()) for w in outs))
+        if getattr(self, "_out_key", None) != key:
+            with torch.no_grad():
+                self._out = [None if w is None else w.detach().to(device=device, dtype=dtype).contiguous()
+                             for w in outs]
+            self._out_key = key
+        return self._out
+
     def logits_for_last_hidden(self, last_hidden, lm_head_weight, *, max_heads=None):
-        """Per-head logits [B, V] through the tied LM head (``medusa_heads.py:241-277``)."""
+        """Per-head logits [B, V]: an untied head through its own ``output``, the others
+        through the LM head (``medusa_heads.py:241-277``)."""
         if last_hidden.dim() == 3:
             last_hidden = last_hidden[:, -1, :]
         B = last_hidden.shape[0]
         proj = self.project_all(last_hidden, max_heads)
         if proj.numel() == 0:
             return []
-        logits = F.linear(proj, lm_head_weight.to(proj.dtype))
-        return list(logits.split(B, dim=0))
+        own = self.output_weights(proj.dtype, proj.device)
+        n = proj.shape[0] // B
+        if all(w is None for w in own[:n]):
+            return list(F.linear(proj, lm_head_weight.to(proj.dtype)).split(B, dim=0))
+        return [F.linear(proj[h * B:(h + 1) * B], (lm_head_weight if own[h] is None else own[h]).to(proj.dtype))
+                for h in range(n)]
 
     def chain_next_state(self, state, token_ids, embedding_weight):
         """Next chain state from the parent state and the path token's embedding
@@ -185,21 +202,37 @@ class MedusaHeads(nn.Module):
         torch.save(self.state_dict(), d / "medusa_heads.pt")
 
     @classmethod
-    def from_pretrained(cls, load_directory, *, map_location="cpu", dtype=None, lm_head=None, **overrides):
-        """Shape-filtered load, as ``medusa_heads.py:442-480`` (weights-only unpickling)."""
+    def from_pretrained(cls, load_directory, *, map_location="cpu", dtype=None, lm_head=None,
+                        chain_bottleneck_ratio=None, chain_gate_init=None, reflex_fast_state_dim=None,
+                        reflex_init_scale=None, device=None):
+        """Shape-filtered load of a directory written by ``save_pretrained``, as
+        ``medusa_heads.py:442-480``: ``medusa_config.json`` gives the architecture (the
+        keyword arguments that are not None win), ``medusa_heads.pt`` is read with
+        weights-only unpickling and every tensor whose name and shape match is loaded;
+        the others keep their initial values (``_loaded_state_keys`` /
+        ``_loaded_compatible_keys`` record what the file held and what was taken).
+        ``device`` (not in the reference) moves the module after loading."""
         d = Path(load_directory)
         cfg = json.loads((d / "medusa_config.json").read_text(encoding="utf-8"))
-        kw = dict(dtype=dtype, tie_lm_head=cfg.get("tie_lm_head", True), lm_head=lm_head,
-                  medusa_loss_decay=cfg.get("medusa_loss_decay", 0.8),
-                  chain_bottleneck_ratio=overrides.get("chain_bottleneck_ratio") or cfg.get("chain_bottleneck_ratio", 8),
-                  chain_gate_init=overrides.get("chain_gate_init", cfg.get("chain_gate_init", -3.0)))
-        model = cls(cfg["hidden_size"], cfg["vocab_size"], cfg["num_heads"], **kw)
+
+        def pick(arg, key, default):
+            return arg if arg is not None else cfg.get(key, default)
+
+        model = cls(cfg["hidden_size"], cfg["vocab_size"], cfg["num_heads"], dtype=dtype,
+                    tie_lm_head=cfg.get("tie_lm_head", True), lm_head=lm_head,
+                    medusa_loss_decay=cfg.get("medusa_loss_decay", 0.8),
+                    chain_bottleneck_ratio=pick(chain_bottleneck_ratio, "chain_bottleneck_ratio", 8),
+                    chain_gate_init=pick(chain_gate_init, "chain_gate_init", -3.0),
+                    reflex_fast_state_dim=pick(reflex_fast_state_dim, "reflex_fast_state_dim", 0),
+                    reflex_init_scale=pick(reflex_init_scale, "reflex_init_scale", 0.0))
         state = torch.load(d / "medusa_heads.pt", map_location=map_location, weights_only=True)
         current = model.state_dict()
         compatible = {k: v for k, v in state.items() if k in current and tuple(current[k].shape) == tuple(v.shape)}
         model.load_state_dict(compatible, strict=False)
         model._loaded_state_keys = set(state.keys())
         model._loaded_compatible_keys = set(compatible.keys())
+        if device is not None:
+            model = model.to(device)
         return model
 
     @classmethod

@@ -132,6 +132,132 @@ class KVCache:
         self.seq_len.index_copy_(0, dst_rows.long(), self.seq_len.index_select(0, src_rows.long()))
 
 
+# ------------------------------------------------------------------ Hugging Face weights
+def unwrap_causal_lm(causal_lm):
+    """The causal LM under a PEFT wrapper (``qwen_flashgrpo_wrapper.py:7-12``)."""
+    if hasattr(causal_lm, "get_base_model"):
+        return causal_lm.get_base_model()
+    if hasattr(causal_lm, "base_model") and hasattr(causal_lm.base_model, "model"):
+        return causal_lm.base_model.model
+    return causal_lm
+
+
+def hf_target_config(c) -> TargetConfig:
+    """TargetConfig of a transformers Qwen2/Llama config."""
+    rope = getattr(c, "rope_theta", None) or (getattr(c, "rope_parameters", None) or {}).get("rope_theta", 1e4)
+    return TargetConfig(
+        num_layers=c.num_hidden_layers, hidden=c.hidden_size, q_heads=c.num_attention_heads,
+        kv_heads=getattr(c, "num_key_value_heads", None) or c.num_attention_heads,
+        head_dim=getattr(c, "head_dim", None) or c.hidden_size // c.num_attention_heads,
+        intermediate=c.intermediate_size, vocab=c.vocab_size, rope_theta=float(rope), rms_eps=float(c.rms_norm_eps),
+        qkv_bias=bool(getattr(c, "attention_bias", False) or c.model_type == "qwen2"),
+        tie_word_embeddings=bool(getattr(c, "tie_word_embeddings", False)), name=c.model_type)
+
+
+def hf_parameter_key(model) -> tuple:
+    """(address, version counter) of every parameter: changes when an optimizer step,
+    an in-place edit or a reassignment touches any of them (adapters included)."""
+    return tuple((p.data_ptr(), p._version) for p in model.parameters())
+
+
+def _active_adapters(mod) -> list:
+    act = getattr(mod, "active_adapters", None)
+    if act is None:
+        act = getattr(mod, "active_adapter", [])
+    return [act] if isinstance(act, str) else list(act)
+
+
+def hf_linear_weight(mod):
+    """(weight, bias) a linear module applies, in float32 when an adapter delta is
+    merged. A LoRA-wrapped linear (PEFT layout: ``base_layer``, ``lora_A``/``lora_B``
+    module dicts, ``scaling``) adds ``scaling[a] * lora_B[a].weight @ lora_A[a].weight``
+    (and ``scaling[a] * lora_B[a].bias`` when the adapter has one) for every active
+    adapter unless the adapters are merged into the base weight or disabled."""
+    base = getattr(mod, "base_layer", None)
+    if base is None:
+        return mod.weight, getattr(mod, "bias", None)
+    while getattr(base, "base_layer", None) is not None:  # nested wrappers
+        base = base.base_layer
+    w, b = base.weight, getattr(base, "bias", None)
+    if getattr(mod, "merged", False) or getattr(mod, "disable_adapters", False):
+        return w, b
+    lora_a, lora_b = getattr(mod, "lora_A", {}), getattr(mod, "lora_B", {})
+    use_dora = getattr(mod, "use_dora", {}) or {}
+    out_w, out_b = None, None
+    for name in _active_adapters(mod):
+        if name not in lora_a:
+            continue
+        if use_dora.get(name, False):
+            raise NotImplementedError(f"DoRA adapter {name!r}: only plain LoRA deltas are merged")
+        if getattr(mod, "fan_in_fan_out", False):
+            raise NotImplementedError("fan_in_fan_out LoRA layers are not merged")
+        scale = float(mod.scaling[name])
+        A, B = lora_a[name].weight, lora_b[name].weight
+        if out_w is None:
+            out_w = w.detach().float().clone()
+        out_w += scale * (B.detach().float() @ A.detach().float())
+        bb = getattr(lora_b[name], "bias", None)
+        if bb is not None:
+            if out_b is None:
+                out_b = b.detach().float().clone() if b is not None else torch.zeros_like(bb.detach().float())
+            out_b += scale * bb.detach().float()
+    return (w if out_w is None else out_w), (b if out_b is None else out_b)
+
+
+def _plain_weight(mod, what):
+    if getattr(mod, "base_layer", None) is not None or hasattr(mod, "lora_embedding_A"):
+        raise NotImplementedError(f"{what}: adapters on this module are not merged")
+    return mod.weight
+
+
+def _read_hf_weights(base, cfg: TargetConfig, dev, dt, into: dict | None = None) -> dict:
+    """The native weight dict of a transformers causal LM, one layer at a time. With
+    ``into`` the tensors of an existing dict are overwritten in place (shapes must
+    match); otherwise fresh tensors are allocated (never aliases of the parameters)."""
+
+    def put(dst, src):
+        src = src.detach()
+        if dst is None:
+            return src.to(device=dev, dtype=dt, copy=True).contiguous()
+        dst.copy_(src.to(device=dev, dtype=dt))
+        return dst
+
+    def cat(dst, parts):
+        # merged adapter weights are float32: concatenate wide, round to dt once
+        wide = any(p.dtype != dt for p in parts)
+        t = torch.cat([p.detach().to(device=dev, dtype=torch.float32 if wide else dt) for p in parts]).to(dt)
+        if dst is None:
+            return t.contiguous()
+        dst.copy_(t)
+        return dst
+
+    body = base.model
+    w = into if into is not None else {"layers": [None] * cfg.num_layers}
+    w["embed"] = put(w.get("embed"), _plain_weight(body.embed_tokens, "embed_tokens"))
+    w["final_norm"] = put(w.get("final_norm"), body.norm.weight)
+    for i, layer in enumerate(body.layers):
+        at, mlp = layer.self_attn, layer.mlp
+        lw = w["layers"][i] or {}
+        q, k, v = (hf_linear_weight(m) for m in (at.q_proj, at.k_proj, at.v_proj))
+        lw["qkv_w"] = cat(lw.get("qkv_w"), [q[0], k[0], v[0]])
+        lw["qkv_b"] = cat(lw.get("qkv_b"), [q[1], k[1], v[1]]) if q[1] is not None else None
+        lw["o_w"] = put(lw.get("o_w"), hf_linear_weight(at.o_proj)[0])
+        lw["gate_up_w"] = cat(lw.get("gate_up_w"), [hf_linear_weight(mlp.gate_proj)[0],
+                                                    hf_linear_weight(mlp.up_proj)[0]])
+        lw["down_w"] = put(lw.get("down_w"), hf_linear_weight(mlp.down_proj)[0])
+        lw["input_norm"] = put(lw.get("input_norm"), layer.input_layernorm.weight)
+        lw["post_norm"] = put(lw.get("post_norm"), layer.post_attention_layernorm.weight)
+        w["layers"][i] = lw
+    head = getattr(base, "lm_head", None)
+    tied = head is None or head.weight.data_ptr() == body.embed_tokens.weight.data_ptr()
+    if tied:
+        w["lm_head"] = w["embed"]
+    else:
+        cur = w.get("lm_head")
+        w["lm_head"] = put(None if cur is w["embed"] else cur, _plain_weight(head, "lm_head"))
+    return w
+
+
 _HIP = None
 
 
@@ -216,6 +342,8 @@ class TargetModel:
         self._graph_seen = {}   # graph key -> eager calls so far
         self._graph_pool = None
         self._retired = []      # buffers replaced while graphs that address them exist
+        self._hf_source = None  # the Hugging Face model the weights were read from (from_hf)
+        self._hf_key = None
         if self.device.type == "cuda":
             use_tuned_gemms()
 
@@ -275,52 +403,43 @@ class TargetModel:
 
     @classmethod
     def from_hf(cls, hf_model, *, dtype=None, device=None):
-        """Convert a transformers Qwen2/Llama causal LM (optionally PEFT-wrapped)."""
-        base = hf_model
-        if hasattr(base, "get_base_model"):
-            base = base.get_base_model()
-        c = base.config
-        cfg = TargetConfig(
-            num_layers=c.num_hidden_layers, hidden=c.hidden_size, q_heads=c.num_attention_heads,
-            kv_heads=getattr(c, "num_key_value_heads", c.num_attention_heads),
-            head_dim=getattr(c, "head_dim", None) or c.hidden_size // c.num_attention_heads,
-            intermediate=c.intermediate_size, vocab=c.vocab_size,
-            rope_theta=float(getattr(c, "rope_theta", None) or (getattr(c, "rope_parameters", None) or {}).get(
-                "rope_theta", 1e4)),
-            rms_eps=float(c.rms_norm_eps), qkv_bias=bool(getattr(c, "attention_bias", False) or
-                                                         c.model_type == "qwen2"),
-            tie_word_embeddings=bool(getattr(c, "tie_word_embeddings", False)), name=c.model_type)
-        sd = base.state_dict()
-        dev = device or next(base.parameters()).device
+        """Convert a transformers Qwen2/Llama causal LM, optionally PEFT-wrapped
+        (the reference trainer's LoRA target, ``flashgrpo_trainer.py:701-708``).
+
+        Every weight is copied (nothing aliases the live parameters) and each
+        projection is read through its module: a LoRA-wrapped linear contributes
+        ``base_layer.weight + scaling * lora_B @ lora_A`` for its active, unmerged
+        adapters. The model keeps a link to ``hf_model``; ``sync_from_hf`` re-reads
+        the weights in place when any parameter changed since the last read (an
+        optimizer step between rollouts).
+        """
+        base = unwrap_causal_lm(hf_model)
+        cfg = hf_target_config(base.config)
+        dev = torch.device(device) if device is not None else next(base.parameters()).device
         dt = dtype or next(base.parameters()).dtype
-
-        def g(k):
-            return sd[k].to(device=dev, dtype=dt).contiguous()
-
-        w = {"embed": g("model.embed_tokens.weight"), "final_norm": g("model.norm.weight"), "layers": []}
-        for i in range(cfg.num_layers):
-            p = f"model.layers.{i}."
-            qkv_b = None
-            if p + "self_attn.q_proj.bias" in sd:
-                qkv_b = torch.cat([g(p + "self_attn.q_proj.bias"), g(p + "self_attn.k_proj.bias"),
-                                   g(p + "self_attn.v_proj.bias")])
-            w["layers"].append({
-                "input_norm": g(p + "input_layernorm.weight"),
-                "qkv_w": torch.cat([g(p + "self_attn.q_proj.weight"), g(p + "self_attn.k_proj.weight"),
-                                    g(p + "self_attn.v_proj.weight")]),
-                "qkv_b": qkv_b,
-                "o_w": g(p + "self_attn.o_proj.weight"),
-                "post_norm": g(p + "post_attention_layernorm.weight"),
-                "gate_up_w": torch.cat([g(p + "mlp.gate_proj.weight"), g(p + "mlp.up_proj.weight")]),
-                "down_w": g(p + "mlp.down_proj.weight"),
-            })
-        w["lm_head"] = g("lm_head.weight") if "lm_head.weight" in sd else w["embed"]
+        w = _read_hf_weights(base, cfg, dev, dt)
         cfg.qkv_bias = w["layers"][0]["qkv_b"] is not None
         m = cls(cfg, w, dtype=dt, device=dev)
-        rot = getattr(base.model, "rotary_emb", None)
+        rot = getattr(getattr(base, "model", base), "rotary_emb", None)
         if rot is not None and hasattr(rot, "inv_freq"):
-            m.inv_freq = rot.inv_freq.detach().to(device=dev, dtype=torch.float32)
+            m.inv_freq = rot.inv_freq.detach().to(device=dev, dtype=torch.float32).clone()
+        m._hf_source = hf_model
+        m._hf_key = hf_parameter_key(hf_model)
         return m
+
+    def sync_from_hf(self, *, force: bool = False) -> bool:
+        """Re-read the linked Hugging Face model's weights into this model's tensors
+        (in place, so their device addresses stay valid) when any of its parameters
+        changed since the last read. Returns True when weights were copied."""
+        src = getattr(self, "_hf_source", None)
+        if src is None:
+            return False
+        key = hf_parameter_key(src)
+        if not force and key == self._hf_key:
+            return False
+        _read_hf_weights(unwrap_causal_lm(src), self.cfg, self.device, self.dtype, into=self.w)
+        self._hf_key = key
+        return True
 
     @property
     def lm_head_weight(self) -> torch.Tensor:
@@ -423,10 +542,11 @@ class TargetModel:
         K.rmsnorm(x, self.w["final_norm"], cfg.rms_eps, delta=delta, out=out)
         return out.view(B, N, H)
 
-    def logits(self, hidden: torch.Tensor, *, row_index=None, row_active=None, out=None,
-               out_dtype=None) -> torch.Tensor:
+    def logits(self, hidden: torch.Tensor, *, row_index=None, row_active=None, out=None, out_dtype=None,
+               weight: torch.Tensor | None = None) -> torch.Tensor:
         """LM-head rows: hidden rows (optionally gathered by row_index); rows with
-        row_active == 0 may be left unwritten.
+        row_active == 0 may be left unwritten. ``weight`` [V, H] replaces the tied LM
+        head (an untied Medusa head's own output projection).
 
         Gathered or skippable rows (the lazy walk projection) run the fg_lm_head
         kernel, which reads only the listed rows and skips tiles with no active row.
@@ -434,14 +554,13 @@ class TargetModel:
         faster than fg_lm_head at every row count from 96 to 2304 on MI355X.
         """
         x = hidden.reshape(-1, self.cfg.hidden)
+        w = self.w["lm_head"] if weight is None else weight
         if (row_index is None and row_active is None and self.dtype == torch.bfloat16
                 and (out_dtype is None or out_dtype == self.dtype)):
-            w = self.w["lm_head"]
             if out is None:
                 return F.linear(x, w)
             return torch.matmul(x, w.t(), out=out)
-        return K.lm_head(x, self.w["lm_head"], row_index=row_index, row_active=row_active, out=out,
-                         out_dtype=out_dtype)
+        return K.lm_head(x, w, row_index=row_index, row_active=row_active, out=out, out_dtype=out_dtype)
 
     def prefill(self, input_ids: torch.Tensor, cache: KVCache, *, lengths=None, chunk: int = PREFILL_CHUNK,
                 row_map: torch.Tensor | None = None) -> torch.Tensor:
@@ -516,9 +635,28 @@ def forward_tree(causal_lm: TargetModel, ids: torch.Tensor, mask4d: torch.Tensor
         raise ValueError(f"forward_tree: mask4d {tuple(mask4d.shape)} does not match ids {tuple(ids.shape)}")
     if N > 64:
         raise ValueError("forward_tree: trees larger than 64 nodes are not supported")
+    if B != pkv.batch:
+        raise ValueError(f"forward_tree: {B} trees for a cache of {pkv.batch} rows")
     dev = causal_lm.device
+    seq = pkv.seq_len.to(mask4d.device, torch.int64)
+    # The prefix block (the reference's full_attention_mask, tree_attention.py:61-64) must
+    # show every node of row b the same set of exactly seq_len[b] slots: the cache row's
+    # committed tokens, which are what the native forward attends.
+    P = mask4d.shape[3] - N
+    vis = mask4d[:, 0, :, :P] > torch.finfo(mask4d.dtype).min / 2
+    if P and (not bool((vis == vis[:, :1]).all()) or not bool((vis[:, 0].sum(-1) == seq).all())):
+        raise ValueError("forward_tree: the mask's prefix block must let every node of row b see exactly the "
+                         "row's seq_len[b] committed cache tokens")
+    if P == 0 and bool((seq != 0).any()):
+        raise ValueError("forward_tree: the mask has no prefix block but the cache holds committed tokens")
+    if int(seq.max()) + N > pkv.capacity:
+        raise ValueError(f"forward_tree: {N} tree nodes after {int(seq.max())} committed tokens exceed the "
+                         f"cache capacity {pkv.capacity}")
     anc, offset = native_tree_inputs(mask4d, pos, pkv.seq_len)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
     hidden = causal_lm.forward(ids.to(device=dev, dtype=torch.int32), pkv, pos_offset=offset.to(dev),
-                               anc=anc.to(dev))
+                               anc=anc.to(dev), err_flag=err)
+    if int(err.item()):
+        raise RuntimeError(f"forward_tree: a cache write fell outside the cache (flag {int(err.item())})")
     logits = causal_lm.logits(hidden.reshape(B * N, -1)).view(B, N, -1) if compute_logits else None
     return {"hidden_states": hidden, "logits": logits, "past_key_values": pkv}

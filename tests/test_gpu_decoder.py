@@ -46,13 +46,18 @@ def build(ocfg, W, heads, dtype, cell=None):
     tcfg = TargetConfig(ocfg.num_layers, ocfg.hidden, ocfg.q_heads, ocfg.kv_heads, ocfg.head_dim, ocfg.intermediate,
                         ocfg.vocab, ocfg.rope_theta, ocfg.rms_eps, ocfg.qkv_bias, ocfg.tie_word_embeddings)
     model = TargetModel.from_numpy(tcfg, W, dtype=dtype, device=DEV)
-    mh = MedusaHeads(ocfg.hidden, ocfg.vocab, len(heads)).to(DEV)
+    untied = any(src.get("out_w") is not None for src in heads)
+    mh = MedusaHeads(ocfg.hidden, ocfg.vocab, len(heads), tie_lm_head=not untied).to(DEV)
     with torch.no_grad():
         for hd, src in zip(mh.heads, heads):
             hd.fc.weight.copy_(torch.from_numpy(src["fc_w"]))
             hd.fc.bias.copy_(torch.from_numpy(src["fc_b"]))
             hd.norm.weight.copy_(torch.from_numpy(src["ln_w"]))
             hd.norm.bias.copy_(torch.from_numpy(src["ln_b"]))
+            if src.get("out_w") is not None:
+                hd.output.weight.copy_(torch.from_numpy(src["out_w"]))
+            elif untied:
+                hd.output = None  # this head stays tied to the LM head
         if cell is not None:
             cc = mh.chain_cell
             for mod_p, key in ((cc.state_norm.weight, "sn_w"), (cc.state_norm.bias, "sn_b"),
@@ -71,7 +76,7 @@ def rounded(W, heads, dtype, cell=None):
     Wr = {k: r(v) for k, v in W.items() if k not in ("layers", "inv_freq")}
     Wr["inv_freq"] = W["inv_freq"]
     Wr["layers"] = [{k: r(v) for k, v in lw.items()} for lw in W["layers"]]
-    hr = [dict(h, fc_w=r(h["fc_w"]), fc_b=r(h["fc_b"])) for h in heads]
+    hr = [dict(h, fc_w=r(h["fc_w"]), fc_b=r(h["fc_b"]), out_w=r(h.get("out_w"))) for h in heads]
     # the device runs the chain cell in the target's dtype
     cr = None if cell is None else {k: (v if k == "gate" else r(v)) for k, v in cell.items()}
     return Wr, hr, cr
@@ -121,19 +126,37 @@ def check_chain(rec, spec, Wr, heads_r, cell_r, tol, Bc):
     return trees
 
 
-class OracleRow:
-    """Per-sequence float64 oracle cache, advanced by recomputing accepted tokens."""
+def cast_weights(W, heads, dt):
+    """Weights (and Medusa heads) converted once to the oracle's compute dtype, so the
+    oracle's per-call np.asarray(w, dtype) makes no copy."""
+    c = lambda a: None if a is None else np.ascontiguousarray(a, dt)
+    Wc = {k: c(v) for k, v in W.items() if k not in ("layers", "inv_freq")}
+    if W.get("lm_head") is W.get("embed"):
+        Wc["lm_head"] = Wc["embed"]
+    Wc["inv_freq"] = W["inv_freq"]
+    Wc["layers"] = [{k: c(v) for k, v in lw.items()} for lw in W["layers"]]
+    hc = [{k: c(v) for k, v in h.items()} for h in heads]
+    return Wc, hc
 
-    def __init__(self, ocfg, W, prompt):
-        self.cfg, self.W = ocfg, W
-        hid, self.k, self.v = OM.prefill(ocfg, W, np.asarray(prompt)[None])
+
+class OracleRow:
+    """Per-sequence oracle cache, advanced by recomputing accepted tokens (float64, or
+    float32 for the bf16 checks at full-vocabulary geometries)."""
+
+    def __init__(self, ocfg, W, prompt, dtype=np.float64, state=None):
+        self.cfg, self.W, self.dt = ocfg, W, dtype
+        if state is not None:  # (hidden [H], K list [1, Hkv, P, d], V list, length): a given prefix
+            self.hidden, self.k, self.v, self.len = state
+            return
+        hid, self.k, self.v = OM.prefill(ocfg, W, np.asarray(prompt)[None], dtype=dtype)
         self.hidden = hid[0, -1]
         self.len = len(prompt)
 
     def append(self, toks):
         n = len(toks)
         hid, nk, nv = OM.forward(self.cfg, self.W, np.asarray(toks)[None], (self.len + np.arange(n))[None], self.k,
-                                 self.v, np.ones((1, self.len), bool), np.tril(np.ones((n, n), bool))[None])
+                                 self.v, np.ones((1, self.len), bool), np.tril(np.ones((n, n), bool))[None],
+                                 dtype=self.dt)
         self.k = [np.concatenate([a, b], axis=2) for a, b in zip(self.k, nk)]
         self.v = [np.concatenate([a, b], axis=2) for a, b in zip(self.v, nv)]
         self.hidden = hid[0, -1]
@@ -149,15 +172,23 @@ class OracleRow:
                 a = parents[a]
         pos = self.len + np.asarray(depths) - 1
         hid, _, _ = OM.forward(self.cfg, self.W, np.asarray(toks)[None], pos[None], self.k, self.v,
-                               np.ones((1, self.len), bool), allowed)
+                               np.ones((1, self.len), bool), allowed, dtype=self.dt)
         return hid[0]
 
 
-def lockstep(trace, ocfg, Wr, heads_r, spec, prompts, dtype, seed, max_length, emit_correction=False, cell_r=None):
+def lockstep(trace, ocfg, Wr, heads_r, spec, prompts, dtype, seed, max_length, emit_correction=False, cell_r=None,
+             odt=np.float64, rows=None):
+    """Replays every traced round on the oracle. ``odt`` is the oracle's compute dtype
+    (float32 only for bf16 runs, whose tolerance is 2e-2); ``rows`` optionally gives
+    pre-built OracleRows (a prefix taken from the device's cache)."""
     tol = TOL[dtype]
-    rows = {}
-    for s in range(prompts.shape[0]):
-        rows[s] = OracleRow(ocfg, Wr, prompts[s])
+    Wr, heads_r = cast_weights(Wr, heads_r, odt)
+    lm = Wr["lm_head"]
+    if rows is None:
+        rows = {s: OracleRow(ocfg, Wr, prompts[s], odt) for s in range(prompts.shape[0])}
+    else:
+        for row in rows.values():
+            row.W, row.dt = Wr, odt
     kw = dict(do_sample=spec.do_sample and spec.temperature != 0, temperature=spec.temperature, top_p=spec.top_p,
               top_k=spec.top_k)
     stats = dict(rounds=0, deep=0, max_acc=1)
@@ -165,9 +196,10 @@ def lockstep(trace, ocfg, Wr, heads_r, spec, prompts, dtype, seed, max_length, e
     for rec in trace:
         rnd, active = rec["round"], rec["active"]
         Bc = len(active)
+        want_in = OM.logits(np.stack([rows[s].hidden for s in active]), lm, odt)
         for i, s in enumerate(active):
             assert rel(rec["hidden_in"][i], rows[s].hidden) < tol, (rnd, s)
-            assert rel(rec["logits_in"][i], OM.logits(rows[s].hidden, Wr["lm_head"])) < tol, (rnd, s)
+            assert rel(rec["logits_in"][i], want_in[i]) < tol, (rnd, s)
         want_roots = [pending[s] if s in pending else
                       OS.sample_row(rec["logits_in"][i], OS.counter_noise(seed, rnd, s, 0), **kw)
                       for i, s in enumerate(active)]
@@ -180,7 +212,7 @@ def lockstep(trace, ocfg, Wr, heads_r, spec, prompts, dtype, seed, max_length, e
             if "medusa_logits" in rec:
                 nh = plan.active_heads
                 ml = rec["medusa_logits"].reshape(nh, Bc, -1)
-                want_ml = OM.medusa_logits(rec["hidden_in"], heads_r, Wr["lm_head"], nh)
+                want_ml = OM.medusa_logits(rec["hidden_in"], heads_r, lm, nh, dtype=odt)
                 for d in range(nh):
                     assert rel(ml[d], want_ml[d]) < tol
                 if spec.adaptive_tree_enabled:
@@ -213,27 +245,32 @@ def lockstep(trace, ocfg, Wr, heads_r, spec, prompts, dtype, seed, max_length, e
                 assert rel(rec["tree_hidden"][i][:trees[i].node_count], want_h) < tol, (rnd, s)
             nz = [[OS.counter_noise(seed, rnd, s, 1 + t) for t in range(N)] for s in active]
         if "walk_logits" in rec:  # lazy: one projected row per walk step and sequence
-            slots = None
-            want_all = OM.logits(rec["tree_hidden"].reshape(Bc * N, -1), Wr["lm_head"]).reshape(Bc, N, -1)
-            walk_logits = want_all.copy()
-            for i in range(Bc):
-                for t in range(int(rec["walk_last"][i]) + 1):
-                    node = int(rec["acc_nodes"][i, t])
-                    assert rel(rec["walk_logits"][t, i], want_all[i, node]) < tol, (rnd, i, t)
-                    walk_logits[i, node] = rec["walk_logits"][t, i]
-            at, an, last, corr = OS.accept_walk(trees, walk_logits, nz, slots=slots, emit_correction=True, **kw)
+            # The walk samples only at the nodes the device projected; those rows are
+            # checked against the oracle and packed, every other node maps to a trailing
+            # zero row (a walk that left the device's path would read it and mismatch).
+            visited = [(i, t, int(rec["acc_nodes"][i, t])) for i in range(Bc)
+                       for t in range(int(rec["walk_last"][i]) + 1)]
+            if visited:
+                want_rows = OM.logits(np.stack([rec["tree_hidden"][i, n] for i, _, n in visited]), lm, odt)
+            packed = np.zeros((len(visited) + 1, rec["walk_logits"].shape[-1]), np.float64)
+            slots = [[-1] * N for _ in range(Bc)]
+            for j, (i, t, node) in enumerate(visited):
+                assert rel(rec["walk_logits"][t, i], want_rows[j]) < tol, (rnd, i, t)
+                packed[j] = rec["walk_logits"][t, i]
+                slots[i][node] = j
+            at, an, last, corr = OS.accept_walk(trees, packed, nz, slots=slots, emit_correction=True, **kw)
             for i in range(Bc):  # draws made: one per step until a mismatch or a leaf
                 assert int(rec["walk_last"][i]) + 1 == len(at[i]) - (corr[i] is None), (rnd, i)
                 assert rec["acc_nodes"][i, :len(an[i])].tolist() == an[i], (rnd, i)
         elif "tree_logits" in rec:
             if rec["slot_map"] is not None:  # packed internal-node rows
                 r_, n_, slots = OT.internal_slots(trees)
-                want_tl = OM.logits(rec["tree_hidden"][r_, n_], Wr["lm_head"])
+                want_tl = OM.logits(rec["tree_hidden"][r_, n_], lm, odt)
                 assert rec["slot_map"].tolist() == slots
                 walk_logits = rec["tree_logits"]
             else:  # every node projected, dense [B, N, V]
                 slots = None
-                want_tl = OM.logits(rec["tree_hidden"].reshape(Bc * N, -1), Wr["lm_head"])
+                want_tl = OM.logits(rec["tree_hidden"].reshape(Bc * N, -1), lm, odt)
                 walk_logits = rec["tree_logits"].reshape(Bc, N, -1)
             assert rel(rec["tree_logits"], want_tl) < tol
             at, an, last, corr = OS.accept_walk(trees, walk_logits, nz, slots=slots, emit_correction=True, **kw)
@@ -260,11 +297,14 @@ def lockstep(trace, ocfg, Wr, heads_r, spec, prompts, dtype, seed, max_length, e
 
 
 def _run(ocfg, spec, *, dtype, B0, repeats, P, max_length, seed=123, wseed=0, cache_mode="extract_path",
-         internal_only=True, lazy=True):
+         internal_only=True, lazy=True, untied=(), std=0.05, odt=np.float64):
     from flashgrpo_amd.decoding import FlashMedusaConfig, FlashMedusaDecoder
 
-    W = OM.random_weights(ocfg, seed=wseed, std=0.05)
-    heads = OM.random_medusa(ocfg.hidden, spec.num_medusa_heads, seed=wseed + 1, std=0.05)
+    W = OM.random_weights(ocfg, seed=wseed, std=std)
+    heads = OM.random_medusa(ocfg.hidden, spec.num_medusa_heads, seed=wseed + 1, std=std)
+    orng = np.random.default_rng(wseed + 3)
+    for i in untied:  # these heads get their own output projection
+        heads[i]["out_w"] = (orng.standard_normal((ocfg.vocab, ocfg.hidden)) * 0.05).astype(np.float32)
     cell = OM.random_chain_cell(ocfg.hidden, seed=wseed + 2, std=0.05, gate_init=-1.0) \
         if spec.proposal_mode == "chain" else None
     model, mh = build(ocfg, W, heads, dtype, cell)
@@ -296,7 +336,7 @@ def _run(ocfg, spec, *, dtype, B0, repeats, P, max_length, seed=123, wseed=0, ca
     Wr, hr, cr = rounded(W, heads, dtype, cell)
     seed_eff = trace[0]["seed"]
     stats = lockstep(trace, ocfg, Wr, hr, spec, np.repeat(prompts, repeats, axis=0), dtype, seed_eff, max_length,
-                     emit_correction=spec.emit_correction_token, cell_r=cr)
+                     emit_correction=spec.emit_correction_token, cell_r=cr, odt=odt)
     for s, g in enumerate(out["generated_token_ids"]):
         assert len(g) >= 1
     return out, stats
@@ -476,3 +516,81 @@ def test_graph_replayed_rollouts_equal_eager_rollouts():
     assert outs[True] == outs[False]
     lens = [len(g) for g in outs[True][0]]
     assert len(set(lens)) > 1 or 7 in sum(outs[True][0], [])  # rows finish apart (EOS) or at max_length
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_lockstep_untied_medusa_heads(dtype):
+    """Heads 0 and 2 untied (their own output projection), head 1 tied: every head's
+    proposals, trees and the rollout against the oracle (medusa_heads.py:266-276,
+    flash_medusa_decoder.py:297-304)."""
+    spec = OD.DecodeSpec(tree_mode="fixed", max_tree_nodes_per_seq=16, fixed_tree_topk_by_depth=(4, 2, 1),
+                         num_medusa_heads=3, max_tree_depth=4, top_p=1.0)
+    cfg = SMALL if dtype == torch.float32 else SMALL16
+    out, st = _run(cfg, spec, dtype=dtype, B0=2, repeats=2, P=25, max_length=25 + 12, untied=(0, 2))
+    assert st["rounds"] == out["total_verify_rounds"] > 0
+
+
+def _hf_oracle_weights(hf):
+    """The oracle's weight dict (float32 numpy) of a transformers Qwen2 model."""
+    f = lambda t: t.detach().float().cpu().numpy().copy()
+    body = hf.model
+    W = {"embed": f(body.embed_tokens.weight), "final_norm": f(body.norm.weight), "lm_head": f(hf.lm_head.weight),
+         "inv_freq": f(body.rotary_emb.inv_freq), "layers": []}
+    for layer in body.layers:
+        at, mlp = layer.self_attn, layer.mlp
+        W["layers"].append({
+            "input_norm": f(layer.input_layernorm.weight), "post_norm": f(layer.post_attention_layernorm.weight),
+            "q_w": f(at.q_proj.weight), "k_w": f(at.k_proj.weight), "v_w": f(at.v_proj.weight),
+            "q_b": f(at.q_proj.bias), "k_b": f(at.k_proj.bias), "v_b": f(at.v_proj.bias), "o_w": f(at.o_proj.weight),
+            "gate_w": f(mlp.gate_proj.weight), "up_w": f(mlp.up_proj.weight), "down_w": f(mlp.down_proj.weight)})
+    return W
+
+
+def test_hf_target_resynced_between_rollouts():
+    """The reference trainer hands the decoder its live (Hugging Face) policy once and
+    steps the optimizer between rollouts (flashgrpo_trainer.py:835,1294). Two rollouts of
+    one decoder over a transformers Qwen2 model whose weights are edited in place in
+    between: each rollout matches the oracle built from the weights at that moment."""
+    transformers = pytest.importorskip("transformers")
+    from flashgrpo_amd.decoding import FlashMedusaConfig, FlashMedusaDecoder
+    from flashgrpo_amd.models import MedusaHeads
+
+    hc = transformers.Qwen2Config(vocab_size=64, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                                  num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=512,
+                                  rope_theta=1.0e6, rms_norm_eps=1e-6, tie_word_embeddings=False)
+    torch.manual_seed(0)
+    hf = transformers.Qwen2ForCausalLM(hc).to(DEV).float().eval()
+    with torch.no_grad():
+        for p in hf.parameters():
+            p.normal_(0.0, 0.05) if p.dim() > 1 else p.add_(torch.randn_like(p) * 0.05)
+    ocfg = OM.ModelConfig(num_layers=2, hidden=256, q_heads=4, kv_heads=2, head_dim=64, intermediate=512, vocab=64,
+                          rope_theta=1.0e6, rms_eps=1e-6)
+    heads = OM.random_medusa(256, 3, seed=5, std=0.05)
+    mh = MedusaHeads(256, 64, 3).to(DEV)
+    with torch.no_grad():
+        for hd, src in zip(mh.heads, heads):
+            hd.fc.weight.copy_(torch.from_numpy(src["fc_w"]))
+            hd.fc.bias.copy_(torch.from_numpy(src["fc_b"]))
+    spec = OD.DecodeSpec(tree_mode="fixed", max_tree_nodes_per_seq=16, fixed_tree_topk_by_depth=(4, 2, 1),
+                         num_medusa_heads=3, max_tree_depth=4, top_p=1.0)
+    cfg = FlashMedusaConfig(num_medusa_heads=3, tree_mode="fixed", max_tree_nodes_per_seq=16,
+                            fixed_tree_topk_by_depth=(4, 2, 1), max_tree_depth=4, top_p=1.0, noise_seed=3)
+    dec = FlashMedusaDecoder(hf, mh, Tok(-1), cfg)
+    prompts = np.random.default_rng(1).integers(0, 64, (2, 21))
+    outs = []
+    for rollout in range(2):
+        if rollout == 1:
+            with torch.no_grad():  # an optimizer-like in-place step on some parameters
+                hf.model.layers[0].self_attn.q_proj.weight.mul_(1.7)
+                hf.model.layers[1].mlp.up_proj.weight.add_(torch.randn_like(hf.model.layers[1].mlp.up_proj.weight)
+                                                           * 0.05)
+                hf.lm_head.weight.mul_(-1.0)
+        trace = []
+        out = dec.generate(torch.from_numpy(prompts), torch.ones(2, 21, dtype=torch.long), repeated_generate_nums=2,
+                           max_length=21 + 10, generation_step=rollout, trace=trace)
+        W = _hf_oracle_weights(hf)
+        st = lockstep(trace, ocfg, W, heads, spec, np.repeat(prompts, 2, axis=0), torch.float32, trace[0]["seed"],
+                      21 + 10)
+        assert st["rounds"] == out["total_verify_rounds"] > 0
+        outs.append(out["generated_token_ids"])
+    assert outs[0] != outs[1]  # the second rollout really sampled the new policy

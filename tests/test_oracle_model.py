@@ -115,6 +115,26 @@ def test_medusa_block_matches_torch_modules():
         assert np.allclose(M.medusa_project(h, hd), ref, rtol=0, atol=1e-12)
 
 
+def test_medusa_logits_untied_heads_use_their_own_output():
+    """Head 1 untied (its own nn.Linear output, medusa_heads.py:66-72,266-276), heads 0 and 2
+    through the tied LM head: each head's logits equal its torch projection."""
+    rng = np.random.default_rng(8)
+    H, V = 32, 41
+    heads = M.random_medusa(H, 3, seed=9, std=0.3)
+    heads[1]["out_w"] = rng.standard_normal((V, H)).astype(np.float32)
+    lm = rng.standard_normal((V, H)).astype(np.float32)
+    h = rng.standard_normal((4, H))
+    got = M.medusa_logits(h, heads, lm)
+    for i, hd in enumerate(heads):
+        out = torch.nn.Linear(H, V, bias=False).double()
+        with torch.no_grad():
+            out.weight.copy_(torch.from_numpy(np.asarray(hd.get("out_w", lm), np.float64)))
+            want = out(torch.from_numpy(M.medusa_project(h, hd))).numpy()
+        assert np.allclose(got[i], want, rtol=0, atol=1e-10), i
+    # the tied heads really differ from the untied one
+    assert not np.allclose(got[1], M.medusa_project(h, heads[1]) @ lm.T)
+
+
 def _torch_chain_cell(cell, H):
     """The cell's published structure from torch modules (double): LayerNorm ->
     Linear for state and token, SiLU, Linear with bias, sigmoid-gated residual."""
