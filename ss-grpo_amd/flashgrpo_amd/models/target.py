@@ -131,6 +131,26 @@ class KVCache:
         self.kv.index_copy_(2, dst_rows.long(), self.kv.index_select(2, src_rows.long()))
         self.seq_len.index_copy_(0, dst_rows.long(), self.seq_len.index_select(0, src_rows.long()))
 
+    def container_copy(self) -> "KVCache":
+        """A second cache object over the same storage with its own committed lengths
+        (the reference's clone_cache(clone_tensors=False)). Committed rows are shared
+        read-only; the slots past a row's committed length are shared scratch, so two
+        containers that append past the same length overwrite each other there."""
+        c = KVCache.__new__(KVCache)
+        c.__dict__.update(self.__dict__)
+        c.seq_len = self.seq_len.clone()
+        return c
+
+    def select_rows(self, rows: torch.Tensor, capacity: int | None = None) -> "KVCache":
+        """A new cache holding copies of the given rows (in that order)."""
+        rows = rows.to(device=self.device, dtype=torch.long)
+        cap = self.capacity if capacity is None else int(capacity)
+        out = KVCache(self.cfg, int(rows.numel()), cap, dtype=self.dtype, device=self.device)
+        keep = min(cap, self.capacity)
+        out.kv[..., :keep, :].copy_(self.kv.index_select(2, rows)[..., :keep, :])
+        out.seq_len.copy_(self.seq_len.index_select(0, rows).clamp_max(cap))
+        return out
+
 
 # ------------------------------------------------------------------ Hugging Face weights
 def unwrap_causal_lm(causal_lm):
@@ -417,7 +437,8 @@ class TargetModel:
         cfg = hf_target_config(base.config)
         dev = torch.device(device) if device is not None else next(base.parameters()).device
         dt = dtype or next(base.parameters()).dtype
-        w = _read_hf_weights(base, cfg, dev, dt)
+        with torch.no_grad():
+            w = _read_hf_weights(base, cfg, dev, dt)
         cfg.qkv_bias = w["layers"][0]["qkv_b"] is not None
         m = cls(cfg, w, dtype=dt, device=dev)
         rot = getattr(getattr(base, "model", base), "rotary_emb", None)
@@ -437,7 +458,10 @@ class TargetModel:
         key = hf_parameter_key(src)
         if not force and key == self._hf_key:
             return False
-        _read_hf_weights(unwrap_causal_lm(src), self.cfg, self.device, self.dtype, into=self.w)
+        # in-place copies are allowed here whether the weights were made inside or
+        # outside inference mode
+        with torch.inference_mode():
+            _read_hf_weights(unwrap_causal_lm(src), self.cfg, self.device, self.dtype, into=self.w)
         self._hf_key = key
         return True
 
@@ -563,7 +587,7 @@ class TargetModel:
         return K.lm_head(x, w, row_index=row_index, row_active=row_active, out=out, out_dtype=out_dtype)
 
     def prefill(self, input_ids: torch.Tensor, cache: KVCache, *, lengths=None, chunk: int = PREFILL_CHUNK,
-                row_map: torch.Tensor | None = None) -> torch.Tensor:
+                row_map: torch.Tensor | None = None, return_all: bool = False) -> torch.Tensor:
         """Causal prefill of left-aligned prompts in chains of ``chunk`` tokens (the
         attention runs without masks: each new token sees the prefix and the chunk's
         tokens before it).
@@ -571,7 +595,8 @@ class TargetModel:
         input_ids [B, P] (device or host) holds each row's valid tokens left-aligned
         (row b has ``lengths[b]`` of them, default P). Writes cache slots [0, len) of
         every row, sets ``cache.seq_len`` and returns the hidden state of each row's
-        last token [B, H].
+        last token [B, H] (``return_all``: of every position, [B, P, H], left-aligned;
+        positions past a row's length hold the hidden state of filler tokens).
         """
         B, P = input_ids.shape
         ids = input_ids.to(self.device, dtype=torch.int32)
@@ -581,12 +606,15 @@ class TargetModel:
         seq = torch.zeros(B, dtype=torch.int32, device=self.device)
         cache.seq_len.zero_()
         last = torch.empty(B, self.cfg.hidden, dtype=self.dtype, device=self.device)
+        every = torch.zeros(B, P, self.cfg.hidden, dtype=self.dtype, device=self.device) if return_all else None
         chunk = max(1, min(int(chunk), MAX_CHAIN_TOKENS))
         offs_full = torch.arange(chunk, dtype=torch.int32, device=self.device)
         for start in range(0, int(lens.max()), chunk):
             n = min(chunk, P - start)
             tok = ids[:, start:start + n].contiguous()
             hid = self.forward(tok, cache, pos_offset=offs_full[:n], anc=None, seq_len=seq, row_map=row_map)
+            if every is not None:
+                every[:, start:start + n].copy_(hid)
             adv = np.clip(lens - start, 0, n)
             ends = np.nonzero((lens > start) & (lens <= start + n))[0]
             if ends.size:
@@ -598,7 +626,7 @@ class TargetModel:
             cache.seq_len.copy_(seq)
         else:
             cache.seq_len.index_copy_(0, row_map.long(), seq)
-        return last
+        return every if return_all else last
 
 
 def native_tree_inputs(mask4d: torch.Tensor, pos: torch.Tensor, seq_len: torch.Tensor):
@@ -626,9 +654,12 @@ def forward_tree(causal_lm: TargetModel, ids: torch.Tensor, mask4d: torch.Tensor
     applied in registers by the tree-attention kernel; the prefix a node sees is the
     cache row's committed tokens ``[0, pkv.seq_len[b])`` (the valid prefix slots the
     reference's mask marks), and positions become offsets from ``pkv.seq_len``. Node
-    n's K/V land in slot ``seq_len[b] + n`` of the cache, past the committed tokens,
-    so the past is never modified and ``clone_past`` needs no copy. Returns
-    ``{"hidden_states": [B, N, H], "logits": [B, N, V] or None, "past_key_values": pkv}``.
+    n's K/V land in slot ``seq_len[b] + n``, past the committed tokens, so the past's
+    committed rows are never modified. ``clone_past`` (the reference's container copy,
+    ``clone_cache(clone_tensors=False)``) returns the tree in a second cache object over
+    the same storage with its own lengths, so extracting a path from it leaves ``pkv``'s
+    lengths as they were; otherwise ``pkv`` itself is returned. Returns
+    ``{"hidden_states": [B, N, H], "logits": [B, N, V] or None, "past_key_values": cache}``.
     """
     B, N = ids.shape
     if mask4d.dim() != 4 or mask4d.shape[0] != B or mask4d.shape[2] != N or mask4d.shape[3] < N:
@@ -653,10 +684,11 @@ def forward_tree(causal_lm: TargetModel, ids: torch.Tensor, mask4d: torch.Tensor
         raise ValueError(f"forward_tree: {N} tree nodes after {int(seq.max())} committed tokens exceed the "
                          f"cache capacity {pkv.capacity}")
     anc, offset = native_tree_inputs(mask4d, pos, pkv.seq_len)
+    tree_cache = pkv.container_copy() if clone_past else pkv
     err = torch.zeros(1, dtype=torch.int32, device=dev)
-    hidden = causal_lm.forward(ids.to(device=dev, dtype=torch.int32), pkv, pos_offset=offset.to(dev),
+    hidden = causal_lm.forward(ids.to(device=dev, dtype=torch.int32), tree_cache, pos_offset=offset.to(dev),
                                anc=anc.to(dev), err_flag=err)
     if int(err.item()):
         raise RuntimeError(f"forward_tree: a cache write fell outside the cache (flag {int(err.item())})")
     logits = causal_lm.logits(hidden.reshape(B * N, -1)).view(B, N, -1) if compute_logits else None
-    return {"hidden_states": hidden, "logits": logits, "past_key_values": pkv}
+    return {"hidden_states": hidden, "logits": logits, "past_key_values": tree_cache}

@@ -361,3 +361,22 @@ def test_forward_tree_rejects_mismatched_prefix_and_overflow():
                                                     dtype=torch.float32)
     with pytest.raises(ValueError, match="capacity"):
         forward_tree(model, ids, mask, cache, pos)
+
+
+def test_sync_works_for_weights_made_inside_or_outside_inference_mode():
+    """The trainer calls generate under torch.inference_mode: a conversion made there
+    (inference tensors) must still re-sync afterwards, and one made outside must sync
+    inside it."""
+    from flashgrpo_amd.models import TargetModel
+
+    hf = _hf_qwen2(seed=2)
+    with torch.inference_mode():
+        inside = TargetModel.from_hf(hf)
+    outside = TargetModel.from_hf(hf)
+    with torch.no_grad():
+        hf.model.layers[0].mlp.gate_proj.weight.mul_(0.5)
+    assert inside.sync_from_hf()
+    with torch.inference_mode():
+        assert outside.sync_from_hf()
+    for m in (inside, outside):
+        _check_against_modules(m, hf)

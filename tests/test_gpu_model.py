@@ -196,7 +196,9 @@ def test_forward_tree_reference_call_shape(dtype):
                                                           pad_token_id=0, dtype=m.dtype)
     out = forward_tree(m, ids, mask4d, cache, pos, clone_past=True, compute_logits=True)
     N = ids.shape[1]
-    assert out["past_key_values"] is cache and cache.seq_len.cpu().tolist() == lens.tolist()
+    tree_cache = out["past_key_values"]  # a container copy over the same storage (clone_past)
+    assert tree_cache is not cache and tree_cache.kv is cache.kv and tree_cache.seq_len is not cache.seq_len
+    assert cache.seq_len.cpu().tolist() == tree_cache.seq_len.cpu().tolist() == lens.tolist()
     anc = tree_ancestor_bits(trees, N).to(DEV)
     offset = (pos - cache.seq_len.long()[:, None]).to(torch.int32)
     direct = m.forward(ids.to(torch.int32), cache, pos_offset=offset, anc=anc)
