@@ -199,23 +199,138 @@ def planted_walk_gather(cfg, r, work, elem, reps=5):
                                "hbm_frac": round(g_bytes / g_us / 1e3 / HBM_PEAK_GBS, 4)}}
 
 
-def cpu_baseline(model, heads, r, work, seed, layers=2):
-    """Oracle (numpy fp32) verify round on the host: same shapes, decoder stack cut to
-    `layers` of L layers and its forward time scaled back to L layers."""
+class _PlantedAcceptance:
+    """Makes every walk accept a full-depth path, for timing rounds at full acceptance
+    (random-init weights accept no candidate). Inside the context, each logits row a walk
+    samples from gets +60 on the token of the first child of the node it belongs to (a
+    few small torch launches per walk step, counted in the rounds' time), through the
+    kernels module the decoder calls: fg_walk_step's step rows (lazy LM head) and
+    fg_accept_walk's packed internal-node rows."""
+
+    def __init__(self):
+        from flashgrpo_amd import kernels as K
+
+        self.K = K
+        self.walk_step, self.accept_walk = K.walk_step, K.accept_walk
+
+    def __enter__(self):
+        import torch
+
+        K, walk_step, accept_walk = self.K, self.walk_step, self.accept_walk
+
+        def first_child_tokens(tree_tokens, parents, nodes):
+            m = parents == nodes[:, None]
+            child = m.to(torch.int32).argmax(1)
+            return tree_tokens.gather(1, child[:, None].long()).squeeze(1).long(), m.any(1)
+
+        def planted_walk_step(walk, step_logits, tree_tokens, parents, n_nodes, **kw):
+            B = tree_tokens.shape[0]
+            cur, active = walk["state"][:B], walk["state"][B:2 * B] != 0
+            tok, has = first_child_tokens(tree_tokens, parents, cur)
+            rows = torch.arange(B, device=step_logits.device)
+            step_logits[rows, tok] += 60.0 * (has & active).to(step_logits.dtype)
+            return walk_step(walk, step_logits, tree_tokens, parents, n_nodes, **kw)
+
+        def planted_accept_walk(tree_logits, tree_tokens, parents, n_nodes, *, slot_map=None, **kw):
+            B, N = tree_tokens.shape
+            if slot_map is not None:
+                nodes = torch.arange(N, device=tree_tokens.device, dtype=parents.dtype)
+                for n in range(N):
+                    tok, has = first_child_tokens(tree_tokens, parents, nodes[n].expand(B))
+                    slot = slot_map[:, n].long()
+                    ok = has & (slot >= 0)
+                    tree_logits[slot.clamp_min(0)[ok], tok[ok]] += 60.0
+            return accept_walk(tree_logits, tree_tokens, parents, n_nodes, slot_map=slot_map, **kw)
+
+        K.walk_step, K.accept_walk = planted_walk_step, planted_accept_walk
+        return self
+
+    def __exit__(self, *exc):
+        self.K.walk_step, self.K.accept_walk = self.walk_step, self.accept_walk
+
+
+def planted_full_rounds(dec, r, steps, latency_rounds=8):
+    """tok/s and verify-step latency of rounds in which every sequence accepts the tree's
+    full depth, with the lazy walk LM head and with the packed internal-node LM head."""
     import numpy as np
     import torch
+
+    out = {}
+    lazy0 = dec.config.lazy_walk_lm_head
+    try:
+        with _PlantedAcceptance():
+            for lazy in (True, False):
+                dec.config.lazy_walk_lm_head = lazy
+                for _ in range(3):  # warm-up (graph capture of the unchanged forward shape)
+                    dec.step(r)
+                torch.cuda.synchronize()
+                toks, lens = 0, []
+                t0 = time.perf_counter()
+                for _ in range(steps):
+                    toks += dec.step(r)
+                    lens.append(r.last_round["acc_len"].mean())
+                torch.cuda.synchronize()
+                sec = time.perf_counter() - t0
+                r.event_log = []
+                for _ in range(latency_rounds):
+                    dec.step(r)
+                torch.cuda.synchronize()
+                ms = np.array([a.elapsed_time(b) for a, b in r.event_log])
+                r.event_log = None
+                out["lazy" if lazy else "packed"] = {
+                    "tok_s": round(toks / sec, 2), "ms_per_step": round(sec / steps * 1e3, 3),
+                    "accept_len_mean": round(float(np.mean(lens)), 3),
+                    "verify_step_ms": {"median": round(float(np.median(ms)), 3),
+                                       "p90": round(float(np.percentile(ms, 90)), 3)}}
+    finally:
+        dec.config.lazy_walk_lm_head = lazy0
+    return out
+
+
+def measured_rollout(dec, prompts, repeats, rounds):
+    """The reference's own rate (generated tokens over the whole generate() time,
+    prefill included, flashgrpo_trainer.py:1117) for one rollout of ``rounds`` decode
+    rounds, measured end to end."""
+    import torch
+
+    P = prompts.shape[1]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = dec.generate(prompts, torch.ones_like(prompts), repeated_generate_nums=repeats, max_length=P + rounds)
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t0
+    toks = sum(len(g) for g in out["generated_token_ids"])
+    return {"tok_s": round(toks / sec, 2), "seconds": round(sec, 3), "tokens": int(toks),
+            "verify_rounds": int(out["total_verify_rounds"]), "prefill_s": round(out["prefill_time_cost"], 3)}
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(model, heads, r, work, seed, rounds=1):
+    """The oracle (numpy, fp32, every layer of the model) running ``rounds`` verify rounds
+    of the same workload on the host, from the device's current rollout state (its KV
+    cache, hidden states and logits copied to host memory). Nothing is scaled: the
+    figure is the tokens those rounds emit over their wall time."""
+    import numpy as np
 
     from oracle import decode as OD
     from oracle import model as OM
 
     cfg = model.cfg
-    nl = min(layers, cfg.num_layers)
     f = lambda t: t.detach().float().cpu().numpy()
     qd, kd = cfg.q_heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
     W = {"embed": f(model.w["embed"]), "final_norm": f(model.w["final_norm"]), "layers": [],
          "inv_freq": model.inv_freq.cpu().numpy()}
-    W["lm_head"] = W["embed"] if cfg.tie_word_embeddings else f(model.w["lm_head"])
-    for lw in model.w["layers"][:nl]:
+    W["lm_head"] = W["embed"] if model.w["lm_head"] is model.w["embed"] else f(model.w["lm_head"])
+    for lw in model.w["layers"]:
         qkv = f(lw["qkv_w"])
         b = f(lw["qkv_b"]) if lw["qkv_b"] is not None else None
         gu = f(lw["gate_up_w"])
@@ -231,12 +346,13 @@ def cpu_baseline(model, heads, r, work, seed, layers=2):
     cell = {"sn_w": g(cc.state_norm.weight), "sn_b": g(cc.state_norm.bias), "tn_w": g(cc.token_norm.weight),
             "tn_b": g(cc.token_norm.bias), "sp_w": g(cc.state_proj.weight), "tp_w": g(cc.token_proj.weight),
             "op_w": g(cc.out_proj.weight), "op_b": g(cc.out_proj.bias), "gate": float(cc.gate.detach())}
-    ocfg = OM.ModelConfig(nl, cfg.hidden, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.intermediate, cfg.vocab,
-                          cfg.rope_theta, cfg.rms_eps, cfg.qkv_bias, cfg.tie_word_embeddings)
-    cap = int(r.seq_h.max()) + 72
+    ocfg = OM.ModelConfig(cfg.num_layers, cfg.hidden, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.intermediate,
+                          cfg.vocab, cfg.rope_theta, cfg.rms_eps, cfg.qkv_bias, cfg.tie_word_embeddings)
+    # room for `rounds` rounds of the widest tree after the longest committed row
+    cap = int(r.seq_h.max()) + rounds * (int(work["max_nodes"]) + 8) + 8
     rows = r.row_map.long()
-    st = OD.State([f(r.cache.kv[l, 0].index_select(0, rows)[:, :, :cap]) for l in range(nl)],
-                  [f(r.cache.kv[l, 1].index_select(0, rows)[:, :, :cap]) for l in range(nl)],
+    st = OD.State([f(r.cache.kv[l, 0].index_select(0, rows)[:, :, :cap]) for l in range(cfg.num_layers)],
+                  [f(r.cache.kv[l, 1].index_select(0, rows)[:, :, :cap]) for l in range(cfg.num_layers)],
                   r.seq_h.copy(), f(r.hidden), f(r.logits), rows.cpu().numpy(),
                   np.full(len(r.active), -1, np.int64))
     spec = OD.DecodeSpec(num_medusa_heads=work["heads"], tree_mode=work["tree_mode"], cpeak_nodes=work["cpeak"],
@@ -254,29 +370,19 @@ def cpu_baseline(model, heads, r, work, seed, layers=2):
         threads = max(blas) if blas else threads
     except Exception:
         pass
+    tokens = 0
     t0 = time.perf_counter()
-    out = OD.verify_round(ocfg, W, hd, st, spec, seed, 0, 10 ** 9, dtype=np.float32, cell=cell)
-    t_round = time.perf_counter() - t0
-    tree = out["trees"][0]
-    B, N = len(r.active), tree.node_count
-    allowed = np.zeros((B, N, N), bool)
-    for n in range(N):
-        for a in tree.ancestors_including_self(n):
-            allowed[:, n, a] = True
-    valid = np.arange(st.k[0].shape[2])[None, :] < st.seq_len[:, None]
-    toks = np.array([t.tokens for t in out["trees"]])
-    t1 = time.perf_counter()
-    OM.forward(ocfg, W, toks, st.seq_len[:, None] + np.asarray(tree.depths)[None] - 1, st.k, st.v, valid, allowed,
-               dtype=np.float32)
-    t_fwd = time.perf_counter() - t1
-    t_est = t_round + (cfg.num_layers / nl - 1.0) * t_fwd
-    tokens = sum(len(t) for t in out["acc_tokens"])
-    return {"value": round(tokens / t_est, 3), "unit": "tok/s", "cores": int(threads), "kind": "port",
-            "sample": (f"one verify round of the same workload (B={B}, N={N}, vocab {cfg.vocab}) through the numpy "
-                       f"oracle in fp32 with the decoder stack cut to {nl} of {cfg.num_layers} layers; measured "
-                       f"{t_round:.2f} s round + {t_fwd:.2f} s {nl}-layer forward, scaled to {cfg.num_layers} layers "
-                       f"= {t_est:.2f} s for {tokens} tokens"),
-            "seconds": round(t_est, 3)}
+    for rnd in range(rounds):
+        out = OD.verify_round(ocfg, W, hd, st, spec, seed, rnd, 10 ** 9, dtype=np.float32, cell=cell)
+        tokens += sum(len(t) for t in out["acc_tokens"])
+    secs = time.perf_counter() - t0
+    B, N = len(r.active), out["trees"][0].node_count
+    return {"value": round(tokens / secs, 3), "unit": "tok/s", "cores": int(threads), "kind": "port",
+            "cpu": cpu_model(),
+            "sample": (f"{rounds} verify round(s) of the same workload (B={B}, N={N}, all {cfg.num_layers} layers, "
+                       f"vocab {cfg.vocab}) through the numpy oracle in fp32 from the device's rollout state: "
+                       f"{tokens} tokens in {secs:.2f} s, no scaling"),
+            "seconds": round(secs, 3), "rounds": rounds}
 
 
 def summarize_trace(path, top=30):
@@ -364,7 +470,12 @@ def main():
     ap.add_argument("--config", default="7b", choices=sorted(WORKLOADS))
     ap.add_argument("--top-p", type=float, default=1.0, help="1.0 for throughput; 0.95 is the reference default")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-layers", type=int, default=2)
+    ap.add_argument("--no-planted-rounds", action="store_true",
+                    help="skip the full-acceptance rounds (lazy vs packed tree LM head)")
+    ap.add_argument("--no-rollout", action="store_true",
+                    help="skip the measured end-to-end rollout (prefill + the config's decode rounds)")
+    ap.add_argument("--cpu-rounds", type=int, default=None,
+                    help="verify rounds the CPU oracle runs (default: 32 for the tiny config, 1 otherwise)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--roofline-kernel", default="fg_tree_attention",
                     help="C-ABI entry point whose launches are event-timed in the timed rounds")
@@ -506,6 +617,14 @@ def main():
     log(f"phases (ms/round) {phases}")
     planted = planted_walk_gather(cfg, r, work, elem)
     log(f"planted {planted}")
+    full_rounds = None
+    if not args.no_planted_rounds:
+        full_rounds = planted_full_rounds(dec, r, args.steps)
+        log(f"planted full-acceptance rounds {full_rounds}")
+    rollout = None
+    if not args.no_rollout:
+        rollout = measured_rollout(dec, prompts, work["repeats"], int(work["rollout_rounds"]))
+        log(f"measured rollout {rollout}")
 
     def work_totals(rnds, sqs):
         totals = {}
@@ -559,9 +678,9 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
-        cpu = cpu_baseline(model, heads, r, work, seed=args.seed + 2, layers=args.cpu_layers)
+        n_cpu = args.cpu_rounds or (32 if args.config == "tiny" else 1)
+        cpu = cpu_baseline(model, heads, r, work, seed=args.seed + 2, rounds=n_cpu)
         log(f"cpu baseline {cpu['seconds']} s")
-    R = int(work["rollout_rounds"])
     res = {
         "metric": "rollout tok/s per MI355X (Qwen2.5-7B shape); verify-step latency; % roofline",
         "value": round(tokens / elapsed, 2),
@@ -584,10 +703,11 @@ def main():
         "accept_len_mean": round(tokens / max(sum(x["batch"] for x in rounds), 1), 4),
         "prefill_s": round(prefill_s, 2),
         # The reference's own rate (generated tokens over generation time including the
-        # prefill, flashgrpo_trainer.py:1117) for a rollout of the config's decode rounds,
-        # from the measured prefill and the measured per-round time and tokens.
-        "with_prefill": {"tok_s": round(tokens / args.steps * R / (prefill_s + elapsed / args.steps * R), 2),
-                         "decode_rounds": R},
+        # prefill, flashgrpo_trainer.py:1117): one whole rollout of the config's decode
+        # rounds timed end to end (generate()).
+        "with_prefill": rollout,
+        # every sequence accepting the tree's full depth (planted), lazy vs packed tree LM head
+        "planted_full_rounds": full_rounds,
         "hand_kernels_ms_per_step": round(mine_ms / args.steps, 3),
         "ms_per_step_instrumented": round(elapsed_i / args.steps * 1e3, 3),
         "phases_ms": phases,

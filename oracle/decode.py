@@ -268,8 +268,8 @@ def verify_round(cfg, W, heads, st: State, spec: DecodeSpec, seed: int, rnd: int
     width = max(new_len)
     nodes_arr = np.array([p + [p[-1]] * (width - len(p)) for p in acc_n])
     for li in range(L):
-        st.k[li] = OK.compact_rows(st.k[li], st.seq_len, nodes_arr, new_len)
-        st.v[li] = OK.compact_rows(st.v[li], st.seq_len, nodes_arr, new_len)
+        OK.compact_rows_in_place(st.k[li], st.seq_len, nodes_arr, new_len)
+        OK.compact_rows_in_place(st.v[li], st.seq_len, nodes_arr, new_len)
     lastn = np.array([p[-1] for p in acc_n])
     st.hidden = hid[np.arange(B), lastn]
     st.logits = OM.logits(st.hidden, W["lm_head"], dtype).astype(np.float32)

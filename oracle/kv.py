@@ -74,10 +74,15 @@ def compact_rows(cache, seq_len, acc_nodes, acc_len):
     These are exactly the valid rows of the reference's
     ``[old_len, old_len + max_len)`` block for that sequence.
     """
-    out = np.array(cache, copy=True)
-    for b in range(out.shape[0]):
+    return compact_rows_in_place(np.array(cache, copy=True), seq_len, acc_nodes, acc_len)
+
+
+def compact_rows_in_place(cache, seq_len, acc_nodes, acc_len):
+    """``compact_rows`` on ``cache`` itself (only the path rows move, as the reference's
+    ``_compact_tree_layer_in_place``, ``kv_extraction.py:70-84``); returns ``cache``."""
+    for b in range(cache.shape[0]):
         L = int(acc_len[b])
         src = [int(seq_len[b]) + int(n) for n in acc_nodes[b][:L]]
-        rows = out[b][:, src, :].copy()
-        out[b][:, int(seq_len[b]):int(seq_len[b]) + L, :] = rows
-    return out
+        rows = cache[b][:, src, :].copy()
+        cache[b][:, int(seq_len[b]):int(seq_len[b]) + L, :] = rows
+    return cache
