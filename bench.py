@@ -462,6 +462,62 @@ def summarize_pmc(path, symbol):
         print(f"| {name} | {len(v)} | {sum(v) / len(v):.6g} |")
 
 
+def attention_only(args, work):
+    """fg_tree_attention alone at the config's verify shape: batches of 10 back-to-back
+    launches behind a spin kernel, rotating over --cold distinct K/V caches (cold reads),
+    HIP events around each batch. Prints one JSON line (us per launch, GB/s, HBM fraction)."""
+    import numpy as np
+    import torch
+
+    from flashgrpo_amd import kernels as K
+    from flashgrpo_amd.decoding.medusa_tree import TreeTopology
+    from flashgrpo_amd.models import TargetConfig
+
+    cfg = getattr(TargetConfig, work["target"])()
+    B, Hq, Hkv, d = work["prompts"] * work["repeats"], cfg.q_heads, cfg.kv_heads, cfg.head_dim
+    P = work["prefix"]
+    # the dense tree the config's plan realises with random weights (adaptive plans keep their base k)
+    ks = {"7b": [4, 2, 1, 1], "14b": [4, 3, 2], "1.5b": [4, 2], "tiny": [4, 2], "8b": [4, 3, 2, 2]}[args.config]
+    topo = TreeTopology(ks, work["max_nodes"])
+    N = topo.num_nodes
+    cap = P + 64 + 80
+    dev, dt = "cuda", torch.bfloat16 if args.config != "tiny" else torch.float32
+    g = torch.Generator(device=dev).manual_seed(0)
+    kcs = [torch.randn(B, Hkv, cap, d, generator=g, device=dev, dtype=dt) for _ in range(args.cold)]
+    vcs = [torch.randn(B, Hkv, cap, d, generator=g, device=dev, dtype=dt) for _ in range(args.cold)]
+    q = torch.randn(B, N, Hq, d, generator=g, device=dev, dtype=dt)
+    seq = torch.full((B,), P, dtype=torch.int32, device=dev)
+    anc = torch.from_numpy(np.array([b & 0xFFFFFFFFFFFFFFFF for b in topo.anc_bits],
+                                    dtype=np.uint64).view(np.int64)).to(dev)
+    out = torch.empty_like(q)
+
+    def launch(c):
+        K.tree_attention(q, kcs[c], vcs[c], seq_len=seq, anc=anc, num_nodes=N, q_heads=Hq, kv_heads=Hkv,
+                         head_dim=d, out=out)
+
+    for c in range(args.cold):
+        launch(c)
+    torch.cuda.synchronize()
+    evs = []
+    for _ in range(max(args.steps, 1)):
+        torch.cuda._sleep(2_000_000)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for j in range(10):
+            launch(j % args.cold)
+        e1.record()
+        evs.append((e0, e1))
+    torch.cuda.synchronize()
+    us = np.array([a.elapsed_time(b) for a, b in evs]) * 1e3 / 10
+    elem = 2 if dt == torch.bfloat16 else 4
+    byts = 2 * B * Hkv * (P + N) * d * elem + 2 * B * N * Hq * d * elem
+    med = float(np.median(us))
+    print(json.dumps({"kernel": "fg_tree_attention", "config": args.config, "sequences": B, "tree_nodes": N,
+                      "prefix": P, "cold_caches": args.cold, "batches": len(us), "us_median": round(med, 2),
+                      "us_min": round(float(us.min()), 2), "bytes": byts, "GBps": round(byts / med / 1e3, 1),
+                      "hbm_frac": round(byts / med / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -486,6 +542,9 @@ def main():
                     help="rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE counter_collection CSVs of the roofline kernel")
     ap.add_argument("--traffic-scale", nargs=2, type=float, default=(2.0, 1.0), metavar=("FETCH", "WRITE"),
                     help="copy KiB per counter KiB, measured on a plain copy of known size (FETCH_SIZE, WRITE_SIZE)")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="time fg_tree_attention alone at the config's verify shape (batches of 10 launches)")
+    ap.add_argument("--cold", type=int, default=8, help="--attention-only: distinct K/V caches rotated over")
     ap.add_argument("--summarize-trace", metavar="CSV", help="summarise a rocprofv3 kernel trace of this command")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("CSV", "KERNEL"),
                     help="per-dispatch counter means of one kernel from a rocprofv3 --pmc run of this command")
@@ -510,6 +569,9 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     work = dict(WORKLOADS[args.config], top_p=args.top_p)
+    if args.attention_only:
+        attention_only(args, work)
+        return
     if args.warmup < 3:
         # the verify forward's HIP graph is captured on its second graph round and the last
         # warm-up round runs eagerly under the kernel timer, so fewer than three warm-up

@@ -43,6 +43,7 @@
 #include "fg_common.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace {
 
@@ -110,11 +111,47 @@ FG_DEVICE float xor32_sum(float x) {
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
+// LDS stage of one 64-key tile, filled straight from HBM by buffer_load ... lds (each
+// 16-byte-per-lane load writes 1 KB of consecutive LDS, lane l at +16 l):
+//  * K [64 keys][128 d], rows padded to 17 16-byte chunks (272 B): the S^T MFMA's A
+//    fragments (32 keys x 8 d per lane half) are 16-byte reads at compile-time offsets
+//    with the 32 rows of a read on distinct banks; the pad chunk loads chunk 15 again;
+//  * V [64 keys][128 d] row-major, 16-byte chunk c of key k stored at c ^ 4 (k % 4):
+//    the PV A fragments (32 d x 8 keys) are two ds_read_b64_tr_b16 each, whose 16-lane
+//    groups then touch all 64 banks once.
+constexpr int kKRowB = 272;
+constexpr int kKTileB = kKT * kKRowB;        // 17408
+constexpr int kVTileB = kKT * kD * 2;        // 16384
+constexpr int kStageB = kKTileB + kVTileB;   // 33792
+constexpr int kKLoads = kKTileB / 1024;      // 17 1-KB loads
+constexpr int kTileLoads = kKLoads + kVTileB / 1024;  // 33
+constexpr int stages_for(int w) { return w == 8 ? 4 : 2; }  // 4 x 33 KB with one workgroup per CU
+constexpr int loads_per_wave(int w) { return (kTileLoads + w - 1) / w; }
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) v4s lds_v4s;
+
+// s_waitcnt vmcnt(n) leaving the other counters unconstrained (gfx9 encoding).
+template <int N>
+FG_DEVICE void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 template <int W>
 __global__ void __launch_bounds__(W * 64, 2) tree_attn_bf16_kernel(AttnArgs a, int m_tiles) {
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kKT * kKPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][kD * kVtPitch];
-  typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+  constexpr int NB = stages_for(W);
+  constexpr int LPW = loads_per_wave(W);
+  // One array per stage: the compiler tracks the loads into each separately, so
+  // reading stage t does not wait for the loads still filling the others.
+  __shared__ __attribute__((aligned(1024))) unsigned char st0[kStageB];
+  __shared__ __attribute__((aligned(1024))) unsigned char st1[kStageB];
+  __shared__ __attribute__((aligned(1024))) unsigned char st2[NB > 2 ? kStageB : 16];
+  __shared__ __attribute__((aligned(1024))) unsigned char st3[NB > 3 ? kStageB : 16];
+  auto stage = [&](int i) __attribute__((always_inline)) -> unsigned char* {
+    return i == 0 ? st0 : i == 1 ? st1 : i == 2 ? st2 : st3;
+  };
   constexpr int kRowsTile = rows_tile(W);
 
   // A unit is one (sequence, kv head, key part); its m_tiles row tiles read the same
@@ -138,7 +175,6 @@ __global__ void __launch_bounds__(W * 64, 2) tree_attn_bf16_kernel(AttnArgs a, i
   // Keys past the cache's capacity were never written (fg_rope_kv_write flags them):
   // they are not attended, as in the fp32 kernel.
   const int total = min(s0 + a.N, a.capacity);
-  const int nkeys = total;
   const int cb = a.row_map ? a.row_map[b] : b;
   const uint16_t* kbase = (const uint16_t*)a.k + (int64_t)cb * a.cache_batch + (int64_t)hkv * a.cache_head;
   const uint16_t* vbase = (const uint16_t*)a.v + (int64_t)cb * a.cache_batch + (int64_t)hkv * a.cache_head;
@@ -177,177 +213,174 @@ __global__ void __launch_bounds__(W * 64, 2) tree_attn_bf16_kernel(AttnArgs a, i
   const float sl2 = a.scale * 1.44269504088896341f;
   const bf16x2 ones2 = __builtin_bit_cast(bf16x2, 0x3f803f80u);
 
-  // Staging: the first W/2 waves fetch K (thread t: 16-byte chunk t & 15 of keys
-  // (t >> 4) + 2W i), the others V (thread t: dims 8 (t >> 4) + 64 u .. +8 of keys
-  // 4 (t & 15) + i), both with buffer loads over the sequence's keys [0, nkeys)
-  // (past them: 0). CH 16-byte chunks per thread and tile.
-  constexpr int CH = 4 * (8 / W);
-  constexpr int KROWS = 2 * W;  // K rows between a thread's chunks
-  const bool stage_k = __builtin_amdgcn_readfirstlane(wave) < W / 2;  // wave-uniform
-  const int st = tid & (W * 32 - 1);
-  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(stage_k ? kbase : vbase), (short)0, nkeys * (kD * 2), 0x00020000);
-  const uint32_t soff = stage_k ? (uint32_t)((st >> 4) * kD + (st & 15) * 8) * 2u
-                                : (uint32_t)(4 * (st & 15) * kD + (st >> 4) * 8) * 2u;
-  uint16_t* const st_dst = stage_k ? &Ks[0][(st >> 4) * kKPitch + (st & 15) * 8]
-                                   : &Vt[0][(8 * (st >> 4)) * kVtPitch + vt_pos(4 * (st & 15))];
-  // Byte offset of chunk c from the thread's first chunk.
-  auto chunk_off = [&](int c) -> uint32_t {
-    return stage_k ? (uint32_t)(c * KROWS * kD * 2) : (uint32_t)((c & 3) * kD * 2 + (c >> 2) * 64 * 2);
-  };
-  v4u xa[CH], xb[CH];
-#define FG_LOAD8(X, KEY0)                                                                         \
-  {                                                                                               \
-    const uint32_t o_ = soff + (uint32_t)(KEY0) * (uint32_t)(kD * 2);                             \
-    _Pragma("unroll") for (int c_ = 0; c_ < CH; ++c_) X[c_] =                                     \
-        __builtin_amdgcn_raw_buffer_load_b128(rsrc, o_ + chunk_off(c_), 0, 0);                    \
+  // ---------------- HBM -> LDS loads: load i of a tile (0..32) is issued by wave i % W.
+  // Past the sequence's keys [0, total) the buffer returns 0.
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, total * (kD * 2),
+                                                                       0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, total * (kD * 2),
+                                                                       0x00020000);
+  uint32_t ld_off[LPW];  // byte offset in the tile's global rows of this lane's chunk, per load
+#pragma unroll
+  for (int u = 0; u < LPW; ++u) {
+    const int i = wave + W * u;
+    if (i < kKLoads) {
+      const int p = i * 64 + lane, row = p / 17, pc = p % 17;
+      ld_off[u] = (uint32_t)(row * (kD * 2) + (pc < 16 ? pc : 15) * 16);
+    } else {
+      const int row = 4 * (i - kKLoads) + (lane >> 4), c = (lane & 15) ^ (4 * (row & 3));
+      ld_off[u] = (uint32_t)(row * (kD * 2) + c * 16);
+    }
   }
-#define FG_STORE8(X, BUF)                                                                         \
-  {                                                                                               \
-    if (stage_k) {                                                                                \
-      uint16_t* kd_ = st_dst + (BUF) * (kKT * kKPitch);                                           \
-      _Pragma("unroll") for (int c_ = 0; c_ < CH; ++c_) *(v4u*)(kd_ + c_ * KROWS * kKPitch) = X[c_]; \
-    } else {                                                                                      \
-      _Pragma("unroll") for (int u_ = 0; u_ < CH / 4; ++u_) {                                     \
-        uint16_t* vd_ = st_dst + (BUF) * (kD * kVtPitch) + u_ * 64 * kVtPitch;                    \
-        const v4u* y_ = &X[4 * u_];                                                               \
-        _Pragma("unroll") for (int e2 = 0; e2 < 4; ++e2) {                                        \
-          *(uint2*)(vd_ + (2 * e2) * kVtPitch) =                                                  \
-              make_uint2(__builtin_amdgcn_perm(y_[1][e2], y_[0][e2], 0x05040100u),                \
-                         __builtin_amdgcn_perm(y_[3][e2], y_[2][e2], 0x05040100u));               \
-          *(uint2*)(vd_ + (2 * e2 + 1) * kVtPitch) =                                              \
-              make_uint2(__builtin_amdgcn_perm(y_[1][e2], y_[0][e2], 0x07060302u),                \
-                         __builtin_amdgcn_perm(y_[3][e2], y_[2][e2], 0x07060302u));               \
-        }                                                                                         \
-      }                                                                                           \
-    }                                                                                             \
+  // Issued as inline asm: the compiler's own tracking of loads into LDS cannot tell
+  // the stages apart and would wait for every tile in flight before each LDS read;
+  // the waits below (vmcnt before the per-tile barrier) are exact.
+  auto load_lds = [&](__amdgpu_buffer_rsrc_t rs, const unsigned char* dst, uint32_t voff)
+      __attribute__((always_inline)) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)(const lds_void*)dst;
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(m0) : "memory");
+  };
+  auto issue_tile = [&](unsigned char* st, int key0) __attribute__((always_inline)) {
+    const uint32_t t_off = (uint32_t)key0 * (kD * 2);
+#pragma unroll
+    for (int u = 0; u < LPW; ++u) {
+      const int i = wave + W * u;  // wave-uniform
+      if (i < kKLoads)
+        load_lds(krs, st + i * 1024, t_off + ld_off[u]);
+      else if (i < kTileLoads)
+        load_lds(vrs, st + kKTileB + (i - kKLoads) * 1024, t_off + ld_off[u]);
+    }
+  };
+  // this wave's loads per tile (the first waves issue one more)
+  const int my_loads = (kTileLoads - wave + W - 1) / W;
+
+  // ---------------- fragment addresses (bytes within a stage)
+  const uint32_t k_lane = (uint32_t)(l32 * kKRowB + g * 16);
+  // V^T fragment (32 d x 8 keys) via two transposed reads: lane 16 gq + i of a read
+  // gets element i % 4 of the 8 bytes addressed by lane 4 j + i / 4 of its group, for
+  // j = 0..3. Each lane addresses key 4 (gq / 2) + i / 4 (+ 8 for the second read) and
+  // d 32 db + 16 (gq % 2) + 4 (i % 4), so lane l receives keys 4 (l / 32) + j and
+  // 8 + 4 (l / 32) + j of d = 32 db + l % 32: the key order of the P^T fragments.
+  uint32_t v_lane[kD / 32];
+  {
+    const int gq = lane >> 4, i = lane & 15, aa = i >> 2;
+    const int lowc = 2 * (gq & 1) + ((i & 3) >> 1);
+    const uint32_t base = (uint32_t)(kKTileB + (4 * (gq >> 1) + aa) * (kD * 2) + lowc * 16 + 8 * (i & 1));
+#pragma unroll
+    for (int db = 0; db < kD / 32; ++db) v_lane[db] = base + (uint32_t)(64 * (db ^ aa));
   }
 
-  // Tiles are processed in pairs (LDS buffer 0, then 1); when the count is odd the
-  // loop leaves after the first tile of the last pair.
+  auto tile_compute = [&](const unsigned char* st, int key0) __attribute__((always_inline)) {
+    bf16x8 fr[16];
+    // all 16 K fragments before the first MFMA (one LDS latency per tile)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int s = 0; s < kD / 16; ++s)
+        fr[kb * 8 + s] = *(const bf16x8*)(st + k_lane + kb * 32 * kKRowB + s * 32);
+    __builtin_amdgcn_sched_barrier(0);
+    floatx16 sc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sc[kb][i] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < kD / 16; ++s)
+        sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr[kb * 8 + s], qf[s], sc[kb], 0, 0, 0);
+    }
+    // the 16 V^T fragments, read during the S MFMAs
+#pragma unroll
+    for (int db = 0; db < kD / 32; ++db)
+#pragma unroll
+      for (int ks4 = 0; ks4 < 4; ++ks4) {
+        const unsigned char* p0 = st + v_lane[db] + ks4 * 16 * (kD * 2);
+        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)p0);
+        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(p0 + 8 * (kD * 2)));
+        fr[db * 4 + ks4] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+    __builtin_amdgcn_sched_barrier(0);
+    if (key0 + kKT > s0 || key0 + kKT > key_end) {  // tile reaches the tree keys or the part's end
+      const uint64_t visible = a.anc ? tile_allowed_mask(s0 - key0, tree_bits) : low_bits(s0 + qn + 1 - key0);
+      const uint64_t allowed = (visible & low_bits(key_end - key0)) >> (g * 4);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const bool ok = (allowed >> (kb * 32 + c_row32(i, 0))) & 1ull;
+          sc[kb][i] = ok ? sc[kb][i] : -INFINITY;
+        }
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, sc[kb][i]);
+    const float m_new = fmaxf(m_run, xor32_max(tmax) * sl2);
+    // Lazy rescale: the reference max only moves when some lane's max grew by more
+    // than 2^kRescaleSlack, so p <= 2^kRescaleSlack and O / l is unchanged.
+    if (__any(m_new > m_run + kRescaleSlack)) {
+      const float m_sub = m_new == -INFINITY ? 0.0f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_sub);
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < kD / 32; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+      m_run = m_new;
+    }
+    const float m_sub = m_run == -INFINITY ? 0.0f : m_run;
+    float psum = l_run;
+    bf16x8 pf[2][2];  // [kb][ks] B operand of P^T
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        uint32_t packed[4];
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[kb][ks * 8 + j], sl2, -m_sub));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[kb][ks * 8 + j + 1], sl2, -m_sub));
+          packed[j / 2] = fg::pack_bf16x2(p0, p1);
+          psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, packed[j / 2]), ones2, psum, false);
+        }
+        pf[kb][ks] = __builtin_bit_cast(bf16x8, make_uint4(packed[0], packed[1], packed[2], packed[3]));
+      }
+    l_run = psum;
+#pragma unroll
+    for (int db = 0; db < kD / 32; ++db)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr[db * 4 + kb * 2 + ks], pf[kb][ks], o[db], 0, 0, 0);
+  };
+
+  // ---------------- pipeline: tiles t + 1 .. t + NB - 1 are loading while tile t is
+  // computed; one barrier per tile. Loads are issued for NB - 1 tiles past the last
+  // (zeros past the sequence's keys) so every wait below has a fixed count.
   const int ntiles = t_end - t_begin;
   const int kbeg = t_begin * kKT;
-  // Pipeline: while tile t is computed from LDS buffer t % 2, tile t + 1 is already
-  // in the other buffer (stored at the top of the iteration, so the store and its
-  // wait on the loads overlap the compute). With 8 waves tiles t + 2 and t + 3 are
-  // in flight in two register sets; with 4 waves (twice the chunks per thread, two
-  // workgroups per CU) tile t + 2 is in flight in one.
-  if constexpr (W == 8) {
-    FG_LOAD8(xa, kbeg)
-    FG_LOAD8(xb, kbeg + kKT)
-    FG_STORE8(xa, 0)
-    FG_LOAD8(xa, kbeg + 2 * kKT)
-  } else {
-    FG_LOAD8(xa, kbeg)
-    FG_STORE8(xa, 0)
-    FG_LOAD8(xa, kbeg + kKT)
+#pragma unroll
+  for (int h = 0; h < NB - 1; ++h) issue_tile(stage(h), kbeg + h * kKT);
+  for (int t0 = 0; t0 < ntiles; t0 += NB)
+#pragma unroll
+  for (int h = 0; h < NB; ++h) {
+    if (h > 0 && t0 + h >= ntiles) break;  // uniform over the workgroup
+    // this wave's loads of tile t are done once at most NB - 2 tiles of its loads remain
+    if (my_loads == LPW)
+      wait_vmcnt<(NB - 2) * LPW>();
+    else
+      wait_vmcnt<(NB - 2) * (LPW - 1)>();
+    // Tile t is in LDS for every wave and every wave is done with tile t - 1. No LDS
+    // store other than the loads above happens in the loop, so a bare s_barrier after
+    // each wave's own vmcnt wait suffices (__syncthreads' release fence would also wait
+    // for the loads of the tiles still in flight).
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue_tile(stage((h + NB - 1) % NB), kbeg + (t0 + h + NB - 1) * kKT);
+    if (computes) tile_compute(stage(h), kbeg + (t0 + h) * kKT);
   }
-  __syncthreads();
-  const uint16_t* const kf_src = &Ks[0][l32 * kKPitch + g * 8];
-  const uint16_t* const vf_src = &Vt[0][l32 * kVtPitch + g * 8];
-  for (int t0 = 0; t0 < ntiles; t0 += 2)
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    if (h == 1 && t0 + 1 >= ntiles) break;  // uniform over the workgroup
-    const int key0 = kbeg + (t0 + h) * kKT;
-    if constexpr (W == 8) {
-      if (h == 0) {
-        FG_STORE8(xb, 1)
-        FG_LOAD8(xb, key0 + 3 * kKT)
-      } else {
-        FG_STORE8(xa, 0)
-        FG_LOAD8(xa, key0 + 3 * kKT)
-      }
-    } else {
-      FG_STORE8(xa, h ^ 1)
-      FG_LOAD8(xa, key0 + 2 * kKT)
-    }
-
-    if (computes) {
-      const uint16_t* kf_ = kf_src + h * (kKT * kKPitch);
-      const uint16_t* vf_ = vf_src + h * (kD * kVtPitch);
-      // All 16 K fragments of the tile are read before the first MFMA (one LDS
-      // latency per tile instead of one per fragment pair); the same registers then
-      // hold the 16 V^T fragments, read before the exponentials.
-      bf16x8 fr[16];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int s = 0; s < kD / 16; ++s) fr[kb * 8 + s] = *(const bf16x8*)(kf_ + kb * 32 * kKPitch + s * 16);
-      __builtin_amdgcn_sched_barrier(0);
-      floatx16 sc[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sc[kb][i] = 0.0f;
-#pragma unroll
-        for (int s = 0; s < kD / 16; ++s)
-          sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr[kb * 8 + s], qf[s], sc[kb], 0, 0, 0);
-      }
-#pragma unroll
-      for (int db = 0; db < kD / 32; ++db)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) fr[db * 4 + c] = *(const bf16x8*)(vf_ + db * 32 * kVtPitch + c * 16);
-      __builtin_amdgcn_sched_barrier(0);
-      if (key0 + kKT > s0 || key0 + kKT > key_end) {  // tile reaches the tree keys or the part's end
-        const uint64_t visible = a.anc ? tile_allowed_mask(s0 - key0, tree_bits) : low_bits(s0 + qn + 1 - key0);
-        const uint64_t allowed = (visible & low_bits(key_end - key0)) >> (g * 4);
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const bool ok = (allowed >> (kb * 32 + c_row32(i, 0))) & 1ull;
-            sc[kb][i] = ok ? sc[kb][i] : -INFINITY;
-          }
-      }
-      float tmax = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) tmax = fmaxf(tmax, sc[kb][i]);
-      const float m_new = fmaxf(m_run, xor32_max(tmax) * sl2);
-      // Lazy rescale: the reference max only moves when some lane's max grew by
-      // more than 2^kRescaleSlack, so p <= 2^kRescaleSlack and O / l is unchanged.
-      if (__any(m_new > m_run + kRescaleSlack)) {
-        const float m_sub = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_sub);
-        l_run *= alpha;
-#pragma unroll
-        for (int db = 0; db < kD / 32; ++db)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
-        m_run = m_new;
-      }
-      const float m_sub = m_run == -INFINITY ? 0.0f : m_run;
-      float psum = l_run;
-      bf16x8 pf[2][2];  // [kb][ks] B operand of P^T
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          uint32_t packed[4];
-#pragma unroll
-          for (int j = 0; j < 8; j += 2) {
-            const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[kb][ks * 8 + j], sl2, -m_sub));
-            const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[kb][ks * 8 + j + 1], sl2, -m_sub));
-            packed[j / 2] = fg::pack_bf16x2(p0, p1);
-            psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, packed[j / 2]), ones2, psum, false);
-          }
-          pf[kb][ks] = __builtin_bit_cast(bf16x8, make_uint4(packed[0], packed[1], packed[2], packed[3]));
-        }
-      l_run = psum;
-#pragma unroll
-      for (int db = 0; db < kD / 32; ++db)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks)
-            o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr[db * 4 + kb * 2 + ks], pf[kb][ks], o[db], 0, 0, 0);
-    }
-    __syncthreads();
-  }
-#undef FG_LOAD8
-#undef FG_STORE8
+  wait_vmcnt<0>();  // no load may still write this workgroup's LDS when it ends
 
   const float l = xor32_sum(l_run);
   if (a.splits > 1) {  // unnormalised part: O rows (fp32) and (max in log2 units, sum)
