@@ -62,6 +62,23 @@ int fg_lm_head(const void* x, int dtype, int M, int K, int64_t ldx, const int32_
                const int32_t* row_active, const void* w, int64_t ldw, int N, void* out, int out_dtype, int64_t ldo,
                void* stream);
 
+/* Tied LM head over 1..256 rows with the per-row top-k fused:
+ *   logits[m, :] = x[row_index ? row_index[m] : m, :] . w^T        (bf16 x and w)
+ * One persistent launch streams w [N, K] once (bf16, 16-byte aligned rows, K % 64 == 0,
+ * w spanning < 4 GiB; x spanning < 4 GiB from its base); out [M, ldo] (bf16 or fp32,
+ * optional). With kmax in [1, 16] (at most 8 above 192 rows) it also writes each row's top-kmax candidates
+ * (cand_tokens / cand_scores [M, kmax]) and, if row_stats is given, its (max, logsumexp)
+ * [M, 2], ranked and computed exactly as fg_medusa_topk does on the bf16 logits (sanitize
+ * as there), without reading the logits back; workspace >=
+ * fg_lm_head_topk_workspace(M, N, kmax). row_active (kmax 0 only): nothing is computed
+ * when every flag is 0. Replaces decoding/flash_medusa_decoder.py:289-294 (Medusa rows),
+ * :1079-1091 (leaf / next-round rows) and the torch.topk of medusa_tree.py:239-252. */
+size_t fg_lm_head_topk_workspace(int rows, int vocab, int kmax);
+int fg_lm_head_topk(const void* x, int M, int K, int64_t ldx, const int32_t* row_index, const int32_t* row_active,
+                    const void* w, int64_t ldw, int N, void* out, int out_dtype, int64_t ldo, int kmax, int sanitize,
+                    int32_t* cand_tokens, float* cand_scores, float* row_stats, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
 /* Per-row top-kmax candidates, ranked (value desc, index asc).
  * logits [rows, vocab] with row stride row_stride (multiple of 8, 32-byte aligned base).
  * cand_tokens/cand_scores [rows, kmax]; row_stats (optional) [rows, 2] = (max, logsumexp).

@@ -237,7 +237,9 @@ __global__ void __launch_bounds__(W * 64, 2) tree_attn_bf16_kernel(AttnArgs a, i
   auto load_lds = [&](__amdgpu_buffer_rsrc_t rs, const unsigned char* dst, uint32_t voff)
       __attribute__((always_inline)) {
     const uint32_t m0 = (uint32_t)(uintptr_t)(const lds_void*)dst;
-    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(m0) : "memory");
+    // s_nop 4: the compiler's hazard checks do not see into inline asm; the load needs a wait
+    // state after the M0 write and 5 after any VALU write of the SGPRs it reads.
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(m0) : "memory");
   };
   auto issue_tile = [&](unsigned char* st, int key0) __attribute__((always_inline)) {
     const uint32_t t_off = (uint32_t)key0 * (kD * 2);

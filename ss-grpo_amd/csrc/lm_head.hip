@@ -1,0 +1,461 @@
+// Tied LM head over up to 256 rows with the weight streamed once, and the per-row
+// top-k candidates and (max, sum of exp) of the logits produced in the epilogue.
+//
+//   logits[m, n] = x[rows ? rows[m] : m, :] . w[n, :]        m < M <= 256, n < N
+//
+// Replaces the lm_head projections of flashgrpo/decoding/flash_medusa_decoder.py:289-294
+// (Medusa rows), :1079-1091 (leaf / next-round rows) and the per-depth torch.topk of
+// flashgrpo/decoding/medusa_tree.py:239-252 that reads those logits back.
+//
+// Work split: the vocabulary is cut into 32-column blocks dealt out in contiguous runs to
+// every wave of a persistent grid (one workgroup of 8 waves per CU). A wave streams its
+// block's 32 weight rows from HBM into registers as whole 128-byte row pieces (8 lanes per
+// row, 4 loads per 64-wide k-step; this measured 0.76 of HBM against 0.65 for loading the
+// MFMA operand layout directly), turns them into the operand layout through its own 4 KB
+// of LDS, and multiplies them with v_mfma_f32_32x32x16_bf16 against the activation rows,
+// which the workgroup stages per k-step in LDS (HBM -> LDS loads, 3-4 stages). 16-byte
+// pieces are XOR-swizzled in both LDS layouts. MFMA step kk of a k-step uses 16-byte piece
+// 4 g + kk of each row for lane group g, on both operands, so both sum the same products.
+// The weight is read exactly once; the activations (<= 1.8 MB) are re-read from L2 per
+// block round.
+//
+// Epilogue of a block round: the logits are written (optional), and with top-k the
+// workgroup's 256 columns x M rows are rounded to bf16 (the values the reference ranks)
+// and placed in LDS, where each row's running top-K and (max, sum exp) over the
+// workgroup's columns are updated. At the end every workgroup writes its part of each
+// row to part_keys / part_lse, which topk_phase2 (topk.hip) merges per row.
+#include "fg_common.h"
+#include "fg_topk.h"
+
+#include <algorithm>
+#include <mutex>
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kWaves = 8;
+constexpr int kKS = 64;     // k-step
+constexpr int kTileRow = 528;  // bytes per row of the epilogue's bf16 tile (256 columns + 16)
+// k-steps in flight; the activation ring has one stage more
+constexpr int dist_for(int mi) { return mi >= 8 ? 2 : 3; }
+
+template <int N>
+FG_DEVICE void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// 16-byte piece position of piece c of activation row r in LDS (rows of 128 bytes). The
+// swizzle depends on r % 32 only, so every 32-row block has the same layout.
+FG_DEVICE int a_swz(int r) { return (r ^ ((r >> 3) & 3)) & 7; }
+FG_DEVICE int a_pos(int r, int c) { return c ^ a_swz(r); }
+
+struct LmArgs {
+  const void* x;
+  int64_t ldx;
+  const int32_t* rows;        // optional row gather
+  const int32_t* row_active;  // optional: nothing is computed when every flag is 0
+  int M, K;
+  const void* w;
+  int64_t ldw;
+  int N;
+  void* out;  // optional [M, ldo]
+  int64_t ldo;
+  uint64_t* part_keys;  // [M, nparts, KT]
+  float2* part_lse;     // [M, nparts]
+  int nparts;  // = grid: one part per workgroup
+};
+
+template <int MI, int CDT, int KT, bool SAN>
+__global__ void __launch_bounds__(kWaves * 64, 1) lm_stream_kernel(LmArgs a) {
+  constexpr int kDist = dist_for(MI), kStages = kDist + 1;
+  constexpr int MP = MI * 32;
+  constexpr int STAGE = MP * 128;
+  constexpr int LA = STAGE / 1024 / kWaves;  // HBM -> LDS loads per wave and k-step
+  constexpr int LB = 4;                      // weight loads per lane and k-step
+  constexpr int L = LA + LB;
+  static_assert(MI % 2 == 0 && LA >= 1, "rows");
+  static_assert((kDist - 1) * L < 64, "vmcnt");
+  constexpr int XPOSE = kStages * STAGE;     // per-wave 4 KB weight transpose buffers
+  constexpr int TILE = KT ? MP * kTileRow : 0;
+  constexpr int MAIN = XPOSE + kWaves * 4096 > TILE ? XPOSE + kWaves * 4096 : TILE;
+  // each row's running top-KT keys and (max, sum exp) over this workgroup's columns
+  constexpr int LISTS = KT ? MP * (KT * 8 + 8) : 0;
+  constexpr int LDS = MAIN + LISTS;
+  static_assert(LDS <= 160 * 1024 - 256, "LDS");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[LDS];
+  uint64_t* s_keys = (uint64_t*)(smem + MAIN);
+  float2* s_lse = (float2*)(smem + MAIN + MP * KT * 8);
+  __shared__ int s_n0[kWaves], s_nv[kWaves], s_any;
+
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (a.row_active) {
+    if (tid == 0) s_any = 0;
+    __syncthreads();
+    if (tid < a.M && a.row_active[tid]) s_any = 1;
+    __syncthreads();
+    if (!s_any) return;
+  }
+  // Block rd * GW + gw goes to wave gw = wave * G + workgroup in round rd: the blocks of a
+  // partial last round are spread over every CU (a CU's loads, not HBM, bound a round that
+  // only a few CUs run).
+  const int nblk = (a.N + 31) >> 5;
+  const int gw_total = gridDim.x * kWaves;
+  const int gw = wave * gridDim.x + blockIdx.x;
+  const int q = nblk / gw_total, rem = nblk % gw_total;
+  const int my_cnt = q + (gw < rem ? 1 : 0);
+  const int rounds = q + ((int)blockIdx.x < rem ? 1 : 0);  // wave 0 has the most blocks
+  const int KST = a.K / kKS;
+
+  // activation staging: load u of this wave fills LDS rows (wave * LA + u) * 8 + lane / 8
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, -1, 0x00020000);
+  uint32_t xoff[LA];
+#pragma unroll
+  for (int u = 0; u < LA; ++u) {
+    const int r = (wave * LA + u) * 8 + (lane >> 3);
+    const int m = min(r, a.M - 1);
+    const int src = a.rows ? a.rows[m] : m;
+    xoff[u] = (uint32_t)((int64_t)src * a.ldx * 2) + (uint32_t)(a_pos(r, lane & 7) * 16);
+  }
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem + wave * LA * 1024;
+  auto issue_x = [&](int ks, int stage) __attribute__((always_inline)) {
+    const uint32_t koff = (uint32_t)ks * (kKS * 2);
+    const uint32_t st = (uint32_t)stage * STAGE;
+#pragma unroll
+    for (int u = 0; u < LA; ++u) {
+      const uint32_t m0v = lds0 + st + u * 1024;
+      // s_nop 4: the compiler's hazard checks do not see into inline asm, so the asm keeps
+      // the wait states a load needs after a VALU write of an SGPR it reads (5; the compiler
+      // moves spilled SGPRs back with v_readlane) and after the M0 write (1).
+      asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(xoff[u]), "s"(xrs), "s"(koff),
+                   "{m0}"(m0v)
+                   : "memory");
+    }
+  };
+  // weight stream: load q of a k-step brings rows q * 8 + lane / 8 of the block, 16-byte
+  // piece lane % 8 (128 contiguous bytes per row)
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, -1, 0x00020000);
+  uint32_t woff[LB];
+  v4u wr[kDist][LB];
+  // Issued as inline asm so the compiler adds no waits of its own: it would count only these
+  // loads, not the activation loads between them, and wait for younger k-steps too. The
+  // static wait before each k-step's barrier covers them.
+  // (one statement with its own wait states, as for the activation loads)
+  auto issue_w = [&](v4u(&dst)[LB], int koff) __attribute__((always_inline)) {
+    asm volatile(
+        "s_nop 4\n\t"
+        "buffer_load_dwordx4 %0, %4, %8, %9 offen\n\t"
+        "buffer_load_dwordx4 %1, %5, %8, %9 offen\n\t"
+        "buffer_load_dwordx4 %2, %6, %8, %9 offen\n\t"
+        "buffer_load_dwordx4 %3, %7, %8, %9 offen"
+        : "=&v"(dst[0]), "=&v"(dst[1]), "=&v"(dst[2]), "=&v"(dst[3])
+        : "v"(woff[0]), "v"(woff[1]), "v"(woff[2]), "v"(woff[3]), "s"(wrs), "s"(koff));
+  };
+  // this wave's transpose buffer: row r of the block at r * 128, pieces swizzled like x
+  unsigned char* xp = smem + XPOSE + wave * 4096;
+  uint32_t xw[LB];
+#pragma unroll
+  for (int q = 0; q < LB; ++q) {
+    const int r = q * 8 + (lane >> 3);
+    xw[q] = (uint32_t)(r * 128 + a_pos(r, lane & 7) * 16);
+  }
+  // A fragment address of m-block 0, piece kk of this lane's group (bytes within a stage)
+  uint32_t foff[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) foff[kk] = (uint32_t)(l32 * 128 + a_pos(l32, g * 4 + kk) * 16);
+
+  for (int rd = 0; rd < rounds; ++rd) {
+    // Every wave issues the same loads every k-step, so the waits below are static: a wave
+    // without a block this round, and the k-steps past the last, re-read one cached line.
+    const bool active = rd < my_cnt;  // wave-uniform
+    const int n0 = (rd * gw_total + gw) * 32;
+#pragma unroll
+    for (int q = 0; q < LB; ++q)
+      woff[q] = active ? (uint32_t)((int64_t)min(n0 + q * 8 + (lane >> 3), a.N - 1) * a.ldw * 2) +
+                             (uint32_t)((lane & 7) * 16)
+                       : 0u;
+    const int wstep = active ? kKS * 2 : 0;
+    floatx16 acc[MI];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
+
+#pragma unroll
+    for (int h = 0; h < kDist; ++h) {
+      issue_x(h < KST ? h : 0, h % kStages);
+      issue_w(wr[h], h < KST ? h * wstep : 0);
+    }
+    for (int k0 = 0; k0 < KST; k0 += kDist) {
+#pragma unroll
+      for (int sl = 0; sl < kDist; ++sl) {
+        const int ks = k0 + sl;
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<(kDist - 1) * L>();  // k-step ks has landed (younger ones may be in flight)
+        // k-step ks is in LDS for every wave, and every wave is done with ks - 1
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        const int kn = ks + kDist;
+        issue_x(kn < KST ? kn : 0, kn % kStages);
+        if (ks < KST && active) {
+          const unsigned char* st = smem + (ks % kStages) * STAGE;
+          // the weight pieces into operand layout (this wave read the previous ones already)
+#pragma unroll
+          for (int q = 0; q < LB; ++q) *(v4u*)(xp + xw[q]) = wr[sl][q];
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) {
+            const bf16x8 bf = *(const bf16x8*)(xp + foff[kk]);
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+              const bf16x8 af = *(const bf16x8*)(st + i * 32 * 128 + foff[kk]);
+              acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf, af, acc[i], 0, 0, 0);
+            }
+            // one piece's fragments live at a time (hoisting all four would spill at 256 rows)
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // the weight slot is free once its pieces are in LDS
+        issue_w(wr[sl], kn < KST ? kn * wstep : 0);
+      }
+    }
+    wait_vmcnt<0>();
+    // The last k-steps' weight loads are never read: keep their registers allocated until
+    // they have landed, or the compiler could give them to the code below while the loads
+    // still write them.
+#pragma unroll
+    for (int h = 0; h < kDist; ++h)
+      asm volatile("" ::"v"(wr[h][0]), "v"(wr[h][1]), "v"(wr[h][2]), "v"(wr[h][3]));
+    __builtin_amdgcn_sched_barrier(0);
+
+    // acc[i] is a tile of C^T: lane holds row m = 32 i + l32, columns n0 + 8 (v / 4) + 4 g + v % 4
+    if (a.out && active) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int m = i * 32 + l32;
+        if (m >= a.M) continue;
+#pragma unroll
+        for (int v4 = 0; v4 < 4; ++v4) {
+          const int n = n0 + v4 * 8 + g * 4;
+          if (n >= a.N) continue;
+          if constexpr (CDT == fg::kBF16) {
+            uint16_t* o = (uint16_t*)a.out + (int64_t)m * a.ldo + n;
+            if (n + 3 < a.N && (a.ldo & 3) == 0) {
+              *(uint2*)o = make_uint2(fg::pack_bf16x2(acc[i][4 * v4], acc[i][4 * v4 + 1]),
+                                      fg::pack_bf16x2(acc[i][4 * v4 + 2], acc[i][4 * v4 + 3]));
+            } else {
+              for (int e = 0; e < 4 && n + e < a.N; ++e) o[e] = fg::f32_to_bf16(acc[i][4 * v4 + e]);
+            }
+          } else {
+            float* o = (float*)a.out + (int64_t)m * a.ldo + n;
+            if (n + 3 < a.N && (a.ldo & 3) == 0) {
+              *(float4*)o = make_float4(acc[i][4 * v4], acc[i][4 * v4 + 1], acc[i][4 * v4 + 2], acc[i][4 * v4 + 3]);
+            } else {
+              for (int e = 0; e < 4 && n + e < a.N; ++e) o[e] = acc[i][4 * v4 + e];
+            }
+          }
+        }
+      }
+    }
+    if constexpr (KT > 0) {
+      // this round's logits (bf16) into LDS: tile[m][32 wave + c], rows of kTileRow bytes
+      __syncthreads();  // every wave is done reading the activation stages
+      if (lane == 0) {
+        s_n0[wave] = n0;
+        s_nv[wave] = active ? min(32, a.N - n0) : 0;
+      }
+      if (active) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          const int m = i * 32 + l32;
+#pragma unroll
+          for (int v4 = 0; v4 < 4; ++v4) {
+            const int c = wave * 32 + v4 * 8 + g * 4;
+            *(uint2*)(smem + m * kTileRow + c * 2) = make_uint2(fg::pack_bf16x2(acc[i][4 * v4], acc[i][4 * v4 + 1]),
+                                                           fg::pack_bf16x2(acc[i][4 * v4 + 2], acc[i][4 * v4 + 3]));
+          }
+        }
+      }
+      __syncthreads();
+      // TPR threads per row scan 8 columns at a time. Keys at or below the row's KT-th best
+      // key of the earlier rounds cannot enter its list and are skipped.
+      constexpr int TPR = kWaves * 64 / MP;
+      const int m = tid / TPR, sub = tid % TPR;
+      const bool row_ok = m < a.M && m < MP;
+      const uint64_t thr = (row_ok && rd > 0) ? s_keys[m * KT + KT - 1] : 0ull;
+      uint64_t top[KT];
+#pragma unroll
+      for (int i = 0; i < KT; ++i) top[i] = 0;
+      fg::LseAcc acc_l{-INFINITY, 0.0f};
+      if (row_ok) {
+        for (int c = sub * 8; c < 256; c += TPR * 8) {
+          const int wv = c >> 5, nv = s_nv[wv];
+          if ((c & 31) >= nv) continue;
+          const int nbase = s_n0[wv] + (c & 31);
+          const uint4 raw = *(const uint4*)(smem + m * kTileRow + c * 2);
+          const uint32_t wds[4] = {raw.x, raw.y, raw.z, raw.w};
+          float v[8];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            v[2 * j] = fg::sanitize<SAN>(__uint_as_float(wds[j] << 16));
+            v[2 * j + 1] = fg::sanitize<SAN>(__uint_as_float(wds[j] & 0xffff0000u));
+          }
+          const int valid = min(8, nv - (c & 31));
+          float m8 = -INFINITY;
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            if (j < valid) {
+              const uint64_t key = fg::rank_key(v[j], (uint32_t)(nbase + j));
+              if (key > thr) fg::insert_key<KT>(top, key);
+              m8 = fmaxf(m8, v[j]);
+            }
+          const float mx = fmaxf(acc_l.m, m8);
+          float sm = (acc_l.m == -INFINITY) ? 0.0f : acc_l.s * __expf(acc_l.m - mx);
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            if (j < valid) sm += __expf(v[j] - mx);
+          acc_l = {mx, sm};
+        }
+      }
+      fg::lanes_merge<KT>(top, TPR);
+#pragma unroll
+      for (int o = TPR / 2; o > 0; o >>= 1) {
+        fg::LseAcc other{__shfl_xor(acc_l.m, o, 64), __shfl_xor(acc_l.s, o, 64)};
+        acc_l = fg::lse_combine(acc_l, other);
+      }
+      if (row_ok && sub == 0) {
+        if (rd > 0) {
+          uint64_t run[KT];
+#pragma unroll
+          for (int i = 0; i < KT; ++i) run[i] = s_keys[m * KT + i];
+          fg::merge_desc<KT>(top, run);
+          const float2 p = s_lse[m];
+          acc_l = fg::lse_combine(acc_l, fg::LseAcc{p.x, p.y});
+        }
+#pragma unroll
+        for (int i = 0; i < KT; ++i) s_keys[m * KT + i] = top[i];
+        s_lse[m] = make_float2(acc_l.m, acc_l.s);
+      }
+      __syncthreads();  // the tile is read before the next round's activation loads land
+    }
+  }
+  if constexpr (KT > 0) {
+    // this workgroup's part of every row
+    for (int m = tid; m < a.M; m += kWaves * 64) {
+      const int64_t pi = (int64_t)m * a.nparts + blockIdx.x;
+#pragma unroll
+      for (int i = 0; i < KT; ++i) a.part_keys[pi * KT + i] = s_keys[m * KT + i];
+      a.part_lse[pi] = s_lse[m];
+    }
+  }
+}
+
+int g_cus = 0;
+std::once_flag g_cus_once;
+int device_cus() {
+  std::call_once(g_cus_once, [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+      g_cus = n;
+    if (g_cus <= 0) g_cus = 256;
+  });
+  return g_cus;
+}
+
+struct Plan {
+  int grid, rmax, nparts;
+};
+Plan plan_for(int N) {
+  const int nblk = (N + 31) / 32;
+  Plan p;
+  p.grid = std::max(1, std::min(device_cus(), (nblk + kWaves - 1) / kWaves));
+  p.rmax = (nblk + p.grid * kWaves - 1) / (p.grid * kWaves);
+  p.nparts = p.grid;
+  return p;
+}
+int k_bucket(int kmax) { return kmax <= 1 ? 1 : kmax <= 2 ? 2 : kmax <= 4 ? 4 : kmax <= 8 ? 8 : 16; }
+
+template <int MI, int CDT, int KT, bool SAN>
+void launch_mi(const LmArgs& a, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((lm_stream_kernel<MI, CDT, KT, SAN>), dim3(grid), dim3(kWaves * 64), 0, s, a);
+}
+template <int CDT, int KT, bool SAN>
+void launch_rows(const LmArgs& a, int grid, hipStream_t s) {
+  if (a.M <= 64) launch_mi<2, CDT, KT, SAN>(a, grid, s);
+  else if (a.M <= 128) launch_mi<4, CDT, KT, SAN>(a, grid, s);
+  else if (a.M <= 192) launch_mi<6, CDT, KT, SAN>(a, grid, s);
+  else if constexpr (KT <= 8) launch_mi<8, CDT, KT, SAN>(a, grid, s);  // (LDS: the host rejects KT 16 here)
+}
+template <int KT, bool SAN>
+void launch_cdt(const LmArgs& a, int out_dtype, int grid, hipStream_t s) {
+  if (out_dtype == fg::kF32) launch_rows<fg::kF32, KT, SAN>(a, grid, s);
+  else launch_rows<fg::kBF16, KT, SAN>(a, grid, s);
+}
+template <int KT>
+void launch_san(const LmArgs& a, int out_dtype, bool san, int grid, hipStream_t s) {
+  if (san) launch_cdt<KT, true>(a, out_dtype, grid, s);
+  else launch_cdt<KT, false>(a, out_dtype, grid, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t fg_lm_head_topk_workspace(int rows, int vocab, int kmax) {
+  if (rows <= 0 || vocab <= 0 || kmax <= 0) return 256;
+  const Plan p = plan_for(vocab);
+  return (size_t)rows * p.nparts * (k_bucket(kmax) * sizeof(uint64_t) + sizeof(float2)) + 256;
+}
+
+int fg_lm_head_topk(const void* x, int M, int K, int64_t ldx, const int32_t* row_index, const int32_t* row_active,
+                    const void* w, int64_t ldw, int N, void* out, int out_dtype, int64_t ldo, int kmax, int sanitize,
+                    int32_t* cand_tokens, float* cand_scores, float* row_stats, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  FG_REQUIRE(x && w, "fg_lm_head_topk: null pointer");
+  FG_REQUIRE(M >= 1 && M <= 256, "fg_lm_head_topk: M must be in [1, 256]");
+  FG_REQUIRE(N >= 1 && K >= kKS && K % kKS == 0, "fg_lm_head_topk: K must be a positive multiple of 64");
+  FG_REQUIRE(ldx >= K && ldx % 8 == 0 && ldw >= K && ldw % 8 == 0 && ((uintptr_t)x & 15) == 0 &&
+                 ((uintptr_t)w & 15) == 0,
+             "fg_lm_head_topk: x and w need 16-byte aligned rows");
+  FG_REQUIRE((uint64_t)N * (uint64_t)ldw * 2 <= 0xFFFFFFFFull, "fg_lm_head_topk: w must span less than 4 GiB");
+  FG_REQUIRE(out_dtype == fg::kBF16 || out_dtype == fg::kF32, "fg_lm_head_topk: out_dtype");
+  FG_REQUIRE(out || kmax > 0, "fg_lm_head_topk: nothing to compute (no out, kmax 0)");
+  FG_REQUIRE(!out || ldo >= N, "fg_lm_head_topk: ldo < N");
+  FG_REQUIRE(kmax >= 0 && kmax <= 16 && kmax <= N, "fg_lm_head_topk: kmax must be in [0, min(16, N)]");
+  FG_REQUIRE(kmax == 0 || (cand_tokens && cand_scores && workspace), "fg_lm_head_topk: candidate outputs missing");
+  FG_REQUIRE(kmax == 0 || !row_active, "fg_lm_head_topk: row_active only without top-k");
+  FG_REQUIRE(kmax <= 8 || M <= 192, "fg_lm_head_topk: kmax above 8 needs M <= 192");
+  const Plan p = plan_for(N);
+  LmArgs a{};
+  a.x = x; a.ldx = ldx; a.rows = row_index; a.row_active = row_active; a.M = M; a.K = K;
+  a.w = w; a.ldw = ldw; a.N = N; a.out = out; a.ldo = ldo;
+  a.nparts = p.nparts;
+  hipStream_t s = (hipStream_t)stream;
+  if (kmax == 0) {
+    launch_san<0>(a, out_dtype, false, p.grid, s);
+    return fg::check_launch("fg_lm_head_topk");
+  }
+  const int KB = k_bucket(kmax);
+  const size_t need = (size_t)M * p.nparts * (KB * sizeof(uint64_t) + sizeof(float2));
+  FG_REQUIRE(workspace_bytes >= need, "fg_lm_head_topk: workspace too small");
+  a.part_keys = (uint64_t*)workspace;
+  a.part_lse = (float2*)(a.part_keys + (size_t)M * p.nparts * KB);
+  const bool san = sanitize != 0;
+  switch (KB) {
+    case 1: launch_san<1>(a, out_dtype, san, p.grid, s); break;
+    case 2: launch_san<2>(a, out_dtype, san, p.grid, s); break;
+    case 4: launch_san<4>(a, out_dtype, san, p.grid, s); break;
+    case 8: launch_san<8>(a, out_dtype, san, p.grid, s); break;
+    default: launch_san<16>(a, out_dtype, san, p.grid, s); break;
+  }
+  int rc = fg::check_launch("fg_lm_head_topk");
+  if (rc) return rc;
+  return fg::topk_merge_parts(KB, a.part_keys, a.part_lse, M, p.nparts, kmax, cand_tokens, cand_scores, row_stats, s);
+}
+
+}  // extern "C"

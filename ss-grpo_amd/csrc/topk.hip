@@ -17,6 +17,7 @@
 // (flashgrpo/decoding/flash_medusa_decoder.py:477-482); without it NaN ranks
 // above every number, as in torch.topk.
 #include "fg_common.h"
+#include "fg_topk.h"
 
 #include <algorithm>
 #include <climits>
@@ -24,82 +25,14 @@
 
 namespace {
 
+using fg::insert_key;
+using fg::LseAcc;
+using fg::lse_combine;
+using fg::merge_desc;
+using fg::sanitize;
+using fg::wave_merge;
+
 constexpr int kThreads = 256;
-
-template <int K>
-FG_DEVICE void insert_key(uint64_t (&top)[K], uint64_t k) {
-  if (k <= top[K - 1]) return;
-  top[K - 1] = k;
-#pragma unroll
-  for (int i = K - 1; i > 0; --i) {
-    if (top[i] > top[i - 1]) {
-      uint64_t t = top[i];
-      top[i] = top[i - 1];
-      top[i - 1] = t;
-    }
-  }
-}
-
-// Sort a bitonic sequence of K keys into descending order.
-template <int K>
-FG_DEVICE void bitonic_sort_desc(uint64_t (&v)[K]) {
-#pragma unroll
-  for (int len = K / 2; len > 0; len >>= 1) {
-#pragma unroll
-    for (int i = 0; i < K; ++i) {
-      if ((i & len) == 0) {
-        int j = i | len;
-        if (v[j] > v[i]) {
-          uint64_t t = v[i];
-          v[i] = v[j];
-          v[j] = t;
-        }
-      }
-    }
-  }
-}
-
-// top-K of two descending lists, result descending in `a`.
-template <int K>
-FG_DEVICE void merge_desc(uint64_t (&a)[K], const uint64_t (&b)[K]) {
-#pragma unroll
-  for (int i = 0; i < K; ++i) {
-    uint64_t o = b[K - 1 - i];
-    a[i] = o > a[i] ? o : a[i];
-  }
-  bitonic_sort_desc<K>(a);
-}
-
-template <int K>
-FG_DEVICE void wave_merge(uint64_t (&top)[K]) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint64_t other[K];
-#pragma unroll
-    for (int i = 0; i < K; ++i) other[i] = fg::shfl_xor_u64(top[i], o);
-    merge_desc<K>(top, other);
-  }
-}
-
-template <bool SAN>
-FG_DEVICE float sanitize(float v) {
-  if constexpr (SAN) {
-    if (v != v) return -1.0e9f;
-    if (v == INFINITY) return 1.0e9f;
-    if (v == -INFINITY) return -1.0e9f;
-  }
-  return v;
-}
-
-struct LseAcc {
-  float m, s;
-};
-
-FG_DEVICE LseAcc lse_combine(LseAcc a, LseAcc b) {
-  float m = fmaxf(a.m, b.m);
-  if (m == -INFINITY) return {m, 0.0f};
-  return {m, a.s * __expf(a.m - m) + b.s * __expf(b.m - m)};
-}
 
 template <int DT, int K, bool STATS, bool SAN>
 __global__ void __launch_bounds__(kThreads) topk_phase1(const void* __restrict__ logits, int64_t row_stride,
@@ -416,6 +349,30 @@ __global__ void __launch_bounds__(64) sparse_tree_kernel(SparseArgs a) {
 #pragma clang fp contract(on)
 
 }  // namespace
+
+namespace fg {
+int topk_merge_parts(int K, const uint64_t* part_keys, const float2* part_lse, int rows, int nparts, int kout,
+                     int32_t* cand_tokens, float* cand_scores, float* row_stats, hipStream_t s) {
+  const bool stats = row_stats != nullptr;
+#define FG_MERGE(KK)                                                                                          \
+  if (stats)                                                                                                  \
+    hipLaunchKernelGGL((topk_phase2<KK, true>), dim3(rows), dim3(64), 0, s, part_keys, part_lse, nparts, kout,  \
+                       cand_tokens, cand_scores, row_stats);                                                  \
+  else                                                                                                        \
+    hipLaunchKernelGGL((topk_phase2<KK, false>), dim3(rows), dim3(64), 0, s, part_keys, part_lse, nparts, kout, \
+                       cand_tokens, cand_scores, row_stats);
+  switch (K) {
+    case 1: FG_MERGE(1) break;
+    case 2: FG_MERGE(2) break;
+    case 4: FG_MERGE(4) break;
+    case 8: FG_MERGE(8) break;
+    case 16: FG_MERGE(16) break;
+    default: return fail("topk_merge_parts: K must be 1, 2, 4, 8 or 16");
+  }
+#undef FG_MERGE
+  return check_launch("topk merge");
+}
+}  // namespace fg
 
 extern "C" {
 

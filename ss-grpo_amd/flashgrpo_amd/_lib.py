@@ -27,6 +27,8 @@ SIGNATURES = {
     "fg_medusa_heads_workspace": (_SZ, [_I, _I, _I, _I]),
     "fg_medusa_heads": (_I, [_P, _I, _I, _I, _I64, _I, _P, _P, _F, _P, _P, _P, _I, _P, _SZ, _P]),
     "fg_lm_head": (_I, [_P, _I, _I, _I, _I64, _P, _P, _P, _I64, _I, _P, _I, _I64, _P]),
+    "fg_lm_head_topk_workspace": (_SZ, [_I, _I, _I]),
+    "fg_lm_head_topk": (_I, [_P, _I, _I, _I64, _P, _P, _P, _I64, _I, _P, _I, _I64, _I, _I, _P, _P, _P, _P, _SZ, _P]),
     "fg_medusa_topk_workspace": (_SZ, [_I, _I, _I]),
     "fg_medusa_topk": (_I, [_P, _I, _I64, _I, _I, _I, _I, _P, _P, _P, _P, _SZ, _P]),
     "fg_tree_layout": (_I, [_P, _P, _I, _I, _P, _P, _P, _I, _P, _P, _I, _P]),

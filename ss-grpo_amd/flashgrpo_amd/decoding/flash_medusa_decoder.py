@@ -305,11 +305,13 @@ class FlashMedusaDecoder:
                 # base_k without adaptation; the tree gets no nodes at this depth
                 adapted.append(base_k)
                 break
-            with timing.label("chain"):
-                lg = model.logits(states.to(model.dtype))
-            rows.append(int(lg.shape[0]))
             kq = min(max(base_k, 2 if margin else 1), V)
-            cand, score, st = K.medusa_topk(lg, kq, stats=not margin, sanitize=True)
+            with timing.label("chain"):
+                # candidates (and confidences) from the LM-head epilogue; the logits
+                # themselves only when the round is recorded
+                lg, cand, score, st = model.logits_topk(states.to(model.dtype), kq, stats=not margin, sanitize=True,
+                                                        logits=record)
+            rows.append(int(states.shape[0]))
             if margin:
                 row_conf = score[:, 0] - score[:, 1] if kq > 1 else score[:, 0]
             else:
@@ -350,6 +352,19 @@ class FlashMedusaDecoder:
         info = dict(stats={"confidence": confs_host, "topk": list(adapted)}, rows=rows, recs=recs,
                     conf=torch.stack(confs_dev).float() if confs_dev else None)
         return torch.cat(cols, dim=1).contiguous(), chain_plan, info
+
+    def _medusa_candidates(self, proj: torch.Tensor, heads: int, batch: int, kc: int, *, stats: bool,
+                           logits: bool):
+        """Per-row top-kc candidates of the proposal logits (medusa_tree.py:239-252) and,
+        with ``stats``, each row's (max, logsumexp): ``(logits or None, tokens, scores,
+        stats)``. Tied heads take them from the LM-head kernel's epilogue in one launch
+        over every head's rows; untied heads compute the logits first."""
+        own = self.medusa_heads.output_weights(self.model.dtype, self.model.device)[:heads]
+        if all(w is None for w in own):
+            return self.model.logits_topk(proj, kc, stats=stats, logits=logits)
+        mlog = self._medusa_logits(proj, heads, batch)
+        cand, score, st = K.medusa_topk(mlog, kc, stats=stats)
+        return mlog, cand, score, st
 
     def _medusa_logits(self, proj: torch.Tensor, heads: int, batch: int) -> torch.Tensor:
         """[heads*B, V] proposal logits (``flash_medusa_decoder.py:281-304``): one LM-head
@@ -462,23 +477,25 @@ class FlashMedusaDecoder:
             r.sync()
             t0 = time.time()
             proj = self.medusa_heads.project_all(r.hidden, plan.active_heads)
-            with timing.label("medusa"):
-                mlog = self._medusa_logits(proj, plan.active_heads, Bc)
+            V = self.model.cfg.vocab
             if plan.layout == "sparse_asymmetric":
                 # candidate lists of the sparse widths (adaptation only shrinks them)
-                kc = max(sparse_widths(list(plan.nodes_by_head or plan.topk_by_depth)[:3], mlog.shape[-1]))
+                kc = max(sparse_widths(list(plan.nodes_by_head or plan.topk_by_depth)[:3], V))
             else:
                 kc = max(plan.topk_by_depth)
             if cfg.adaptive_tree_enabled and cfg.adaptive_confidence_metric == "margin":
-                kc = max(kc, min(2, mlog.shape[-1]))  # margin = top-1 - top-2 (flash_medusa_decoder.py:327-331)
-            cand, score, stats = K.medusa_topk(mlog, kc, stats=bool(cfg.adaptive_tree_enabled))
+                kc = max(kc, min(2, V))  # margin = top-1 - top-2 (flash_medusa_decoder.py:327-331)
+            with timing.label("medusa"):
+                mlog, cand, score, stats = self._medusa_candidates(proj, plan.active_heads, Bc, kc,
+                                                                   stats=bool(cfg.adaptive_tree_enabled),
+                                                                   logits=trace is not None)
             r.sync()
             m["medusa_time"] += time.time() - t0
             if cfg.adaptive_tree_enabled:
                 both = torch.cat([stats.view(stats.shape[0], -1), score.view(score.shape[0], -1)], 1).cpu().numpy()
                 plan, adaptive_stats = self._adapt_plan(plan, both[:, :2], both[:, 2:], Bc)
             if plan.layout == "sparse_asymmetric" and plan.active_heads > 0:
-                sparse = sparse_tree_device(roots, cand, score, plan, Bc, mlog.shape[-1])
+                sparse = sparse_tree_device(roots, cand, score, plan, Bc, V)
         if sparse is not None:
             # per-row topology (b200 sparse_asymmetric): rows padded to the widest bound
             tree_tokens = sparse["tokens"]

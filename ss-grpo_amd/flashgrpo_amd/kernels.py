@@ -144,6 +144,53 @@ def lm_head(x, weight, *, row_index=None, row_active=None, out=None, out_dtype=N
     return out
 
 
+def lm_head_topk(x, weight, kmax=0, *, row_index=None, row_active=None, out=None, out_dtype=None,
+                 logits=True, stats=False, sanitize=False, workspace=None):
+    """Tied LM head over <= 256 rows (bf16) on the weight-streaming kernel, with the
+    per-row top-kmax candidates fused (``fg_lm_head_topk``).
+
+    Returns (logits [M, N] or None, tokens int32 [M, kmax] or None, scores fp32 [M, kmax]
+    or None, stats fp32 [M, 2] or None); the candidates and stats equal
+    ``medusa_topk(logits, kmax, stats=..., sanitize=...)`` on the bf16 logits.
+    """
+    _dev(x, weight, row_index, row_active)
+    _i32(row_index, "row_index")
+    _i32(row_active, "row_active")
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K)
+    if x2.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("lm_head_topk: x and weight must be bf16")
+    if x2.stride(1) != 1 or weight.stride(1) != 1 or weight.shape[1] != K:
+        raise ValueError("lm_head_topk: operands must be K-contiguous with matching K")
+    if (x2.numel() + x2.storage_offset()) * 2 >= 1 << 32:
+        raise ValueError("lm_head_topk: x must span less than 4 GiB")
+    M = row_index.numel() if row_index is not None else x2.shape[0]
+    N = weight.shape[0]
+    dev = x.device
+    if logits and out is None:
+        out = torch.empty(M, N, dtype=out_dtype or torch.bfloat16, device=dev)
+    elif not logits:
+        out = None
+    tok = torch.empty(M, kmax, dtype=torch.int32, device=dev) if kmax else None
+    sc = torch.empty(M, kmax, dtype=torch.float32, device=dev) if kmax else None
+    st = torch.empty(M, 2, dtype=torch.float32, device=dev) if kmax and stats else None
+    if M == 0:
+        return out, tok, sc, st
+    ws_bytes = 0
+    if kmax:
+        need = _lib.load().fg_lm_head_topk_workspace(M, N, kmax)
+        if workspace is None or workspace.numel() * workspace.element_size() < need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+        ws_bytes = workspace.numel() * workspace.element_size()
+    else:
+        workspace = None
+    _call("fg_lm_head_topk", _ptr(x2), M, K, x2.stride(0), _ptr(row_index), _ptr(row_active), _ptr(weight),
+          weight.stride(0), N, _ptr(out), dtype_code(out) if out is not None else 1,
+          out.stride(0) if out is not None else N, int(kmax), int(bool(sanitize)), _ptr(tok), _ptr(sc), _ptr(st),
+          _ptr(workspace), ws_bytes, _stream())
+    return out, tok, sc, st
+
+
 # ------------------------------------------------------------------ tree construction
 def medusa_topk(logits, kmax, *, stats=False, sanitize=False, workspace=None):
     """Top-kmax candidates per row ranked (value desc, index asc).

@@ -29,6 +29,7 @@ from ..tuning import use_tuned_gemms
 
 MAX_TREE_NODES = 64      # tree nodes per forward (64-bit ancestor masks)
 MAX_CHAIN_TOKENS = 8192  # new tokens per forward without masks (a causal chain)
+LM_STREAM_ROWS = 256  # contiguous LM-head rows up to this count run the weight-streaming kernel
 PREFILL_CHUNK = 1024     # prompt tokens per prefill forward
 
 
@@ -574,17 +575,40 @@ class TargetModel:
 
         Gathered or skippable rows (the lazy walk projection) run the fg_lm_head
         kernel, which reads only the listed rows and skips tiles with no active row.
-        Contiguous bf16 rows are a plain GEMM and go to hipBLASLt, which measured
-        faster than fg_lm_head at every row count from 96 to 2304 on MI355X.
+        Contiguous bf16 rows run the weight-streaming LM-head kernel up to 256 rows
+        (``fg_lm_head_topk``, the weight read once); larger contiguous blocks (prefill
+        sized) are a square GEMM and go to hipBLASLt.
         """
         x = hidden.reshape(-1, self.cfg.hidden)
         w = self.w["lm_head"] if weight is None else weight
         if (row_index is None and row_active is None and self.dtype == torch.bfloat16
                 and (out_dtype is None or out_dtype == self.dtype)):
+            if x.shape[0] <= LM_STREAM_ROWS and x.stride(1) == 1 and w.stride(1) == 1:
+                return K.lm_head_topk(x, w, 0, out=out)[0]
             if out is None:
                 return F.linear(x, w)
             return torch.matmul(x, w.t(), out=out)
         return K.lm_head(x, w, row_index=row_index, row_active=row_active, out=out, out_dtype=out_dtype)
+
+    def logits_topk(self, hidden: torch.Tensor, kmax: int, *, stats: bool = False, sanitize: bool = False,
+                    logits: bool = False, weight: torch.Tensor | None = None, workspace=None):
+        """LM-head rows with each row's top-kmax candidates (value desc, index asc) and
+        optionally (max, logsumexp): ``(logits or None, tokens [R, kmax], scores [R, kmax],
+        stats [R, 2] or None)``, equal to ``medusa_topk(self.logits(hidden), kmax, ...)``.
+
+        Up to 256 bf16 rows the candidates come from the LM-head kernel's epilogue
+        (``fg_lm_head_topk``) without the logits being read back; ``logits`` also returns
+        them. Other shapes compute the logits and run ``medusa_topk`` on them.
+        """
+        x = hidden.reshape(-1, self.cfg.hidden)
+        w = self.w["lm_head"] if weight is None else weight
+        R = x.shape[0]
+        if (self.dtype == torch.bfloat16 and 0 < R <= LM_STREAM_ROWS and (kmax <= 8 or R <= 192)
+                and x.stride(1) == 1 and w.stride(1) == 1 and kmax >= 1):
+            return K.lm_head_topk(x, w, kmax, logits=logits, stats=stats, sanitize=sanitize, workspace=workspace)
+        lg = self.logits(x, weight=weight)
+        tok, sc, st = K.medusa_topk(lg, kmax, stats=stats, sanitize=sanitize)
+        return (lg if logits else None), tok, sc, st
 
     def prefill(self, input_ids: torch.Tensor, cache: KVCache, *, lengths=None, chunk: int = PREFILL_CHUNK,
                 row_map: torch.Tensor | None = None, return_all: bool = False) -> torch.Tensor:
