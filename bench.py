@@ -98,6 +98,8 @@ def algorithmic_work(cfg, rnd, seq_before, elem):
     w = {
         "fg_tree_attention": dict(bytes=L * attn_bytes, flops=L * attn_flops, launches=L),
         "fg_lm_head:medusa": dict(flops=2 * nh * B * H * V, bytes=H * V * elem + nh * B * (H + V) * elem, launches=1),
+        # the same rows with the top-k in the epilogue (logits not written)
+        "fg_lm_head_topk:medusa": dict(flops=2 * nh * B * H * V, bytes=H * V * elem + nh * B * H * elem, launches=1),
         "fg_medusa_heads": dict(flops=2 * nh * B * H * H, bytes=nh * H * H * elem, launches=1),
         "fg_medusa_topk": dict(bytes=nh * B * V * elem, launches=1),
         "fg_sample_tokens": dict(bytes=B * V * elem, launches=1),
@@ -107,9 +109,11 @@ def algorithmic_work(cfg, rnd, seq_before, elem):
         # chain proposals: one LM-head launch and one top-k launch per depth over every
         # parent state; the bootstrap state is Medusa head 0 alone
         R = sum(chain)
-        del w["fg_lm_head:medusa"]
+        del w["fg_lm_head:medusa"], w["fg_lm_head_topk:medusa"]
         w["fg_lm_head:chain"] = dict(flops=2 * R * H * V, bytes=len(chain) * H * V * elem + R * (H + V) * elem,
                                      launches=len(chain))
+        w["fg_lm_head_topk:chain"] = dict(flops=2 * R * H * V, bytes=len(chain) * H * V * elem + R * H * elem,
+                                          launches=len(chain))
         w["fg_medusa_heads"] = dict(flops=2 * B * H * H, bytes=H * H * elem, launches=1)
         w["fg_medusa_topk"] = dict(bytes=R * V * elem, launches=len(chain))
     if rnd.get("lazy"):
@@ -119,6 +123,7 @@ def algorithmic_work(cfg, rnd, seq_before, elem):
         busy = int(rnd["walk_draws"].max()) if draws else 0
         w["fg_lm_head:tree"] = dict(flops=2 * draws * H * V, bytes=busy * H * V * elem + draws * (H + V) * elem,
                                     launches=D)
+        w["fg_lm_head_topk:tree"] = dict(w["fg_lm_head:tree"])
         w["fg_walk_step"] = dict(bytes=draws * V * elem, launches=D)
     else:
         M = B * I
@@ -419,6 +424,7 @@ def summarize_trace(path, top=30):
 
 # Device symbol of each C-ABI entry point whose launches the roofline can name.
 KERNEL_SYMBOLS = {"fg_tree_attention": "tree_attn_bf16_kernel", "fg_lm_head": "gemm_bf16_stream",
+                  "fg_lm_head_topk": "lm_stream_kernel",
                   "fg_sample_tokens": "split_", "fg_kv_path_gather": "kv_path_gather_kernel"}
 
 

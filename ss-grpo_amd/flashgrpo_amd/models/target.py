@@ -573,11 +573,11 @@ class TargetModel:
         row_active == 0 may be left unwritten. ``weight`` [V, H] replaces the tied LM
         head (an untied Medusa head's own output projection).
 
-        Gathered or skippable rows (the lazy walk projection) run the fg_lm_head
-        kernel, which reads only the listed rows and skips tiles with no active row.
-        Contiguous bf16 rows run the weight-streaming LM-head kernel up to 256 rows
-        (``fg_lm_head_topk``, the weight read once); larger contiguous blocks (prefill
-        sized) are a square GEMM and go to hipBLASLt.
+        Up to 256 bf16 rows, contiguous or gathered (the lazy walk's rows, skipped as a
+        whole when no row is active), run the weight-streaming LM-head kernel
+        (``fg_lm_head_topk``, the weight read once). Larger contiguous blocks (prefill
+        sized) are a square GEMM and go to hipBLASLt; larger gathered sets and fp32 run
+        ``fg_lm_head``.
         """
         x = hidden.reshape(-1, self.cfg.hidden)
         w = self.w["lm_head"] if weight is None else weight
@@ -588,6 +588,12 @@ class TargetModel:
             if out is None:
                 return F.linear(x, w)
             return torch.matmul(x, w.t(), out=out)
+        rows = row_index.numel() if row_index is not None else x.shape[0]
+        if (self.dtype == torch.bfloat16 and 0 < rows <= LM_STREAM_ROWS and x.stride(1) == 1 and w.stride(1) == 1
+                and (x.numel() + x.storage_offset()) * 2 < 1 << 32
+                and (out_dtype is None or out_dtype in (torch.bfloat16, torch.float32))):
+            return K.lm_head_topk(x, w, 0, row_index=row_index, row_active=row_active, out=out,
+                                  out_dtype=out_dtype)[0]
         return K.lm_head(x, w, row_index=row_index, row_active=row_active, out=out, out_dtype=out_dtype)
 
     def logits_topk(self, hidden: torch.Tensor, kmax: int, *, stats: bool = False, sanitize: bool = False,
