@@ -524,6 +524,65 @@ def attention_only(args, work):
                       "hbm_frac": round(byts / med / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
 
 
+def lm_head_only(args, work):
+    """The LM-head projection alone at the config's vocabulary and hidden size, for 64, 128,
+    192 and 256 bf16 rows: fg_lm_head_topk (logits only; logits + top-k; top-k without the
+    logits) against hipBLASLt (F.linear with the tuned table) and hipBLASLt + fg_medusa_topk.
+    Batches of 10 launches behind a spin kernel, alternating over two weight copies (cold
+    reads), HIP events around each batch. Prints one JSON line per row count."""
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+
+    from flashgrpo_amd import kernels as K
+    from flashgrpo_amd.models import TargetConfig
+    from flashgrpo_amd.tuning import use_tuned_gemms
+
+    use_tuned_gemms()
+    cfg = getattr(TargetConfig, work["target"])()
+    H, V = cfg.hidden, cfg.vocab
+    dev, dt = "cuda", torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(0)
+    ws = [(torch.randn(V, H, generator=g, device=dev) * 0.02).to(dt) for _ in range(2)]
+    kmax = 4
+
+    def timed(fn):
+        for i in range(4):
+            fn(i)
+        torch.cuda.synchronize()
+        evs = []
+        for _ in range(max(args.steps, 1)):
+            torch.cuda._sleep(2_000_000)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for j in range(10):
+                fn(j)
+            e1.record()
+            evs.append((e0, e1))
+        torch.cuda.synchronize()
+        return float(np.median(np.array([a.elapsed_time(b) for a, b in evs]) * 1e3 / 10))
+
+    for M in (64, 128, 192, 256):
+        x = torch.randn(M, H, generator=g, device=dev).to(dt)
+        out = torch.empty(M, V, dtype=dt, device=dev)
+        wk = torch.empty(K._lib.load().fg_lm_head_topk_workspace(M, V, kmax), dtype=torch.uint8, device=dev)
+        res = {
+            "lm_head": timed(lambda i: K.lm_head_topk(x, ws[i % 2], 0, out=out)),
+            "lm_head+topk": timed(lambda i: K.lm_head_topk(x, ws[i % 2], kmax, out=out, stats=True, workspace=wk)),
+            "topk_only": timed(lambda i: K.lm_head_topk(x, ws[i % 2], kmax, logits=False, stats=True,
+                                                        workspace=wk)),
+            "hipblaslt": timed(lambda i: F.linear(x, ws[i % 2])),
+            "hipblaslt+topk": timed(lambda i: K.medusa_topk(F.linear(x, ws[i % 2]), kmax, stats=True)),
+        }
+        byts = V * H * 2 + M * H * 2 + M * V * 2
+        print(json.dumps({"kernel": "fg_lm_head_topk", "config": args.config, "rows": M, "vocab": V, "hidden": H,
+                          "kmax": kmax, "batches": max(args.steps, 1),
+                          "us_median": {k: round(v, 1) for k, v in res.items()},
+                          "lm_head_hbm_frac": round(byts / res["lm_head"] / 1e3 / HBM_PEAK_GBS, 4),
+                          "weight_only_hbm_frac": round(V * H * 2 / res["lm_head"] / 1e3 / HBM_PEAK_GBS, 4)}),
+              flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -551,6 +610,8 @@ def main():
     ap.add_argument("--attention-only", action="store_true",
                     help="time fg_tree_attention alone at the config's verify shape (batches of 10 launches)")
     ap.add_argument("--cold", type=int, default=8, help="--attention-only: distinct K/V caches rotated over")
+    ap.add_argument("--lm-head-only", action="store_true",
+                    help="time the LM-head kernel alone against hipBLASLt at 64..256 rows and exit")
     ap.add_argument("--summarize-trace", metavar="CSV", help="summarise a rocprofv3 kernel trace of this command")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("CSV", "KERNEL"),
                     help="per-dispatch counter means of one kernel from a rocprofv3 --pmc run of this command")
@@ -577,6 +638,9 @@ def main():
     work = dict(WORKLOADS[args.config], top_p=args.top_p)
     if args.attention_only:
         attention_only(args, work)
+        return
+    if args.lm_head_only:
+        lm_head_only(args, work)
         return
     if args.warmup < 3:
         # the verify forward's HIP graph is captured on its second graph round and the last
