@@ -10,9 +10,10 @@ Replaces the Hugging Face decoder the reference drives through
   accepted path is compacted in place by ``fg_kv_path_gather``;
 * attention is ``fg_tree_attention`` (ancestor bitmask in registers) for the
   tree verify and for prefill, which runs as causal 64-token chains;
-* RMSNorm (+ residual add), rotary + cache write and SwiGLU are HIP kernels;
-  the dense projections are plain library GEMMs (``F.linear``: hipBLASLt or
-  rocBLAS, with the per-shape solution table of ``flashgrpo_amd.tuning``).
+* RMSNorm, rotary + cache write and SwiGLU are HIP kernels; the dense
+  projections are plain library GEMMs (``F.linear``: hipBLASLt or rocBLAS, with
+  the per-shape solution table of ``flashgrpo_amd.tuning``); the O and down
+  projections add into the residual stream in place (``addmm_``, beta = 1).
 """
 from __future__ import annotations
 
@@ -549,22 +550,23 @@ class TargetModel:
         x = self.w["embed"].index_select(0, tokens.reshape(-1).long())  # [T, H] residual stream
         q = self._buf("q", (B, N, cfg.q_heads, d))
         attn = self._buf("attn", (B, N, cfg.q_heads, d))
-        delta = None
         for l, lw in enumerate(self.w["layers"]):
-            h = K.rmsnorm(x, lw["input_norm"], cfg.rms_eps, delta=delta, out=self._buf("h", (T, H)))
+            h = K.rmsnorm(x, lw["input_norm"], cfg.rms_eps, out=self._buf("h", (T, H)))
             qkv = F.linear(h, lw["qkv_w"], lw["qkv_b"])
             K.rope_kv_write(qkv, batch=B, num_nodes=N, q_heads=cfg.q_heads, kv_heads=cfg.kv_heads, head_dim=d,
                             seq_len=seq_len, pos_offset=pos_offset, inv_freq=self.inv_freq, q_out=q,
                             k_cache=cache.k(l), v_cache=cache.v(l), row_map=row_map, err_flag=err_flag)
             K.tree_attention(q, cache.k(l), cache.v(l), seq_len=seq_len, anc=anc, num_nodes=N, q_heads=cfg.q_heads,
                              kv_heads=cfg.kv_heads, head_dim=d, out=attn, row_map=row_map)
-            o = F.linear(attn.view(T, cfg.q_heads * d), lw["o_w"])
-            h2 = K.rmsnorm(x, lw["post_norm"], cfg.rms_eps, delta=o, out=self._buf("h", (T, H)))
+            # residual adds inside the GEMMs (beta = 1, the residual stream updated in place):
+            # the norms then read one tensor instead of two and write one instead of two
+            x.addmm_(attn.view(T, cfg.q_heads * d), lw["o_w"].t())
+            h2 = K.rmsnorm(x, lw["post_norm"], cfg.rms_eps, out=self._buf("h", (T, H)))
             gu = F.linear(h2, lw["gate_up_w"])
             act = K.swiglu(gu, out=self._buf("act", (T, cfg.intermediate)))
-            delta = F.linear(act, lw["down_w"])
+            x.addmm_(act, lw["down_w"].t())
         out = torch.empty(T, H, dtype=self.dtype, device=self.device)
-        K.rmsnorm(x, self.w["final_norm"], cfg.rms_eps, delta=delta, out=out)
+        K.rmsnorm(x, self.w["final_norm"], cfg.rms_eps, out=out)
         return out.view(B, N, H)
 
     def logits(self, hidden: torch.Tensor, *, row_index=None, row_active=None, out=None, out_dtype=None,
