@@ -210,7 +210,8 @@ class _PlantedAcceptance:
     samples from gets +60 on the token of the first child of the node it belongs to (a
     few small torch launches per walk step, counted in the rounds' time), through the
     kernels module the decoder calls: fg_walk_step's step rows (lazy LM head) and
-    fg_accept_walk's packed internal-node rows."""
+    fg_accept_walk's packed internal-node rows. Planted walk steps take the rows' maxima
+    from the planted logits (the chunk-maxima launch) instead of the LM head's."""
 
     def __init__(self):
         from flashgrpo_amd import kernels as K
@@ -229,6 +230,9 @@ class _PlantedAcceptance:
             return tree_tokens.gather(1, child[:, None].long()).squeeze(1).long(), m.any(1)
 
         def planted_walk_step(walk, step_logits, tree_tokens, parents, n_nodes, **kw):
+            # the planted logits no longer match the row maxima the LM head wrote with them:
+            # the step takes its chunk maxima from the logits (one launch more)
+            kw.pop("parts", None)
             B = tree_tokens.shape[0]
             cur, active = walk["state"][:B], walk["state"][B:2 * B] != 0
             tok, has = first_child_tokens(tree_tokens, parents, cur)

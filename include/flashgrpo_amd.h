@@ -71,13 +71,19 @@ int fg_lm_head(const void* x, int dtype, int M, int K, int64_t ldx, const int32_
  * [M, 2], ranked and computed exactly as fg_medusa_topk does on the bf16 logits (sanitize
  * as there), without reading the logits back; workspace >=
  * fg_lm_head_topk_workspace(M, N, kmax). row_active (kmax 0 only): nothing is computed
- * when every flag is 0. Replaces decoding/flash_medusa_decoder.py:289-294 (Medusa rows),
+ * when every flag is 0. part_max / part_key (optional; kmax 0 with out): each workgroup
+ * writes, for every row m, the maximum of the row's stored logits over its columns (NaN
+ * ignored) to part_max[m * P + p] and their largest rank key (value desc, index asc,
+ * NaN first: the first maximum) to part_key[m * P + p], P = fg_lm_head_topk_parts(N):
+ * the row maxima fg_walk_step needs before it can weigh the logits.
+ * Replaces decoding/flash_medusa_decoder.py:289-294 (Medusa rows),
  * :1079-1091 (leaf / next-round rows) and the torch.topk of medusa_tree.py:239-252. */
 size_t fg_lm_head_topk_workspace(int rows, int vocab, int kmax);
+int fg_lm_head_topk_parts(int vocab);
 int fg_lm_head_topk(const void* x, int M, int K, int64_t ldx, const int32_t* row_index, const int32_t* row_active,
                     const void* w, int64_t ldw, int N, void* out, int out_dtype, int64_t ldo, int kmax, int sanitize,
-                    int32_t* cand_tokens, float* cand_scores, float* row_stats, void* workspace,
-                    size_t workspace_bytes, void* stream);
+                    int32_t* cand_tokens, float* cand_scores, float* row_stats, float* part_max, uint64_t* part_key,
+                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* Per-row top-kmax candidates, ranked (value desc, index asc).
  * logits [rows, vocab] with row stride row_stride (multiple of 8, 32-byte aligned base).
@@ -206,7 +212,11 @@ int fg_accept_walk(const void* tree_logits, int dtype, int64_t row_stride, int v
  *   fg_walk_step   -- draw for every active row b from row b of step_logits
  *                     (noise column noise_col0 + walk_step, counter draw draw0 + walk_step).
  * After the walk, state[2*batch + b] is the step whose logits row b last sampled (-1: none).
- * fg_walk_step's workspace is optional, as for fg_sample_tokens (rows = batch). */
+ * fg_walk_step's workspace is optional, as for fg_sample_tokens (rows = batch). With a
+ * workspace, an unrestricted or greedy step whose row maxima parts are given (part_max /
+ * part_key [batch, nparts], as fg_lm_head_topk writes them with the step's logits) skips
+ * the chunk-maxima launch. next_row_index / next_row_active (optional): the step also writes the next
+ * step's rows, as fg_walk_rows would (rows that are already inactive keep their entries). */
 int fg_walk_begin(const int32_t* tree_tokens, const int32_t* parents, const int32_t* n_nodes, int nmax, int batch,
                   int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
                   int32_t* correction, int32_t* state, void* stream);
@@ -216,8 +226,9 @@ int fg_walk_step(const void* step_logits, int dtype, int64_t row_stride, int voc
                  const uint32_t* noise, int noise_stride, int noise_col0, uint64_t seed, uint64_t step,
                  const int32_t* seq_ids, int draw0, float temperature, int greedy, int top_k, uint32_t top_p_fixed,
                  int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
-                 int32_t* correction, int32_t* state, int32_t* err_flag, void* workspace, size_t workspace_bytes,
-                 void* stream);
+                 int32_t* correction, int32_t* state, int32_t* err_flag, const float* part_max,
+                 const uint64_t* part_key, int nparts, int32_t* next_row_index, int32_t* next_row_active,
+                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* Length clamp (max(1, max_length - old_len)), EOS cut (eos_token_id < 0: none),
  * finished flags and, when pending_root != NULL, the next round's forced root

@@ -122,9 +122,10 @@ FG_DEVICE float rank_key_value(uint64_t k) {
 // single/expf.c), evaluated with separately rounded multiplies and adds so that
 // the CPU oracle (numpy float32) reproduces every bit. Inputs below -64 (and
 // NaN) give 0.
-FG_DEVICE float exp_fg(float t) {
+//
+// exp_fg_core: the evaluation itself, for -64 <= t <= 0.
+FG_DEVICE float exp_fg_core(float t) {
 #pragma clang fp contract(off)
-  if (!(t >= -64.0f)) return 0.0f;
   float kf = rintf(t * 1.44269504088896341f);
   float r = t - kf * 0.693359375f;
   r = r - kf * -2.12194440e-4f;
@@ -148,16 +149,41 @@ FG_DEVICE float exp_fg(float t) {
   return y * scale;
 }
 
-// trunc(e * 2^40) as uint64, by exponent/mantissa arithmetic (exact).
+// Branch-free: the polynomial runs on max(t, -64) and the result is selected.
+FG_DEVICE float exp_fg(float t) {
+  const bool in = t >= -64.0f;
+  const float e = exp_fg_core(in ? t : -64.0f);
+  return in ? e : 0.0f;
+}
+
+// trunc(e * 2^40) as uint64 for 0 <= e < 2^23, by exponent/mantissa arithmetic (exact).
+// Branch-free: zero (exponent field 0; exp_fg never returns subnormals) and values
+// below 2^-40 shift the 24-bit significand out entirely.
 FG_DEVICE uint64_t quantize_q40(float e) {
-  uint32_t b = __float_as_uint(e);
-  int ex = (int)((b >> 23) & 0xff);
-  if (ex == 0) return 0;  // zero (exp_fg never returns subnormals)
-  uint64_t m = (uint64_t)((b & 0x7fffffu) | 0x800000u);
-  int sh = ex - 127 + 40 - 23;  // value = m * 2^sh
-  if (sh >= 0) return m << sh;
-  if (sh <= -24) return 0;
-  return m >> (-sh);
+  const uint32_t b = __float_as_uint(e);
+  const int ex = (int)((b >> 23) & 0xff);
+  const uint64_t m = (uint64_t)((b & 0x7fffffu) | 0x800000u);
+  const int sh = ex - 127 + 40 - 23;  // value = m * 2^sh
+  const uint64_t up = m << (sh > 0 ? sh : 0);
+  const uint64_t down = m >> (sh < 0 ? (-sh < 63 ? -sh : 63) : 0);
+  return sh >= 0 ? up : down;
+}
+
+// The sampling weight quantize_q40(exp_fg(t)) of t = s - max s (t <= 0, or NaN), in fewer
+// operations: t is clamped to -64 (exp_fg(-64) * 2^40 < 1, so below -64 and NaN still
+// give 0), and for 0 <= e <= 1 the float v = e * 2^40 is cut into 32-bit halves, each
+// converted with truncation: hi = trunc(v * 2^-32) and lo = trunc(v - hi * 2^32), where
+// the scalings are exact and the subtraction is exact (v's ulp is at least 2^9 once
+// v >= 2^32). The split equals quantize_q40(e) for every float e in [0, 1] (checked
+// exhaustively over those 1,065,353,217 values).
+FG_DEVICE uint64_t weight_q40(float t) {
+#pragma clang fp contract(off)
+  const float e = exp_fg_core(fmaxf(t, -64.0f));
+  const float v = e * 1099511627776.0f;          // 2^40
+  const float h = v * 2.3283064365386963e-10f;   // 2^-32
+  const uint32_t hi = (uint32_t)h;
+  const float lo = v - (float)hi * 4294967296.0f;
+  return ((uint64_t)hi << 32) | (uint64_t)(uint32_t)lo;
 }
 
 // floor(a * u / 2^32) for a < 2^64, u < 2^32.

@@ -19,7 +19,10 @@
 // The weight is read exactly once; the activations (<= 1.8 MB) are re-read from L2 per
 // block round.
 //
-// Epilogue of a block round: the logits are written (optional), and with top-k the
+// Epilogue of a block round: the logits are written (optional); without top-k, each row's
+// maximum and first maximum over the workgroup's columns can be kept (part_max / part_key,
+// one part per workgroup: the row maxima a sampler needs before it can weigh the logits);
+// with top-k the
 // workgroup's 256 columns x M rows are rounded to bf16 (the values the reference ranks)
 // and placed in LDS, where each row's running top-K and (max, sum exp) over the
 // workgroup's columns are updated. At the end every workgroup writes its part of each
@@ -67,11 +70,14 @@ struct LmArgs {
   int64_t ldo;
   uint64_t* part_keys;  // [M, nparts, KT]
   float2* part_lse;     // [M, nparts]
+  float* part_max;      // [M, nparts] (PM): max of the stored logits, NaN ignored
+  uint64_t* part_key;   // [M, nparts] (PM): largest rank key (the first maximum, NaN first)
   int nparts;  // = grid: one part per workgroup
 };
 
-template <int MI, int CDT, int KT, bool SAN>
+template <int MI, int CDT, int KT, bool SAN, bool PM>
 __global__ void __launch_bounds__(kWaves * 64, 1) lm_stream_kernel(LmArgs a) {
+  static_assert(!PM || KT == 0, "row maxima parts come with the logits-only epilogue");
   constexpr int kDist = dist_for(MI), kStages = kDist + 1;
   constexpr int MP = MI * 32;
   constexpr int STAGE = MP * 128;
@@ -168,6 +174,14 @@ __global__ void __launch_bounds__(kWaves * 64, 1) lm_stream_kernel(LmArgs a) {
   uint32_t foff[4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) foff[kk] = (uint32_t)(l32 * 128 + a_pos(l32, g * 4 + kk) * 16);
+  // PM: running maximum and best rank key of row 32 i + l32 over this lane's columns
+  float pm_max[PM ? MI : 1];
+  uint64_t pm_key[PM ? MI : 1];
+#pragma unroll
+  for (int i = 0; i < (PM ? MI : 1); ++i) {
+    pm_max[i] = -INFINITY;
+    pm_key[i] = 0;
+  }
 
   for (int rd = 0; rd < rounds; ++rd) {
     // Every wave issues the same loads every k-step, so the waits below are static: a wave
@@ -262,6 +276,24 @@ __global__ void __launch_bounds__(kWaves * 64, 1) lm_stream_kernel(LmArgs a) {
         }
       }
     }
+    if constexpr (PM) {
+      // over the values as stored (rounded to bf16 for a bf16 output)
+      if (active) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int n = n0 + (v >> 2) * 8 + g * 4 + (v & 3);
+            if (n < a.N) {
+              const float val = CDT == fg::kBF16 ? fg::bf16_to_f32(fg::f32_to_bf16(acc[i][v])) : acc[i][v];
+              pm_max[i] = fmaxf(pm_max[i], val);
+              const uint64_t k = fg::rank_key(val, (uint32_t)n);
+              pm_key[i] = k > pm_key[i] ? k : pm_key[i];
+            }
+          }
+        }
+      }
+    }
     if constexpr (KT > 0) {
       // this round's logits (bf16) into LDS: tile[m][32 wave + c], rows of kTileRow bytes
       __syncthreads();  // every wave is done reading the activation stages
@@ -344,6 +376,34 @@ __global__ void __launch_bounds__(kWaves * 64, 1) lm_stream_kernel(LmArgs a) {
       __syncthreads();  // the tile is read before the next round's activation loads land
     }
   }
+  if constexpr (PM) {
+    // lane groups 0 and 1 hold the same rows; then the waves' maxima meet in LDS
+    __syncthreads();  // every wave is done with the activation stages
+    float* s_pmax = (float*)smem;                              // [kWaves][MP]
+    uint64_t* s_pkey = (uint64_t*)(smem + kWaves * MP * 4);   // [kWaves][MP]
+    static_assert(kWaves * MP * 12 <= kStages * STAGE, "row maxima staging");
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const float mo = __shfl_xor(pm_max[i], 32, 64);
+      const uint64_t ko = fg::shfl_xor_u64(pm_key[i], 32);
+      if (g == 0) {
+        s_pmax[wave * MP + i * 32 + l32] = fmaxf(pm_max[i], mo);
+        s_pkey[wave * MP + i * 32 + l32] = ko > pm_key[i] ? ko : pm_key[i];
+      }
+    }
+    __syncthreads();
+    for (int m = tid; m < a.M; m += kWaves * 64) {
+      float mx = s_pmax[m];
+      uint64_t k = s_pkey[m];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) {
+        mx = fmaxf(mx, s_pmax[w * MP + m]);
+        k = s_pkey[w * MP + m] > k ? s_pkey[w * MP + m] : k;
+      }
+      a.part_max[(int64_t)m * a.nparts + blockIdx.x] = mx;
+      a.part_key[(int64_t)m * a.nparts + blockIdx.x] = k;
+    }
+  }
   if constexpr (KT > 0) {
     // this workgroup's part of every row
     for (int m = tid; m < a.M; m += kWaves * 64) {
@@ -380,16 +440,16 @@ Plan plan_for(int N) {
 }
 int k_bucket(int kmax) { return kmax <= 1 ? 1 : kmax <= 2 ? 2 : kmax <= 4 ? 4 : kmax <= 8 ? 8 : 16; }
 
-template <int MI, int CDT, int KT, bool SAN>
+template <int MI, int CDT, int KT, bool SAN, bool PM>
 void launch_mi(const LmArgs& a, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((lm_stream_kernel<MI, CDT, KT, SAN>), dim3(grid), dim3(kWaves * 64), 0, s, a);
+  hipLaunchKernelGGL((lm_stream_kernel<MI, CDT, KT, SAN, PM>), dim3(grid), dim3(kWaves * 64), 0, s, a);
 }
-template <int CDT, int KT, bool SAN>
+template <int CDT, int KT, bool SAN, bool PM = false>
 void launch_rows(const LmArgs& a, int grid, hipStream_t s) {
-  if (a.M <= 64) launch_mi<2, CDT, KT, SAN>(a, grid, s);
-  else if (a.M <= 128) launch_mi<4, CDT, KT, SAN>(a, grid, s);
-  else if (a.M <= 192) launch_mi<6, CDT, KT, SAN>(a, grid, s);
-  else if constexpr (KT <= 8) launch_mi<8, CDT, KT, SAN>(a, grid, s);  // (LDS: the host rejects KT 16 here)
+  if (a.M <= 64) launch_mi<2, CDT, KT, SAN, PM>(a, grid, s);
+  else if (a.M <= 128) launch_mi<4, CDT, KT, SAN, PM>(a, grid, s);
+  else if (a.M <= 192) launch_mi<6, CDT, KT, SAN, PM>(a, grid, s);
+  else if constexpr (KT <= 8) launch_mi<8, CDT, KT, SAN, PM>(a, grid, s);  // (LDS: the host rejects KT 16 here)
 }
 template <int KT, bool SAN>
 void launch_cdt(const LmArgs& a, int out_dtype, int grid, hipStream_t s) {
@@ -406,6 +466,8 @@ void launch_san(const LmArgs& a, int out_dtype, bool san, int grid, hipStream_t 
 
 extern "C" {
 
+int fg_lm_head_topk_parts(int vocab) { return vocab > 0 ? plan_for(vocab).nparts : 0; }
+
 size_t fg_lm_head_topk_workspace(int rows, int vocab, int kmax) {
   if (rows <= 0 || vocab <= 0 || kmax <= 0) return 256;
   const Plan p = plan_for(vocab);
@@ -414,8 +476,8 @@ size_t fg_lm_head_topk_workspace(int rows, int vocab, int kmax) {
 
 int fg_lm_head_topk(const void* x, int M, int K, int64_t ldx, const int32_t* row_index, const int32_t* row_active,
                     const void* w, int64_t ldw, int N, void* out, int out_dtype, int64_t ldo, int kmax, int sanitize,
-                    int32_t* cand_tokens, float* cand_scores, float* row_stats, void* workspace,
-                    size_t workspace_bytes, void* stream) {
+                    int32_t* cand_tokens, float* cand_scores, float* row_stats, float* part_max,
+                    uint64_t* part_key, void* workspace, size_t workspace_bytes, void* stream) {
   FG_REQUIRE(x && w, "fg_lm_head_topk: null pointer");
   FG_REQUIRE(M >= 1 && M <= 256, "fg_lm_head_topk: M must be in [1, 256]");
   FG_REQUIRE(N >= 1 && K >= kKS && K % kKS == 0, "fg_lm_head_topk: K must be a positive multiple of 64");
@@ -430,12 +492,21 @@ int fg_lm_head_topk(const void* x, int M, int K, int64_t ldx, const int32_t* row
   FG_REQUIRE(kmax == 0 || (cand_tokens && cand_scores && workspace), "fg_lm_head_topk: candidate outputs missing");
   FG_REQUIRE(kmax == 0 || !row_active, "fg_lm_head_topk: row_active only without top-k");
   FG_REQUIRE(kmax <= 8 || M <= 192, "fg_lm_head_topk: kmax above 8 needs M <= 192");
+  FG_REQUIRE(!part_max == !part_key, "fg_lm_head_topk: part_max and part_key go together");
+  FG_REQUIRE(!part_max || (kmax == 0 && out), "fg_lm_head_topk: row maxima parts need out and kmax 0");
   const Plan p = plan_for(N);
   LmArgs a{};
   a.x = x; a.ldx = ldx; a.rows = row_index; a.row_active = row_active; a.M = M; a.K = K;
   a.w = w; a.ldw = ldw; a.N = N; a.out = out; a.ldo = ldo;
   a.nparts = p.nparts;
   hipStream_t s = (hipStream_t)stream;
+  if (kmax == 0 && part_max) {
+    a.part_max = part_max;
+    a.part_key = part_key;
+    if (out_dtype == fg::kF32) launch_rows<fg::kF32, 0, false, true>(a, p.grid, s);
+    else launch_rows<fg::kBF16, 0, false, true>(a, p.grid, s);
+    return fg::check_launch("fg_lm_head_topk");
+  }
   if (kmax == 0) {
     launch_san<0>(a, out_dtype, false, p.grid, s);
     return fg::check_launch("fg_lm_head_topk");

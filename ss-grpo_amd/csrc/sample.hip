@@ -13,9 +13,10 @@
 // Integer sums make every result independent of reduction order.
 //
 // Unrestricted and greedy draws with a workspace run split over 16 chunks per
-// row (three launches, see "split sampling"), top-p draws without top-k too
-// (seven launches, see "split top-p"). Otherwise: one 1024-thread workgroup per
-// sampled row. The row is split into 16
+// row (chunk maxima, then one draw launch; a walk step whose row maxima come from
+// the LM head's epilogue is the draw launch alone, see "split sampling"), top-p
+// draws without top-k over seven launches (see "split top-p"). Otherwise: one
+// 1024-thread workgroup per sampled row. The row is split into 16
 // contiguous wave segments; a wave walks its segment 512 elements (8 per lane,
 // 16-byte loads) per step. Top-k / top-p use an MSB-first 4 x 8-bit radix
 // select over the keys with count or q-weighted histograms in LDS.
@@ -58,7 +59,7 @@ struct Row {
     return n < 0 ? 0 : n;
   }
   FG_DEVICE float scaled(float x) const { return scale ? __fdiv_rn(x, T) : x; }
-  FG_DEVICE uint64_t weight(float s) const { return fg::quantize_q40(fg::exp_fg(s - m)); }
+  FG_DEVICE uint64_t weight(float s) const { return fg::weight_q40(s - m); }
 };
 
 // Candidate-set predicate: key > kappa, or key == kappa and index <= last.
@@ -350,10 +351,13 @@ __global__ void walk_rows_kernel(const int32_t* __restrict__ state, int batch, i
 }
 
 // Walk update of tree b after its draw `tok` at `parent` (one thread).
+// next_rows / next_active (optional): the LM-head rows of the next walk step of tree b,
+// as walk_rows_kernel would write them.
 FG_DEVICE void walk_apply(int b, int tok, int parent, const int32_t* tree_tokens, const int32_t* parents,
                           const int32_t* n_nodes, int nmax, int batch, int walk_step, int32_t* acc_tokens,
                           int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
-                          int32_t* correction, int32_t* state, int32_t* err_flag) {
+                          int32_t* correction, int32_t* state, int32_t* err_flag, int32_t* next_rows = nullptr,
+                          int32_t* next_active = nullptr) {
   state[2 * batch + b] = walk_step;
   const int nn = n_nodes[b];
   const int32_t* pb = parents + (int64_t)b * nmax;
@@ -382,6 +386,10 @@ FG_DEVICE void walk_apply(int b, int tok, int parent, const int32_t* tree_tokens
     for (int c = match + 1; c < nn; ++c) has_child |= pb[c] == match;
     state[batch + b] = has_child;
   }
+  if (next_rows) {
+    next_rows[b] = b * nmax + state[b];
+    next_active[b] = state[batch + b];
+  }
 }
 
 template <int DT>
@@ -391,7 +399,7 @@ __global__ void __launch_bounds__(kThreads) walk_step_kernel(
     int nmax, int batch, int walk_step, int rows_by_batch, const uint32_t* __restrict__ noise, int noise_stride,
     int noise_col0, uint64_t seed, uint64_t step, const int32_t* __restrict__ seq_ids, int draw0, SampleParams sp,
     int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
-    int32_t* correction, int32_t* state, int32_t* err_flag) {
+    int32_t* correction, int32_t* state, int32_t* err_flag, int32_t* next_rows, int32_t* next_active) {
   __shared__ Shared sh;
   const int b = blockIdx.x;
   if (!state[batch + b]) return;
@@ -403,6 +411,7 @@ __global__ void __launch_bounds__(kThreads) walk_step_kernel(
     if (threadIdx.x == 0) {
       if (err_flag) atomicOr(err_flag, 2);
       state[batch + b] = 0;
+      if (next_active) next_active[b] = 0;
     }
     return;
   }
@@ -413,17 +422,23 @@ __global__ void __launch_bounds__(kThreads) walk_step_kernel(
   int tok = block_sample<DT>(rowp, vocab, sp, u, sh);
   if (threadIdx.x == 0)
     walk_apply(b, tok, parent, tree_tokens, parents, n_nodes, nmax, batch, walk_step, acc_tokens, acc_nodes, acc_stride,
-               acc_len, last_node, correction, state, err_flag);
+               acc_len, last_node, correction, state, err_flag, next_rows, next_active);
 }
 
 // ------------------------------------------------------------------ split sampling
 // Unrestricted draws (no top-k / top-p) and greedy draws spread one row over
-// kSplitChunks workgroups instead of one: (1) per chunk, the raw maximum and the
-// first-maximum rank key; (2) per chunk, the q-mass sum against the row maximum;
-// (3) per row, the chunk whose running mass crosses the target, then the index
-// inside it -- the same integer rule as block_sample, so the token is identical.
+// kSplitChunks workgroups instead of one. The row maximum and its first maximum
+// come as parts: per-chunk parts of split_max_kernel, or the per-workgroup parts
+// the LM head writes with the logits (fg_lm_head_topk's row maxima). Then (1) per
+// chunk, the q-mass against the row maximum (split_sum_kernel); (2) per row, the
+// chunk whose running mass crosses the target and the index inside it
+// (split_pick_kernel) -- the same integer rule as block_sample, so the token is
+// identical. Greedy draws need only the parts and the pick. The chunk sums are
+// handed over at a launch boundary: a device-scope fence per workgroup to hand
+// them over inside one launch measured slower than the second launch.
 constexpr int kSplitChunks = 16;
 constexpr int kSplitThreads = 256;
+constexpr int kSplitWaves = kSplitThreads / 64;
 
 struct SplitArgs {
   const void* logits;
@@ -439,6 +454,13 @@ struct SplitArgs {
   float* part_max;           // [rows, kSplitChunks]
   uint64_t* part_key;
   uint64_t* part_sum;
+  float* row_m;              // [rows] scaled row maximum (sum launch -> pick launch)
+  uint64_t* row_best;        // [rows] first maximum's rank key
+  // row maxima parts read by the draw launch: [rows, src_stride], src_parts used
+  const float* src_max;
+  const uint64_t* src_key;
+  int src_parts;
+  int64_t src_stride;
   // split top-p (see "split top-p")
   uint32_t tp32;
   uint64_t* hist;            // [rows, kSplitChunks, 256] chunk histograms of one radix level
@@ -464,31 +486,50 @@ FG_DEVICE bool split_skip(const SplitArgs& a, int r) {
   return (a.forced && a.forced[r] >= 0) || (a.active && !a.active[r]);
 }
 
+// Elements per workgroup pass: kSplitLoads groups of 8 per thread, all loads in flight
+// before the weights are computed.
+constexpr int kSplitLoads = 4;
+constexpr int kSplitPass = kSplitThreads * 8 * kSplitLoads;
+
+// Loads elements i0 .. i0 + 7 of a chunk ending at hi; past hi come -inf, whose weight is
+// 0 against any row maximum, so the weights need no per-element test.
+template <int DT>
+FG_DEVICE void split_load8(const char* p, int i0, int hi, float (&x)[8]) {
+  if (i0 + 8 <= hi) {
+    fg::load8<DT>(p, i0, x);
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) x[j] = i0 + j < hi ? fg::load_elem<DT>(p, i0 + j) : -INFINITY;
+}
+
+// Chunk maxima (raw maximum, NaN ignored, and the first-maximum rank key).
 template <int DT>
 __global__ void __launch_bounds__(kSplitThreads) split_max_kernel(SplitArgs a) {
   const int c = blockIdx.x, r = blockIdx.y;
   if (split_skip(a, r)) return;
-  __shared__ float smax[kSplitThreads / 64];
-  __shared__ uint64_t skey[kSplitThreads / 64];
+  __shared__ float smax[kSplitWaves];
+  __shared__ uint64_t skey[kSplitWaves];
   const char* p = split_row<DT>(a, r);
   const int lo = c * a.chunk, hi = min(a.vocab, lo + a.chunk);
   float mx = -INFINITY;
   uint64_t best = 0;
-  for (int i0 = lo + threadIdx.x * 8; i0 < hi; i0 += kSplitThreads * 8) {
-    float x[8];
-    if (i0 + 8 <= hi) {
-      fg::load8<DT>(p, i0, x);
-    } else {
+  for (int base = lo; base < hi; base += kSplitPass) {
+    float x[kSplitLoads][8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) x[j] = i0 + j < hi ? fg::load_elem<DT>(p, i0 + j) : -INFINITY;
-    }
+    for (int u = 0; u < kSplitLoads; ++u) split_load8<DT>(p, base + (u * kSplitThreads + threadIdx.x) * 8, hi, x[u]);
+    // the -inf padding past hi never wins: a real element's key is at least as large
+    // and its index smaller
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (i0 + j < hi) {
-        mx = fmaxf(mx, x[j]);
-        uint64_t k = ((uint64_t)fg::sort_key32(x[j]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)(i0 + j));
+    for (int u = 0; u < kSplitLoads; ++u) {
+      const int i0 = base + (u * kSplitThreads + threadIdx.x) * 8;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        mx = fmaxf(mx, x[u][j]);
+        const uint64_t k = fg::rank_key(x[u][j], (uint32_t)(i0 + j));
         best = k > best ? k : best;
       }
+    }
   }
   mx = fg::wave_max(mx);
   best = fg::wave_max_u64(best);
@@ -500,7 +541,7 @@ __global__ void __launch_bounds__(kSplitThreads) split_max_kernel(SplitArgs a) {
   __syncthreads();
   if (threadIdx.x == 0) {
 #pragma unroll
-    for (int w = 1; w < kSplitThreads / 64; ++w) {
+    for (int w = 1; w < kSplitWaves; ++w) {
       mx = fmaxf(mx, smax[w]);
       best = skey[w] > best ? skey[w] : best;
     }
@@ -516,112 +557,234 @@ FG_DEVICE float split_row_max(const SplitArgs& a, int r) {
   return a.scale ? __fdiv_rn(mx, a.temperature) : mx;
 }
 
-template <int DT>
-__global__ void __launch_bounds__(kSplitThreads) split_sum_kernel(SplitArgs a) {
-  const int c = blockIdx.x, r = blockIdx.y;
-  if (a.greedy || split_skip(a, r)) return;
-  __shared__ uint64_t ssum[kSplitThreads / 64];
-  const char* p = split_row<DT>(a, r);
-  const float m = split_row_max(a, r);
-  const int lo = c * a.chunk, hi = min(a.vocab, lo + a.chunk);
-  uint64_t acc = 0;
-  for (int i0 = lo + threadIdx.x * 8; i0 < hi; i0 += kSplitThreads * 8) {
-    float x[8];
-    if (i0 + 8 <= hi) {
-      fg::load8<DT>(p, i0, x);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) x[j] = i0 + j < hi ? fg::load_elem<DT>(p, i0 + j) : 0.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (i0 + j < hi) {
-        const float sv = a.scale ? __fdiv_rn(x[j], a.temperature) : x[j];
-        acc += fg::quantize_q40(fg::exp_fg(sv - m));
-      }
-  }
-  acc = fg::wave_sum_u64(acc);
-  if ((threadIdx.x & 63) == 0) ssum[threadIdx.x >> 6] = acc;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint64_t t = 0;
-#pragma unroll
-    for (int w = 0; w < kSplitThreads / 64; ++w) t += ssum[w];
-    a.part_sum[r * kSplitChunks + c] = t;
-  }
+// q weight of raw logit x against the scaled row maximum m.
+template <bool SCALE>
+FG_DEVICE uint64_t split_weight(float x, float T, float m) {
+  const float sv = SCALE ? __fdiv_rn(x, T) : x;
+  return fg::weight_q40(sv - m);
 }
 
-// The token of row r from the chunk partials (whole block; every thread returns it).
-template <int DT>
-FG_DEVICE int split_pick(const SplitArgs& a, int r, uint32_t u, Shared& sh) {
-  uint64_t best = 0;
-  for (int c = 0; c < kSplitChunks; ++c) {
-    uint64_t k = a.part_key[r * kSplitChunks + c];
+template <bool SCALE>
+FG_DEVICE uint64_t split_weight8(const float (&x)[8], float T, float m) {
+  uint64_t acc = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc += split_weight<SCALE>(x[j], T, m);
+  return acc;
+}
+
+// Per row: the raw maximum and first maximum from the row's parts (whole block).
+FG_DEVICE void split_parts_max(const SplitArgs& a, int r, float* smax, uint64_t* skey, float& mx, uint64_t& best) {
+  const int tid = threadIdx.x;
+  mx = -INFINITY;
+  best = 0;
+  for (int q = tid; q < a.src_parts; q += kSplitThreads) {
+    mx = fmaxf(mx, a.src_max[r * a.src_stride + q]);
+    const uint64_t k = a.src_key[r * a.src_stride + q];
     best = k > best ? k : best;
   }
-  if (a.greedy) return (int)fg::rank_key_index(best);
-  uint64_t total = 0;
-  for (int c = 0; c < kSplitChunks; ++c) total += a.part_sum[r * kSplitChunks + c];
-  if (total == 0) return (int)fg::rank_key_index(best);
-  const uint64_t target = fg::mulhi_u64_u32(total, u);
-  uint64_t before = 0;
-  int cs = kSplitChunks - 1;
-  for (int c = 0; c < kSplitChunks; ++c) {
-    const uint64_t ps = a.part_sum[r * kSplitChunks + c];
-    if (before + ps > target) {
-      cs = c;
+  mx = fg::wave_max(mx);
+  best = fg::wave_max_u64(best);
+  if ((tid & 63) == 0) {
+    smax[tid >> 6] = mx;
+    skey[tid >> 6] = best;
+  }
+  __syncthreads();
+  mx = smax[0];
+  best = skey[0];
+#pragma unroll
+  for (int w = 1; w < kSplitWaves; ++w) {
+    mx = fmaxf(mx, smax[w]);
+    best = skey[w] > best ? skey[w] : best;
+  }
+}
+
+// q-mass of each chunk against the row maximum taken from the row's parts; chunk 0 also
+// keeps the scaled maximum and the first maximum for the pick launch.
+template <int DT, bool SCALE>
+__global__ void __launch_bounds__(kSplitThreads) split_sum_kernel(SplitArgs a) {
+  const int c = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
+  if (split_skip(a, r)) return;
+  __shared__ float smax[kSplitWaves];
+  __shared__ uint64_t skey[kSplitWaves];
+  __shared__ uint64_t ssum[kSplitWaves];
+  const char* p = split_row<DT>(a, r);
+  const int lo = c * a.chunk, hi = min(a.vocab, lo + a.chunk);
+  // the first pass's logits are in flight while the row maximum is gathered from the parts
+  float x[kSplitLoads][8];
+#pragma unroll
+  for (int u = 0; u < kSplitLoads; ++u) split_load8<DT>(p, lo + (u * kSplitThreads + tid) * 8, hi, x[u]);
+  float mx;
+  uint64_t best;
+  split_parts_max(a, r, smax, skey, mx, best);
+  const float m = SCALE ? __fdiv_rn(mx, a.temperature) : mx;
+  uint64_t acc = 0;
+  for (int base = lo; base < hi; base += kSplitPass) {
+    if (base != lo) {
+#pragma unroll
+      for (int u = 0; u < kSplitLoads; ++u) split_load8<DT>(p, base + (u * kSplitThreads + tid) * 8, hi, x[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kSplitLoads; ++u) acc += split_weight8<SCALE>(x[u], a.temperature, m);
+  }
+  acc = fg::wave_sum_u64(acc);
+  if ((tid & 63) == 0) ssum[tid >> 6] = acc;
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t t = 0;
+#pragma unroll
+    for (int w = 0; w < kSplitWaves; ++w) t += ssum[w];
+    a.part_sum[r * kSplitChunks + c] = t;
+    if (c == 0) {
+      a.row_m[r] = m;
+      a.row_best[r] = best;
+    }
+  }
+}
+
+// First index in [lo, hi) whose inclusive running q-mass exceeds target (the whole
+// block; -1 if none), kSplitPass elements per step, scanned in index order.
+template <int DT, bool SCALE>
+FG_DEVICE int split_locate(const SplitArgs& a, const char* p, int lo, int hi, float m, uint64_t target,
+                           uint64_t* wsum, int* found) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) *found = -1;
+  uint64_t run = 0;  // block-uniform
+  for (int base = lo; base < hi; base += kSplitPass) {
+    // thread t holds the kSplitLoads * 8 consecutive elements base + t * 8 * kSplitLoads ...
+    float x[kSplitLoads][8];
+#pragma unroll
+    for (int u = 0; u < kSplitLoads; ++u) split_load8<DT>(p, base + (tid * kSplitLoads + u) * 8, hi, x[u]);
+    uint64_t wu[kSplitLoads], mine = 0;
+#pragma unroll
+    for (int u = 0; u < kSplitLoads; ++u) {
+      wu[u] = split_weight8<SCALE>(x[u], a.temperature, m);
+      mine += wu[u];
+    }
+    const uint64_t incl = fg::wave_incl_scan_u64(mine);
+    __syncthreads();  // wsum of the previous step has been read
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    uint64_t woff = 0, stot = 0;
+#pragma unroll
+    for (int w = 0; w < kSplitWaves; ++w) {
+      if (w < wave) woff += wsum[w];
+      stot += wsum[w];
+    }
+    if (run + stot > target) {
+      uint64_t cum = run + woff + incl - mine;
+      if (cum <= target && target < cum + mine) {
+        for (int u = 0; u < kSplitLoads; ++u) {
+          if (cum + wu[u] > target) {
+            const int i0 = base + (tid * kSplitLoads + u) * 8;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              cum += split_weight<SCALE>(x[u][j], a.temperature, m);
+              if (cum > target) {
+                *found = i0 + j;
+                break;
+              }
+            }
+            break;
+          }
+          cum += wu[u];
+        }
+      }
       break;
     }
-    before += ps;
+    run += stot;
   }
-  const int lo = cs * a.chunk;
-  Row<DT> rr;
-  rr.p = split_row<DT>(a, r) + (int64_t)lo * (DT == fg::kBF16 ? 2 : 4);
-  rr.V = min(a.vocab, lo + a.chunk) - lo;
-  rr.seg = (((rr.V + kWaves - 1) / kWaves) + kStep - 1) / kStep * kStep;
-  rr.scale = a.scale;
-  rr.T = a.temperature;
-  rr.m = split_row_max(a, r);
-  block_sum<true, DT>(rr, kAll, sh);
-  const int idx = block_locate<true, DT>(rr, kAll, target - before, sh);
-  return idx >= 0 ? lo + idx : (int)fg::rank_key_index(best);  // idx < 0 cannot happen: the chunk holds the target
+  __syncthreads();
+  return *found;
 }
 
-template <int DT>
-__global__ void __launch_bounds__(kThreads) split_sample_kernel(SplitArgs a, const uint32_t* __restrict__ noise,
-                                                                int noise_stride, int noise_col, uint64_t seed,
-                                                                uint64_t step, const int32_t* __restrict__ seq_ids,
-                                                                int draw, int32_t* __restrict__ out) {
-  __shared__ Shared sh;
-  const int r = blockIdx.x;
-  if (a.forced && a.forced[r] >= 0) {
-    if (threadIdx.x == 0) out[r] = a.forced[r];
-    return;
-  }
-  const uint32_t seq = seq_ids ? (uint32_t)seq_ids[r] : (uint32_t)r;
-  const uint32_t u = noise_value(noise, (int64_t)r * noise_stride + noise_col, seed, step, seq, (uint32_t)draw);
-  const int tok = split_pick<DT>(a, r, u, sh);
-  if (threadIdx.x == 0) out[r] = tok;
-}
+// Outputs of a draw: a token per row, or one step of the acceptance walk.
+struct DrawOut {
+  const uint32_t* noise;
+  int noise_stride;
+  int noise_col;   // walk: noise column noise_col + walk_step
+  uint64_t seed, step;
+  const int32_t* seq_ids;
+  int draw;        // walk: counter draw draw + walk_step
+  int32_t* out;    // [rows] (sample mode)
+  // walk mode
+  const int32_t* tree_tokens;
+  const int32_t* parents;
+  const int32_t* n_nodes;
+  int nmax, batch, walk_step;
+  int32_t* acc_tokens;
+  int32_t* acc_nodes;
+  int acc_stride;
+  int32_t* acc_len;
+  int32_t* last_node;
+  int32_t* correction;
+  int32_t* state;
+  int32_t* err_flag;
+  int32_t* next_rows;    // optional: the next walk step's LM-head rows
+  int32_t* next_active;
+};
 
-template <int DT>
-__global__ void __launch_bounds__(kThreads) split_walk_kernel(
-    SplitArgs a, const int32_t* __restrict__ tree_tokens, const int32_t* __restrict__ parents,
-    const int32_t* __restrict__ n_nodes, int nmax, int batch, int walk_step, const uint32_t* __restrict__ noise,
-    int noise_stride, int noise_col0, uint64_t seed, uint64_t step, const int32_t* __restrict__ seq_ids, int draw0,
-    int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
-    int32_t* correction, int32_t* state, int32_t* err_flag) {
-  __shared__ Shared sh;
-  const int b = blockIdx.x;
-  if (!state[batch + b]) return;
-  const int parent = state[b];
-  const uint32_t seq = seq_ids ? (uint32_t)seq_ids[b] : (uint32_t)b;
-  const uint32_t u = noise_value(noise, (int64_t)b * noise_stride + noise_col0 + walk_step, seed, step, seq,
-                                 (uint32_t)(draw0 + walk_step));
-  const int tok = split_pick<DT>(a, b, u, sh);
-  if (threadIdx.x == 0)
-    walk_apply(b, tok, parent, tree_tokens, parents, n_nodes, nmax, batch, walk_step, acc_tokens, acc_nodes,
-               acc_stride, acc_len, last_node, correction, state, err_flag);
+// The draw of each row (one workgroup per row) from the chunk sums of split_sum_kernel
+// (greedy draws: from the row's parts alone): the chunk whose running mass crosses the
+// target, then the index inside it.
+template <int DT, bool WALK, bool SCALE>
+__global__ void __launch_bounds__(kSplitThreads) split_pick_kernel(SplitArgs a, DrawOut d) {
+  const int r = blockIdx.x, tid = threadIdx.x;
+  __shared__ float smax[kSplitWaves];
+  __shared__ uint64_t skey[kSplitWaves];
+  __shared__ uint64_t wsum[kSplitWaves];
+  __shared__ int s_found;
+  if constexpr (WALK) {
+    if (!d.state[d.batch + r]) return;
+  } else {
+    if (a.forced && a.forced[r] >= 0) {
+      if (tid == 0) d.out[r] = a.forced[r];
+      return;
+    }
+  }
+  int tok;
+  if (a.greedy) {
+    float mx;
+    uint64_t best;
+    split_parts_max(a, r, smax, skey, mx, best);
+    tok = (int)fg::rank_key_index(best);
+  } else {
+    tok = (int)fg::rank_key_index(a.row_best[r]);
+    uint64_t sums[kSplitChunks], total = 0;
+#pragma unroll
+    for (int q = 0; q < kSplitChunks; ++q) {
+      sums[q] = a.part_sum[r * kSplitChunks + q];
+      total += sums[q];
+    }
+    if (total > 0) {
+      const uint32_t seq = d.seq_ids ? (uint32_t)d.seq_ids[r] : (uint32_t)r;
+      const int ws = WALK ? d.walk_step : 0;
+      const uint32_t u = noise_value(d.noise, (int64_t)r * d.noise_stride + d.noise_col + ws, d.seed, d.step, seq,
+                                     (uint32_t)(d.draw + ws));
+      const uint64_t target = fg::mulhi_u64_u32(total, u);
+      uint64_t before = 0;
+      int cs = kSplitChunks - 1;
+      for (int q = 0; q < kSplitChunks; ++q) {
+        if (before + sums[q] > target) {
+          cs = q;
+          break;
+        }
+        before += sums[q];
+      }
+      const int clo = cs * a.chunk, chi = min(a.vocab, clo + a.chunk);
+      const int idx = split_locate<DT, SCALE>(a, split_row<DT>(a, r), clo, chi, a.row_m[r], target - before, wsum,
+                                              &s_found);
+      if (idx >= 0) tok = idx;  // always: the chunk holds the target
+    }
+  }
+  if (tid == 0) {
+    if constexpr (WALK) {
+      walk_apply(r, tok, d.state[r], d.tree_tokens, d.parents, d.n_nodes, d.nmax, d.batch, d.walk_step, d.acc_tokens,
+                 d.acc_nodes, d.acc_stride, d.acc_len, d.last_node, d.correction, d.state, d.err_flag, d.next_rows,
+                 d.next_active);
+    } else {
+      d.out[r] = tok;
+    }
+  }
 }
 
 // ------------------------------------------------------------------ split top-p
@@ -737,7 +900,7 @@ __global__ void __launch_bounds__(kSplitThreads) split_topp_level_kernel(SplitAr
   for_chunk<DT>(a, r, c, [&](int, float sv, uint32_t key) {
     if ((key & st.pmask) == st.prefix)
       atomicAdd((unsigned long long*)&hs[(key >> shift) & 255u],
-                (unsigned long long)fg::quantize_q40(fg::exp_fg(sv - m)));
+                (unsigned long long)fg::weight_q40(sv - m));
   });
   __syncthreads();
   a.hist[((size_t)r * kSplitChunks + c) * 256 + threadIdx.x] = hs[threadIdx.x];
@@ -760,7 +923,7 @@ __global__ void __launch_bounds__(kSplitThreads) split_topp_cut_kernel(SplitArgs
   uint64_t above = 0, tie = 0;
   for_chunk<DT>(a, r, c, [&](int, float sv, uint32_t key) {
     if (key >= kappa) {
-      const uint64_t w = fg::quantize_q40(fg::exp_fg(sv - m));
+      const uint64_t w = fg::weight_q40(sv - m);
       if (key > kappa) above += w;
       else tie += w;
     }
@@ -881,7 +1044,7 @@ __global__ void __launch_bounds__(kThreads) split_topp_walk_kernel(
     const int32_t* __restrict__ n_nodes, int nmax, int batch, int walk_step, const uint32_t* __restrict__ noise,
     int noise_stride, int noise_col0, uint64_t seed, uint64_t step, const int32_t* __restrict__ seq_ids, int draw0,
     int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
-    int32_t* correction, int32_t* state, int32_t* err_flag) {
+    int32_t* correction, int32_t* state, int32_t* err_flag, int32_t* next_rows, int32_t* next_active) {
   __shared__ Shared sh;
   const int b = blockIdx.x;
   if (!state[batch + b]) return;
@@ -892,7 +1055,7 @@ __global__ void __launch_bounds__(kThreads) split_topp_walk_kernel(
   const int tok = split_topp_pick<DT>(a, b, u, sh);
   if (threadIdx.x == 0)
     walk_apply(b, tok, parent, tree_tokens, parents, n_nodes, nmax, batch, walk_step, acc_tokens, acc_nodes,
-               acc_stride, acc_len, last_node, correction, state, err_flag);
+               acc_stride, acc_len, last_node, correction, state, err_flag, next_rows, next_active);
 }
 
 // Chunk partials of the split top-p path: max, four radix levels, the cut (6 launches).
@@ -905,17 +1068,24 @@ void split_topp_partials(const SplitArgs& a, int rows, hipStream_t s) {
   hipLaunchKernelGGL(split_topp_cut_kernel<DT>, grid, dim3(kSplitThreads), 0, s, a);
 }
 
-// Chunk partials of the split path: fills a.part_* (2 launches).
-template <int DT>
-void split_partials(const SplitArgs& a, int rows, hipStream_t s) {
-  dim3 grid(kSplitChunks, rows);
-  hipLaunchKernelGGL(split_max_kernel<DT>, grid, dim3(kSplitThreads), 0, s, a);
-  if (!a.greedy) hipLaunchKernelGGL(split_sum_kernel<DT>, grid, dim3(kSplitThreads), 0, s, a);
+// A split draw: the chunk maxima unless a.src_* already hold row maxima parts, the
+// chunk sums (not for greedy draws), the pick (1 to 3 launches).
+template <int DT, bool WALK, bool SCALE>
+void split_draw_scaled(const SplitArgs& a, const DrawOut& d, int rows, bool with_max, hipStream_t s) {
+  if (with_max) hipLaunchKernelGGL(split_max_kernel<DT>, dim3(kSplitChunks, rows), dim3(kSplitThreads), 0, s, a);
+  if (!a.greedy)
+    hipLaunchKernelGGL((split_sum_kernel<DT, SCALE>), dim3(kSplitChunks, rows), dim3(kSplitThreads), 0, s, a);
+  hipLaunchKernelGGL((split_pick_kernel<DT, WALK, SCALE>), dim3(rows), dim3(kSplitThreads), 0, s, a, d);
+}
+template <int DT, bool WALK>
+void split_draw(const SplitArgs& a, const DrawOut& d, int rows, bool with_max, hipStream_t s) {
+  if (a.scale) split_draw_scaled<DT, WALK, true>(a, d, rows, with_max, s);
+  else split_draw_scaled<DT, WALK, false>(a, d, rows, with_max, s);
 }
 
 constexpr size_t split_workspace_bytes(int rows) {
   return (size_t)rows * kSplitChunks * (4 + 8 + 8) + (size_t)rows * kSplitChunks * 256 * 8 +
-         (size_t)rows * 2 * sizeof(SelState) + (size_t)rows * kSplitChunks * 16 + 256;
+         (size_t)rows * 2 * sizeof(SelState) + (size_t)rows * kSplitChunks * 16 + (size_t)rows * (8 + 4) + 256;
 }
 
 // Scratch of fg_sample_tokens_noalloc: the split partials of up to
@@ -961,7 +1131,13 @@ bool split_setup(SplitArgs& a, void* workspace, size_t bytes, int rows, const vo
   a.part_a = a.hist + (size_t)rows * kSplitChunks * 256;
   a.part_t = a.part_a + (size_t)rows * kSplitChunks;
   a.sel = (SelState*)(a.part_t + (size_t)rows * kSplitChunks);
-  a.part_max = (float*)(a.sel + (size_t)rows * 2);
+  a.row_best = (uint64_t*)(a.sel + (size_t)rows * 2);
+  a.part_max = (float*)(a.row_best + rows);
+  a.row_m = a.part_max + (size_t)rows * kSplitChunks;
+  a.src_max = a.part_max;
+  a.src_key = a.part_key;
+  a.src_parts = kSplitChunks;
+  a.src_stride = kSplitChunks;
   a.tp32 = 0;
   a.logits = logits;
   a.row_stride = row_stride;
@@ -1032,15 +1208,11 @@ int sample_tokens_impl(const char* who, const void* logits, int dtype, int64_t r
       split_setup(a, workspace, workspace_bytes, rows, logits, row_stride, vocab, temperature, sp.greedy)) {
     a.row_index = row_index;
     a.forced = forced;
-    if (dtype == fg::kBF16) {
-      split_partials<fg::kBF16>(a, rows, s);
-      hipLaunchKernelGGL(split_sample_kernel<fg::kBF16>, dim3(rows), dim3(kThreads), 0, s, a, noise, noise_stride,
-                         noise_col, seed, step, seq_ids, draw, out_tokens);
-    } else {
-      split_partials<fg::kF32>(a, rows, s);
-      hipLaunchKernelGGL(split_sample_kernel<fg::kF32>, dim3(rows), dim3(kThreads), 0, s, a, noise, noise_stride,
-                         noise_col, seed, step, seq_ids, draw, out_tokens);
-    }
+    DrawOut d{};
+    d.noise = noise; d.noise_stride = noise_stride; d.noise_col = noise_col;
+    d.seed = seed; d.step = step; d.seq_ids = seq_ids; d.draw = draw; d.out = out_tokens;
+    if (dtype == fg::kBF16) split_draw<fg::kBF16, false>(a, d, rows, true, s);
+    else split_draw<fg::kF32, false>(a, d, rows, true, s);
     return fg::check_launch(who);
   }
   if (!sp.greedy && sp.top_k == 0 && sp.tp32 != 0 &&
@@ -1124,12 +1296,12 @@ int fg_accept_walk(const void* tree_logits, int dtype, int64_t row_stride, int v
       hipLaunchKernelGGL(walk_step_kernel<fg::kBF16>, dim3(batch), dim3(kThreads), 0, s, tree_logits, row_stride,
                          vocab, slot_map, tree_tokens, parents, n_nodes, nmax, batch, t, 0, noise, noise_stride,
                          noise_col0, seed, step, seq_ids, draw0, sp, acc_tokens, acc_nodes, acc_stride, acc_len,
-                         last_node, correction, workspace, err_flag);
+                         last_node, correction, workspace, err_flag, nullptr, nullptr);
     else
       hipLaunchKernelGGL(walk_step_kernel<fg::kF32>, dim3(batch), dim3(kThreads), 0, s, tree_logits, row_stride,
                          vocab, slot_map, tree_tokens, parents, n_nodes, nmax, batch, t, 0, noise, noise_stride,
                          noise_col0, seed, step, seq_ids, draw0, sp, acc_tokens, acc_nodes, acc_stride, acc_len,
-                         last_node, correction, workspace, err_flag);
+                         last_node, correction, workspace, err_flag, nullptr, nullptr);
   }
   return fg::check_launch("fg_accept_walk");
 }
@@ -1159,8 +1331,9 @@ int fg_walk_step(const void* step_logits, int dtype, int64_t row_stride, int voc
                  const uint32_t* noise, int noise_stride, int noise_col0, uint64_t seed, uint64_t step,
                  const int32_t* seq_ids, int draw0, float temperature, int greedy, int top_k, uint32_t top_p_fixed,
                  int32_t* acc_tokens, int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
-                 int32_t* correction, int32_t* state, int32_t* err_flag, void* workspace, size_t workspace_bytes,
-                 void* stream) {
+                 int32_t* correction, int32_t* state, int32_t* err_flag, const float* part_max,
+                 const uint64_t* part_key, int nparts, int32_t* next_row_index, int32_t* next_row_active,
+                 void* workspace, size_t workspace_bytes, void* stream) {
   FG_REQUIRE(step_logits && tree_tokens && parents && n_nodes && acc_tokens && acc_nodes && acc_len && last_node &&
                  correction && state,
              "fg_walk_step: null pointer");
@@ -1169,23 +1342,31 @@ int fg_walk_step(const void* step_logits, int dtype, int64_t row_stride, int voc
   FG_REQUIRE(dtype == fg::kF32 || dtype == fg::kBF16, "fg_walk_step: dtype");
   FG_REQUIRE(row_stride >= vocab && row_stride % 8 == 0 && ((uintptr_t)step_logits & 31) == 0,
              "fg_walk_step: rows must be 32-byte aligned (row_stride % 8 == 0)");
+  FG_REQUIRE(!part_max == !part_key && (!part_max || nparts > 0), "fg_walk_step: part_max / part_key / nparts");
+  FG_REQUIRE(!next_row_index == !next_row_active, "fg_walk_step: next_row_index and next_row_active go together");
   SampleParams sp = make_params(temperature, greedy, top_k, vocab, top_p_fixed);
   hipStream_t s = (hipStream_t)stream;
   SplitArgs a;
   if ((sp.greedy || (sp.top_k == 0 && sp.tp32 == 0)) &&
       split_setup(a, workspace, workspace_bytes, batch, step_logits, row_stride, vocab, temperature, sp.greedy)) {
     a.active = state + batch;
-    if (dtype == fg::kBF16) {
-      split_partials<fg::kBF16>(a, batch, s);
-      hipLaunchKernelGGL(split_walk_kernel<fg::kBF16>, dim3(batch), dim3(kThreads), 0, s, a, tree_tokens, parents,
-                         n_nodes, nmax, batch, walk_step, noise, noise_stride, noise_col0, seed, step, seq_ids, draw0,
-                         acc_tokens, acc_nodes, acc_stride, acc_len, last_node, correction, state, err_flag);
-    } else {
-      split_partials<fg::kF32>(a, batch, s);
-      hipLaunchKernelGGL(split_walk_kernel<fg::kF32>, dim3(batch), dim3(kThreads), 0, s, a, tree_tokens, parents,
-                         n_nodes, nmax, batch, walk_step, noise, noise_stride, noise_col0, seed, step, seq_ids, draw0,
-                         acc_tokens, acc_nodes, acc_stride, acc_len, last_node, correction, state, err_flag);
+    const bool with_max = part_max == nullptr;
+    if (!with_max) {
+      a.src_max = part_max;
+      a.src_key = part_key;
+      a.src_parts = nparts;
+      a.src_stride = nparts;
     }
+    DrawOut d{};
+    d.noise = noise; d.noise_stride = noise_stride; d.noise_col = noise_col0;
+    d.seed = seed; d.step = step; d.seq_ids = seq_ids; d.draw = draw0;
+    d.tree_tokens = tree_tokens; d.parents = parents; d.n_nodes = n_nodes;
+    d.nmax = nmax; d.batch = batch; d.walk_step = walk_step;
+    d.acc_tokens = acc_tokens; d.acc_nodes = acc_nodes; d.acc_stride = acc_stride; d.acc_len = acc_len;
+    d.last_node = last_node; d.correction = correction; d.state = state; d.err_flag = err_flag;
+    d.next_rows = next_row_index; d.next_active = next_row_active;
+    if (dtype == fg::kBF16) split_draw<fg::kBF16, true>(a, d, batch, with_max, s);
+    else split_draw<fg::kF32, true>(a, d, batch, with_max, s);
     return fg::check_launch("fg_walk_step");
   }
   if (!sp.greedy && sp.top_k == 0 && sp.tp32 != 0 &&
@@ -1196,12 +1377,14 @@ int fg_walk_step(const void* step_logits, int dtype, int64_t row_stride, int voc
       split_topp_partials<fg::kBF16>(a, batch, s);
       hipLaunchKernelGGL(split_topp_walk_kernel<fg::kBF16>, dim3(batch), dim3(kThreads), 0, s, a, tree_tokens, parents,
                          n_nodes, nmax, batch, walk_step, noise, noise_stride, noise_col0, seed, step, seq_ids, draw0,
-                         acc_tokens, acc_nodes, acc_stride, acc_len, last_node, correction, state, err_flag);
+                         acc_tokens, acc_nodes, acc_stride, acc_len, last_node, correction, state, err_flag,
+                         next_row_index, next_row_active);
     } else {
       split_topp_partials<fg::kF32>(a, batch, s);
       hipLaunchKernelGGL(split_topp_walk_kernel<fg::kF32>, dim3(batch), dim3(kThreads), 0, s, a, tree_tokens, parents,
                          n_nodes, nmax, batch, walk_step, noise, noise_stride, noise_col0, seed, step, seq_ids, draw0,
-                         acc_tokens, acc_nodes, acc_stride, acc_len, last_node, correction, state, err_flag);
+                         acc_tokens, acc_nodes, acc_stride, acc_len, last_node, correction, state, err_flag,
+                         next_row_index, next_row_active);
     }
     return fg::check_launch("fg_walk_step");
   }
@@ -1209,12 +1392,12 @@ int fg_walk_step(const void* step_logits, int dtype, int64_t row_stride, int voc
     hipLaunchKernelGGL(walk_step_kernel<fg::kBF16>, dim3(batch), dim3(kThreads), 0, s, step_logits, row_stride, vocab,
                        nullptr, tree_tokens, parents, n_nodes, nmax, batch, walk_step, 1, noise, noise_stride,
                        noise_col0, seed, step, seq_ids, draw0, sp, acc_tokens, acc_nodes, acc_stride, acc_len,
-                       last_node, correction, state, err_flag);
+                       last_node, correction, state, err_flag, next_row_index, next_row_active);
   else
     hipLaunchKernelGGL(walk_step_kernel<fg::kF32>, dim3(batch), dim3(kThreads), 0, s, step_logits, row_stride, vocab,
                        nullptr, tree_tokens, parents, n_nodes, nmax, batch, walk_step, 1, noise, noise_stride,
                        noise_col0, seed, step, seq_ids, draw0, sp, acc_tokens, acc_nodes, acc_stride, acc_len,
-                       last_node, correction, state, err_flag);
+                       last_node, correction, state, err_flag, next_row_index, next_row_active);
   return fg::check_launch("fg_walk_step");
 }
 

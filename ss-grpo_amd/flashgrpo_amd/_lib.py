@@ -28,7 +28,9 @@ SIGNATURES = {
     "fg_medusa_heads": (_I, [_P, _I, _I, _I, _I64, _I, _P, _P, _F, _P, _P, _P, _I, _P, _SZ, _P]),
     "fg_lm_head": (_I, [_P, _I, _I, _I, _I64, _P, _P, _P, _I64, _I, _P, _I, _I64, _P]),
     "fg_lm_head_topk_workspace": (_SZ, [_I, _I, _I]),
-    "fg_lm_head_topk": (_I, [_P, _I, _I, _I64, _P, _P, _P, _I64, _I, _P, _I, _I64, _I, _I, _P, _P, _P, _P, _SZ, _P]),
+    "fg_lm_head_topk_parts": (_I, [_I]),
+    "fg_lm_head_topk": (_I, [_P, _I, _I, _I64, _P, _P, _P, _I64, _I, _P, _I, _I64, _I, _I, _P, _P, _P, _P, _P, _P, _SZ,
+                             _P]),
     "fg_medusa_topk_workspace": (_SZ, [_I, _I, _I]),
     "fg_medusa_topk": (_I, [_P, _I, _I64, _I, _I, _I, _I, _P, _P, _P, _P, _SZ, _P]),
     "fg_tree_layout": (_I, [_P, _P, _I, _I, _P, _P, _P, _I, _P, _P, _I, _P]),
@@ -52,7 +54,7 @@ SIGNATURES = {
     "fg_walk_begin": (_I, [_P, _P, _P, _I, _I, _P, _P, _I, _P, _P, _P, _P, _P]),
     "fg_walk_rows": (_I, [_P, _I, _I, _P, _P, _P]),
     "fg_walk_step": (_I, [_P, _I, _I64, _I, _P, _P, _P, _I, _I, _I, _P, _I, _I, _U64, _U64, _P, _I, _F, _I, _I, _U32,
-                          _P, _P, _I, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+                          _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _SZ, _P]),
     "fg_accept_finalize": (_I, [_P, _P, _I, _P, _P, _P, _P, _I, _I, _P, _P, _I, _P]),
     "fg_kv_path_gather": (_I, [_P, _I, _I, _I, _I, _I, _I64, _I64, _I64, _I, _P, _P, _P, _I, _P, _I, _P, _P]),
 }

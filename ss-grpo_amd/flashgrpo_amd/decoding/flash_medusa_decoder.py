@@ -5,15 +5,17 @@ Same configuration dataclass, constructor and ``generate`` contract as
 included). One verify round, per active sequence:
 
   root draw            fg_sample_tokens (draw 0; b200 mode: pending correction forced)
-  Medusa proposals     fg_medusa_heads -> fg_lm_head -> fg_medusa_topk (+ row stats)
+  Medusa proposals     fg_medusa_heads -> fg_lm_head_topk (tied LM head with the
+                       per-depth top-k and row stats in its epilogue)
   plan / tree          plan_tree (host), adaptive refit from per-head confidence
                        quantiles, cached TreeTopology, fg_tree_layout
   chain proposals      (proposal_mode="chain") per depth: fg_lm_head over every parent
                        state -> fg_medusa_topk (sanitised, + row stats) -> children
                        in dense-BFS order under the budget -> ChainDraftCell step
   tree verify          TargetModel.forward (tree attention with ancestor bit masks)
-  acceptance           lazy (default): per walk step t, fg_walk_rows -> fg_lm_head over
-                       the node each row samples from -> fg_walk_step (draw 1+t);
+  acceptance           lazy (default): per walk step t, fg_lm_head_topk over the node
+                       each row samples from (with the rows' maxima) -> fg_walk_step
+                       (draw 1+t; it also writes the next step's rows);
                        packed: fg_lm_head over internal nodes + fg_accept_walk;
                        then fg_accept_finalize (clamp, EOS)
   cache update         fg_kv_path_gather (extract_path) or a chain re-forward
@@ -570,14 +572,18 @@ class FlashMedusaDecoder:
         if walk_logits is not None:
             # Walk step t samples row b from the node its walk stands on; only those
             # rows are projected (inactive rows' tiles are skipped).
+            # With the weight-streaming LM head, each step's launch also leaves the rows' maxima
+            # (the draw then needs no chunk-maxima launch) and every step writes the next
+            # step's rows.
             walk = K.walk_begin(tree_tokens, tv["parents"], tv["n_nodes"], acc_stride=D + 1)
+            parts = model.walk_parts(Bc, hidden_t)
+            K.walk_rows(walk, N)
             for t in range(D):
-                K.walk_rows(walk, N)
                 with timing.label("tree"):
                     model.logits(hidden_t, row_index=walk["row_index"], row_active=walk["row_active"],
-                                 out=walk_logits[t])
+                                 out=walk_logits[t], parts=parts)
                 K.walk_step(walk, walk_logits[t], tree_tokens, tv["parents"], tv["n_nodes"], walk_step=t,
-                            **walk_kw)
+                            parts=parts, next_rows=True, **walk_kw)
         elif tree_logits is not None:
             walk = K.accept_walk(tree_logits, tree_tokens, tv["parents"], tv["n_nodes"], max_walk_steps=D,
                                  slot_map=slot_map, **walk_kw)
@@ -594,7 +600,7 @@ class FlashMedusaDecoder:
         cols = [walk["acc_tokens"], walk["acc_len"].view(-1, 1), finished_d.view(-1, 1),
                 walk["last_node"].view(-1, 1), r.err.expand(Bc).view(-1, 1)]
         if walk_logits is not None:
-            cols += [walk["state"][2 * Bc:].view(-1, 1), walk["acc_nodes"]]
+            cols += [walk["state"][2 * Bc:3 * Bc].view(-1, 1), walk["acc_nodes"]]
         if b200:
             cols.append(new_pending.view(-1, 1))
         if sparse is not None:

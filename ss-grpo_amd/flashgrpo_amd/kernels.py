@@ -144,14 +144,21 @@ def lm_head(x, weight, *, row_index=None, row_active=None, out=None, out_dtype=N
     return out
 
 
+def lm_head_parts(vocab):
+    """Row maxima parts per row that ``lm_head_topk(..., parts=...)`` writes."""
+    return int(_lib.load().fg_lm_head_topk_parts(int(vocab)))
+
+
 def lm_head_topk(x, weight, kmax=0, *, row_index=None, row_active=None, out=None, out_dtype=None,
-                 logits=True, stats=False, sanitize=False, workspace=None):
+                 logits=True, stats=False, sanitize=False, workspace=None, parts=None):
     """Tied LM head over <= 256 rows (bf16) on the weight-streaming kernel, with the
     per-row top-kmax candidates fused (``fg_lm_head_topk``).
 
     Returns (logits [M, N] or None, tokens int32 [M, kmax] or None, scores fp32 [M, kmax]
     or None, stats fp32 [M, 2] or None); the candidates and stats equal
     ``medusa_topk(logits, kmax, stats=..., sanitize=...)`` on the bf16 logits.
+    ``parts`` (kmax 0): a (part_max fp32, part_key int64) pair of [M, lm_head_parts(N)]
+    tensors that receive each row's per-workgroup maxima (for ``walk_step``).
     """
     _dev(x, weight, row_index, row_active)
     _i32(row_index, "row_index")
@@ -184,10 +191,17 @@ def lm_head_topk(x, weight, kmax=0, *, row_index=None, row_active=None, out=None
         ws_bytes = workspace.numel() * workspace.element_size()
     else:
         workspace = None
+    pmax = pkey = None
+    if parts is not None:
+        pmax, pkey = parts
+        P = lm_head_parts(N)
+        if (kmax or pmax.dtype != torch.float32 or pkey.dtype != torch.int64 or tuple(pmax.shape) != (M, P)
+                or tuple(pkey.shape) != (M, P) or not pmax.is_contiguous() or not pkey.is_contiguous()):
+            raise ValueError(f"lm_head_topk: parts must be contiguous fp32 / int64 [{M}, {P}] with kmax 0")
     _call("fg_lm_head_topk", _ptr(x2), M, K, x2.stride(0), _ptr(row_index), _ptr(row_active), _ptr(weight),
           weight.stride(0), N, _ptr(out), dtype_code(out) if out is not None else 1,
           out.stride(0) if out is not None else N, int(kmax), int(bool(sanitize)), _ptr(tok), _ptr(sc), _ptr(st),
-          _ptr(workspace), ws_bytes, _stream())
+          _ptr(pmax), _ptr(pkey), _ptr(workspace), ws_bytes, _stream())
     return out, tok, sc, st
 
 
@@ -430,9 +444,19 @@ def walk_rows(walk, nmax):
 
 def walk_step(walk, step_logits, tree_tokens, parents, n_nodes, *, walk_step, noise=None, noise_col0=0, seed=0,
               step=0, seq_ids=None, draw0=1, temperature=1.0, greedy=False, top_k=None, top_p=1.0, err_flag=None,
-              split=True):
-    """One walk step: active row b draws from row b of step_logits."""
+              split=True, parts=None, next_rows=False):
+    """One walk step: active row b draws from row b of step_logits.
+
+    ``parts``: the (part_max, part_key) row maxima that ``lm_head_topk`` wrote with
+    step_logits (an unrestricted / greedy step then needs no chunk-maxima launch). ``next_rows``: also
+    fill walk['row_index'] / walk['row_active'] for the next step (as ``walk_rows``)."""
     _dev(step_logits, tree_tokens, parents, n_nodes, noise, seq_ids)
+    if parts is not None:
+        _dev(*parts)
+        pm, pk = parts
+        if (pm.dtype != torch.float32 or pk.dtype != torch.int64 or pm.dim() != 2 or pm.shape != pk.shape
+                or pm.shape[0] != tree_tokens.shape[0] or not pm.is_contiguous() or not pk.is_contiguous()):
+            raise ValueError("walk_step: parts must be contiguous fp32 / int64 [batch, P] pairs")
     B, nmax = tree_tokens.shape
     lg = aligned_rows(step_logits)
     V = lg.shape[-1]
@@ -444,8 +468,10 @@ def walk_step(walk, step_logits, tree_tokens, parents, n_nodes, *, walk_step, no
           int(seed) & (2 ** 64 - 1), int(step), _ptr(seq_ids), int(draw0), use_T, int(g), int(top_k or 0),
           top_p_fixed(top_p), _ptr(walk["acc_tokens"]), _ptr(walk["acc_nodes"]), walk["acc_tokens"].stride(0),
           _ptr(walk["acc_len"]), _ptr(walk["last_node"]), _ptr(walk["correction"]), _ptr(walk["state"]),
-          _ptr(err_flag), _ptr(walk["workspace"]) if split else None, walk["workspace"].numel() if split else 0,
-          _stream())
+          _ptr(err_flag), _ptr(parts[0]) if parts is not None else None, _ptr(parts[1]) if parts is not None else None,
+          parts[0].shape[1] if parts is not None else 0, _ptr(walk["row_index"]) if next_rows else None,
+          _ptr(walk["row_active"]) if next_rows else None, _ptr(walk["workspace"]) if split else None,
+          walk["workspace"].numel() if split else 0, _stream())
 
 
 def accept_finalize(walk, old_len, *, max_length, eos_token_id, finished=None, pending_root=None):

@@ -569,8 +569,21 @@ class TargetModel:
         K.rmsnorm(x, self.w["final_norm"], cfg.rms_eps, out=out)
         return out.view(B, N, H)
 
+    def walk_parts(self, rows: int, hidden: torch.Tensor):
+        """Row maxima buffers (part_max fp32, part_key int64 [rows, P]) for ``logits(...,
+        parts=...)`` when gathered rows of ``hidden`` take the weight-streaming LM head
+        (which then writes them), else None."""
+        x = hidden.reshape(-1, self.cfg.hidden)
+        w = self.w["lm_head"]
+        if not (self.dtype == torch.bfloat16 and 0 < rows <= LM_STREAM_ROWS and x.stride(1) == 1
+                and w.stride(1) == 1 and (x.numel() + x.storage_offset()) * 2 < 1 << 32):
+            return None
+        P = K.lm_head_parts(w.shape[0])
+        return (torch.empty(rows, P, dtype=torch.float32, device=x.device),
+                torch.empty(rows, P, dtype=torch.int64, device=x.device))
+
     def logits(self, hidden: torch.Tensor, *, row_index=None, row_active=None, out=None, out_dtype=None,
-               weight: torch.Tensor | None = None) -> torch.Tensor:
+               weight: torch.Tensor | None = None, parts=None) -> torch.Tensor:
         """LM-head rows: hidden rows (optionally gathered by row_index); rows with
         row_active == 0 may be left unwritten. ``weight`` [V, H] replaces the tied LM
         head (an untied Medusa head's own output projection).
@@ -579,14 +592,17 @@ class TargetModel:
         whole when no row is active), run the weight-streaming LM-head kernel
         (``fg_lm_head_topk``, the weight read once). Larger contiguous blocks (prefill
         sized) are a square GEMM and go to hipBLASLt; larger gathered sets and fp32 run
-        ``fg_lm_head``.
+        ``fg_lm_head``. ``parts`` (from ``walk_parts``): the streaming kernel also writes
+        each row's maxima parts.
         """
         x = hidden.reshape(-1, self.cfg.hidden)
         w = self.w["lm_head"] if weight is None else weight
         if (row_index is None and row_active is None and self.dtype == torch.bfloat16
                 and (out_dtype is None or out_dtype == self.dtype)):
             if x.shape[0] <= LM_STREAM_ROWS and x.stride(1) == 1 and w.stride(1) == 1:
-                return K.lm_head_topk(x, w, 0, out=out)[0]
+                return K.lm_head_topk(x, w, 0, out=out, parts=parts)[0]
+            if parts is not None:
+                raise ValueError("logits: row maxima parts need the weight-streaming LM head (see walk_parts)")
             if out is None:
                 return F.linear(x, w)
             return torch.matmul(x, w.t(), out=out)
@@ -595,7 +611,9 @@ class TargetModel:
                 and (x.numel() + x.storage_offset()) * 2 < 1 << 32
                 and (out_dtype is None or out_dtype in (torch.bfloat16, torch.float32))):
             return K.lm_head_topk(x, w, 0, row_index=row_index, row_active=row_active, out=out,
-                                  out_dtype=out_dtype)[0]
+                                  out_dtype=out_dtype, parts=parts)[0]
+        if parts is not None:
+            raise ValueError("logits: row maxima parts need the weight-streaming LM head (see walk_parts)")
         return K.lm_head(x, w, row_index=row_index, row_active=row_active, out=out, out_dtype=out_dtype)
 
     def logits_topk(self, hidden: torch.Tensor, kmax: int, *, stats: bool = False, sanitize: bool = False,

@@ -302,14 +302,19 @@ def test_sample_tokens_bit_exact(dtype, mode):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("mode", [{}, {"temperature": 0.7}, {"greedy": True}, {"temperature": 1.3}])
 def test_split_sampling_equals_single_workgroup(dtype, mode):
-    """Rows split over 16 workgroups (unrestricted / greedy draws) give the tokens of
-    the one-workgroup-per-row kernel, including flat rows, ties and short vocabularies."""
+    """Rows split over 16 workgroups (unrestricted / greedy draws: chunk maxima, then one
+    draw launch) give the tokens of the one-workgroup-per-row kernel, including flat rows,
+    ties, -inf and NaN entries, rows of only -inf or NaN, and short vocabularies."""
     g = torch.Generator(device="cpu").manual_seed(23)
     for V in (5, 37, 1000, 32000, 152064):
         x = torch.randn(48, V, generator=g) * 2.0
         x[0] = 0.0
         x[1] = torch.round(x[1])
         x[2, V // 3] = 30.0
+        x[3, : V // 2] = float("-inf")
+        x[4, V - 1] = float("nan")
+        x[5] = float("-inf")
+        x[6] = float("nan")
         xd = x.to(dtype).to(DEV)
         for draw in range(3):
             kw = dict(seed=99, step=draw, draw=draw, temperature=mode.get("temperature", 1.0),
@@ -718,3 +723,55 @@ def test_rope_kv_write_rmsnorm_swiglu(dtype):
     sg = K().swiglu(gu)
     g_ = to_np(gu)
     assert rel_err(to_np(sg), OM.silu(g_[:, :96].astype(np.float64)) * g_[:, 96:]) < TOL[dtype]
+
+
+@pytest.mark.parametrize("mode", [{}, {"temperature": 0.7}, {"greedy": True}, {"top_p": 0.9}])
+def test_walk_with_lm_head_parts_equals_plain_walk(mode):
+    """The lazy walk with the LM head's row maxima (no chunk-maxima launch in an
+    unrestricted / greedy step, next rows written by the step) equals the walk with chunk maxima and
+    fg_walk_rows, and the one-workgroup-per-row walk, step by step; planted logits make
+    sequences accept several nodes."""
+    rng = np.random.default_rng(5)
+    B, ks, budget, V, H = 16, [4, 2, 1, 1], 32, 5003, 128
+    parents, _, _ = OT.dense_topology(ks, budget)
+    N, D = len(parents), len(ks)
+    toks = rng.integers(0, V, (B, N)).astype(np.int32)
+    trees = [OT.Tree(toks[b].tolist(), parents, None) for b in range(B)]
+    w = torch.from_numpy(rng.standard_normal((V, H)).astype(np.float32) * 0.05).to(torch.bfloat16).to(DEV)
+    hid = torch.from_numpy(rng.standard_normal((B * N, H)).astype(np.float32) * 0.5)
+    wf = w.float().cpu()
+    for b, t in enumerate(trees):  # steer most internal nodes toward one of their children
+        for n in range(N):
+            kids = t.children(n)
+            if kids and (b + n) % 4:
+                tok = t.tokens[kids[(b + n) % len(kids)]]
+                hid[b * N + n] = wf[tok] * (14.0 / float(wf[tok].pow(2).sum()))
+    hid = hid.to(torch.bfloat16).to(DEV)
+    tt = torch.from_numpy(toks).to(DEV)
+    pp = torch.tensor([parents] * B, dtype=torch.int32, device=DEV)
+    nn = torch.full((B,), N, dtype=torch.int32, device=DEV)
+    P = K().lm_head_parts(V)
+    kw = dict(seed=3, step=2, temperature=mode.get("temperature", 1.0), greedy=mode.get("greedy", False),
+              top_p=mode.get("top_p", 1.0))
+    runs = []
+    for variant in ("parts", "split", "single"):
+        wk = K().walk_begin(tt, pp, nn, acc_stride=D + 1)
+        parts = (torch.empty(B, P, dtype=torch.float32, device=DEV), torch.empty(B, P, dtype=torch.int64, device=DEV))
+        steps = []
+        K().walk_rows(wk, N)
+        for t in range(D):
+            if variant != "parts" and t > 0:
+                K().walk_rows(wk, N)
+            lg = torch.full((B, V), 5.0, dtype=torch.bfloat16, device=DEV)
+            K().lm_head_topk(hid, w, 0, row_index=wk["row_index"], row_active=wk["row_active"], out=lg,
+                             parts=parts if variant == "parts" else None)
+            K().walk_step(wk, lg, tt, pp, nn, walk_step=t, split=variant != "single",
+                          parts=parts if variant == "parts" else None, next_rows=variant == "parts", **kw)
+            steps.append(wk["state"][: 3 * B].clone())
+        runs.append((wk, steps))
+    for wk, steps in runs[1:]:
+        for k in ("acc_tokens", "acc_nodes", "acc_len", "last_node", "correction"):
+            assert torch.equal(runs[0][0][k], wk[k]), k
+        for t in range(D):
+            assert torch.equal(runs[0][1][t], steps[t]), t
+    assert int(runs[0][0]["acc_len"].max()) >= 3  # the planted paths were walked

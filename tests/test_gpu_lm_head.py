@@ -171,3 +171,53 @@ def test_target_logits_topk_routes_and_matches():
     h3 = torch.randn(300, 128, device=DEV).to(torch.bfloat16)
     lg3, tok3, _, _ = model.logits_topk(h3, 3, logits=True)
     assert tok3.shape == (300, 3) and torch.equal(tok3, K().medusa_topk(lg3, 3)[0])
+
+
+def _rank_keys_np(xs):
+    """fg rank keys (value desc, index asc; NaN first, -0 == +0) of float32 rows, as uint64."""
+    b = xs.astype(np.float32).view(np.uint32).astype(np.uint64)
+    key = np.where(b & 0x80000000, (~b) & 0xFFFFFFFF, b | 0x80000000)
+    key = np.where(xs == 0, 0x80000000, key)
+    key = np.where(np.isnan(xs), 0xFFFFFFFF, key).astype(np.uint64)
+    idx = np.arange(xs.shape[-1], dtype=np.uint64)
+    return (key << np.uint64(32)) | (np.uint64(0xFFFFFFFF) - idx)
+
+
+@pytest.mark.parametrize("M,N,out_dtype", [(16, 152064, torch.bfloat16), (64, 32000, torch.bfloat16),
+                                           (100, 5003, torch.float32), (200, 9000, torch.bfloat16)])
+def test_row_maxima_parts(M, N, out_dtype):
+    """The per-workgroup row maxima parts reduce to each row's maximum of the stored logits
+    (NaN ignored) and to the rank key of its first maximum (NaN first)."""
+    torch.manual_seed(M)
+    Kd = 128
+    src = (torch.randn(M + 5, Kd, device=DEV)).to(torch.bfloat16)
+    w = (torch.randn(N, Kd, device=DEV) * 0.1).to(torch.bfloat16)
+    w[N // 2] = w[N // 3]          # exact ties between two columns
+    w[7, 0] = float("nan")         # a NaN column
+    src[2, :] = 0.0                # a row of zeros: every logit is +-0 (and NaN in column 7)
+    idx = torch.randperm(M + 5, device=DEV)[:M].to(torch.int32)
+    P = K().lm_head_parts(N)
+    pm = torch.empty(M, P, dtype=torch.float32, device=DEV)
+    pk = torch.empty(M, P, dtype=torch.int64, device=DEV)
+    lg = K().lm_head_topk(src, w, 0, row_index=idx, out_dtype=out_dtype, parts=(pm, pk))[0]
+    ref = K().lm_head_topk(src, w, 0, row_index=idx, out_dtype=out_dtype)[0]
+    xs = to_np(lg)
+    assert np.array_equal(xs, to_np(ref), equal_nan=True)  # the parts do not change the logits
+    want_max = np.where(np.isnan(xs), -np.inf, xs).max(axis=1)
+    assert np.array_equal(to_np(pm).max(axis=1), want_max)
+    keys = pk.cpu().numpy().view(np.uint64)
+    assert np.array_equal(keys.max(axis=1), _rank_keys_np(xs).max(axis=1))
+
+
+def test_row_maxima_parts_rejections():
+    from flashgrpo_amd._lib import NativeError
+
+    x = torch.randn(4, 64, device=DEV).to(torch.bfloat16)
+    w = torch.randn(500, 64, device=DEV).to(torch.bfloat16)
+    P = K().lm_head_parts(500)
+    pm = torch.empty(4, P, dtype=torch.float32, device=DEV)
+    pk = torch.empty(4, P, dtype=torch.int64, device=DEV)
+    with pytest.raises((ValueError, NativeError)):
+        K().lm_head_topk(x, w, 2, parts=(pm, pk))
+    with pytest.raises(ValueError):
+        K().lm_head_topk(x, w, 0, parts=(pm[:, :1].contiguous(), pk[:, :1].contiguous()))
