@@ -40,11 +40,18 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kWaves = 8;
+constexpr int kBlocks = 8;  // 32-column blocks per workgroup and round (W waves x NB blocks)
 constexpr int kKS = 64;     // k-step
 constexpr int kTileRow = 528;  // bytes per row of the epilogue's bf16 tile (256 columns + 16)
 // k-steps in flight; the activation ring has one stage more
 constexpr int dist_for(int mi) { return mi >= 8 ? 2 : 3; }
+// Waves per workgroup (W waves x NB = 8 / W blocks of 32 columns). A layout of 4 waves x 2
+// blocks at 256 rows (one wave per SIMD, the accumulators in 256 AGPRs) would read each
+// activation fragment once for two blocks, halving the LDS reads that bound the 8-wave
+// layout there; built, it returned wrong logits for the row blocks whose accumulators sit in
+// AGPRs 0-63 and 128-191 (the compiler moves accumulators between AGPRs and VGPRs around the
+// asm-issued weight loads), so every row count runs 8 waves.
+constexpr int waves_for(int) { return 8; }
 
 template <int N>
 FG_DEVICE void wait_vmcnt() {
@@ -75,20 +82,22 @@ struct LmArgs {
   int nparts;  // = grid: one part per workgroup
 };
 
-template <int MI, int CDT, int KT, bool SAN, bool PM>
-__global__ void __launch_bounds__(kWaves * 64, 1) lm_stream_kernel(LmArgs a) {
+template <int MI, int CDT, int KT, bool SAN, bool PM, int W>
+__global__ void __launch_bounds__(W * 64, 1) lm_stream_kernel(LmArgs a) {
   static_assert(!PM || KT == 0, "row maxima parts come with the logits-only epilogue");
+  constexpr int NB = kBlocks / W;  // 32-column blocks per wave and round
+  static_assert(NB * W == kBlocks, "waves");
   constexpr int kDist = dist_for(MI), kStages = kDist + 1;
   constexpr int MP = MI * 32;
   constexpr int STAGE = MP * 128;
-  constexpr int LA = STAGE / 1024 / kWaves;  // HBM -> LDS loads per wave and k-step
-  constexpr int LB = 4;                      // weight loads per lane and k-step
+  constexpr int LA = STAGE / 1024 / W;  // HBM -> LDS loads per wave and k-step
+  constexpr int LB = 4 * NB;            // weight loads per lane and k-step
   constexpr int L = LA + LB;
   static_assert(MI % 2 == 0 && LA >= 1, "rows");
   static_assert((kDist - 1) * L < 64, "vmcnt");
-  constexpr int XPOSE = kStages * STAGE;     // per-wave 4 KB weight transpose buffers
+  constexpr int XPOSE = kStages * STAGE;     // per-wave NB x 4 KB weight transpose buffers
   constexpr int TILE = KT ? MP * kTileRow : 0;
-  constexpr int MAIN = XPOSE + kWaves * 4096 > TILE ? XPOSE + kWaves * 4096 : TILE;
+  constexpr int MAIN = XPOSE + kBlocks * 4096 > TILE ? XPOSE + kBlocks * 4096 : TILE;
   // each row's running top-KT keys and (max, sum exp) over this workgroup's columns
   constexpr int LISTS = KT ? MP * (KT * 8 + 8) : 0;
   constexpr int LDS = MAIN + LISTS;
@@ -96,7 +105,7 @@ __global__ void __launch_bounds__(kWaves * 64, 1) lm_stream_kernel(LmArgs a) {
   __shared__ __attribute__((aligned(1024))) unsigned char smem[LDS];
   uint64_t* s_keys = (uint64_t*)(smem + MAIN);
   float2* s_lse = (float2*)(smem + MAIN + MP * KT * 8);
-  __shared__ int s_n0[kWaves], s_nv[kWaves], s_any;
+  __shared__ int s_n0[kBlocks], s_nv[kBlocks], s_any;
 
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -107,11 +116,11 @@ __global__ void __launch_bounds__(kWaves * 64, 1) lm_stream_kernel(LmArgs a) {
     __syncthreads();
     if (!s_any) return;
   }
-  // Block rd * GW + gw goes to wave gw = wave * G + workgroup in round rd: the blocks of a
-  // partial last round are spread over every CU (a CU's loads, not HBM, bound a round that
-  // only a few CUs run).
-  const int nblk = (a.N + 31) >> 5;
-  const int gw_total = gridDim.x * kWaves;
+  // Wave block (NB x 32 columns) rd * GW + gw goes to wave gw = wave * G + workgroup in round
+  // rd: the blocks of a partial last round are spread over every CU (a CU's loads, not HBM,
+  // bound a round that only a few CUs run).
+  const int nblk = (a.N + 32 * NB - 1) / (32 * NB);
+  const int gw_total = gridDim.x * W;
   const int gw = wave * gridDim.x + blockIdx.x;
   const int q = nblk / gw_total, rem = nblk % gw_total;
   const int my_cnt = q + (gw < rem ? 1 : 0);
@@ -143,8 +152,8 @@ __global__ void __launch_bounds__(kWaves * 64, 1) lm_stream_kernel(LmArgs a) {
                    : "memory");
     }
   };
-  // weight stream: load q of a k-step brings rows q * 8 + lane / 8 of the block, 16-byte
-  // piece lane % 8 (128 contiguous bytes per row)
+  // weight stream: load q of a k-step brings rows q * 8 + lane / 8 of the wave block,
+  // 16-byte piece lane % 8 (128 contiguous bytes per row)
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, -1, 0x00020000);
   uint32_t woff[LB];
   v4u wr[kDist][LB];
@@ -153,17 +162,21 @@ __global__ void __launch_bounds__(kWaves * 64, 1) lm_stream_kernel(LmArgs a) {
   // static wait before each k-step's barrier covers them.
   // (one statement with its own wait states, as for the activation loads)
   auto issue_w = [&](v4u(&dst)[LB], int koff) __attribute__((always_inline)) {
-    asm volatile(
-        "s_nop 4\n\t"
-        "buffer_load_dwordx4 %0, %4, %8, %9 offen\n\t"
-        "buffer_load_dwordx4 %1, %5, %8, %9 offen\n\t"
-        "buffer_load_dwordx4 %2, %6, %8, %9 offen\n\t"
-        "buffer_load_dwordx4 %3, %7, %8, %9 offen"
-        : "=&v"(dst[0]), "=&v"(dst[1]), "=&v"(dst[2]), "=&v"(dst[3])
-        : "v"(woff[0]), "v"(woff[1]), "v"(woff[2]), "v"(woff[3]), "s"(wrs), "s"(koff));
+#pragma unroll
+    for (int h = 0; h < NB; ++h)
+      asm volatile(
+          "s_nop 4\n\t"
+          "buffer_load_dwordx4 %0, %4, %8, %9 offen\n\t"
+          "buffer_load_dwordx4 %1, %5, %8, %9 offen\n\t"
+          "buffer_load_dwordx4 %2, %6, %8, %9 offen\n\t"
+          "buffer_load_dwordx4 %3, %7, %8, %9 offen"
+          : "=&v"(dst[4 * h]), "=&v"(dst[4 * h + 1]), "=&v"(dst[4 * h + 2]), "=&v"(dst[4 * h + 3])
+          : "v"(woff[4 * h]), "v"(woff[4 * h + 1]), "v"(woff[4 * h + 2]), "v"(woff[4 * h + 3]), "s"(wrs),
+            "s"(koff));
   };
-  // this wave's transpose buffer: row r of the block at r * 128, pieces swizzled like x
-  unsigned char* xp = smem + XPOSE + wave * 4096;
+  // this wave's transpose buffer: row r of the wave block at r * 128 (block nb at nb * 4 KB),
+  // pieces swizzled like x
+  unsigned char* xp = smem + XPOSE + wave * 4096 * NB;
   uint32_t xw[LB];
 #pragma unroll
   for (int q = 0; q < LB; ++q) {
@@ -187,18 +200,20 @@ __global__ void __launch_bounds__(kWaves * 64, 1) lm_stream_kernel(LmArgs a) {
     // Every wave issues the same loads every k-step, so the waits below are static: a wave
     // without a block this round, and the k-steps past the last, re-read one cached line.
     const bool active = rd < my_cnt;  // wave-uniform
-    const int n0 = (rd * gw_total + gw) * 32;
+    const int n0 = (rd * gw_total + gw) * 32 * NB;
 #pragma unroll
     for (int q = 0; q < LB; ++q)
       woff[q] = active ? (uint32_t)((int64_t)min(n0 + q * 8 + (lane >> 3), a.N - 1) * a.ldw * 2) +
                              (uint32_t)((lane & 7) * 16)
                        : 0u;
     const int wstep = active ? kKS * 2 : 0;
-    floatx16 acc[MI];
+    floatx16 acc[MI][NB];
 #pragma unroll
     for (int i = 0; i < MI; ++i)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][nb][v] = 0.0f;
 
 #pragma unroll
     for (int h = 0; h < kDist; ++h) {
@@ -223,11 +238,15 @@ __global__ void __launch_bounds__(kWaves * 64, 1) lm_stream_kernel(LmArgs a) {
           for (int q = 0; q < LB; ++q) *(v4u*)(xp + xw[q]) = wr[sl][q];
 #pragma unroll
           for (int kk = 0; kk < 4; ++kk) {
-            const bf16x8 bf = *(const bf16x8*)(xp + foff[kk]);
+            bf16x8 bf[NB];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) bf[nb] = *(const bf16x8*)(xp + nb * 4096 + foff[kk]);
 #pragma unroll
             for (int i = 0; i < MI; ++i) {
               const bf16x8 af = *(const bf16x8*)(st + i * 32 * 128 + foff[kk]);
-              acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf, af, acc[i], 0, 0, 0);
+#pragma unroll
+              for (int nb = 0; nb < NB; ++nb)
+                acc[i][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[nb], af, acc[i][nb], 0, 0, 0);
             }
             // one piece's fragments live at a time (hoisting all four would spill at 256 rows)
             __builtin_amdgcn_sched_barrier(0);
@@ -244,33 +263,39 @@ __global__ void __launch_bounds__(kWaves * 64, 1) lm_stream_kernel(LmArgs a) {
     // still write them.
 #pragma unroll
     for (int h = 0; h < kDist; ++h)
-      asm volatile("" ::"v"(wr[h][0]), "v"(wr[h][1]), "v"(wr[h][2]), "v"(wr[h][3]));
+#pragma unroll
+      for (int q4 = 0; q4 < LB; q4 += 4)
+        asm volatile("" ::"v"(wr[h][q4]), "v"(wr[h][q4 + 1]), "v"(wr[h][q4 + 2]), "v"(wr[h][q4 + 3]));
     __builtin_amdgcn_sched_barrier(0);
 
-    // acc[i] is a tile of C^T: lane holds row m = 32 i + l32, columns n0 + 8 (v / 4) + 4 g + v % 4
+    // acc[i][nb] is a tile of C^T: lane holds row m = 32 i + l32, columns
+    // n0 + 32 nb + 8 (v / 4) + 4 g + v % 4
     if (a.out && active) {
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
         const int m = i * 32 + l32;
         if (m >= a.M) continue;
 #pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
         for (int v4 = 0; v4 < 4; ++v4) {
-          const int n = n0 + v4 * 8 + g * 4;
+          const int n = n0 + nb * 32 + v4 * 8 + g * 4;
           if (n >= a.N) continue;
           if constexpr (CDT == fg::kBF16) {
             uint16_t* o = (uint16_t*)a.out + (int64_t)m * a.ldo + n;
             if (n + 3 < a.N && (a.ldo & 3) == 0) {
-              *(uint2*)o = make_uint2(fg::pack_bf16x2(acc[i][4 * v4], acc[i][4 * v4 + 1]),
-                                      fg::pack_bf16x2(acc[i][4 * v4 + 2], acc[i][4 * v4 + 3]));
+              *(uint2*)o = make_uint2(fg::pack_bf16x2(acc[i][nb][4 * v4], acc[i][nb][4 * v4 + 1]),
+                                      fg::pack_bf16x2(acc[i][nb][4 * v4 + 2], acc[i][nb][4 * v4 + 3]));
             } else {
-              for (int e = 0; e < 4 && n + e < a.N; ++e) o[e] = fg::f32_to_bf16(acc[i][4 * v4 + e]);
+              for (int e = 0; e < 4 && n + e < a.N; ++e) o[e] = fg::f32_to_bf16(acc[i][nb][4 * v4 + e]);
             }
           } else {
             float* o = (float*)a.out + (int64_t)m * a.ldo + n;
             if (n + 3 < a.N && (a.ldo & 3) == 0) {
-              *(float4*)o = make_float4(acc[i][4 * v4], acc[i][4 * v4 + 1], acc[i][4 * v4 + 2], acc[i][4 * v4 + 3]);
+              *(float4*)o = make_float4(acc[i][nb][4 * v4], acc[i][nb][4 * v4 + 1], acc[i][nb][4 * v4 + 2],
+                                        acc[i][nb][4 * v4 + 3]);
             } else {
-              for (int e = 0; e < 4 && n + e < a.N; ++e) o[e] = acc[i][4 * v4 + e];
+              for (int e = 0; e < 4 && n + e < a.N; ++e) o[e] = acc[i][nb][4 * v4 + e];
             }
           }
         }
@@ -282,10 +307,13 @@ __global__ void __launch_bounds__(kWaves * 64, 1) lm_stream_kernel(LmArgs a) {
 #pragma unroll
         for (int i = 0; i < MI; ++i) {
 #pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
           for (int v = 0; v < 16; ++v) {
-            const int n = n0 + (v >> 2) * 8 + g * 4 + (v & 3);
+            const int n = n0 + nb * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
             if (n < a.N) {
-              const float val = CDT == fg::kBF16 ? fg::bf16_to_f32(fg::f32_to_bf16(acc[i][v])) : acc[i][v];
+              const float val =
+                  CDT == fg::kBF16 ? fg::bf16_to_f32(fg::f32_to_bf16(acc[i][nb][v])) : acc[i][nb][v];
               pm_max[i] = fmaxf(pm_max[i], val);
               const uint64_t k = fg::rank_key(val, (uint32_t)n);
               pm_key[i] = k > pm_key[i] ? k : pm_key[i];
@@ -298,25 +326,31 @@ __global__ void __launch_bounds__(kWaves * 64, 1) lm_stream_kernel(LmArgs a) {
       // this round's logits (bf16) into LDS: tile[m][32 wave + c], rows of kTileRow bytes
       __syncthreads();  // every wave is done reading the activation stages
       if (lane == 0) {
-        s_n0[wave] = n0;
-        s_nv[wave] = active ? min(32, a.N - n0) : 0;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          s_n0[wave * NB + nb] = n0 + nb * 32;
+          s_nv[wave * NB + nb] = active ? max(0, min(32, a.N - n0 - nb * 32)) : 0;
+        }
       }
       if (active) {
 #pragma unroll
         for (int i = 0; i < MI; ++i) {
           const int m = i * 32 + l32;
 #pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
           for (int v4 = 0; v4 < 4; ++v4) {
-            const int c = wave * 32 + v4 * 8 + g * 4;
-            *(uint2*)(smem + m * kTileRow + c * 2) = make_uint2(fg::pack_bf16x2(acc[i][4 * v4], acc[i][4 * v4 + 1]),
-                                                           fg::pack_bf16x2(acc[i][4 * v4 + 2], acc[i][4 * v4 + 3]));
+            const int c = (wave * NB + nb) * 32 + v4 * 8 + g * 4;
+            *(uint2*)(smem + m * kTileRow + c * 2) =
+                make_uint2(fg::pack_bf16x2(acc[i][nb][4 * v4], acc[i][nb][4 * v4 + 1]),
+                           fg::pack_bf16x2(acc[i][nb][4 * v4 + 2], acc[i][nb][4 * v4 + 3]));
           }
         }
       }
       __syncthreads();
       // TPR threads per row scan 8 columns at a time. Keys at or below the row's KT-th best
       // key of the earlier rounds cannot enter its list and are skipped.
-      constexpr int TPR = kWaves * 64 / MP;
+      constexpr int TPR = W * 64 / MP;
       const int m = tid / TPR, sub = tid % TPR;
       const bool row_ok = m < a.M && m < MP;
       const uint64_t thr = (row_ok && rd > 0) ? s_keys[m * KT + KT - 1] : 0ull;
@@ -379,9 +413,9 @@ __global__ void __launch_bounds__(kWaves * 64, 1) lm_stream_kernel(LmArgs a) {
   if constexpr (PM) {
     // lane groups 0 and 1 hold the same rows; then the waves' maxima meet in LDS
     __syncthreads();  // every wave is done with the activation stages
-    float* s_pmax = (float*)smem;                              // [kWaves][MP]
-    uint64_t* s_pkey = (uint64_t*)(smem + kWaves * MP * 4);   // [kWaves][MP]
-    static_assert(kWaves * MP * 12 <= kStages * STAGE, "row maxima staging");
+    float* s_pmax = (float*)smem;                         // [W][MP]
+    uint64_t* s_pkey = (uint64_t*)(smem + W * MP * 4);   // [W][MP]
+    static_assert(W * MP * 12 <= kStages * STAGE, "row maxima staging");
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
       const float mo = __shfl_xor(pm_max[i], 32, 64);
@@ -392,11 +426,11 @@ __global__ void __launch_bounds__(kWaves * 64, 1) lm_stream_kernel(LmArgs a) {
       }
     }
     __syncthreads();
-    for (int m = tid; m < a.M; m += kWaves * 64) {
+    for (int m = tid; m < a.M; m += W * 64) {
       float mx = s_pmax[m];
       uint64_t k = s_pkey[m];
 #pragma unroll
-      for (int w = 1; w < kWaves; ++w) {
+      for (int w = 1; w < W; ++w) {
         mx = fmaxf(mx, s_pmax[w * MP + m]);
         k = s_pkey[w * MP + m] > k ? s_pkey[w * MP + m] : k;
       }
@@ -406,7 +440,7 @@ __global__ void __launch_bounds__(kWaves * 64, 1) lm_stream_kernel(LmArgs a) {
   }
   if constexpr (KT > 0) {
     // this workgroup's part of every row
-    for (int m = tid; m < a.M; m += kWaves * 64) {
+    for (int m = tid; m < a.M; m += W * 64) {
       const int64_t pi = (int64_t)m * a.nparts + blockIdx.x;
 #pragma unroll
       for (int i = 0; i < KT; ++i) a.part_keys[pi * KT + i] = s_keys[m * KT + i];
@@ -433,8 +467,8 @@ struct Plan {
 Plan plan_for(int N) {
   const int nblk = (N + 31) / 32;
   Plan p;
-  p.grid = std::max(1, std::min(device_cus(), (nblk + kWaves - 1) / kWaves));
-  p.rmax = (nblk + p.grid * kWaves - 1) / (p.grid * kWaves);
+  p.grid = std::max(1, std::min(device_cus(), (nblk + kBlocks - 1) / kBlocks));
+  p.rmax = (nblk + p.grid * kBlocks - 1) / (p.grid * kBlocks);
   p.nparts = p.grid;
   return p;
 }
@@ -442,7 +476,8 @@ int k_bucket(int kmax) { return kmax <= 1 ? 1 : kmax <= 2 ? 2 : kmax <= 4 ? 4 : 
 
 template <int MI, int CDT, int KT, bool SAN, bool PM>
 void launch_mi(const LmArgs& a, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((lm_stream_kernel<MI, CDT, KT, SAN, PM>), dim3(grid), dim3(kWaves * 64), 0, s, a);
+  constexpr int W = waves_for(MI);
+  hipLaunchKernelGGL((lm_stream_kernel<MI, CDT, KT, SAN, PM, W>), dim3(grid), dim3(W * 64), 0, s, a);
 }
 template <int CDT, int KT, bool SAN, bool PM = false>
 void launch_rows(const LmArgs& a, int grid, hipStream_t s) {
