@@ -738,6 +738,7 @@ def main():
     # Phase rounds (continuing): the decoder's statistical_time mode synchronises
     # at each phase boundary, so the phases add up to slightly more than a round.
     phase_keys = ("medusa_time", "verify_time", "accept_time", "cache_time")
+    dec.flush(r)  # the queued round completes outside the phase rounds
     before = {k: r.m[k] for k in phase_keys}
     r.statistical_time = True
     n_phase = max(min(args.steps, 8), 1)
@@ -751,6 +752,7 @@ def main():
     phases["other"] = round(elapsed_p / n_phase * 1e3 - sum(phases.values()), 3)
     phases["rounds"] = n_phase
     log(f"phases (ms/round) {phases}")
+    dec.flush(r)  # the planted walk and gather work on the committed cache state
     planted = planted_walk_gather(cfg, r, work, elem)
     log(f"planted {planted}")
     full_rounds = None
@@ -815,6 +817,7 @@ def main():
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         n_cpu = args.cpu_rounds or (32 if args.config == "tiny" else 1)
+        dec.flush(r)
         cpu = cpu_baseline(model, heads, r, work, seed=args.seed + 2, rounds=n_cpu)
         log(f"cpu baseline {cpu['seconds']} s")
     res = {

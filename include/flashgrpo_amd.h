@@ -71,7 +71,7 @@ int fg_lm_head(const void* x, int dtype, int M, int K, int64_t ldx, const int32_
  * [M, 2], ranked and computed exactly as fg_medusa_topk does on the bf16 logits (sanitize
  * as there), without reading the logits back; workspace >=
  * fg_lm_head_topk_workspace(M, N, kmax). row_active (kmax 0 only): nothing is computed
- * when every flag is 0. part_max / part_key (optional; kmax 0 with out): each workgroup
+ * when every flag is 0, and rows whose flag is 0 are not written. part_max / part_key (optional; kmax 0 with out): each workgroup
  * writes, for every row m, the maximum of the row's stored logits over its columns (NaN
  * ignored) to part_max[m * P + p] and their largest rank key (value desc, index asc,
  * NaN first: the first maximum) to part_key[m * P + p], P = fg_lm_head_topk_parts(N):

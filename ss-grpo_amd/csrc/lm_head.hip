@@ -274,7 +274,7 @@ __global__ void __launch_bounds__(W * 64, 1) lm_stream_kernel(LmArgs a) {
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
         const int m = i * 32 + l32;
-        if (m >= a.M) continue;
+        if (m >= a.M || (a.row_active && !a.row_active[m])) continue;  // inactive rows stay unwritten
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll

@@ -152,15 +152,21 @@ class FlashMedusaConfig:
 
 def _quantile(values: np.ndarray, q: float) -> float:
     """Linear-interpolation quantile (torch.quantile's default)."""
-    v = np.sort(values.astype(np.float64))
-    pos = q * (v.size - 1)
+    return _quantile_rows(values.reshape(1, -1), q)[0]
+
+
+def _quantile_rows(values: np.ndarray, q: float) -> list:
+    """``_quantile`` of every row of a 2-D array (float64)."""
+    v = np.sort(values.astype(np.float64), axis=1)
+    pos = q * (v.shape[1] - 1)
     lo = int(math.floor(pos))
-    hi = min(lo + 1, v.size - 1)
-    return float(v[lo] + (v[hi] - v[lo]) * (pos - lo))
+    hi = min(lo + 1, v.shape[1] - 1)
+    return (v[:, lo] + (v[:, hi] - v[:, lo]) * (pos - lo)).tolist()
 
 
 class FlashMedusaDecoder:
     def __init__(self, target_model, medusa_heads, tokenizer, config: FlashMedusaConfig):
+        self._fit_cache = {}  # (adapted top-k, budget) -> fitted top-k
         if config.acceptance != "exact_target":
             raise NotImplementedError("Only exact_target acceptance is implemented in the main FlashGRPO path")
         if config.cache_update_mode not in {"extract_path", "recompute_accepted"}:
@@ -240,22 +246,27 @@ class FlashMedusaDecoder:
         cfg = self.config
         heads = min(len(plan.topk_by_depth), plan.active_heads)
         q = min(1.0, max(0.0, float(cfg.adaptive_confidence_quantile)))
-        confs = []
-        for d in range(heads):
-            rows = slice(d * batch, (d + 1) * batch)
-            if cfg.adaptive_confidence_metric == "margin":
-                sc = cand_scores[rows]
-                score = sc[:, 0] - sc[:, 1] if sc.shape[1] > 1 else sc[:, 0]
-            else:
-                st = stats[rows].astype(np.float64)
-                score = np.exp(st[:, 0] - st[:, 1])
-            confs.append(_quantile(np.nan_to_num(score, nan=0.0, posinf=0.0, neginf=0.0), q))
+        # every head at once (the host time here is on the round's critical path): per row
+        # the score, non-finite -> 0, then the linear-interpolation quantile per head
+        if cfg.adaptive_confidence_metric == "margin":
+            sc = cand_scores[:heads * batch].reshape(heads, batch, -1)
+            score = sc[..., 0] - sc[..., 1] if sc.shape[2] > 1 else sc[..., 0]
+        else:
+            st = stats[:heads * batch].astype(np.float64).reshape(heads, batch, 2)
+            score = np.exp(st[..., 0] - st[..., 1])
+        score = np.where(np.isfinite(score), score, 0.0).astype(np.float64)
+        confs = _quantile_rows(score, q)
         adapted = [self._topk_from_confidence(c, int(k), d) for d, (k, c) in
                    enumerate(zip(plan.topk_by_depth, confs))]
         if adapted:
-            adapted = fit_topk_to_budget(adapted, plan.node_budget_per_seq,
-                                         min_topk_by_depth=list(cfg.adaptive_min_topk_by_depth)[:len(adapted)],
-                                         depth_weight_decay=float(cfg.adaptive_depth_weight_decay))
+            key = (tuple(adapted), int(plan.node_budget_per_seq))
+            fitted = self._fit_cache.get(key)
+            if fitted is None:
+                fitted = self._fit_cache[key] = fit_topk_to_budget(
+                    adapted, plan.node_budget_per_seq,
+                    min_topk_by_depth=list(cfg.adaptive_min_topk_by_depth)[:len(adapted)],
+                    depth_weight_decay=float(cfg.adaptive_depth_weight_decay))
+            adapted = list(fitted)
         ks = [max(1, int(k)) for k in adapted]
         # a sparse plan takes the fitted list as its per-head node counts
         # (flashgrpo_b200/decoding/flash_medusa_decoder.py:1063-1077)
@@ -443,9 +454,89 @@ class FlashMedusaDecoder:
         r.err = torch.zeros(1, dtype=torch.int32, device=dev)
         return r
 
+    def _front(self, r: "Rollout", rnd: int, logits, hidden, row_map, pending, record: bool) -> dict:
+        """The device work that opens round ``rnd``: the root draw and, for Medusa
+        proposals, the heads and the tied LM head with the per-depth top-k (and row
+        stats) over the given next-state rows. Nothing here waits for the host."""
+        cfg = self.config
+        greedy = (not cfg.do_sample) or cfg.temperature == 0
+        Bc = int(row_map.shape[0])
+        roots = K.sample_tokens(logits, seed=r.seed, step=rnd, seq_ids=row_map, draw=0, forced=pending,
+                                temperature=cfg.temperature, greedy=greedy, top_k=cfg.top_k, top_p=cfg.top_p)
+        use_tree = r.generation_step >= int(cfg.enable_medusa_spec_after)
+        plan = self._plan(Bc) if use_tree else TreePlan(1, 0, [], 1, cfg.tree_mode, cfg.tree_layout)
+        use_chain = use_tree and cfg.proposal_mode == "chain" and r.generation_step >= int(cfg.chain_enable_after)
+        f = dict(rnd=rnd, batch=Bc, roots=roots, plan=plan, use_tree=use_tree, use_chain=use_chain, med=None)
+        if plan.active_heads > 0 and not use_chain:
+            proj = self.medusa_heads.project_all(hidden, plan.active_heads)
+            V = self.model.cfg.vocab
+            if plan.layout == "sparse_asymmetric":
+                # candidate lists of the sparse widths (adaptation only shrinks them)
+                kc = max(sparse_widths(list(plan.nodes_by_head or plan.topk_by_depth)[:3], V))
+            else:
+                kc = max(plan.topk_by_depth)
+            if cfg.adaptive_tree_enabled and cfg.adaptive_confidence_metric == "margin":
+                kc = max(kc, min(2, V))  # margin = top-1 - top-2 (flash_medusa_decoder.py:327-331)
+            with timing.label("medusa"):
+                f["med"] = self._medusa_candidates(proj, plan.active_heads, Bc, kc,
+                                                   stats=bool(cfg.adaptive_tree_enabled), logits=record)
+            if cfg.adaptive_tree_enabled:
+                _, _, score, stats = f["med"]
+                # what the adaptive plan reads back: (max, logsumexp) and the candidate scores
+                f["both_d"] = torch.cat([stats.view(stats.shape[0], -1), score.view(score.shape[0], -1)], 1)
+        return f
+
+    def _front_rows(self, f: dict, keep: np.ndarray) -> dict | None:
+        """``f`` restricted to the rows that continue (their draws and candidates do not
+        depend on the other rows), or None when the plan of the smaller batch differs."""
+        Bn = int(keep.size)
+        plan = self._plan(Bn) if f["use_tree"] else f["plan"]
+        if Bn == 0 or plan != f["plan"]:
+            return None
+        dev = f["roots"].device
+        kt = torch.from_numpy(keep).to(dev)
+        g = dict(f, batch=Bn, roots=f["roots"].index_select(0, kt))
+        if f["med"] is not None:
+            heads = f["plan"].active_heads
+            rows_np = (np.arange(heads)[:, None] * f["batch"] + keep[None, :]).reshape(-1)
+            rows = torch.from_numpy(rows_np).to(dev)
+            g["med"] = tuple(None if t is None else t.index_select(0, rows) for t in f["med"])
+            if f.get("both_d") is not None:
+                g["both_d"] = f["both_d"].index_select(0, rows)
+            if f.get("both_h") is not None:
+                g["both_h"] = f["both_h"][rows_np]
+        return g
+
     @torch.no_grad()
     def step(self, r: "Rollout", trace: list | None = None) -> int:
-        """One verify round over the active rows; returns the tokens it emitted."""
+        """One verify round over the active rows; returns the tokens it emitted.
+
+        Rounds are pipelined on the host: a round is queued (``_launch``: proposals, tree,
+        verify forward, walk, KV extraction, next state, the next round's proposals, the
+        read-back), and a call completes the queued round (``_complete``: its one host
+        sync, state update, finished rows dropped), queues the next round at once, and
+        only then does the completed round's bookkeeping (``_bookkeep``), so the GPU runs
+        the next round while the host works. Without pipelining (``statistical_time``,
+        a trace being recorded) a call queues and completes one round."""
+        ctx = r.inflight if r.inflight is not None else self._launch(r, trace)
+        r.inflight = None
+        res = self._complete(r, ctx, trace)
+        if r.active and not r.statistical_time and trace is None:
+            r.inflight = self._launch(r, None)
+        return self._bookkeep(r, ctx, res, trace)
+
+    @torch.no_grad()
+    def flush(self, r: "Rollout") -> int:
+        """Complete a round queued by ``step`` (returns its tokens; 0 if none is queued).
+        Call before reading or changing the rollout's device state directly."""
+        ctx, r.inflight = r.inflight, None
+        if ctx is None:
+            return 0
+        return self._bookkeep(r, ctx, self._complete(r, ctx, None), None)
+
+    def _launch(self, r: "Rollout", trace: list | None) -> dict:
+        """Queue one verify round; nothing here waits for the GPU except the adaptive
+        plan's read-back when the round's proposals were not queued by the previous one."""
         cfg = self.config
         model = self.model
         dev = r.device
@@ -455,11 +546,14 @@ class FlashMedusaDecoder:
         _, eos_id = self._token_ids()
         Bc = len(r.active)
         rnd = m["rounds"]
-        roots = K.sample_tokens(r.logits, seed=r.seed, step=rnd, seq_ids=r.row_map, draw=0, forced=r.pending,
-                                temperature=cfg.temperature, greedy=greedy, top_k=cfg.top_k, top_p=cfg.top_p)
-        use_tree = r.generation_step >= int(cfg.enable_medusa_spec_after)
-        plan = self._plan(Bc) if use_tree else TreePlan(1, 0, [], 1, cfg.tree_mode, cfg.tree_layout)
-        use_chain = use_tree and cfg.proposal_mode == "chain" and r.generation_step >= int(cfg.chain_enable_after)
+        f, r.front = r.front, None
+        if f is None or f["rnd"] != rnd or f["batch"] != Bc:
+            r.sync()
+            t0 = time.time()
+            f = self._front(r, rnd, r.logits, r.hidden, r.row_map, r.pending, trace is not None)
+            r.sync()
+            m["medusa_time"] += time.time() - t0
+        roots, plan, use_tree, use_chain = f["roots"], f["plan"], f["use_tree"], f["use_chain"]
         cand = score = mlog = tree_tokens = chain_conf = sparse = None
         chain_recs, chain_rows = [], []
         adaptive_stats = {}
@@ -476,25 +570,11 @@ class FlashMedusaDecoder:
             r.sync()
             m["medusa_time"] += time.time() - t0
         elif plan.active_heads > 0:
-            r.sync()
-            t0 = time.time()
-            proj = self.medusa_heads.project_all(r.hidden, plan.active_heads)
             V = self.model.cfg.vocab
-            if plan.layout == "sparse_asymmetric":
-                # candidate lists of the sparse widths (adaptation only shrinks them)
-                kc = max(sparse_widths(list(plan.nodes_by_head or plan.topk_by_depth)[:3], V))
-            else:
-                kc = max(plan.topk_by_depth)
-            if cfg.adaptive_tree_enabled and cfg.adaptive_confidence_metric == "margin":
-                kc = max(kc, min(2, V))  # margin = top-1 - top-2 (flash_medusa_decoder.py:327-331)
-            with timing.label("medusa"):
-                mlog, cand, score, stats = self._medusa_candidates(proj, plan.active_heads, Bc, kc,
-                                                                   stats=bool(cfg.adaptive_tree_enabled),
-                                                                   logits=trace is not None)
-            r.sync()
-            m["medusa_time"] += time.time() - t0
+            mlog, cand, score, stats = f["med"]
             if cfg.adaptive_tree_enabled:
-                both = torch.cat([stats.view(stats.shape[0], -1), score.view(score.shape[0], -1)], 1).cpu().numpy()
+                # read back with the previous round's results when that round queued this one
+                both = f["both_h"] if f.get("both_h") is not None else f["both_d"].cpu().numpy()
                 plan, adaptive_stats = self._adapt_plan(plan, both[:, :2], both[:, 2:], Bc)
             if plan.layout == "sparse_asymmetric" and plan.active_heads > 0:
                 sparse = sparse_tree_device(roots, cand, score, plan, Bc, V)
@@ -509,17 +589,12 @@ class FlashMedusaDecoder:
             topo = TreeTopology.for_plan(plan)
             N = topo.num_nodes
             D = topo.max_depth
-        r.plan_last = {"B_cur": Bc, "node_budget_per_seq": plan.node_budget_per_seq,
-                       "active_heads": plan.active_heads, "topk_by_depth": plan.topk_by_depth,
-                       "actual_nodes": plan.actual_nodes,
-                       "proposal_mode": ("chain" if use_chain else "medusa") if use_tree else "target_only",
-                       "adaptive_tree": adaptive_stats}
-        m["active_sum"] += Bc
-        m["samples"] += 1
+        plan_last = {"B_cur": Bc, "node_budget_per_seq": plan.node_budget_per_seq,
+                     "active_heads": plan.active_heads, "topk_by_depth": plan.topk_by_depth,
+                     "actual_nodes": plan.actual_nodes,
+                     "proposal_mode": ("chain" if use_chain else "medusa") if use_tree else "target_only",
+                     "adaptive_tree": adaptive_stats}
         if sparse is None:
-            m["node_sum"] += N
-            for dpt, c in topo.depth_counts.items():
-                r.proposed_by_depth[dpt] = r.proposed_by_depth.get(dpt, 0) + c * Bc
             dshared = topo.device(dev)
             dmap = topo.device(dev, Bc)
             tv = dict(pos_offset=dshared["pos_offset"], anc=dshared["anc"], parents=dmap["parents"],
@@ -530,6 +605,12 @@ class FlashMedusaDecoder:
                 tree_tokens, _ = K.tree_layout(cand, score, Bc, roots, dshared["depth"], dshared["rank"], N)
             else:
                 tree_tokens = roots.view(Bc, 1)
+        m["active_sum"] += Bc
+        m["samples"] += 1
+        if sparse is None:
+            m["node_sum"] += N
+            for dpt, cnt in topo.depth_counts.items():
+                r.proposed_by_depth[dpt] = r.proposed_by_depth.get(dpt, 0) + cnt * Bc
         # ---------------- verify forward + tree LM head
         tree_logits = slot_map = hidden_t = walk_logits = walk = None
         lazy = bool(cfg.lazy_walk_lm_head) and N > 1
@@ -595,6 +676,46 @@ class FlashMedusaDecoder:
         new_pending = torch.empty(Bc, dtype=torch.int32, device=dev) if b200 else None
         finished_d = K.accept_finalize(walk, r.seq, max_length=r.max_length, eos_token_id=eos_id,
                                        pending_root=new_pending)
+        # ---------------- cache update + next state, queued before the round's host sync (they
+        # need only device data, so the GPU has work while the host reads the round's results)
+        extracted = False
+        leaf_d = None
+        state_in = (r.logits, r.hidden)  # the round's inputs, for the trace
+        if cfg.cache_update_mode == "extract_path" and (tree_logits is not None or walk_logits is not None):
+            r.sync()
+            t0 = time.time()
+            r.cache.gather_path(r.seq, walk["acc_nodes"], walk["acc_len"], N, row_map=r.row_map, err_flag=r.err)
+            ar = torch.arange(Bc, device=dev)
+            last = walk["last_node"].long()
+            r.hidden = hidden_t[ar, last].contiguous()
+            if walk_logits is None and slot_map is None:
+                r.logits = tree_logits.index_select(0, ar * N + last)
+            else:
+                if walk_logits is not None:
+                    # the last accepted node at position acc_len-1 was sampled from at that
+                    # walk step unless it is a leaf (then it has no projected row)
+                    tpos = (walk["acc_len"].long() - 1).clamp(0, D - 1)
+                    r.logits = walk_logits[tpos, ar]
+                else:
+                    slots = slot_map[ar, last]
+                    r.logits = tree_logits.index_select(0, slots.clamp_min(0).long())
+                # rows whose last node is a leaf get their LM-head row here (no launch when none is)
+                if sparse is not None:
+                    leaf_d = (sparse["n_children"].gather(1, last.view(-1, 1)) == 0).view(-1).to(torch.int32)
+                else:
+                    leaf_d = dshared["leaf"].index_select(0, last)
+                with timing.label("leaf"):
+                    model.logits_masked(r.hidden, leaf_d, r.logits)
+            r.sync()
+            dt_ = time.time() - t0
+            m["extract_time"] += dt_
+            m["cache_time"] += dt_
+            m["extract_ok"] += 1
+            extracted = True
+        elif cfg.cache_update_mode == "extract_path" and plan.active_heads > 0:
+            m["extract_fallback"] += 1
+            if not cfg.allow_recompute_fallback:
+                raise RuntimeError("KV extraction was requested but no tree cache was available")
         # ---------------- the one host sync of the round
         W = walk["acc_tokens"].shape[1]
         cols = [walk["acc_tokens"], walk["acc_len"].view(-1, 1), finished_d.view(-1, 1),
@@ -605,17 +726,126 @@ class FlashMedusaDecoder:
             cols.append(new_pending.view(-1, 1))
         if sparse is not None:
             # last node is a leaf; nodes per row; non-root nodes per depth 2..D+1
-            leaf_d = sparse["n_children"].gather(1, walk["last_node"].long().view(-1, 1)) == 0
             per_depth = (sparse["depth"].unsqueeze(2) == torch.arange(2, D + 2, device=dev, dtype=torch.int32)).sum(1)
-            cols += [leaf_d.to(torch.int32), sparse["n_nodes"].view(-1, 1), per_depth.to(torch.int32)]
-        pack = torch.cat(cols, dim=1).cpu().numpy()
-        m["accept_time"] += time.time() - t_acc
-        if chain_conf is not None:
-            adaptive_stats["confidence"] = conf_h.tolist()
-        acc_tok_h, acc_len_h = pack[:, :W], pack[:, W]
-        fin_h, last_h = pack[:, W + 1].astype(bool), pack[:, W + 2]
+            leaf_s = sparse["n_children"].gather(1, walk["last_node"].long().view(-1, 1)) == 0
+            cols += [leaf_s.to(torch.int32), sparse["n_nodes"].view(-1, 1), per_depth.to(torch.int32)]
+        if leaf_d is not None:
+            cols.append(leaf_d.view(-1, 1))
+        pack_d = torch.cat(cols, dim=1)
+        nxt = None
+        if extracted and not r.statistical_time:
+            # The next round's opening work, queued before the read-back for every row (rows
+            # that finish this round are dropped from it afterwards).
+            # Its adaptive-plan statistics come back with this round's results: one host
+            # sync per round, and the GPU works while the host reads them.
+            nxt = self._front(r, rnd + 1, r.logits, r.hidden, r.row_map, new_pending if b200 else r.pending,
+                              trace is not None)
+        seq_next = r.seq + walk["acc_len"]  # committed lengths after this round (device)
+        pack_h = torch.empty(pack_d.shape, dtype=pack_d.dtype, pin_memory=True)
+        pack_h.copy_(pack_d, non_blocking=True)
+        both_h = None
+        if nxt is not None and nxt.get("both_d") is not None:
+            both_h = torch.empty(nxt["both_d"].shape, dtype=nxt["both_d"].dtype, pin_memory=True)
+            both_h.copy_(nxt["both_d"], non_blocking=True)
+        done = torch.cuda.Event()
+        done.record()
+        return dict(rnd=rnd, Bc=Bc, N=N, D=D, W=W, plan=plan, use_tree=use_tree, use_chain=use_chain,
+                    sparse=sparse, topo=None if sparse is not None else topo, roots=roots, mlog=mlog, cand=cand,
+                    tree_tokens=tree_tokens, tree_logits=tree_logits, slot_map=slot_map, hidden_t=hidden_t,
+                    walk_logits=walk_logits, walk=walk, new_pending=new_pending, extracted=extracted,
+                    leaf_d=leaf_d, state_in=state_in, seq_in=r.seq, active_in=list(r.active), ev_start=ev_start,
+                    chain_recs=chain_recs, chain_rows=chain_rows, chain_conf=chain_conf,
+                    conf_h=conf_h if chain_conf is not None else None, adaptive_stats=adaptive_stats,
+                    plan_last=plan_last, nxt=nxt, pack_h=pack_h, both_h=both_h, done=done, t_acc=t_acc,
+                    seq_next=seq_next)
+
+    def _complete(self, r: "Rollout", c: dict, trace: list | None) -> dict:
+        """Wait for a queued round's read-back and bring the rollout's state up to date:
+        committed lengths, the b200 pending roots, the next round's queued proposals,
+        and the rows that finished dropped. Returns the round's host arrays."""
+        cfg = self.config
+        model = self.model
+        dev = r.device
+        m = r.m
+        b200 = bool(cfg.emit_correction_token)
+        Bc, N, D, W, plan = c["Bc"], c["N"], c["D"], c["W"], c["plan"]
+        walk, walk_logits, hidden_t = c["walk"], c["walk_logits"], c["hidden_t"]
+        # spin on the event: a blocking wait adds its wake-up latency to the GPU's idle time
+        done = c["done"]
+        while not done.query():
+            pass
+        pack = c["pack_h"].numpy()
+        m["accept_time"] += time.time() - c["t_acc"]
+        # only what the next round needs before it is queued; the rest is read in _bookkeep
+        acc_len_h = pack[:, W]
+        fin_h = pack[:, W + 1].astype(bool)
         if int(pack[0, W + 3]):
             raise RuntimeError(f"flashgrpo_amd kernel reported an index error (flag {int(pack[0, W + 3])})")
+        nxt = c["nxt"]
+        if nxt is not None:
+            nxt["both_h"] = None if c["both_h"] is None else c["both_h"].numpy()
+            r.front = self._front_rows(nxt, np.nonzero(~fin_h)[0]) if fin_h.any() else nxt
+        # ---------------- next state when the cache is recomputed (extraction ran before the sync)
+        if not c["extracted"]:
+            r.sync()
+            t0 = time.time()
+            if N == 1 and hidden_t is not None:
+                # root-only round: the forward already wrote the root's K/V at slot seq_len
+                r.hidden = hidden_t[:, 0].contiguous()
+            else:
+                wmax = int(acc_len_h.max())
+                cols_ = torch.arange(wmax, device=dev)[None, :]
+                # entries past a row's accepted length are padding: use token 0
+                chain = torch.where(cols_ < walk["acc_len"][:, None], walk["acc_tokens"][:, :wmax],
+                                    torch.zeros((), dtype=torch.int32, device=dev)).contiguous()
+                h = model.forward(chain, r.cache, pos_offset=torch.arange(wmax, dtype=torch.int32, device=dev),
+                                  anc=as_mask_tensor(chain_bits(wmax), dev), seq_len=r.seq, row_map=r.row_map,
+                                  err_flag=r.err)
+                r.hidden = h[torch.arange(Bc, device=dev), (walk["acc_len"] - 1).long()].contiguous()
+            with timing.label("next"):
+                r.logits = model.logits(r.hidden)
+            r.sync()
+            dt_ = time.time() - t0
+            m["cache_time"] += dt_
+            if cfg.cache_update_mode == "extract_path" and plan.active_heads > 0:
+                m["recompute_time"] += dt_
+        if c["ev_start"] is not None and r.event_log is not None:
+            ev_end = torch.cuda.Event(enable_timing=True)
+            ev_end.record()
+            r.event_log.append((c["ev_start"], ev_end))
+        r.seq = c["seq_next"]
+        r.seq_h = r.seq_h + acc_len_h
+        if b200:
+            r.pending = c["new_pending"]
+        m["rounds"] += 1
+        if fin_h.any():
+            keep = np.nonzero(~fin_h)[0]
+            if keep.size == 0:
+                r.active = []
+            else:
+                kt = torch.from_numpy(keep).to(dev)
+                r.active = [r.active[i] for i in keep]
+                r.row_map = r.row_map.index_select(0, kt)
+                r.seq = r.seq.index_select(0, kt)
+                r.seq_h = r.seq_h[keep]
+                r.hidden = r.hidden.index_select(0, kt)
+                r.logits = r.logits.index_select(0, kt)
+                if b200:
+                    r.pending = r.pending.index_select(0, kt)
+        return dict(pack=pack, fin_h=fin_h)
+
+    def _parse_round(self, r: "Rollout", c: dict, h: dict) -> dict:
+        """The completed round's host arrays from its read-back (and the metrics in it)."""
+        m = r.m
+        b200 = bool(self.config.emit_correction_token)
+        D, W, walk_logits, sparse = c["D"], c["W"], c["walk_logits"], c["sparse"]
+        pack = h["pack"]
+        if c["chain_conf"] is not None:
+            c["adaptive_stats"]["confidence"] = c["conf_h"].tolist()
+        acc_tok_h, acc_len_h = pack[:, :W], pack[:, W]
+        last_h = pack[:, W + 2]
+        if c["leaf_d"] is not None:
+            m["tree_lm_head_rows"] += int(pack[:, -1].sum())
         col = W + 4
         walk_last_h = acc_nodes_h = None
         if walk_logits is not None:
@@ -625,6 +855,7 @@ class FlashMedusaDecoder:
         if b200:
             m["corrections"] += int(np.count_nonzero(pack[:, col] >= 0))
         sparse_leaf_h = None
+        sparse = c["sparse"]
         proposed_before = sum(r.proposed_by_depth.get(j + 2, 0) for j in range(D))
         if sparse is not None:
             c0 = col + (1 if b200 else 0)
@@ -632,10 +863,29 @@ class FlashMedusaDecoder:
             m["node_sum"] += float(pack[:, c0 + 1].mean())
             for j in range(D):
                 r.proposed_by_depth[j + 2] = r.proposed_by_depth.get(j + 2, 0) + int(pack[:, c0 + 2 + j].sum())
+        proposed_sparse = sum(r.proposed_by_depth.get(j + 2, 0) for j in range(D)) - proposed_before
+        return dict(pack=pack, acc_tok_h=acc_tok_h, acc_len_h=acc_len_h, fin_h=h["fin_h"], last_h=last_h,
+                    walk_last_h=walk_last_h, acc_nodes_h=acc_nodes_h, sparse_leaf_h=sparse_leaf_h,
+                    proposed_sparse=proposed_sparse, col=col)
+
+    def _bookkeep(self, r: "Rollout", c: dict, h: dict, trace: list | None) -> int:
+        """Host-only accounting of a completed round (tokens, histograms, metrics, the
+        trace record); returns the tokens it emitted."""
+        h = self._parse_round(r, c, h)
+        m = r.m
+        b200 = bool(self.config.emit_correction_token)
+        Bc, N, D, plan, sparse, topo = c["Bc"], c["N"], c["D"], c["plan"], c["sparse"], c["topo"]
+        pack, acc_tok_h, acc_len_h, fin_h, last_h = h["pack"], h["acc_tok_h"], h["acc_len_h"], h["fin_h"], h["last_h"]
+        walk_last_h, acc_nodes_h, sparse_leaf_h, col = h["walk_last_h"], h["acc_nodes_h"], h["sparse_leaf_h"], h["col"]
+        rnd = c["rnd"]
+        roots, mlog, cand, tree_tokens = c["roots"], c["mlog"], c["cand"], c["tree_tokens"]
+        tree_logits, slot_map, hidden_t, walk_logits = c["tree_logits"], c["slot_map"], c["hidden_t"], c["walk_logits"]
+        chain_recs, chain_rows, state_in = c["chain_recs"], c["chain_rows"], c["state_in"]
+        r.plan_last = c["plan_last"]
         if trace is not None:
-            rec = dict(round=rnd, active=list(r.active), plan=list(plan.topk_by_depth),
-                       budget=plan.node_budget_per_seq, seq_len=r.seq.cpu().numpy().copy(),
-                       logits_in=r.logits.float().cpu().numpy(), hidden_in=r.hidden.float().cpu().numpy(),
+            rec = dict(round=rnd, active=list(c["active_in"]), plan=list(plan.topk_by_depth),
+                       budget=plan.node_budget_per_seq, seq_len=c["seq_in"].cpu().numpy().copy(),
+                       logits_in=state_in[0].float().cpu().numpy(), hidden_in=state_in[1].float().cpu().numpy(),
                        roots=roots.cpu().numpy(), tree_tokens=tree_tokens.cpu().numpy(), acc_tokens=acc_tok_h.copy(),
                        acc_len=acc_len_h.copy(), finished=fin_h.copy(), last_node=last_h.copy(), seed=r.seed)
             if mlog is not None:
@@ -663,74 +913,6 @@ class FlashMedusaDecoder:
             if b200:
                 rec["pending"] = pack[:, col].copy()
             trace.append(rec)
-        # ---------------- cache update + next state
-        extracted = False
-        if cfg.cache_update_mode == "extract_path" and (tree_logits is not None or walk_logits is not None):
-            r.sync()
-            t0 = time.time()
-            r.cache.gather_path(r.seq, walk["acc_nodes"], walk["acc_len"], N, row_map=r.row_map, err_flag=r.err)
-            ar = torch.arange(Bc, device=dev)
-            last = walk["last_node"].long()
-            r.hidden = hidden_t[ar, last].contiguous()
-            if walk_logits is None and slot_map is None:
-                r.logits = tree_logits.index_select(0, ar * N + last)
-            else:
-                if walk_logits is not None:
-                    # the last accepted node at position acc_len-1 was sampled from at that
-                    # walk step unless it is a leaf (then it has no projected row)
-                    tpos = (walk["acc_len"].long() - 1).clamp(0, D - 1)
-                    r.logits = walk_logits[tpos, ar]
-                else:
-                    slots = slot_map[ar, last]
-                    r.logits = tree_logits.index_select(0, slots.clamp_min(0).long())
-                if sparse_leaf_h is not None:
-                    leaf = np.nonzero(sparse_leaf_h)[0]
-                else:
-                    leaf = np.nonzero(np.array([topo.slot_of[int(n)] < 0 for n in last_h]))[0]
-                if leaf.size:
-                    li = torch.from_numpy(leaf).to(dev)
-                    with timing.label("leaf"):
-                        r.logits.index_copy_(0, li, model.logits(r.hidden.index_select(0, li)))
-                    m["tree_lm_head_rows"] += int(leaf.size)
-            r.sync()
-            dt_ = time.time() - t0
-            m["extract_time"] += dt_
-            m["cache_time"] += dt_
-            m["extract_ok"] += 1
-            extracted = True
-        elif cfg.cache_update_mode == "extract_path" and plan.active_heads > 0:
-            m["extract_fallback"] += 1
-            if not cfg.allow_recompute_fallback:
-                raise RuntimeError("KV extraction was requested but no tree cache was available")
-        if not extracted:
-            r.sync()
-            t0 = time.time()
-            if N == 1 and hidden_t is not None:
-                # root-only round: the forward already wrote the root's K/V at slot seq_len
-                r.hidden = hidden_t[:, 0].contiguous()
-            else:
-                wmax = int(acc_len_h.max())
-                cols_ = torch.arange(wmax, device=dev)[None, :]
-                # entries past a row's accepted length are padding: use token 0
-                chain = torch.where(cols_ < walk["acc_len"][:, None], walk["acc_tokens"][:, :wmax],
-                                    torch.zeros((), dtype=torch.int32, device=dev)).contiguous()
-                h = model.forward(chain, r.cache, pos_offset=torch.arange(wmax, dtype=torch.int32, device=dev),
-                                  anc=as_mask_tensor(chain_bits(wmax), dev), seq_len=r.seq, row_map=r.row_map,
-                                  err_flag=r.err)
-                r.hidden = h[torch.arange(Bc, device=dev), (walk["acc_len"] - 1).long()].contiguous()
-            with timing.label("next"):
-                r.logits = model.logits(r.hidden)
-            r.sync()
-            dt_ = time.time() - t0
-            m["cache_time"] += dt_
-            if cfg.cache_update_mode == "extract_path" and plan.active_heads > 0:
-                m["recompute_time"] += dt_
-        if ev_start is not None:
-            ev_end = torch.cuda.Event(enable_timing=True)
-            ev_end.record()
-            r.event_log.append((ev_start, ev_end))
-        r.seq = r.seq + walk["acc_len"]
-        r.seq_h = r.seq_h + acc_len_h
         if walk_last_h is not None:
             draws = walk_last_h.astype(np.int64) + 1
         elif N > 1 and sparse_leaf_h is not None:
@@ -745,15 +927,13 @@ class FlashMedusaDecoder:
                             last_node=last_h.copy(), walk_draws=draws, heads=plan.active_heads, batch=Bc,
                             lazy=walk_last_h is not None, walk_steps=D if walk_last_h is not None else 0,
                             chain_rows=list(chain_rows))
-        if b200:
-            r.pending = new_pending
         # ---------------- bookkeeping
-        m["rounds"] += 1
         lens = acc_len_h.astype(np.int64)
         emitted = int(lens.sum())
         toks = acc_tok_h.tolist()
+        active_in = c["active_in"]
         for i, L in enumerate(lens.tolist()):
-            r.generated[r.active[i]].extend(toks[i][:L])
+            r.generated[active_in[i]].extend(toks[i][:L])
         for L, c in enumerate(np.bincount(lens).tolist()):
             if c:
                 r.accept_hist[L] = r.accept_hist.get(L, 0) + c
@@ -763,31 +943,19 @@ class FlashMedusaDecoder:
         m["total_decoded_steps"] += Bc
         m["accepted"] += int(np.maximum(lens - 1, 0).sum())
         if sparse is not None:
-            m["proposed"] += sum(r.proposed_by_depth.get(j + 2, 0) for j in range(D)) - proposed_before
+            m["proposed"] += h["proposed_sparse"]
         else:
             m["proposed"] += max(N - 1, 0) * Bc
-        if fin_h.any():
-            keep = np.nonzero(~fin_h)[0]
-            if keep.size == 0:
-                r.active = []
-            else:
-                kt = torch.from_numpy(keep).to(dev)
-                r.active = [r.active[i] for i in keep]
-                r.row_map = r.row_map.index_select(0, kt)
-                r.seq = r.seq.index_select(0, kt)
-                r.seq_h = r.seq_h[keep]
-                r.hidden = r.hidden.index_select(0, kt)
-                r.logits = r.logits.index_select(0, kt)
-                if b200:
-                    r.pending = r.pending.index_select(0, kt)
         return emitted
 
     def finish(self, r: "Rollout") -> dict:
         """Result dict with the keys of ``flash_medusa_decoder.py:1189-1229``."""
         cfg = self.config
         m = r.m
+        self.flush(r)
         if r.cache is not None:
             self.model.drop_graphs(r.cache)  # the rollout's cache goes with it
+        r.front = None
         total_time = time.time() - r.total_start
         accept_rate = m["accepted"] / max(m["proposed"], 1)
         avg_accept = m["total_acc_length"] / max(m["total_decoded_steps"], 1)
@@ -870,6 +1038,8 @@ class Rollout:
         self.active = []
         self.row_map = self.seq = self.hidden = self.logits = self.pending = self.err = None
         self.seq_h = None
+        self.front = None  # the next round's queued opening work (FlashMedusaDecoder._front)
+        self.inflight = None  # a queued round not yet completed (FlashMedusaDecoder.step)
         self.generated = []
         self.prefill_time = 0.0
         self.total_start = time.time()

@@ -307,7 +307,8 @@ class TreeTopology:
             arr = np.array([b & 0xFFFFFFFFFFFFFFFF for b in self.anc_bits], dtype=np.uint64).view(np.int64)
             d = dict(depth=torch.tensor(self.depths, **i32), rank=torch.tensor(self.ranks, **i32),
                      pos_offset=torch.tensor([x - 1 for x in self.depths], **i32),
-                     anc=torch.from_numpy(arr).to(device))
+                     anc=torch.from_numpy(arr).to(device),
+                     leaf=torch.tensor([1 if s < 0 else 0 for s in self.slot_of], **i32))
             if batch is not None:
                 N, I = self.num_nodes, len(self.internal)
                 d["parents"] = torch.tensor([self.parents] * batch, **i32)

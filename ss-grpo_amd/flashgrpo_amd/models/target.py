@@ -616,6 +616,19 @@ class TargetModel:
             raise ValueError("logits: row maxima parts need the weight-streaming LM head (see walk_parts)")
         return K.lm_head(x, w, row_index=row_index, row_active=row_active, out=out, out_dtype=out_dtype)
 
+    def logits_masked(self, hidden: torch.Tensor, row_active: torch.Tensor, out: torch.Tensor) -> None:
+        """out[m] = LM-head row of hidden[m] where row_active[m] != 0; the other rows of out
+        keep their contents (nothing is computed when no row is active). Decided on the
+        device, so a caller need not know the active rows."""
+        x = hidden.reshape(-1, self.cfg.hidden)
+        w = self.w["lm_head"]
+        if (self.dtype == torch.bfloat16 and out.dtype == torch.bfloat16 and 0 < x.shape[0] <= LM_STREAM_ROWS
+                and x.stride(1) == 1 and w.stride(1) == 1 and (x.numel() + x.storage_offset()) * 2 < 1 << 32):
+            K.lm_head_topk(x, w, 0, row_active=row_active, out=out)  # inactive rows are not written
+            return
+        tmp = K.lm_head(x, w, row_active=row_active, out_dtype=out.dtype)
+        torch.where(row_active.view(-1, 1) != 0, tmp, out, out=out)
+
     def logits_topk(self, hidden: torch.Tensor, kmax: int, *, stats: bool = False, sanitize: bool = False,
                     logits: bool = False, weight: torch.Tensor | None = None, workspace=None):
         """LM-head rows with each row's top-kmax candidates (value desc, index asc) and

@@ -594,3 +594,42 @@ def test_hf_target_resynced_between_rollouts():
         assert st["rounds"] == out["total_verify_rounds"] > 0
         outs.append(out["generated_token_ids"])
     assert outs[0] != outs[1]  # the second rollout really sampled the new policy
+
+
+@pytest.mark.parametrize("mode", ["adaptive", "b200_sparse", "chain"])
+def test_pipelined_rounds_equal_sequential_rounds(mode):
+    """step() queues the next round (proposals, verify, walk, extraction) before the
+    completed round's bookkeeping and reads the next round's adaptive-plan statistics
+    back with the current round's results. The rollout emits exactly the tokens and
+    metrics of the same rollout run one round at a time (statistical_time) and of the
+    traced run, with rows finishing at different rounds (EOS and max_length)."""
+    from flashgrpo_amd.decoding import FlashMedusaConfig, FlashMedusaDecoder
+
+    W = OM.random_weights(SMALL16, seed=5, std=0.05)
+    heads = OM.random_medusa(SMALL16.hidden, 4, seed=6, std=0.05)
+    cell = OM.random_chain_cell(SMALL16.hidden, seed=7, std=0.05, gate_init=-1.0) if mode == "chain" else None
+    model, mh = build(SMALL16, W, heads, torch.bfloat16, cell)
+    kw = dict(num_medusa_heads=4, tree_mode="concurrency_aware", cpeak_nodes=64, max_tree_nodes_per_seq=24,
+              adaptive_tree_enabled=True, adaptive_min_topk_by_depth=(1, 1, 1), adaptive_confidence_low=0.02,
+              adaptive_confidence_high=0.1, top_p=0.95, noise_seed=21)
+    if mode == "b200_sparse":
+        kw.update(tree_layout="sparse_asymmetric", emit_correction_token=True)
+    if mode == "chain":
+        kw.update(proposal_mode="chain", adaptive_tree_enabled=False)
+    prompts = np.random.default_rng(4).integers(0, SMALL16.vocab, (3, 19))
+    outs = []
+    for how in ("pipelined", "statistical", "traced"):
+        dec = FlashMedusaDecoder(model, mh, Tok(5), FlashMedusaConfig(**kw))
+        out = dec.generate(torch.from_numpy(prompts), torch.ones(3, 19, dtype=torch.long), repeated_generate_nums=3,
+                           max_length=19 + 30, statistical_time=how == "statistical",
+                           trace=[] if how == "traced" else None)
+        outs.append(out)
+    keys = ("total_verify_rounds", "total_accepted_draft_tokens", "total_proposed_draft_tokens",
+            "average_active_batch_size", "average_tree_nodes_per_seq", "tree_lm_head_rows", "accept_length_histogram",
+            "medusa_proposed_by_depth", "last_tree_plan")
+    for o in outs[1:]:
+        assert o["generated_token_ids"] == outs[0]["generated_token_ids"]
+        for k in keys:
+            assert o[k] == outs[0][k], k
+    lens = [len(g) for g in outs[0]["generated_token_ids"]]
+    assert len(set(lens)) > 1  # rows finished at different rounds

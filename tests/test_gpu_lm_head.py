@@ -135,7 +135,28 @@ def test_row_active_skips_launch():
     act = torch.zeros(8, dtype=torch.int32, device=DEV)
     act[6] = 1
     K().lm_head_topk(x, w, 0, out=out, row_active=act)
-    assert rel_err(to_np(out), to_np(x.float() @ w.float().t())) < 2e-2
+    # the active row is written, the others keep their contents
+    assert rel_err(to_np(out[6]), to_np(x[6].float() @ w.float().t())) < 2e-2
+    assert bool((out[:6] == 3.0).all()) and bool((out[7:] == 3.0).all())
+
+
+def test_target_logits_masked_writes_active_rows_only():
+    from flashgrpo_amd.models.target import TargetModel, TargetConfig
+
+    for dtype in (torch.bfloat16, torch.float32):
+        cfg = TargetConfig(num_layers=1, hidden=128, q_heads=2, kv_heads=1, head_dim=64, intermediate=256, vocab=3001)
+        model = TargetModel.random(cfg, seed=2, dtype=dtype, device=DEV)
+        h = torch.randn(20, 128, device=DEV).to(dtype)
+        out = torch.full((20, 3001), 5.0, dtype=dtype, device=DEV)
+        act = torch.zeros(20, dtype=torch.int32, device=DEV)
+        act[[1, 7, 19]] = 1
+        model.logits_masked(h, act, out)
+        full = model.logits(h)
+        rows = act.bool()
+        assert torch.equal(out[rows], full[rows]), dtype
+        assert bool((out[~rows] == 5.0).all()), dtype
+        model.logits_masked(h, torch.zeros_like(act), out)  # no active row: nothing changes
+        assert torch.equal(out[rows], full[rows]) and bool((out[~rows] == 5.0).all())
 
 
 def test_rejects_unsupported_shapes():
