@@ -196,11 +196,19 @@ def planted_walk_gather(cfg, r, work, elem, reps=5):
     w_us = sum(a.elapsed_time(b) for a, b in walk_ms) / len(walk_ms) * 1e3
     g_us = sum(a.elapsed_time(b) for a, b in gather_ms) / len(gather_ms) * 1e3
     w_bytes = B * V * elem
-    g_bytes = 2 * cfg.num_layers * 2 * B * cfg.kv_heads * (D + 1) * cfg.head_dim * elem
+    # rows a path keeps in place (the root, and node j == j) are not moved: the bytes are
+    # the moved rows' reads and writes; ref_bytes also counts the rows left in place (the
+    # reference's gather + copy_ reads and writes every accepted row)
+    nodes = walk["acc_nodes"][:, :D + 1].long()
+    moved = int((nodes != torch.arange(D + 1, device=dev)[None, :]).sum())
+    row_bytes = 2 * cfg.num_layers * 2 * cfg.kv_heads * cfg.head_dim * elem
+    g_bytes = row_bytes * moved
+    g_ref_bytes = row_bytes * B * (D + 1)
     return {"depth": D, "sequences": B,
             "walk_step": {"avg_us": round(w_us, 2), "bytes": w_bytes, "GBps": round(w_bytes / w_us / 1e3, 1),
                           "hbm_frac": round(w_bytes / w_us / 1e3 / HBM_PEAK_GBS, 4)},
-            "kv_path_gather": {"avg_us": round(g_us, 2), "bytes": g_bytes, "GBps": round(g_bytes / g_us / 1e3, 1),
+            "kv_path_gather": {"avg_us": round(g_us, 2), "bytes": g_bytes, "moved_rows": moved,
+                               "ref_bytes": g_ref_bytes, "GBps": round(g_bytes / g_us / 1e3, 1),
                                "hbm_frac": round(g_bytes / g_us / 1e3 / HBM_PEAK_GBS, 4)}}
 
 

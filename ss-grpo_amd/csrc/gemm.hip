@@ -13,6 +13,7 @@
 // 414-433, 1079-1091 and MedusaPredictionHead.project_hidden
 // (flashgrpo/models/medusa_heads.py:74-78).
 #include "fg_common.h"
+#include "fg_stream.h"
 
 #include <algorithm>
 
@@ -842,8 +843,15 @@ int fg_lm_head(const void* x, int dtype, int M, int K, int64_t ldx, const int32_
   return launch_gemm(g, dtype, out_dtype, kEpiNone, 1, (hipStream_t)stream);
 }
 
+// The normalised rows, then (bf16, weight-streamed fc) the fp32 partial sums 16-byte aligned.
+static size_t medusa_ln_bytes(int batch, int hidden, int heads, int dtype) {
+  return ((size_t)batch * hidden * heads * fg::elem_bytes(dtype) + 15) & ~(size_t)15;
+}
+
 size_t fg_medusa_heads_workspace(int batch, int hidden, int heads, int dtype) {
-  return (size_t)batch * hidden * heads * fg::elem_bytes(dtype) + 256;
+  if (batch <= 0 || hidden <= 0 || heads <= 0) return 256;
+  const size_t parts = dtype == fg::kBF16 ? fg::medusa_stream_parts_bytes(batch, hidden, heads) : 0;
+  return medusa_ln_bytes(batch, hidden, heads, dtype) + parts + 256;
 }
 
 // out[h*B + b, :] = hidden[b] + SiLU(fc_h(LayerNorm_h(hidden[b]))) for each head h.
@@ -853,7 +861,7 @@ int fg_medusa_heads(const void* hidden, int dtype, int batch, int H, int64_t ldh
   FG_REQUIRE(hidden && ln_w && ln_b && fc_w && fc_b && out && workspace, "fg_medusa_heads: null pointer");
   FG_REQUIRE(batch > 0 && H > 0 && heads > 0, "fg_medusa_heads: empty shape");
   FG_REQUIRE(dtype == fg::kF32 || dtype == fg::kBF16, "fg_medusa_heads: dtype");
-  FG_REQUIRE(workspace_bytes >= (size_t)batch * H * heads * fg::elem_bytes(dtype), "fg_medusa_heads: workspace");
+  FG_REQUIRE(workspace_bytes >= fg_medusa_heads_workspace(batch, H, heads, dtype) - 256, "fg_medusa_heads: workspace");
   hipStream_t s = (hipStream_t)stream;
   const bool vec = H % 8 == 0 && H <= 8 * 256 * 4 && ldh % 8 == 0 && ((uintptr_t)hidden & 15) == 0 &&
                    ((uintptr_t)workspace & 15) == 0 && ((uintptr_t)ln_w & 15) == 0 && ((uintptr_t)ln_b & 15) == 0;
@@ -871,6 +879,11 @@ int fg_medusa_heads(const void* hidden, int dtype, int batch, int H, int64_t ldh
                        batch, ln_w, ln_b, ln_eps, workspace);
   int rc = fg::check_launch("fg_medusa_heads(ln)");
   if (rc) return rc;
+  if (vec && dtype == fg::kBF16 && fg::medusa_stream_ok(batch, H, heads) && ldh % 4 == 0 &&
+      ((uintptr_t)out & 15) == 0 && ((uintptr_t)fc_w & 15) == 0 && ((uintptr_t)fc_b & 7) == 0) {
+    float* parts = (float*)((char*)workspace + medusa_ln_bytes(batch, H, heads, dtype));
+    return fg::medusa_stream(workspace, batch, H, heads, fc_w, fc_b, hidden, ldh, dtype, out, out_dtype, parts, s);
+  }
   GemmArgs g{};
   g.A = workspace; g.lda = H; g.a_batch = (int64_t)batch * H;
   g.B = fc_w; g.ldb = H; g.b_batch = (int64_t)H * H;

@@ -30,26 +30,33 @@ __global__ void __launch_bounds__(kThreads) kv_path_gather_kernel(
   r /= kv_heads;
   const int b = r % batch;
   const int t = r / batch;
+  const int32_t* nodes = acc_nodes + (int64_t)b * acc_stride;
+  // Every per-sequence value is loaded in one round trip (the path entries up to the row
+  // stride, independent of its length), then the whole row is validated before touching
+  // the caches.
   const int n_acc = acc_len[b];
   const int s0 = seq_len[b];
-  const int32_t* nodes = acc_nodes + (int64_t)b * acc_stride;
-  // Validate the whole row before touching memory.
+  const int cb = row_map ? row_map[b] : b;
+  const uint64_t tptr = tensor_ptrs[t];
+  int nd[MAXACC];
+#pragma unroll
+  for (int j = 0; j < MAXACC; ++j) nd[j] = j < acc_stride ? nodes[j] : j;
   bool ok = n_acc >= 1 && n_acc <= acc_stride && n_acc <= tree_nodes && s0 >= 0 && s0 + tree_nodes <= capacity;
-  for (int j = 0; j < n_acc && ok; ++j) ok = nodes[j] >= 0 && nodes[j] < tree_nodes;
+#pragma unroll
+  for (int j = 0; j < MAXACC; ++j) {
+    ok &= j >= n_acc || (nd[j] >= 0 && nd[j] < tree_nodes);
+    nd[j] = j < n_acc ? nd[j] : j;
+  }
   if (!ok) {
     if (t == 0 && h == 0 && col == 0 && err_flag) atomicOr(err_flag, 1);
     return;
   }
-  const int cb = row_map ? row_map[b] : b;
-  char* base = (char*)(uintptr_t)tensor_ptrs[t] + (int64_t)cb * batch_stride_b + (int64_t)h * head_stride_b +
+  char* base = (char*)(uintptr_t)tptr + (int64_t)cb * batch_stride_b + (int64_t)h * head_stride_b +
                (int64_t)col * 16 + (int64_t)s0 * row_stride_b;
   uint4 v[MAXACC];
-  int nd[MAXACC];
 #pragma unroll
-  for (int j = 0; j < MAXACC; ++j) {
-    nd[j] = j < n_acc ? nodes[j] : j;
+  for (int j = 0; j < MAXACC; ++j)
     v[j] = nd[j] != j ? *(const uint4*)(base + (int64_t)nd[j] * row_stride_b) : make_uint4(0, 0, 0, 0);
-  }
 #pragma unroll
   for (int j = 0; j < MAXACC; ++j)
     if (nd[j] != j) *(uint4*)(base + (int64_t)j * row_stride_b) = v[j];

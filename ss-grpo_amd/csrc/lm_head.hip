@@ -80,11 +80,18 @@ struct LmArgs {
   float* part_max;      // [M, nparts] (PM): max of the stored logits, NaN ignored
   uint64_t* part_key;   // [M, nparts] (PM): largest rank key (the first maximum, NaN first)
   int nparts;  // = grid: one part per workgroup
+  // Medusa fc (MED): `heads` products of the same shape, x, w and out advancing per head,
+  // each cut into `ksplit` key ranges. Workgroup task t = (h * ksplit + p) * ngroups + c
+  // computes columns [256 c, 256 c + 256) of head h over k-steps
+  // [p * KST / ksplit, (p + 1) * KST / ksplit) into fp32 rows (p * heads + h) * M + m of out.
+  int heads, ksplit, ngroups;
+  int64_t x_head_bytes, w_head_bytes;
 };
 
-template <int MI, int CDT, int KT, bool SAN, bool PM, int W>
+template <int MI, int CDT, int KT, bool SAN, bool PM, int W, bool MED = false>
 __global__ void __launch_bounds__(W * 64, 1) lm_stream_kernel(LmArgs a) {
   static_assert(!PM || KT == 0, "row maxima parts come with the logits-only epilogue");
+  static_assert(!MED || (KT == 0 && !PM && CDT == fg::kF32), "Medusa tasks write fp32 partial sums only");
   constexpr int NB = kBlocks / W;  // 32-column blocks per wave and round
   static_assert(NB * W == kBlocks, "waves");
   constexpr int kDist = dist_for(MI), kStages = kDist + 1;
@@ -124,7 +131,9 @@ __global__ void __launch_bounds__(W * 64, 1) lm_stream_kernel(LmArgs a) {
   const int gw = wave * gridDim.x + blockIdx.x;
   const int q = nblk / gw_total, rem = nblk % gw_total;
   const int my_cnt = q + (gw < rem ? 1 : 0);
-  const int rounds = q + ((int)blockIdx.x < rem ? 1 : 0);  // wave 0 has the most blocks
+  // wave 0 has the most blocks; Medusa tasks are dealt out per workgroup (grid <= tasks)
+  const int rounds = MED ? (a.heads * a.ksplit * a.ngroups - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x
+                         : q + ((int)blockIdx.x < rem ? 1 : 0);
   const int KST = a.K / kKS;
 
   // activation staging: load u of this wave fills LDS rows (wave * LA + u) * 8 + lane / 8
@@ -138,8 +147,8 @@ __global__ void __launch_bounds__(W * 64, 1) lm_stream_kernel(LmArgs a) {
     xoff[u] = (uint32_t)((int64_t)src * a.ldx * 2) + (uint32_t)(a_pos(r, lane & 7) * 16);
   }
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem + wave * LA * 1024;
-  auto issue_x = [&](int ks, int stage) __attribute__((always_inline)) {
-    const uint32_t koff = (uint32_t)ks * (kKS * 2);
+  // koff: byte offset of the k-step within the rows (plus the head's offset for MED)
+  auto issue_x = [&](uint32_t koff, int stage) __attribute__((always_inline)) {
     const uint32_t st = (uint32_t)stage * STAGE;
 #pragma unroll
     for (int u = 0; u < LA; ++u) {
@@ -199,14 +208,31 @@ __global__ void __launch_bounds__(W * 64, 1) lm_stream_kernel(LmArgs a) {
   for (int rd = 0; rd < rounds; ++rd) {
     // Every wave issues the same loads every k-step, so the waits below are static: a wave
     // without a block this round, and the k-steps past the last, re-read one cached line.
-    const bool active = rd < my_cnt;  // wave-uniform
-    const int n0 = (rd * gw_total + gw) * 32 * NB;
+    bool active = rd < my_cnt;  // wave-uniform
+    int n0 = (rd * gw_total + gw) * 32 * NB;
+    // k-steps [kb, kb + kst) (workgroup-uniform); xb / wb: byte offsets of the first k-step
+    // in x and in this wave's weight rows; orow: first output row
+    int kb = 0, kst = KST;
+    uint32_t xb = 0, wb = 0;
+    int64_t orow = 0;
+    if constexpr (MED) {
+      const int t = rd * (int)gridDim.x + (int)blockIdx.x;
+      const int c = t % a.ngroups, hp = t / a.ngroups, p = hp % a.ksplit, h = hp / a.ksplit;
+      n0 = c * (32 * kBlocks) + wave * 32 * NB;
+      active = n0 < a.N;
+      kb = p * KST / a.ksplit;
+      kst = (p + 1) * KST / a.ksplit - kb;
+      xb = (uint32_t)(h * a.x_head_bytes) + (uint32_t)kb * (kKS * 2);
+      wb = active ? (uint32_t)(h * a.w_head_bytes) + (uint32_t)kb * (kKS * 2) : 0u;
+      orow = (int64_t)(p * a.heads + h) * a.M;
+    }
 #pragma unroll
     for (int q = 0; q < LB; ++q)
       woff[q] = active ? (uint32_t)((int64_t)min(n0 + q * 8 + (lane >> 3), a.N - 1) * a.ldw * 2) +
                              (uint32_t)((lane & 7) * 16)
                        : 0u;
     const int wstep = active ? kKS * 2 : 0;
+    const uint32_t xstep = kKS * 2;
     floatx16 acc[MI][NB];
 #pragma unroll
     for (int i = 0; i < MI; ++i)
@@ -217,10 +243,10 @@ __global__ void __launch_bounds__(W * 64, 1) lm_stream_kernel(LmArgs a) {
 
 #pragma unroll
     for (int h = 0; h < kDist; ++h) {
-      issue_x(h < KST ? h : 0, h % kStages);
-      issue_w(wr[h], h < KST ? h * wstep : 0);
+      issue_x(xb + (h < kst ? h : 0) * xstep, h % kStages);
+      issue_w(wr[h], wb + (h < kst ? h * wstep : 0));
     }
-    for (int k0 = 0; k0 < KST; k0 += kDist) {
+    for (int k0 = 0; k0 < kst; k0 += kDist) {
 #pragma unroll
       for (int sl = 0; sl < kDist; ++sl) {
         const int ks = k0 + sl;
@@ -230,8 +256,8 @@ __global__ void __launch_bounds__(W * 64, 1) lm_stream_kernel(LmArgs a) {
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         const int kn = ks + kDist;
-        issue_x(kn < KST ? kn : 0, kn % kStages);
-        if (ks < KST && active) {
+        issue_x(xb + (kn < kst ? kn : 0) * xstep, kn % kStages);
+        if (ks < kst && active) {
           const unsigned char* st = smem + (ks % kStages) * STAGE;
           // the weight pieces into operand layout (this wave read the previous ones already)
 #pragma unroll
@@ -254,7 +280,7 @@ __global__ void __launch_bounds__(W * 64, 1) lm_stream_kernel(LmArgs a) {
         }
         __builtin_amdgcn_sched_barrier(0);
         // the weight slot is free once its pieces are in LDS
-        issue_w(wr[sl], kn < KST ? kn * wstep : 0);
+        issue_w(wr[sl], wb + (kn < kst ? kn * wstep : 0));
       }
     }
     wait_vmcnt<0>();
@@ -282,7 +308,7 @@ __global__ void __launch_bounds__(W * 64, 1) lm_stream_kernel(LmArgs a) {
           const int n = n0 + nb * 32 + v4 * 8 + g * 4;
           if (n >= a.N) continue;
           if constexpr (CDT == fg::kBF16) {
-            uint16_t* o = (uint16_t*)a.out + (int64_t)m * a.ldo + n;
+            uint16_t* o = (uint16_t*)a.out + (orow + m) * a.ldo + n;
             if (n + 3 < a.N && (a.ldo & 3) == 0) {
               *(uint2*)o = make_uint2(fg::pack_bf16x2(acc[i][nb][4 * v4], acc[i][nb][4 * v4 + 1]),
                                       fg::pack_bf16x2(acc[i][nb][4 * v4 + 2], acc[i][nb][4 * v4 + 3]));
@@ -290,7 +316,7 @@ __global__ void __launch_bounds__(W * 64, 1) lm_stream_kernel(LmArgs a) {
               for (int e = 0; e < 4 && n + e < a.N; ++e) o[e] = fg::f32_to_bf16(acc[i][nb][4 * v4 + e]);
             }
           } else {
-            float* o = (float*)a.out + (int64_t)m * a.ldo + n;
+            float* o = (float*)a.out + (orow + m) * a.ldo + n;
             if (n + 3 < a.N && (a.ldo & 3) == 0) {
               *(float4*)o = make_float4(acc[i][nb][4 * v4], acc[i][nb][4 * v4 + 1], acc[i][nb][4 * v4 + 2],
                                         acc[i][nb][4 * v4 + 3]);
@@ -497,7 +523,117 @@ void launch_san(const LmArgs& a, int out_dtype, bool san, int grid, hipStream_t 
   else launch_cdt<KT, false>(a, out_dtype, grid, s);
 }
 
+// ------------------------------------------------------------------ Medusa fc
+constexpr int kMedMaxSplit = 8;
+
+struct MedPlan {
+  int ngroups, ksplit, grid;
+};
+// As many key ranges as keep every CU busy with one task (at least 4 k-steps per range).
+MedPlan med_plan(int H, int heads) {
+  MedPlan p;
+  p.ngroups = (H + 32 * kBlocks - 1) / (32 * kBlocks);
+  const int base = heads * p.ngroups;
+  p.ksplit = std::max(1, std::min({device_cus() / base, H / kKS / 4, kMedMaxSplit}));
+  p.grid = std::min(device_cus(), base * p.ksplit);
+  return p;
+}
+
+FG_DEVICE float med_silu(float x) { return x / (1.0f + __expf(-x)); }
+
+// out[h * M + m, n] = R[m, n] + SiLU(sum_p parts[p, h, m, n] + bias[h, n]), 4 columns per thread.
+template <int ODT, int RDT>
+__global__ void __launch_bounds__(256) medusa_combine_kernel(const float* __restrict__ parts, int ksplit, int heads,
+                                                             int M, int N, const uint16_t* __restrict__ bias,
+                                                             const void* __restrict__ R, int64_t ldr,
+                                                             void* __restrict__ out) {
+  const int nq = N >> 2;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)heads * M * nq) return;
+  const int c = (int)(idx % nq) * 4;
+  const int64_t hm = idx / nq;  // h * M + m
+  const int h = (int)(hm / M), m = (int)(hm % M);
+  const int64_t plane = (int64_t)heads * M * N;
+  float4 pv[kMedMaxSplit];
+#pragma unroll
+  for (int p = 0; p < kMedMaxSplit; ++p)
+    if (p < ksplit) pv[p] = *(const float4*)(parts + p * plane + hm * N + c);
+  const uint2 bw = *(const uint2*)(bias + (int64_t)h * N + c);
+  float r[4];
+  if constexpr (RDT == fg::kBF16) {
+    const uint2 rw = *(const uint2*)((const uint16_t*)R + (int64_t)m * ldr + c);
+    r[0] = __uint_as_float(rw.x << 16); r[1] = __uint_as_float(rw.x & 0xffff0000u);
+    r[2] = __uint_as_float(rw.y << 16); r[3] = __uint_as_float(rw.y & 0xffff0000u);
+  } else {
+    const float4 rv = *(const float4*)((const float*)R + (int64_t)m * ldr + c);
+    r[0] = rv.x; r[1] = rv.y; r[2] = rv.z; r[3] = rv.w;
+  }
+  float s[4] = {pv[0].x, pv[0].y, pv[0].z, pv[0].w};
+#pragma unroll
+  for (int p = 1; p < kMedMaxSplit; ++p)
+    if (p < ksplit) {
+      s[0] += pv[p].x; s[1] += pv[p].y; s[2] += pv[p].z; s[3] += pv[p].w;
+    }
+  const float b[4] = {__uint_as_float(bw.x << 16), __uint_as_float(bw.x & 0xffff0000u),
+                      __uint_as_float(bw.y << 16), __uint_as_float(bw.y & 0xffff0000u)};
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = r[e] + med_silu(s[e] + b[e]);
+  if constexpr (ODT == fg::kBF16)
+    *(uint2*)((uint16_t*)out + hm * N + c) = make_uint2(fg::pack_bf16x2(v[0], v[1]), fg::pack_bf16x2(v[2], v[3]));
+  else
+    *(float4*)((float*)out + hm * N + c) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
 }  // namespace
+
+namespace fg {
+
+bool medusa_stream_ok(int batch, int H, int heads) {
+  return batch >= 1 && batch <= 256 && heads >= 1 && H >= kKS && H % kKS == 0 &&
+         (uint64_t)heads * H * H * 2 < 0xFFFFFFFFull && (uint64_t)heads * batch * H * 2 < 0xFFFFFFFFull;
+}
+
+size_t medusa_stream_parts_bytes(int batch, int H, int heads) {
+  return medusa_stream_ok(batch, H, heads) ? (size_t)med_plan(H, heads).ksplit * heads * batch * H * 4 : 0;
+}
+
+int medusa_stream(const void* a, int batch, int H, int heads, const void* fc_w, const void* fc_b, const void* R,
+                  int64_t ldr, int r_dtype, void* out, int out_dtype, float* parts, hipStream_t s) {
+  FG_REQUIRE(medusa_stream_ok(batch, H, heads), "medusa_stream: shape");
+  FG_REQUIRE(((uintptr_t)a & 15) == 0 && ((uintptr_t)fc_w & 15) == 0 && ((uintptr_t)parts & 15) == 0 &&
+                 ((uintptr_t)fc_b & 7) == 0 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)R & 15) == 0 &&
+                 ldr % 4 == 0,
+             "medusa_stream: alignment");
+  const MedPlan p = med_plan(H, heads);
+  LmArgs la{};
+  la.x = a; la.ldx = H; la.M = batch; la.K = H;
+  la.w = fc_w; la.ldw = H; la.N = H;
+  la.out = parts; la.ldo = H;
+  la.nparts = p.grid;
+  la.heads = heads; la.ksplit = p.ksplit; la.ngroups = p.ngroups;
+  la.x_head_bytes = (int64_t)batch * H * 2;
+  la.w_head_bytes = (int64_t)H * H * 2;
+  if (batch <= 64) hipLaunchKernelGGL((lm_stream_kernel<2, kF32, 0, false, false, 8, true>), dim3(p.grid), dim3(512), 0, s, la);
+  else if (batch <= 128) hipLaunchKernelGGL((lm_stream_kernel<4, kF32, 0, false, false, 8, true>), dim3(p.grid), dim3(512), 0, s, la);
+  else hipLaunchKernelGGL((lm_stream_kernel<8, kF32, 0, false, false, 8, true>), dim3(p.grid), dim3(512), 0, s, la);
+  int rc = check_launch("fg_medusa_heads(stream)");
+  if (rc) return rc;
+  const int64_t threads = (int64_t)heads * batch * (H / 4);
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  const uint16_t* bias = (const uint16_t*)fc_b;
+  if (out_dtype == kBF16 && r_dtype == kBF16)
+    hipLaunchKernelGGL((medusa_combine_kernel<kBF16, kBF16>), grid, dim3(256), 0, s, parts, p.ksplit, heads, batch, H, bias, R, ldr, out);
+  else if (out_dtype == kBF16)
+    hipLaunchKernelGGL((medusa_combine_kernel<kBF16, kF32>), grid, dim3(256), 0, s, parts, p.ksplit, heads, batch, H, bias, R, ldr, out);
+  else if (r_dtype == kBF16)
+    hipLaunchKernelGGL((medusa_combine_kernel<kF32, kBF16>), grid, dim3(256), 0, s, parts, p.ksplit, heads, batch, H, bias, R, ldr, out);
+  else
+    hipLaunchKernelGGL((medusa_combine_kernel<kF32, kF32>), grid, dim3(256), 0, s, parts, p.ksplit, heads, batch, H, bias, R, ldr, out);
+  return check_launch("fg_medusa_heads(combine)");
+}
+
+}  // namespace fg
 
 extern "C" {
 

@@ -543,6 +543,40 @@ def test_medusa_heads_match_oracle(dtype):
         assert rel_err(to_np(out[i * B:(i + 1) * B]), want) < TOL[dtype]
 
 
+@pytest.mark.parametrize("B,H,nh", [(64, 3584, 4), (16, 576, 3), (100, 1024, 5), (200, 512, 2), (1, 128, 1)])
+def test_medusa_heads_stream_matches_fp32_reference(B, H, nh):
+    """bf16 Medusa fc through the weight stream (key ranges summed by a second launch):
+    the normalised rows are read back from the workspace the call used, and
+    hidden + SiLU(rows . fc_w^T + fc_b) is recomputed in fp32 from them. Shapes cover the
+    Qwen2.5-7B block (4 heads x 3584, 64 rows), a last 256-column group that is partly
+    empty (576), 65-128 and 129-256 rows, and one row of one head. Repeated calls give
+    identical bits (the ranges are added in a fixed order)."""
+    torch.manual_seed(B * 7 + H)
+    dt = torch.bfloat16
+    hid = torch.randn(B + 3, H, device=DEV).to(dt)[:B]
+    ln_w = 1 + 0.1 * torch.randn(nh, H, device=DEV)
+    ln_b = 0.1 * torch.randn(nh, H, device=DEV)
+    fc_w = (torch.randn(nh, H, H, device=DEV) * 0.03).to(dt)
+    fc_b = (torch.randn(nh, H, device=DEV) * 0.1).to(dt)
+    need = K()._lib.load().fg_medusa_heads_workspace(B, H, nh, 1)
+    assert need >= nh * B * H * 2 + 256
+    ws = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    out = K().medusa_heads(hid, ln_w, ln_b, fc_w, fc_b, out_dtype=torch.float32, workspace=ws)
+    rows = ws[:nh * B * H * 2].view(dt).view(nh, B, H).float()
+    ref = torch.bmm(rows, fc_w.float().transpose(1, 2).contiguous()) + fc_b.float()[:, None, :]
+    ref = hid.float()[None] + torch.nn.functional.silu(ref)
+    assert rel_err(to_np(out.view(nh, B, H)), to_np(ref)) < 1e-5
+    # the normalised rows themselves against LayerNorm in fp32 (bf16 rounding of the output)
+    ln = torch.nn.functional.layer_norm(hid.float(), (H,), eps=1e-5)
+    ln_ref = ln[None] * ln_w[:, None, :] + ln_b[:, None, :]
+    assert rel_err(to_np(rows), to_np(ln_ref)) < 1e-2
+    out_bf = K().medusa_heads(hid, ln_w, ln_b, fc_w, fc_b, workspace=ws)
+    assert out_bf.dtype == dt
+    assert torch.equal(out_bf, out.to(dt))
+    again = K().medusa_heads(hid, ln_w, ln_b, fc_w, fc_b, out_dtype=torch.float32, workspace=ws)
+    assert torch.equal(again, out)
+
+
 # ------------------------------------------------------------------ attention and layer pieces
 def _attn_reference(q, kc, vc, seq, anc, N, G):
     B, _, Hq, d = q.shape
