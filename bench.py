@@ -530,10 +530,78 @@ def attention_only(args, work):
     elem = 2 if dt == torch.bfloat16 else 4
     byts = 2 * B * Hkv * (P + N) * d * elem + 2 * B * N * Hq * d * elem
     med = float(np.median(us))
+    if getattr(args, "calibrate_copy", False):
+        # a device copy of known size in the same run: what FETCH_SIZE / WRITE_SIZE read for it
+        # scales the counters of the attention launches into bytes
+        src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(COPY_REPS):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     print(json.dumps({"kernel": "fg_tree_attention", "config": args.config, "sequences": B, "tree_nodes": N,
                       "prefix": P, "cold_caches": args.cold, "batches": len(us), "us_median": round(med, 2),
                       "us_min": round(float(us.min()), 2), "bytes": byts, "GBps": round(byts / med / 1e3, 1),
                       "hbm_frac": round(byts / med / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
+
+
+COPY_BYTES = 256 << 20
+COPY_REPS = 3
+COPY_SYMBOL = "copyBuffer"
+
+
+def measure_traffic(args, symbol, timeout_s=240):
+    """HBM bytes per launch of the roofline kernel from two rocprofv3 --pmc passes
+    (FETCH_SIZE, then WRITE_SIZE, each its own run) over `bench.py --attention-only` at
+    the same shape, each counter scaled by what it reads for a 256 MiB device copy in the
+    same run. Returns (bytes, detail) or (None, reason)."""
+    import csv
+    import shutil
+    import signal
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3") or ("/opt/rocm/bin/rocprofv3" if os.path.exists("/opt/rocm/bin/rocprofv3")
+                                         else None)
+    if prof is None:
+        return None, "rocprofv3 not found"
+    tmp = os.environ.get("TMPDIR") if os.path.isdir(os.environ.get("TMPDIR", "")) else "/tmp"
+    means = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        out = tempfile.mkdtemp(prefix="fg_pmc_", dir=tmp)
+        cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "run", "--", sys.executable,
+               os.path.abspath(__file__), "--attention-only", "--config", args.config, "--steps", "2",
+               "--calibrate-copy"]
+        print(f"bench: traffic pass {counter}", file=sys.stderr, flush=True)
+        proc = subprocess.Popen(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, start_new_session=True,
+                                env=dict(os.environ, TMPDIR=tmp))
+        try:
+            proc.wait(timeout=timeout_s)
+        except subprocess.TimeoutExpired:
+            os.killpg(proc.pid, signal.SIGKILL)
+            proc.wait()
+            return None, f"{counter} pass timed out"
+        paths = [os.path.join(dp, f) for dp, _, fs in os.walk(out) for f in fs if f.endswith("counter_collection.csv")]
+        if not paths:
+            return None, f"{counter} pass wrote no counter CSV (exit {proc.returncode})"
+        vals = {symbol: [], COPY_SYMBOL: []}
+        with open(paths[0], newline="") as fh:
+            for row in csv.DictReader(fh):
+                if row.get("Counter_Name") != counter:
+                    continue
+                for key in vals:
+                    if key in row["Kernel_Name"]:
+                        vals[key].append(float(row["Counter_Value"]))
+        shutil.rmtree(out, ignore_errors=True)
+        if not vals[symbol] or not vals[COPY_SYMBOL]:
+            return None, f"{counter}: no dispatches of {symbol} or of the calibration copy"
+        # the runtime may split one copy over several dispatches: the copy's figure is the
+        # sum over its dispatches per copy
+        means[counter] = (sum(vals[symbol]) / len(vals[symbol]), sum(vals[COPY_SYMBOL]) / COPY_REPS)
+    scale = {c: COPY_BYTES / (m[1] * 1024.0) for c, m in means.items()}  # copy bytes per counted byte
+    total = sum(m[0] * 1024.0 * scale[c] for c, m in means.items())
+    detail = {c: {"KiB_per_launch": round(m[0], 1), "copy_KiB": round(m[1], 1), "scale": round(scale[c], 4)}
+              for c, m in means.items()}
+    return int(total), detail
 
 
 def lm_head_only(args, work):
@@ -622,6 +690,10 @@ def main():
     ap.add_argument("--attention-only", action="store_true",
                     help="time fg_tree_attention alone at the config's verify shape (batches of 10 launches)")
     ap.add_argument("--cold", type=int, default=8, help="--attention-only: distinct K/V caches rotated over")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="--attention-only: also run a 256 MiB device copy (counter calibration)")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 --pmc passes that measure the roofline kernel's HBM traffic")
     ap.add_argument("--lm-head-only", action="store_true",
                     help="time the LM-head kernel alone against hipBLASLt at 64..256 rows and exit")
     ap.add_argument("--summarize-trace", metavar="CSV", help="summarise a rocprofv3 kernel trace of this command")
@@ -821,6 +893,13 @@ def main():
     if args.traffic_from:
         roofline["traffic"] = pmc_traffic(args.traffic_from[0], args.traffic_from[1],
                                           KERNEL_SYMBOLS.get(name, name), args.traffic_scale)
+    elif not args.no_traffic and name == "fg_tree_attention" and dtype == torch.bfloat16:
+        traffic, detail = measure_traffic(args, KERNEL_SYMBOLS[name])
+        roofline["traffic"] = traffic
+        roofline["traffic_source"] = ("rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (one run each) over "
+                                      "`bench.py --attention-only` at this shape, scaled by a 256 MiB copy")
+        roofline["traffic_detail"] = detail
+        log(f"traffic {traffic} {detail}")
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
