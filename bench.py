@@ -583,20 +583,34 @@ def measure_traffic(args, symbol, timeout_s=240):
         paths = [os.path.join(dp, f) for dp, _, fs in os.walk(out) for f in fs if f.endswith("counter_collection.csv")]
         if not paths:
             return None, f"{counter} pass wrote no counter CSV (exit {proc.returncode})"
-        vals = {symbol: [], COPY_SYMBOL: []}
         with open(paths[0], newline="") as fh:
-            for row in csv.DictReader(fh):
-                if row.get("Counter_Name") != counter:
-                    continue
-                for key in vals:
-                    if key in row["Kernel_Name"]:
-                        vals[key].append(float(row["Counter_Value"]))
+            m = counter_means(csv.DictReader(fh), counter, symbol)
         shutil.rmtree(out, ignore_errors=True)
-        if not vals[symbol] or not vals[COPY_SYMBOL]:
+        if m is None:
             return None, f"{counter}: no dispatches of {symbol} or of the calibration copy"
-        # the runtime may split one copy over several dispatches: the copy's figure is the
-        # sum over its dispatches per copy
-        means[counter] = (sum(vals[symbol]) / len(vals[symbol]), sum(vals[COPY_SYMBOL]) / COPY_REPS)
+        means[counter] = m
+    return traffic_from_means(means)
+
+
+def counter_means(rows, counter, symbol):
+    """(mean KiB per dispatch of `symbol`, KiB per calibration copy) of one counter from the
+    rows of a rocprofv3 counter_collection CSV; None if either is missing. The runtime may
+    split one copy over several dispatches, so the copy's figure is the sum of its dispatches
+    divided by the number of copies."""
+    vals = {symbol: [], COPY_SYMBOL: []}
+    for row in rows:
+        if row.get("Counter_Name") != counter:
+            continue
+        for key in vals:
+            if key in row["Kernel_Name"]:
+                vals[key].append(float(row["Counter_Value"]))
+    if not vals[symbol] or not vals[COPY_SYMBOL]:
+        return None
+    return sum(vals[symbol]) / len(vals[symbol]), sum(vals[COPY_SYMBOL]) / COPY_REPS
+
+
+def traffic_from_means(means):
+    """Bytes per launch: each counter's KiB per launch times copy bytes / counted copy bytes."""
     scale = {c: COPY_BYTES / (m[1] * 1024.0) for c, m in means.items()}  # copy bytes per counted byte
     total = sum(m[0] * 1024.0 * scale[c] for c, m in means.items())
     detail = {c: {"KiB_per_launch": round(m[0], 1), "copy_KiB": round(m[1], 1), "scale": round(scale[c], 4)}
