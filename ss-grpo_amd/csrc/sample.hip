@@ -491,6 +491,12 @@ FG_DEVICE bool split_skip(const SplitArgs& a, int r) {
 constexpr int kSplitLoads = 4;
 constexpr int kSplitPass = kSplitThreads * 8 * kSplitLoads;
 
+// Load group u of a pass starting at base (elements base + (u * kSplitThreads + t) * 8 ..
+// + 7 of thread t) holds an element before hi. Uniform over the workgroup: a group wholly
+// past the chunk end is neither loaded nor weighed (a 9,504-element chunk is one full pass
+// of 8,192 and one group of the second).
+FG_DEVICE bool split_group_live(int base, int u, int hi) { return base + u * kSplitThreads * 8 < hi; }
+
 // Loads elements i0 .. i0 + 7 of a chunk ending at hi; past hi come -inf, whose weight is
 // 0 against any row maximum, so the weights need no per-element test.
 template <int DT>
@@ -517,11 +523,13 @@ __global__ void __launch_bounds__(kSplitThreads) split_max_kernel(SplitArgs a) {
   for (int base = lo; base < hi; base += kSplitPass) {
     float x[kSplitLoads][8];
 #pragma unroll
-    for (int u = 0; u < kSplitLoads; ++u) split_load8<DT>(p, base + (u * kSplitThreads + threadIdx.x) * 8, hi, x[u]);
+    for (int u = 0; u < kSplitLoads; ++u)
+      if (split_group_live(base, u, hi)) split_load8<DT>(p, base + (u * kSplitThreads + threadIdx.x) * 8, hi, x[u]);
     // the -inf padding past hi never wins: a real element's key is at least as large
     // and its index smaller
 #pragma unroll
     for (int u = 0; u < kSplitLoads; ++u) {
+      if (!split_group_live(base, u, hi)) continue;
       const int i0 = base + (u * kSplitThreads + threadIdx.x) * 8;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -612,7 +620,8 @@ __global__ void __launch_bounds__(kSplitThreads) split_sum_kernel(SplitArgs a) {
   // the first pass's logits are in flight while the row maximum is gathered from the parts
   float x[kSplitLoads][8];
 #pragma unroll
-  for (int u = 0; u < kSplitLoads; ++u) split_load8<DT>(p, lo + (u * kSplitThreads + tid) * 8, hi, x[u]);
+  for (int u = 0; u < kSplitLoads; ++u)
+    if (split_group_live(lo, u, hi)) split_load8<DT>(p, lo + (u * kSplitThreads + tid) * 8, hi, x[u]);
   float mx;
   uint64_t best;
   split_parts_max(a, r, smax, skey, mx, best);
@@ -621,10 +630,12 @@ __global__ void __launch_bounds__(kSplitThreads) split_sum_kernel(SplitArgs a) {
   for (int base = lo; base < hi; base += kSplitPass) {
     if (base != lo) {
 #pragma unroll
-      for (int u = 0; u < kSplitLoads; ++u) split_load8<DT>(p, base + (u * kSplitThreads + tid) * 8, hi, x[u]);
+      for (int u = 0; u < kSplitLoads; ++u)
+        if (split_group_live(base, u, hi)) split_load8<DT>(p, base + (u * kSplitThreads + tid) * 8, hi, x[u]);
     }
 #pragma unroll
-    for (int u = 0; u < kSplitLoads; ++u) acc += split_weight8<SCALE>(x[u], a.temperature, m);
+    for (int u = 0; u < kSplitLoads; ++u)
+      if (split_group_live(base, u, hi)) acc += split_weight8<SCALE>(x[u], a.temperature, m);
   }
   acc = fg::wave_sum_u64(acc);
   if ((tid & 63) == 0) ssum[tid >> 6] = acc;
@@ -642,56 +653,53 @@ __global__ void __launch_bounds__(kSplitThreads) split_sum_kernel(SplitArgs a) {
 }
 
 // First index in [lo, hi) whose inclusive running q-mass exceeds target (the whole
-// block; -1 if none), kSplitPass elements per step, scanned in index order.
+// block; -1 if none), scanned in index order one group of kSplitThreads x 8 elements at a
+// time (thread t holds 8 consecutive elements of a group), stopping at the group that holds
+// the target: on average half the chunk is weighed. A pass's groups are loaded together.
 template <int DT, bool SCALE>
 FG_DEVICE int split_locate(const SplitArgs& a, const char* p, int lo, int hi, float m, uint64_t target,
                            uint64_t* wsum, int* found) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (tid == 0) *found = -1;
   uint64_t run = 0;  // block-uniform
-  for (int base = lo; base < hi; base += kSplitPass) {
-    // thread t holds the kSplitLoads * 8 consecutive elements base + t * 8 * kSplitLoads ...
+  bool done = false;
+  for (int base = lo; base < hi && !done; base += kSplitPass) {
     float x[kSplitLoads][8];
 #pragma unroll
-    for (int u = 0; u < kSplitLoads; ++u) split_load8<DT>(p, base + (tid * kSplitLoads + u) * 8, hi, x[u]);
-    uint64_t wu[kSplitLoads], mine = 0;
+    for (int u = 0; u < kSplitLoads; ++u)
+      if (split_group_live(base, u, hi)) split_load8<DT>(p, base + (u * kSplitThreads + tid) * 8, hi, x[u]);
 #pragma unroll
     for (int u = 0; u < kSplitLoads; ++u) {
-      wu[u] = split_weight8<SCALE>(x[u], a.temperature, m);
-      mine += wu[u];
-    }
-    const uint64_t incl = fg::wave_incl_scan_u64(mine);
-    __syncthreads();  // wsum of the previous step has been read
-    if (lane == 63) wsum[wave] = incl;
-    __syncthreads();
-    uint64_t woff = 0, stot = 0;
+      if (!split_group_live(base, u, hi)) break;  // uniform
+      const uint64_t mine = split_weight8<SCALE>(x[u], a.temperature, m);
+      const uint64_t incl = fg::wave_incl_scan_u64(mine);
+      __syncthreads();  // wsum of the previous group has been read
+      if (lane == 63) wsum[wave] = incl;
+      __syncthreads();
+      uint64_t woff = 0, stot = 0;
 #pragma unroll
-    for (int w = 0; w < kSplitWaves; ++w) {
-      if (w < wave) woff += wsum[w];
-      stot += wsum[w];
-    }
-    if (run + stot > target) {
-      uint64_t cum = run + woff + incl - mine;
-      if (cum <= target && target < cum + mine) {
-        for (int u = 0; u < kSplitLoads; ++u) {
-          if (cum + wu[u] > target) {
-            const int i0 = base + (tid * kSplitLoads + u) * 8;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              cum += split_weight<SCALE>(x[u][j], a.temperature, m);
-              if (cum > target) {
-                *found = i0 + j;
-                break;
-              }
-            }
-            break;
-          }
-          cum += wu[u];
-        }
+      for (int w = 0; w < kSplitWaves; ++w) {
+        if (w < wave) woff += wsum[w];
+        stot += wsum[w];
       }
-      break;
+      if (run + stot > target) {  // uniform: this group holds the target
+        uint64_t cum = run + woff + incl - mine;
+        if (cum <= target && target < cum + mine) {
+          const int i0 = base + (u * kSplitThreads + tid) * 8;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            cum += split_weight<SCALE>(x[u][j], a.temperature, m);
+            if (cum > target) {
+              *found = i0 + j;
+              break;
+            }
+          }
+        }
+        done = true;
+        break;
+      }
+      run += stot;
     }
-    run += stot;
   }
   __syncthreads();
   return *found;
