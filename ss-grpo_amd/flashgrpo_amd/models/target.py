@@ -310,33 +310,45 @@ def _graph_memset_nodes(graph: torch.cuda.CUDAGraph) -> int:
 
 
 class _ForwardGraph:
-    """One captured verify forward: static input buffers, the graph, its output."""
+    """One captured verify forward: static input buffers and two graphs, the first layer
+    and the rest. Launching a graph of ~250 nodes costs ~120 us of host time, and a
+    round's GPU idles until its forward's first kernels are queued; with the split, the
+    second launch runs on the host while the GPU works through the first layer."""
 
-    def __init__(self, graph, inputs, out):
-        self.graph, self.inputs, self.out = graph, inputs, out
+    FIRST_LAYERS = 1
+
+    def __init__(self, graphs, inputs, out):
+        self.graphs, self.inputs, self.out = graphs, inputs, out
 
     @classmethod
     def capture(cls, model, tokens, cache, pos_offset, anc, seq_len, row_map, err_flag):
         inputs = dict(tokens=tokens.clone(), pos=pos_offset.clone(), anc=anc.clone(), seq=seq_len.clone(),
                       row_map=None if row_map is None else row_map.clone())
-
-        def run_eager():
-            return model._forward_eager(inputs["tokens"], cache, pos_offset=inputs["pos"], anc=inputs["anc"],
-                                        seq_len=inputs["seq"], row_map=inputs["row_map"], err_flag=err_flag)
-
+        kw = dict(pos_offset=inputs["pos"], anc=inputs["anc"], seq_len=inputs["seq"], row_map=inputs["row_map"],
+                  err_flag=err_flag)
         # A warm-up on the current stream allocates every buffer and workspace the
         # launches use outside the graph's pool (it rewrites the same tree slots the
         # caller's forward writes).
-        run_eager()
+        model._forward_eager(inputs["tokens"], cache, **kw)
         if model._graph_pool is None:
             model._graph_pool = torch.cuda.graph_pool_handle()
-        g = torch.cuda.CUDAGraph(keep_graph=True)
-        with torch.cuda.graph(g, pool=model._graph_pool):
-            out = run_eager()
-        if _graph_memset_nodes(g):
+        L = model.cfg.num_layers
+        split = min(cls.FIRST_LAYERS, L)
+        g1 = torch.cuda.CUDAGraph(keep_graph=True)
+        with torch.cuda.graph(g1, pool=model._graph_pool):
+            st = model._forward_begin(inputs["tokens"], cache, **kw)
+            model._forward_layers(st, 0, split)
+        g2 = torch.cuda.CUDAGraph(keep_graph=True)
+        with torch.cuda.graph(g2, pool=model._graph_pool):
+            model._forward_layers(st, split, L)
+            out = model._forward_end(st)
+        if _graph_memset_nodes(g1) or _graph_memset_nodes(g2):
             return None
-        g.instantiate()
-        return cls(g, inputs, out)
+        g1.instantiate()
+        g2.instantiate()
+        # st["x"] (the residual stream, allocated in the first graph's capture) stays
+        # referenced through the second graph, which reads it
+        return cls((g1, g2, st), inputs, out)
 
     def run(self, tokens, pos_offset, anc, seq_len, row_map):
         st = self.inputs
@@ -346,7 +358,8 @@ class _ForwardGraph:
         st["seq"].copy_(seq_len)
         if row_map is not None:
             st["row_map"].copy_(row_map)
-        self.graph.replay()
+        self.graphs[0].replay()
+        self.graphs[1].replay()
         return self.out
 
 
@@ -539,18 +552,36 @@ class TargetModel:
                                    err_flag=err_flag)
 
     def _forward_eager(self, tokens, cache, *, pos_offset, anc, seq_len, row_map, err_flag):
+        st = self._forward_begin(tokens, cache, pos_offset=pos_offset, anc=anc, seq_len=seq_len, row_map=row_map,
+                                 err_flag=err_flag)
+        self._forward_layers(st, 0, self.cfg.num_layers)
+        return self._forward_end(st)
+
+    def _forward_begin(self, tokens, cache, *, pos_offset, anc, seq_len, row_map, err_flag) -> dict:
+        """Shape checks and the embedding rows: the forward's state for _forward_layers."""
         cfg = self.cfg
         B, N = tokens.shape
         if anc is not None and N > MAX_TREE_NODES:
             raise ValueError(f"at most {MAX_TREE_NODES} tree nodes per forward")
         if N > MAX_CHAIN_TOKENS:
             raise ValueError(f"at most {MAX_CHAIN_TOKENS} new tokens per forward")
+        d = cfg.head_dim
+        x = self.w["embed"].index_select(0, tokens.reshape(-1).long())  # [T, H] residual stream
+        return dict(x=x, B=B, N=N, cache=cache, pos_offset=pos_offset, anc=anc, seq_len=seq_len, row_map=row_map,
+                    err_flag=err_flag, q=self._buf("q", (B, N, cfg.q_heads, d)),
+                    attn=self._buf("attn", (B, N, cfg.q_heads, d)))
+
+    def _forward_layers(self, st: dict, l0: int, l1: int) -> None:
+        """Decoder layers [l0, l1) on the residual stream st["x"] (updated in place)."""
+        cfg = self.cfg
+        x, B, N, cache = st["x"], st["B"], st["N"], st["cache"]
+        seq_len, pos_offset, anc, row_map, err_flag = (st["seq_len"], st["pos_offset"], st["anc"], st["row_map"],
+                                                       st["err_flag"])
+        q, attn = st["q"], st["attn"]
         T = B * N
         H, d = cfg.hidden, cfg.head_dim
-        x = self.w["embed"].index_select(0, tokens.reshape(-1).long())  # [T, H] residual stream
-        q = self._buf("q", (B, N, cfg.q_heads, d))
-        attn = self._buf("attn", (B, N, cfg.q_heads, d))
-        for l, lw in enumerate(self.w["layers"]):
+        for l in range(l0, l1):
+            lw = self.w["layers"][l]
             h = K.rmsnorm(x, lw["input_norm"], cfg.rms_eps, out=self._buf("h", (T, H)))
             qkv = F.linear(h, lw["qkv_w"], lw["qkv_b"])
             K.rope_kv_write(qkv, batch=B, num_nodes=N, q_heads=cfg.q_heads, kv_heads=cfg.kv_heads, head_dim=d,
@@ -565,8 +596,12 @@ class TargetModel:
             gu = F.linear(h2, lw["gate_up_w"])
             act = K.swiglu(gu, out=self._buf("act", (T, cfg.intermediate)))
             x.addmm_(act, lw["down_w"].t())
-        out = torch.empty(T, H, dtype=self.dtype, device=self.device)
-        K.rmsnorm(x, self.w["final_norm"], cfg.rms_eps, out=out)
+
+    def _forward_end(self, st: dict) -> torch.Tensor:
+        """The final norm: hidden states [B, N, H]."""
+        B, N, H = st["B"], st["N"], self.cfg.hidden
+        out = torch.empty(B * N, H, dtype=self.dtype, device=self.device)
+        K.rmsnorm(st["x"], self.w["final_norm"], self.cfg.rms_eps, out=out)
         return out.view(B, N, H)
 
     def walk_parts(self, rows: int, hidden: torch.Tensor):
