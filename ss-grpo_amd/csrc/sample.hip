@@ -350,7 +350,11 @@ __global__ void walk_rows_kernel(const int32_t* __restrict__ state, int batch, i
   row_active[b] = state[batch + b];
 }
 
-// Walk update of tree b after its draw `tok` at `parent` (one thread).
+// Walk update of tree b after its draw `tok` at `parent`, by the 64 lanes of one wave
+// (nmax <= 64, host-checked): lane c loads node c's parent and token, one ballot finds the
+// first child of `parent` drawing `tok` (the lowest such node index) and a second whether
+// that child has children; lane 0 writes the results. A serial scan by one thread would
+// wait for up to 2 nmax dependent loads. tok and parent are taken from lane 0.
 // next_rows / next_active (optional): the LM-head rows of the next walk step of tree b,
 // as walk_rows_kernel would write them.
 FG_DEVICE void walk_apply(int b, int tok, int parent, const int32_t* tree_tokens, const int32_t* parents,
@@ -358,16 +362,18 @@ FG_DEVICE void walk_apply(int b, int tok, int parent, const int32_t* tree_tokens
                           int32_t* acc_nodes, int acc_stride, int32_t* acc_len, int32_t* last_node,
                           int32_t* correction, int32_t* state, int32_t* err_flag, int32_t* next_rows = nullptr,
                           int32_t* next_active = nullptr) {
-  state[2 * batch + b] = walk_step;
+  const int lane = threadIdx.x & 63;
+  tok = __builtin_amdgcn_readfirstlane(tok);
+  parent = __builtin_amdgcn_readfirstlane(parent);
   const int nn = n_nodes[b];
-  const int32_t* pb = parents + (int64_t)b * nmax;
-  const int32_t* tb = tree_tokens + (int64_t)b * nmax;
-  int match = -1;
-  for (int c = 1; c < nn; ++c)
-    if (pb[c] == parent && tb[c] == tok) {
-      match = c;
-      break;
-    }
+  const bool in = lane >= 1 && lane < nn;
+  const int pc = in ? parents[(int64_t)b * nmax + lane] : -2;
+  const int tc = in ? tree_tokens[(int64_t)b * nmax + lane] : 0;
+  const uint64_t hit = __ballot(in && pc == parent && tc == tok);
+  const int match = hit ? (int)__builtin_ctzll(hit) : -1;
+  const uint64_t kids = __ballot(in && match >= 0 && lane > match && pc == match);
+  if (lane != 0) return;
+  state[2 * batch + b] = walk_step;
   if (match < 0) {
     correction[b] = tok;
     state[batch + b] = 0;
@@ -382,9 +388,7 @@ FG_DEVICE void walk_apply(int b, int tok, int parent, const int32_t* tree_tokens
     }
     last_node[b] = match;
     state[b] = match;
-    int has_child = 0;
-    for (int c = match + 1; c < nn; ++c) has_child |= pb[c] == match;
-    state[batch + b] = has_child;
+    state[batch + b] = kids != 0ull;
   }
   if (next_rows) {
     next_rows[b] = b * nmax + state[b];
@@ -420,7 +424,7 @@ __global__ void __launch_bounds__(kThreads) walk_step_kernel(
   uint32_t u = noise_value(noise, (int64_t)b * noise_stride + noise_col0 + walk_step, seed, step, seq,
                            (uint32_t)(draw0 + walk_step));
   int tok = block_sample<DT>(rowp, vocab, sp, u, sh);
-  if (threadIdx.x == 0)
+  if (threadIdx.x < 64)
     walk_apply(b, tok, parent, tree_tokens, parents, n_nodes, nmax, batch, walk_step, acc_tokens, acc_nodes, acc_stride,
                acc_len, last_node, correction, state, err_flag, next_rows, next_active);
 }
@@ -784,14 +788,13 @@ __global__ void __launch_bounds__(kSplitThreads) split_pick_kernel(SplitArgs a, 
       if (idx >= 0) tok = idx;  // always: the chunk holds the target
     }
   }
-  if (tid == 0) {
-    if constexpr (WALK) {
+  if constexpr (WALK) {
+    if (tid < 64)
       walk_apply(r, tok, d.state[r], d.tree_tokens, d.parents, d.n_nodes, d.nmax, d.batch, d.walk_step, d.acc_tokens,
                  d.acc_nodes, d.acc_stride, d.acc_len, d.last_node, d.correction, d.state, d.err_flag, d.next_rows,
                  d.next_active);
-    } else {
-      d.out[r] = tok;
-    }
+  } else {
+    if (tid == 0) d.out[r] = tok;
   }
 }
 
@@ -1061,7 +1064,7 @@ __global__ void __launch_bounds__(kThreads) split_topp_walk_kernel(
   const uint32_t u = noise_value(noise, (int64_t)b * noise_stride + noise_col0 + walk_step, seed, step, seq,
                                  (uint32_t)(draw0 + walk_step));
   const int tok = split_topp_pick<DT>(a, b, u, sh);
-  if (threadIdx.x == 0)
+  if (threadIdx.x < 64)
     walk_apply(b, tok, parent, tree_tokens, parents, n_nodes, nmax, batch, walk_step, acc_tokens, acc_nodes,
                acc_stride, acc_len, last_node, correction, state, err_flag, next_rows, next_active);
 }

@@ -304,9 +304,12 @@ def test_sample_tokens_bit_exact(dtype, mode):
 def test_split_sampling_equals_single_workgroup(dtype, mode):
     """Rows split over 16 workgroups (unrestricted / greedy draws: chunk maxima, then one
     draw launch) give the tokens of the one-workgroup-per-row kernel, including flat rows,
-    ties, -inf and NaN entries, rows of only -inf or NaN, and short vocabularies."""
+    ties, -inf and NaN entries, rows of only -inf or NaN, and short vocabularies. The
+    vocabularies put the chunk end (V / 16 rounded up to 8) inside the first load group,
+    inside the last group of a pass, exactly at a pass end and one step into a second pass
+    (the 1.5B, 8B and 7B vocabularies among them)."""
     g = torch.Generator(device="cpu").manual_seed(23)
-    for V in (5, 37, 1000, 32000, 152064):
+    for V in (5, 37, 1000, 32000, 128256, 131072, 131200, 151936, 152064):
         x = torch.randn(48, V, generator=g) * 2.0
         x[0] = 0.0
         x[1] = torch.round(x[1])
