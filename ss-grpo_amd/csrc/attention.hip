@@ -16,26 +16,18 @@
 //    KV head, so every K/V tile loaded from HBM serves all of them; the row tiles
 //    of one KV head run on one XCD and share its L2;
 //  * each wave owns 32 query rows, two waves per SIMD; a wave whose rows are all
-//    past the tile only stages K/V;
+//    past the tile only issues its share of the tile loads;
 //  * S^T = K Q^T (keys on the M side) puts one query per lane: the online
 //    softmax row max / sum are per-lane values plus one exchange with the other
 //    half-wave (v_permlane32_swap);
 //  * O^T += V^T P^T: P^T is fed straight from the S^T accumulators (bf16) as the
 //    B operand; l is summed from the same bf16 P (v_dot2c_f32_bf16);
-//  * the first W/2 waves stage K, the others V, with buffer loads over the
-//    sequence's keys [0, min(seq_len + N, capacity)) (loads past the end return 0);
-//  * V^T rows hold the 64 keys of a tile in the order 0-3, 8-11, 4-7, 12-15 per
-//    16-key block, so the 8 keys a lane feeds the PV MFMA (4g..4g+3 and
-//    8+4g..8+4g+3 of a block) are one 16-byte read at a compile-time offset; the
-//    staging writes are 4-key runs (8 bytes) with consecutive lanes on consecutive
-//    runs of one row, and a row pitch of 9 16-byte chunks puts 8 consecutive rows
-//    on distinct banks (reads and writes are conflict-free);
+//  * K/V tiles of 64 keys go from HBM straight into LDS (buffer_load ... lds, the 33
+//    1-KB loads of a tile spread over the waves, zeros past the sequence's keys
+//    [0, min(seq_len + N, capacity))) through a ring of stages (the layouts and the
+//    wait rule are described at the stage constants below); one barrier per tile;
 //  * per tile all 16 K fragments are read from LDS before the first MFMA and the
-//    16 V^T fragments are read during the S MFMAs (one LDS latency per phase);
-//  * K/V tiles are double-buffered in LDS; at the top of iteration t the
-//    registers of tile t+1 are stored to the other LDS buffer and the loads of the
-//    next tile are issued (W = 8: two register sets, tiles t+2 and t+3 in flight;
-//    W = 4: one set, tile t+2); one barrier per 64-key tile;
+//    16 V fragments (transposed reads) during the S MFMAs (one LDS latency per phase);
 //  * the ancestor mask is evaluated only on tiles that reach the tree keys, and
 //    the running max (and the O rescale) only moves when a lane's max grows by
 //    more than 2^8, so after the first keys the rescale is almost never taken.
@@ -76,8 +68,6 @@ struct AttnArgs {
 
 constexpr int kD = 128;            // head dim of the MFMA path
 constexpr int kKT = 64;            // keys per tile
-constexpr int kKPitch = kD + 8;    // bf16 elements per K row in LDS
-constexpr int kVtPitch = kKT + 8;  // bf16 elements per V^T row in LDS (9 16-byte chunks)
 constexpr float kRescaleSlack = 8.0f;  // log2 units
 constexpr int rows_tile(int w) { return w * 32; }
 
@@ -94,10 +84,6 @@ FG_DEVICE uint64_t tile_allowed_mask(int sh, uint64_t tree_bits) {
 // Bits j < n of a 64-bit mask (n clamped to [0, 64]).
 FG_DEVICE uint64_t low_bits(int n) { return n <= 0 ? 0ull : n >= 64 ? ~0ull : ((1ull << n) - 1ull); }
 
-// Position of key k in a V^T row (see the layout notes above).
-FG_DEVICE int vt_pos(int k) {
-  return (k & ~15) | (k & 3) | (((k >> 3) & 1) << 2) | (((k >> 2) & 1) << 3);
-}
 
 // Max / sum of a value with the same lane of the other half-wave.
 FG_DEVICE float xor32_max(float x) {
