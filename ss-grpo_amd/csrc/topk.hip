@@ -208,6 +208,8 @@ __global__ void tree_layout_kernel(const int32_t* __restrict__ cand_tokens, cons
 constexpr int kSpMaxNodes = 128;  // nodes assembled before the budget cut
 constexpr int kSpMaxParents = 64;
 constexpr int kSpMaxPool = 1024;  // (parent, candidate) pairs of one head
+// parents of one head x candidates per parent (kstride <= 16, host-checked): 16 pairs per lane
+static_assert(kSpMaxPool == kSpMaxParents * 16 && kSpMaxPool == 64 * 16, "sparse pick pool");
 
 struct SparseArgs {
   const int32_t* cand_tokens;
