@@ -7,6 +7,9 @@ test_gpu_decoder.py):
   [4, 2], 13 nodes) in lockstep with the oracle;
 * Qwen2.5-14B geometry (hidden 5120, 40/8 heads of 128, MLP 13824, vocabulary 152064,
   4 Medusa heads, 64-node budget -> [4, 3, 2], 41 nodes) in lockstep with the oracle;
+* Llama-3.1-8B geometry (hidden 4096, 32/8 heads of 128, MLP 14336, vocabulary 128256,
+  theta 5e5, RMS eps 1e-5, no QKV bias, untied LM head, chain proposals from Medusa head 1
+  and a 4096-wide ChainDraftCell, 48-node budget, temperature 0.7) in lockstep with the oracle;
 * one full-size Qwen2.5-7B verify round: 64 sequences (8 prompts x 8 repeats), a
   2048-token prefix, hidden 3584, 28/4 heads of 128, MLP 18944, vocabulary 152064, 4
   Medusa heads, adaptive plan with a 32-node budget (-> [4, 2, 1, 1], 29 nodes), checked
@@ -64,6 +67,22 @@ def test_lockstep_14b_geometry():
     assert st["rounds"] == out["total_verify_rounds"] >= 2
     plan = out["last_tree_plan"]
     assert plan["node_budget_per_seq"] == 64 and plan["topk_by_depth"] == [4, 3, 2] and plan["actual_nodes"] == 41
+
+
+def test_lockstep_8b_chain_geometry():
+    """8B chain config at full width, 4 sequences (2 prompts x 2 repeats): cpeak 192 gives
+    the config's 48-node budget (cpeak 4608 at 96 sequences). Every round's proposals come
+    from the chain path (Medusa head 1 for depth 2, the recurrent cell after it)."""
+    cfg = OM.ModelConfig(num_layers=1, hidden=4096, q_heads=32, kv_heads=8, head_dim=128, intermediate=14336,
+                         vocab=128256, rope_theta=5e5, rms_eps=1e-5, qkv_bias=False, tie_word_embeddings=False)
+    spec = OD.DecodeSpec(tree_mode="concurrency_aware", cpeak_nodes=192, max_tree_nodes_per_seq=48,
+                         fixed_tree_topk_by_depth=(4, 3, 2), num_medusa_heads=4, max_tree_depth=5,
+                         adaptive_tree_enabled=True, adaptive_confidence_low=0.2, adaptive_confidence_high=0.7,
+                         temperature=0.7, top_p=1.0, proposal_mode="chain")
+    out, st = _run(cfg, spec, dtype=torch.bfloat16, B0=2, repeats=2, P=64, max_length=64 + 5, std=0.02, odt=F32)
+    assert st["chain_rounds"] == st["rounds"] == out["total_verify_rounds"] >= 2
+    plan = out["last_tree_plan"]
+    assert plan["proposal_mode"] == "chain" and plan["node_budget_per_seq"] == 48
 
 
 def _oracle_weights(model, heads):
