@@ -129,9 +129,13 @@ class KVCache:
                          tree_nodes=tree_nodes, row_map=row_map, err_flag=err_flag)
 
     def repeat_rows(self, src_rows: torch.Tensor, dst_rows: torch.Tensor) -> None:
-        """Copy cache rows src -> dst (all layers), e.g. GRPO repeats of one prompt."""
-        self.kv.index_copy_(2, dst_rows.long(), self.kv.index_select(2, src_rows.long()))
-        self.seq_len.index_copy_(0, dst_rows.long(), self.seq_len.index_select(0, src_rows.long()))
+        """Copy cache rows src -> dst (all layers), e.g. GRPO repeats of one prompt. One layer
+        at a time: the gathered temporary holds one layer's source rows (one gather over every
+        layer would hold all of them, 91 GiB for the 14B config's 112 repeated rows)."""
+        src, dst = src_rows.long(), dst_rows.long()
+        for layer in self.kv:  # [2, B, Hkv, capacity, d]
+            layer.index_copy_(1, dst, layer.index_select(1, src))
+        self.seq_len.index_copy_(0, dst, self.seq_len.index_select(0, src))
 
     def container_copy(self) -> "KVCache":
         """A second cache object over the same storage with its own committed lengths
