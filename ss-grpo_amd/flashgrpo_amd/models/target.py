@@ -153,7 +153,8 @@ class KVCache:
         cap = self.capacity if capacity is None else int(capacity)
         out = KVCache(self.cfg, int(rows.numel()), cap, dtype=self.dtype, device=self.device)
         keep = min(cap, self.capacity)
-        out.kv[..., :keep, :].copy_(self.kv.index_select(2, rows)[..., :keep, :])
+        for src, dst in zip(self.kv, out.kv):  # one layer's gathered rows at a time
+            dst[..., :keep, :].copy_(src.index_select(1, rows)[..., :keep, :])
         out.seq_len.copy_(self.seq_len.index_select(0, rows).clamp_max(cap))
         return out
 
