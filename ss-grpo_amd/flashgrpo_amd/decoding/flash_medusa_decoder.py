@@ -687,7 +687,9 @@ class FlashMedusaDecoder:
             r.cache.gather_path(r.seq, walk["acc_nodes"], walk["acc_len"], N, row_map=r.row_map, err_flag=r.err)
             ar = torch.arange(Bc, device=dev)
             last = walk["last_node"].long()
-            r.hidden = hidden_t[ar, last].contiguous()
+            # row gathers as index_select over flattened leading dims (one vectorised gather
+            # launch; two-index advanced indexing ran 34 us for the 7B walk logits)
+            r.hidden = hidden_t.flatten(0, 1).index_select(0, ar * hidden_t.shape[1] + last)
             if walk_logits is None and slot_map is None:
                 r.logits = tree_logits.index_select(0, ar * N + last)
             else:
@@ -695,7 +697,7 @@ class FlashMedusaDecoder:
                     # the last accepted node at position acc_len-1 was sampled from at that
                     # walk step unless it is a leaf (then it has no projected row)
                     tpos = (walk["acc_len"].long() - 1).clamp(0, D - 1)
-                    r.logits = walk_logits[tpos, ar]
+                    r.logits = walk_logits.flatten(0, 1).index_select(0, tpos * walk_logits.shape[1] + ar)
                 else:
                     slots = slot_map[ar, last]
                     r.logits = tree_logits.index_select(0, slots.clamp_min(0).long())
