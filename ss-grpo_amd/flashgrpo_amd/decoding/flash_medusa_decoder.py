@@ -165,8 +165,17 @@ def _quantile_rows(values: np.ndarray, q: float) -> list:
 
 
 class FlashMedusaDecoder:
+    def _arange(self, n: int, dev) -> torch.Tensor:
+        """arange(n) on dev, made once (one fewer launch per use in the per-round path)."""
+        key = (int(n), str(dev))
+        t = self._ar_cache.get(key)
+        if t is None:
+            t = self._ar_cache[key] = torch.arange(int(n), device=dev)
+        return t
+
     def __init__(self, target_model, medusa_heads, tokenizer, config: FlashMedusaConfig):
         self._fit_cache = {}  # (adapted top-k, budget) -> fitted top-k
+        self._ar_cache = {}   # (n, device) -> arange(n), read-only
         if config.acceptance != "exact_target":
             raise NotImplementedError("Only exact_target acceptance is implemented in the main FlashGRPO path")
         if config.cache_update_mode not in {"extract_path", "recompute_accepted"}:
@@ -685,19 +694,19 @@ class FlashMedusaDecoder:
             r.sync()
             t0 = time.time()
             r.cache.gather_path(r.seq, walk["acc_nodes"], walk["acc_len"], N, row_map=r.row_map, err_flag=r.err)
-            ar = torch.arange(Bc, device=dev)
+            ar = self._arange(Bc, dev)
             last = walk["last_node"].long()
             # row gathers as index_select over flattened leading dims (one vectorised gather
             # launch; two-index advanced indexing ran 34 us for the 7B walk logits)
-            r.hidden = hidden_t.flatten(0, 1).index_select(0, ar * hidden_t.shape[1] + last)
+            r.hidden = hidden_t.flatten(0, 1).index_select(0, torch.add(last, ar, alpha=hidden_t.shape[1]))
             if walk_logits is None and slot_map is None:
-                r.logits = tree_logits.index_select(0, ar * N + last)
+                r.logits = tree_logits.index_select(0, torch.add(last, ar, alpha=N))
             else:
                 if walk_logits is not None:
                     # the last accepted node at position acc_len-1 was sampled from at that
                     # walk step unless it is a leaf (then it has no projected row)
                     tpos = (walk["acc_len"].long() - 1).clamp(0, D - 1)
-                    r.logits = walk_logits.flatten(0, 1).index_select(0, tpos * walk_logits.shape[1] + ar)
+                    r.logits = walk_logits.flatten(0, 1).index_select(0, torch.add(ar, tpos, alpha=walk_logits.shape[1]))
                 else:
                     slots = slot_map[ar, last]
                     r.logits = tree_logits.index_select(0, slots.clamp_min(0).long())
