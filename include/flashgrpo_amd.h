@@ -207,7 +207,7 @@ int fg_accept_walk(const void* tree_logits, int dtype, int64_t row_stride, int v
 
 /* The same walk one step at a time, for callers that compute each step's logits
  * rows on demand (the LM head of only the nodes the walk actually samples):
- *   fg_walk_begin  -- initialise outputs and the walk state (3*batch int32);
+ *   fg_walk_begin  -- initialise outputs (acc rows: the root, then zeros) and the walk state (3*batch int32);
  *   fg_walk_rows   -- row_index[b] = b*nmax + current parent of b, row_active[b];
  *   fg_walk_step   -- draw for every active row b from row b of step_logits
  *                     (noise column noise_col0 + walk_step, counter draw draw0 + walk_step).

@@ -331,6 +331,10 @@ __global__ void walk_init_kernel(const int32_t* __restrict__ tree_tokens, const 
   if (b >= batch) return;
   acc_tokens[(int64_t)b * acc_stride] = tree_tokens[(int64_t)b * nmax];
   acc_nodes[(int64_t)b * acc_stride] = 0;
+  for (int j = 1; j < acc_stride; ++j) {  // the rest of the rows start at 0
+    acc_tokens[(int64_t)b * acc_stride + j] = 0;
+    acc_nodes[(int64_t)b * acc_stride + j] = 0;
+  }
   acc_len[b] = 1;
   last_node[b] = 0;
   correction[b] = -1;

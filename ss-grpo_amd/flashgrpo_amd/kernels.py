@@ -421,8 +421,8 @@ def walk_begin(tree_tokens, parents, n_nodes, *, acc_stride):
     _dev(tree_tokens, parents, n_nodes)
     B, nmax = tree_tokens.shape
     dev = tree_tokens.device
-    w = dict(acc_tokens=torch.zeros(B, acc_stride, dtype=torch.int32, device=dev),
-             acc_nodes=torch.zeros(B, acc_stride, dtype=torch.int32, device=dev),
+    w = dict(acc_tokens=torch.empty(B, acc_stride, dtype=torch.int32, device=dev),  # zeroed by fg_walk_begin
+             acc_nodes=torch.empty(B, acc_stride, dtype=torch.int32, device=dev),
              acc_len=torch.empty(B, dtype=torch.int32, device=dev),
              last_node=torch.empty(B, dtype=torch.int32, device=dev),
              correction=torch.empty(B, dtype=torch.int32, device=dev),

@@ -371,6 +371,9 @@ def test_split_top_p_walk_step_equals_single_workgroup():
     walks = []
     for split in (True, False):
         w = K().walk_begin(tt, pp, nn, acc_stride=D + 1)
+        # the root, then zeros (the output buffers come uninitialised from walk_begin)
+        assert torch.equal(w["acc_tokens"][:, 0], tt[:, 0]) and not w["acc_tokens"][:, 1:].any()
+        assert not w["acc_nodes"].any() and bool((w["acc_len"] == 1).all())
         for t in range(D):
             K().walk_rows(w, N)
             rows = torch.from_numpy(packed[np.minimum(np.arange(B), packed.shape[0] - 1)]).to(DEV)
