@@ -659,6 +659,9 @@ int fg_lm_head_topk(const void* x, int M, int K, int64_t ldx, const int32_t* row
   FG_REQUIRE(out_dtype == fg::kBF16 || out_dtype == fg::kF32, "fg_lm_head_topk: out_dtype");
   FG_REQUIRE(out || kmax > 0, "fg_lm_head_topk: nothing to compute (no out, kmax 0)");
   FG_REQUIRE(!out || ldo >= N, "fg_lm_head_topk: ldo < N");
+  // rows whose stride is a multiple of 4 take 4-column vector stores (8 bytes bf16, 16 fp32)
+  FG_REQUIRE(!out || ldo % 4 != 0 || ((uintptr_t)out & (out_dtype == fg::kBF16 ? 7 : 15)) == 0,
+             "fg_lm_head_topk: out must be aligned to 4 columns when ldo is a multiple of 4");
   FG_REQUIRE(kmax >= 0 && kmax <= 16 && kmax <= N, "fg_lm_head_topk: kmax must be in [0, min(16, N)]");
   FG_REQUIRE(kmax == 0 || (cand_tokens && cand_scores && workspace), "fg_lm_head_topk: candidate outputs missing");
   FG_REQUIRE(kmax == 0 || !row_active, "fg_lm_head_topk: row_active only without top-k");

@@ -40,12 +40,47 @@ def _compile(src: str) -> str:
     return obj
 
 
+# Sources whose kernels issue register-destination loads as inline assembly; their device
+# assembly is checked for uses of a load's registers before it lands (_isa_check).
+ASM_CHECKED = {"lm_head.hip": "lm_stream_kernel"}
+
+
+def _device_asm(src: str) -> str:
+    out = os.path.join(BUILD, os.path.basename(src).replace(".hip", ".gfx950.s"))
+    cmd = [hipcc(), *HIP_FLAGS, "-I", CSRC, "--cuda-device-only", "-S", src, "-o", out]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc -S failed for {src}:\n{res.stderr}")
+    return out
+
+
+def check_inline_asm_loads(asm_path: str, name_filter: str) -> int:
+    """Raises if any kernel matching name_filter touches an in-flight load's registers."""
+    from ._isa_check import check_asm
+
+    with open(asm_path) as f:
+        n, hazards = check_asm(f.read(), name_filter)
+    if not n:
+        raise RuntimeError(f"{asm_path}: no kernel named *{name_filter}* to check")
+    if hazards:
+        lines = "\n".join(f"  {fn[:60]} line {ln}: {ins} uses {regs}" for fn, ln, ins, regs in hazards[:10])
+        raise RuntimeError(f"{asm_path}: {len(hazards)} use(s) of in-flight load registers:\n{lines}")
+    return n
+
+
 def build(verbose: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
     sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    workers = max(1, min(len(sources), os.cpu_count() or 4, 8))
+    checked = [s for s in sources if os.path.basename(s) in ASM_CHECKED]
+    workers = max(1, min(len(sources) + len(checked), os.cpu_count() or 4, 10))
     with cf.ThreadPoolExecutor(workers) as ex:
+        asm_jobs = [ex.submit(_device_asm, s) for s in checked]  # the longest jobs first
         objs = list(ex.map(_compile, sources))
+        asms = [j.result() for j in asm_jobs]
+    for src, asm in zip(checked, asms):
+        n = check_inline_asm_loads(asm, ASM_CHECKED[os.path.basename(src)])
+        if verbose:
+            print(f"{os.path.basename(src)}: {n} kernels free of early uses of inline-asm load registers")
     tmp = LIB_PATH + ".tmp"
     cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp]
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -749,8 +749,12 @@ class FlashMedusaDecoder:
             # that finish this round are dropped from it afterwards).
             # Its adaptive-plan statistics come back with this round's results: one host
             # sync per round, and the GPU works while the host reads them.
+            # medusa_time gets the host time of queuing it (the GPU runs it overlapped with
+            # this round's read-back; statistical_time rounds are timed phase by phase)
+            t_front = time.time()
             nxt = self._front(r, rnd + 1, r.logits, r.hidden, r.row_map, new_pending if b200 else r.pending,
                               trace is not None)
+            m["medusa_time"] += time.time() - t_front
         seq_next = r.seq + walk["acc_len"]  # committed lengths after this round (device)
         pack_h = torch.empty(pack_d.shape, dtype=pack_d.dtype, pin_memory=True)
         pack_h.copy_(pack_d, non_blocking=True)

@@ -178,6 +178,14 @@ def lm_head_topk(x, weight, kmax=0, *, row_index=None, row_active=None, out=None
         out = torch.empty(M, N, dtype=out_dtype or torch.bfloat16, device=dev)
     elif not logits:
         out = None
+    elif out is not None:
+        _dev(out)
+        if out.dtype not in (torch.bfloat16, torch.float32) or (out_dtype is not None and out.dtype != out_dtype):
+            raise TypeError("lm_head_topk: out must be bf16 or fp32 (and match out_dtype)")
+        if out.dim() != 2 or tuple(out.shape) != (M, N) or out.stride(1) != 1 or out.stride(0) < N:
+            raise ValueError(f"lm_head_topk: out must be a [{M}, {N}] view with unit column stride")
+        if out.stride(0) % 4 == 0 and out.data_ptr() % (4 * out.element_size()):
+            raise ValueError("lm_head_topk: out rows with a stride of 4k elements need a base aligned to 4 columns")
     tok = torch.empty(M, kmax, dtype=torch.int32, device=dev) if kmax else None
     sc = torch.empty(M, kmax, dtype=torch.float32, device=dev) if kmax else None
     st = torch.empty(M, 2, dtype=torch.float32, device=dev) if kmax and stats else None

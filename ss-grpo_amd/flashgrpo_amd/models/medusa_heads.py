@@ -89,9 +89,13 @@ class MedusaPredictionHead(nn.Module):
             self.output = None
         else:
             self.output = nn.Linear(hidden_size, vocab_size, bias=False, dtype=dtype)
-            if lm_head is not None and getattr(lm_head, "shape", None) == self.output.weight.shape:
+            # the reference copies ``lm_head.weight`` of an nn.Module LM head
+            # (``medusa_heads.py:69-72``, built so by ``flashgrpo_trainer.py:727-733``);
+            # a bare [V, H] weight tensor is taken as well
+            src = lm_head.weight if isinstance(getattr(lm_head, "weight", None), torch.Tensor) else lm_head
+            if isinstance(src, torch.Tensor) and tuple(src.shape) == tuple(self.output.weight.shape):
                 with torch.no_grad():
-                    self.output.weight.copy_(lm_head.detach().to(self.output.weight.dtype))
+                    self.output.weight.copy_(src.detach().to(self.output.weight.dtype))
 
     def project_hidden(self, hidden_states):
         """Single-head residual block on the device (fg_medusa_heads with one head)."""

@@ -75,6 +75,34 @@ class TargetConfig:
         return TargetConfig(48, 5120, 40, 8, 128, 13824, 152064, 1.0e6, 1e-6, True, False, "qwen2.5-14b")
 
 
+def lm_gemm_ok(x: torch.Tensor, w: torch.Tensor) -> bool:
+    """Operand rules of the hand-written bf16 LM-head kernels (``fg_lm_head_topk``,
+    ``fg_lm_head``): K a multiple of 64, both operands K-contiguous with 16-byte aligned
+    rows (base address and row stride), the weight under 4 GiB."""
+    K_ = x.shape[-1]
+    return (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and K_ % 64 == 0 and w.shape[-1] == K_
+            and x.stride(-1) == 1 and w.stride(-1) == 1 and (x.dim() < 2 or x.stride(0) % 8 == 0)
+            and w.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0
+            and w.shape[0] * w.stride(0) * 2 <= 0xFFFFFFFF)
+
+
+def lm_stream_ok(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None) -> bool:
+    """``lm_gemm_ok`` plus the weight-streaming kernel's own limits: x spans under 4 GiB
+    from its first row, and a given output has unit column stride and, when its row stride
+    is a multiple of 4 elements, a base aligned for 4-column stores (8 bytes bf16, 16 fp32)."""
+    if not lm_gemm_ok(x, w):
+        return False
+    x2 = x.reshape(-1, x.shape[-1])
+    if ((x2.shape[0] - 1) * x2.stride(0) + x2.shape[1]) * 2 >= 1 << 32:
+        return False
+    if out is not None:
+        # 4-column vector stores when the row stride is a multiple of 4 elements
+        if out.dim() != 2 or out.stride(1) != 1 or (out.stride(0) % 4 == 0
+                                                     and out.data_ptr() % (4 * out.element_size())):
+            return False
+    return True
+
+
 def inv_freq_table(head_dim: int, theta: float) -> torch.Tensor:
     """fp32 theta^(-2i/d), computed in float64 then rounded once."""
     i = np.arange(0, head_dim, 2, dtype=np.float64)
@@ -615,8 +643,7 @@ class TargetModel:
         (which then writes them), else None."""
         x = hidden.reshape(-1, self.cfg.hidden)
         w = self.w["lm_head"]
-        if not (self.dtype == torch.bfloat16 and 0 < rows <= LM_STREAM_ROWS and x.stride(1) == 1
-                and w.stride(1) == 1 and (x.numel() + x.storage_offset()) * 2 < 1 << 32):
+        if not (0 < rows <= LM_STREAM_ROWS and lm_stream_ok(x, w)):
             return None
         P = K.lm_head_parts(w.shape[0])
         return (torch.empty(rows, P, dtype=torch.float32, device=x.device),
@@ -637,9 +664,10 @@ class TargetModel:
         """
         x = hidden.reshape(-1, self.cfg.hidden)
         w = self.w["lm_head"] if weight is None else weight
+        stream = lm_stream_ok(x, w, out)
         if (row_index is None and row_active is None and self.dtype == torch.bfloat16
                 and (out_dtype is None or out_dtype == self.dtype)):
-            if x.shape[0] <= LM_STREAM_ROWS and x.stride(1) == 1 and w.stride(1) == 1:
+            if x.shape[0] <= LM_STREAM_ROWS and stream:
                 return K.lm_head_topk(x, w, 0, out=out, parts=parts)[0]
             if parts is not None:
                 raise ValueError("logits: row maxima parts need the weight-streaming LM head (see walk_parts)")
@@ -647,13 +675,22 @@ class TargetModel:
                 return F.linear(x, w)
             return torch.matmul(x, w.t(), out=out)
         rows = row_index.numel() if row_index is not None else x.shape[0]
-        if (self.dtype == torch.bfloat16 and 0 < rows <= LM_STREAM_ROWS and x.stride(1) == 1 and w.stride(1) == 1
-                and (x.numel() + x.storage_offset()) * 2 < 1 << 32
+        if (0 < rows <= LM_STREAM_ROWS and stream
                 and (out_dtype is None or out_dtype in (torch.bfloat16, torch.float32))):
             return K.lm_head_topk(x, w, 0, row_index=row_index, row_active=row_active, out=out,
                                   out_dtype=out_dtype, parts=parts)[0]
         if parts is not None:
             raise ValueError("logits: row maxima parts need the weight-streaming LM head (see walk_parts)")
+        if self.dtype == torch.bfloat16 and not lm_gemm_ok(x, w):
+            # operands the hand-written kernels do not take (hidden size not a multiple of 64,
+            # unaligned rows): hipBLASLt over the gathered rows
+            xs = x if row_index is None else x.index_select(0, row_index.long())
+            y = F.linear(xs, w).to(out_dtype or self.dtype)
+            if out is None:
+                return y
+            if row_active is None:
+                return out.copy_(y)
+            return torch.where(row_active.view(-1, 1) != 0, y, out, out=out)
         return K.lm_head(x, w, row_index=row_index, row_active=row_active, out=out, out_dtype=out_dtype)
 
     def logits_masked(self, hidden: torch.Tensor, row_active: torch.Tensor, out: torch.Tensor) -> None:
@@ -662,11 +699,10 @@ class TargetModel:
         device, so a caller need not know the active rows."""
         x = hidden.reshape(-1, self.cfg.hidden)
         w = self.w["lm_head"]
-        if (self.dtype == torch.bfloat16 and out.dtype == torch.bfloat16 and 0 < x.shape[0] <= LM_STREAM_ROWS
-                and x.stride(1) == 1 and w.stride(1) == 1 and (x.numel() + x.storage_offset()) * 2 < 1 << 32):
+        if out.dtype == torch.bfloat16 and 0 < x.shape[0] <= LM_STREAM_ROWS and lm_stream_ok(x, w, out):
             K.lm_head_topk(x, w, 0, row_active=row_active, out=out)  # inactive rows are not written
             return
-        tmp = K.lm_head(x, w, row_active=row_active, out_dtype=out.dtype)
+        tmp = self.logits(x, row_active=row_active, out_dtype=out.dtype)
         torch.where(row_active.view(-1, 1) != 0, tmp, out, out=out)
 
     def logits_topk(self, hidden: torch.Tensor, kmax: int, *, stats: bool = False, sanitize: bool = False,
@@ -682,8 +718,7 @@ class TargetModel:
         x = hidden.reshape(-1, self.cfg.hidden)
         w = self.w["lm_head"] if weight is None else weight
         R = x.shape[0]
-        if (self.dtype == torch.bfloat16 and 0 < R <= LM_STREAM_ROWS and (kmax <= 8 or R <= 192)
-                and x.stride(1) == 1 and w.stride(1) == 1 and kmax >= 1):
+        if 0 < R <= LM_STREAM_ROWS and (kmax <= 8 or R <= 192) and kmax >= 1 and lm_stream_ok(x, w):
             return K.lm_head_topk(x, w, kmax, logits=logits, stats=stats, sanitize=sanitize, workspace=workspace)
         lg = self.logits(x, weight=weight)
         tok, sc, st = K.medusa_topk(lg, kmax, stats=stats, sanitize=sanitize)

@@ -317,6 +317,42 @@ def test_medusa_checkpoint_loading_is_weights_only(tmp_path):
         MedusaHeads.from_pretrained(tmp_path)
 
 
+def test_untied_heads_copy_the_lm_head_module_weight(tmp_path):
+    """Heads built as the trainer builds them (``flashgrpo_trainer.py:727-733``:
+    ``lm_head=base.lm_head``, an nn.Module) start from the LM head's weight
+    (``medusa_heads.py:69-72``), and ``from_pretrained`` keeps that copy for the
+    ``output`` keys a checkpoint lacks or that its shape filter drops
+    (``flashgrpo_trainer.py:749-753``)."""
+    from flashgrpo_amd.models import MedusaHeads
+
+    torch.manual_seed(3)
+    lm_head = nn.Linear(16, 40, bias=False)
+    m = MedusaHeads(hidden_size=16, vocab_size=40, num_heads=2, dtype=torch.float32, tie_lm_head=False,
+                    lm_head=lm_head)
+    for hd in m.heads:
+        assert torch.equal(hd.output.weight, lm_head.weight)
+    # a bare weight tensor is taken too; a mismatched shape leaves nn.Linear's init
+    t = MedusaHeads(16, 40, 1, tie_lm_head=False, lm_head=lm_head.weight)
+    assert torch.equal(t.heads[0].output.weight, lm_head.weight)
+    other = MedusaHeads(16, 40, 1, tie_lm_head=False, lm_head=nn.Linear(16, 41, bias=False))
+    assert not torch.equal(other.heads[0].output.weight[:40], lm_head.weight)
+    # bf16 heads from an fp32 module: copied with a cast
+    b = MedusaHeads(16, 40, 1, dtype=torch.bfloat16, tie_lm_head=False, lm_head=lm_head)
+    assert torch.equal(b.heads[0].output.weight, lm_head.weight.to(torch.bfloat16))
+
+    # a tied checkpoint has no output keys: loaded untied with the trainer's lm_head,
+    # every head keeps the copy
+    MedusaHeads.random(16, 40, 2, seed=1).save_pretrained(tmp_path)
+    cfg_path = tmp_path / "medusa_config.json"
+    cfg = json.loads(cfg_path.read_text())
+    cfg["tie_lm_head"] = False
+    cfg_path.write_text(json.dumps(cfg))
+    back = MedusaHeads.from_pretrained(tmp_path, map_location="cpu", dtype=torch.float32, lm_head=lm_head)
+    assert not any(k.endswith("output.weight") for k in back._loaded_compatible_keys)
+    for hd in back.heads:
+        assert torch.equal(hd.output.weight, lm_head.weight)
+
+
 def test_medusa_output_weights_follow_parameter_updates():
     from flashgrpo_amd.models import MedusaHeads
 
@@ -380,3 +416,25 @@ def test_sync_works_for_weights_made_inside_or_outside_inference_mode():
         assert outside.sync_from_hf()
     for m in (inside, outside):
         _check_against_modules(m, hf)
+
+
+# ------------------------------------------------------------------ LM-head routing rules
+def test_lm_head_routing_predicates():
+    """The hand-written LM-head kernels take bf16 operands with K % 64 == 0 and 16-byte
+    aligned rows; anything else routes to the library GEMM (host-side decision only)."""
+    from flashgrpo_amd.models.target import lm_gemm_ok, lm_stream_ok
+
+    bf = torch.bfloat16
+    x = torch.zeros(8, 128, dtype=bf)
+    w = torch.zeros(100, 128, dtype=bf)
+    assert lm_gemm_ok(x, w) and lm_stream_ok(x, w)
+    assert not lm_gemm_ok(torch.zeros(8, 96, dtype=bf), torch.zeros(100, 96, dtype=bf))   # K % 64
+    assert not lm_gemm_ok(x.float(), w.float())                                           # dtype
+    assert not lm_gemm_ok(torch.zeros(8, 129, dtype=bf)[:, 1:], w)                        # base not 16-byte aligned
+    assert not lm_gemm_ok(torch.zeros(8, 132, dtype=bf)[:, :128], w)                      # row stride 132
+    assert not lm_gemm_ok(x, torch.zeros(128, 100, dtype=bf).t())                         # weight not K-contiguous
+    out = torch.zeros(8, 100, dtype=bf)
+    assert lm_stream_ok(x, w, out)
+    assert not lm_stream_ok(x, w, torch.zeros(100, 8, dtype=bf).t())                      # output column stride
+    assert not lm_stream_ok(x, w, torch.zeros(8, 104, dtype=bf)[:, 1:101])               # 4-column store alignment
+    assert lm_stream_ok(x, w, torch.zeros(8, 103, dtype=bf)[:, :100])                     # stride 103: scalar stores

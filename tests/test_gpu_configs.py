@@ -105,18 +105,43 @@ def _oracle_weights(model, heads):
     return W, hd
 
 
-def test_full_size_7b_round():
+FULL_SIZE = {
+    # name: (prefix, prompts, repeats, TargetConfig args after num_layers, Medusa heads, decoder config,
+    #        expected plan, expected nodes)
+    "7b": (2048, 8, 8, (3584, 28, 4, 128, 18944, 152064, 1e6, 1e-6, True, False), 4,
+           dict(tree_mode="concurrency_aware", cpeak_nodes=2048, max_tree_nodes_per_seq=32, max_tree_depth=5,
+                fixed_tree_topk_by_depth=(4, 3, 2), adaptive_tree_enabled=True, adaptive_min_topk_by_depth=(1, 1, 1)),
+           [4, 2, 1, 1], 29),
+    "14b": (4096, 16, 8, (5120, 40, 8, 128, 13824, 152064, 1e6, 1e-6, True, False), 4,
+            dict(tree_mode="concurrency_aware", cpeak_nodes=8192, max_tree_nodes_per_seq=64, max_tree_depth=5,
+                 fixed_tree_topk_by_depth=(4, 3, 2)),
+            [4, 3, 2], 41),
+    "1p5b": (512, 4, 8, (1536, 12, 2, 128, 8960, 151936, 1e6, 1e-6, True, True), 3,
+             dict(tree_mode="concurrency_aware", cpeak_nodes=512, max_tree_nodes_per_seq=16, max_tree_depth=4,
+                  fixed_tree_topk_by_depth=(4, 3, 2)),
+             [4, 2], 13),
+}
+
+
+@pytest.mark.parametrize("name", ["7b", "14b", "1p5b"])
+def test_full_size_round(name):
+    """One verify round at a BASELINE configuration's full batch, prefix, width and
+    vocabulary (one decoder layer): 7B (64 sequences = 8 prompts x 8 repeats, 2048-token
+    prefix, adaptive 32-node budget -> [4, 2, 1, 1]), 14B (128 = 16 x 8, 4096-token prefix,
+    64-node budget -> [4, 3, 2], three Medusa heads x 128 rows = 384 LM-head rows, 1024
+    attention workgroups over 65 key tiles) and 1.5B (32 = 4 x 8, 512-token prefix, 16-node
+    budget -> [4, 2]). Checked from the device's post-prefill cache (prefill itself checked
+    on one prompt), in lockstep with the oracle, then the extraction bit for bit."""
     from flashgrpo_amd.decoding import FlashMedusaConfig, FlashMedusaDecoder
     from flashgrpo_amd.models import MedusaHeads, TargetConfig, TargetModel
 
-    P, B0, R, V, H = 2048, 8, 8, 152064, 3584
-    tcfg = TargetConfig(1, H, 28, 4, 128, 18944, V, 1e6, 1e-6, True, False, "qwen2.5-7b-1-layer")
+    P, B0, R, dims, nh, dkw, want_plan, want_nodes = FULL_SIZE[name]
+    H, V = dims[0], dims[5]
+    print(f"full-size round {name}: B={B0 * R} P={P} H={H} V={V}", flush=True)
+    tcfg = TargetConfig(1, *dims, name=f"{name}-1-layer")
     model = TargetModel.random(tcfg, seed=0, dtype=torch.bfloat16, device=DEV)
-    heads = MedusaHeads.random(H, V, 4, seed=1, device=DEV)
-    dcfg = FlashMedusaConfig(num_medusa_heads=4, tree_mode="concurrency_aware", cpeak_nodes=2048,
-                             max_tree_nodes_per_seq=32, max_tree_depth=5, fixed_tree_topk_by_depth=(4, 3, 2),
-                             adaptive_tree_enabled=True, adaptive_min_topk_by_depth=(1, 1, 1), temperature=1.0,
-                             top_p=1.0, noise_seed=2)
+    heads = MedusaHeads.random(H, V, nh, seed=1, device=DEV)
+    dcfg = FlashMedusaConfig(num_medusa_heads=nh, temperature=1.0, top_p=1.0, noise_seed=2, **dkw)
     dec = FlashMedusaDecoder(model, heads, Tok(-1), dcfg)
     prompts = np.random.default_rng(3).integers(0, V, (B0, P))
     r = dec.start(torch.from_numpy(prompts), torch.ones(B0, P, dtype=torch.long), repeated_generate_nums=R,
@@ -135,10 +160,10 @@ def test_full_size_7b_round():
     dec.step(r, trace)
     torch.cuda.synchronize()
     rec = trace[0]
-    assert len(rec["active"]) == B and rec["plan"] == [4, 2, 1, 1] and rec["tree_tokens"].shape == (B, 29)
+    assert len(rec["active"]) == B and rec["plan"] == want_plan and rec["tree_tokens"].shape == (B, want_nodes)
     W, hd = _oracle_weights(model, heads)
-    ocfg = OM.ModelConfig(1, H, 28, 4, 128, 18944, V, 1e6, 1e-6, True, False)
-    # prefill of prompt 0 (2048 causal tokens through the chunked chain attention)
+    ocfg = OM.ModelConfig(1, *dims)
+    # prefill of prompt 0 (causal tokens through the chunked chain attention)
     hid, pk, pv = OM.prefill(ocfg, W, prompts[:1], dtype=F32)
     assert rel(kv0[0, 0, :, :P], pk[0][0]) < 2e-2 and rel(kv0[1, 0, :, :P], pv[0][0]) < 2e-2
     assert rel(rec["hidden_in"][0], hid[0, -1]) < 2e-2
@@ -149,9 +174,7 @@ def test_full_size_7b_round():
     rows = {s: OracleRow(ocfg, None, None, F32, state=(rec["hidden_in"][i], [kv0[0, s:s + 1, :, :P]],
                                                        [kv0[1, s:s + 1, :, :P]], P))
             for i, s in enumerate(rec["active"])}
-    spec = OD.DecodeSpec(tree_mode="concurrency_aware", cpeak_nodes=2048, max_tree_nodes_per_seq=32,
-                         fixed_tree_topk_by_depth=(4, 3, 2), num_medusa_heads=4, max_tree_depth=5,
-                         adaptive_tree_enabled=True, top_p=1.0)
+    spec = OD.DecodeSpec(num_medusa_heads=nh, top_p=1.0, **dkw)
     st = lockstep(trace, ocfg, W, hd, spec, None, torch.bfloat16, rec["seed"], P + 64, odt=F32, rows=rows)
     assert st["rounds"] == 1
     # extraction: accepted rows moved bit-exactly, every other slot untouched

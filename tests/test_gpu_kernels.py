@@ -815,3 +815,73 @@ def test_walk_with_lm_head_parts_equals_plain_walk(mode):
         for t in range(D):
             assert torch.equal(runs[0][1][t], steps[t]), t
     assert int(runs[0][0]["acc_len"].max()) >= 3  # the planted paths were walked
+
+
+@pytest.mark.parametrize("mode", [{}, {"temperature": 0.7}, {"top_p": 0.9}, {"greedy": True}])
+def test_planted_deep_lazy_walk_full_vocab_matches_oracle(mode):
+    """The lazy walk at the 7B configuration's vocabulary, batch and tree (V = 152064, 64
+    sequences, [4, 2, 1, 1] in 32 nodes) against ``oracle.sampling.accept_walk``: hidden
+    rows steer four of every five internal nodes to one of their children, so most
+    sequences accept deep paths; each step projects the rows the walk stands on with the
+    weight-streaming LM head (row maxima parts, next rows written by the step) and draws
+    with ``fg_walk_step`` under counter noise. The oracle walks the same trees on the
+    device's logits rows (checked against an fp32 product) with the same noise; accepted
+    tokens, nodes, lengths, last nodes and correction tokens are equal."""
+    rng = np.random.default_rng(11)
+    B, ks, budget, V, H = 64, [4, 2, 1, 1], 32, 152064, 256
+    parents, _, _ = OT.dense_topology(ks, budget)
+    N, D = len(parents), len(ks)
+    toks = rng.integers(0, V, (B, N)).astype(np.int32)
+    trees = [OT.Tree(toks[b].tolist(), parents, None) for b in range(B)]
+    g = torch.Generator(device="cpu").manual_seed(5)
+    w = (torch.randn(V, H, generator=g) * 0.05).to(torch.bfloat16)
+    hid = torch.from_numpy(rng.standard_normal((B * N, H)).astype(np.float32) * 0.5)
+    wf = w.float()
+    for b, t in enumerate(trees):
+        for n in range(N):
+            kids = t.children(n)
+            if kids and (b + n) % 5:
+                tok = t.tokens[kids[(b + n) % len(kids)]]
+                hid[b * N + n] = wf[tok] * (24.0 / float(wf[tok].pow(2).sum()))
+    hid, w = hid.to(torch.bfloat16).to(DEV), w.to(DEV)
+    tt = torch.from_numpy(toks).to(DEV)
+    pp = torch.tensor([parents] * B, dtype=torch.int32, device=DEV)
+    nn = torch.full((B,), N, dtype=torch.int32, device=DEV)
+    P = K().lm_head_parts(V)
+    parts = (torch.empty(B, P, dtype=torch.float32, device=DEV), torch.empty(B, P, dtype=torch.int64, device=DEV))
+    T, greedy, top_p = mode.get("temperature", 1.0), mode.get("greedy", False), mode.get("top_p", 1.0)
+    wk = K().walk_begin(tt, pp, nn, acc_stride=D + 1)
+    K().walk_rows(wk, N)
+    step_logits = []
+    for t in range(D):
+        lg = torch.full((B, V), 5.0, dtype=torch.bfloat16, device=DEV)
+        K().lm_head_topk(hid, w, 0, row_index=wk["row_index"], row_active=wk["row_active"], out=lg, parts=parts)
+        K().walk_step(wk, lg, tt, pp, nn, walk_step=t, seed=3, step=2, temperature=T, greedy=greedy, top_p=top_p,
+                      parts=parts, next_rows=True)
+        step_logits.append(lg)
+    torch.cuda.synchronize()
+    acc_len = wk["acc_len"].cpu().numpy()
+    acc_nodes = wk["acc_nodes"].cpu().numpy()
+    # the rows each sequence sampled from, packed; nodes the device never stood on map to a
+    # trailing zero row (a walk that left the device's path would read it and mismatch)
+    visited = [(b, t, int(acc_nodes[b, t])) for b in range(B) for t in range(int(acc_len[b]))
+               if trees[b].children(int(acc_nodes[b, t]))]
+    packed = np.zeros((len(visited) + 1, V), np.float32)
+    slots = [[len(visited)] * N for _ in range(B)]
+    for j, (b, t, node) in enumerate(visited):
+        packed[j] = to_np(step_logits[t][b])
+        slots[b][node] = j
+    rows = torch.tensor([b * N + node for b, _, node in visited], device=DEV)
+    want_lg = to_np(hid[rows].float() @ w.float().t())
+    assert rel_err(packed[:-1], want_lg) < 2e-2
+    nz = [[OS.counter_noise(3, 2, b, 1 + t) for t in range(D)] for b in range(B)]
+    at, an, last, corr = OS.accept_walk(trees, packed, nz, do_sample=not greedy, temperature=T, top_p=top_p,
+                                        top_k=None, slots=slots, emit_correction=True)
+    for b in range(B):
+        L = int(acc_len[b])
+        assert L == len(at[b]), b
+        assert wk["acc_tokens"][b, :L].tolist() == at[b], b
+        assert acc_nodes[b, :L].tolist() == an[b], b
+        assert int(wk["last_node"][b]) == last[b], b
+        assert int(wk["correction"][b]) == (-1 if corr[b] is None else corr[b]), b
+    assert int(acc_len.max()) == D + 1 and int((acc_len == D + 1).sum()) >= B // 4

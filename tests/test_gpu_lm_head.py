@@ -176,6 +176,50 @@ def test_rejects_unsupported_shapes():
         K().lm_head_topk(torch.randn(4, 128, device=DEV), w, 0)
 
 
+def test_target_lm_head_routes_hidden_96():
+    """A bf16 target whose hidden size is not a multiple of 64 (96) runs every LM-head
+    route on the library GEMM (the hand-written kernels take K % 64 == 0 only): contiguous,
+    gathered and masked rows, the top-k path and the walk's row-maxima parts (None)."""
+    from flashgrpo_amd.models.target import TargetModel, TargetConfig
+
+    cfg = TargetConfig(num_layers=1, hidden=96, q_heads=1, kv_heads=1, head_dim=96, intermediate=192, vocab=3001)
+    model = TargetModel.random(cfg, seed=4, dtype=torch.bfloat16, device=DEV)
+    w = model.w["lm_head"]
+    h = torch.randn(20, 96, device=DEV).to(torch.bfloat16)
+    ref = (h.float() @ w.float().t())
+    full = model.logits(h)
+    assert full.shape == (20, 3001) and rel_err(to_np(full), to_np(ref)) < 2e-2
+    idx = torch.tensor([3, 3, 0, 19], dtype=torch.int32, device=DEV)
+    g = model.logits(h, row_index=idx)
+    assert torch.equal(g, full[idx.long()])
+    act = torch.zeros(20, dtype=torch.int32, device=DEV)
+    act[[2, 5]] = 1
+    out = torch.full((20, 3001), 7.0, dtype=torch.bfloat16, device=DEV)
+    model.logits_masked(h, act, out)
+    assert torch.equal(out[act.bool()], full[act.bool()]) and bool((out[~act.bool()] == 7.0).all())
+    lg, tok, sc, st = model.logits_topk(h, 4, stats=True, logits=True)
+    assert torch.equal(lg, full)
+    check_candidates(lg, tok, sc, st, 4, False)
+    assert model.walk_parts(20, h) is None
+
+
+def test_lm_head_topk_validates_out():
+    """A caller's out tensor of the wrong shape, layout, dtype or alignment is refused
+    before any launch."""
+    x = torch.randn(8, 128, device=DEV).to(torch.bfloat16)
+    w = torch.randn(1000, 128, device=DEV).to(torch.bfloat16)
+    good = torch.empty(8, 1000, dtype=torch.bfloat16, device=DEV)
+    ref = K().lm_head_topk(x, w, 0)[0]
+    assert torch.equal(K().lm_head_topk(x, w, 0, out=good)[0], ref)
+    bad = [torch.empty(7, 1000, dtype=torch.bfloat16, device=DEV),              # too few rows
+           torch.empty(1000, 8, dtype=torch.bfloat16, device=DEV).t(),          # transposed
+           torch.empty(8, 1001, dtype=torch.bfloat16, device=DEV)[:, 1:],       # base not 4-column aligned
+           torch.empty(8, 1000, dtype=torch.float16, device=DEV)]               # dtype
+    for o in bad:
+        with pytest.raises((ValueError, TypeError)):
+            K().lm_head_topk(x, w, 0, out=o)
+
+
 def test_target_logits_topk_routes_and_matches():
     """TargetModel.logits_topk: the fused path (<= 256 bf16 rows) equals logits + top-k."""
     from flashgrpo_amd.models.target import TargetModel, TargetConfig
