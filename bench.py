@@ -171,32 +171,53 @@ def planted_walk_gather(cfg, r, work, elem, reps=5):
         logits[t, ar, tokens[:, path[t + 1]].long()] += 60.0
     kw = dict(seed=7, step=0, seq_ids=r.row_map, draw0=1, temperature=work["temperature"], greedy=False,
               top_p=work["top_p"], err_flag=r.err)
+    # The lazy walk gets each step's row maxima from the LM head that writes the step's logits
+    # (fg_lm_head_topk's part_max / part_key), so a decoder walk step is the q-mass and pick
+    # launches. Here the planted logits come from torch, so the same maxima are formed once per
+    # step outside the timed region (one part per row: the maximum and its first index's rank key).
+    parts = []
+    for t in range(D):
+        lf = logits[t].float()
+        mx, arg = lf.max(dim=1)
+        bits = mx.view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+        key32 = torch.where(mx < 0, (~bits) & 0xFFFFFFFF, bits | 0x80000000)
+        key32 = torch.where(mx == 0, torch.full_like(key32, 0x80000000), key32)
+        pk = ((key32 << 32) | (0xFFFFFFFF - arg.to(torch.int64))).view(B, 1).contiguous()
+        parts.append((mx.view(B, 1).contiguous(), pk))
     ev = lambda: torch.cuda.Event(enable_timing=True)
-    walk_ms, gather_ms = [], []
-    for _ in range(reps):
-        # a spin kernel first, so the host has queued the launches below before they
-        # run and the events time the GPU, not the launch rate
+    # evicts L2 and the 256 MB Infinity Cache between gather launches: each gather then reads
+    # its rows from HBM, as it does in a rollout (the rows were written a round earlier)
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    walk_ms, walk_max_ms, gather_ms = [], [], []
+    for rep in range(reps):
+        for with_parts, out in ((True, walk_ms), (False, walk_max_ms)):
+            # a spin kernel first, so the host has queued the launches below before they
+            # run and the events time the GPU, not the launch rate
+            torch.cuda._sleep(4_000_000)
+            walk = K.walk_begin(tokens, parents, n_nodes, acc_stride=D + 1)
+            for t in range(D):
+                K.walk_rows(walk, N)
+                e0, e1 = ev(), ev()
+                e0.record()
+                K.walk_step(walk, logits[t], tokens, parents, n_nodes, walk_step=t,
+                            parts=parts[t] if with_parts else None, **kw)
+                e1.record()
+                out.append((e0, e1))
+        flush.fill_(rep & 0xFF)
         torch.cuda._sleep(4_000_000)
-        walk = K.walk_begin(tokens, parents, n_nodes, acc_stride=D + 1)
-        for t in range(D):
-            K.walk_rows(walk, N)
-            e0, e1 = ev(), ev()
-            e0.record()
-            K.walk_step(walk, logits[t], tokens, parents, n_nodes, walk_step=t, **kw)
-            e1.record()
-            walk_ms.append((e0, e1))
         e0, e1 = ev(), ev()
         e0.record()
         r.cache.gather_path(r.seq, walk["acc_nodes"], walk["acc_len"], N, row_map=r.row_map, err_flag=r.err)
         e1.record()
         gather_ms.append((e0, e1))
     torch.cuda.synchronize()
+    del flush
     if not bool((walk["acc_len"] == D + 1).all()) or int(r.err.max()) != 0:
         raise RuntimeError("planted walk did not accept the full depth")
-    # The gather alone, as batches of back-to-back repeats of the last walk's paths between
-    # two events: events around one launch of a ~5 us kernel add their own few us. Repeats
-    # move the same tree slots past the committed lengths again (the committed rows are
-    # never written) and take the same time.
+    # Back-to-back repeats of the last walk's gather between two events: the rows are then
+    # resident in L2 / the Infinity Cache, so this is a warm figure, not an HBM rate. Repeats
+    # move the same tree slots past the committed lengths again (the committed rows are never
+    # written) and take the same time.
     batch_ms = []
     for _ in range(reps):
         torch.cuda._sleep(4_000_000)
@@ -209,9 +230,10 @@ def planted_walk_gather(cfg, r, work, elem, reps=5):
     torch.cuda.synchronize()
     if int(r.err.max()) != 0:
         raise RuntimeError("planted gather reported an index error")
-    w_us = sum(a.elapsed_time(b) for a, b in walk_ms) / len(walk_ms) * 1e3
-    g_us_single = sum(a.elapsed_time(b) for a, b in gather_ms) / len(gather_ms) * 1e3
-    g_us = sorted(a.elapsed_time(b) for a, b in batch_ms)[len(batch_ms) // 2] * 1e3 / GATHER_BATCH
+    mean_us = lambda evs: sum(a.elapsed_time(b) for a, b in evs) / len(evs) * 1e3
+    w_us, wm_us = mean_us(walk_ms), mean_us(walk_max_ms)
+    g_us = sorted(a.elapsed_time(b) for a, b in gather_ms)[len(gather_ms) // 2] * 1e3
+    g_warm = sorted(a.elapsed_time(b) for a, b in batch_ms)[len(batch_ms) // 2] * 1e3 / GATHER_BATCH
     w_bytes = B * V * elem
     # rows a path keeps in place (the root, and node j == j) are not moved: the bytes are
     # the moved rows' reads and writes; ref_bytes also counts the rows left in place (the
@@ -221,15 +243,19 @@ def planted_walk_gather(cfg, r, work, elem, reps=5):
     row_bytes = 2 * cfg.num_layers * 2 * cfg.kv_heads * cfg.head_dim * elem
     g_bytes = row_bytes * moved
     g_ref_bytes = row_bytes * B * (D + 1)
+    rate = lambda b, us: round(b / us / 1e3, 1)
     return {"depth": D, "sequences": B,
-            "walk_step": {"avg_us": round(w_us, 2), "bytes": w_bytes, "GBps": round(w_bytes / w_us / 1e3, 1),
-                          "hbm_frac": round(w_bytes / w_us / 1e3 / HBM_PEAK_GBS, 4)},
-            # avg_us: median batch of GATHER_BATCH launches / GATHER_BATCH; single_launch_us: events
-            # around each launch. hbm_frac counts the bytes the kernel moves; ref_hbm_frac the
-            # algorithmic bytes of the reference's gather + copy_ (every accepted row read and written)
-            "kv_path_gather": {"avg_us": round(g_us, 2), "single_launch_us": round(g_us_single, 2),
+            # walk_step: the decoder's step (row maxima supplied); with_max_us: plus the chunk-maxima
+            # launch (a draw whose logits did not come from the LM head)
+            "walk_step": {"avg_us": round(w_us, 2), "with_max_us": round(wm_us, 2), "bytes": w_bytes,
+                          "GBps": rate(w_bytes, w_us), "hbm_frac": round(w_bytes / w_us / 1e3 / HBM_PEAK_GBS, 4)},
+            # avg_us: one launch on cold rows (caches flushed before it; events around the launch
+            # add ~2 us). hbm_frac counts the bytes the kernel moves; ref_hbm_frac the algorithmic
+            # bytes of the reference's gather + copy_ (every accepted row read and written).
+            # warm_batch_us: back-to-back repeats, rows cache-resident (not an HBM rate)
+            "kv_path_gather": {"avg_us": round(g_us, 2), "warm_batch_us": round(g_warm, 2),
                                "bytes": g_bytes, "moved_rows": moved, "ref_bytes": g_ref_bytes,
-                               "GBps": round(g_bytes / g_us / 1e3, 1),
+                               "GBps": rate(g_bytes, g_us),
                                "hbm_frac": round(g_bytes / g_us / 1e3 / HBM_PEAK_GBS, 4),
                                "ref_hbm_frac": round(g_ref_bytes / g_us / 1e3 / HBM_PEAK_GBS, 4)}}
 

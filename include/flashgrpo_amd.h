@@ -177,7 +177,7 @@ int fg_sample_tokens(const void* logits, int dtype, int64_t row_stride, int rows
 /* fg_sample_tokens without a workspace argument and without any allocation. No
  * counterpart in the reference: it is for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
- * The split partials live in a static device array of the library (8.6 MB per GPU,
+ * The split partials live in a static device array of the library (9.1 MB per GPU,
  * held until the process ends) that holds rows <= fg_sample_tokens_noalloc_max_rows()
  * (256); more rows are rejected with an error. Same arguments, rule and tokens as
  * fg_sample_tokens with a large enough workspace. Every call on one GPU shares that

@@ -6,77 +6,87 @@ The reference draws with ``torch.multinomial`` (``flashgrpo/decoding/acceptance.
 which cannot take caller noise. This build fixes one deterministic
 noise-to-token rule that the HIP kernels reproduce bit for bit:
 
-1. ``s_i = fp32(x_i) / T`` (correctly rounded; T <= 0 or None means no scaling),
-   ``m = max s``, ``t_i = s_i - m``.
-2. ``e_i = exp_fg(t_i)``: Cody-Waite range reduction plus the Cephes ``expf``
-   minimax polynomial (S. L. Moshier, Cephes Math Library), evaluated with
-   separately rounded fp32 multiplies and adds (no fused multiply-add), 0 below -64.
-3. ``q_i = trunc(e_i * 2^40)`` as uint64; all sums are exact integer sums.
-4. Candidate order O = (fp32 key of s_i desc, index asc).  ``top_k`` keeps the
+1. ``m = max x`` over the fp32 logits (NaN ignored); ``kt = fp32(2^20 / ln 2)``,
+   divided (correctly rounded, once) by T when 0 < T != 1.
+2. ``a_i = trunc(min(fp32(fp32(m - x_i) * kt), Z_MAX))``, a fixed-point base-2
+   exponent with 20 fraction bits (NaN, -inf and anything 40 octaves below m clamp
+   to Z_MAX, whose weight is 0).
+3. ``q_i = floor(2^40 * 2^(-a_i / 2^20))`` as uint64, evaluated as
+   ``w = T[r] - ((T[r] - T[r+1]) * f >> 10)`` with ``r`` bits 10-19 and ``f`` bits 0-9
+   of a_i, ``T[r] = round(2^31 * 2^(-r/1024))``, then ``q = (w << 32) >> (23 + a_i >> 20)``.
+   So q_i = 2^40 exp((x_i - m) / T) to within ~1e-6 relative (2^-20 octave steps,
+   linear interpolation between 1024 table points); all sums are exact integer sums.
+4. Candidate order O = (fp32 key of x_i desc, index asc).  ``top_k`` keeps the
    first k of O.  ``top_p`` keeps O-position j iff the q-mass of the kept
    candidates before j is <= floor(total * tp32 / 2^32), tp32 = floor(top_p * 2^32)
    (the reference rule "keep while preceding cumsum <= top_p",
    ``acceptance.py:62-66``, in exact integers).
 5. Draw: ``target = floor(total_kept * u / 2^32)``; the token is the lowest
    vocabulary index among kept candidates whose inclusive q prefix (vocabulary
-   order) exceeds ``target``.
+   order) exceeds ``target``; a row whose kept mass is 0 draws its first maximum.
 Greedy (``do_sample`` false or T == 0) is argmax with the first maximum
 (``acceptance.py:43-44``).
 """
 from __future__ import annotations
+
+from decimal import ROUND_HALF_EVEN, Decimal, localcontext
 
 import numpy as np
 
 from .tree import sort_key32
 
 F32 = np.float32
-LOG2E = F32(1.44269504088896341)
-LN2_HI = F32(0.693359375)
-LN2_LO = F32(-2.12194440e-4)
-# Cephes expf polynomial coefficients (cephes/single/expf.c).
-EXP_P = [F32(1.9875691500e-4), F32(1.3981999507e-3), F32(8.3334519073e-3),
-         F32(4.1665795894e-2), F32(1.6666665459e-1), F32(5.0000001201e-1)]
 Q_SHIFT = 40
-EXP_CUTOFF = F32(-64.0)
+KT_BASE = F32(1512775.375)           # fp32(2^20 / ln 2)
+Z_MAX = F32((41 << 20) - 4)          # a >> 20 = 40: shift 63, weight 0
 
 
-def exp_fg(t) -> np.ndarray:
-    """Deterministic fp32 exp for t <= 0 (see module docstring, step 2)."""
-    t = np.asarray(t, dtype=F32)
+def exp2_table() -> np.ndarray:
+    """T[r] = round(2^31 * 2^(-r / 1024)), r = 0..1024, from 60-digit decimal arithmetic."""
+    with localcontext() as ctx:
+        ctx.prec = 60
+        two = Decimal(2)
+        vals = [int((two ** (Decimal(-r) / 1024) * (1 << 31)).to_integral_value(ROUND_HALF_EVEN))
+                for r in range(1025)]
+    return np.array(vals, dtype=np.uint64)
+
+
+_TABLE = exp2_table()
+
+
+def weight_scale(temperature) -> np.float32:
+    """kt of step 1: fp32(2^20 / ln 2), divided by T when 0 < T != 1."""
+    if temperature is not None and temperature > 0 and F32(temperature) != F32(1.0):
+        return F32(KT_BASE / F32(temperature))
+    return KT_BASE
+
+
+def row_max(x) -> np.float32:
+    """max x with NaN ignored (-inf for an empty or all-NaN row)."""
+    x = np.asarray(x, F32)
+    if x.size == 0 or np.all(np.isnan(x)):
+        return F32(-np.inf)
+    return F32(np.nanmax(x))
+
+
+def fixed_exponent(x, temperature=None, m=None) -> np.ndarray:
+    """a_i of step 2 (uint32)."""
+    x = np.asarray(x, F32)
+    m = row_max(x) if m is None else F32(m)
     with np.errstate(invalid="ignore", over="ignore"):
-        ok = t >= EXP_CUTOFF
-        tt = np.where(ok, t, F32(0.0)).astype(F32)
-        kf = np.rint(tt * LOG2E).astype(F32)
-        r = (tt - kf * LN2_HI).astype(F32)
-        r = (r - kf * LN2_LO).astype(F32)
-        z = (r * r).astype(F32)
-        p = EXP_P[0]
-        for c in EXP_P[1:]:
-            p = (p * r).astype(F32)
-            p = (p + c).astype(F32)
-        y = (p * z).astype(F32)
-        y = (y + r).astype(F32)
-        y = (y + F32(1.0)).astype(F32)
-        ki = kf.astype(np.int32)
-        scale = ((ki + 127).astype(np.uint32) << np.uint32(23)).view(F32)
-        e = (y * scale).astype(F32)
-    return np.where(ok, e, F32(0.0)).astype(F32)
+        d = (m - x).astype(F32)
+        z = np.fmin((d * weight_scale(temperature)).astype(F32), Z_MAX)
+    return z.astype(np.uint32)
 
 
-def scaled_logits(x, temperature) -> np.ndarray:
-    x = np.asarray(x).astype(F32)
-    if temperature is not None and temperature > 0:
-        return (x / F32(temperature)).astype(F32)
-    return x
-
-
-def quantized_weights(s) -> np.ndarray:
-    """q_i = trunc(exp_fg(s_i - max s) * 2^40) as uint64 (module docstring 1-3)."""
-    s = np.asarray(s, dtype=F32)
-    m = np.max(s)
-    t = (s - m).astype(F32)
-    e = exp_fg(t)
-    return (e * F32(2.0 ** Q_SHIFT)).astype(np.uint64)
+def quantized_weights(x, temperature=None) -> np.ndarray:
+    """q_i of step 3 (uint64) for the logits row x at temperature T."""
+    a = fixed_exponent(x, temperature).astype(np.uint64)
+    r = (a >> np.uint64(10)) & np.uint64(1023)
+    f = a & np.uint64(1023)
+    t0 = _TABLE[r]
+    w = t0 - (((t0 - _TABLE[r + np.uint64(1)]) * f) >> np.uint64(10))
+    return (w << np.uint64(32)) >> ((a >> np.uint64(20)) + np.uint64(23))
 
 
 def top_p_fixed(top_p) -> int:
@@ -86,10 +96,11 @@ def top_p_fixed(top_p) -> int:
     return int(float(top_p) * 4294967296.0)
 
 
-def kept_mask(s, q, *, top_k=None, top_p=None) -> np.ndarray:
+def kept_mask(x, q, *, top_k=None, top_p=None) -> np.ndarray:
     """Boolean mask of the candidates kept by top-k then top-p (docstring step 4)."""
-    V = s.shape[-1]
-    key = sort_key32(s)
+    x = np.asarray(x, F32)
+    V = x.shape[-1]
+    key = sort_key32(x)
     idx = np.arange(V, dtype=np.uint64)
     order = np.argsort(~((key << np.uint64(32)) | (np.uint64(0xFFFFFFFF) - idx)), kind="stable")
     n_keep = V
@@ -109,12 +120,11 @@ def kept_mask(s, q, *, top_k=None, top_p=None) -> np.ndarray:
 
 def sample_row(x, u32, *, do_sample=True, temperature=1.0, top_p=1.0, top_k=None) -> int:
     """One supplied-noise draw from one logits row (module docstring)."""
-    x = np.asarray(x)
+    x = np.asarray(x).astype(F32)
     if (not do_sample) or temperature == 0:
-        return int(np.argmax(x.astype(F32)))
-    s = scaled_logits(x, temperature)
-    q = quantized_weights(s)
-    keep = kept_mask(s, q, top_k=top_k, top_p=top_p)
+        return int(np.argmax(x))
+    q = quantized_weights(x, temperature)
+    keep = kept_mask(x, q, top_k=top_k, top_p=top_p)
     qk = np.where(keep, q, np.uint64(0))
     total = int(qk.sum(dtype=np.uint64))
     if total == 0:
@@ -133,9 +143,9 @@ def sample_rows(logits, noise, **kw) -> np.ndarray:
 
 def token_probabilities(x, *, temperature=1.0, top_p=1.0, top_k=None) -> np.ndarray:
     """Exact probability of each token under the rule, over all 2^32 noise values."""
-    s = scaled_logits(x, temperature)
-    q = quantized_weights(s)
-    keep = kept_mask(s, q, top_k=top_k, top_p=top_p)
+    x = np.asarray(x).astype(F32)
+    q = quantized_weights(x, temperature)
+    keep = kept_mask(x, q, top_k=top_k, top_p=top_p)
     qk = [int(v) if k else 0 for v, k in zip(q.tolist(), keep.tolist())]
     total = sum(qk)
     probs = []
@@ -271,9 +281,9 @@ def mulhi_u64_u32(total: int, u) -> np.ndarray:
 
 def sample_same_row(x, noise, *, temperature=1.0, top_p=1.0, top_k=None) -> np.ndarray:
     """Vectorised ``sample_row`` of one row under many noise values (distribution tests)."""
-    s = scaled_logits(x, temperature)
-    q = quantized_weights(s)
-    keep = kept_mask(s, q, top_k=top_k, top_p=top_p)
+    x = np.asarray(x).astype(F32)
+    q = quantized_weights(x, temperature)
+    keep = kept_mask(x, q, top_k=top_k, top_p=top_p)
     qk = np.where(keep, q, np.uint64(0))
     total = int(qk.sum(dtype=np.uint64))
     target = mulhi_u64_u32(total, noise)

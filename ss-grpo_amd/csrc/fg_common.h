@@ -9,6 +9,8 @@
 
 #include <string>
 
+#include "fg_exp2_table.h"
+
 #define FG_DEVICE __device__ __forceinline__
 
 namespace fg {
@@ -116,74 +118,30 @@ FG_DEVICE float rank_key_value(uint64_t k) {
   return __uint_as_float(b);
 }
 
-// ------------------------------------------------------------------ exp_fg
-// Deterministic fp32 exp for t <= 0: Cody-Waite reduction with a split ln2 and
-// the Cephes expf minimax polynomial (S. L. Moshier, Cephes Math Library,
-// single/expf.c), evaluated with separately rounded multiplies and adds so that
-// the CPU oracle (numpy float32) reproduces every bit. Inputs below -64 (and
-// NaN) give 0.
-//
-// exp_fg_core: the evaluation itself, for -64 <= t <= 0.
-FG_DEVICE float exp_fg_core(float t) {
+// ------------------------------------------------------------------ sampling weight
+// The integer weight of logit x in a row with maximum m (NaN ignored):
+//   a = trunc(min((m - x) * kt, kWeightZmax))   fp32 ops, each rounded; kt = kWeightKt / T
+//   q = floor(2^40 * 2^-(a / 2^20))             = 2^40 * exp(-(m - x) / T), 2^20 steps per octave
+// evaluated as w = T[r] - (D[r] * f >> 10) for the table entry r = bits 10-19 of a (T[r] =
+// round(2^31 * 2^(-r/1024)), D[r] = T[r] - T[r+1]) and the low bits f = bits 0-9, then
+// q = (w << 32) >> (23 + (a >> 20)). x = m gives 2^40; -inf, NaN and anything 40 octaves
+// below m give 0 (the clamp keeps the shift at most 63). tbl: kExp2Table staged in LDS.
+FG_DEVICE uint64_t weight_q40(float m, float x, float kt, const uint64_t* tbl) {
 #pragma clang fp contract(off)
-  float kf = rintf(t * 1.44269504088896341f);
-  float r = t - kf * 0.693359375f;
-  r = r - kf * -2.12194440e-4f;
-  float z = r * r;
-  float p = 1.9875691500e-4f;
-  p = p * r;
-  p = p + 1.3981999507e-3f;
-  p = p * r;
-  p = p + 8.3334519073e-3f;
-  p = p * r;
-  p = p + 4.1665795894e-2f;
-  p = p * r;
-  p = p + 1.6666665459e-1f;
-  p = p * r;
-  p = p + 5.0000001201e-1f;
-  float y = p * z;
-  y = y + r;
-  y = y + 1.0f;
-  int ki = (int)kf;
-  float scale = __uint_as_float((uint32_t)(ki + 127) << 23);
-  return y * scale;
+  const float z = fminf((m - x) * kt, kWeightZmax);
+  const uint32_t a = (uint32_t)z;
+  const uint64_t e = tbl[(a >> 10) & 1023u];
+  const uint32_t w = (uint32_t)e - (__umul24((uint32_t)(e >> 32), a & 1023u) >> 10);
+  return ((uint64_t)w << 32) >> ((a >> 20) + 23u);
 }
 
-// Branch-free: the polynomial runs on max(t, -64) and the result is selected.
-FG_DEVICE float exp_fg(float t) {
-  const bool in = t >= -64.0f;
-  const float e = exp_fg_core(in ? t : -64.0f);
-  return in ? e : 0.0f;
-}
+// kt for temperature T (> 0 divides, otherwise no scaling), correctly rounded.
+FG_DEVICE float weight_kt(bool scale, float T) { return scale ? __fdiv_rn(kWeightKt, T) : kWeightKt; }
 
-// trunc(e * 2^40) as uint64 for 0 <= e < 2^23, by exponent/mantissa arithmetic (exact).
-// Branch-free: zero (exponent field 0; exp_fg never returns subnormals) and values
-// below 2^-40 shift the 24-bit significand out entirely.
-FG_DEVICE uint64_t quantize_q40(float e) {
-  const uint32_t b = __float_as_uint(e);
-  const int ex = (int)((b >> 23) & 0xff);
-  const uint64_t m = (uint64_t)((b & 0x7fffffu) | 0x800000u);
-  const int sh = ex - 127 + 40 - 23;  // value = m * 2^sh
-  const uint64_t up = m << (sh > 0 ? sh : 0);
-  const uint64_t down = m >> (sh < 0 ? (-sh < 63 ? -sh : 63) : 0);
-  return sh >= 0 ? up : down;
-}
-
-// The sampling weight quantize_q40(exp_fg(t)) of t = s - max s (t <= 0, or NaN), in fewer
-// operations: t is clamped to -64 (exp_fg(-64) * 2^40 < 1, so below -64 and NaN still
-// give 0), and for 0 <= e <= 1 the float v = e * 2^40 is cut into 32-bit halves, each
-// converted with truncation: hi = trunc(v * 2^-32) and lo = trunc(v - hi * 2^32), where
-// the scalings are exact and the subtraction is exact (v's ulp is at least 2^9 once
-// v >= 2^32). The split equals quantize_q40(e) for every float e in [0, 1] (checked
-// exhaustively over those 1,065,353,217 values).
-FG_DEVICE uint64_t weight_q40(float t) {
-#pragma clang fp contract(off)
-  const float e = exp_fg_core(fmaxf(t, -64.0f));
-  const float v = e * 1099511627776.0f;          // 2^40
-  const float h = v * 2.3283064365386963e-10f;   // 2^-32
-  const uint32_t hi = (uint32_t)h;
-  const float lo = v - (float)hi * 4294967296.0f;
-  return ((uint64_t)hi << 32) | (uint64_t)(uint32_t)lo;
+// Copies kExp2Table into LDS (every thread of the block takes part; a barrier must
+// follow before the first weight_q40).
+FG_DEVICE void exp2_table_to_lds(uint64_t* dst) {
+  for (int i = threadIdx.x; i < 1024; i += blockDim.x) dst[i] = kExp2Table[i];
 }
 
 // floor(a * u / 2^32) for a < 2^64, u < 2^32.

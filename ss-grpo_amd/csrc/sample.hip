@@ -5,8 +5,9 @@
 // flashgrpo_b200/decoding/acceptance.py:184-267). torch.multinomial cannot take
 // caller noise, so the draw follows one integer inverse-CDF rule that the CPU
 // oracle reproduces bit for bit:
-//   s_i = x_i / T (correctly rounded), m = max s, q_i = trunc(exp_fg(s_i - m) * 2^40)
-//   candidate order (key(s) desc, index asc); top_k keeps the first k; top_p
+//   m = max x (NaN ignored), q_i = weight_q40(m, x_i, kt): 2^40 * 2^-(a_i / 2^20) for the
+//   fixed-point exponent a_i = trunc((m - x_i) * fp32(2^20 / ln 2) / T) (fg_common.h)
+//   candidate order (key(x) desc, index asc); top_k keeps the first k; top_p
 //   keeps position j while the preceding kept mass <= floor(total * tp32 / 2^32)
 //   target = floor(total_kept * u32 / 2^32); token = first kept index (vocab
 //   order) whose inclusive q prefix exceeds target.
@@ -31,6 +32,7 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kStep = 512;  // elements per wave step
 
 struct Shared {
+  uint64_t exp2[1024];  // kExp2Table
   uint64_t wsum[kWaves];
   uint64_t hist[256];
   uint64_t wkey[kWaves];
@@ -44,9 +46,9 @@ struct Row {
   const char* p;
   int V;
   int seg;
-  float T;
-  bool scale;
-  float m;  // max scaled logit
+  float kt;             // weight scale: fp32(2^20 / ln 2) / T
+  const uint64_t* tbl;  // kExp2Table in LDS
+  float m;              // row maximum (NaN ignored)
 
   FG_DEVICE int load(int i0, float (&x)[8]) const {
     if (i0 + 8 <= V) {
@@ -58,8 +60,9 @@ struct Row {
     for (int j = 0; j < 8; ++j) x[j] = j < n ? fg::load_elem<DT>(p, i0 + j) : 0.0f;
     return n < 0 ? 0 : n;
   }
-  FG_DEVICE float scaled(float x) const { return scale ? __fdiv_rn(x, T) : x; }
-  FG_DEVICE uint64_t weight(float s) const { return fg::weight_q40(s - m); }
+  // candidates are ranked by the logits themselves (the temperature scales the weight)
+  FG_DEVICE float scaled(float x) const { return x; }
+  FG_DEVICE uint64_t weight(float s) const { return fg::weight_q40(m, s, kt, tbl); }
 };
 
 // Candidate-set predicate: key > kappa, or key == kappa and index <= last.
@@ -230,9 +233,7 @@ FG_DEVICE KeyCut radix_select(const Row<DT>& r, KeyCut within, uint64_t target, 
 
 // First maximum of the raw logits (rank keys: value desc, index asc).
 template <int DT>
-FG_DEVICE int block_argmax(const Row<DT>& r0, Shared& sh) {
-  Row<DT> raw = r0;
-  raw.scale = false;
+FG_DEVICE int block_argmax(const Row<DT>& raw, Shared& sh) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   uint64_t best = 0;
   for_wave_segment(raw, [&](int i, float, uint32_t key) {
@@ -264,17 +265,13 @@ FG_DEVICE int block_sample(const void* rowp, int V, const SampleParams& sp, uint
   r.p = (const char*)rowp;
   r.V = V;
   r.seg = (((V + kWaves - 1) / kWaves) + kStep - 1) / kStep * kStep;
-  r.scale = sp.temperature > 0.0f && sp.temperature != 1.0f;
-  r.T = sp.temperature;
+  r.kt = fg::weight_kt(sp.temperature > 0.0f && sp.temperature != 1.0f, sp.temperature);
+  r.tbl = sh.exp2;
   r.m = 0.0f;
   if (sp.greedy) return block_argmax<DT>(r, sh);
-  // Row max of raw logits; division by T > 0 is monotone, so max(x/T) = max(x)/T.
+  fg::exp2_table_to_lds(sh.exp2);  // visible after the barriers of the max below
   float mx = -INFINITY;
-  {
-    Row<DT> raw = r;
-    raw.scale = false;
-    for_wave_segment(raw, [&](int, float s, uint32_t) { mx = fmaxf(mx, s); });
-  }
+  for_wave_segment(r, [&](int, float s, uint32_t) { mx = fmaxf(mx, s); });
   mx = fg::wave_max(mx);
   __syncthreads();
   if (lane == 0) sh.wmax[wave] = mx;
@@ -282,7 +279,7 @@ FG_DEVICE int block_sample(const void* rowp, int V, const SampleParams& sp, uint
   mx = -INFINITY;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, sh.wmax[w]);
-  r.m = r.scale ? __fdiv_rn(mx, r.T) : mx;
+  r.m = mx;
 
   KeyCut keep = kAll;
   if (sp.top_k > 0) keep = radix_select<false, DT>(r, kAll, (uint64_t)(sp.top_k - 1), sh);
@@ -462,7 +459,9 @@ struct SplitArgs {
   float* part_max;           // [rows, kSplitChunks]
   uint64_t* part_key;
   uint64_t* part_sum;
-  float* row_m;              // [rows] scaled row maximum (sum launch -> pick launch)
+  uint64_t* part_gsum;       // [rows, kSplitChunks, kSplitMaxGroups] q-mass per group of kSplitGroup
+  int groups;                // groups per chunk (group sums kept only up to kSplitMaxGroups)
+  float* row_m;              // [rows] row maximum (sum launch -> pick launch)
   uint64_t* row_best;        // [rows] first maximum's rank key
   // row maxima parts read by the draw launch: [rows, src_stride], src_parts used
   const float* src_max;
@@ -497,7 +496,11 @@ FG_DEVICE bool split_skip(const SplitArgs& a, int r) {
 // Elements per workgroup pass: kSplitLoads groups of 8 per thread, all loads in flight
 // before the weights are computed.
 constexpr int kSplitLoads = 4;
-constexpr int kSplitPass = kSplitThreads * 8 * kSplitLoads;
+constexpr int kSplitGroup = kSplitThreads * 8;
+constexpr int kSplitPass = kSplitGroup * kSplitLoads;
+// Per-group q-mass is kept for chunks of up to kSplitMaxGroups groups (vocabularies up to
+// 16 x 16 x 2,048 = 524,288): the pick then weighs one group instead of the whole chunk.
+constexpr int kSplitMaxGroups = 16;
 
 // Load group u of a pass starting at base (elements base + (u * kSplitThreads + t) * 8 ..
 // + 7 of thread t) holds an element before hi. Uniform over the workgroup: a group wholly
@@ -517,7 +520,10 @@ FG_DEVICE void split_load8(const char* p, int i0, int hi, float (&x)[8]) {
   for (int j = 0; j < 8; ++j) x[j] = i0 + j < hi ? fg::load_elem<DT>(p, i0 + j) : -INFINITY;
 }
 
-// Chunk maxima (raw maximum, NaN ignored, and the first-maximum rank key).
+// Chunk maxima (raw maximum, NaN ignored, and the first-maximum rank key). Per pass a thread
+// takes the maximum of its elements (NaN ignored) and then the first index holding it (the
+// first NaN when there is one, which ranks highest), and forms one rank key per pass instead
+// of one per element.
 template <int DT>
 __global__ void __launch_bounds__(kSplitThreads) split_max_kernel(SplitArgs a) {
   const int c = blockIdx.x, r = blockIdx.y;
@@ -533,18 +539,33 @@ __global__ void __launch_bounds__(kSplitThreads) split_max_kernel(SplitArgs a) {
 #pragma unroll
     for (int u = 0; u < kSplitLoads; ++u)
       if (split_group_live(base, u, hi)) split_load8<DT>(p, base + (u * kSplitThreads + threadIdx.x) * 8, hi, x[u]);
-    // the -inf padding past hi never wins: a real element's key is at least as large
-    // and its index smaller
+    // the -inf padding past hi never wins: real elements come first and the first index holding
+    // the maximum is taken
+    float pm = -INFINITY;
+    bool nan = false;
 #pragma unroll
     for (int u = 0; u < kSplitLoads; ++u) {
       if (!split_group_live(base, u, hi)) continue;
-      const int i0 = base + (u * kSplitThreads + threadIdx.x) * 8;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        mx = fmaxf(mx, x[u][j]);
-        const uint64_t k = fg::rank_key(x[u][j], (uint32_t)(i0 + j));
-        best = k > best ? k : best;
+        pm = fmaxf(pm, x[u][j]);
+        nan |= x[u][j] != x[u][j];
       }
+    }
+    int first = -1;
+    float kv = pm;
+#pragma unroll
+    for (int u = kSplitLoads - 1; u >= 0; --u) {
+      if (!split_group_live(base, u, hi)) continue;
+      const int i0 = base + (u * kSplitThreads + threadIdx.x) * 8;
+#pragma unroll
+      for (int j = 7; j >= 0; --j) first = (nan ? x[u][j] != x[u][j] : x[u][j] == pm) ? i0 + j : first;
+    }
+    if (nan) kv = __uint_as_float(0x7fc00000u);
+    mx = fmaxf(mx, pm);
+    if (first >= 0) {
+      const uint64_t k = fg::rank_key(kv, (uint32_t)first);
+      best = k > best ? k : best;
     }
   }
   mx = fg::wave_max(mx);
@@ -566,25 +587,19 @@ __global__ void __launch_bounds__(kSplitThreads) split_max_kernel(SplitArgs a) {
   }
 }
 
-// Row maximum of the scaled logits from the chunk maxima (x / T is monotone).
+// Row maximum from the chunk maxima.
 FG_DEVICE float split_row_max(const SplitArgs& a, int r) {
   float mx = -INFINITY;
   for (int c = 0; c < kSplitChunks; ++c) mx = fmaxf(mx, a.part_max[r * kSplitChunks + c]);
-  return a.scale ? __fdiv_rn(mx, a.temperature) : mx;
+  return mx;
 }
 
-// q weight of raw logit x against the scaled row maximum m.
-template <bool SCALE>
-FG_DEVICE uint64_t split_weight(float x, float T, float m) {
-  const float sv = SCALE ? __fdiv_rn(x, T) : x;
-  return fg::weight_q40(sv - m);
-}
+FG_DEVICE float split_kt(const SplitArgs& a) { return fg::weight_kt(a.scale != 0, a.temperature); }
 
-template <bool SCALE>
-FG_DEVICE uint64_t split_weight8(const float (&x)[8], float T, float m) {
+FG_DEVICE uint64_t split_weight8(const float (&x)[8], float kt, float m, const uint64_t* tbl) {
   uint64_t acc = 0;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) acc += split_weight<SCALE>(x[j], T, m);
+  for (int j = 0; j < 8; ++j) acc += fg::weight_q40(m, x[j], kt, tbl);
   return acc;
 }
 
@@ -616,13 +631,14 @@ FG_DEVICE void split_parts_max(const SplitArgs& a, int r, float* smax, uint64_t*
 
 // q-mass of each chunk against the row maximum taken from the row's parts; chunk 0 also
 // keeps the scaled maximum and the first maximum for the pick launch.
-template <int DT, bool SCALE>
+template <int DT>
 __global__ void __launch_bounds__(kSplitThreads) split_sum_kernel(SplitArgs a) {
   const int c = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
   if (split_skip(a, r)) return;
+  __shared__ uint64_t tbl[1024];
   __shared__ float smax[kSplitWaves];
   __shared__ uint64_t skey[kSplitWaves];
-  __shared__ uint64_t ssum[kSplitWaves];
+  __shared__ uint64_t gsum[kSplitMaxGroups];
   const char* p = split_row<DT>(a, r);
   const int lo = c * a.chunk, hi = min(a.vocab, lo + a.chunk);
   // the first pass's logits are in flight while the row maximum is gathered from the parts
@@ -630,11 +646,16 @@ __global__ void __launch_bounds__(kSplitThreads) split_sum_kernel(SplitArgs a) {
 #pragma unroll
   for (int u = 0; u < kSplitLoads; ++u)
     if (split_group_live(lo, u, hi)) split_load8<DT>(p, lo + (u * kSplitThreads + tid) * 8, hi, x[u]);
+  fg::exp2_table_to_lds(tbl);  // visible after the barrier in split_parts_max
+  if (tid < kSplitMaxGroups) gsum[tid] = 0;
   float mx;
   uint64_t best;
   split_parts_max(a, r, smax, skey, mx, best);
-  const float m = SCALE ? __fdiv_rn(mx, a.temperature) : mx;
-  uint64_t acc = 0;
+  const float m = mx, kt = split_kt(a);
+  // each group's q-mass: wave sums added into LDS (group g of the chunk = elements
+  // [lo + 2048 g, lo + 2048 (g + 1)) = load group u of pass g / 4)
+  const bool keep_groups = a.groups <= kSplitMaxGroups;
+  int g = 0;
   for (int base = lo; base < hi; base += kSplitPass) {
     if (base != lo) {
 #pragma unroll
@@ -642,16 +663,21 @@ __global__ void __launch_bounds__(kSplitThreads) split_sum_kernel(SplitArgs a) {
         if (split_group_live(base, u, hi)) split_load8<DT>(p, base + (u * kSplitThreads + tid) * 8, hi, x[u]);
     }
 #pragma unroll
-    for (int u = 0; u < kSplitLoads; ++u)
-      if (split_group_live(base, u, hi)) acc += split_weight8<SCALE>(x[u], a.temperature, m);
+    for (int u = 0; u < kSplitLoads; ++u) {
+      if (!split_group_live(base, u, hi)) continue;
+      const uint64_t w = fg::wave_sum_u64(split_weight8(x[u], kt, m, tbl));
+      if ((tid & 63) == 0) atomicAdd((unsigned long long*)&gsum[keep_groups ? g + u : 0], (unsigned long long)w);
+    }
+    g += kSplitLoads;
   }
-  acc = fg::wave_sum_u64(acc);
-  if ((tid & 63) == 0) ssum[tid >> 6] = acc;
   __syncthreads();
   if (tid == 0) {
     uint64_t t = 0;
-#pragma unroll
-    for (int w = 0; w < kSplitWaves; ++w) t += ssum[w];
+    const int ng = keep_groups ? a.groups : 1;
+    for (int q = 0; q < ng; ++q) {
+      t += gsum[q];
+      if (keep_groups) a.part_gsum[((size_t)r * kSplitChunks + c) * kSplitMaxGroups + q] = gsum[q];
+    }
     a.part_sum[r * kSplitChunks + c] = t;
     if (c == 0) {
       a.row_m[r] = m;
@@ -664,8 +690,8 @@ __global__ void __launch_bounds__(kSplitThreads) split_sum_kernel(SplitArgs a) {
 // block; -1 if none), scanned in index order one group of kSplitThreads x 8 elements at a
 // time (thread t holds 8 consecutive elements of a group), stopping at the group that holds
 // the target: on average half the chunk is weighed. A pass's groups are loaded together.
-template <int DT, bool SCALE>
-FG_DEVICE int split_locate(const SplitArgs& a, const char* p, int lo, int hi, float m, uint64_t target,
+template <int DT>
+FG_DEVICE int split_locate(const char* p, int lo, int hi, float m, float kt, const uint64_t* tbl, uint64_t target,
                            uint64_t* wsum, int* found) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (tid == 0) *found = -1;
@@ -679,7 +705,7 @@ FG_DEVICE int split_locate(const SplitArgs& a, const char* p, int lo, int hi, fl
 #pragma unroll
     for (int u = 0; u < kSplitLoads; ++u) {
       if (!split_group_live(base, u, hi)) break;  // uniform
-      const uint64_t mine = split_weight8<SCALE>(x[u], a.temperature, m);
+      const uint64_t mine = split_weight8(x[u], kt, m, tbl);
       const uint64_t incl = fg::wave_incl_scan_u64(mine);
       __syncthreads();  // wsum of the previous group has been read
       if (lane == 63) wsum[wave] = incl;
@@ -696,7 +722,7 @@ FG_DEVICE int split_locate(const SplitArgs& a, const char* p, int lo, int hi, fl
           const int i0 = base + (u * kSplitThreads + tid) * 8;
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            cum += split_weight<SCALE>(x[u][j], a.temperature, m);
+            cum += fg::weight_q40(m, x[u][j], kt, tbl);
             if (cum > target) {
               *found = i0 + j;
               break;
@@ -742,9 +768,10 @@ struct DrawOut {
 // The draw of each row (one workgroup per row) from the chunk sums of split_sum_kernel
 // (greedy draws: from the row's parts alone): the chunk whose running mass crosses the
 // target, then the index inside it.
-template <int DT, bool WALK, bool SCALE>
+template <int DT, bool WALK>
 __global__ void __launch_bounds__(kSplitThreads) split_pick_kernel(SplitArgs a, DrawOut d) {
   const int r = blockIdx.x, tid = threadIdx.x;
+  __shared__ uint64_t tbl[1024];
   __shared__ float smax[kSplitWaves];
   __shared__ uint64_t skey[kSplitWaves];
   __shared__ uint64_t wsum[kSplitWaves];
@@ -772,6 +799,7 @@ __global__ void __launch_bounds__(kSplitThreads) split_pick_kernel(SplitArgs a, 
       total += sums[q];
     }
     if (total > 0) {
+      fg::exp2_table_to_lds(tbl);  // visible after split_locate's first barrier
       const uint32_t seq = d.seq_ids ? (uint32_t)d.seq_ids[r] : (uint32_t)r;
       const int ws = WALK ? d.walk_step : 0;
       const uint32_t u = noise_value(d.noise, (int64_t)r * d.noise_stride + d.noise_col + ws, d.seed, d.step, seq,
@@ -786,9 +814,24 @@ __global__ void __launch_bounds__(kSplitThreads) split_pick_kernel(SplitArgs a, 
         }
         before += sums[q];
       }
-      const int clo = cs * a.chunk, chi = min(a.vocab, clo + a.chunk);
-      const int idx = split_locate<DT, SCALE>(a, split_row<DT>(a, r), clo, chi, a.row_m[r], target - before, wsum,
-                                              &s_found);
+      int clo = cs * a.chunk, chi = min(a.vocab, clo + a.chunk);
+      if (a.groups <= kSplitMaxGroups) {
+        // the group of 2,048 whose running mass crosses the target: one group is weighed
+        const uint64_t* gs = a.part_gsum + ((size_t)r * kSplitChunks + cs) * kSplitMaxGroups;
+        const int ng = (chi - clo + kSplitGroup - 1) / kSplitGroup;
+        int q = ng - 1;
+        for (int k = 0; k < ng; ++k) {
+          if (before + gs[k] > target) {
+            q = k;
+            break;
+          }
+          before += gs[k];
+        }
+        clo += q * kSplitGroup;
+        chi = min(chi, clo + kSplitGroup);
+      }
+      const int idx = split_locate<DT>(split_row<DT>(a, r), clo, chi, a.row_m[r], split_kt(a), tbl, target - before,
+                                       wsum, &s_found);
       if (idx >= 0) tok = idx;  // always: the chunk holds the target
     }
   }
@@ -830,8 +873,7 @@ FG_DEVICE void for_chunk(const SplitArgs& a, int r, int c, F&& f) {
 #pragma unroll
     for (int j = 0; j < 8; ++j)
       if (i0 + j < hi) {
-        const float sv = a.scale ? __fdiv_rn(x[j], a.temperature) : x[j];
-        f(i0 + j, sv, fg::sort_key32(sv));
+        f(i0 + j, x[j], fg::sort_key32(x[j]));
       }
   }
 }
@@ -897,17 +939,19 @@ template <int DT>
 __global__ void __launch_bounds__(kSplitThreads) split_topp_level_kernel(SplitArgs a, int level) {
   const int c = blockIdx.x, r = blockIdx.y;
   if (split_skip(a, r)) return;
+  __shared__ uint64_t tbl[1024];
   __shared__ uint64_t hs[256];
   __shared__ uint64_t red[kSplitThreads / 64];
   __shared__ int sdig;
   __shared__ uint64_t sabove;
+  fg::exp2_table_to_lds(tbl);  // visible after the barriers below
   SelState st{0u, 0u, 0ull, 0ull};
   if (level >= 2) st = a.sel[r * 2 + ((level - 2) & 1)];
   if (level >= 1) {
     split_merge_level(a, r, 24 - 8 * (level - 1), level == 1, st, hs, red, &sdig, &sabove);
     if (c == 0 && threadIdx.x == 0) a.sel[r * 2 + ((level - 1) & 1)] = st;
   }
-  const float m = split_row_max(a, r);
+  const float m = split_row_max(a, r), kt = split_kt(a);
   const int shift = 24 - 8 * level;
   __syncthreads();
   hs[threadIdx.x] = 0;
@@ -915,7 +959,7 @@ __global__ void __launch_bounds__(kSplitThreads) split_topp_level_kernel(SplitAr
   for_chunk<DT>(a, r, c, [&](int, float sv, uint32_t key) {
     if ((key & st.pmask) == st.prefix)
       atomicAdd((unsigned long long*)&hs[(key >> shift) & 255u],
-                (unsigned long long)fg::weight_q40(sv - m));
+                (unsigned long long)fg::weight_q40(m, sv, kt, tbl));
   });
   __syncthreads();
   a.hist[((size_t)r * kSplitChunks + c) * 256 + threadIdx.x] = hs[threadIdx.x];
@@ -926,19 +970,21 @@ template <int DT>
 __global__ void __launch_bounds__(kSplitThreads) split_topp_cut_kernel(SplitArgs a) {
   const int c = blockIdx.x, r = blockIdx.y;
   if (split_skip(a, r)) return;
+  __shared__ uint64_t tbl[1024];
   __shared__ uint64_t hs[256];
   __shared__ uint64_t red[kSplitThreads / 64];
   __shared__ int sdig;
   __shared__ uint64_t sabove;
+  fg::exp2_table_to_lds(tbl);  // visible after the barriers of the merge
   SelState st = a.sel[r * 2 + 0];  // after level 2
   split_merge_level(a, r, 0, false, st, hs, red, &sdig, &sabove);
   if (c == 0 && threadIdx.x == 0) a.sel[r * 2 + 1] = st;
-  const float m = split_row_max(a, r);
+  const float m = split_row_max(a, r), kt = split_kt(a);
   const uint32_t kappa = st.prefix;
   uint64_t above = 0, tie = 0;
   for_chunk<DT>(a, r, c, [&](int, float sv, uint32_t key) {
     if (key >= kappa) {
-      const uint64_t w = fg::weight_q40(sv - m);
+      const uint64_t w = fg::weight_q40(m, sv, kt, tbl);
       if (key > kappa) above += w;
       else tie += w;
     }
@@ -966,14 +1012,14 @@ struct KeptIn {
 };
 
 template <int DT>
-FG_DEVICE Row<DT> chunk_row(const SplitArgs& a, int r, int c) {
+FG_DEVICE Row<DT> chunk_row(const SplitArgs& a, int r, int c, const uint64_t* tbl) {
   const int lo = c * a.chunk;
   Row<DT> rr;
   rr.p = split_row<DT>(a, r) + (int64_t)lo * (DT == fg::kBF16 ? 2 : 4);
   rr.V = max(0, min(a.vocab, lo + a.chunk) - lo);
   rr.seg = (((rr.V + kWaves - 1) / kWaves) + kStep - 1) / kStep * kStep;
-  rr.scale = a.scale;
-  rr.T = a.temperature;
+  rr.kt = split_kt(a);
+  rr.tbl = tbl;
   rr.m = split_row_max(a, r);
   return rr;
 }
@@ -981,6 +1027,7 @@ FG_DEVICE Row<DT> chunk_row(const SplitArgs& a, int r, int c) {
 // The token of row r (whole block; every thread returns it).
 template <int DT>
 FG_DEVICE int split_topp_pick(const SplitArgs& a, int r, uint32_t u, Shared& sh) {
+  fg::exp2_table_to_lds(sh.exp2);  // visible after the first barrier of block_sum
   const SelState st = a.sel[r * 2 + 1];
   const uint32_t kappa = st.prefix;
   const uint64_t* pa = a.part_a + r * kSplitChunks;
@@ -999,7 +1046,7 @@ FG_DEVICE int split_topp_pick(const SplitArgs& a, int r, uint32_t u, Shared& sh)
   uint32_t last = 0xffffffffu;
   uint64_t tie_cs = 0;  // tie mass kept in chunk cs
   if (cs >= 0) {
-    const Row<DT> rr = chunk_row<DT>(a, r, cs);
+    const Row<DT> rr = chunk_row<DT>(a, r, cs, sh.exp2);
     block_sum<true, DT>(rr, TieAt{kappa}, sh);
     const int idx = block_locate<true, DT>(rr, TieAt{kappa}, need - tb, sh);
     if (idx >= 0) {
@@ -1029,7 +1076,7 @@ FG_DEVICE int split_topp_pick(const SplitArgs& a, int r, uint32_t u, Shared& sh)
     }
     before += kc;
   }
-  const Row<DT> r2 = chunk_row<DT>(a, r, c2);
+  const Row<DT> r2 = chunk_row<DT>(a, r, c2, sh.exp2);
   const KeptIn kept{kappa, last, (uint32_t)(c2 * a.chunk)};
   block_sum<true, DT>(r2, kept, sh);
   const int idx = block_locate<true, DT>(r2, kept, target - before, sh);
@@ -1085,26 +1132,21 @@ void split_topp_partials(const SplitArgs& a, int rows, hipStream_t s) {
 
 // A split draw: the chunk maxima unless a.src_* already hold row maxima parts, the
 // chunk sums (not for greedy draws), the pick (1 to 3 launches).
-template <int DT, bool WALK, bool SCALE>
-void split_draw_scaled(const SplitArgs& a, const DrawOut& d, int rows, bool with_max, hipStream_t s) {
-  if (with_max) hipLaunchKernelGGL(split_max_kernel<DT>, dim3(kSplitChunks, rows), dim3(kSplitThreads), 0, s, a);
-  if (!a.greedy)
-    hipLaunchKernelGGL((split_sum_kernel<DT, SCALE>), dim3(kSplitChunks, rows), dim3(kSplitThreads), 0, s, a);
-  hipLaunchKernelGGL((split_pick_kernel<DT, WALK, SCALE>), dim3(rows), dim3(kSplitThreads), 0, s, a, d);
-}
 template <int DT, bool WALK>
 void split_draw(const SplitArgs& a, const DrawOut& d, int rows, bool with_max, hipStream_t s) {
-  if (a.scale) split_draw_scaled<DT, WALK, true>(a, d, rows, with_max, s);
-  else split_draw_scaled<DT, WALK, false>(a, d, rows, with_max, s);
+  if (with_max) hipLaunchKernelGGL(split_max_kernel<DT>, dim3(kSplitChunks, rows), dim3(kSplitThreads), 0, s, a);
+  if (!a.greedy) hipLaunchKernelGGL(split_sum_kernel<DT>, dim3(kSplitChunks, rows), dim3(kSplitThreads), 0, s, a);
+  hipLaunchKernelGGL((split_pick_kernel<DT, WALK>), dim3(rows), dim3(kSplitThreads), 0, s, a, d);
 }
 
 constexpr size_t split_workspace_bytes(int rows) {
   return (size_t)rows * kSplitChunks * (4 + 8 + 8) + (size_t)rows * kSplitChunks * 256 * 8 +
-         (size_t)rows * 2 * sizeof(SelState) + (size_t)rows * kSplitChunks * 16 + (size_t)rows * (8 + 4) + 256;
+         (size_t)rows * 2 * sizeof(SelState) + (size_t)rows * kSplitChunks * 16 + (size_t)rows * (8 + 4) +
+         (size_t)rows * kSplitChunks * kSplitMaxGroups * 8 + 256;
 }
 
 // Scratch of fg_sample_tokens_noalloc: the split partials of up to
-// kNoAllocMaxRows rows (8.6 MB per device, held until the process ends). Each
+// kNoAllocMaxRows rows (9.1 MB per device, held until the process ends). Each
 // kernel of the split paths writes every partial it owns before a later launch
 // reads it, so nothing in it has to start at zero. Host code never hands
 // `scratch` itself to a kernel (in host code the name is only a stand-in): it
@@ -1147,7 +1189,8 @@ bool split_setup(SplitArgs& a, void* workspace, size_t bytes, int rows, const vo
   a.part_t = a.part_a + (size_t)rows * kSplitChunks;
   a.sel = (SelState*)(a.part_t + (size_t)rows * kSplitChunks);
   a.row_best = (uint64_t*)(a.sel + (size_t)rows * 2);
-  a.part_max = (float*)(a.row_best + rows);
+  a.part_gsum = a.row_best + rows;
+  a.part_max = (float*)(a.part_gsum + (size_t)rows * kSplitChunks * kSplitMaxGroups);
   a.row_m = a.part_max + (size_t)rows * kSplitChunks;
   a.src_max = a.part_max;
   a.src_key = a.part_key;
@@ -1158,6 +1201,7 @@ bool split_setup(SplitArgs& a, void* workspace, size_t bytes, int rows, const vo
   a.row_stride = row_stride;
   a.vocab = vocab;
   a.chunk = ((vocab + kSplitChunks - 1) / kSplitChunks + 7) / 8 * 8;
+  a.groups = (a.chunk + kSplitGroup - 1) / kSplitGroup;
   a.temperature = temperature;
   a.greedy = greedy || temperature == 0.0f;
   a.scale = !a.greedy && temperature > 0.0f && temperature != 1.0f;

@@ -213,11 +213,14 @@ def test_lm_head_topk_validates_out():
     assert torch.equal(K().lm_head_topk(x, w, 0, out=good)[0], ref)
     bad = [torch.empty(7, 1000, dtype=torch.bfloat16, device=DEV),              # too few rows
            torch.empty(1000, 8, dtype=torch.bfloat16, device=DEV).t(),          # transposed
-           torch.empty(8, 1001, dtype=torch.bfloat16, device=DEV)[:, 1:],       # base not 4-column aligned
+           torch.empty(8, 1004, dtype=torch.bfloat16, device=DEV)[:, 1:1001],   # stride 4k, base not 4-column aligned
            torch.empty(8, 1000, dtype=torch.float16, device=DEV)]               # dtype
     for o in bad:
         with pytest.raises((ValueError, TypeError)):
             K().lm_head_topk(x, w, 0, out=o)
+    # a row stride that is not a multiple of 4 takes element stores: any base offset is fine
+    odd = torch.empty(8, 1001, dtype=torch.bfloat16, device=DEV)[:, 1:]
+    assert torch.equal(K().lm_head_topk(x, w, 0, out=odd)[0], ref)
 
 
 def test_target_logits_topk_routes_and_matches():

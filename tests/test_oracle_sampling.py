@@ -1,6 +1,8 @@
 """Pins the oracle's supplied-noise sampler and the exact_target acceptance walk.
 
-Pins: exp_fg against float64 exp; the exact per-token probability of the
+Pins: the weight table against float64 2^x and against the device's generated header,
+the weight against float64 exp (accuracy, special values, monotonicity); the exact
+per-token probability of the
 noise rule against the reference's closed form ``logits_to_probs``; the
 reference's distribution tests (50k draws, |dp| < 0.015) and known answers
 (greedy, packed == dense, b200 correction token and its emitted-token law).
@@ -21,15 +23,74 @@ def _noise(n, seed=1234, draw=1):
     return np.array([S.counter_noise(seed, 0, i, draw) for i in range(n)], dtype=np.uint64)
 
 
-def test_exp_fg_accuracy_and_special_values():
-    t = np.linspace(-64.0, 0.0, 2_000_001, dtype=np.float32)
-    e = S.exp_fg(t).astype(np.float64)
-    ref = np.exp(t.astype(np.float64))
-    rel = np.abs(e - ref) / ref
-    assert rel.max() < 3.0e-7
-    assert S.exp_fg(np.float32(0.0)) == np.float32(1.0)
-    assert S.exp_fg(np.float32(-64.5)) == 0.0 and S.exp_fg(np.float32(-np.inf)) == 0.0
-    assert S.exp_fg(np.float32(np.nan)) == 0.0
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "ss-grpo_amd", "csrc",
+                      "fg_exp2_table.h")
+
+
+def _header_table():
+    import re
+
+    text = open(HEADER).read()
+    vals = [int(v, 16) for v in re.findall(r"0x([0-9a-f]{16})ull", text)]
+    kt = float(re.search(r"kWeightKt = ([0-9.e+-]+)f", text).group(1))
+    zmax = float(re.search(r"kWeightZmax = ([0-9.e+-]+)f", text).group(1))
+    return vals, kt, zmax
+
+
+def test_weight_table_pins():
+    t = S._TABLE.astype(np.int64)
+    assert t[0] == 2 ** 31 and t[1024] == 2 ** 30 and np.all(np.diff(t) < 0)
+    exact = 2.0 ** 31 * np.exp2(-np.arange(1025) / 1024.0)  # float64: ~2e-7 absolute error
+    frac = exact - np.floor(exact)
+    assert np.all(np.abs(frac - 0.5) > 1e-5)  # no entry near a rounding tie: float64 decides it
+    assert np.array_equal(t, np.floor(exact + 0.5).astype(np.int64))
+    # 2^(-r/1024) * 2^(-(1024-r)/1024) = 1/2: products of mirrored entries within rounding of 2^61
+    prod = t[1:1024].astype(object) * t[1023:0:-1].astype(object)
+    assert all(abs(p - 2 ** 61) <= (a + b) // 2 + 1 for p, a, b in zip(prod, t[1:1024], t[1023:0:-1]))
+    # the device's generated table packs T[r] | (T[r] - T[r+1]) << 32, and the same constants
+    vals, kt, zmax = _header_table()
+    assert vals == [int(t[r]) | (int(t[r] - t[r + 1]) << 32) for r in range(1024)]
+    assert np.float32(kt) == S.KT_BASE and np.float32(zmax) == S.Z_MAX
+
+
+def test_weight_scale_is_nearest_float32():
+    exact = 2.0 ** 20 / np.log(2.0)
+    kt = float(S.KT_BASE)
+    ulp = float(np.spacing(S.KT_BASE))
+    assert abs(kt - exact) <= ulp / 2
+    assert S.weight_scale(1.0) == S.KT_BASE and S.weight_scale(None) == S.KT_BASE
+    assert S.weight_scale(0.7) == np.float32(S.KT_BASE / np.float32(0.7))
+
+
+@pytest.mark.parametrize("T_", [1.0, 0.7, 1.3])
+def test_weight_accuracy_against_exp(T_):
+    """q / 2^40 against float64 exp((x - m) / T) for 2M logits spread over the range that
+    carries weight: within 2.5e-6 relative (fp32 rounding of m - x and of its product with
+    kt, 2^-20-octave steps and the linear interpolation), and within one unit of q where
+    q is small."""
+    x = np.concatenate([[0.0], -np.linspace(0.0, 27.0 * T_, 2_000_001)[1:]]).astype(np.float32)
+    q = S.quantized_weights(x, T_).astype(np.float64)
+    want = np.exp(x.astype(np.float64) / np.float64(np.float32(T_))) * 2.0 ** 40
+    big = want > 2.0 ** 24
+    assert np.max(np.abs(q[big] - want[big]) / want[big]) < 2.5e-6
+    assert np.max(np.abs(q[~big] - want[~big])) <= 1.0 + 2.5e-6 * 2.0 ** 24
+    assert q[0] == 2.0 ** 40
+
+
+def test_weight_special_values_and_order():
+    x = np.array([1.0, np.nan, -np.inf, 1.0 - 30.0, 0.5, 1.0], np.float32)
+    q = S.quantized_weights(x)
+    assert q[0] == q[5] == 2 ** 40 and q[1] == 0 and q[2] == 0 and q[3] == 0 and 0 < q[4] < 2 ** 40
+    assert S.row_max(x) == np.float32(1.0)  # NaN ignored, as the device's fmaxf
+    assert S.quantized_weights(np.array([np.inf, 0.0, np.inf], np.float32)).tolist() == [0, 0, 0]
+    assert S.quantized_weights(np.full(3, -np.inf, np.float32)).tolist() == [0, 0, 0]
+    # a weight never increases as the logit decreases
+    grid = -np.sort(np.random.default_rng(1).random(200_000).astype(np.float32) * 30.0)  # 0 down to -30
+    grid = np.concatenate([[np.float32(0.0)], grid]).astype(np.float32)
+    qg = S.quantized_weights(grid)
+    assert np.all(np.diff(qg.astype(np.int64)) <= 0)
+    # zeros of either sign weigh the same
+    assert S.quantized_weights(np.array([0.0, -0.0], np.float32)).tolist() == [2 ** 40, 2 ** 40]
 
 
 def test_quantised_max_is_exactly_two_pow_40():
