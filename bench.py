@@ -189,6 +189,7 @@ def planted_walk_gather(cfg, r, work, elem, reps=5):
     # its rows from HBM, as it does in a rollout (the rows were written a round earlier)
     flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     walk_ms, walk_max_ms, gather_ms = [], [], []
+    # the walk reads logits the LM head has just written (cache-resident, as in the decoder)
     for rep in range(reps):
         for with_parts, out in ((True, walk_ms), (False, walk_max_ms)):
             # a spin kernel first, so the host has queued the launches below before they
@@ -203,6 +204,8 @@ def planted_walk_gather(cfg, r, work, elem, reps=5):
                             parts=parts[t] if with_parts else None, **kw)
                 e1.record()
                 out.append((e0, e1))
+    # the gather reads rows the verify forward wrote a round earlier (evicted since)
+    for rep in range(reps):
         flush.fill_(rep & 0xFF)
         torch.cuda._sleep(4_000_000)
         e0, e1 = ev(), ev()

@@ -494,8 +494,9 @@ FG_DEVICE bool split_skip(const SplitArgs& a, int r) {
 }
 
 // Elements per workgroup pass: kSplitLoads groups of 8 per thread, all loads in flight
-// before the weights are computed.
-constexpr int kSplitLoads = 4;
+// before the weights are computed (5 groups: a 152,064-logit row's 9,504-element chunk is
+// one pass, so a chunk costs one memory round trip).
+constexpr int kSplitLoads = 5;
 constexpr int kSplitGroup = kSplitThreads * 8;
 constexpr int kSplitPass = kSplitGroup * kSplitLoads;
 // Per-group q-mass is kept for chunks of up to kSplitMaxGroups groups (vocabularies up to

@@ -210,3 +210,34 @@ def test_forward_tree_reference_call_shape(dtype):
         want, _, _ = OM.tree_verify(ocfg, Wr, np.array([trees[b].tokens]), [trees[b].depths], [trees[b].parents],
                                     ks, vs, [lens[b]])
         assert rel(out["hidden_states"][b, :n].float().cpu().numpy(), want[0]) < TOL[dtype]
+
+
+def test_residual_add_rounding_against_the_reference_order():
+    """The O and down projections add into the residual stream in one GEMM (``addmm_``,
+    beta 1): the fp32 accumulator plus the bf16 residual is rounded to bf16 once. The
+    reference's HF layer rounds the projection output to bf16 and then the sum again
+    (``residual + attn_output`` on bf16 tensors). Measured at the 7B O-projection shape
+    (1856 rows, 3584 x 3584) against the float64 sum: the one-rounding result is at least as
+    close to it on average, and the two differ by at most the three half-units of rounding
+    that separate them (of the projection, the sum and the rounded sum)."""
+    g = torch.Generator(device=DEV).manual_seed(11)
+    M, K, N = 1856, 3584, 3584
+    x = (torch.randn(M, N, device=DEV, generator=g) * 0.5).to(torch.bfloat16)
+    a = (torch.randn(M, K, device=DEV, generator=g) * 0.5).to(torch.bfloat16)
+    w = (torch.randn(N, K, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
+    dev = x.clone()
+    dev.addmm_(a, w.t())
+    d64 = a.double() @ w.double().t()
+    truth = x.double() + d64
+    two_step = (x.float() + d64.to(torch.bfloat16).float()).to(torch.bfloat16)  # the reference's order
+    err_dev = (dev.double() - truth).abs()
+    err_ref = (two_step.double() - truth).abs()
+    diff = (dev.double() - two_step.double()).abs()
+    ulp = dev.double().abs().clamp_min(1e-30) * 2.0 ** -7  # at most one bf16 unit of the result
+    frac = float((diff > 0).double().mean())
+    print(f"residual rounding: mean |err| one rounding {float(err_dev.mean()):.3e}, reference order "
+          f"{float(err_ref.mean()):.3e}; {100 * frac:.2f} % of elements differ, "
+          f"{100 * float((diff > ulp).double().mean()):.4f} % by more than one unit of the result")
+    assert float(err_dev.mean()) <= 1.01 * float(err_ref.mean())
+    big = torch.maximum(torch.maximum(x.double().abs(), d64.abs()), truth.abs())
+    assert bool((diff <= 3.0 * 2.0 ** -8 * big + 1e-30).all())
