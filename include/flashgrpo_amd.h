@@ -22,6 +22,8 @@
  *   fg_rope_kv_write    models/qwen_flashgrpo_wrapper.py:172-180 (HF rotary + DynamicCache.update)
  *   fg_tree_attention   decoding/tree_attention.py:6-67 + the HF attention it feeds
  *   fg_rmsnorm, fg_swiglu  models/qwen_flashgrpo_wrapper.py:172-180 (HF decoder layer)
+ *   fg_gate_up_swiglu   models/qwen_flashgrpo_wrapper.py:172-180 (the HF decoder layer's MLP
+ *                       act_fn(gate_proj(x)) * up_proj(x), the two projections and the product in one GEMM)
  *   fg_sample_tokens    decoding/acceptance.py:34-130 (sample_from_logits)
  *   fg_accept_walk      decoding/acceptance.py:179-260 (exact_accept_paths_batch);
  *   fg_walk_begin/rows/step  the same walk, one step per call (lazy LM-head rows);
@@ -155,6 +157,13 @@ int fg_rmsnorm(void* x, const void* delta, const void* weight, void* y, int dtyp
                void* stream);
 /* out[t, i] = SiLU(gate_up[t, i]) * gate_up[t, inter + i] */
 int fg_swiglu(const void* gate_up, void* out, int dtype, int rows, int inter, void* stream);
+/* out[t, i] = SiLU(bf16(x[t] . w[i])) * bf16(x[t] . w[inter + i]), i < inter: the gate/up
+ * projection (w = [gate; up], [2*inter, hidden] bf16, rows `ldw` apart) with SwiGLU in its
+ * epilogue; bf16 x [rows, hidden] (row stride ldx) and out [rows, inter] (row stride ldo).
+ * hidden % 64 == 0, inter % 4 == 0; x and w rows 16-byte aligned, out rows 8-byte aligned.
+ * tile_rows: 0 (chosen from the shape), 192 or 256 rows per workgroup tile. */
+int fg_gate_up_swiglu(const void* x, int64_t ldx, const void* w_gate_up, int64_t ldw, void* out, int64_t ldo, int rows,
+                      int inter, int hidden, int tile_rows, void* stream);
 
 /* Workspace (bytes) that lets fg_sample_tokens / fg_walk_step split each row of an
  * unrestricted (no top-k, no top-p) or greedy draw over several workgroups. */

@@ -360,6 +360,39 @@ def swiglu(gate_up, *, out=None):
     return out
 
 
+def gate_up_swiglu_ok(x, w) -> bool:
+    """Whether fg_gate_up_swiglu takes x [rows, hidden] and w [2*inter, hidden] as they are:
+    bf16 on the GPU, hidden a multiple of 64, inter a multiple of 4, unit column strides and
+    16-byte aligned rows."""
+    if not (x.is_cuda and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and x.dim() == 2 and w.dim() == 2):
+        return False
+    H = x.shape[1]
+    if H == 0 or H % 64 or w.shape[1] != H or w.shape[0] % 8 or x.shape[0] == 0:
+        return False
+    if x.stride(1) != 1 or w.stride(1) != 1 or x.stride(0) % 8 or w.stride(0) % 8:
+        return False
+    return x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0
+
+
+def gate_up_swiglu(x, w, *, out=None, tile_rows=0):
+    """SiLU(x . w[:I]^T) * (x . w[I:]^T) with both projections rounded to bf16 first, as one GEMM
+    (``fg_gate_up_swiglu``): x [rows, H] bf16, w [2I, H] bf16 (gate rows, then up rows) ->
+    [rows, I] bf16."""
+    _dev(x, w)
+    if not gate_up_swiglu_ok(x, w):
+        raise ValueError("gate_up_swiglu: needs bf16 x [rows, H] and w [2I, H] with H % 64 == 0, I % 4 == 0, "
+                         "unit column strides and 16-byte aligned rows")
+    rows, H = x.shape
+    inter = w.shape[0] // 2
+    if out is None:
+        out = torch.empty(rows, inter, dtype=torch.bfloat16, device=x.device)
+    elif out.dtype != torch.bfloat16 or tuple(out.shape) != (rows, inter) or out.stride(1) != 1:
+        raise ValueError(f"gate_up_swiglu: out must be bf16 [{rows}, {inter}] with unit column stride")
+    _call("fg_gate_up_swiglu", _ptr(x), x.stride(0), _ptr(w), w.stride(0), _ptr(out), out.stride(0), rows, inter, H,
+          int(tile_rows), _stream())
+    return out
+
+
 # ------------------------------------------------------------------ sampling / acceptance
 def sample_workspace(rows, device):
     """Scratch that lets unrestricted / greedy draws run split over several workgroups per row."""

@@ -396,6 +396,23 @@ class _ForwardGraph:
         return self.out
 
 
+_CUS = {}
+
+
+def mlp_fused_wins(rows: int, inter: int, device) -> bool:
+    """Whether the fused gate/up + SwiGLU GEMM is the faster MLP input for this shape: when its
+    tiles (192 or 256 rows x 128 columns) fit one pass over the compute units. There the pass it
+    saves decides (Qwen2.5-1.5B verify rounds, 512 rows, 210 tiles: 39-43 us against 43-60 us for
+    the hipBLASLt projection + fg_swiglu); on larger launches hipBLASLt's projection runs 15-20 %
+    faster than the fused kernel's and the pair wins (Qwen2.5-7B, 1856 rows: ~390 + 34 us against
+    ~455-470 us)."""
+    key = str(device)
+    if key not in _CUS:
+        _CUS[key] = torch.cuda.get_device_properties(torch.device(device)).multi_processor_count
+    cols = -(-inter // 128)
+    return min(-(-rows // bm) * cols for bm in (192, 256)) <= _CUS[key]
+
+
 class TargetModel:
     """Decoder weights on the device plus the verify / prefill forward."""
 
@@ -412,6 +429,10 @@ class TargetModel:
         self._retired = []      # buffers replaced while graphs that address them exist
         self._hf_source = None  # the Hugging Face model the weights were read from (from_hf)
         self._hf_key = None
+        # the MLP's gate/up projection and SwiGLU as one GEMM (fg_gate_up_swiglu): None chooses per
+        # shape (mlp_fused_wins), True wherever the operands allow, False never (the hipBLASLt
+        # projection, then fg_swiglu); call drop_graphs() after a change
+        self.fused_mlp = None
         if self.device.type == "cuda":
             use_tuned_gemms()
 
@@ -626,8 +647,12 @@ class TargetModel:
             # the norms then read one tensor instead of two and write one instead of two
             x.addmm_(attn.view(T, cfg.q_heads * d), lw["o_w"].t())
             h2 = K.rmsnorm(x, lw["post_norm"], cfg.rms_eps, out=self._buf("h", (T, H)))
-            gu = F.linear(h2, lw["gate_up_w"])
-            act = K.swiglu(gu, out=self._buf("act", (T, cfg.intermediate)))
+            act = self._buf("act", (T, cfg.intermediate))
+            fused = mlp_fused_wins(T, cfg.intermediate, h2.device) if self.fused_mlp is None else self.fused_mlp
+            if fused and K.gate_up_swiglu_ok(h2, lw["gate_up_w"]):
+                K.gate_up_swiglu(h2, lw["gate_up_w"], out=act)
+            else:
+                K.swiglu(F.linear(h2, lw["gate_up_w"]), out=act)
             x.addmm_(act, lw["down_w"].t())
 
     def _forward_end(self, st: dict) -> torch.Tensor:

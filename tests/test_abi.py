@@ -47,6 +47,14 @@ def test_library_loads_and_reports_errors_without_gpu_work():
                               ctypes.c_void_p(64), None, 0, None)
     assert rc != 0 and b"vocab" in lib.fg_last_error()
     assert lib.fg_sample_workspace(64) >= 64 * 16 * 20 and lib.fg_sample_workspace(0) == 0
+    # the fused MLP GEMM: K (hidden) must be a multiple of 64, tile heights 192 / 256 only
+    p = ctypes.c_void_p(256)
+    rc = lib.fg_gate_up_swiglu(p, 96, p, 96, p, 8, 4, 8, 96, 0, None)
+    assert rc != 0 and b"multiple of 64" in lib.fg_last_error()
+    rc = lib.fg_gate_up_swiglu(p, 64, p, 64, p, 8, 4, 8, 64, 128, None)
+    assert rc != 0 and b"tile_rows" in lib.fg_last_error()
+    rc = lib.fg_gate_up_swiglu(None, 64, p, 64, p, 8, 4, 8, 64, 0, None)
+    assert rc != 0 and b"null pointer" in lib.fg_last_error()
 
 
 def test_tree_attention_split_policy():

@@ -241,3 +241,40 @@ def test_residual_add_rounding_against_the_reference_order():
     assert float(err_dev.mean()) <= 1.01 * float(err_ref.mean())
     big = torch.maximum(torch.maximum(x.double().abs(), d64.abs()), truth.abs())
     assert bool((diff <= 3.0 * 2.0 ** -8 * big + 1e-30).all())
+
+
+def test_fused_mlp_forward_matches_unfused():
+    """The verify forward with the MLP's gate/up projection and SwiGLU in one GEMM
+    (fg_gate_up_swiglu) against the hipBLASLt projection + fg_swiglu: the KV the forward writes
+    and its hidden states agree to bf16 rounding; the per-shape choice takes the fused GEMM for
+    small launches and the pair for the 7B verify rounds."""
+    from flashgrpo_amd import kernels as KK
+    from flashgrpo_amd.decoding.medusa_tree import TreeTopology
+
+    from flashgrpo_amd.models.target import mlp_fused_wins
+
+    ocfg = _cfgs(torch.bfloat16)
+    m = _model(ocfg, OM.random_weights(ocfg, seed=6, std=0.05), torch.bfloat16)
+    assert m.fused_mlp is None and mlp_fused_wins(3 * 13, ocfg.intermediate, DEV)  # small launch: fused
+    assert not mlp_fused_wins(1856, 18944, DEV)  # Qwen2.5-7B verify rounds: hipBLASLt + fg_swiglu
+    assert mlp_fused_wins(512, 8960, DEV)  # Qwen2.5-1.5B verify rounds
+    lw = m.w["layers"][0]
+    h = torch.zeros(3, ocfg.hidden, dtype=torch.bfloat16, device=DEV)
+    assert KK.gate_up_swiglu_ok(h, lw["gate_up_w"])
+    rng = np.random.default_rng(6)
+    B, P = 3, 70
+    prompts = torch.from_numpy(rng.integers(0, ocfg.vocab, (B, P))).to(DEV)
+    topo = TreeTopology([3, 2, 1], 12)
+    d = topo.device(DEV)
+    toks = torch.from_numpy(rng.integers(0, ocfg.vocab, (B, topo.num_nodes))).to(DEV).to(torch.int32)
+    outs = {}
+    for fused in (True, False):
+        m.fused_mlp = fused
+        m.drop_graphs()
+        cache = m.new_cache(B, 128)
+        m.prefill(prompts, cache)
+        outs[fused] = (m.forward(toks, cache, pos_offset=d["pos_offset"], anc=d["anc"]).float().cpu().numpy(),
+                       cache.kv.float().cpu().numpy())
+    m.fused_mlp = None
+    assert rel(outs[True][0], outs[False][0]) < 1e-2
+    assert rel(outs[True][1], outs[False][1]) < 1e-2
