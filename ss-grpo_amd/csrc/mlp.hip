@@ -21,7 +21,8 @@
 // v_mfma_f32_32x32x16_bf16 (the wave's (BM/2) x 128 block is (BM/64) x 4 MFMA tiles, computed
 // transposed so each lane ends with 4 consecutive output columns of one row); the fragment reads
 // of sub-step s+1 are interleaved with the MFMAs of sub-step s, and the loads of k-step t+2 are
-// issued between the MFMAs of k-step t's last sub-step, after the one barrier of the step.
+// issued between the MFMAs of k-step t's last sub-step, after the one barrier of the step. The
+// output block of each wave goes out through LDS as whole 128-byte row segments.
 // Workgroups are numbered so that each XCD takes a contiguous run of tiles along M for one weight
 // stripe: the stripe is read from HBM once per XCD and reused from its L2.
 #include "fg_common.h"
@@ -57,6 +58,7 @@ struct MlpArgs {
   uint16_t* out;
   int64_t ldo;
   int rows, inter, hidden;
+  int vec16;  // out rows 16-byte aligned: whole 8-column chunks as one store
   int tiles_m, tiles, per_xcd;
 };
 
@@ -207,25 +209,41 @@ __global__ void __launch_bounds__(256, 1) gate_up_swiglu_kernel(MlpArgs p) {
   for (; t < nk; ++t) step(t, std::false_type{});
   wait_vmcnt<0>();  // no load still writing LDS when the workgroup ends
 
-  // Epilogue: acc[i] (gate) and acc[i + 2] (up) hold the same 4 output columns of one row per lane.
+  // Epilogue: acc[i] (gate) and acc[i + 2] (up) hold the same 4 output columns of one row per lane
+  // (32 rows per store instruction). After the last barrier no wave reads the ring and no load is in
+  // flight, so each wave stages its own (BM/2) x 64 bf16 block in LDS (rows of 128 bytes, 16-byte
+  // chunk q of row r stored at chunk q ^ (r % 8)) and writes it back as whole 128-byte row segments.
+  unsigned char* stage = smem + wave * (WM * 128);
 #pragma unroll
-  for (int k = 0; k < FM; ++k) {
-    const int m = m0 + wm * WM + k * 32 + l32;
-    if (m >= p.rows) continue;
+  for (int k = 0; k < FM; ++k)
 #pragma unroll
     for (int i = 0; i < FN / 2; ++i)
 #pragma unroll
       for (int v4 = 0; v4 < 4; ++v4) {
-        const int c = c0 + wn * 64 + i * 32 + v4 * 8 + half * 4;
-        if (c >= p.inter) continue;
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float gt = round_bf16(acc[i][k][4 * v4 + e]), up = round_bf16(acc[i + FN / 2][k][4 * v4 + e]);
           o[e] = gt / (1.0f + __expf(-gt)) * up;  // the expression of fg_swiglu
         }
-        *(uint2*)(p.out + (int64_t)m * p.ldo + c) = make_uint2(fg::pack_bf16x2(o[0], o[1]), fg::pack_bf16x2(o[2], o[3]));
+        const int r = k * 32 + l32, q = i * 4 + v4;
+        *(uint2*)(stage + r * 128 + ((q ^ (r & 7)) * 16) + half * 8) =
+            make_uint2(fg::pack_bf16x2(o[0], o[1]), fg::pack_bf16x2(o[2], o[3]));
       }
+  const int cw = c0 + wn * 64;
+#pragma unroll
+  for (int it = 0; it < WM / 8; ++it) {
+    const int r = it * 8 + (lane >> 3), q = lane & 7;
+    const uint4 v = *(const uint4*)(stage + r * 128 + ((q ^ (r & 7)) * 16));
+    const int m = m0 + wm * WM + r, c = cw + q * 8;
+    if (m >= p.rows || c >= p.inter) continue;
+    uint16_t* dst = p.out + (int64_t)m * p.ldo + c;
+    if (p.vec16 && c + 8 <= p.inter) {
+      *(uint4*)dst = v;
+    } else {
+      *(uint2*)dst = make_uint2(v.x, v.y);
+      if (c + 4 < p.inter) *(uint2*)(dst + 4) = make_uint2(v.z, v.w);
+    }
   }
 }
 
@@ -272,6 +290,7 @@ int fg_gate_up_swiglu(const void* x, int64_t ldx, const void* w_gate_up, int64_t
   p.rows = rows;
   p.inter = inter;
   p.hidden = hidden;
+  p.vec16 = ldo % 8 == 0 && ((uintptr_t)out & 15) == 0;
   hipStream_t s = (hipStream_t)stream;
   if ((tile_rows ? tile_rows : pick_tile_rows(rows, inter)) == 192)
     launch<192>(p, s);

@@ -26,7 +26,7 @@ import torch.nn.functional as F
 
 from .. import kernels as K
 from .. import timing
-from ..tuning import use_tuned_gemms
+from ..tuning import mlp_table_path, use_tuned_gemms
 
 MAX_TREE_NODES = 64      # tree nodes per forward (64-bit ancestor masks)
 MAX_CHAIN_TOKENS = 8192  # new tokens per forward without masks (a causal chain)
@@ -399,18 +399,25 @@ class _ForwardGraph:
 _CUS = {}
 
 
-def mlp_fused_wins(rows: int, inter: int, device) -> bool:
-    """Whether the fused gate/up + SwiGLU GEMM is the faster MLP input for this shape: when its
-    tiles (192 or 256 rows x 128 columns) fit one pass over the compute units. There the pass it
-    saves decides (Qwen2.5-1.5B verify rounds, 512 rows, 210 tiles: 39-43 us against 43-60 us for
-    the hipBLASLt projection + fg_swiglu); on larger launches hipBLASLt's projection runs 15-20 %
-    faster than the fused kernel's and the pair wins (Qwen2.5-7B, 1856 rows: ~390 + 34 us against
-    ~455-470 us)."""
+def mlp_path(rows: int, inter: int, hidden: int, device) -> int:
+    """How a decoder layer computes its MLP input for ``rows`` rows: 0 for the hipBLASLt
+    projection + fg_swiglu, else the tile height (192 or 256) of the fused gate/up + SwiGLU GEMM.
+
+    The measured table (``tuning/mlp_mi355x.csv``) decides for the sizes it covers: which path
+    is faster depends on the library's solution for the shape (Qwen2.5-7B verify rounds, 1856
+    rows: 443 against 457 us, the pair; Qwen2.5-14B, 3712 rows: 957 against 905 us, the fused
+    GEMM). Other sizes take the fused GEMM when its tiles make one pass over the compute units,
+    where the pass it saves decides (Qwen2.5-1.5B, 512 rows: 58 against 39 us).
+    """
+    measured = mlp_table_path(rows, inter, hidden)
+    if measured is not None:
+        return measured
     key = str(device)
     if key not in _CUS:
         _CUS[key] = torch.cuda.get_device_properties(torch.device(device)).multi_processor_count
     cols = -(-inter // 128)
-    return min(-(-rows // bm) * cols for bm in (192, 256)) <= _CUS[key]
+    fits = min(-(-rows // bm) * cols for bm in (192, 256)) <= _CUS[key]
+    return -1 if fits else 0  # -1: fused, the kernel picks the tile height
 
 
 class TargetModel:
@@ -430,7 +437,7 @@ class TargetModel:
         self._hf_source = None  # the Hugging Face model the weights were read from (from_hf)
         self._hf_key = None
         # the MLP's gate/up projection and SwiGLU as one GEMM (fg_gate_up_swiglu): None chooses per
-        # shape (mlp_fused_wins), True wherever the operands allow, False never (the hipBLASLt
+        # shape (mlp_path), True wherever the operands allow, False never (the hipBLASLt
         # projection, then fg_swiglu); call drop_graphs() after a change
         self.fused_mlp = None
         if self.device.type == "cuda":
@@ -648,9 +655,12 @@ class TargetModel:
             x.addmm_(attn.view(T, cfg.q_heads * d), lw["o_w"].t())
             h2 = K.rmsnorm(x, lw["post_norm"], cfg.rms_eps, out=self._buf("h", (T, H)))
             act = self._buf("act", (T, cfg.intermediate))
-            fused = mlp_fused_wins(T, cfg.intermediate, h2.device) if self.fused_mlp is None else self.fused_mlp
-            if fused and K.gate_up_swiglu_ok(h2, lw["gate_up_w"]):
-                K.gate_up_swiglu(h2, lw["gate_up_w"], out=act)
+            if self.fused_mlp is None:
+                path = mlp_path(T, cfg.intermediate, H, h2.device)
+            else:
+                path = -1 if self.fused_mlp else 0
+            if path and K.gate_up_swiglu_ok(h2, lw["gate_up_w"]):
+                K.gate_up_swiglu(h2, lw["gate_up_w"], out=act, tile_rows=max(path, 0))
             else:
                 K.swiglu(F.linear(h2, lw["gate_up_w"]), out=act)
             x.addmm_(act, lw["down_w"].t())

@@ -10,13 +10,53 @@ different PyTorch / ROCm / hipBLASLt build is ignored by TunableOp's validators.
 
 Set ``FLASHGRPO_AMD_GEMM_TABLE=off`` to leave TunableOp untouched, or to a path to
 use another table.
+
+``mlp_mi355x.csv`` (``make_mlp_table.py``) holds, per (rows, intermediate, hidden), the
+measured times of the two ways to compute a decoder layer's MLP input -- the tuned
+projection followed by ``fg_swiglu``, or the fused ``fg_gate_up_swiglu`` at either tile
+height -- and the faster one; ``mlp_table_path`` looks it up
+(``FLASHGRPO_AMD_MLP_TABLE=off`` or another path).
 """
 from __future__ import annotations
 
 import os
 
 DEFAULT_TABLE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "gemm_mi355x.csv")
+DEFAULT_MLP_TABLE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "mlp_mi355x.csv")
 _state = {"done": False, "active": False}
+_mlp = {}
+_CHOICE = {"pair": 0, "fused192": 192, "fused256": 256}
+
+
+def _mlp_entries() -> dict:
+    """(inter, hidden) -> sorted [(rows, path)] from the MLP path table (read once)."""
+    if "entries" not in _mlp:
+        entries = {}
+        choice = os.environ.get("FLASHGRPO_AMD_MLP_TABLE", "")
+        path = DEFAULT_MLP_TABLE if not choice else (None if choice.lower() == "off" else choice)
+        if path and os.path.exists(path):
+            with open(path) as f:
+                header = f.readline().strip().split(",")
+                for line in f:
+                    row = dict(zip(header, line.strip().split(",")))
+                    if row.get("choice") in _CHOICE:
+                        key = (int(row["inter"]), int(row["hidden"]))
+                        entries.setdefault(key, []).append((int(row["rows"]), _CHOICE[row["choice"]]))
+        _mlp["entries"] = {k: sorted(v) for k, v in entries.items()}
+    return _mlp["entries"]
+
+
+def mlp_table_path(rows: int, inter: int, hidden: int):
+    """The measured MLP input path for this shape: 0 (projection + fg_swiglu) or the fused GEMM's
+    tile height (192 / 256), taken from the table entry of these sizes nearest in row count on a log
+    scale (ties to the larger count); None when the table has no entry for (inter, hidden)."""
+    cands = _mlp_entries().get((int(inter), int(hidden)))
+    if not cands:
+        return None
+    import math
+
+    lr = math.log(max(int(rows), 1))
+    return min(cands, key=lambda e: (abs(math.log(e[0]) - lr), -e[0]))[1]
 
 
 def use_tuned_gemms(path: str | None = None) -> bool:

@@ -1,0 +1,97 @@
+"""Regenerate the MLP input-path table (run on the MI355X it is meant for).
+
+    python -m flashgrpo_amd.tuning.make_mlp_table --out mlp_mi355x.csv [--reps 20]
+
+For the (intermediate, hidden) sizes of every target preset and a grid of row counts
+(powers of two plus the verify-round and prefill shapes of the benchmark workloads), it
+times the two ways the decoder layer can compute its MLP input SiLU(x.Wg^T) * (x.Wu^T):
+the hipBLASLt projection (through the GEMM solution table) followed by ``fg_swiglu``, and
+``fg_gate_up_swiglu`` at both tile heights. Each time is the minimum over ``reps``
+launches with the weight alternating between two copies (so it is read from HBM). One
+row per shape names the fastest path.
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import sys
+
+GRID = (64, 128, 256, 512, 1024, 2048, 4096, 8192)
+# preset -> extra row counts: verify rounds (sequences x tree nodes) and prefill chunks
+# (prompts x chunk) of the benchmark workloads
+SHAPES = {
+    "tiny": (8 * 16, 4 * 256),
+    "qwen25_1p5b": (32 * 13, 32 * 16, 4 * 512),
+    "qwen25_7b": (64 * 13, 64 * 29, 64 * 32),
+    "qwen25_14b": (128 * 41, 16 * 1024),
+    "llama31_8b": (96 * 48, 12 * 1024),
+}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--out", required=True)
+    ap.add_argument("--reps", type=int, default=20)
+    args = ap.parse_args()
+    import torch
+    import torch.nn.functional as F
+
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))))
+    from flashgrpo_amd import kernels as K
+    from flashgrpo_amd.models.target import TargetConfig
+    from flashgrpo_amd.tuning import use_tuned_gemms
+
+    use_tuned_gemms()
+
+    def best(fn):
+        for _ in range(3):
+            fn()
+        ts = []
+        for _ in range(args.reps):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            fn()
+            e.record()
+            e.synchronize()
+            ts.append(s.elapsed_time(e) * 1e3)
+        return min(ts)
+
+    lines = ["rows,inter,hidden,pair_us,fused192_us,fused256_us,choice"]
+    done = set()
+    for preset, extra in SHAPES.items():
+        cfg = getattr(TargetConfig, preset)()
+        I, H = cfg.intermediate, cfg.hidden
+        if (I, H) in done:
+            continue
+        done.add((I, H))
+        g = torch.Generator(device="cuda").manual_seed(I)
+        ws = [(torch.randn(2 * I, H, device="cuda", generator=g) * 0.05).to(torch.bfloat16) for _ in range(2)]
+        for rows in sorted(set(GRID) | set(extra)):
+            x = (torch.randn(rows, H, device="cuda", generator=g) * 0.5).to(torch.bfloat16)
+            out = torch.empty(rows, I, dtype=torch.bfloat16, device="cuda")
+            it = [0]
+
+            def pair():
+                it[0] += 1
+                K.swiglu(F.linear(x, ws[it[0] % 2]), out=out)
+
+            def fused(tile):
+                def run():
+                    it[0] += 1
+                    K.gate_up_swiglu(x, ws[it[0] % 2], out=out, tile_rows=tile)
+                return run
+
+            t = {"pair": best(pair), "fused192": best(fused(192)), "fused256": best(fused(256))}
+            choice = min(t, key=t.get)
+            lines.append(f"{rows},{I},{H},{t['pair']:.1f},{t['fused192']:.1f},{t['fused256']:.1f},{choice}")
+            print(f"{cfg.name} rows {rows}: " + ", ".join(f"{k} {v:.1f}" for k, v in t.items()) + f" -> {choice}",
+                  flush=True)
+            del x, out
+        del ws
+        torch.cuda.empty_cache()
+    with open(args.out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+
+
+if __name__ == "__main__":
+    main()
