@@ -24,6 +24,8 @@
  *   fg_rmsnorm, fg_swiglu  models/qwen_flashgrpo_wrapper.py:172-180 (HF decoder layer)
  *   fg_gate_up_swiglu   models/qwen_flashgrpo_wrapper.py:172-180 (the HF decoder layer's MLP
  *                       act_fn(gate_proj(x)) * up_proj(x), the two projections and the product in one GEMM)
+ *   fg_chain_cell_norm  models/medusa_heads.py:12-42 (ChainDraftCell state_norm / token_norm,
+ *                       the two LayerNorms whose outputs its projections take side by side)
  *   fg_sample_tokens    decoding/acceptance.py:34-130 (sample_from_logits)
  *   fg_accept_walk      decoding/acceptance.py:179-260 (exact_accept_paths_batch);
  *   fg_walk_begin/rows/step  the same walk, one step per call (lazy LM-head rows);
@@ -164,6 +166,13 @@ int fg_swiglu(const void* gate_up, void* out, int dtype, int rows, int inter, vo
  * tile_rows: 0 (chosen from the shape), 192 or 256 rows per workgroup tile. */
 int fg_gate_up_swiglu(const void* x, int64_t ldx, const void* w_gate_up, int64_t ldw, void* out, int64_t ldo, int rows,
                       int inter, int hidden, int tile_rows, void* stream);
+
+/* out[r] = [LayerNorm(state[r]) * state_w + state_b, LayerNorm(token[r]) * token_w + token_b]
+ * ([rows, 2*hidden], row stride 2*hidden): the ChainDraftCell's normalised inputs side by side.
+ * Weights and biases in the row dtype; hidden % 8 == 0, hidden <= 8192, 16-byte aligned rows. */
+int fg_chain_cell_norm(const void* state, int64_t ld_state, const void* token, int64_t ld_token, int dtype,
+                       int rows, int hidden, const void* state_w, const void* state_b, const void* token_w,
+                       const void* token_b, float eps, void* out, void* stream);
 
 /* Workspace (bytes) that lets fg_sample_tokens / fg_walk_step split each row of an
  * unrestricted (no top-k, no top-p) or greedy draw over several workgroups. */

@@ -2,7 +2,8 @@
 // embedding fused with the tree K/V slot write, RMSNorm (optionally fused with
 // the residual add) and the SwiGLU gate. These mirror the Qwen2/Llama decoder
 // layer that the reference runs through transformers
-// (flashgrpo/models/qwen_flashgrpo_wrapper.py:172-180).
+// (flashgrpo/models/qwen_flashgrpo_wrapper.py:172-180). Also the chain proposals'
+// ChainDraftCell input normalisation (flashgrpo/models/medusa_heads.py:12-42).
 #include "fg_common.h"
 
 namespace {
@@ -159,6 +160,67 @@ __global__ void __launch_bounds__(256) swiglu_kernel(const void* __restrict__ gu
   fg::store8<DT>(out, t * F + ch * 8, o);
 }
 
+// The ChainDraftCell's two normalised inputs side by side: workgroup (r, 0) writes
+// out[r, 0:H] = LayerNorm(state[r]) * sw + sb and (r, 1) out[r, H:2H] = LayerNorm(token[r]) * tw + tb
+// (mean, then the mean squared deviation, over the row held in registers; fp32 math, affine
+// weights in the row dtype). H % 8 == 0, H <= 8192.
+template <int DT>
+__global__ void __launch_bounds__(256) chain_cell_norm_kernel(const void* __restrict__ state, int64_t lds_,
+                                                              const void* __restrict__ token, int64_t ldt,
+                                                              const void* __restrict__ sw, const void* __restrict__ sb,
+                                                              const void* __restrict__ tw, const void* __restrict__ tb,
+                                                              int H, float eps, void* __restrict__ out) {
+  const int r = blockIdx.x, which = blockIdx.y, tid = threadIdx.x;
+  const void* src = which ? token : state;
+  const int64_t base = (int64_t)r * (which ? ldt : lds_);
+  const void* w = which ? tw : sw;
+  const void* bb = which ? tb : sb;
+  const int nch = H / 8;
+  __shared__ float red[8];
+  float v[kNormChunks][8];
+  float s = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kNormChunks; ++c) {
+    const int ch = tid + c * 256;
+    if (ch < nch) {
+      fg::load8<DT>(src, base + ch * 8, v[c]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += v[c][j];
+    }
+  }
+  s = fg::wave_sum(s);
+  if ((tid & 63) == 0) red[tid >> 6] = s;
+  __syncthreads();
+  const float mean = (red[0] + red[1] + red[2] + red[3]) / (float)H;
+  float q = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kNormChunks; ++c)
+    if (tid + c * 256 < nch) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float d = v[c][j] - mean;
+        q += d * d;
+      }
+    }
+  q = fg::wave_sum(q);
+  if ((tid & 63) == 0) red[4 + (tid >> 6)] = q;
+  __syncthreads();
+  const float rstd = rsqrtf((red[4] + red[5] + red[6] + red[7]) / (float)H + eps);
+  const int64_t obase = (int64_t)r * 2 * H + (int64_t)which * H;
+#pragma unroll
+  for (int c = 0; c < kNormChunks; ++c) {
+    const int ch = tid + c * 256;
+    if (ch < nch) {
+      float wv[8], bv[8], y[8];
+      fg::load8<DT>(w, ch * 8, wv);
+      fg::load8<DT>(bb, ch * 8, bv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = (v[c][j] - mean) * rstd * wv[j] + bv[j];
+      fg::store8<DT>(out, obase + ch * 8, y);
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -202,6 +264,29 @@ int fg_rmsnorm(void* x, const void* delta, const void* weight, void* y, int dtyp
   else
     hipLaunchKernelGGL(rmsnorm_kernel<fg::kF32>, dim3(rows), dim3(256), 0, s, x, delta, weight, y, hidden, eps);
   return fg::check_launch("fg_rmsnorm");
+}
+
+int fg_chain_cell_norm(const void* state, int64_t ld_state, const void* token, int64_t ld_token, int dtype,
+                       int rows, int hidden, const void* state_w, const void* state_b, const void* token_w,
+                       const void* token_b, float eps, void* out, void* stream) {
+  FG_REQUIRE(state && token && state_w && state_b && token_w && token_b && out, "fg_chain_cell_norm: null pointer");
+  FG_REQUIRE(dtype == fg::kBF16 || dtype == fg::kF32, "fg_chain_cell_norm: dtype");
+  FG_REQUIRE(rows > 0 && rows <= 65535 && hidden > 0, "fg_chain_cell_norm: bad shape");
+  FG_REQUIRE(hidden % 8 == 0 && hidden <= 8 * 256 * kNormChunks, "fg_chain_cell_norm: hidden must be a multiple of 8, at most 8192");
+  FG_REQUIRE(ld_state >= hidden && ld_token >= hidden && ld_state % 8 == 0 && ld_token % 8 == 0,
+             "fg_chain_cell_norm: row strides must be multiples of 8, at least hidden");
+  const uintptr_t al = (uintptr_t)state | (uintptr_t)token | (uintptr_t)state_w | (uintptr_t)state_b |
+                       (uintptr_t)token_w | (uintptr_t)token_b | (uintptr_t)out;
+  FG_REQUIRE((al & 15) == 0, "fg_chain_cell_norm: 16-byte alignment");
+  const dim3 grid((unsigned)rows, 2);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == fg::kBF16)
+    hipLaunchKernelGGL(chain_cell_norm_kernel<fg::kBF16>, grid, dim3(256), 0, s, state, ld_state, token, ld_token,
+                       state_w, state_b, token_w, token_b, hidden, eps, out);
+  else
+    hipLaunchKernelGGL(chain_cell_norm_kernel<fg::kF32>, grid, dim3(256), 0, s, state, ld_state, token, ld_token,
+                       state_w, state_b, token_w, token_b, hidden, eps, out);
+  return fg::check_launch("fg_chain_cell_norm");
 }
 
 int fg_swiglu(const void* gate_up, void* out, int dtype, int rows, int inter, void* stream) {

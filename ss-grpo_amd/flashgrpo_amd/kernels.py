@@ -360,6 +360,26 @@ def swiglu(gate_up, *, out=None):
     return out
 
 
+def chain_cell_norm(state, token, state_w, state_b, token_w, token_b, eps, *, out=None):
+    """[rows, 2H] = [LayerNorm(state) * state_w + state_b, LayerNorm(token) * token_w + token_b]
+    (``fg_chain_cell_norm``): the ChainDraftCell's two normalised inputs side by side. state and
+    token [rows, H] in one dtype (unit column stride), the affine weights [H] in that dtype."""
+    _dev(state, token, state_w, state_b, token_w, token_b)
+    rows, H = state.shape
+    if tuple(token.shape) != (rows, H) or token.dtype != state.dtype or state.stride(1) != 1 or token.stride(1) != 1:
+        raise ValueError("chain_cell_norm: state and token must be [rows, H] of one dtype with unit column stride")
+    ws = [t.contiguous() for t in (state_w, state_b, token_w, token_b)]
+    if any(t.dtype != state.dtype or t.numel() != H for t in ws):
+        raise ValueError("chain_cell_norm: affine weights must be [H] in the row dtype")
+    if out is None:
+        out = torch.empty(rows, 2 * H, dtype=state.dtype, device=state.device)
+    elif tuple(out.shape) != (rows, 2 * H) or not out.is_contiguous() or out.dtype != state.dtype:
+        raise ValueError("chain_cell_norm: out must be a contiguous [rows, 2H] tensor of the row dtype")
+    _call("fg_chain_cell_norm", _ptr(state), state.stride(0), _ptr(token), token.stride(0), dtype_code(state), rows, H,
+          *[_ptr(t) for t in ws], float(eps), _ptr(out), _stream())
+    return out
+
+
 def gate_up_swiglu_ok(x, w) -> bool:
     """Whether fg_gate_up_swiglu takes x [rows, hidden] and w [2*inter, hidden] as they are:
     bf16 on the GPU, hidden a multiple of 64, inter a multiple of 4, unit column strides and

@@ -63,11 +63,21 @@ class ChainDraftCell(nn.Module):
 
     def step(self, state, token_embedding):
         """The cell in the state's dtype (weights cast once and cached), as the rollout
-        runs the Medusa heads in the target's dtype."""
+        runs the Medusa heads in the target's dtype. On the GPU the two LayerNorms are one
+        HIP launch (``fg_chain_cell_norm``); the projections run on hipBLASLt."""
         w = self._weights(state.dtype, state.device)
         H = state.shape[-1]
-        x = torch.cat([F.layer_norm(state, (H,), w["sn_w"], w["sn_b"], w["eps"]),
-                       F.layer_norm(token_embedding.to(state.dtype), (H,), w["tn_w"], w["tn_b"], w["eps"])], dim=-1)
+        tok = token_embedding.to(state.dtype)
+        if state.is_cuda:
+            # both LayerNorms in one launch, written side by side (fg_chain_cell_norm)
+            from .. import kernels as K
+
+            rows = lambda t: t.reshape(-1, H) if t.is_contiguous() else t.reshape(-1, H).contiguous()
+            x = K.chain_cell_norm(rows(state), rows(tok), w["sn_w"], w["sn_b"], w["tn_w"], w["tn_b"], w["eps"])
+            x = x.view(*state.shape[:-1], 2 * H)
+        else:
+            x = torch.cat([F.layer_norm(state, (H,), w["sn_w"], w["sn_b"], w["eps"]),
+                           F.layer_norm(tok, (H,), w["tn_w"], w["tn_b"], w["eps"])], dim=-1)
         delta = F.linear(F.silu(F.linear(x, w["proj"])), w["out_w"], w["out_b"])
         return torch.addcmul(state, delta, w["gate"])
 

@@ -55,6 +55,8 @@ def test_library_loads_and_reports_errors_without_gpu_work():
     assert rc != 0 and b"tile_rows" in lib.fg_last_error()
     rc = lib.fg_gate_up_swiglu(None, 64, p, 64, p, 8, 4, 8, 64, 0, None)
     assert rc != 0 and b"null pointer" in lib.fg_last_error()
+    rc = lib.fg_chain_cell_norm(p, 12, p, 12, 1, 4, 12, p, p, p, p, 1e-5, p, None)
+    assert rc != 0 and b"multiple of 8" in lib.fg_last_error()
 
 
 def test_tree_attention_split_policy():
