@@ -692,10 +692,10 @@ class TargetModel:
 
         Up to 256 bf16 rows, contiguous or gathered (the lazy walk's rows, skipped as a
         whole when no row is active), run the weight-streaming LM-head kernel
-        (``fg_lm_head_topk``, the weight read once). Larger contiguous blocks (prefill
-        sized) are a square GEMM and go to hipBLASLt; larger gathered sets and fp32 run
-        ``fg_lm_head``. ``parts`` (from ``walk_parts``): the streaming kernel also writes
-        each row's maxima parts.
+        (``fg_lm_head_topk``, the weight read once). Larger blocks are a square GEMM and go to
+        hipBLASLt (gathered ones after an index_select of their rows); larger gathered sets
+        with ``row_active`` and fp32 run ``fg_lm_head``. ``parts`` (from ``walk_parts``): the
+        streaming kernel also writes each row's maxima parts.
         """
         x = hidden.reshape(-1, self.cfg.hidden)
         w = self.w["lm_head"] if weight is None else weight
@@ -716,6 +716,15 @@ class TargetModel:
                                   out_dtype=out_dtype, parts=parts)[0]
         if parts is not None:
             raise ValueError("logits: row maxima parts need the weight-streaming LM head (see walk_parts)")
+        if (self.dtype == torch.bfloat16 and row_index is not None and row_active is None
+                and (out_dtype is None or out_dtype == torch.bfloat16)):
+            # a gathered block above the streaming kernel's rows (the packed tree's internal
+            # nodes) is a square GEMM: gather its rows (rows x H) and run one hipBLASLt GEMM that
+            # reads the weight once, instead of one weight stream per 256 rows
+            xs = x.index_select(0, row_index.long())
+            if out is None:
+                return F.linear(xs, w)
+            return torch.matmul(xs, w.t(), out=out)
         if self.dtype == torch.bfloat16 and not lm_gemm_ok(x, w):
             # operands the hand-written kernels do not take (hidden size not a multiple of 64,
             # unaligned rows): hipBLASLt over the gathered rows

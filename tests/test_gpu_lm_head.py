@@ -203,6 +203,32 @@ def test_target_lm_head_routes_hidden_96():
     assert model.walk_parts(20, h) is None
 
 
+def test_target_logits_gathers_large_blocks_into_one_gemm():
+    """Gathered bf16 rows above 256 (the packed tree's internal nodes) are gathered and
+    projected by one GEMM: equal to the contiguous projection of the same rows, within bf16
+    of an fp32 product, also into a given out; with row_active they stay on fg_lm_head (its
+    active rows checked)."""
+    from flashgrpo_amd.models.target import TargetModel, TargetConfig
+
+    cfg = TargetConfig(num_layers=1, hidden=256, q_heads=2, kv_heads=1, head_dim=128, intermediate=512, vocab=5003)
+    model = TargetModel.random(cfg, seed=5, dtype=torch.bfloat16, device=DEV)
+    w = model.w["lm_head"]
+    h = torch.randn(400, 256, device=DEV).to(torch.bfloat16)
+    idx = torch.tensor(list(range(399, -1, -1)) + [7] * 37, dtype=torch.int32, device=DEV)  # 437 rows, repeats
+    got = model.logits(h, row_index=idx)
+    want = model.logits(h[idx.long()].contiguous())
+    assert got.shape == (437, 5003) and torch.equal(got, want)
+    assert rel_err(to_np(got), to_np(h[idx.long()].float() @ w.float().t())) < 2e-2
+    out = torch.empty(437, 5003, dtype=torch.bfloat16, device=DEV)
+    assert model.logits(h, row_index=idx, out=out).data_ptr() == out.data_ptr() and torch.equal(out, want)
+    act = torch.ones(437, dtype=torch.int32, device=DEV)
+    act[::3] = 0
+    masked = torch.full((437, 5003), 9.0, dtype=torch.bfloat16, device=DEV)
+    model.logits(h, row_index=idx, row_active=act, out=masked)
+    on = act.bool()  # inactive rows may be left unwritten or written
+    assert rel_err(to_np(masked[on]), to_np(want[on])) < 2e-2
+
+
 def test_lm_head_topk_validates_out():
     """A caller's out tensor of the wrong shape, layout, dtype or alignment is refused
     before any launch."""
