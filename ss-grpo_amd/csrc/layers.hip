@@ -146,7 +146,13 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(void* __restrict__ x, cons
 }
 
 // out[t, i] = silu(gu[t, i]) * gu[t, F + i]; 8 elements per thread, one grid row
-// per token. Requires F % 8 == 0.
+// per token. Requires F % 8 == 0. In bf16, SiLU(gate) is rounded to bf16 before the
+// product, as the Hugging Face MLP computes act_fn(gate) * up under bf16 autocast.
+FG_DEVICE float silu_in(float g, int dt) {
+  const float s = g / (1.0f + __expf(-g));
+  return dt == fg::kBF16 ? fg::bf16_to_f32(fg::f32_to_bf16(s)) : s;
+}
+
 template <int DT>
 __global__ void __launch_bounds__(256) swiglu_kernel(const void* __restrict__ gu, void* __restrict__ out, int F) {
   const int ch = blockIdx.x * 256 + threadIdx.x;
@@ -156,7 +162,7 @@ __global__ void __launch_bounds__(256) swiglu_kernel(const void* __restrict__ gu
   fg::load8<DT>(gu, t * 2 * F + ch * 8, g);
   fg::load8<DT>(gu, t * 2 * F + F + ch * 8, u);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) o[j] = g[j] / (1.0f + __expf(-g[j])) * u[j];
+  for (int j = 0; j < 8; ++j) o[j] = silu_in(g[j], DT) * u[j];
   fg::store8<DT>(out, t * F + ch * 8, o);
 }
 

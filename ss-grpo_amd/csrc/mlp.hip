@@ -1,10 +1,11 @@
 // The decoder layer's MLP input projection with its activation fused into the GEMM epilogue:
 //
-//   out[M, I] = silu(bf16(x . Wg^T)) * bf16(x . Wu^T)        W = [Wg; Wu], the [2I, H] gate_up weight
+//   out[M, I] = bf16(silu(bf16(x . Wg^T))) * bf16(x . Wu^T)        W = [Wg; Wu], the [2I, H] gate_up weight
 //
-// bf16 operands, fp32 accumulation; gate and up are rounded to bf16 before the activation, as the
-// unfused projection + `fg_swiglu` (and the Hugging Face MLP the reference runs) round them, so
-// the result equals that pair's whenever the two GEMMs' fp32 sums round to the same bf16 values.
+// bf16 operands, fp32 accumulation; gate and up are rounded to bf16 before the activation and
+// SiLU(gate) before the product, as the unfused projection + `fg_swiglu` (and the Hugging Face
+// MLP the reference runs under bf16 autocast) round them, so the result equals that pair's
+// whenever the two GEMMs' fp32 sums round to the same bf16 values.
 // The [M, 2I] gate/up intermediate is never written.
 //
 // Replaces `act_fn(gate_proj(x)) * up_proj(x)` of the Hugging Face Qwen2/Llama MLP inside each
@@ -224,7 +225,7 @@ __global__ void __launch_bounds__(256, 1) gate_up_swiglu_kernel(MlpArgs p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float gt = round_bf16(acc[i][k][4 * v4 + e]), up = round_bf16(acc[i + FN / 2][k][4 * v4 + e]);
-          o[e] = gt / (1.0f + __expf(-gt)) * up;  // the expression of fg_swiglu
+          o[e] = round_bf16(gt / (1.0f + __expf(-gt))) * up;  // the expression of fg_swiglu (bf16)
         }
         const int r = k * 32 + l32, q = i * 4 + v4;
         *(uint2*)(stage + r * 128 + ((q ^ (r & 7)) * 16) + half * 8) =

@@ -1,7 +1,7 @@
 """The fused MLP input GEMM ``fg_gate_up_swiglu``: SiLU(bf16(x.Wg^T)) * bf16(x.Wu^T) in one kernel.
 
-Checked against a float64 product rounded the way the unfused path rounds (gate and up to bf16,
-the activation in fp32, the result to bf16): every element within the error that one bf16
+Checked against a float64 product rounded the way the unfused path and the reference's MLP
+under bf16 autocast round (gate and up to bf16, SiLU(gate) to bf16, the product to bf16): every element within the error that one bf16
 rounding flip of gate or up can cause, and almost every element bit-equal (a dropped rounding,
 a swapped gate/up block or a wrong column block fails the second check). The kernel is also
 compared with the unfused pair it replaces (hipBLASLt projection + ``fg_swiglu``), with both tile
@@ -36,11 +36,13 @@ def operands(rows, hidden, inter, seed, *, x_pad=0, w_pad=0):
 
 
 def reference(x, w):
-    """float64 products -> bf16 gate/up -> SiLU(gate) * up in fp32 -> bf16, and the bf16 gate/up."""
+    """float64 products -> bf16 gate/up -> bf16 SiLU(gate) -> times up in fp32 -> bf16 (the rounding
+    points of the Hugging Face MLP under bf16 autocast), and the bf16 gate/up."""
     inter = w.shape[0] // 2
     gu = (x.double() @ w.double().t()).float().to(torch.bfloat16)
     gt, up = gu[:, :inter].float(), gu[:, inter:].float()
-    return (gt / (1.0 + torch.exp(-gt)) * up).to(torch.bfloat16), gt, up
+    act = (gt / (1.0 + torch.exp(-gt))).to(torch.bfloat16).float()
+    return (act * up).to(torch.bfloat16), gt, up
 
 
 def accumulation_error(x, w):
@@ -57,11 +59,12 @@ def check_against_reference(out, x, w, min_exact=0.99):
     err = accumulation_error(x, w)
     eg, eu = err[:, :inter], err[:, inter:]
     # gate and up may each differ from the rounded exact products by their fp32 accumulation error
-    # plus one bf16 rounding flip (2^-7 of the value); SiLU' <= 1.1 and |SiLU(g)| <= |g|, so
-    # SiLU(gate)*up moves by <= 1.1 (2^-7 |g| + eg) (|u| + eu) + (|g| + eg) (2^-7 |u| + eu);
+    # plus one bf16 rounding flip (2^-7 of the value), and the bf16 SiLU(gate) by one more flip;
+    # SiLU' <= 1.1 and |SiLU(g)| <= |g|, so SiLU(gate)*up moves by
+    # <= (1.1 (2^-7 |g| + eg) + 2^-7 |g|) (|u| + eu) + (|g| + eg) (2^-7 |u| + eu);
     # the result's own rounding may then differ by one ulp (2^-7 |o|)
     ag, au = gt.abs(), up.abs()
-    tol = (1.1 * (2.0 ** -7 * ag + eg) * (au + eu) + (ag + eg) * (2.0 ** -7 * au + eu)
+    tol = ((1.1 * (2.0 ** -7 * ag + eg) + 2.0 ** -7 * ag) * (au + eu) + (ag + eg) * (2.0 ** -7 * au + eu)
            + 2.0 ** -6 * r.abs() + 1e-30)
     bad = (o - r).abs() > tol
     assert not bad.any(), f"{int(bad.sum())} elements outside the one-flip bound; worst {float((o - r).abs().max())}"
