@@ -8,6 +8,17 @@
 
 namespace {
 
+// A value rounded to the row dtype (bf16: round to nearest even; fp32: itself). The
+// explicit roundings below keep the rounding points of the Hugging Face modules (and the
+// rotary products are not contracted into FMAs, so fp32 rows round them too).
+template <int DT>
+FG_DEVICE float rnd(float x) {
+  if constexpr (DT == fg::kBF16)
+    return fg::bf16_to_f32(fg::f32_to_bf16(x));
+  else
+    return x;
+}
+
 // 4 consecutive elements as floats (8 bytes bf16 / 16 bytes fp32).
 template <int DT>
 FG_DEVICE void load4(const void* p, int64_t i, float (&v)[4]) {
@@ -55,8 +66,8 @@ __global__ void __launch_bounds__(256) rope_kv_write_kernel(
   if (!slot_ok && threadIdx.x == 0 && err_flag) atomicOr(err_flag, 8);
   for (int i = threadIdx.x; i < half; i += blockDim.x) {
     const float ang = (float)pos * inv_freq[i];
-    cs[i] = cosf(ang);
-    sn[i] = sinf(ang);
+    cs[i] = rnd<DT>(cosf(ang));  // the HF rotary embedding casts cos / sin to the model dtype
+    sn[i] = rnd<DT>(sinf(ang));
   }
   __syncthreads();
   const int64_t row = (int64_t)tok * ld_qkv;
@@ -70,9 +81,11 @@ __global__ void __launch_bounds__(256) rope_kv_write_kernel(
     load4<DT>(qkv, src + i0 + half, x2);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+#pragma clang fp contract(off)
+      // q * cos + rotate_half(q) * sin, each product and the sum rounded to the row dtype
       const float c = cs[i0 + j], sv = sn[i0 + j];
-      y1[j] = x1[j] * c - x2[j] * sv;
-      y2[j] = x2[j] * c + x1[j] * sv;
+      y1[j] = rnd<DT>(rnd<DT>(x1[j] * c) - rnd<DT>(x2[j] * sv));
+      y2[j] = rnd<DT>(rnd<DT>(x2[j] * c) + rnd<DT>(x1[j] * sv));
     }
     if (h < Hq) {
       const int64_t dst = ((int64_t)tok * Hq + h) * d;
@@ -138,8 +151,10 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(void* __restrict__ x, cons
     if (ch < nch) {
       float wv[8], o[8];
       fg::load8<DT>(w, ch * 8, wv);
+      // x * rsqrt(mean x^2 + eps) rounded to the row dtype, then times the weight (the HF
+      // RMSNorm's order)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] = v[c][j] * rs * wv[j];
+      for (int j = 0; j < 8; ++j) o[j] = wv[j] * rnd<DT>(v[c][j] * rs);
       fg::store8<DT>(y, base + ch * 8, o);
     }
   }

@@ -104,9 +104,10 @@ def lm_stream_ok(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = No
 
 
 def inv_freq_table(head_dim: int, theta: float) -> torch.Tensor:
-    """fp32 theta^(-2i/d), computed in float64 then rounded once."""
-    i = np.arange(0, head_dim, 2, dtype=np.float64)
-    return torch.from_numpy((1.0 / theta ** (i / head_dim)).astype(np.float32))
+    """fp32 theta^(-2i/d) computed the way the Hugging Face rotary embedding computes its
+    default table (``1 / theta ** (arange(0, d, 2).float() / d)`` in fp32 with torch on the
+    host), so the rotation angles match the reference's bit for bit."""
+    return 1.0 / (float(theta) ** (torch.arange(0, head_dim, 2, dtype=torch.int64).float() / head_dim))
 
 
 def chain_bits(n: int) -> list:
