@@ -65,7 +65,13 @@ FG_DEVICE void epilogue_store(const GemmArgs& g, int z, int m, int n, float acc,
     float b = fg::load_elem<BDT>(g.bias, z * g.bias_batch + n);
     float r = g.r_dtype == fg::kBF16 ? fg::load_elem<fg::kBF16>(g.R, z * g.r_batch + (int64_t)m * g.ldr + n)
                                      : fg::load_elem<fg::kF32>(g.R, z * g.r_batch + (int64_t)m * g.ldr + n);
-    v = r + silu(v + b);
+    if constexpr (CDT == fg::kBF16) {
+      // the reference's bf16 rounding points: fc(x) + b, SiLU of it, then the residual sum
+      const float f = fg::bf16_to_f32(fg::f32_to_bf16(v + b));
+      v = r + fg::bf16_to_f32(fg::f32_to_bf16(silu(f)));
+    } else {
+      v = r + silu(v + b);
+    }
   }
   fg::store_elem<CDT>(g.C, z * g.c_batch + (int64_t)m * g.ldc + n, v);
 }

@@ -541,7 +541,8 @@ MedPlan med_plan(int H, int heads) {
 
 FG_DEVICE float med_silu(float x) { return x / (1.0f + __expf(-x)); }
 
-// out[h * M + m, n] = R[m, n] + SiLU(sum_p parts[p, h, m, n] + bias[h, n]), 4 columns per thread.
+// out[h * M + m, n] = R[m, n] + SiLU(sum_p parts[p, h, m, n] + bias[h, n]), 4 columns per thread
+// (with bf16 output rounded where the reference's bf16 head rounds: fc + bias, SiLU, sum).
 template <int ODT, int RDT>
 __global__ void __launch_bounds__(256) medusa_combine_kernel(const float* __restrict__ parts, int ksplit, int heads,
                                                              int M, int N, const uint16_t* __restrict__ bias,
@@ -578,7 +579,16 @@ __global__ void __launch_bounds__(256) medusa_combine_kernel(const float* __rest
                       __uint_as_float(bw.y << 16), __uint_as_float(bw.y & 0xffff0000u)};
   float v[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = r[e] + med_silu(s[e] + b[e]);
+  for (int e = 0; e < 4; ++e) {
+    if constexpr (ODT == fg::kBF16) {
+      // the reference's bf16 rounding points (project_hidden under bf16 autocast): the fc output
+      // fc(x) + b, SiLU of it, then the residual sum (stored below)
+      const float f = fg::bf16_to_f32(fg::f32_to_bf16(s[e] + b[e]));
+      v[e] = r[e] + fg::bf16_to_f32(fg::f32_to_bf16(med_silu(f)));
+    } else {
+      v[e] = r[e] + med_silu(s[e] + b[e]);
+    }
+  }
   if constexpr (ODT == fg::kBF16)
     *(uint2*)((uint16_t*)out + hm * N + c) = make_uint2(fg::pack_bf16x2(v[0], v[1]), fg::pack_bf16x2(v[2], v[3]));
   else

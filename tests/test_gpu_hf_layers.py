@@ -100,3 +100,33 @@ def test_swiglu_matches_the_mlp_activation():
     assert frac_equal(got, want) >= 0.999
     once = (F.silu(gu[:, :I].float()) * gu[:, I:].float()).to(BF)
     assert frac_equal(once, want) < 0.9
+
+
+def test_medusa_block_matches_the_reference_head_under_autocast():
+    """fg_medusa_heads against the reference's MedusaPredictionHead.project_hidden run the way its
+    decoder runs it (flashgrpo/models/medusa_heads.py:74-78 under torch.autocast(bf16),
+    flash_medusa_decoder.py:265-274): LayerNorm in fp32, fc in bf16, SiLU on the bf16 fc output,
+    then the residual sum -- built here from torch.nn modules with fp32 master weights."""
+    import torch.nn as nn
+
+    torch.manual_seed(4)
+    B, H = 64, 3584
+    ln, fc = nn.LayerNorm(H).to(DEV), nn.Linear(H, H).to(DEV)
+    with torch.no_grad():
+        ln.weight.add_(torch.randn(H, device=DEV) * 0.1)
+        ln.bias.add_(torch.randn(H, device=DEV) * 0.1)
+        fc.weight.mul_(0.0).add_(torch.randn(H, H, device=DEV) * 0.02)
+        fc.bias.add_(torch.randn(H, device=DEV) * 0.05)
+    h = torch.randn(B, H, device=DEV).to(BF)
+    with torch.no_grad(), torch.autocast("cuda", dtype=BF):
+        want = h + F.silu(fc(ln(h)))
+    assert want.dtype == BF
+    got = K().medusa_heads(h, ln.weight.detach()[None], ln.bias.detach()[None],
+                           fc.weight.detach().to(BF)[None].contiguous(), fc.bias.detach().to(BF)[None].contiguous(),
+                           eps=ln.eps)
+    torch.cuda.synchronize()
+    # the fc sums run in a different order than the library GEMM, so a few roundings differ
+    assert frac_equal(got, want) >= 0.98
+    once_ref = (h.float() + F.silu(F.layer_norm(h.float(), (H,), ln.weight, ln.bias, ln.eps).to(BF).float()
+                                   @ fc.weight.to(BF).float().t() + fc.bias.to(BF).float())).to(BF)
+    assert frac_equal(once_ref, want) < 0.9

@@ -578,7 +578,13 @@ def test_medusa_heads_stream_matches_fp32_reference(B, H, nh):
     assert rel_err(to_np(rows), to_np(ln_ref)) < 1e-2
     out_bf = K().medusa_heads(hid, ln_w, ln_b, fc_w, fc_b, workspace=ws)
     assert out_bf.dtype == dt
-    assert torch.equal(out_bf, out.to(dt))
+    # bf16 output: rounded where the reference's bf16 head rounds (fc + bias, SiLU, the sum); the
+    # emulation's fc sums run in the library's order, so a rounding tie may fall the other way
+    pre = torch.bmm(rows, fc_w.float().transpose(1, 2).contiguous()) + fc_b.float()[:, None, :]
+    emu = (hid.float()[None] + torch.nn.functional.silu(pre.to(dt).float()).to(dt).float()).to(dt)
+    same = float((out_bf.view(nh, B, H).view(torch.int16) == emu.view(torch.int16)).float().mean())
+    assert same >= 0.98, same
+    assert rel_err(to_np(out_bf), to_np(out)) < 2e-2
     again = K().medusa_heads(hid, ln_w, ln_b, fc_w, fc_b, out_dtype=torch.float32, workspace=ws)
     assert torch.equal(again, out)
 
