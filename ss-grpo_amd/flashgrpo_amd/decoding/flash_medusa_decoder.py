@@ -381,9 +381,9 @@ class FlashMedusaDecoder:
         with ``stats``, each row's (max, logsumexp): ``(logits or None, tokens, scores,
         stats)``. Tied heads take them from the LM-head kernel's epilogue in one launch
         over every head's rows; untied heads compute the logits first."""
-        own = self.medusa_heads.output_weights(self.model.dtype, self.model.device)[:heads]
+        own = self.medusa_heads.output_weights(proj.dtype, self.model.device)[:heads]
         if all(w is None for w in own):
-            return self.model.logits_topk(proj, kc, stats=stats, logits=logits)
+            return self.model.logits_topk(proj.to(self.model.dtype), kc, stats=stats, logits=logits)
         mlog = self._medusa_logits(proj, heads, batch)
         cand, score, st = K.medusa_topk(mlog, kc, stats=stats)
         return mlog, cand, score, st
@@ -391,15 +391,26 @@ class FlashMedusaDecoder:
     def _medusa_logits(self, proj: torch.Tensor, heads: int, batch: int) -> torch.Tensor:
         """[heads*B, V] proposal logits (``flash_medusa_decoder.py:281-304``): one LM-head
         GEMM over every head's rows when all heads are tied, otherwise each head's rows
-        through its own ``output`` projection (an untied head) or the LM head."""
+        through its own ``output`` projection (an untied head) or the LM head.
+
+        ``proj`` is in the model's dtype under the heads' autocast, else in the heads'
+        parameter dtype (``medusa_heads.py:266-276`` without autocast): the LM head then
+        takes the rows cast to the model's dtype and an untied head's own projection runs
+        in the heads' dtype, so mixed heads give logits in that dtype (the LM head's bf16
+        values held exactly)."""
         model = self.model
-        own = self.medusa_heads.output_weights(model.dtype, model.device)[:heads]
+        own = self.medusa_heads.output_weights(proj.dtype, model.device)[:heads]
         if all(w is None for w in own):
-            return model.logits(proj)
-        out = torch.empty((heads * batch, model.cfg.vocab), dtype=model.dtype, device=model.device)
+            return model.logits(proj.to(model.dtype))
+        out = torch.empty((heads * batch, model.cfg.vocab), dtype=proj.dtype, device=model.device)
         for h, w in enumerate(own):
             rows = slice(h * batch, (h + 1) * batch)
-            model.logits(proj[rows], out=out[rows], weight=w)
+            if proj.dtype == model.dtype:
+                model.logits(proj[rows], out=out[rows], weight=w)
+            elif w is None:
+                out[rows].copy_(model.logits(proj[rows].to(model.dtype)))
+            else:
+                torch.matmul(proj[rows], w.t(), out=out[rows])
         return out
 
     # ------------------------------------------------------------------ rollout
@@ -477,7 +488,10 @@ class FlashMedusaDecoder:
         use_chain = use_tree and cfg.proposal_mode == "chain" and r.generation_step >= int(cfg.chain_enable_after)
         f = dict(rnd=rnd, batch=Bc, roots=roots, plan=plan, use_tree=use_tree, use_chain=use_chain, med=None)
         if plan.active_heads > 0 and not use_chain:
-            proj = self.medusa_heads.project_all(hidden, plan.active_heads)
+            # the heads under bf16 autocast (head_inference_autocast, flash_medusa_decoder.py:
+            # 268-272), else in their parameter dtype
+            heads_dt = hidden.dtype if cfg.head_inference_autocast else self.medusa_heads.heads[0].norm.weight.dtype
+            proj = self.medusa_heads.project_all(hidden.to(heads_dt), plan.active_heads)
             V = self.model.cfg.vocab
             if plan.layout == "sparse_asymmetric":
                 # candidate lists of the sparse widths (adaptation only shrinks them)

@@ -52,34 +52,39 @@ class ChainDraftCell(nn.Module):
                 self._cast = dict(
                     sn_w=c(self.state_norm.weight), sn_b=c(self.state_norm.bias),
                     tn_w=c(self.token_norm.weight), tn_b=c(self.token_norm.bias),
-                    # [bottleneck, 2H]: state_proj and token_proj side by side, one GEMM over
-                    # the concatenated normalised inputs gives their sum
-                    proj=c(torch.cat([self.state_proj.weight, self.token_proj.weight], dim=1)),
+                    sp_w=c(self.state_proj.weight), tp_w=c(self.token_proj.weight),
                     out_w=c(self.out_proj.weight), out_b=c(self.out_proj.bias),
-                    gate=torch.sigmoid(self.gate.detach().float()).to(device=device, dtype=dtype),
+                    # sigmoid in the gate's own dtype, as the module's forward takes it
+                    gate=torch.sigmoid(self.gate.detach()).to(device=device),
                     eps=float(self.state_norm.eps))
             self._cast_key = key
         return self._cast
 
     def step(self, state, token_embedding):
-        """The cell in the state's dtype (weights cast once and cached), as the rollout
-        runs the Medusa heads in the target's dtype. On the GPU the two LayerNorms are one
-        HIP launch (``fg_chain_cell_norm``); the projections run on hipBLASLt."""
-        w = self._weights(state.dtype, state.device)
+        """The cell in its parameters' dtype, as ``medusa_heads.py:36-42`` runs it (the
+        rollout calls it outside autocast, ``flash_medusa_decoder.py:435-539``): the state
+        and the embedding are cast to that dtype and the new state keeps it. On the GPU the
+        two LayerNorms are one HIP launch (``fg_chain_cell_norm``); the two projections,
+        their sum, SiLU, the output projection and the gated residual are the module's
+        own torch calls, so every intermediate is rounded where the module rounds it."""
+        dt = self.state_norm.weight.dtype
+        w = self._weights(dt, state.device)
         H = state.shape[-1]
-        tok = token_embedding.to(state.dtype)
-        if state.is_cuda:
+        s = state.to(dt)
+        tok = token_embedding.to(dt)
+        if s.is_cuda:
             # both LayerNorms in one launch, written side by side (fg_chain_cell_norm)
             from .. import kernels as K
 
             rows = lambda t: t.reshape(-1, H) if t.is_contiguous() else t.reshape(-1, H).contiguous()
-            x = K.chain_cell_norm(rows(state), rows(tok), w["sn_w"], w["sn_b"], w["tn_w"], w["tn_b"], w["eps"])
-            x = x.view(*state.shape[:-1], 2 * H)
+            x = K.chain_cell_norm(rows(s), rows(tok), w["sn_w"], w["sn_b"], w["tn_w"], w["tn_b"], w["eps"])
+            xs, xt = x[:, :H].view(*s.shape), x[:, H:].view(*s.shape)
         else:
-            x = torch.cat([F.layer_norm(state, (H,), w["sn_w"], w["sn_b"], w["eps"]),
-                           F.layer_norm(tok, (H,), w["tn_w"], w["tn_b"], w["eps"])], dim=-1)
-        delta = F.linear(F.silu(F.linear(x, w["proj"])), w["out_w"], w["out_b"])
-        return torch.addcmul(state, delta, w["gate"])
+            xs = F.layer_norm(s, (H,), w["sn_w"], w["sn_b"], w["eps"])
+            xt = F.layer_norm(tok, (H,), w["tn_w"], w["tn_b"], w["eps"])
+        mixed = F.linear(xs, w["sp_w"]) + F.linear(xt, w["tp_w"])
+        delta = F.linear(F.silu(mixed), w["out_w"], w["out_b"])
+        return s + w["gate"] * delta
 
 
 class MedusaPredictionHead(nn.Module):
@@ -108,10 +113,12 @@ class MedusaPredictionHead(nn.Module):
                     self.output.weight.copy_(src.detach().to(self.output.weight.dtype))
 
     def project_hidden(self, hidden_states):
-        """Single-head residual block on the device (fg_medusa_heads with one head)."""
+        """Single-head residual block on the device (fg_medusa_heads with one head), in the
+        head's parameter dtype as ``medusa_heads.py:74-78`` computes it outside autocast
+        (the chain bootstrap, ``flash_medusa_decoder.py:455-456``)."""
         h = hidden_states
         lead = h.shape[:-1]
-        flat = h.reshape(-1, self.hidden_size).contiguous()
+        flat = h.reshape(-1, self.hidden_size).to(self.norm.weight.dtype).contiguous()
         out = K.medusa_heads(flat, self.norm.weight.detach()[None], self.norm.bias.detach()[None],
                              self.fc.weight.detach().to(flat.dtype)[None].contiguous(),
                              self.fc.bias.detach().to(flat.dtype)[None].contiguous(), eps=self.norm.eps)
@@ -193,7 +200,7 @@ class MedusaHeads(nn.Module):
 
     def chain_next_state(self, state, token_ids, embedding_weight):
         """Next chain state from the parent state and the path token's embedding
-        (``medusa_heads.py:279-286``), computed in the state's dtype."""
+        (``medusa_heads.py:279-286``), computed in the cell's parameter dtype."""
         emb = embedding_weight.index_select(0, token_ids.to(embedding_weight.device).long())
         return self.chain_cell.step(state, emb)
 

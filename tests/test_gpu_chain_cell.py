@@ -59,8 +59,14 @@ def test_matches_float64_layer_norms(dtype, rows, H, pad):
     assert float((out.float() - torch_ref.float()).abs().max()) <= 2 * ulp * float(torch_ref.float().abs().max())
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_cell_step_matches_module_forward(dtype):
+@pytest.mark.parametrize("cell_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("state_dtype", [torch.bfloat16, torch.float32])
+def test_cell_step_matches_module_forward(cell_dtype, state_dtype):
+    """The step runs in the cell's parameter dtype, whatever the state's (the rollout hands
+    it bf16 hidden rows and fp32 states of fp32 heads), and returns that dtype, as the
+    module's forward does. In fp32 it agrees with the forward to fp32 rounding; in bf16
+    almost every element is bit-equal (only the LayerNorm, one HIP launch, differs from
+    torch's, by a bf16 rounding flip now and then)."""
     from flashgrpo_amd.models.medusa_heads import ChainDraftCell
 
     torch.manual_seed(3)
@@ -69,14 +75,43 @@ def test_cell_step_matches_module_forward(dtype):
     with torch.no_grad():
         for p in cell.parameters():
             p.add_(torch.randn_like(p) * 0.05)
-    state = (torch.randn(37, H, device=DEV) * 2).to(dtype)
-    tok = torch.randn(37, H, device=DEV).to(dtype)
+    cell = cell.to(cell_dtype)
+    state = (torch.randn(37, H, device=DEV) * 2).to(state_dtype)
+    tok = torch.randn(37, H, device=DEV).to(torch.bfloat16)
     got = cell.step(state, tok)
     with torch.no_grad():
-        want = cell.to(dtype)(state, tok)
+        want = cell(state, tok)
     torch.cuda.synchronize()
-    tol = 2e-2 if dtype == torch.bfloat16 else 1e-5
-    assert float((got.float() - want.float()).abs().max()) <= tol * float(want.float().abs().max())
+    assert got.dtype == want.dtype == cell_dtype
+    if cell_dtype == torch.float32:
+        assert float((got - want).abs().max()) <= 1e-5 * float(want.abs().max())
+    else:
+        exact = float((got.view(torch.int16) == want.view(torch.int16)).float().mean())
+        assert exact >= 0.97, exact
+        assert float((got.float() - want.float()).abs().max()) <= 2.0 ** -6 * float(want.float().abs().max())
+
+
+def test_chain_bootstrap_head_runs_in_its_parameter_dtype():
+    """Medusa head 0 bootstraps chain proposals outside autocast: fp32 heads give an fp32
+    state from the bf16 hidden rows, h + SiLU(fc(LayerNorm(h))) with no bf16 rounding."""
+    from flashgrpo_amd.models.medusa_heads import MedusaHeads
+
+    torch.manual_seed(5)
+    H = 512
+    heads = MedusaHeads(H, 1000, 2).to(DEV)
+    with torch.no_grad():
+        for p in heads.parameters():
+            p.add_(torch.randn_like(p) * 0.05)
+    hid = (torch.randn(21, H, device=DEV) * 2).to(torch.bfloat16)
+    got = heads.heads[0].project_hidden(hid)
+    hd = heads.heads[0]
+    with torch.no_grad():
+        x = hid.double()
+        want = x + F.silu(F.linear(F.layer_norm(x, (H,), hd.norm.weight.double(), hd.norm.bias.double(), hd.norm.eps),
+                                   hd.fc.weight.double(), hd.fc.bias.double()))
+    torch.cuda.synchronize()
+    assert got.dtype == torch.float32
+    assert float((got.double() - want).abs().max()) <= 1e-5 * float(want.abs().max())
 
 
 def test_rejects_bad_operands():

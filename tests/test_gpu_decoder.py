@@ -77,9 +77,9 @@ def rounded(W, heads, dtype, cell=None):
     Wr["inv_freq"] = W["inv_freq"]
     Wr["layers"] = [{k: r(v) for k, v in lw.items()} for lw in W["layers"]]
     hr = [dict(h, fc_w=r(h["fc_w"]), fc_b=r(h["fc_b"]), out_w=r(h.get("out_w"))) for h in heads]
-    # the device runs the chain cell in the target's dtype
-    cr = None if cell is None else {k: (v if k == "gate" else r(v)) for k, v in cell.items()}
-    return Wr, hr, cr
+    # the chain cell (and the head that bootstraps it) run in their own fp32 parameters,
+    # outside the bf16 autocast of the proposal heads
+    return Wr, hr, cell
 
 
 def _k_near(conf, base_k, d, spec):
@@ -91,14 +91,14 @@ def _k_near(conf, base_k, d, spec):
             for c in (conf - 1e-6, conf, conf + 1e-6)}
 
 
-def check_chain(rec, spec, Wr, heads_r, cell_r, tol, Bc):
+def check_chain(rec, spec, Wr, boot_head, cell_r, tol, Bc):
     """Chain proposals of one round from the device's own per-depth states and logits:
     bootstrap state, logits of every state, adapted k, tree tokens (exact given the
     logits) and each next state (cell on the device's parent state)."""
     ch = rec["chain"]
     roots = rec["roots"]
     if spec.chain_bootstrap_from_medusa:
-        boot = OM.medusa_project(rec["hidden_in"], heads_r[0])
+        boot = OM.medusa_project(rec["hidden_in"], boot_head)
     else:
         boot = OM.chain_cell(rec["hidden_in"], Wr["embed"][roots], cell_r)
     assert rel(ch[0]["states"], boot) < tol
@@ -177,10 +177,12 @@ class OracleRow:
 
 
 def lockstep(trace, ocfg, Wr, heads_r, spec, prompts, dtype, seed, max_length, emit_correction=False, cell_r=None,
-             odt=np.float64, rows=None):
+             odt=np.float64, rows=None, boot_head=None):
     """Replays every traced round on the oracle. ``odt`` is the oracle's compute dtype
     (float32 only for bf16 runs, whose tolerance is 2e-2); ``rows`` optionally gives
-    pre-built OracleRows (a prefix taken from the device's cache)."""
+    pre-built OracleRows (a prefix taken from the device's cache); ``boot_head`` is the
+    head that bootstraps chain proposals in its own parameter dtype (default: head 0 of
+    ``heads_r``)."""
     tol = TOL[dtype]
     Wr, heads_r = cast_weights(Wr, heads_r, odt)
     lm = Wr["lm_head"]
@@ -206,7 +208,7 @@ def lockstep(trace, ocfg, Wr, heads_r, spec, prompts, dtype, seed, max_length, e
         assert rec["roots"].tolist() == want_roots, rnd
         plan = OD.plan_for(spec, Bc)
         if "chain" in rec:
-            trees = check_chain(rec, spec, Wr, heads_r, cell_r, tol, Bc)
+            trees = check_chain(rec, spec, Wr, heads_r[0] if boot_head is None else boot_head, cell_r, tol, Bc)
             stats["chain_rounds"] = stats.get("chain_rounds", 0) + 1
         else:
             if "medusa_logits" in rec:
@@ -297,7 +299,7 @@ def lockstep(trace, ocfg, Wr, heads_r, spec, prompts, dtype, seed, max_length, e
 
 
 def _run(ocfg, spec, *, dtype, B0, repeats, P, max_length, seed=123, wseed=0, cache_mode="extract_path",
-         internal_only=True, lazy=True, untied=(), std=0.05, odt=np.float64):
+         internal_only=True, lazy=True, untied=(), std=0.05, odt=np.float64, head_autocast=True):
     from flashgrpo_amd.decoding import FlashMedusaConfig, FlashMedusaDecoder
 
     W = OM.random_weights(ocfg, seed=wseed, std=std)
@@ -326,7 +328,8 @@ def _run(ocfg, spec, *, dtype, B0, repeats, P, max_length, seed=123, wseed=0, ca
                             sparse_min_head3_nodes=spec.sparse_min_head3_nodes,
                             sparse_head3_min_budget=spec.sparse_head3_min_budget,
                             sparse_branch_score_temperature=spec.sparse_branch_score_temperature,
-                            sparse_diversity_penalty=spec.sparse_diversity_penalty)
+                            sparse_diversity_penalty=spec.sparse_diversity_penalty,
+                            head_inference_autocast=head_autocast)
     dec = FlashMedusaDecoder(model, mh, Tok(spec.eos_token_id), cfg)
     rng = np.random.default_rng(wseed + 7)
     prompts = rng.integers(0, ocfg.vocab, (B0, P))
@@ -334,9 +337,11 @@ def _run(ocfg, spec, *, dtype, B0, repeats, P, max_length, seed=123, wseed=0, ca
     out = dec.generate(torch.from_numpy(prompts), torch.ones(B0, P, dtype=torch.long), repeated_generate_nums=repeats,
                        max_length=max_length, trace=trace)
     Wr, hr, cr = rounded(W, heads, dtype, cell)
+    if not head_autocast:
+        hr = heads  # the proposal heads run in their own fp32 parameters
     seed_eff = trace[0]["seed"]
     stats = lockstep(trace, ocfg, Wr, hr, spec, np.repeat(prompts, repeats, axis=0), dtype, seed_eff, max_length,
-                     emit_correction=spec.emit_correction_token, cell_r=cr, odt=odt)
+                     emit_correction=spec.emit_correction_token, cell_r=cr, odt=odt, boot_head=heads[0])
     for s, g in enumerate(out["generated_token_ids"]):
         assert len(g) >= 1
     return out, stats
@@ -527,6 +532,18 @@ def test_lockstep_untied_medusa_heads(dtype):
                          num_medusa_heads=3, max_tree_depth=4, top_p=1.0)
     cfg = SMALL if dtype == torch.float32 else SMALL16
     out, st = _run(cfg, spec, dtype=dtype, B0=2, repeats=2, P=25, max_length=25 + 12, untied=(0, 2))
+    assert st["rounds"] == out["total_verify_rounds"] > 0
+
+
+def test_lockstep_heads_without_autocast():
+    """head_inference_autocast=False: the fp32 heads' residual blocks and head 1's own output
+    projection in fp32, the tied heads' rows cast to bf16 for the LM head
+    (flash_medusa_decoder.py:268-272 with autocast off, medusa_heads.py:266-276); checked
+    against the oracle on the unrounded head weights."""
+    spec = OD.DecodeSpec(tree_mode="fixed", max_tree_nodes_per_seq=16, fixed_tree_topk_by_depth=(4, 2, 1),
+                         num_medusa_heads=3, max_tree_depth=4, top_p=1.0)
+    out, st = _run(SMALL16, spec, dtype=torch.bfloat16, B0=2, repeats=2, P=25, max_length=25 + 12, untied=(1,),
+                   head_autocast=False)
     assert st["rounds"] == out["total_verify_rounds"] > 0
 
 
