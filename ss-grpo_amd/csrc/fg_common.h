@@ -50,6 +50,14 @@ FG_DEVICE uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
+// x rounded to the nearest bf16 (ties to even), as a float: one v_cvt_pk_bf16_f32 and a shift.
+FG_DEVICE float round_bf16(float x) { return __uint_as_float(pack_bf16x2(x, 0.0f) << 16); }
+
+// SiLU(x) = x / (1 + e^-x), the quotient taken as x times the hardware reciprocal
+// (v_rcp_f32, 1 ulp) instead of the ten-instruction IEEE division: within 2 ulp of the
+// correctly rounded value, so a bf16 rounding of it differs only next to a rounding tie.
+FG_DEVICE float silu_f32(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+
 template <int DT>
 FG_DEVICE float load_elem(const void* p, int64_t i) {
   if constexpr (DT == kBF16)

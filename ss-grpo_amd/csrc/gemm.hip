@@ -47,7 +47,6 @@ struct GemmArgs {
   int M, N, K;
 };
 
-FG_DEVICE float silu(float x) { return x / (1.0f + __expf(-x)); }
 
 // Block-uniform: does any row of [m0, m0 + rows) have a non-zero row_active flag?
 FG_DEVICE bool tile_has_active_row(const GemmArgs& g, int m0, int rows) {
@@ -67,10 +66,10 @@ FG_DEVICE void epilogue_store(const GemmArgs& g, int z, int m, int n, float acc,
                                      : fg::load_elem<fg::kF32>(g.R, z * g.r_batch + (int64_t)m * g.ldr + n);
     if constexpr (CDT == fg::kBF16) {
       // the reference's bf16 rounding points: fc(x) + b, SiLU of it, then the residual sum
-      const float f = fg::bf16_to_f32(fg::f32_to_bf16(v + b));
-      v = r + fg::bf16_to_f32(fg::f32_to_bf16(silu(f)));
+      const float f = fg::round_bf16(v + b);
+      v = r + fg::round_bf16(fg::silu_f32(f));
     } else {
-      v = r + silu(v + b);
+      v = r + fg::silu_f32(v + b);
     }
   }
   fg::store_elem<CDT>(g.C, z * g.c_batch + (int64_t)m * g.ldc + n, v);

@@ -14,7 +14,7 @@ namespace {
 template <int DT>
 FG_DEVICE float rnd(float x) {
   if constexpr (DT == fg::kBF16)
-    return fg::bf16_to_f32(fg::f32_to_bf16(x));
+    return fg::round_bf16(x);
   else
     return x;
 }
@@ -164,8 +164,8 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(void* __restrict__ x, cons
 // per token. Requires F % 8 == 0. In bf16, SiLU(gate) is rounded to bf16 before the
 // product, as the Hugging Face MLP computes act_fn(gate) * up under bf16 autocast.
 FG_DEVICE float silu_in(float g, int dt) {
-  const float s = g / (1.0f + __expf(-g));
-  return dt == fg::kBF16 ? fg::bf16_to_f32(fg::f32_to_bf16(s)) : s;
+  const float s = fg::silu_f32(g);
+  return dt == fg::kBF16 ? fg::round_bf16(s) : s;
 }
 
 template <int DT>

@@ -539,7 +539,6 @@ MedPlan med_plan(int H, int heads) {
   return p;
 }
 
-FG_DEVICE float med_silu(float x) { return x / (1.0f + __expf(-x)); }
 
 // out[h * M + m, n] = R[m, n] + SiLU(sum_p parts[p, h, m, n] + bias[h, n]), 4 columns per thread
 // (with bf16 output rounded where the reference's bf16 head rounds: fc + bias, SiLU, sum).
@@ -583,10 +582,10 @@ __global__ void __launch_bounds__(256) medusa_combine_kernel(const float* __rest
     if constexpr (ODT == fg::kBF16) {
       // the reference's bf16 rounding points (project_hidden under bf16 autocast): the fc output
       // fc(x) + b, SiLU of it, then the residual sum (stored below)
-      const float f = fg::bf16_to_f32(fg::f32_to_bf16(s[e] + b[e]));
-      v[e] = r[e] + fg::bf16_to_f32(fg::f32_to_bf16(med_silu(f)));
+      const float f = fg::round_bf16(s[e] + b[e]);
+      v[e] = r[e] + fg::round_bf16(fg::silu_f32(f));
     } else {
-      v[e] = r[e] + med_silu(s[e] + b[e]);
+      v[e] = r[e] + fg::silu_f32(s[e] + b[e]);
     }
   }
   if constexpr (ODT == fg::kBF16)

@@ -49,7 +49,6 @@ FG_DEVICE void wait_vmcnt() {
 }
 FG_DEVICE void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4)); }
 
-FG_DEVICE float round_bf16(float x) { return __uint_as_float(fg::pack_bf16x2(x, 0.0f) << 16); }
 
 struct MlpArgs {
   const uint16_t* x;
@@ -224,8 +223,8 @@ __global__ void __launch_bounds__(256, 1) gate_up_swiglu_kernel(MlpArgs p) {
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float gt = round_bf16(acc[i][k][4 * v4 + e]), up = round_bf16(acc[i + FN / 2][k][4 * v4 + e]);
-          o[e] = round_bf16(gt / (1.0f + __expf(-gt))) * up;  // the expression of fg_swiglu (bf16)
+          const float gt = fg::round_bf16(acc[i][k][4 * v4 + e]), up = fg::round_bf16(acc[i + FN / 2][k][4 * v4 + e]);
+          o[e] = fg::round_bf16(fg::silu_f32(gt)) * up;  // the expression of fg_swiglu (bf16)
         }
         const int r = k * 32 + l32, q = i * 4 + v4;
         *(uint2*)(stage + r * 128 + ((q ^ (r & 7)) * 16) + half * 8) =
