@@ -1,6 +1,7 @@
 """Regenerate the MLP input-path table (run on the MI355X it is meant for).
 
     python -m flashgrpo_amd.tuning.make_mlp_table --out mlp_mi355x.csv [--reps 20]
+        [--presets qwen25_7b,...] [--rows 1856,...]
 
 For the (intermediate, hidden) sizes of every target preset and a grid of row counts
 (powers of two plus the verify-round and prefill shapes of the benchmark workloads), it
@@ -8,7 +9,8 @@ times the two ways the decoder layer can compute its MLP input SiLU(x.Wg^T) * (x
 the hipBLASLt projection (through the GEMM solution table) followed by ``fg_swiglu``, and
 ``fg_gate_up_swiglu`` at both tile heights. Each time is the minimum over ``reps``
 launches with the weight alternating between two copies (so it is read from HBM). One
-row per shape names the fastest path.
+row per shape names the fastest path. ``--presets`` / ``--rows`` restrict the run to some
+presets and row counts (a profiling run of one shape); the full table needs neither.
 """
 from __future__ import annotations
 
@@ -32,7 +34,11 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--out", required=True)
     ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--presets", default="", help="comma-separated preset names (default: all)")
+    ap.add_argument("--rows", default="", help="comma-separated row counts (default: the full grid)")
     args = ap.parse_args()
+    only_presets = {p for p in args.presets.split(",") if p}
+    only_rows = {int(r) for r in args.rows.split(",") if r}
     import torch
     import torch.nn.functional as F
 
@@ -59,6 +65,8 @@ def main():
     lines = ["rows,inter,hidden,pair_us,fused192_us,fused256_us,choice"]
     done = set()
     for preset, extra in SHAPES.items():
+        if only_presets and preset not in only_presets:
+            continue
         cfg = getattr(TargetConfig, preset)()
         I, H = cfg.intermediate, cfg.hidden
         if (I, H) in done:
@@ -66,7 +74,7 @@ def main():
         done.add((I, H))
         g = torch.Generator(device="cuda").manual_seed(I)
         ws = [(torch.randn(2 * I, H, device="cuda", generator=g) * 0.05).to(torch.bfloat16) for _ in range(2)]
-        for rows in sorted(set(GRID) | set(extra)):
+        for rows in sorted(only_rows or (set(GRID) | set(extra))):
             x = (torch.randn(rows, H, device="cuda", generator=g) * 0.5).to(torch.bfloat16)
             out = torch.empty(rows, I, dtype=torch.bfloat16, device="cuda")
             it = [0]
