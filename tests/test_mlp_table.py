@@ -20,7 +20,9 @@ def rows():
 def test_table_choices_are_the_fastest_measured_path():
     for r in rows():
         t = {k: float(r[k + "_us"]) for k in ("pair", "fused192", "fused256")}
-        assert r["choice"] == min(t, key=t.get), r
+        # the generator picks on unrounded times; the file keeps one decimal, so a
+        # choice may tie the minimum after rounding but never exceed it by a step
+        assert t[r["choice"]] <= min(t.values()) + 0.05, r
         assert all(v > 0 for v in t.values())
 
 
