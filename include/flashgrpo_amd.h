@@ -24,6 +24,10 @@
  *   fg_rmsnorm, fg_swiglu  models/qwen_flashgrpo_wrapper.py:172-180 (HF decoder layer)
  *   fg_gate_up_swiglu   models/qwen_flashgrpo_wrapper.py:172-180 (the HF decoder layer's MLP
  *                       act_fn(gate_proj(x)) * up_proj(x), the two projections and the product in one GEMM)
+ *   fg_linear_parts, fg_residual_rmsnorm_parts, fg_rope_kv_write_parts
+ *                       models/qwen_flashgrpo_wrapper.py:172-180 (the HF decoder layer's q/k/v, o and
+ *                       down projections, finished with the bias + rotary + cache write or the
+ *                       residual add + next RMSNorm)
  *   fg_chain_cell_norm  models/medusa_heads.py:12-42 (ChainDraftCell state_norm / token_norm,
  *                       the two LayerNorms whose outputs its projections take side by side)
  *   fg_sample_tokens    decoding/acceptance.py:34-130 (sample_from_logits)
@@ -166,6 +170,35 @@ int fg_swiglu(const void* gate_up, void* out, int dtype, int rows, int inter, vo
  * tile_rows: 0 (chosen from the shape), 192 or 256 rows per workgroup tile. */
 int fg_gate_up_swiglu(const void* x, int64_t ldx, const void* w_gate_up, int64_t ldw, void* out, int64_t ldo, int rows,
                       int inter, int hidden, int tile_rows, void* stream);
+
+/* Split-K projection: part[s][r, c] = sum over split s's k-steps of x[r, k] * w[c, k], fp32
+ * (bf16 x [rows, hidden] row stride ldx, w [cols, hidden] row stride ldw; part [splits, rows, cols]
+ * contiguous). Replaces the q/k/v, o and down projections (nn.Linear) of the HF decoder layers the
+ * reference's tree verify runs: models/qwen_flashgrpo_wrapper.py:172-180. hidden % 64 == 0,
+ * cols % 4 == 0, 16-byte aligned rows; splits in [1, hidden/64] with
+ * ceil(nk / ceil(nk / splits)) == splits (nk = hidden / 64), so that every split has k-steps;
+ * tile_m, tile_n: 64 or 128 output rows / columns per workgroup. */
+int fg_linear_parts(const void* x, int64_t ldx, const void* w, int64_t ldw, float* part, int rows, int cols,
+                    int hidden, int splits, int tile_m, int tile_n, void* stream);
+
+/* The residual add and the following RMSNorm of an O or down projection given as split-K parts
+ * [splits, rows, hidden]: x[r] = bf16(x[r] + bf16(sum_s part[s][r])) in place (bf16 x, row stride
+ * ldx), then h[r] = weight * bf16(x[r] * rsqrt(mean(x[r]^2) + eps)) (bf16, row stride ldh).
+ * Replaces `residual + self_attn(...)` / `residual + mlp(...)` and the next RMSNorm of the HF
+ * decoder layer (models/qwen_flashgrpo_wrapper.py:172-180). hidden % 8 == 0, hidden <= 8192. */
+int fg_residual_rmsnorm_parts(const float* part, int splits, int rows, int hidden, void* x, int64_t ldx,
+                              const void* weight, float eps, void* h, int64_t ldh, void* stream);
+
+/* fg_rope_kv_write with the projected qkv rows given as split-K parts [splits, batch*num_nodes,
+ * (q_heads + 2*kv_heads)*head_dim] (fg_linear_parts): each value is bf16(sum_s part + bias) (bias
+ * [width] in `dtype`, or NULL), then rotated and written as fg_rope_kv_write does. Replaces the
+ * q/k/v projections' bias add with the HF rotary embedding and DynamicCache.update
+ * (models/qwen_flashgrpo_wrapper.py:172-180). */
+int fg_rope_kv_write_parts(const float* part, int splits, const void* bias, int dtype, int batch, int num_nodes,
+                           int q_heads, int kv_heads, int head_dim, const int32_t* seq_len, const int32_t* pos_offset,
+                           int64_t pos_batch_stride, const float* inv_freq, void* q_out, void* k_cache, void* v_cache,
+                           int64_t cache_batch_stride, int64_t cache_head_stride, int capacity,
+                           const int32_t* row_map, int32_t* err_flag, void* stream);
 
 /* out[r] = [LayerNorm(state[r]) * state_w + state_b, LayerNorm(token[r]) * token_w + token_b]
  * ([rows, 2*hidden], row stride 2*hidden): the ChainDraftCell's normalised inputs side by side.

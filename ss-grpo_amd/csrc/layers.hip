@@ -42,6 +42,38 @@ FG_DEVICE void store4(void* p, int64_t i, const float (&v)[4]) {
     *(float4*)((float*)p + i) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
+// Where rope_kv_write_kernel reads a token's projected qkv row: a row of the qkv tensor, or
+// (part != nullptr) the fp32 split-K partial sums of the projection (fg_linear_parts, row stride
+// ld = the projection's width) summed in split order, plus the bias, rounded to the row dtype as the
+// projection's output would be.
+template <int DT>
+struct QkvSource {
+  const void* qkv;
+  const float* part;
+  int64_t part_stride;
+  int splits;
+  const void* bias;
+
+  FG_DEVICE void get4(int64_t row, int col, float (&v)[4]) const {
+    if (part == nullptr) {
+      load4<DT>(qkv, row + col, v);
+      return;
+    }
+    const float* src = part + row + col;
+    float4 a = *(const float4*)src;
+    for (int s = 1; s < splits; ++s) {
+      const float4 b = *(const float4*)(src + s * part_stride);
+      a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+    }
+    float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (bias) load4<DT>(bias, col, bv);
+    v[0] = rnd<DT>(a.x + bv[0]);
+    v[1] = rnd<DT>(a.y + bv[1]);
+    v[2] = rnd<DT>(a.z + bv[2]);
+    v[3] = rnd<DT>(a.w + bv[3]);
+  }
+};
+
 // One workgroup per token (b, n). qkv row = [q heads | k heads | v heads] x d.
 // Position = seq_len[b] + pos_offset[b * pos_stride + n]; cache slot = seq_len[b] + n.
 // cos/sin of the token's d/2 angles are computed once into LDS; each thread then
@@ -49,7 +81,7 @@ FG_DEVICE void store4(void* p, int64_t i, const float (&v)[4]) {
 // Requires d % 8 == 0 and d <= 256.
 template <int DT>
 __global__ void __launch_bounds__(256) rope_kv_write_kernel(
-    const void* __restrict__ qkv, int64_t ld_qkv, int N, int Hq, int Hkv, int d, const int32_t* __restrict__ seq_len,
+    QkvSource<DT> qkv, int64_t ld_qkv, int N, int Hq, int Hkv, int d, const int32_t* __restrict__ seq_len,
     const int32_t* __restrict__ pos_offset, int64_t pos_stride, const float* __restrict__ inv_freq,
     void* __restrict__ q_out,
     void* __restrict__ k_cache, void* __restrict__ v_cache, int64_t cache_batch, int64_t cache_head, int capacity,
@@ -75,10 +107,9 @@ __global__ void __launch_bounds__(256) rope_kv_write_kernel(
   // q and k heads: rotate pairs (i, i + d/2), 4 pairs per item
   for (int e = threadIdx.x; e < (Hq + Hkv) * quads; e += blockDim.x) {
     const int h = e / quads, i0 = (e % quads) * 4;
-    const int64_t src = row + (int64_t)h * d;
     float x1[4], x2[4], y1[4], y2[4];
-    load4<DT>(qkv, src + i0, x1);
-    load4<DT>(qkv, src + i0 + half, x2);
+    qkv.get4(row, h * d + i0, x1);
+    qkv.get4(row, h * d + i0 + half, x2);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
 #pragma clang fp contract(off)
@@ -100,8 +131,14 @@ __global__ void __launch_bounds__(256) rope_kv_write_kernel(
   const int oct = d / 8;
   for (int e = threadIdx.x; slot_ok && e < Hkv * oct; e += blockDim.x) {
     const int hk = e / oct, i0 = (e % oct) * 8;
-    float x[8];
-    fg::load8<DT>(qkv, row + (int64_t)(Hq + Hkv + hk) * d + i0, x);
+    float x[8], lo[4], hi[4];
+    qkv.get4(row, (Hq + Hkv + hk) * d + i0, lo);
+    qkv.get4(row, (Hq + Hkv + hk) * d + i0 + 4, hi);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      x[j] = lo[j];
+      x[4 + j] = hi[j];
+    }
     fg::store8<DT>(v_cache, (int64_t)cb * cache_batch + (int64_t)hk * cache_head + (int64_t)slot * d + i0, x);
   }
 }
@@ -246,30 +283,70 @@ __global__ void __launch_bounds__(256) chain_cell_norm_kernel(const void* __rest
 
 extern "C" {
 
+}  // extern "C"
+
+namespace {
+
+int rope_kv_write_launch(const char* what, const void* qkv, const float* part, int64_t part_stride, int splits,
+                         const void* bias, int dtype, int64_t ld_qkv, int batch, int num_nodes, int q_heads,
+                         int kv_heads, int head_dim, const int32_t* seq_len, const int32_t* pos_offset,
+                         int64_t pos_batch_stride, const float* inv_freq, void* q_out, void* k_cache, void* v_cache,
+                         int64_t cache_batch_stride, int64_t cache_head_stride, int capacity, const int32_t* row_map,
+                         int32_t* err_flag, void* stream) {
+  const std::string w(what);
+  FG_REQUIRE((qkv || part) && seq_len && pos_offset && inv_freq && q_out && k_cache && v_cache, w + ": null pointer");
+  FG_REQUIRE(batch > 0 && num_nodes > 0 && q_heads > 0 && kv_heads > 0, w + ": bad shape");
+  FG_REQUIRE(pos_batch_stride == 0 || pos_batch_stride >= num_nodes, w + ": pos_batch_stride must be 0 or >= num_nodes");
+  FG_REQUIRE(head_dim > 0 && head_dim % 8 == 0 && head_dim <= 256, w + ": head_dim must be a multiple of 8 in [8, 256]");
+  FG_REQUIRE(ld_qkv % 8 == 0 && ((uintptr_t)qkv & 15) == 0 && ((uintptr_t)part & 15) == 0 &&
+                 ((uintptr_t)bias & 15) == 0 && ((uintptr_t)q_out & 15) == 0 && ((uintptr_t)k_cache & 15) == 0 &&
+                 ((uintptr_t)v_cache & 15) == 0 && cache_batch_stride % 8 == 0 && cache_head_stride % 8 == 0,
+             w + ": rows must be 16-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  dim3 grid(batch * num_nodes);
+  if (dtype == fg::kBF16) {
+    const QkvSource<fg::kBF16> src{qkv, part, part_stride, splits, bias};
+    hipLaunchKernelGGL(rope_kv_write_kernel<fg::kBF16>, grid, dim3(256), 0, s, src, ld_qkv, num_nodes, q_heads,
+                       kv_heads, head_dim, seq_len, pos_offset, pos_batch_stride, inv_freq, q_out, k_cache, v_cache,
+                       cache_batch_stride, cache_head_stride, capacity, row_map, err_flag);
+  } else {
+    const QkvSource<fg::kF32> src{qkv, part, part_stride, splits, bias};
+    hipLaunchKernelGGL(rope_kv_write_kernel<fg::kF32>, grid, dim3(256), 0, s, src, ld_qkv, num_nodes, q_heads,
+                       kv_heads, head_dim, seq_len, pos_offset, pos_batch_stride, inv_freq, q_out, k_cache, v_cache,
+                       cache_batch_stride, cache_head_stride, capacity, row_map, err_flag);
+  }
+  return fg::check_launch(what);
+}
+
+}  // namespace
+
+extern "C" {
+
 int fg_rope_kv_write(const void* qkv, int dtype, int64_t ld_qkv, int batch, int num_nodes, int q_heads, int kv_heads,
                      int head_dim, const int32_t* seq_len, const int32_t* pos_offset, int64_t pos_batch_stride,
                      const float* inv_freq, void* q_out, void* k_cache, void* v_cache, int64_t cache_batch_stride,
                      int64_t cache_head_stride, int capacity, const int32_t* row_map, int32_t* err_flag,
                      void* stream) {
-  FG_REQUIRE(qkv && seq_len && pos_offset && inv_freq && q_out && k_cache && v_cache, "fg_rope_kv_write: null pointer");
-  FG_REQUIRE(batch > 0 && num_nodes > 0 && q_heads > 0 && kv_heads > 0, "fg_rope_kv_write: bad shape");
-  FG_REQUIRE(pos_batch_stride == 0 || pos_batch_stride >= num_nodes, "fg_rope_kv_write: pos_batch_stride must be 0 or >= num_nodes");
-  FG_REQUIRE(head_dim > 0 && head_dim % 8 == 0 && head_dim <= 256, "fg_rope_kv_write: head_dim must be a multiple of 8 in [8, 256]");
-  FG_REQUIRE(ld_qkv % 8 == 0 && ((uintptr_t)qkv & 15) == 0 && ((uintptr_t)q_out & 15) == 0 &&
-                 ((uintptr_t)k_cache & 15) == 0 && ((uintptr_t)v_cache & 15) == 0 && cache_batch_stride % 8 == 0 &&
-                 cache_head_stride % 8 == 0,
-             "fg_rope_kv_write: rows must be 16-byte aligned");
-  hipStream_t s = (hipStream_t)stream;
-  dim3 grid(batch * num_nodes);
-  if (dtype == fg::kBF16)
-    hipLaunchKernelGGL(rope_kv_write_kernel<fg::kBF16>, grid, dim3(256), 0, s, qkv, ld_qkv, num_nodes, q_heads,
-                       kv_heads, head_dim, seq_len, pos_offset, pos_batch_stride, inv_freq, q_out, k_cache, v_cache,
-                       cache_batch_stride, cache_head_stride, capacity, row_map, err_flag);
-  else
-    hipLaunchKernelGGL(rope_kv_write_kernel<fg::kF32>, grid, dim3(256), 0, s, qkv, ld_qkv, num_nodes, q_heads,
-                       kv_heads, head_dim, seq_len, pos_offset, pos_batch_stride, inv_freq, q_out, k_cache, v_cache,
-                       cache_batch_stride, cache_head_stride, capacity, row_map, err_flag);
-  return fg::check_launch("fg_rope_kv_write");
+  FG_REQUIRE(qkv, "fg_rope_kv_write: null pointer");
+  return rope_kv_write_launch("fg_rope_kv_write", qkv, nullptr, 0, 1, nullptr, dtype, ld_qkv, batch, num_nodes,
+                              q_heads, kv_heads, head_dim, seq_len, pos_offset, pos_batch_stride, inv_freq, q_out,
+                              k_cache, v_cache, cache_batch_stride, cache_head_stride, capacity, row_map, err_flag,
+                              stream);
+}
+
+int fg_rope_kv_write_parts(const float* part, int splits, const void* bias, int dtype, int batch, int num_nodes,
+                           int q_heads, int kv_heads, int head_dim, const int32_t* seq_len, const int32_t* pos_offset,
+                           int64_t pos_batch_stride, const float* inv_freq, void* q_out, void* k_cache, void* v_cache,
+                           int64_t cache_batch_stride, int64_t cache_head_stride, int capacity,
+                           const int32_t* row_map, int32_t* err_flag, void* stream) {
+  FG_REQUIRE(part && splits >= 1, "fg_rope_kv_write_parts: part must be given with splits >= 1");
+  FG_REQUIRE(batch > 0 && num_nodes > 0 && q_heads > 0 && kv_heads > 0 && head_dim > 0,
+             "fg_rope_kv_write_parts: bad shape");
+  const int64_t width = (int64_t)(q_heads + 2 * kv_heads) * head_dim;
+  return rope_kv_write_launch("fg_rope_kv_write_parts", nullptr, part, (int64_t)batch * num_nodes * width, splits, bias,
+                              dtype, width, batch, num_nodes, q_heads, kv_heads, head_dim, seq_len, pos_offset,
+                              pos_batch_stride, inv_freq, q_out, k_cache, v_cache, cache_batch_stride,
+                              cache_head_stride, capacity, row_map, err_flag, stream);
 }
 
 int fg_rmsnorm(void* x, const void* delta, const void* weight, void* y, int dtype, int rows, int hidden, float eps,

@@ -1,0 +1,361 @@
+// The decoder layer's dense projections (QKV, O, down) as split-K MFMA GEMMs with fp32 partial
+// sums, and the kernels that finish them:
+//
+//   part[s][m, n] = sum over k-steps of split s of x[m, k] * w[n, k]          (fg_linear_parts)
+//   x[m] = bf16(x[m] + bf16(sum_s part[s][m])),  h[m] = RMSNorm(x[m]) * g      (fg_residual_rmsnorm_parts)
+//
+// and, for the QKV projection, the rotary embedding + tree K/V slot write reading the parts
+// (fg_rope_kv_write_parts in layers.hip). The residual add rounds the projection to bf16 and then
+// the sum, as the Hugging Face decoder layer the reference runs under bf16 autocast does
+// (`hidden_states = residual + self.o_proj(...)`, flashgrpo/models/qwen_flashgrpo_wrapper.py:
+// 172-180 runs those layers); the parts are summed in split order, so the result does not depend
+// on the schedule.
+//
+// Why split-K: the verify forward's projections have few rows (Qwen2.5-1.5B: 32 sequences x 13
+// tree nodes = 416) against long reductions (the down projection: K = 8960), so output tiles alone
+// cannot fill 256 CUs; each split takes a contiguous range of k-steps of one output tile.
+//
+// Tiling (gfx950): one workgroup of 4 waves (2 x 2, one wave's (BM/2) x (BN/2) block each) per
+// (output tile, split). K advances 64 per step through a two-stage LDS ring filled by direct
+// HBM->LDS buffer loads (`buffer_load_dwordx4 ... lds`, 1 KB = 8 rows of 128 bytes per instruction),
+// 16-byte chunks XOR-swizzled by row so that the fragment reads of 32 consecutive rows hit distinct
+// banks. Each k-step is four k16 sub-steps of v_mfma_f32_32x32x16_bf16 with the weight rows as the
+// first operand, so each lane ends with 4 consecutive output columns of one row; the fragment reads
+// of sub-step s+1 are interleaved with the MFMAs of sub-step s, and the loads of k-step t+2 are
+// issued between the MFMAs of k-step t's last sub-step, after the step's one barrier.
+// Workgroups are numbered so that each XCD takes a contiguous run of tiles along M for one weight
+// stripe and split: the stripe is read from HBM once per XCD and reused from its L2.
+#include "fg_common.h"
+
+#include <type_traits>
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kBK = 64;          // K per step
+constexpr int kRowBytes = 128;   // one LDS row: kBK bf16
+constexpr int kSub = kBK / 16;   // k16 MFMA sub-steps per step
+
+template <int N>
+FG_DEVICE void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt field is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+FG_DEVICE void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4)); }
+
+struct LinArgs {
+  const uint16_t* x;  // [rows, ldx]
+  int64_t ldx;
+  const uint16_t* w;  // [cols, ldw]
+  int64_t ldw;
+  float* part;        // [splits][rows][cols]
+  int64_t part_stride;
+  int rows, cols;
+  int nks;            // k-steps in total (hidden / 64)
+  int ks_per_split;
+  int tiles_m, tiles_n, tiles, per_xcd;
+};
+
+template <int BM, int BN>
+__global__ void __launch_bounds__(256, 2) linear_parts_kernel(LinArgs p) {
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int FM = WM / 32, FN = WN / 32;  // MFMA tiles per wave: rows x columns
+  constexpr int A_BYTES = BM * kRowBytes, B_BYTES = BN * kRowBytes, STAGE = A_BYTES + B_BYTES;
+  constexpr int LA = BM / 32, LB = BN / 32, LPW = LA + LB;  // 1 KB loads per wave per step
+  static_assert(FM >= 1 && FN >= 1 && LA * 4 * 8 == BM && LB * 4 * 8 == BN, "tile sizes: multiples of 64");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * STAGE];
+
+  // XCD-aware order: workgroup b runs on XCD b % 8; XCD x takes tiles x*per_xcd .. +per_xcd-1,
+  // which walk down M for one (weight stripe, split) before the next.
+  const int xcd = blockIdx.x % 8, j = blockIdx.x / 8;
+  const int tile = xcd * p.per_xcd + j;
+  if (j >= p.per_xcd || tile >= p.tiles) return;  // whole workgroup: before any barrier
+  const int tm = tile % p.tiles_m, rest = tile / p.tiles_m;
+  const int tn = rest % p.tiles_n, split = rest / p.tiles_n;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int ks0 = split * p.ks_per_split;
+  const int nk = min(p.nks - ks0, p.ks_per_split);  // >= 1: the host makes every split non-empty
+  const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, half = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+
+  // Buffer descriptors: rows past the matrix end read as zero (rows >= p.rows, columns >= p.cols).
+  const int64_t x_bytes = (int64_t)(p.rows - m0) * p.ldx * 2;
+  const int64_t w_bytes = (int64_t)(p.cols - n0) * p.ldw * 2;
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.x + (int64_t)m0 * p.ldx), (short)0, (int)(x_bytes < 0x7fffffff ? x_bytes : 0x7fffffff), 0x00020000);
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.w + (int64_t)n0 * p.ldw), (short)0, (int)(w_bytes < 0x7fffffff ? w_bytes : 0x7fffffff), 0x00020000);
+
+  // Load lanes: lane l writes LDS bytes l*16 .. of its 1 KB, i.e. row l/8, stored chunk l%8, which
+  // holds the row's logical chunk (l%8) ^ (row%8). Wave w loads x rows (w*LA + u)*8 .. and weight
+  // rows (w*LB + u)*8 ..
+  const int lrow = lane >> 3;
+  const int lchunk = (lane & 7) ^ (lrow & 7);
+  uint32_t xoff[LA], woff[LB];
+#pragma unroll
+  for (int u = 0; u < LA; ++u) xoff[u] = (uint32_t)(((wave * LA + u) * 8 + lrow) * p.ldx * 2 + lchunk * 16);
+#pragma unroll
+  for (int u = 0; u < LB; ++u) woff[u] = (uint32_t)(((wave * LB + u) * 8 + lrow) * p.ldw * 2 + lchunk * 16);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void*)smem;
+
+  // One 1 KB HBM->LDS load (q < LA: x rows, else weight rows) of k-step ks of this split into ring
+  // slot `slot`. M0 holds the LDS address; the s_nop covers the M0-write -> LDS-DMA hazard.
+  auto issue = [&](int ks, int slot, int q) __attribute__((always_inline)) {
+    const uint32_t koff = (uint32_t)(ks0 + ks) * (kBK * 2);
+    const uint32_t sbase = lds0 + slot * STAGE;
+    if (q < LA) {
+      const uint32_t m0v = sbase + (wave * LA + q) * 1024;
+      asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(xoff[q]), "s"(xrs), "s"(koff),
+                   "{m0}"(m0v)
+                   : "memory");
+    } else {
+      const uint32_t m0v = sbase + A_BYTES + (wave * LB + q - LA) * 1024;
+      asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(woff[q - LA]), "s"(wrs), "s"(koff),
+                   "{m0}"(m0v)
+                   : "memory");
+    }
+  };
+
+  // Fragment reads: lane l of a 32-row MFMA tile reads row l%32, k16 sub-step s, 8-element half
+  // l/32, i.e. logical chunk 2s + l/32, stored at chunk (2s + l/32) ^ (row % 8).
+  uint32_t frag[kSub];
+#pragma unroll
+  for (int s = 0; s < kSub; ++s) frag[s] = (uint32_t)(l32 * kRowBytes + (((2 * s + half) ^ (l32 & 7)) * 16));
+  floatx16 acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int k = 0; k < FM; ++k)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][k][v] = 0.0f;
+  bf16x8 ra[2][FM], rb[2][FN];
+  auto read = [&](int slot, int s, int buf) __attribute__((always_inline)) {
+    const unsigned char* st = smem + slot * STAGE;
+#pragma unroll
+    for (int f = 0; f < FM; ++f) ra[buf][f] = *(const bf16x8*)(st + frag[s] + (wm * WM + f * 32) * kRowBytes);
+#pragma unroll
+    for (int f = 0; f < FN; ++f)
+      rb[buf][f] = *(const bf16x8*)(st + A_BYTES + frag[s] + (wn * WN + f * 32) * kRowBytes);
+  };
+  // One sub-step's MFMAs, the next sub-step's fragment reads placed between them.
+  auto mfma_step = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int k = 0; k < FM; ++k)
+        acc[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rb[buf][i], ra[buf][k], acc[i][k], 0, 0, 0);
+    constexpr int NM = FM * FN, NR = FM + FN, NI = NM < NR ? NM : NR;
+#pragma unroll
+    for (int q = 0; q < NI; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+    }
+    if constexpr (NM > NI) __builtin_amdgcn_sched_group_barrier(0x008, NM - NI, 0);
+    if constexpr (NR > NI) __builtin_amdgcn_sched_group_barrier(0x100, NR - NI, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Prologue: k-steps 0 and 1 in flight, wait for step 0.
+#pragma unroll
+  for (int q = 0; q < LPW; ++q) issue(0, 0, q);
+  if (nk > 1) {
+#pragma unroll
+    for (int q = 0; q < LPW; ++q) issue(1, 1, q);
+    wait_vmcnt<LPW>();
+  } else {
+    wait_vmcnt<0>();
+  }
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  read(0, 0, 0);
+
+  // k-step t in slot t % 2; with_load: also load k-step t + 2 into the slot once it is consumed.
+  auto step = [&](int t, auto with_load) __attribute__((always_inline)) {
+    const int slot = t & 1;
+#pragma unroll
+    for (int s = 0; s < kSub - 1; ++s) {
+      read(slot, s + 1, (s + 1) & 1);
+      mfma_step(s & 1);
+    }
+    wait_lgkmcnt0();   // this wave's reads of the slot are done
+    wait_vmcnt<0>();   // k-step t + 1 (the only loads in flight) has landed for this wave
+    __builtin_amdgcn_s_barrier();  // ... and for every wave, and no wave still reads slot t
+    __builtin_amdgcn_sched_barrier(0);
+    if (t + 1 < nk) read(slot ^ 1, 0, 0);
+    constexpr int kLast = (kSub - 1) & 1;
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int k = 0; k < FM; ++k) {
+        acc[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rb[kLast][i], ra[kLast][k], acc[i][k], 0, 0, 0);
+        if constexpr (decltype(with_load)::value) {
+          if (i * FM + k < LPW) {
+            __builtin_amdgcn_sched_barrier(0);
+            issue(t + 2, slot, i * FM + k);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      }
+    if constexpr (decltype(with_load)::value) {
+#pragma unroll
+      for (int q = FM * FN; q < LPW; ++q) issue(t + 2, slot, q);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  int t = 0;
+  for (; t + 2 < nk; ++t) step(t, std::true_type{});
+  for (; t < nk; ++t) step(t, std::false_type{});
+  wait_vmcnt<0>();  // no load still writing LDS when the workgroup ends
+
+  // Epilogue: acc[i][k] lane l holds output row m0 + wm*WM + k*32 + l%32 and the columns
+  // n0 + wn*WN + i*32 + 8g + 4*(l/32) + 0..3 in elements 4g..4g+3: 16-byte fp32 stores, the two
+  // half-waves of a row writing 32 contiguous bytes.
+  float* dst = p.part + (int64_t)split * p.part_stride;
+#pragma unroll
+  for (int k = 0; k < FM; ++k) {
+    const int m = m0 + wm * WM + k * 32 + l32;
+    if (m >= p.rows) continue;
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + wn * WN + i * 32 + 8 * g + 4 * half;
+        if (n < p.cols)
+          *(float4*)(dst + (int64_t)m * p.cols + n) =
+              make_float4(acc[i][k][4 * g], acc[i][k][4 * g + 1], acc[i][k][4 * g + 2], acc[i][k][4 * g + 3]);
+      }
+  }
+}
+
+template <int BM, int BN>
+void launch(LinArgs p, hipStream_t s) {
+  p.tiles_m = (p.rows + BM - 1) / BM;
+  p.tiles_n = (p.cols + BN - 1) / BN;
+  const int splits = (p.nks + p.ks_per_split - 1) / p.ks_per_split;
+  p.tiles = p.tiles_m * p.tiles_n * splits;
+  p.per_xcd = (p.tiles + 7) / 8;
+  hipLaunchKernelGGL((linear_parts_kernel<BM, BN>), dim3(8 * p.per_xcd), dim3(256), 0, s, p);
+}
+
+// x[r] = bf16(x[r] + bf16(sum_s part[s][r])); h[r] = RMSNorm(x[r]) * g. One workgroup per row,
+// 8 columns per thread and chunk; the row stays in registers between the two passes.
+constexpr int kNormChunks = 4;
+
+__global__ void __launch_bounds__(256) residual_rmsnorm_parts_kernel(const float* __restrict__ part,
+                                                                     int64_t part_stride, int splits,
+                                                                     uint16_t* __restrict__ x, int64_t ldx,
+                                                                     const uint16_t* __restrict__ g,
+                                                                     uint16_t* __restrict__ h, int64_t ldh, int H,
+                                                                     float eps) {
+  const int64_t r = blockIdx.x;
+  const int nch = H / 8;
+  __shared__ float red[4];
+  float v[kNormChunks][8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kNormChunks; ++c) {
+    const int ch = threadIdx.x + c * 256;
+    if (ch < nch) {
+      const float* src = part + r * H + ch * 8;
+      float4 a = *(const float4*)src, b = *(const float4*)(src + 4);
+      for (int s = 1; s < splits; ++s) {  // in split order
+        const float4 a2 = *(const float4*)(src + s * part_stride), b2 = *(const float4*)(src + s * part_stride + 4);
+        a.x += a2.x; a.y += a2.y; a.z += a2.z; a.w += a2.w;
+        b.x += b2.x; b.y += b2.y; b.z += b2.z; b.w += b2.w;
+      }
+      const float y[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      float xv[8];
+      fg::load8<fg::kBF16>(x, r * ldx + ch * 8, xv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[c][e] = fg::round_bf16(xv[e] + fg::round_bf16(y[e]));
+      fg::store8<fg::kBF16>(x, r * ldx + ch * 8, v[c]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += v[c][e] * v[c][e];
+    }
+  }
+  ss = fg::wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float rs = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + eps);
+#pragma unroll
+  for (int c = 0; c < kNormChunks; ++c) {
+    const int ch = threadIdx.x + c * 256;
+    if (ch < nch) {
+      float wv[8], o[8];
+      fg::load8<fg::kBF16>(g, ch * 8, wv);
+      // x * rsqrt(mean x^2 + eps) rounded to bf16, then times the weight (the HF RMSNorm's order)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = wv[e] * fg::round_bf16(v[c][e] * rs);
+      fg::store8<fg::kBF16>(h, r * ldh + ch * 8, o);
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int fg_linear_parts(const void* x, int64_t ldx, const void* w, int64_t ldw, float* part, int rows, int cols,
+                    int hidden, int splits, int tile_m, int tile_n, void* stream) {
+  FG_REQUIRE(x && w && part, "fg_linear_parts: null pointer");
+  FG_REQUIRE(rows > 0 && rows <= (1 << 24) && cols > 0 && cols <= (1 << 24) && hidden > 0,
+             "fg_linear_parts: bad shape");
+  FG_REQUIRE(hidden % kBK == 0, "fg_linear_parts: hidden size must be a multiple of 64");
+  FG_REQUIRE(cols % 4 == 0, "fg_linear_parts: output columns must be a multiple of 4");
+  FG_REQUIRE(ldx >= hidden && ldw >= hidden && ldx < (1 << 22) && ldw < (1 << 22), "fg_linear_parts: bad row strides");
+  FG_REQUIRE(ldx % 8 == 0 && ldw % 8 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0,
+             "fg_linear_parts: x and weight rows must start 16-byte aligned");
+  FG_REQUIRE(((uintptr_t)part & 15) == 0, "fg_linear_parts: part must be 16-byte aligned");
+  const int nks = hidden / kBK;
+  FG_REQUIRE(splits >= 1 && splits <= nks, "fg_linear_parts: splits must be in [1, hidden / 64]");
+  const int per = (nks + splits - 1) / splits;
+  FG_REQUIRE((nks + per - 1) / per == splits,
+             "fg_linear_parts: splits must give every split a k-step (ceil(nk / ceil(nk / splits)) == splits)");
+  FG_REQUIRE((tile_m == 64 || tile_m == 128) && (tile_n == 64 || tile_n == 128),
+             "fg_linear_parts: tile_m and tile_n must be 64 or 128");
+  const int64_t tiles = (int64_t)((rows + tile_m - 1) / tile_m) * ((cols + tile_n - 1) / tile_n) * splits;
+  FG_REQUIRE(tiles < (1 << 30), "fg_linear_parts: too many tiles");
+  LinArgs p{};
+  p.x = (const uint16_t*)x;
+  p.ldx = ldx;
+  p.w = (const uint16_t*)w;
+  p.ldw = ldw;
+  p.part = part;
+  p.part_stride = (int64_t)rows * cols;
+  p.rows = rows;
+  p.cols = cols;
+  p.nks = nks;
+  p.ks_per_split = per;
+  hipStream_t s = (hipStream_t)stream;
+  if (tile_m == 64 && tile_n == 64)
+    launch<64, 64>(p, s);
+  else if (tile_m == 64)
+    launch<64, 128>(p, s);
+  else if (tile_n == 64)
+    launch<128, 64>(p, s);
+  else
+    launch<128, 128>(p, s);
+  return fg::check_launch("fg_linear_parts");
+}
+
+int fg_residual_rmsnorm_parts(const float* part, int splits, int rows, int hidden, void* x, int64_t ldx,
+                              const void* weight, float eps, void* h, int64_t ldh, void* stream) {
+  FG_REQUIRE(part && x && weight && h, "fg_residual_rmsnorm_parts: null pointer");
+  FG_REQUIRE(rows > 0 && splits >= 1 && hidden > 0, "fg_residual_rmsnorm_parts: bad shape");
+  FG_REQUIRE(hidden % 8 == 0 && hidden <= 8 * 256 * kNormChunks,
+             "fg_residual_rmsnorm_parts: hidden must be a multiple of 8, at most 8192");
+  FG_REQUIRE(ldx >= hidden && ldh >= hidden && ldx % 8 == 0 && ldh % 8 == 0,
+             "fg_residual_rmsnorm_parts: row strides must be multiples of 8, at least hidden");
+  FG_REQUIRE((((uintptr_t)part | (uintptr_t)x | (uintptr_t)weight | (uintptr_t)h) & 15) == 0,
+             "fg_residual_rmsnorm_parts: 16-byte alignment");
+  hipLaunchKernelGGL(residual_rmsnorm_parts_kernel, dim3(rows), dim3(256), 0, (hipStream_t)stream, part,
+                     (int64_t)rows * hidden, splits, (uint16_t*)x, ldx, (const uint16_t*)weight, (uint16_t*)h, ldh,
+                     hidden, eps);
+  return fg::check_launch("fg_residual_rmsnorm_parts");
+}
+
+}  // extern "C"

@@ -413,6 +413,108 @@ def gate_up_swiglu(x, w, *, out=None, tile_rows=0):
     return out
 
 
+LINEAR_TILES = (64, 128)
+
+
+def linear_splits(hidden: int, splits: int) -> int:
+    """The largest split count <= ``splits`` that gives every split of ``hidden / 64``
+    k-steps at least one (the rule fg_linear_parts checks)."""
+    nk = hidden // 64
+    s = max(1, min(int(splits), nk))
+    while s > 1 and -(-nk // -(-nk // s)) != s:
+        s -= 1
+    return s
+
+
+def linear_ok(x, w) -> bool:
+    """Whether fg_linear_parts takes x [rows, K] and w [N, K] as they are: bf16 on the GPU,
+    K a multiple of 64, N a multiple of 4, unit column strides and 16-byte aligned rows."""
+    if not (x.is_cuda and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and x.dim() == 2 and w.dim() == 2):
+        return False
+    K_ = x.shape[1]
+    if K_ == 0 or K_ % 64 or w.shape[1] != K_ or w.shape[0] % 4 or x.shape[0] == 0:
+        return False
+    if x.stride(1) != 1 or w.stride(1) != 1 or x.stride(0) % 8 or w.stride(0) % 8:
+        return False
+    return x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0 and x.stride(0) < (1 << 22) and w.stride(0) < (1 << 22)
+
+
+def linear_parts(x, w, *, splits=1, tile=(128, 128), out=None):
+    """Split-K partial products of x [rows, K] . w [N, K]^T (``fg_linear_parts``): fp32
+    [splits, rows, N] whose sum over the first dimension (in order) is the projection.
+    ``splits`` must satisfy the kernel's rule (see ``linear_splits``)."""
+    _dev(x, w)
+    if not linear_ok(x, w):
+        raise ValueError("linear_parts: needs bf16 x [rows, K] and w [N, K] with K % 64 == 0, N % 4 == 0, "
+                         "unit column strides and 16-byte aligned rows")
+    rows, K_ = x.shape
+    N = w.shape[0]
+    tm, tn = (int(t) for t in tile)
+    if tm not in LINEAR_TILES or tn not in LINEAR_TILES:
+        raise ValueError(f"linear_parts: tile sizes must be in {LINEAR_TILES}")
+    if linear_splits(K_, splits) != int(splits):
+        raise ValueError(f"linear_parts: {splits} splits leave a split of {K_ // 64} k-steps empty")
+    shape = (int(splits), rows, N)
+    if out is None:
+        out = torch.empty(shape, dtype=torch.float32, device=x.device)
+    elif out.dtype != torch.float32 or tuple(out.shape) != shape or not out.is_contiguous() or out.data_ptr() % 16:
+        raise ValueError(f"linear_parts: out must be a contiguous 16-byte aligned fp32 {list(shape)} tensor")
+    _call("fg_linear_parts", _ptr(x), x.stride(0), _ptr(w), w.stride(0), _ptr(out), rows, N, K_, int(splits), tm, tn,
+          _stream())
+    return out
+
+
+def residual_rmsnorm_parts(parts, x, weight, eps, *, out=None):
+    """x <- bf16(x + bf16(parts.sum(0))) in place, then RMSNorm(x) * weight
+    (``fg_residual_rmsnorm_parts``): parts fp32 [S, rows, H], x bf16 [rows, H]."""
+    _dev(parts, x, weight)
+    S, rows, H = parts.shape
+    if parts.dtype != torch.float32 or not parts.is_contiguous():
+        raise ValueError("residual_rmsnorm_parts: parts must be contiguous fp32 [S, rows, H]")
+    if x.dtype != torch.bfloat16 or tuple(x.shape) != (rows, H) or x.stride(1) != 1:
+        raise ValueError(f"residual_rmsnorm_parts: x must be bf16 [{rows}, {H}] with unit column stride")
+    if weight.dtype != torch.bfloat16 or weight.numel() != H or not weight.is_contiguous():
+        raise ValueError("residual_rmsnorm_parts: weight must be a contiguous bf16 [H] tensor")
+    if out is None:
+        out = torch.empty(rows, H, dtype=torch.bfloat16, device=x.device)
+    elif out.dtype != torch.bfloat16 or tuple(out.shape) != (rows, H) or out.stride(1) != 1:
+        raise ValueError(f"residual_rmsnorm_parts: out must be bf16 [{rows}, {H}] with unit column stride")
+    _call("fg_residual_rmsnorm_parts", _ptr(parts), S, rows, H, _ptr(x), x.stride(0), _ptr(weight), float(eps),
+          _ptr(out), out.stride(0), _stream())
+    return out
+
+
+def rope_kv_write_parts(parts, bias, *, batch, num_nodes, q_heads, kv_heads, head_dim, seq_len, pos_offset,
+                        inv_freq, q_out, k_cache, v_cache, row_map=None, err_flag=None):
+    """``rope_kv_write`` with the qkv rows given as split-K parts fp32 [S, batch*num_nodes,
+    (q_heads + 2 kv_heads) * head_dim] plus the projection's bias (or None), each value
+    rounded to the cache dtype after the sum (``fg_rope_kv_write_parts``)."""
+    _dev(parts, bias, seq_len, pos_offset, inv_freq, q_out, k_cache, v_cache, row_map)
+    _i32(seq_len, "seq_len")
+    _i32(pos_offset, "pos_offset")
+    _i32(row_map, "row_map")
+    width = (q_heads + 2 * kv_heads) * head_dim
+    if parts.dtype != torch.float32 or not parts.is_contiguous() or tuple(parts.shape[1:]) != (batch * num_nodes,
+                                                                                                width):
+        raise ValueError(f"rope_kv_write_parts: parts must be contiguous fp32 [S, {batch * num_nodes}, {width}]")
+    if bias is not None and (bias.dtype != k_cache.dtype or bias.numel() != width or not bias.is_contiguous()):
+        raise ValueError("rope_kv_write_parts: bias must be a contiguous [width] tensor of the cache dtype")
+    if k_cache.stride(-1) != 1 or k_cache.stride(-2) != head_dim:
+        raise ValueError("rope_kv_write_parts: cache rows must be contiguous [.., capacity, d]")
+    if pos_offset.dim() == 2:
+        if tuple(pos_offset.shape) != (batch, num_nodes) or not pos_offset.is_contiguous():
+            raise ValueError("rope_kv_write_parts: per-sequence pos_offset must be contiguous [batch, num_nodes]")
+        pos_stride = num_nodes
+    else:
+        if pos_offset.numel() < num_nodes:
+            raise ValueError("rope_kv_write_parts: pos_offset shorter than num_nodes")
+        pos_stride = 0
+    _call("fg_rope_kv_write_parts", _ptr(parts), parts.shape[0], _ptr(bias), dtype_code(k_cache), batch, num_nodes,
+          q_heads, kv_heads, head_dim, _ptr(seq_len), _ptr(pos_offset), pos_stride, _ptr(inv_freq), _ptr(q_out),
+          _ptr(k_cache), _ptr(v_cache), k_cache.stride(0), k_cache.stride(1), k_cache.shape[-2], _ptr(row_map),
+          _ptr(err_flag), _stream())
+
+
 # ------------------------------------------------------------------ sampling / acceptance
 def sample_workspace(rows, device):
     """Scratch that lets unrestricted / greedy draws run split over several workgroups per row."""

@@ -10,10 +10,15 @@ Replaces the Hugging Face decoder the reference drives through
   accepted path is compacted in place by ``fg_kv_path_gather``;
 * attention is ``fg_tree_attention`` (ancestor bitmask in registers) for the
   tree verify and for prefill, which runs as causal 64-token chains;
-* RMSNorm, rotary + cache write and SwiGLU are HIP kernels; the dense
-  projections are plain library GEMMs (``F.linear``: hipBLASLt or rocBLAS, with
-  the per-shape solution table of ``flashgrpo_amd.tuning``); the O and down
-  projections add into the residual stream in place (``addmm_``, beta = 1).
+* RMSNorm, rotary + cache write and SwiGLU are HIP kernels. Each dense
+  projection runs, per shape, whichever path the measured tables of
+  ``flashgrpo_amd.tuning`` found faster: the split-K MFMA GEMM
+  (``fg_linear_parts``) whose fp32 parts are finished by the rotary + cache
+  write (QKV) or by the residual add + next RMSNorm (O, down), or the library
+  GEMM (``F.linear``: hipBLASLt or rocBLAS with the per-shape solution table;
+  the O and down projections add into the residual stream in place, ``addmm_``
+  with beta = 1); the MLP input is the fused gate/up + SwiGLU GEMM or the
+  library projection + ``fg_swiglu``.
 """
 from __future__ import annotations
 
@@ -26,7 +31,7 @@ import torch.nn.functional as F
 
 from .. import kernels as K
 from .. import timing
-from ..tuning import mlp_table_path, use_tuned_gemms
+from ..tuning import linear_table_plan, mlp_table_path, use_tuned_gemms
 
 MAX_TREE_NODES = 64      # tree nodes per forward (64-bit ancestor masks)
 MAX_CHAIN_TOKENS = 8192  # new tokens per forward without masks (a causal chain)
@@ -400,6 +405,13 @@ class _ForwardGraph:
 _CUS = {}
 
 
+def _cu_count(device) -> int:
+    key = str(device)
+    if key not in _CUS:
+        _CUS[key] = torch.cuda.get_device_properties(torch.device(device)).multi_processor_count
+    return _CUS[key]
+
+
 def mlp_path(rows: int, inter: int, hidden: int, device) -> int:
     """How a decoder layer computes its MLP input for ``rows`` rows: 0 for the hipBLASLt
     projection + fg_swiglu, else the tile height (192 or 256) of the fused gate/up + SwiGLU GEMM.
@@ -413,12 +425,35 @@ def mlp_path(rows: int, inter: int, hidden: int, device) -> int:
     measured = mlp_table_path(rows, inter, hidden)
     if measured is not None:
         return measured
-    key = str(device)
-    if key not in _CUS:
-        _CUS[key] = torch.cuda.get_device_properties(torch.device(device)).multi_processor_count
     cols = -(-inter // 128)
-    fits = min(-(-rows // bm) * cols for bm in (192, 256)) <= _CUS[key]
+    fits = min(-(-rows // bm) * cols for bm in (192, 256)) <= _cu_count(device)
     return -1 if fits else 0  # -1: fused, the kernel picks the tile height
+
+
+def default_linear_plan(rows: int, cols: int, hidden: int, cus: int = 256) -> tuple:
+    """A split-K plan (tile_m, tile_n, splits) for a shape no measurement covers: 128 x 128
+    tiles when there are at least a quarter as many as CUs, else 64 x 128; then the split count
+    that brings the workgroups nearest to two per CU with at least four k-steps per split."""
+    tm, tn = (128, 128) if -(-rows // 128) * -(-cols // 128) >= cus // 4 else (64, 128)
+    tiles = -(-rows // tm) * -(-cols // tn)
+    nk = hidden // 64
+    best = 1
+    for s in range(1, max(1, nk // 4) + 1):
+        if K.linear_splits(hidden, s) == s and abs(tiles * s - 2 * cus) < abs(tiles * best - 2 * cus):
+            best = s
+    return tm, tn, best
+
+
+def linear_path(kind: str, rows: int, cols: int, hidden: int):
+    """How a decoder layer computes projection ``kind`` ("qkv", "o" or "down") for ``rows``
+    rows: (tile_m, tile_n, splits) of the split-K GEMM, or None for the library projection.
+
+    The measured table (``tuning/linear_mi355x.csv``) decides for the sizes it covers (split-K at
+    the Qwen2.5-1.5B verify rows, where the library's tiles leave most CUs idle; the library at the
+    Qwen2.5-7B ones). Other sizes take the library.
+    """
+    measured = linear_table_plan(kind, rows, cols, hidden)
+    return measured or None
 
 
 class TargetModel:
@@ -441,6 +476,10 @@ class TargetModel:
         # shape (mlp_path), True wherever the operands allow, False never (the hipBLASLt
         # projection, then fg_swiglu); call drop_graphs() after a change
         self.fused_mlp = None
+        # the QKV, O and down projections as split-K GEMMs (fg_linear_parts) finished by the rotary
+        # + cache write or the residual add + RMSNorm: None chooses per shape (linear_path), True
+        # wherever the operands allow (default_linear_plan), False never; drop_graphs() after a change
+        self.split_k_linear = None
         if self.device.type == "cuda":
             use_tuned_gemms()
 
@@ -642,19 +681,38 @@ class TargetModel:
         q, attn = st["q"], st["attn"]
         T = B * N
         H, d = cfg.hidden, cfg.head_dim
+        L = cfg.num_layers
         for l in range(l0, l1):
             lw = self.w["layers"][l]
-            h = K.rmsnorm(x, lw["input_norm"], cfg.rms_eps, out=self._buf("h", (T, H)))
-            qkv = F.linear(h, lw["qkv_w"], lw["qkv_b"])
-            K.rope_kv_write(qkv, batch=B, num_nodes=N, q_heads=cfg.q_heads, kv_heads=cfg.kv_heads, head_dim=d,
-                            seq_len=seq_len, pos_offset=pos_offset, inv_freq=self.inv_freq, q_out=q,
-                            k_cache=cache.k(l), v_cache=cache.v(l), row_map=row_map, err_flag=err_flag)
+            # the input norm, unless the previous layer's down projection finish wrote it
+            h = st.pop("h", None)
+            if h is None:
+                h = K.rmsnorm(x, lw["input_norm"], cfg.rms_eps, out=self._buf("h", (T, H)))
+            plan = self._linear_plan("qkv", h, lw["qkv_w"])
+            if plan:
+                parts = self._linear_parts(h, lw["qkv_w"], plan)
+                K.rope_kv_write_parts(parts, lw["qkv_b"], batch=B, num_nodes=N, q_heads=cfg.q_heads,
+                                      kv_heads=cfg.kv_heads, head_dim=d, seq_len=seq_len, pos_offset=pos_offset,
+                                      inv_freq=self.inv_freq, q_out=q, k_cache=cache.k(l), v_cache=cache.v(l),
+                                      row_map=row_map, err_flag=err_flag)
+            else:
+                qkv = F.linear(h, lw["qkv_w"], lw["qkv_b"])
+                K.rope_kv_write(qkv, batch=B, num_nodes=N, q_heads=cfg.q_heads, kv_heads=cfg.kv_heads, head_dim=d,
+                                seq_len=seq_len, pos_offset=pos_offset, inv_freq=self.inv_freq, q_out=q,
+                                k_cache=cache.k(l), v_cache=cache.v(l), row_map=row_map, err_flag=err_flag)
             K.tree_attention(q, cache.k(l), cache.v(l), seq_len=seq_len, anc=anc, num_nodes=N, q_heads=cfg.q_heads,
                              kv_heads=cfg.kv_heads, head_dim=d, out=attn, row_map=row_map)
-            # residual adds inside the GEMMs (beta = 1, the residual stream updated in place):
-            # the norms then read one tensor instead of two and write one instead of two
-            x.addmm_(attn.view(T, cfg.q_heads * d), lw["o_w"].t())
-            h2 = K.rmsnorm(x, lw["post_norm"], cfg.rms_eps, out=self._buf("h", (T, H)))
+            a2 = attn.view(T, cfg.q_heads * d)
+            plan = self._linear_plan("o", a2, lw["o_w"])
+            if plan:
+                # bf16(x + bf16(o_proj)) and the post-attention norm from the parts
+                h2 = K.residual_rmsnorm_parts(self._linear_parts(a2, lw["o_w"], plan), x, lw["post_norm"],
+                                              cfg.rms_eps, out=self._buf("h", (T, H)))
+            else:
+                # residual adds inside the GEMMs (beta = 1, the residual stream updated in place):
+                # the norms then read one tensor instead of two and write one instead of two
+                x.addmm_(a2, lw["o_w"].t())
+                h2 = K.rmsnorm(x, lw["post_norm"], cfg.rms_eps, out=self._buf("h", (T, H)))
             act = self._buf("act", (T, cfg.intermediate))
             if self.fused_mlp is None:
                 path = mlp_path(T, cfg.intermediate, H, h2.device)
@@ -664,13 +722,41 @@ class TargetModel:
                 K.gate_up_swiglu(h2, lw["gate_up_w"], out=act, tile_rows=max(path, 0))
             else:
                 K.swiglu(F.linear(h2, lw["gate_up_w"]), out=act)
-            x.addmm_(act, lw["down_w"].t())
+            plan = self._linear_plan("down", act, lw["down_w"])
+            if plan:
+                # the residual add and the next norm (the following layer's input norm, or the final
+                # norm into the forward's output) from the parts
+                last = l == L - 1
+                nw = self.w["final_norm"] if last else self.w["layers"][l + 1]["input_norm"]
+                out = (torch.empty(T, H, dtype=self.dtype, device=self.device) if last
+                       else self._buf("h", (T, H)))
+                K.residual_rmsnorm_parts(self._linear_parts(act, lw["down_w"], plan), x, nw, cfg.rms_eps, out=out)
+                st["final" if last else "h"] = out
+            else:
+                x.addmm_(act, lw["down_w"].t())
+
+    def _linear_plan(self, kind: str, x: torch.Tensor, w: torch.Tensor):
+        """(tile_m, tile_n, splits) when projection ``kind`` of x by w runs split-K, else None."""
+        if self.split_k_linear is False or not K.linear_ok(x, w):
+            return None
+        rows, hidden = x.shape
+        if self.split_k_linear:
+            return default_linear_plan(rows, w.shape[0], hidden, _cu_count(x.device))
+        return linear_path(kind, rows, w.shape[0], hidden)
+
+    def _linear_parts(self, x: torch.Tensor, w: torch.Tensor, plan) -> torch.Tensor:
+        tm, tn, s = plan
+        parts = self._buf("parts", (s, x.shape[0], w.shape[0]), torch.float32)
+        return K.linear_parts(x, w, splits=s, tile=(tm, tn), out=parts)
 
     def _forward_end(self, st: dict) -> torch.Tensor:
-        """The final norm: hidden states [B, N, H]."""
+        """The final norm: hidden states [B, N, H] (already written when the last down projection
+        ran split-K)."""
         B, N, H = st["B"], st["N"], self.cfg.hidden
-        out = torch.empty(B * N, H, dtype=self.dtype, device=self.device)
-        K.rmsnorm(st["x"], self.w["final_norm"], self.cfg.rms_eps, out=out)
+        out = st.pop("final", None)
+        if out is None:
+            out = torch.empty(B * N, H, dtype=self.dtype, device=self.device)
+            K.rmsnorm(st["x"], self.w["final_norm"], self.cfg.rms_eps, out=out)
         return out.view(B, N, H)
 
     def walk_parts(self, rows: int, hidden: torch.Tensor):

@@ -16,6 +16,13 @@ measured times of the two ways to compute a decoder layer's MLP input -- the tun
 projection followed by ``fg_swiglu``, or the fused ``fg_gate_up_swiglu`` at either tile
 height -- and the faster one; ``mlp_table_path`` looks it up
 (``FLASHGRPO_AMD_MLP_TABLE=off`` or another path).
+
+``linear_mi355x.csv`` (``make_linear_table.py``) holds, per projection kind (qkv, o, down) and
+(rows, columns, hidden), the measured times of the library projection with the op that follows it
+(``fg_rope_kv_write``; the residual add and ``fg_rmsnorm``) against the split-K
+``fg_linear_parts`` with the kernel that finishes its parts, the best tile and split count of the
+latter, and the faster path; ``linear_table_plan`` looks it up
+(``FLASHGRPO_AMD_LINEAR_TABLE=off`` or another path).
 """
 from __future__ import annotations
 
@@ -23,6 +30,7 @@ import os
 
 DEFAULT_TABLE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "gemm_mi355x.csv")
 DEFAULT_MLP_TABLE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "mlp_mi355x.csv")
+DEFAULT_LINEAR_TABLE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "linear_mi355x.csv")
 _state = {"done": False, "active": False}
 _mlp = {}
 _CHOICE = {"pair": 0, "fused192": 192, "fused256": 256}
@@ -53,6 +61,47 @@ def mlp_table_path(rows: int, inter: int, hidden: int):
     cands = _mlp_entries().get((int(inter), int(hidden)))
     if not cands:
         return None
+    import math
+
+    lr = math.log(max(int(rows), 1))
+    return min(cands, key=lambda e: (abs(math.log(e[0]) - lr), -e[0]))[1]
+
+
+_lin = {}
+
+
+def _linear_entries() -> dict:
+    """(kind, cols, hidden) -> sorted [(rows, plan)] from the projection path table (read once);
+    plan is (tile_m, tile_n, splits) for the split-K kernel or () for the library."""
+    if "entries" not in _lin:
+        entries = {}
+        choice = os.environ.get("FLASHGRPO_AMD_LINEAR_TABLE", "")
+        path = DEFAULT_LINEAR_TABLE if not choice else (None if choice.lower() == "off" else choice)
+        if path and os.path.exists(path):
+            with open(path) as f:
+                header = f.readline().strip().split(",")
+                for line in f:
+                    row = dict(zip(header, line.strip().split(",")))
+                    if row.get("choice") not in ("library", "split_k"):
+                        continue
+                    plan = ((int(row["tile_m"]), int(row["tile_n"]), int(row["splits"]))
+                            if row["choice"] == "split_k" else ())
+                    key = (row["kind"], int(row["cols"]), int(row["hidden"]))
+                    entries.setdefault(key, []).append((int(row["rows"]), plan))
+        _lin["entries"] = {k: sorted(v) for k, v in entries.items()}
+    return _lin["entries"]
+
+
+def linear_table_plan(kind: str, rows: int, cols: int, hidden: int):
+    """The measured projection path for this shape: (tile_m, tile_n, splits) of the split-K kernel,
+    () for the library projection, from the table entry of this kind and these sizes nearest in row
+    count on a log scale (ties to the larger count); None when the table has no such entry. Row
+    counts above twice the largest measured one take the library."""
+    cands = _linear_entries().get((kind, int(cols), int(hidden)))
+    if not cands:
+        return None
+    if int(rows) > 2 * cands[-1][0]:
+        return ()
     import math
 
     lr = math.log(max(int(rows), 1))
