@@ -377,17 +377,22 @@ class _ForwardGraph:
         with torch.cuda.graph(g1, pool=model._graph_pool):
             st = model._forward_begin(inputs["tokens"], cache, **kw)
             model._forward_layers(st, 0, split)
-        g2 = torch.cuda.CUDAGraph(keep_graph=True)
-        with torch.cuda.graph(g2, pool=model._graph_pool):
-            model._forward_layers(st, split, L)
-            out = model._forward_end(st)
-        if _graph_memset_nodes(g1) or _graph_memset_nodes(g2):
+            if split == L:  # no later layer: one graph (the final norm may already be written)
+                out = model._forward_end(st)
+        graphs = [g1]
+        if split < L:
+            g2 = torch.cuda.CUDAGraph(keep_graph=True)
+            with torch.cuda.graph(g2, pool=model._graph_pool):
+                model._forward_layers(st, split, L)
+                out = model._forward_end(st)
+            graphs.append(g2)
+        if any(_graph_memset_nodes(g) for g in graphs):
             return None
-        g1.instantiate()
-        g2.instantiate()
+        for g in graphs:
+            g.instantiate()
         # st["x"] (the residual stream, allocated in the first graph's capture) stays
         # referenced through the second graph, which reads it
-        return cls((g1, g2, st), inputs, out)
+        return cls((*graphs, st), inputs, out)
 
     def run(self, tokens, pos_offset, anc, seq_len, row_map):
         st = self.inputs
@@ -397,8 +402,8 @@ class _ForwardGraph:
         st["seq"].copy_(seq_len)
         if row_map is not None:
             st["row_map"].copy_(row_map)
-        self.graphs[0].replay()
-        self.graphs[1].replay()
+        for g in self.graphs[:-1]:  # the last entry is the capture's forward state
+            g.replay()
         return self.out
 
 

@@ -1,7 +1,7 @@
 """Regenerate the projection-path table (run on the MI355X it is meant for).
 
-    python -m flashgrpo_amd.tuning.make_linear_table --out linear_mi355x.csv [--reps 20]
-        [--presets qwen25_1p5b,...] [--rows 416,...]
+    python -m flashgrpo_amd.tuning.make_linear_table --out linear_mi355x.csv
+        [--presets qwen25_1p5b,...] [--rows 416,...] [--reps 10]
 
 For the QKV, O and down projections of every bf16 target preset and a grid of row counts
 (powers of two plus the verify-round shapes of the benchmark workloads), it times the two ways
@@ -14,9 +14,13 @@ a decoder layer can compute the projection together with the op that consumes it
   (``fg_rope_kv_write_parts``, ``fg_residual_rmsnorm_parts``), over tile sizes and split counts
   that put between 64 and 1024 workgroups on the chip.
 
-Each time is the minimum over ``reps`` launches with the weight rotating over enough copies to
-exceed the 256 MB last-level cache (so it is read from HBM, as in a forward over all layers).
-One row per shape names the faster path and the best split-K tile and split count.
+The verify forward replays its launches as a HIP graph, so each path is timed the same way: one
+graph holding ``batch`` back-to-back calls, the weight rotating over enough copies to exceed the
+256 MB last-level cache (so it is read from HBM, as in a forward over all layers), replayed
+``reps`` times between events; a call's time is the fastest replay divided by ``batch``. (Events
+around single eager launches add the launch gaps, which would favour whichever path has the
+shorter kernels at small shapes.) One row per shape names the faster path and the best split-K
+tile and split count.
 """
 from __future__ import annotations
 
@@ -54,7 +58,7 @@ def split_candidates(K, rows, cols, hidden):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--out", required=True)
-    ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--reps", type=int, default=10)
     ap.add_argument("--presets", default="", help="comma-separated preset names (default: all)")
     ap.add_argument("--rows", default="", help="comma-separated row counts (default: the full grid)")
     args = ap.parse_args()
@@ -71,17 +75,23 @@ def main():
     use_tuned_gemms()
     dev = "cuda"
 
-    def best(fn):
-        for _ in range(3):
-            fn()
+    def best(fn, batch):
+        fn()  # eager first: library handles, workspaces and the TunableOp lookup outside the graph
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(batch):
+                fn()
+        g.replay()
         ts = []
         for _ in range(args.reps):
             s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             s.record()
-            fn()
+            g.replay()
             e.record()
             e.synchronize()
-            ts.append(s.elapsed_time(e) * 1e3)
+            ts.append(s.elapsed_time(e) * 1e3 / batch)
+        del g
         return min(ts)
 
     lines = ["kind,rows,cols,hidden,library_us,split_k_us,tile_m,tile_n,splits,choice"]
@@ -95,6 +105,7 @@ def main():
         for kind, N, Kd in kinds:
             g = torch.Generator(device=dev).manual_seed(N + Kd)
             copies = min(32, max(2, -(-512 * 2 ** 20 // (N * Kd * 2))))
+            batch = max(copies, 8)
             ws = [(torch.randn(N, Kd, device=dev, generator=g) * 0.02).to(torch.bfloat16) for _ in range(copies)]
             bias = (torch.randn(N, device=dev, generator=g) * 0.02).to(torch.bfloat16) if cfg.qkv_bias else None
             norm_w = torch.ones(H, dtype=torch.bfloat16, device=dev)
@@ -138,11 +149,11 @@ def main():
                                                      res, norm_w, cfg.rms_eps, out=h)
                         return run
 
-                t_lib = best(library)
+                t_lib = best(library, batch)
                 top = None
                 for tm, tn, s in split_candidates(K, rows, N, Kd):
                     buf = torch.empty(s, rows, N, dtype=torch.float32, device=dev)
-                    t = best(split_k(tm, tn, s, buf))
+                    t = best(split_k(tm, tn, s, buf), batch)
                     del buf
                     if top is None or t < top[0]:
                         top = (t, tm, tn, s)
