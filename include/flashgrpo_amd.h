@@ -167,7 +167,7 @@ int fg_swiglu(const void* gate_up, void* out, int dtype, int rows, int inter, vo
  * projection (w = [gate; up], [2*inter, hidden] bf16, rows `ldw` apart) with SwiGLU in its
  * epilogue; bf16 x [rows, hidden] (row stride ldx) and out [rows, inter] (row stride ldo).
  * hidden % 64 == 0, inter % 4 == 0; x and w rows 16-byte aligned, out rows 8-byte aligned.
- * tile_rows: 0 (chosen from the shape), 192 or 256 rows per workgroup tile. */
+ * tile_rows: 0 (chosen from the shape), 64, 128, 192 or 256 rows per workgroup tile. */
 int fg_gate_up_swiglu(const void* x, int64_t ldx, const void* w_gate_up, int64_t ldw, void* out, int64_t ldo, int rows,
                       int inter, int hidden, int tile_rows, void* stream);
 
@@ -177,9 +177,10 @@ int fg_gate_up_swiglu(const void* x, int64_t ldx, const void* w_gate_up, int64_t
  * reference's tree verify runs: models/qwen_flashgrpo_wrapper.py:172-180. hidden % 64 == 0,
  * cols % 4 == 0, 16-byte aligned rows; splits in [1, hidden/64] with
  * ceil(nk / ceil(nk / splits)) == splits (nk = hidden / 64), so that every split has k-steps;
- * tile_m, tile_n: 64 or 128 output rows / columns per workgroup. */
+ * tile_m, tile_n: 64 or 128 output rows / columns per workgroup; stages: 2, 3 or 4 k-steps of
+ * 64 in the LDS ring (stages - 1 of them loading while one is computed), 0 for 4. */
 int fg_linear_parts(const void* x, int64_t ldx, const void* w, int64_t ldw, float* part, int rows, int cols,
-                    int hidden, int splits, int tile_m, int tile_n, void* stream);
+                    int hidden, int splits, int tile_m, int tile_n, int stages, void* stream);
 
 /* The residual add and the following RMSNorm of an O or down projection given as split-K parts
  * [splits, rows, hidden]: x[r] = bf16(x[r] + bf16(sum_s part[s][r])) in place (bf16 x, row stride

@@ -16,18 +16,21 @@
 // cannot fill 256 CUs; each split takes a contiguous range of k-steps of one output tile.
 //
 // Tiling (gfx950): one workgroup of 4 waves (2 x 2, one wave's (BM/2) x (BN/2) block each) per
-// (output tile, split). K advances 64 per step through a two-stage LDS ring filled by direct
+// (output tile, split). K advances 64 per step through an NS-stage LDS ring filled by direct
 // HBM->LDS buffer loads (`buffer_load_dwordx4 ... lds`, 1 KB = 8 rows of 128 bytes per instruction),
 // 16-byte chunks XOR-swizzled by row so that the fragment reads of 32 consecutive rows hit distinct
 // banks. Each k-step is four k16 sub-steps of v_mfma_f32_32x32x16_bf16 with the weight rows as the
 // first operand, so each lane ends with 4 consecutive output columns of one row; the fragment reads
-// of sub-step s+1 are interleaved with the MFMAs of sub-step s, and the loads of k-step t+2 are
-// issued between the MFMAs of k-step t's last sub-step, after the step's one barrier.
+// of sub-step s+1 are interleaved with the MFMAs of sub-step s, and the loads of k-step t+NS are
+// issued between the MFMAs of k-step t's last sub-step, after the step's one barrier, so NS - 1
+// k-steps of loads are in flight while one is computed. At the verify forward's row counts every
+// workgroup is resident at once and runs a chain of K / (64 splits) steps, so the time per step
+// is the load latency divided by the steps in flight, not the MFMA work: more stages, not more
+// workgroups, shorten it.
 // Workgroups are numbered so that each XCD takes a contiguous run of tiles along M for one weight
 // stripe and split: the stripe is read from HBM once per XCD and reused from its L2.
 #include "fg_common.h"
 
-#include <type_traits>
 
 namespace {
 
@@ -59,14 +62,16 @@ struct LinArgs {
   int tiles_m, tiles_n, tiles, per_xcd;
 };
 
-template <int BM, int BN>
-__global__ void __launch_bounds__(256, 2) linear_parts_kernel(LinArgs p) {
+template <int BM, int BN, int NS>
+__global__ void __launch_bounds__(256, NS * (BM + BN) * kRowBytes <= 80 * 1024 ? 2 : 1)
+    linear_parts_kernel(LinArgs p) {
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int FM = WM / 32, FN = WN / 32;  // MFMA tiles per wave: rows x columns
   constexpr int A_BYTES = BM * kRowBytes, B_BYTES = BN * kRowBytes, STAGE = A_BYTES + B_BYTES;
   constexpr int LA = BM / 32, LB = BN / 32, LPW = LA + LB;  // 1 KB loads per wave per step
   static_assert(FM >= 1 && FN >= 1 && LA * 4 * 8 == BM && LB * 4 * 8 == BN, "tile sizes: multiples of 64");
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * STAGE];
+  static_assert(NS >= 2 && NS * STAGE <= 160 * 1024 && (NS - 1) * LPW < 64, "ring stages: LDS and vmcnt");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * STAGE];
 
   // XCD-aware order: workgroup b runs on XCD b % 8; XCD x takes tiles x*per_xcd .. +per_xcd-1,
   // which walk down M for one (weight stripe, split) before the next.
@@ -159,56 +164,50 @@ __global__ void __launch_bounds__(256, 2) linear_parts_kernel(LinArgs p) {
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // Prologue: k-steps 0 and 1 in flight, wait for step 0.
+  // Prologue: k-steps 0 .. NS-1 in flight, wait for step 0. A k-step past the split's last one
+  // loads the last one again (L2-resident, into a slot never read), so every wait below waits
+  // for a fixed count.
+  const int last = nk - 1;
 #pragma unroll
-  for (int q = 0; q < LPW; ++q) issue(0, 0, q);
-  if (nk > 1) {
+  for (int h = 0; h < NS; ++h)
 #pragma unroll
-    for (int q = 0; q < LPW; ++q) issue(1, 1, q);
-    wait_vmcnt<LPW>();
-  } else {
-    wait_vmcnt<0>();
-  }
+    for (int q = 0; q < LPW; ++q) issue(min(h, last), h, q);
+  wait_vmcnt<(NS - 1) * LPW>();
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
   read(0, 0, 0);
 
-  // k-step t in slot t % 2; with_load: also load k-step t + 2 into the slot once it is consumed.
-  auto step = [&](int t, auto with_load) __attribute__((always_inline)) {
-    const int slot = t & 1;
+  // k-step t in slot t % NS, which takes k-step t + NS once consumed.
+  auto step = [&](int t) __attribute__((always_inline)) {
+    const int slot = t % NS;
 #pragma unroll
     for (int s = 0; s < kSub - 1; ++s) {
       read(slot, s + 1, (s + 1) & 1);
       mfma_step(s & 1);
     }
-    wait_lgkmcnt0();   // this wave's reads of the slot are done
-    wait_vmcnt<0>();   // k-step t + 1 (the only loads in flight) has landed for this wave
-    __builtin_amdgcn_s_barrier();  // ... and for every wave, and no wave still reads slot t
+    wait_lgkmcnt0();              // this wave's reads of the slot are done
+    wait_vmcnt<(NS - 2) * LPW>(); // k-step t + 1 has landed for this wave (t + 2 .. t + NS - 1 may not)
+    __builtin_amdgcn_s_barrier(); // ... and for every wave, and no wave still reads slot t
     __builtin_amdgcn_sched_barrier(0);
-    if (t + 1 < nk) read(slot ^ 1, 0, 0);
+    if (t + 1 < nk) read((t + 1) % NS, 0, 0);
+    const int next = min(t + NS, last);
     constexpr int kLast = (kSub - 1) & 1;
 #pragma unroll
     for (int i = 0; i < FN; ++i)
 #pragma unroll
       for (int k = 0; k < FM; ++k) {
         acc[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rb[kLast][i], ra[kLast][k], acc[i][k], 0, 0, 0);
-        if constexpr (decltype(with_load)::value) {
-          if (i * FM + k < LPW) {
-            __builtin_amdgcn_sched_barrier(0);
-            issue(t + 2, slot, i * FM + k);
-            __builtin_amdgcn_sched_barrier(0);
-          }
+        if (i * FM + k < LPW) {
+          __builtin_amdgcn_sched_barrier(0);
+          issue(next, slot, i * FM + k);
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
-    if constexpr (decltype(with_load)::value) {
 #pragma unroll
-      for (int q = FM * FN; q < LPW; ++q) issue(t + 2, slot, q);
-    }
+    for (int q = FM * FN; q < LPW; ++q) issue(next, slot, q);
     __builtin_amdgcn_sched_barrier(0);
   };
-  int t = 0;
-  for (; t + 2 < nk; ++t) step(t, std::true_type{});
-  for (; t < nk; ++t) step(t, std::false_type{});
+  for (int t = 0; t < nk; ++t) step(t);
   wait_vmcnt<0>();  // no load still writing LDS when the workgroup ends
 
   // Epilogue: acc[i][k] lane l holds output row m0 + wm*WM + k*32 + l%32 and the columns
@@ -231,14 +230,21 @@ __global__ void __launch_bounds__(256, 2) linear_parts_kernel(LinArgs p) {
   }
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int NS>
 void launch(LinArgs p, hipStream_t s) {
   p.tiles_m = (p.rows + BM - 1) / BM;
   p.tiles_n = (p.cols + BN - 1) / BN;
   const int splits = (p.nks + p.ks_per_split - 1) / p.ks_per_split;
   p.tiles = p.tiles_m * p.tiles_n * splits;
   p.per_xcd = (p.tiles + 7) / 8;
-  hipLaunchKernelGGL((linear_parts_kernel<BM, BN>), dim3(8 * p.per_xcd), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((linear_parts_kernel<BM, BN, NS>), dim3(8 * p.per_xcd), dim3(256), 0, s, p);
+}
+
+template <int BM, int BN>
+void launch_stages(LinArgs p, int stages, hipStream_t s) {
+  if (stages == 2) launch<BM, BN, 2>(p, s);
+  else if (stages == 3) launch<BM, BN, 3>(p, s);
+  else launch<BM, BN, 4>(p, s);
 }
 
 // x[r] = bf16(x[r] + bf16(sum_s part[s][r])); h[r] = RMSNorm(x[r]) * g. One workgroup per row,
@@ -300,7 +306,7 @@ __global__ void __launch_bounds__(256) residual_rmsnorm_parts_kernel(const float
 extern "C" {
 
 int fg_linear_parts(const void* x, int64_t ldx, const void* w, int64_t ldw, float* part, int rows, int cols,
-                    int hidden, int splits, int tile_m, int tile_n, void* stream) {
+                    int hidden, int splits, int tile_m, int tile_n, int stages, void* stream) {
   FG_REQUIRE(x && w && part, "fg_linear_parts: null pointer");
   FG_REQUIRE(rows > 0 && rows <= (1 << 24) && cols > 0 && cols <= (1 << 24) && hidden > 0,
              "fg_linear_parts: bad shape");
@@ -317,6 +323,7 @@ int fg_linear_parts(const void* x, int64_t ldx, const void* w, int64_t ldw, floa
              "fg_linear_parts: splits must give every split a k-step (ceil(nk / ceil(nk / splits)) == splits)");
   FG_REQUIRE((tile_m == 64 || tile_m == 128) && (tile_n == 64 || tile_n == 128),
              "fg_linear_parts: tile_m and tile_n must be 64 or 128");
+  FG_REQUIRE(stages == 0 || (stages >= 2 && stages <= 4), "fg_linear_parts: stages must be 0 (4), 2, 3 or 4");
   const int64_t tiles = (int64_t)((rows + tile_m - 1) / tile_m) * ((cols + tile_n - 1) / tile_n) * splits;
   FG_REQUIRE(tiles < (1 << 30), "fg_linear_parts: too many tiles");
   LinArgs p{};
@@ -331,14 +338,15 @@ int fg_linear_parts(const void* x, int64_t ldx, const void* w, int64_t ldw, floa
   p.nks = nks;
   p.ks_per_split = per;
   hipStream_t s = (hipStream_t)stream;
+  const int ns = stages ? stages : 4;
   if (tile_m == 64 && tile_n == 64)
-    launch<64, 64>(p, s);
+    launch_stages<64, 64>(p, ns, s);
   else if (tile_m == 64)
-    launch<64, 128>(p, s);
+    launch_stages<64, 128>(p, ns, s);
   else if (tile_n == 64)
-    launch<128, 64>(p, s);
+    launch_stages<128, 64>(p, ns, s);
   else
-    launch<128, 128>(p, s);
+    launch_stages<128, 128>(p, ns, s);
   return fg::check_launch("fg_linear_parts");
 }
 

@@ -13,22 +13,25 @@
 // 172-180 runs the HF decoder layers).
 //
 // Tiling (gfx950): one workgroup of 4 waves (2 x 2, one per SIMD) per output tile of BM rows x 128
-// intermediate columns. The tile's 256 weight rows sit in LDS as [gate 64 | up 64 | gate 64 | up 64],
+// intermediate columns (BM = 64, 128, 192 or 256). The tile's 256 weight rows sit in LDS as [gate 64 | up 64 | gate 64 | up 64],
 // so the wave that owns output columns c .. c+63 holds both the gate and the up accumulators of
-// those columns and applies the activation in registers. K advances 64 per step through a two-stage
-// LDS ring filled by direct HBM->LDS buffer loads (`buffer_load_dwordx4 ... lds`, 1 KB = 8 rows
+// those columns and applies the activation in registers. K advances 64 per step through an NS-stage
+// LDS ring (the deepest that fits 160 KB: 4 stages for 64-row tiles, 3 for 128, 2 for 192 and
+// 256) filled by direct HBM->LDS buffer loads (`buffer_load_dwordx4 ... lds`, 1 KB = 8 rows
 // per instruction), rows of 128 bytes with the 16-byte chunks XOR-swizzled by row so that the
 // fragment reads of 32 consecutive rows hit distinct banks. Each k-step is four k16 sub-steps of
 // v_mfma_f32_32x32x16_bf16 (the wave's (BM/2) x 128 block is (BM/64) x 4 MFMA tiles, computed
 // transposed so each lane ends with 4 consecutive output columns of one row); the fragment reads
-// of sub-step s+1 are interleaved with the MFMAs of sub-step s, and the loads of k-step t+2 are
-// issued between the MFMAs of k-step t's last sub-step, after the one barrier of the step. The
+// of sub-step s+1 are interleaved with the MFMAs of sub-step s, and the loads of k-step t+NS are
+// issued between the MFMAs of k-step t's last sub-step, after the one barrier of the step. When
+// every workgroup is resident at once (few rows), each runs a chain of hidden/64 steps whose time
+// per step is the load latency over the NS - 1 steps in flight: the shallow-tile, deep-ring
+// variants are for those shapes. The
 // output block of each wave goes out through LDS as whole 128-byte row segments.
 // Workgroups are numbered so that each XCD takes a contiguous run of tiles along M for one weight
 // stripe: the stripe is read from HBM once per XCD and reused from its L2.
 #include "fg_common.h"
 
-#include <type_traits>
 
 namespace {
 
@@ -62,15 +65,19 @@ struct MlpArgs {
   int tiles_m, tiles, per_xcd;
 };
 
+constexpr int stages_for(int bm) { return (int)((160 * 1024) / ((bm + kBN) * kRowBytes)) < 4 ? (int)((160 * 1024) / ((bm + kBN) * kRowBytes)) : 4; }
+
 template <int BM>
 __global__ void __launch_bounds__(256, 1) gate_up_swiglu_kernel(MlpArgs p) {
+  constexpr int NS = stages_for(BM);
   constexpr int WM = BM / 2;                       // rows per wave
   constexpr int FM = WM / 32, FN = 4;              // MFMA tiles per wave: rows x (2 gate + 2 up)
   constexpr int A_BYTES = BM * kRowBytes, B_BYTES = kBN * kRowBytes, STAGE = A_BYTES + B_BYTES;
   constexpr int LA = A_BYTES / 4096, LB = B_BYTES / 4096, LPW = LA + LB;  // 1 KB loads per wave per step
   static_assert(LA * 4096 == A_BYTES && LB == 8, "each wave loads BM/4 x-rows and one 64-row weight block");
   static_assert(FM * FN <= LPW, "the loads of a step are spread over the last sub-step's MFMAs");
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * STAGE];
+  static_assert(NS >= 2 && NS * STAGE <= 160 * 1024 && (NS - 1) * LPW < 64, "ring stages: LDS and vmcnt");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * STAGE];
 
   // XCD-aware tile order: workgroup b runs on XCD b % 8; XCD x takes tiles x*per_xcd .. +per_xcd-1,
   // which walk down M for one weight stripe before the next stripe.
@@ -159,58 +166,56 @@ __global__ void __launch_bounds__(256, 1) gate_up_swiglu_kernel(MlpArgs p) {
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // Prologue: k-steps 0 and 1 in flight, wait for step 0.
+  // Prologue: k-steps 0 .. NS-1 in flight, wait for step 0. A k-step past the last one loads the
+  // last one again (L2-resident, into a slot never read), so every wait below waits for a fixed
+  // count.
+  const int last = nk - 1;
 #pragma unroll
-  for (int q = 0; q < LPW; ++q) issue(0, 0, q);
-  if (nk > 1) {
+  for (int h = 0; h < NS; ++h)
 #pragma unroll
-    for (int q = 0; q < LPW; ++q) issue(1, 1, q);
-    wait_vmcnt<LPW>();
-  } else {
-    wait_vmcnt<0>();
-  }
+    for (int q = 0; q < LPW; ++q) issue(min(h, last), h, q);
+  wait_vmcnt<(NS - 1) * LPW>();
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
   read(0, 0, 0);
 
-  // k-step t in slot t % 2; with_load: also load k-step t + 2 into the slot once it is consumed.
-  auto step = [&](int t, auto with_load) __attribute__((always_inline)) {
-    const int slot = t & 1;
+  // k-step t in slot t % NS, which takes k-step t + NS once consumed.
+  auto step = [&](int t) __attribute__((always_inline)) {
+    const int slot = t % NS;
 #pragma unroll
     for (int s = 0; s < kSub - 1; ++s) {
       read(slot, s + 1, (s + 1) & 1);
       mfma_step(s & 1);
     }
-    wait_lgkmcnt0();   // this wave's reads of the slot are done
-    wait_vmcnt<0>();   // k-step t + 1 (the only loads in flight) has landed for this wave
-    __builtin_amdgcn_s_barrier();  // ... and for every wave, and no wave still reads slot t
+    wait_lgkmcnt0();              // this wave's reads of the slot are done
+    wait_vmcnt<(NS - 2) * LPW>(); // k-step t + 1 has landed for this wave (t + 2 .. t + NS - 1 may not)
+    __builtin_amdgcn_s_barrier(); // ... and for every wave, and no wave still reads slot t
     __builtin_amdgcn_sched_barrier(0);
-    if (t + 1 < nk) read(slot ^ 1, 0, 0);
+    if (t + 1 < nk) read((t + 1) % NS, 0, 0);
+    const int next = min(t + NS, last);
     constexpr int kLast = (kSub - 1) & 1;
 #pragma unroll
     for (int i = 0; i < FN; ++i)
 #pragma unroll
       for (int k = 0; k < FM; ++k) {
         acc[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rb[kLast][i], ra[kLast][k], acc[i][k], 0, 0, 0);
-        if constexpr (decltype(with_load)::value) {
-          __builtin_amdgcn_sched_barrier(0);
-          issue(t + 2, slot, i * FM + k);
-          __builtin_amdgcn_sched_barrier(0);
-        }
+        __builtin_amdgcn_sched_barrier(0);
+        issue(next, slot, i * FM + k);
+        __builtin_amdgcn_sched_barrier(0);
       }
-    if constexpr (decltype(with_load)::value) {
 #pragma unroll
-      for (int q = FM * FN; q < LPW; ++q) issue(t + 2, slot, q);
-    }
+    for (int q = FM * FN; q < LPW; ++q) issue(next, slot, q);
     __builtin_amdgcn_sched_barrier(0);
   };
-  int t = 0;
-  for (; t + 2 < nk; ++t) step(t, std::true_type{});
-  for (; t < nk; ++t) step(t, std::false_type{});
-  wait_vmcnt<0>();  // no load still writing LDS when the workgroup ends
+  for (int t = 0; t < nk; ++t) step(t);
+  // The last steps' loads (repeats of the last k-step) may still be writing the ring: every wave
+  // waits for its own, then the barrier makes the ring free for the epilogue's staging.
+  wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
 
   // Epilogue: acc[i] (gate) and acc[i + 2] (up) hold the same 4 output columns of one row per lane
-  // (32 rows per store instruction). After the last barrier no wave reads the ring and no load is in
+  // (32 rows per store instruction). After the barrier above no wave reads the ring and no load is in
   // flight, so each wave stages its own (BM/2) x 64 bf16 block in LDS (rows of 128 bytes, 16-byte
   // chunk q of row r stored at chunk q ^ (r % 8)) and writes it back as whole 128-byte row segments.
   unsigned char* stage = smem + wave * (WM * 128);
@@ -255,8 +260,9 @@ void launch(MlpArgs p, hipStream_t s) {
   hipLaunchKernelGGL(gate_up_swiglu_kernel<BM>, dim3(8 * p.per_xcd), dim3(256), 0, s, p);
 }
 
-// Tile height: the one with the fewer MFMA row-blocks over whole waves of 256 concurrent tiles
-// (one per CU); ties go to 256 rows (more MFMAs per LDS byte).
+// Tile height when the caller leaves it open: of 192 and 256, the one with the fewer MFMA
+// row-blocks over whole waves of 256 concurrent tiles (one per CU); ties go to 256 rows (more
+// MFMAs per LDS byte). The 64- and 128-row tiles are taken when a caller's measurement asks.
 int pick_tile_rows(int rows, int inter) {
   const int64_t cols = (inter + kCols - 1) / kCols;
   auto cost = [&](int bm) { return ((((rows + bm - 1) / bm) * cols + 255) / 256) * bm; };
@@ -278,8 +284,9 @@ int fg_gate_up_swiglu(const void* x, int64_t ldx, const void* w_gate_up, int64_t
   FG_REQUIRE(ldx % 8 == 0 && ldw % 8 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w_gate_up & 15) == 0,
              "fg_gate_up_swiglu: x and weight rows must start 16-byte aligned");
   FG_REQUIRE(ldo % 4 == 0 && ((uintptr_t)out & 7) == 0, "fg_gate_up_swiglu: out rows must start 8-byte aligned");
-  FG_REQUIRE(tile_rows == 0 || tile_rows == 192 || tile_rows == 256, "fg_gate_up_swiglu: tile_rows must be 0, 192 or 256");
-  FG_REQUIRE((int64_t)((rows + 191) / 192) * ((inter + kCols - 1) / kCols) < (1 << 30), "fg_gate_up_swiglu: too many tiles");
+  FG_REQUIRE(tile_rows == 0 || tile_rows == 64 || tile_rows == 128 || tile_rows == 192 || tile_rows == 256,
+             "fg_gate_up_swiglu: tile_rows must be 0, 64, 128, 192 or 256");
+  FG_REQUIRE((int64_t)((rows + 63) / 64) * ((inter + kCols - 1) / kCols) < (1 << 30), "fg_gate_up_swiglu: too many tiles");
   MlpArgs p{};
   p.x = (const uint16_t*)x;
   p.ldx = ldx;
@@ -292,10 +299,12 @@ int fg_gate_up_swiglu(const void* x, int64_t ldx, const void* w_gate_up, int64_t
   p.hidden = hidden;
   p.vec16 = ldo % 8 == 0 && ((uintptr_t)out & 15) == 0;
   hipStream_t s = (hipStream_t)stream;
-  if ((tile_rows ? tile_rows : pick_tile_rows(rows, inter)) == 192)
-    launch<192>(p, s);
-  else
-    launch<256>(p, s);
+  switch (tile_rows ? tile_rows : pick_tile_rows(rows, inter)) {
+    case 64: launch<64>(p, s); break;
+    case 128: launch<128>(p, s); break;
+    case 192: launch<192>(p, s); break;
+    default: launch<256>(p, s); break;
+  }
   return fg::check_launch("fg_gate_up_swiglu");
 }
 

@@ -45,7 +45,7 @@ SIGNATURES = {
     "fg_swiglu": (_I, [_P, _P, _I, _I, _I, _P]),
     "fg_chain_cell_norm": (_I, [_P, _I64, _P, _I64, _I, _I, _I, _P, _P, _P, _P, _F, _P, _P]),
     "fg_gate_up_swiglu": (_I, [_P, _I64, _P, _I64, _P, _I64, _I, _I, _I, _I, _P]),
-    "fg_linear_parts": (_I, [_P, _I64, _P, _I64, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "fg_linear_parts": (_I, [_P, _I64, _P, _I64, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "fg_residual_rmsnorm_parts": (_I, [_P, _I, _I, _I, _P, _I64, _P, _F, _P, _I64, _P]),
     "fg_rope_kv_write_parts": (_I, [_P, _I, _P, _I, _I, _I, _I, _I, _I, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I,
                                     _P, _P, _P]),

@@ -397,7 +397,7 @@ def gate_up_swiglu_ok(x, w) -> bool:
 def gate_up_swiglu(x, w, *, out=None, tile_rows=0):
     """SiLU(x . w[:I]^T) * (x . w[I:]^T) with both projections rounded to bf16 first, as one GEMM
     (``fg_gate_up_swiglu``): x [rows, H] bf16, w [2I, H] bf16 (gate rows, then up rows) ->
-    [rows, I] bf16."""
+    [rows, I] bf16. tile_rows: 0 (the kernel's choice of 192 / 256), 64, 128, 192 or 256."""
     _dev(x, w)
     if not gate_up_swiglu_ok(x, w):
         raise ValueError("gate_up_swiglu: needs bf16 x [rows, H] and w [2I, H] with H % 64 == 0, I % 4 == 0, "
@@ -439,10 +439,11 @@ def linear_ok(x, w) -> bool:
     return x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0 and x.stride(0) < (1 << 22) and w.stride(0) < (1 << 22)
 
 
-def linear_parts(x, w, *, splits=1, tile=(128, 128), out=None):
+def linear_parts(x, w, *, splits=1, tile=(128, 128), stages=0, out=None):
     """Split-K partial products of x [rows, K] . w [N, K]^T (``fg_linear_parts``): fp32
     [splits, rows, N] whose sum over the first dimension (in order) is the projection.
-    ``splits`` must satisfy the kernel's rule (see ``linear_splits``)."""
+    ``splits`` must satisfy the kernel's rule (see ``linear_splits``); ``stages``: k-steps in
+    the kernel's LDS ring (2-4, 0 for 4)."""
     _dev(x, w)
     if not linear_ok(x, w):
         raise ValueError("linear_parts: needs bf16 x [rows, K] and w [N, K] with K % 64 == 0, N % 4 == 0, "
@@ -452,6 +453,8 @@ def linear_parts(x, w, *, splits=1, tile=(128, 128), out=None):
     tm, tn = (int(t) for t in tile)
     if tm not in LINEAR_TILES or tn not in LINEAR_TILES:
         raise ValueError(f"linear_parts: tile sizes must be in {LINEAR_TILES}")
+    if int(stages) not in (0, 2, 3, 4):
+        raise ValueError("linear_parts: stages must be 0, 2, 3 or 4")
     if linear_splits(K_, splits) != int(splits):
         raise ValueError(f"linear_parts: {splits} splits leave a split of {K_ // 64} k-steps empty")
     shape = (int(splits), rows, N)
@@ -460,7 +463,7 @@ def linear_parts(x, w, *, splits=1, tile=(128, 128), out=None):
     elif out.dtype != torch.float32 or tuple(out.shape) != shape or not out.is_contiguous() or out.data_ptr() % 16:
         raise ValueError(f"linear_parts: out must be a contiguous 16-byte aligned fp32 {list(shape)} tensor")
     _call("fg_linear_parts", _ptr(x), x.stride(0), _ptr(w), w.stride(0), _ptr(out), rows, N, K_, int(splits), tm, tn,
-          _stream())
+          int(stages), _stream())
     return out
 
 

@@ -419,7 +419,8 @@ def _cu_count(device) -> int:
 
 def mlp_path(rows: int, inter: int, hidden: int, device) -> int:
     """How a decoder layer computes its MLP input for ``rows`` rows: 0 for the hipBLASLt
-    projection + fg_swiglu, else the tile height (192 or 256) of the fused gate/up + SwiGLU GEMM.
+    projection + fg_swiglu, else the tile height (64, 128, 192 or 256; -1 lets the kernel pick 192
+    or 256) of the fused gate/up + SwiGLU GEMM.
 
     The measured table (``tuning/mlp_mi355x.csv``) decides for the sizes it covers: which path
     is faster depends on the library's solution for the shape (Qwen2.5-7B verify rounds, 1856
@@ -436,9 +437,10 @@ def mlp_path(rows: int, inter: int, hidden: int, device) -> int:
 
 
 def default_linear_plan(rows: int, cols: int, hidden: int, cus: int = 256) -> tuple:
-    """A split-K plan (tile_m, tile_n, splits) for a shape no measurement covers: 128 x 128
+    """A split-K plan (tile_m, tile_n, splits, stages) for a shape no measurement covers: 128 x 128
     tiles when there are at least a quarter as many as CUs, else 64 x 128; then the split count
-    that brings the workgroups nearest to two per CU with at least four k-steps per split."""
+    that brings the workgroups nearest to two per CU with at least four k-steps per split; a
+    4-stage ring."""
     tm, tn = (128, 128) if -(-rows // 128) * -(-cols // 128) >= cus // 4 else (64, 128)
     tiles = -(-rows // tm) * -(-cols // tn)
     nk = hidden // 64
@@ -446,12 +448,12 @@ def default_linear_plan(rows: int, cols: int, hidden: int, cus: int = 256) -> tu
     for s in range(1, max(1, nk // 4) + 1):
         if K.linear_splits(hidden, s) == s and abs(tiles * s - 2 * cus) < abs(tiles * best - 2 * cus):
             best = s
-    return tm, tn, best
+    return tm, tn, best, 4
 
 
 def linear_path(kind: str, rows: int, cols: int, hidden: int):
     """How a decoder layer computes projection ``kind`` ("qkv", "o" or "down") for ``rows``
-    rows: (tile_m, tile_n, splits) of the split-K GEMM, or None for the library projection.
+    rows: (tile_m, tile_n, splits, stages) of the split-K GEMM, or None for the library projection.
 
     The measured table (``tuning/linear_mi355x.csv``) decides for the sizes it covers (split-K at
     the Qwen2.5-1.5B verify rows, where the library's tiles leave most CUs idle; the library at the
@@ -741,7 +743,7 @@ class TargetModel:
                 x.addmm_(act, lw["down_w"].t())
 
     def _linear_plan(self, kind: str, x: torch.Tensor, w: torch.Tensor):
-        """(tile_m, tile_n, splits) when projection ``kind`` of x by w runs split-K, else None."""
+        """(tile_m, tile_n, splits, stages) when projection ``kind`` of x by w runs split-K, else None."""
         if self.split_k_linear is False or not K.linear_ok(x, w):
             return None
         rows, hidden = x.shape
@@ -750,9 +752,9 @@ class TargetModel:
         return linear_path(kind, rows, w.shape[0], hidden)
 
     def _linear_parts(self, x: torch.Tensor, w: torch.Tensor, plan) -> torch.Tensor:
-        tm, tn, s = plan
+        tm, tn, s, ns = plan
         parts = self._buf("parts", (s, x.shape[0], w.shape[0]), torch.float32)
-        return K.linear_parts(x, w, splits=s, tile=(tm, tn), out=parts)
+        return K.linear_parts(x, w, splits=s, tile=(tm, tn), stages=ns, out=parts)
 
     def _forward_end(self, st: dict) -> torch.Tensor:
         """The final norm: hidden states [B, N, H] (already written when the last down projection

@@ -13,8 +13,8 @@ use another table.
 
 ``mlp_mi355x.csv`` (``make_mlp_table.py``) holds, per (rows, intermediate, hidden), the
 measured times of the two ways to compute a decoder layer's MLP input -- the tuned
-projection followed by ``fg_swiglu``, or the fused ``fg_gate_up_swiglu`` at either tile
-height -- and the faster one; ``mlp_table_path`` looks it up
+projection followed by ``fg_swiglu``, or the fused ``fg_gate_up_swiglu`` at each tile
+height -- and the fastest; ``mlp_table_path`` looks it up
 (``FLASHGRPO_AMD_MLP_TABLE=off`` or another path).
 
 ``linear_mi355x.csv`` (``make_linear_table.py``) holds, per projection kind (qkv, o, down) and
@@ -33,7 +33,7 @@ DEFAULT_MLP_TABLE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "ml
 DEFAULT_LINEAR_TABLE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "linear_mi355x.csv")
 _state = {"done": False, "active": False}
 _mlp = {}
-_CHOICE = {"pair": 0, "fused192": 192, "fused256": 256}
+_CHOICE = {"pair": 0, "fused64": 64, "fused128": 128, "fused192": 192, "fused256": 256}
 
 
 def _mlp_entries() -> dict:
@@ -56,7 +56,7 @@ def _mlp_entries() -> dict:
 
 def mlp_table_path(rows: int, inter: int, hidden: int):
     """The measured MLP input path for this shape: 0 (projection + fg_swiglu) or the fused GEMM's
-    tile height (192 / 256), taken from the table entry of these sizes nearest in row count on a log
+    tile height (64 / 128 / 192 / 256), taken from the table entry of these sizes nearest in row count on a log
     scale (ties to the larger count); None when the table has no entry for (inter, hidden)."""
     cands = _mlp_entries().get((int(inter), int(hidden)))
     if not cands:
@@ -72,7 +72,7 @@ _lin = {}
 
 def _linear_entries() -> dict:
     """(kind, cols, hidden) -> sorted [(rows, plan)] from the projection path table (read once);
-    plan is (tile_m, tile_n, splits) for the split-K kernel or () for the library."""
+    plan is (tile_m, tile_n, splits, stages) for the split-K kernel or () for the library."""
     if "entries" not in _lin:
         entries = {}
         choice = os.environ.get("FLASHGRPO_AMD_LINEAR_TABLE", "")
@@ -84,7 +84,8 @@ def _linear_entries() -> dict:
                     row = dict(zip(header, line.strip().split(",")))
                     if row.get("choice") not in ("library", "split_k"):
                         continue
-                    plan = ((int(row["tile_m"]), int(row["tile_n"]), int(row["splits"]))
+                    # a table without a stages column was measured with the 2-stage ring
+                    plan = ((int(row["tile_m"]), int(row["tile_n"]), int(row["splits"]), int(row.get("stages", 2)))
                             if row["choice"] == "split_k" else ())
                     key = (row["kind"], int(row["cols"]), int(row["hidden"]))
                     entries.setdefault(key, []).append((int(row["rows"]), plan))
@@ -93,7 +94,7 @@ def _linear_entries() -> dict:
 
 
 def linear_table_plan(kind: str, rows: int, cols: int, hidden: int):
-    """The measured projection path for this shape: (tile_m, tile_n, splits) of the split-K kernel,
+    """The measured projection path for this shape: (tile_m, tile_n, splits, stages) of the split-K kernel,
     () for the library projection, from the table entry of this kind and these sizes nearest in row
     count on a log scale (ties to the larger count); None when the table has no such entry. Row
     counts above twice the largest measured one take the library."""

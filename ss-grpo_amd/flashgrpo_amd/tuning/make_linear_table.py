@@ -12,7 +12,7 @@ a decoder layer can compute the projection together with the op that consumes it
   by ``fg_rmsnorm`` (O, down);
 * ``fg_linear_parts`` followed by the kernel that finishes its fp32 parts
   (``fg_rope_kv_write_parts``, ``fg_residual_rmsnorm_parts``), over tile sizes and split counts
-  that put between 64 and 1024 workgroups on the chip.
+  that put between 64 and 1024 workgroups on the chip, with a 2- or 4-stage LDS ring.
 
 The verify forward replays its launches as a HIP graph, so each path is timed the same way: one
 graph holding ``batch`` back-to-back calls, the weight rotating over enough copies to exceed the
@@ -37,21 +37,22 @@ SHAPES = {
     "llama31_8b": (96 * 48,),
 }
 TILES = ((64, 64), (64, 128), (128, 64), (128, 128))
+STAGES = (2, 4)
 
 
 def split_candidates(K, rows, cols, hidden):
-    """(tile_m, tile_n, splits) with 64-1024 workgroups (one split when the tiles alone exceed
-    that) and at least two k-steps per split."""
+    """(tile_m, tile_n, splits, stages) with 64-1024 workgroups (one split when the tiles alone
+    exceed that), at least two k-steps per split, and a 2- or 4-stage ring."""
     out = []
     nk = hidden // 64
     for tm, tn in TILES:
         tiles = -(-rows // tm) * -(-cols // tn)
         if tiles >= 1024:
-            out.append((tm, tn, 1))
+            out += [(tm, tn, 1, ns) for ns in STAGES]
             continue
         for s in range(1, nk // 2 + 1):
             if K.linear_splits(hidden, s) == s and 64 <= tiles * s <= 1024:
-                out.append((tm, tn, s))
+                out += [(tm, tn, s, ns) for ns in STAGES]
     return out
 
 
@@ -94,7 +95,7 @@ def main():
         del g
         return min(ts)
 
-    lines = ["kind,rows,cols,hidden,library_us,split_k_us,tile_m,tile_n,splits,choice"]
+    lines = ["kind,rows,cols,hidden,library_us,split_k_us,tile_m,tile_n,splits,stages,choice"]
     for preset, extra in SHAPES.items():
         if only_presets and preset not in only_presets:
             continue
@@ -133,34 +134,35 @@ def main():
                     def library():
                         K.rope_kv_write(F.linear(x, w_next(), bias), **rope)
 
-                    def split_k(tm, tn, s, buf):
+                    def split_k(tm, tn, s, ns, buf):
                         def run():
-                            K.rope_kv_write_parts(K.linear_parts(x, w_next(), splits=s, tile=(tm, tn), out=buf),
-                                                  bias, **rope)
+                            K.rope_kv_write_parts(K.linear_parts(x, w_next(), splits=s, tile=(tm, tn), stages=ns,
+                                                                 out=buf), bias, **rope)
                         return run
                 else:
                     def library():
                         res.addmm_(x, w_next().t())
                         K.rmsnorm(res, norm_w, cfg.rms_eps, out=h)
 
-                    def split_k(tm, tn, s, buf):
+                    def split_k(tm, tn, s, ns, buf):
                         def run():
-                            K.residual_rmsnorm_parts(K.linear_parts(x, w_next(), splits=s, tile=(tm, tn), out=buf),
-                                                     res, norm_w, cfg.rms_eps, out=h)
+                            K.residual_rmsnorm_parts(K.linear_parts(x, w_next(), splits=s, tile=(tm, tn), stages=ns,
+                                                                    out=buf), res, norm_w, cfg.rms_eps, out=h)
                         return run
 
                 t_lib = best(library, batch)
                 top = None
-                for tm, tn, s in split_candidates(K, rows, N, Kd):
+                for tm, tn, s, ns in split_candidates(K, rows, N, Kd):
                     buf = torch.empty(s, rows, N, dtype=torch.float32, device=dev)
-                    t = best(split_k(tm, tn, s, buf), batch)
+                    t = best(split_k(tm, tn, s, ns, buf), batch)
                     del buf
                     if top is None or t < top[0]:
-                        top = (t, tm, tn, s)
+                        top = (t, tm, tn, s, ns)
                 choice = "split_k" if top[0] < t_lib else "library"
-                lines.append(f"{kind},{rows},{N},{Kd},{t_lib:.1f},{top[0]:.1f},{top[1]},{top[2]},{top[3]},{choice}")
+                lines.append(f"{kind},{rows},{N},{Kd},{t_lib:.1f},{top[0]:.1f},{top[1]},{top[2]},{top[3]},{top[4]},"
+                             f"{choice}")
                 print(f"{cfg.name} {kind} rows {rows}: library {t_lib:.1f}, split-K {top[0]:.1f} "
-                      f"(tile {top[1]}x{top[2]}, {top[3]} splits) -> {choice}", flush=True)
+                      f"(tile {top[1]}x{top[2]}, {top[3]} splits, {top[4]} stages) -> {choice}", flush=True)
                 del x, res, h
             del ws
             torch.cuda.empty_cache()

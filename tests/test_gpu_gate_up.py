@@ -82,8 +82,8 @@ def test_matches_rounded_float64_reference(rows, hidden, inter):
     check_against_reference(out, x, w)
 
 
-@pytest.mark.parametrize("tile_rows", [192, 256])
-def test_both_tile_heights_agree_bitwise(tile_rows):
+@pytest.mark.parametrize("tile_rows", [64, 128, 192, 256])
+def test_every_tile_height_agrees_bitwise(tile_rows):
     x, w = operands(300, 512, 520, seed=5)
     auto = K().gate_up_swiglu(x, w)
     forced = K().gate_up_swiglu(x, w, tile_rows=tile_rows)
@@ -107,12 +107,13 @@ def test_strided_operands_and_untouched_padding():
     assert torch.equal(dense.view(torch.int16), out.contiguous().view(torch.int16))
 
 
-@pytest.mark.parametrize("rows,hidden,inter", [(1856, 3584, 18944), (512, 1536, 8960)])
-def test_decoder_shapes_match_the_unfused_pair(rows, hidden, inter):
+@pytest.mark.parametrize("rows,hidden,inter,tile", [(1856, 3584, 18944, 0), (512, 1536, 8960, 0),
+                                                    (416, 1536, 8960, 64), (416, 1536, 8960, 128)])
+def test_decoder_shapes_match_the_unfused_pair(rows, hidden, inter, tile):
     """Qwen2.5-7B and 1.5B verify-round shapes (B x tree nodes rows) against the projection +
     SwiGLU kernels it replaces, and against the rounded float64 reference."""
     x, w = operands(rows, hidden, inter, seed=rows)
-    fused = K().gate_up_swiglu(x, w)
+    fused = K().gate_up_swiglu(x, w, tile_rows=tile)
     unfused = K().swiglu(F.linear(x, w))
     torch.cuda.synchronize()
     same = float((fused.view(torch.int16) == unfused.view(torch.int16)).float().mean())
@@ -130,4 +131,4 @@ def test_rejects_unsupported_operands():
     with pytest.raises(ValueError):
         K().gate_up_swiglu(x, w, out=torch.empty(8, 9, dtype=torch.bfloat16, device=DEV))
     with pytest.raises(ValueError, match="tile_rows"):
-        K().gate_up_swiglu(x, w, tile_rows=128)
+        K().gate_up_swiglu(x, w, tile_rows=96)

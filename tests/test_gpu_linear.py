@@ -66,26 +66,29 @@ def test_parts_sum_matches_float64(rows, hidden, cols):
     x, w = operands(rows, hidden, cols, seed=rows + cols)
     ref = None
     for tile in ((64, 64), (64, 128), (128, 64), (128, 128)):
-        p = K().linear_parts(x, w, splits=1, tile=tile)
-        check_parts(p, x, w)
-        if ref is None:
-            ref = p
-        else:
-            assert torch.equal(p, ref), f"tile {tile} accumulates differently from (64, 64)"
+        for stages in (2, 3, 4):
+            p = K().linear_parts(x, w, splits=1, tile=tile, stages=stages)
+            check_parts(p, x, w)
+            if ref is None:
+                ref = p
+            else:
+                assert torch.equal(p, ref), f"tile {tile}, {stages} stages accumulate differently from (64, 64)"
     nk = hidden // 64
     for s in sorted({2, 3, 5, nk}):
         if s <= nk and K().linear_splits(hidden, s) == s:
             p = K().linear_parts(x, w, splits=s, tile=(128, 64))
             assert p.shape == (s, rows, cols)
             check_parts(p, x, w)
+            assert torch.equal(p, K().linear_parts(x, w, splits=s, tile=(128, 64), stages=2))
 
 
 def test_long_reduction_and_padded_strides():
     """The 1.5B down projection's reduction length (8960) with padded operand rows."""
     x, w = operands(96, 8960, 256, seed=5, x_pad=64, w_pad=8)
-    for s in (1, 4, 7):
+    for s in (1, 4, 7, 35, 70):  # 140 k-steps: from one split to two k-steps per split (fewer than the ring)
         s = K().linear_splits(8960, s)
-        check_parts(K().linear_parts(x, w, splits=s, tile=(64, 128)), x, w)
+        for stages in (2, 4):
+            check_parts(K().linear_parts(x, w, splits=s, tile=(64, 128), stages=stages), x, w)
 
 
 def test_invalid_split_counts_and_operands_are_rejected():
@@ -95,6 +98,8 @@ def test_invalid_split_counts_and_operands_are_rejected():
         K().linear_parts(x, w, splits=4)       # 3 k-steps
     with pytest.raises(ValueError):
         K().linear_parts(x, w, tile=(256, 64))
+    with pytest.raises(ValueError):
+        K().linear_parts(x, w, stages=5)
     with pytest.raises(ValueError):
         K().linear_parts(x[:, :100], w[:, :100])  # K not a multiple of 64
     with pytest.raises(ValueError):

@@ -300,7 +300,7 @@ def test_split_k_projections_match_library_projections():
     ocfg = _cfgs(torch.bfloat16)
     m = _model(ocfg, OM.random_weights(ocfg, seed=7, std=0.05), torch.bfloat16)
     assert m.split_k_linear is None and linear_path("o", 39, 777, 1024) is None
-    tm, tn, s = default_linear_plan(416, 1536, 8960)
+    tm, tn, s, _ = default_linear_plan(416, 1536, 8960)
     assert (tm, tn) in ((64, 128), (128, 128)) and s > 1
     rng = np.random.default_rng(7)
     B, P = 3, 70

@@ -24,8 +24,8 @@ def test_choices_are_the_faster_measured_path_and_plans_are_valid():
         fast = "split_k" if sk < lib else "library"
         # one decimal in the file: a choice may tie after rounding but never lose by a step
         assert r["choice"] == fast or abs(lib - sk) < 0.05, r
-        tm, tn, s = int(r["tile_m"]), int(r["tile_n"]), int(r["splits"])
-        assert tm in K.LINEAR_TILES and tn in K.LINEAR_TILES, r
+        tm, tn, s, ns = int(r["tile_m"]), int(r["tile_n"]), int(r["splits"]), int(r["stages"])
+        assert tm in K.LINEAR_TILES and tn in K.LINEAR_TILES and ns in (2, 3, 4), r
         assert K.linear_splits(int(r["hidden"]), s) == s, r
 
 
@@ -41,22 +41,23 @@ def test_table_covers_the_bf16_benchmark_models_and_lookup_returns_entries():
     for r in rows():
         plan = tuning.linear_table_plan(r["kind"], int(r["rows"]), int(r["cols"]), int(r["hidden"]))
         if r["choice"] == "split_k":
-            assert plan == (int(r["tile_m"]), int(r["tile_n"]), int(r["splits"]))
+            assert plan == (int(r["tile_m"]), int(r["tile_n"]), int(r["splits"]), int(r["stages"]))
         else:
             assert plan == ()
 
 
 def test_lookup_nearest_row_count_and_library_beyond_the_measured_range(monkeypatch):
-    monkeypatch.setitem(tuning._lin, "entries", {("o", 64, 128): [(64, (64, 64, 2)), (256, ()), (1024, (128, 128, 1))]})
-    assert tuning.linear_table_plan("o", 100, 64, 128) == (64, 64, 2)
+    monkeypatch.setitem(tuning._lin, "entries", {("o", 64, 128): [(64, (64, 64, 2, 4)), (256, ()),
+                                                                    (1024, (128, 128, 1, 2))]})
+    assert tuning.linear_table_plan("o", 100, 64, 128) == (64, 64, 2, 4)
     assert tuning.linear_table_plan("o", 128, 64, 128) == ()          # equal log distance: the larger count
-    assert tuning.linear_table_plan("o", 2048, 64, 128) == (128, 128, 1)
+    assert tuning.linear_table_plan("o", 2048, 64, 128) == (128, 128, 1, 2)
     assert tuning.linear_table_plan("o", 2049, 64, 128) == ()        # beyond twice the largest measured count
     assert tuning.linear_table_plan("qkv", 64, 64, 128) is None       # kind not in the table
 
 
 def test_default_plan_satisfies_the_kernel_rules():
     for rows_, cols, hidden in ((1, 64, 64), (416, 1536, 8960), (1856, 4608, 3584), (96, 2048, 1536)):
-        tm, tn, s = default_linear_plan(rows_, cols, hidden)
-        assert tm in K.LINEAR_TILES and tn in K.LINEAR_TILES
+        tm, tn, s, ns = default_linear_plan(rows_, cols, hidden)
+        assert tm in K.LINEAR_TILES and tn in K.LINEAR_TILES and ns in (2, 3, 4)
         assert K.linear_splits(hidden, s) == s

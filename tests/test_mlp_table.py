@@ -19,7 +19,7 @@ def rows():
 @pytest.mark.skipif(not os.path.exists(TABLE), reason="no MLP path table")
 def test_table_choices_are_the_fastest_measured_path():
     for r in rows():
-        t = {k: float(r[k + "_us"]) for k in ("pair", "fused192", "fused256")}
+        t = {k: float(r[k + "_us"]) for k in ("pair", "fused64", "fused128", "fused192", "fused256")}
         # the generator picks on unrounded times; the file keeps one decimal, so a
         # choice may tie the minimum after rounding but never exceed it by a step
         assert t[r["choice"]] <= min(t.values()) + 0.05, r
@@ -32,7 +32,7 @@ def test_table_covers_every_benchmark_model_and_lookup_returns_entries():
     for preset in ("tiny", "qwen25_1p5b", "qwen25_7b", "qwen25_14b", "llama31_8b"):
         cfg = getattr(TargetConfig, preset)()
         assert (cfg.intermediate, cfg.hidden) in have, preset
-    code = {"pair": 0, "fused192": 192, "fused256": 256}
+    code = {"pair": 0, "fused64": 64, "fused128": 128, "fused192": 192, "fused256": 256}
     for r in rows():
         assert tuning.mlp_table_path(int(r["rows"]), int(r["inter"]), int(r["hidden"])) == code[r["choice"]]
 
