@@ -47,12 +47,23 @@ def test_library_loads_and_reports_errors_without_gpu_work():
                               ctypes.c_void_p(64), None, 0, None)
     assert rc != 0 and b"vocab" in lib.fg_last_error()
     assert lib.fg_sample_workspace(64) >= 64 * 16 * 20 and lib.fg_sample_workspace(0) == 0
-    # the fused MLP GEMM: K (hidden) must be a multiple of 64, tile heights 192 / 256 only
+    # the fused MLP GEMM: K (hidden) must be a multiple of 64, tile heights 64 / 128 / 192 / 256 only
     p = ctypes.c_void_p(256)
     rc = lib.fg_gate_up_swiglu(p, 96, p, 96, p, 8, 4, 8, 96, 0, None)
     assert rc != 0 and b"multiple of 64" in lib.fg_last_error()
-    rc = lib.fg_gate_up_swiglu(p, 64, p, 64, p, 8, 4, 8, 64, 128, None)
+    rc = lib.fg_gate_up_swiglu(p, 64, p, 64, p, 8, 4, 8, 64, 96, None)
     assert rc != 0 and b"tile_rows" in lib.fg_last_error()
+    # the split-K projection: K a multiple of 64, every split non-empty, 2-4 ring stages
+    rc = lib.fg_linear_parts(p, 96, p, 96, p, 8, 16, 96, 1, 64, 64, 0, None)
+    assert rc != 0 and b"multiple of 64" in lib.fg_last_error()
+    rc = lib.fg_linear_parts(p, 192, p, 192, p, 8, 16, 192, 4, 64, 64, 0, None)
+    assert rc != 0 and b"splits" in lib.fg_last_error()
+    rc = lib.fg_linear_parts(p, 192, p, 192, p, 8, 16, 192, 3, 64, 64, 5, None)
+    assert rc != 0 and b"stages" in lib.fg_last_error()
+    rc = lib.fg_linear_parts(p, 192, p, 192, p, 8, 16, 192, 3, 256, 64, 0, None)
+    assert rc != 0 and b"tile_m" in lib.fg_last_error()
+    rc = lib.fg_residual_rmsnorm_parts(p, 1, 4, 12, p, 12, p, 1e-6, p, 12, None)
+    assert rc != 0 and b"multiple of 8" in lib.fg_last_error()
     rc = lib.fg_gate_up_swiglu(None, 64, p, 64, p, 8, 4, 8, 64, 0, None)
     assert rc != 0 and b"null pointer" in lib.fg_last_error()
     rc = lib.fg_chain_cell_norm(p, 12, p, 12, 1, 4, 12, p, p, p, p, 1e-5, p, None)
