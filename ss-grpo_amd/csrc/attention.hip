@@ -399,28 +399,35 @@ __global__ void __launch_bounds__(W * 64, 2) tree_attn_bf16_kernel(AttnArgs a, i
   }
 }
 
-// Key-split combine: one wave per (sequence, node, q head) row; lane j owns dims
-// 2j, 2j+1. O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s (parts with no
-// allowed key have m_s = -inf and weigh 0).
-__global__ void __launch_bounds__(64) tree_attn_combine_kernel(AttnArgs a, int rows) {
-  const int row = blockIdx.x;
-  const int lane = threadIdx.x;
+// Key-split combine: 8 (sequence, node, q head) rows per 256-thread workgroup, one half-wave
+// per row, lane j owning dims 4j .. 4j+3 (16-byte loads of each part's O row).
+// O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s (parts with no allowed key have m_s = -inf
+// and weigh 0), each sum taken over the parts in order.
+constexpr int kCombineRows = 8;
+
+__global__ void __launch_bounds__(256) tree_attn_combine_kernel(AttnArgs a, int rows) {
+  const int row = blockIdx.x * kCombineRows + (threadIdx.x >> 5);
+  const int lane = threadIdx.x & 31;
+  if (row >= rows) return;
   float mx = -INFINITY;
   for (int p = 0; p < a.splits; ++p) mx = fmaxf(mx, a.ml_part[(int64_t)p * rows + row].x);
-  float den = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  float den = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (mx != -INFINITY) {
     for (int p = 0; p < a.splits; ++p) {
       const float2 ml = a.ml_part[(int64_t)p * rows + row];
       if (ml.x == -INFINITY) continue;
       const float w = __builtin_amdgcn_exp2f(ml.x - mx);
-      const float2 ov = *(const float2*)(a.o_part + ((int64_t)p * rows + row) * kD + 2 * lane);
+      const float4 ov = *(const float4*)(a.o_part + ((int64_t)p * rows + row) * kD + 4 * lane);
       den += w * ml.y;
-      o0 += w * ov.x;
-      o1 += w * ov.y;
+      o[0] += w * ov.x;
+      o[1] += w * ov.y;
+      o[2] += w * ov.z;
+      o[3] += w * ov.w;
     }
   }
   const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-  *(uint32_t*)((uint16_t*)a.out + (int64_t)row * kD + 2 * lane) = fg::pack_bf16x2(o0 * inv, o1 * inv);
+  *(uint2*)((uint16_t*)a.out + (int64_t)row * kD + 4 * lane) =
+      make_uint2(fg::pack_bf16x2(o[0] * inv, o[1] * inv), fg::pack_bf16x2(o[2] * inv, o[3] * inv));
 }
 
 // fp32: one wave per (sequence, node, q head), 64 keys per step. Lane j scores key
@@ -574,7 +581,9 @@ extern "C" int fg_tree_attention(const void* q, void* out, const void* k_cache, 
       launch_attn_bf16<8>(a, M, s);
     else
       launch_attn_bf16<4>(a, M, s);
-    if (split) hipLaunchKernelGGL(tree_attn_combine_kernel, dim3((unsigned)rows), dim3(64), 0, s, a, (int)rows);
+    if (split)
+      hipLaunchKernelGGL(tree_attn_combine_kernel, dim3((unsigned)((rows + kCombineRows - 1) / kCombineRows)),
+                         dim3(256), 0, s, a, (int)rows);
   } else if (dtype == fg::kF32) {
     FG_REQUIRE(head_dim == 64 || head_dim == 128, "fg_tree_attention: fp32 path supports head_dim 64 or 128");
     FG_REQUIRE(((uintptr_t)k_cache & 15) == 0 && cache_head_stride % 4 == 0 && cache_batch_stride % 4 == 0,
