@@ -670,6 +670,107 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs g, int epi) {
     for (int j = 0; j < 4; ++j) epilogue_store<CDT, fg::kF32>(g, z, m0 + ty * 4 + i, n0 + tx * 4 + j, acc[i][j], epi);
 }
 
+// fp32 Medusa block, split over K: blockIdx.z = z * ksplit + p takes k in [p * kper, (p + 1) * kper)
+// of batch z's product and writes the raw sums to parts[p][z][m][n] (64 x 64 tile, 4 x 4 outputs
+// per thread, each thread loading one 16-byte run of 4 k values of A and of B per 16-deep k-step).
+// medusa_f32_combine_kernel finishes the block. The unsplit kernel above runs a 96 x 4096 x 4096
+// bootstrap (the chain path's head 0, fp32 master weights) as 128 workgroups walking all of K.
+template <int DUMMY>
+__global__ void __launch_bounds__(256) gemm_f32_split_kernel(GemmArgs g, int ksplit, int kper, float* parts) {
+  constexpr int T = 64, BKf = 16;
+  __shared__ float As[BKf][T + 1];
+  __shared__ float Bs[BKf][T + 1];
+  const int z = blockIdx.z / ksplit, sp = blockIdx.z % ksplit;
+  const int m0 = blockIdx.y * T, n0 = blockIdx.x * T;
+  const int k_begin = sp * kper, k_end = min(g.K, k_begin + kper);
+  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+  const float* Ab = (const float*)g.A + z * g.a_batch;
+  const float* Bb = (const float*)g.B + z * g.b_batch;
+  // loader: thread t takes row t / 4 and k run 4 * (t % 4) of the 64 x 16 tile of A and of B
+  const int lr = threadIdx.x >> 2, lk = (threadIdx.x & 3) * 4;
+  const bool a_ok = m0 + lr < g.M, b_ok = n0 + lr < g.N;
+  const float* arow = Ab + (int64_t)(a_ok ? m0 + lr : 0) * g.lda;
+  const float* brow = Bb + (int64_t)(b_ok ? n0 + lr : 0) * g.ldb;
+  float acc[4][4] = {};
+  for (int k0 = k_begin; k0 < k_end; k0 += BKf) {
+    const int k = k0 + lk;
+    float4 av = make_float4(0.0f, 0.0f, 0.0f, 0.0f), bv = av;
+    if (k + 4 <= k_end) {
+      if (a_ok) av = *(const float4*)(arow + k);
+      if (b_ok) bv = *(const float4*)(brow + k);
+    } else {  // the part's last k-step (K a multiple of 4 keeps runs whole)
+      if (a_ok && k < k_end) av = *(const float4*)(arow + k);
+      if (b_ok && k < k_end) bv = *(const float4*)(brow + k);
+    }
+    As[lk][lr] = av.x; As[lk + 1][lr] = av.y; As[lk + 2][lr] = av.z; As[lk + 3][lr] = av.w;
+    Bs[lk][lr] = bv.x; Bs[lk + 1][lr] = bv.y; Bs[lk + 2][lr] = bv.z; Bs[lk + 3][lr] = bv.w;
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < BKf; ++kk) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = As[kk][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+  float* dst = parts + ((int64_t)sp * gridDim.z / ksplit + z) * (int64_t)g.M * g.N;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + ty * 4 + i, n = n0 + tx * 4;
+    if (m < g.M && n < g.N)  // N % 4 == 0
+      *(float4*)(dst + (int64_t)m * g.N + n) = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+  }
+}
+
+// out[z * M + m, n] = R[m, n] + SiLU(sum_p parts[p][z][m][n] + bias[z][n]) in fp32 (the module's fp32
+// forward: no intermediate rounding), parts summed in order; 4 columns per thread.
+template <int ODT>
+__global__ void __launch_bounds__(256) medusa_f32_combine_kernel(const float* __restrict__ parts, int ksplit,
+                                                                 int heads, int M, int N,
+                                                                 const float* __restrict__ bias,
+                                                                 const float* __restrict__ R, int64_t ldr,
+                                                                 void* __restrict__ out) {
+  const int nq = N >> 2;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)heads * M * nq) return;
+  const int c = (int)(idx % nq) * 4;
+  const int64_t hm = idx / nq;  // h * M + m
+  const int h = (int)(hm / M), m = (int)(hm % M);
+  const int64_t plane = (int64_t)heads * M * N;
+  float4 sv = *(const float4*)(parts + hm * N + c);
+  for (int p = 1; p < ksplit; ++p) {
+    const float4 pv = *(const float4*)(parts + p * plane + hm * N + c);
+    sv.x += pv.x; sv.y += pv.y; sv.z += pv.z; sv.w += pv.w;
+  }
+  const float4 bv = *(const float4*)(bias + (int64_t)h * N + c);
+  const float4 rv = *(const float4*)(R + (int64_t)m * ldr + c);
+  const float v[4] = {rv.x + fg::silu_f32(sv.x + bv.x), rv.y + fg::silu_f32(sv.y + bv.y),
+                      rv.z + fg::silu_f32(sv.z + bv.z), rv.w + fg::silu_f32(sv.w + bv.w)};
+  if constexpr (ODT == fg::kBF16)
+    *(uint2*)((uint16_t*)out + hm * N + c) = make_uint2(fg::pack_bf16x2(v[0], v[1]), fg::pack_bf16x2(v[2], v[3]));
+  else
+    *(float4*)((float*)out + hm * N + c) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+struct F32Split {
+  int ksplit, kper;
+};
+// Splits of K (each a multiple of 16, at most 8) that bring heads x 64 x 64 tiles to about two
+// workgroups per CU; 1 when the tiles alone fill the chip.
+F32Split f32_split(int M, int N, int K, int heads) {
+  const int64_t tiles = (int64_t)heads * ((M + 63) / 64) * ((N + 63) / 64);
+  int ks = tiles >= 512 ? 1 : (int)std::min<int64_t>(8, (512 + tiles - 1) / tiles);
+  ks = std::max(1, std::min(ks, K / 64));
+  const int kper = ((K + ks - 1) / ks + 15) / 16 * 16;
+  return {(K + kper - 1) / kper, kper};
+}
+
 int launch_gemm(const GemmArgs& g, int dtype, int out_dtype, int epi, int batch, hipStream_t s) {
   FG_REQUIRE(g.M > 0 && g.N > 0 && g.K > 0 && batch > 0, "gemm: empty shape");
   if (dtype == fg::kBF16) {
@@ -853,9 +954,18 @@ static size_t medusa_ln_bytes(int batch, int hidden, int heads, int dtype) {
   return ((size_t)batch * hidden * heads * fg::elem_bytes(dtype) + 15) & ~(size_t)15;
 }
 
+// The fp32 block's split-K path: H a multiple of 4, 16-byte aligned rows.
+static bool medusa_f32_split_ok(int H, int64_t ldh) { return H % 4 == 0 && ldh % 4 == 0; }
+
 size_t fg_medusa_heads_workspace(int batch, int hidden, int heads, int dtype) {
   if (batch <= 0 || hidden <= 0 || heads <= 0) return 256;
-  const size_t parts = dtype == fg::kBF16 ? fg::medusa_stream_parts_bytes(batch, hidden, heads) : 0;
+  size_t parts = 0;
+  if (dtype == fg::kBF16) {
+    parts = fg::medusa_stream_parts_bytes(batch, hidden, heads);
+  } else if (medusa_f32_split_ok(hidden, hidden)) {
+    const F32Split sp = f32_split(batch, hidden, hidden, heads);
+    parts = (size_t)sp.ksplit * heads * batch * hidden * 4;
+  }
   return medusa_ln_bytes(batch, hidden, heads, dtype) + parts + 256;
 }
 
@@ -896,6 +1006,25 @@ int fg_medusa_heads(const void* hidden, int dtype, int batch, int H, int64_t ldh
   g.bias = fc_b; g.bias_batch = H;
   g.R = hidden; g.ldr = ldh; g.r_batch = 0; g.r_dtype = dtype;
   g.M = batch; g.N = H; g.K = H;
+  if (dtype == fg::kF32 && medusa_f32_split_ok(H, ldh) && ((uintptr_t)fc_w & 15) == 0 && ((uintptr_t)fc_b & 15) == 0 &&
+      ((uintptr_t)hidden & 15) == 0 && ((uintptr_t)out & (out_dtype == fg::kBF16 ? 7 : 15)) == 0) {
+    // fp32 heads: K split into parts that fill the chip, then the fp32 combine
+    const F32Split sp = f32_split(batch, H, H, heads);
+    float* parts = (float*)((char*)workspace + medusa_ln_bytes(batch, H, heads, dtype));
+    const dim3 grid((H + 63) / 64, (batch + 63) / 64, heads * sp.ksplit);
+    hipLaunchKernelGGL(gemm_f32_split_kernel<0>, grid, dim3(256), 0, s, g, sp.ksplit, sp.kper, parts);
+    rc = fg::check_launch("fg_medusa_heads(f32 split)");
+    if (rc) return rc;
+    const int64_t threads = (int64_t)heads * batch * (H / 4);
+    const dim3 cgrid((unsigned)((threads + 255) / 256));
+    if (out_dtype == fg::kBF16)
+      hipLaunchKernelGGL(medusa_f32_combine_kernel<fg::kBF16>, cgrid, dim3(256), 0, s, parts, sp.ksplit, heads, batch,
+                         H, (const float*)fc_b, (const float*)hidden, ldh, out);
+    else
+      hipLaunchKernelGGL(medusa_f32_combine_kernel<fg::kF32>, cgrid, dim3(256), 0, s, parts, sp.ksplit, heads, batch,
+                         H, (const float*)fc_b, (const float*)hidden, ldh, out);
+    return fg::check_launch("fg_medusa_heads(f32 combine)");
+  }
   return launch_gemm(g, dtype, out_dtype, kEpiMedusa, heads, s);
 }
 

@@ -549,6 +549,36 @@ def test_medusa_heads_match_oracle(dtype):
         assert rel_err(to_np(out[i * B:(i + 1) * B]), want) < TOL[dtype]
 
 
+@pytest.mark.parametrize("B,H,nh", [(96, 4096, 1), (64, 3584, 4), (7, 516, 2), (130, 256, 3)])
+def test_medusa_heads_fp32_split_matches_float64(B, H, nh):
+    """fp32 Medusa blocks (the chain path's head-0 bootstrap with fp32 master weights: 96 rows x
+    4096 at the Llama-3.1-8B shape) run split over K into parts that a combine kernel sums in order
+    with the bias, SiLU and residual. Checked against float64 on the normalised rows the call
+    wrote, within the fp32 accumulation bound, for hidden sizes that are not multiples of 64 (516)
+    and row counts past one 64-row tile; repeated calls give identical bits."""
+    torch.manual_seed(B + H + nh)
+    hid = torch.randn(B + 2, H, device=DEV)[:B]
+    ln_w = 1 + 0.1 * torch.randn(nh, H, device=DEV)
+    ln_b = 0.1 * torch.randn(nh, H, device=DEV)
+    fc_w = torch.randn(nh, H, H, device=DEV) * 0.03
+    fc_b = torch.randn(nh, H, device=DEV) * 0.1
+    need = K()._lib.load().fg_medusa_heads_workspace(B, H, nh, 0)
+    ws = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    out = K().medusa_heads(hid, ln_w, ln_b, fc_w, fc_b, out_dtype=torch.float32, workspace=ws)
+    rows = ws[:nh * B * H * 4].view(torch.float32).view(nh, B, H).double()
+    pre = torch.bmm(rows, fc_w.double().transpose(1, 2).contiguous()) + fc_b.double()[:, None, :]
+    ref = hid.double()[None] + torch.nn.functional.silu(pre)
+    # fp32 sums of H products (split parts plus their in-order sum), SiLU' <= 1.1
+    bound = 1.1 * (H + 16) * 2.0 ** -24 * (torch.bmm(rows.abs(), fc_w.double().abs().transpose(1, 2).contiguous())
+                                           + fc_b.double().abs()[:, None, :]) + 4 * 2.0 ** -24 * ref.abs() + 1e-30
+    err = (out.view(nh, B, H).double() - ref).abs()
+    assert bool((err <= bound).all()), float((err - bound).max())
+    ln = torch.nn.functional.layer_norm(hid.double(), (H,), eps=1e-5)
+    assert rel_err(to_np(rows), to_np(ln[None] * ln_w.double()[:, None, :] + ln_b.double()[:, None, :])) < 1e-5
+    again = K().medusa_heads(hid, ln_w, ln_b, fc_w, fc_b, out_dtype=torch.float32, workspace=ws)
+    assert torch.equal(out, again)
+
+
 @pytest.mark.parametrize("B,H,nh", [(64, 3584, 4), (16, 576, 3), (100, 1024, 5), (200, 512, 2), (1, 128, 1)])
 def test_medusa_heads_stream_matches_fp32_reference(B, H, nh):
     """bf16 Medusa fc through the weight stream (key ranges summed by a second launch):
