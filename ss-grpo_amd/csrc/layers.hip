@@ -42,11 +42,11 @@ FG_DEVICE void store4(void* p, int64_t i, const float (&v)[4]) {
     *(float4*)((float*)p + i) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
-// Where rope_kv_write_kernel reads a token's projected qkv row: a row of the qkv tensor, or
-// (part != nullptr) the fp32 split-K partial sums of the projection (fg_linear_parts, row stride
+// Where rope_kv_write_kernel reads a token's projected qkv row: a row of the qkv tensor
+// (PARTS false), or the fp32 split-K partial sums of the projection (fg_linear_parts, row stride
 // ld = the projection's width) summed in split order, plus the bias, rounded to the row dtype as the
-// projection's output would be.
-template <int DT>
+// projection's output would be (PARTS true).
+template <int DT, bool PARTS>
 struct QkvSource {
   const void* qkv;
   const float* part;
@@ -55,7 +55,7 @@ struct QkvSource {
   const void* bias;
 
   FG_DEVICE void get4(int64_t row, int col, float (&v)[4]) const {
-    if (part == nullptr) {
+    if constexpr (!PARTS) {
       load4<DT>(qkv, row + col, v);
       return;
     }
@@ -72,6 +72,21 @@ struct QkvSource {
     v[2] = rnd<DT>(a.z + bv[2]);
     v[3] = rnd<DT>(a.w + bv[3]);
   }
+
+  FG_DEVICE void get8(int64_t row, int col, float (&v)[8]) const {
+    if constexpr (!PARTS) {
+      fg::load8<DT>(qkv, row + col, v);
+    } else {
+      float lo[4], hi[4];
+      get4(row, col, lo);
+      get4(row, col + 4, hi);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[j] = lo[j];
+        v[4 + j] = hi[j];
+      }
+    }
+  }
 };
 
 // One workgroup per token (b, n). qkv row = [q heads | k heads | v heads] x d.
@@ -79,9 +94,9 @@ struct QkvSource {
 // cos/sin of the token's d/2 angles are computed once into LDS; each thread then
 // rotates 4 consecutive pairs (i, i + d/2) of one head with 8/16-byte accesses.
 // Requires d % 8 == 0 and d <= 256.
-template <int DT>
+template <int DT, bool PARTS>
 __global__ void __launch_bounds__(256) rope_kv_write_kernel(
-    QkvSource<DT> qkv, int64_t ld_qkv, int N, int Hq, int Hkv, int d, const int32_t* __restrict__ seq_len,
+    QkvSource<DT, PARTS> qkv, int64_t ld_qkv, int N, int Hq, int Hkv, int d, const int32_t* __restrict__ seq_len,
     const int32_t* __restrict__ pos_offset, int64_t pos_stride, const float* __restrict__ inv_freq,
     void* __restrict__ q_out,
     void* __restrict__ k_cache, void* __restrict__ v_cache, int64_t cache_batch, int64_t cache_head, int capacity,
@@ -131,14 +146,8 @@ __global__ void __launch_bounds__(256) rope_kv_write_kernel(
   const int oct = d / 8;
   for (int e = threadIdx.x; slot_ok && e < Hkv * oct; e += blockDim.x) {
     const int hk = e / oct, i0 = (e % oct) * 8;
-    float x[8], lo[4], hi[4];
-    qkv.get4(row, (Hq + Hkv + hk) * d + i0, lo);
-    qkv.get4(row, (Hq + Hkv + hk) * d + i0 + 4, hi);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      x[j] = lo[j];
-      x[4 + j] = hi[j];
-    }
+    float x[8];
+    qkv.get8(row, (Hq + Hkv + hk) * d + i0, x);
     fg::store8<DT>(v_cache, (int64_t)cb * cache_batch + (int64_t)hk * cache_head + (int64_t)slot * d + i0, x);
   }
 }
@@ -304,17 +313,18 @@ int rope_kv_write_launch(const char* what, const void* qkv, const float* part, i
              w + ": rows must be 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
   dim3 grid(batch * num_nodes);
-  if (dtype == fg::kBF16) {
-    const QkvSource<fg::kBF16> src{qkv, part, part_stride, splits, bias};
-    hipLaunchKernelGGL(rope_kv_write_kernel<fg::kBF16>, grid, dim3(256), 0, s, src, ld_qkv, num_nodes, q_heads,
-                       kv_heads, head_dim, seq_len, pos_offset, pos_batch_stride, inv_freq, q_out, k_cache, v_cache,
-                       cache_batch_stride, cache_head_stride, capacity, row_map, err_flag);
-  } else {
-    const QkvSource<fg::kF32> src{qkv, part, part_stride, splits, bias};
-    hipLaunchKernelGGL(rope_kv_write_kernel<fg::kF32>, grid, dim3(256), 0, s, src, ld_qkv, num_nodes, q_heads,
-                       kv_heads, head_dim, seq_len, pos_offset, pos_batch_stride, inv_freq, q_out, k_cache, v_cache,
-                       cache_batch_stride, cache_head_stride, capacity, row_map, err_flag);
+#define FG_ROPE(DTv, PARTSv)                                                                                     \
+  {                                                                                                              \
+    const QkvSource<DTv, PARTSv> src{qkv, part, part_stride, splits, bias};                                      \
+    hipLaunchKernelGGL((rope_kv_write_kernel<DTv, PARTSv>), grid, dim3(256), 0, s, src, ld_qkv, num_nodes, q_heads, \
+                       kv_heads, head_dim, seq_len, pos_offset, pos_batch_stride, inv_freq, q_out, k_cache, v_cache, \
+                       cache_batch_stride, cache_head_stride, capacity, row_map, err_flag);                       \
   }
+  if (dtype == fg::kBF16 && part) FG_ROPE(fg::kBF16, true)
+  else if (dtype == fg::kBF16) FG_ROPE(fg::kBF16, false)
+  else if (part) FG_ROPE(fg::kF32, true)
+  else FG_ROPE(fg::kF32, false)
+#undef FG_ROPE
   return fg::check_launch(what);
 }
 
