@@ -13,24 +13,26 @@
 // 172-180 runs the HF decoder layers).
 //
 // Tiling (gfx950): one workgroup of 4 waves (2 x 2, one per SIMD) per output tile of BM rows x 128
-// intermediate columns (BM = 64, 128, 192 or 256). The tile's 256 weight rows sit in LDS as [gate 64 | up 64 | gate 64 | up 64],
-// so the wave that owns output columns c .. c+63 holds both the gate and the up accumulators of
-// those columns and applies the activation in registers. K advances 64 per step through an NS-stage
-// LDS ring (the deepest that fits 160 KB: 4 stages for 64-row tiles, 3 for 128, 2 for 192 and
-// 256) filled by direct HBM->LDS buffer loads (`buffer_load_dwordx4 ... lds`, 1 KB = 8 rows
-// per instruction), rows of 128 bytes with the 16-byte chunks XOR-swizzled by row so that the
-// fragment reads of 32 consecutive rows hit distinct banks. Each k-step is four k16 sub-steps of
-// v_mfma_f32_32x32x16_bf16 (the wave's (BM/2) x 128 block is (BM/64) x 4 MFMA tiles, computed
-// transposed so each lane ends with 4 consecutive output columns of one row); the fragment reads
-// of sub-step s+1 are interleaved with the MFMAs of sub-step s, and the loads of k-step t+NS are
-// issued between the MFMAs of k-step t's last sub-step, after the one barrier of the step. When
-// every workgroup is resident at once (few rows), each runs a chain of hidden/64 steps whose time
-// per step is the load latency over the NS - 1 steps in flight: the shallow-tile, deep-ring
-// variants are for those shapes. The
-// output block of each wave goes out through LDS as whole 128-byte row segments.
+// intermediate columns (BM = 64, 128, 192 or 256). The tile's 256 weight rows sit in LDS as
+// [gate 64 | up 64 | gate 64 | up 64], so the wave that owns output columns c .. c+63 holds both
+// the gate and the up accumulators of those columns and applies the activation in registers.
+// K advances 64 per step through an NS-stage LDS ring (the deepest that fits 160 KB: 4 stages for
+// 64-row tiles, 3 for 128, 2 for 192 and 256) filled by direct HBM->LDS buffer loads
+// (`buffer_load_dwordx4 ... lds`, 1 KB = 8 rows per instruction), rows of 128 bytes with the
+// 16-byte chunks XOR-swizzled by row so that the fragment reads of 32 consecutive rows hit
+// distinct banks. Each k-step is four k16 sub-steps of v_mfma_f32_32x32x16_bf16 (the wave's
+// (BM/2) x 128 block is (BM/64) x 4 MFMA tiles, computed transposed so each lane ends with 4
+// consecutive output columns of one row); the fragment reads of sub-step s+1 are interleaved with
+// the MFMAs of sub-step s, and the loads of k-step t+NS are issued between the MFMAs of k-step t's
+// last sub-step, after the one barrier of the step. The output block of each wave goes out
+// through LDS as whole 128-byte row segments.
 // Workgroups are numbered so that each XCD takes a contiguous run of tiles along M for one weight
-// stripe: the stripe is read from HBM once per XCD and reused from its L2.
+// stripe: the stripe is read from HBM once per XCD and reused from its L2. Which tile height (or
+// the library projection + fg_swiglu) is fastest depends on the shape; the caller decides from
+// measurements.
 #include "fg_common.h"
+
+#include <algorithm>
 
 
 namespace {
@@ -65,7 +67,8 @@ struct MlpArgs {
   int tiles_m, tiles, per_xcd;
 };
 
-constexpr int stages_for(int bm) { return (int)((160 * 1024) / ((bm + kBN) * kRowBytes)) < 4 ? (int)((160 * 1024) / ((bm + kBN) * kRowBytes)) : 4; }
+// Ring depth of a BM-row tile: as many k-steps as fit the CU's 160 KB of LDS, at most 4.
+constexpr int stages_for(int bm) { return std::min(4, (160 * 1024) / ((bm + kBN) * kRowBytes)); }
 
 template <int BM>
 __global__ void __launch_bounds__(256, 1) gate_up_swiglu_kernel(MlpArgs p) {
