@@ -31,6 +31,8 @@
 // stripe and split: the stripe is read from HBM once per XCD and reused from its L2.
 #include "fg_common.h"
 
+#include <type_traits>
+
 
 namespace {
 
@@ -48,6 +50,31 @@ FG_DEVICE void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 FG_DEVICE void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4)); }
+
+// Wait until at most `steps` k-steps of this wave's loads (LPW each) are outstanding, for a
+// wave-uniform steps in [0, MAXS] (immediates for s_waitcnt; larger values wait for MAXS).
+template <int LPW, int MAXS>
+FG_DEVICE void wait_steps(int steps) {
+  if constexpr (MAXS >= 3) {
+    if (steps >= 3) {
+      wait_vmcnt<3 * LPW>();
+      return;
+    }
+  }
+  if constexpr (MAXS >= 2) {
+    if (steps >= 2) {
+      wait_vmcnt<2 * LPW>();
+      return;
+    }
+  }
+  if constexpr (MAXS >= 1) {
+    if (steps >= 1) {
+      wait_vmcnt<LPW>();
+      return;
+    }
+  }
+  wait_vmcnt<0>();
+}
 
 struct LinArgs {
   const uint16_t* x;  // [rows, ldx]
@@ -164,50 +191,60 @@ __global__ void __launch_bounds__(256, NS * (BM + BN) * kRowBytes <= 80 * 1024 ?
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // Prologue: k-steps 0 .. NS-1 in flight, wait for step 0. A k-step past the split's last one
-  // loads the last one again (L2-resident, into a slot never read), so every wait below waits
-  // for a fixed count.
-  const int last = nk - 1;
+  // Prologue: k-steps 0 .. min(NS, nk) - 1 in flight, wait for step 0.
+  const int first = min(NS, nk);
 #pragma unroll
   for (int h = 0; h < NS; ++h)
+    if (h < first) {
 #pragma unroll
-    for (int q = 0; q < LPW; ++q) issue(min(h, last), h, q);
-  wait_vmcnt<(NS - 1) * LPW>();
+      for (int q = 0; q < LPW; ++q) issue(h, h, q);
+    }
+  wait_steps<LPW, NS - 1>(first - 1);
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
   read(0, 0, 0);
 
   // k-step t in slot t % NS, which takes k-step t + NS once consumed.
-  auto step = [&](int t) __attribute__((always_inline)) {
+  auto step = [&](int t, auto with_load) __attribute__((always_inline)) {
     const int slot = t % NS;
 #pragma unroll
     for (int s = 0; s < kSub - 1; ++s) {
       read(slot, s + 1, (s + 1) & 1);
       mfma_step(s & 1);
     }
-    wait_lgkmcnt0();              // this wave's reads of the slot are done
-    wait_vmcnt<(NS - 2) * LPW>(); // k-step t + 1 has landed for this wave (t + 2 .. t + NS - 1 may not)
-    __builtin_amdgcn_s_barrier(); // ... and for every wave, and no wave still reads slot t
+    wait_lgkmcnt0();  // this wave's reads of the slot are done
+    // k-step t + 1 has landed for this wave; t + 2 .. min(t + NS - 1, nk - 1) may still load
+    if constexpr (decltype(with_load)::value)
+      wait_vmcnt<(NS - 2) * LPW>();
+    else
+      wait_steps<LPW, NS - 2>(min(NS - 2, nk - 2 - t));
+    __builtin_amdgcn_s_barrier();  // ... and for every wave, and no wave still reads slot t
     __builtin_amdgcn_sched_barrier(0);
     if (t + 1 < nk) read((t + 1) % NS, 0, 0);
-    const int next = min(t + NS, last);
+    constexpr bool load = decltype(with_load)::value;  // slot t takes k-step t + NS
     constexpr int kLast = (kSub - 1) & 1;
 #pragma unroll
     for (int i = 0; i < FN; ++i)
 #pragma unroll
       for (int k = 0; k < FM; ++k) {
         acc[i][k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(rb[kLast][i], ra[kLast][k], acc[i][k], 0, 0, 0);
-        if (i * FM + k < LPW) {
-          __builtin_amdgcn_sched_barrier(0);
-          issue(next, slot, i * FM + k);
-          __builtin_amdgcn_sched_barrier(0);
+        if constexpr (load) {
+          if (i * FM + k < LPW) {
+            __builtin_amdgcn_sched_barrier(0);
+            issue(t + NS, slot, i * FM + k);
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
       }
+    if constexpr (load) {
 #pragma unroll
-    for (int q = FM * FN; q < LPW; ++q) issue(next, slot, q);
+      for (int q = FM * FN; q < LPW; ++q) issue(t + NS, slot, q);
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
-  for (int t = 0; t < nk; ++t) step(t);
+  int t = 0;
+  for (; t + NS < nk; ++t) step(t, std::true_type{});  // NS - 1 steps in flight at each wait
+  for (; t < nk; ++t) step(t, std::false_type{});      // the tail: no more loads to issue
   wait_vmcnt<0>();  // no load still writing LDS when the workgroup ends
 
   // Epilogue: acc[i][k] lane l holds output row m0 + wm*WM + k*32 + l%32 and the columns

@@ -1,7 +1,7 @@
 """Regenerate the projection-path table (run on the MI355X it is meant for).
 
     python -m flashgrpo_amd.tuning.make_linear_table --out linear_mi355x.csv
-        [--presets qwen25_1p5b,...] [--rows 416,...] [--reps 10]
+        [--presets qwen25_1p5b,...] [--rows 416,...] [--kinds qkv,o,down] [--plan TM,TN,S,NS] [--reps 10]
 
 For the QKV, O and down projections of every bf16 target preset and a grid of row counts
 (powers of two plus the verify-round shapes of the benchmark workloads), it times the two ways
@@ -20,7 +20,8 @@ graph holding ``batch`` back-to-back calls, the weight rotating over enough copi
 ``reps`` times between events; a call's time is the fastest replay divided by ``batch``. (Events
 around single eager launches add the launch gaps, which would favour whichever path has the
 shorter kernels at small shapes.) One row per shape names the faster path and the best split-K
-tile and split count.
+tile and split count. ``--presets`` / ``--rows`` / ``--kinds`` restrict the run and ``--plan`` times
+one split-K plan instead of the sweep (a profiling run of one shape); the full table needs none.
 """
 from __future__ import annotations
 
@@ -62,7 +63,11 @@ def main():
     ap.add_argument("--reps", type=int, default=10)
     ap.add_argument("--presets", default="", help="comma-separated preset names (default: all)")
     ap.add_argument("--rows", default="", help="comma-separated row counts (default: the full grid)")
+    ap.add_argument("--kinds", default="", help="comma-separated projections: qkv, o, down (default: all)")
+    ap.add_argument("--plan", default="", help="tile_m,tile_n,splits,stages: time this split-K plan only")
     args = ap.parse_args()
+    only_kinds = {k for k in args.kinds.split(",") if k}
+    plan = tuple(int(v) for v in args.plan.split(",")) if args.plan else None
     only_presets = {p for p in args.presets.split(",") if p}
     only_rows = {int(r) for r in args.rows.split(",") if r}
     import torch
@@ -104,6 +109,8 @@ def main():
         inv = inv_freq_table(d, cfg.rope_theta).to(dev)
         kinds = (("qkv", (Hq + 2 * Hkv) * d, H), ("o", H, Hq * d), ("down", H, cfg.intermediate))
         for kind, N, Kd in kinds:
+            if only_kinds and kind not in only_kinds:
+                continue
             g = torch.Generator(device=dev).manual_seed(N + Kd)
             copies = min(32, max(2, -(-512 * 2 ** 20 // (N * Kd * 2))))
             batch = max(copies, 8)
@@ -152,7 +159,7 @@ def main():
 
                 t_lib = best(library, batch)
                 top = None
-                for tm, tn, s, ns in split_candidates(K, rows, N, Kd):
+                for tm, tn, s, ns in ([plan] if plan else split_candidates(K, rows, N, Kd)):
                     buf = torch.empty(s, rows, N, dtype=torch.float32, device=dev)
                     t = best(split_k(tm, tn, s, ns, buf), batch)
                     del buf
