@@ -206,19 +206,24 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(void* __restrict__ x, cons
   }
 }
 
-// out[t, i] = silu(gu[t, i]) * gu[t, F + i]; 8 elements per thread, one grid row
-// per token. Requires F % 8 == 0. In bf16, SiLU(gate) is rounded to bf16 before the
-// product, as the Hugging Face MLP computes act_fn(gate) * up under bf16 autocast.
+// out[t, i] = silu(gu[t, i]) * gu[t, F + i]; 8 elements per thread over a flat grid of
+// rows x F/8 chunks (a grid row per token left the last workgroup of each row partly idle:
+// 34.8 against 33.2 µs at the Qwen2.5-7B shape). Requires F % 8 == 0. In bf16, SiLU(gate) is
+// rounded to bf16 before the product, as the Hugging Face MLP computes act_fn(gate) * up under
+// bf16 autocast.
 FG_DEVICE float silu_in(float g, int dt) {
   const float s = fg::silu_f32(g);
   return dt == fg::kBF16 ? fg::round_bf16(s) : s;
 }
 
 template <int DT>
-__global__ void __launch_bounds__(256) swiglu_kernel(const void* __restrict__ gu, void* __restrict__ out, int F) {
-  const int ch = blockIdx.x * 256 + threadIdx.x;
-  if (ch * 8 >= F) return;
-  const int64_t t = blockIdx.y;
+__global__ void __launch_bounds__(256) swiglu_kernel(const void* __restrict__ gu, void* __restrict__ out, int F,
+                                                     int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int chunks = F / 8;
+  const int64_t t = i / chunks;
+  const int ch = (int)(i - t * chunks);
   float g[8], u[8], o[8];
   fg::load8<DT>(gu, t * 2 * F + ch * 8, g);
   fg::load8<DT>(gu, t * 2 * F + F + ch * 8, u);
@@ -401,13 +406,14 @@ int fg_swiglu(const void* gate_up, void* out, int dtype, int rows, int inter, vo
   FG_REQUIRE(gate_up && out && rows > 0 && inter > 0, "fg_swiglu: bad arguments");
   FG_REQUIRE(inter % 8 == 0 && ((uintptr_t)gate_up & 15) == 0 && ((uintptr_t)out & 15) == 0,
              "fg_swiglu: intermediate size must be a multiple of 8 with 16-byte aligned rows");
-  FG_REQUIRE(rows <= 65535, "fg_swiglu: at most 65535 rows per call");
-  dim3 grid((unsigned)((inter / 8 + 255) / 256), (unsigned)rows);
+  const int64_t total = (int64_t)rows * (inter / 8);
+  FG_REQUIRE((total + 255) / 256 < (1ll << 31), "fg_swiglu: too many rows for one call");
+  const dim3 grid((unsigned)((total + 255) / 256));
   hipStream_t s = (hipStream_t)stream;
   if (dtype == fg::kBF16)
-    hipLaunchKernelGGL(swiglu_kernel<fg::kBF16>, grid, dim3(256), 0, s, gate_up, out, inter);
+    hipLaunchKernelGGL(swiglu_kernel<fg::kBF16>, grid, dim3(256), 0, s, gate_up, out, inter, total);
   else
-    hipLaunchKernelGGL(swiglu_kernel<fg::kF32>, grid, dim3(256), 0, s, gate_up, out, inter);
+    hipLaunchKernelGGL(swiglu_kernel<fg::kF32>, grid, dim3(256), 0, s, gate_up, out, inter, total);
   return fg::check_launch("fg_swiglu");
 }
 
