@@ -351,11 +351,19 @@ def rmsnorm(x, weight, eps, *, delta=None, out=None):
 
 
 def swiglu(gate_up, *, out=None):
+    """SiLU(gate_up[:, :F]) * gate_up[:, F:] (``fg_swiglu``): gate_up a contiguous [rows, 2F]
+    tensor (F a multiple of 8), out a contiguous [rows, F] tensor of the same dtype."""
     _dev(gate_up)
+    if gate_up.dim() != 2 or gate_up.shape[1] % 16 or not gate_up.is_contiguous():
+        raise ValueError("swiglu: gate_up must be a contiguous [rows, 2F] tensor with F a multiple of 8")
     rows, two_f = gate_up.shape
     F = two_f // 2
     if out is None:
         out = torch.empty(rows, F, dtype=gate_up.dtype, device=gate_up.device)
+    elif tuple(out.shape) != (rows, F) or out.dtype != gate_up.dtype or not out.is_contiguous():
+        raise ValueError(f"swiglu: out must be a contiguous [{rows}, {F}] tensor of the input dtype")
+    if rows == 0:
+        return out
     _call("fg_swiglu", _ptr(gate_up), _ptr(out), dtype_code(gate_up), rows, F, _stream())
     return out
 

@@ -100,6 +100,15 @@ def test_swiglu_matches_the_mlp_activation():
     assert frac_equal(got, want) >= 0.999
     once = (F.silu(gu[:, :I].float()) * gu[:, I:].float()).to(BF)
     assert frac_equal(once, want) < 0.9
+    # the flat grid reads rows of 2F and writes rows of F: other layouts are refused on the host
+    with pytest.raises(ValueError):
+        K().swiglu(gu[:, 8:8 + 2 * 96])  # a column slice (row stride 2I, not 2F)
+    with pytest.raises(ValueError):
+        K().swiglu(gu, out=torch.empty(200, 2 * I, dtype=BF, device=DEV)[:, :I])
+    with pytest.raises(ValueError):
+        K().swiglu(torch.zeros(4, 2 * 100, dtype=BF, device=DEV))  # F not a multiple of 8
+    part = K().swiglu(gu[:64])  # a row slice is contiguous
+    assert torch.equal(part, got[:64])
 
 
 def test_medusa_block_matches_the_reference_head_under_autocast():
