@@ -299,6 +299,16 @@ def rope_kv_write(qkv, *, batch, num_nodes, q_heads, kv_heads, head_dim, seq_len
     _i32(row_map, "row_map")
     if k_cache.stride(-1) != 1 or k_cache.stride(-2) != head_dim:
         raise ValueError("rope_kv_write: cache rows must be contiguous [.., capacity, d]")
+    if v_cache.stride() != k_cache.stride() or v_cache.shape != k_cache.shape or v_cache.dtype != k_cache.dtype:
+        raise ValueError("rope_kv_write: v_cache must have k_cache's shape, strides and dtype")
+    width = (q_heads + 2 * kv_heads) * head_dim
+    if qkv.dtype != k_cache.dtype or qkv.stride(-1) != 1 or qkv.shape[-1] < width or \
+            qkv.numel() // qkv.shape[-1] != batch * num_nodes:
+        raise ValueError(f"rope_kv_write: qkv must hold {batch * num_nodes} rows of >= {width} unit-stride values "
+                         "in the cache dtype")
+    if not q_out.is_contiguous() or q_out.numel() != batch * num_nodes * q_heads * head_dim or \
+            q_out.dtype != k_cache.dtype:
+        raise ValueError("rope_kv_write: q_out must be a contiguous [batch * num_nodes, q_heads, d] tensor")
     if pos_offset.dim() == 2:
         if tuple(pos_offset.shape) != (batch, num_nodes) or not pos_offset.is_contiguous():
             raise ValueError("rope_kv_write: per-sequence pos_offset must be contiguous [batch, num_nodes]")
@@ -340,11 +350,21 @@ def tree_attention(q, k_cache, v_cache, *, seq_len, anc, num_nodes, q_heads, kv_
 
 
 def rmsnorm(x, weight, eps, *, delta=None, out=None):
+    """RMSNorm(x [+ delta]) * weight over the last dimension (``fg_rmsnorm``); with delta the
+    sum is written back to x first. x, delta and out contiguous, one dtype, one shape."""
     _dev(x, weight, delta)
     H = x.shape[-1]
     rows = x.numel() // H
+    if not x.is_contiguous() or weight.numel() != H or weight.dtype != x.dtype or not weight.is_contiguous():
+        raise ValueError("rmsnorm: x must be contiguous and weight a contiguous [H] tensor of its dtype")
+    if delta is not None and (delta.shape != x.shape or delta.dtype != x.dtype or not delta.is_contiguous()):
+        raise ValueError("rmsnorm: delta must be a contiguous tensor of x's shape and dtype")
     if out is None:
         out = torch.empty_like(x)
+    elif out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
+        raise ValueError("rmsnorm: out must be a contiguous tensor of x's shape and dtype")
+    if rows == 0:
+        return out
     _call("fg_rmsnorm", _ptr(x), _ptr(delta), _ptr(weight), _ptr(out), dtype_code(x), rows, H, float(eps),
               _stream())
     return out
