@@ -746,6 +746,9 @@ def main():
     ap.add_argument("--cpu-rounds", type=int, default=None,
                     help="verify rounds the CPU oracle runs (default: 32 for the tiny config, 1 otherwise)")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--decoder-gemms", default="table", choices=("table", "hand", "library"),
+                    help="decoder projections: as the measured path tables choose (default), all on the "
+                         "hand-written split-K / fused MLP kernels, or all on hipBLASLt")
     ap.add_argument("--roofline-kernel", default="fg_tree_attention",
                     help="C-ABI entry point whose launches are event-timed in the timed rounds")
     ap.add_argument("--roofline-every", type=int, default=7,
@@ -805,6 +808,10 @@ def main():
     elem = 4 if dtype == torch.float32 else 2
     log = lambda msg: print(f"bench: {msg}", file=sys.stderr, flush=True)
     cfg, model, heads, dec = build(work, dtype, seed=args.seed)
+    if args.decoder_gemms != "table":
+        hand = args.decoder_gemms == "hand"
+        model.split_k_linear = hand  # QKV, O, down: fg_linear_parts + its finishing kernels, or the library
+        model.fused_mlp = hand       # gate/up: fg_gate_up_swiglu, or the library projection + fg_swiglu
     log(f"built {work['name']} ({dtype})")
     g = torch.Generator().manual_seed(args.seed + 3)
     prompts = torch.randint(0, cfg.vocab, (work["prompts"], work["prefix"]), generator=g)
@@ -992,7 +999,8 @@ def main():
                    "tree_nodes": rounds[-1]["num_nodes"], "internal_nodes": rounds[-1]["internal"],
                    "topk_by_depth": r.plan_last.get("topk_by_depth"), "temperature": work["temperature"],
                    "top_p": work["top_p"], "parallelism": "single GPU",
-                   "verify_forward": "HIP graph replay (eager in the roofline-timed rounds)"},
+                   "verify_forward": "HIP graph replay (eager in the roofline-timed rounds)",
+                   "decoder_gemms": args.decoder_gemms},
         "tokens": int(tokens),
         "accept_len_mean": round(tokens / max(sum(x["batch"] for x in rounds), 1), 4),
         "prefill_s": round(prefill_s, 2),

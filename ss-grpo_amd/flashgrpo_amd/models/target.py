@@ -31,7 +31,8 @@ import torch.nn.functional as F
 
 from .. import kernels as K
 from .. import timing
-from ..tuning import linear_table_plan, mlp_table_path, use_tuned_gemms
+from ..tuning import (linear_table_plan, linear_table_split_plan, mlp_table_fused_tile, mlp_table_path,
+                      use_tuned_gemms)
 
 MAX_TREE_NODES = 64      # tree nodes per forward (64-bit ancestor masks)
 MAX_CHAIN_TOKENS = 8192  # new tokens per forward without masks (a causal chain)
@@ -480,12 +481,14 @@ class TargetModel:
         self._hf_source = None  # the Hugging Face model the weights were read from (from_hf)
         self._hf_key = None
         # the MLP's gate/up projection and SwiGLU as one GEMM (fg_gate_up_swiglu): None chooses per
-        # shape (mlp_path), True wherever the operands allow, False never (the hipBLASLt
-        # projection, then fg_swiglu); call drop_graphs() after a change
+        # shape (mlp_path), True wherever the operands allow (at the shape's fastest measured tile
+        # height, else the kernel's pick), False never (the hipBLASLt projection, then fg_swiglu);
+        # call drop_graphs() after a change
         self.fused_mlp = None
         # the QKV, O and down projections as split-K GEMMs (fg_linear_parts) finished by the rotary
         # + cache write or the residual add + RMSNorm: None chooses per shape (linear_path), True
-        # wherever the operands allow (default_linear_plan), False never; drop_graphs() after a change
+        # wherever the operands allow (the shape's best measured split-K plan, else
+        # default_linear_plan), False never; drop_graphs() after a change
         self.split_k_linear = None
         if self.device.type == "cuda":
             use_tuned_gemms()
@@ -724,7 +727,8 @@ class TargetModel:
             if self.fused_mlp is None:
                 path = mlp_path(T, cfg.intermediate, H, h2.device)
             else:
-                path = -1 if self.fused_mlp else 0
+                # forced fused: the fastest measured tile height of the shape, else the kernel's pick
+                path = (mlp_table_fused_tile(T, cfg.intermediate, H) or -1) if self.fused_mlp else 0
             if path and K.gate_up_swiglu_ok(h2, lw["gate_up_w"]):
                 K.gate_up_swiglu(h2, lw["gate_up_w"], out=act, tile_rows=max(path, 0))
             else:
@@ -747,8 +751,9 @@ class TargetModel:
         if self.split_k_linear is False or not K.linear_ok(x, w):
             return None
         rows, hidden = x.shape
-        if self.split_k_linear:
-            return default_linear_plan(rows, w.shape[0], hidden, _cu_count(x.device))
+        if self.split_k_linear:  # forced: the best measured split-K plan of the shape, else the default
+            return (linear_table_split_plan(kind, rows, w.shape[0], hidden)
+                    or default_linear_plan(rows, w.shape[0], hidden, _cu_count(x.device)))
         return linear_path(kind, rows, w.shape[0], hidden)
 
     def _linear_parts(self, x: torch.Tensor, w: torch.Tensor, plan) -> torch.Tensor:

@@ -36,21 +36,39 @@ _mlp = {}
 _CHOICE = {"pair": 0, "fused64": 64, "fused128": 128, "fused192": 192, "fused256": 256}
 
 
+def _nearest(cands, rows: int):
+    """The value of the (rows, value) entry nearest to ``rows`` on a log scale (ties to the larger count)."""
+    import math
+
+    lr = math.log(max(int(rows), 1))
+    return min(cands, key=lambda e: (abs(math.log(e[0]) - lr), -e[0]))[1]
+
+
+def _mlp_read() -> None:
+    """Reads the MLP path table once: (inter, hidden) -> sorted [(rows, path)] of the fastest
+    path, and -> sorted [(rows, tile height)] of the fastest fused GEMM."""
+    entries, fused = {}, {}
+    choice = os.environ.get("FLASHGRPO_AMD_MLP_TABLE", "")
+    path = DEFAULT_MLP_TABLE if not choice else (None if choice.lower() == "off" else choice)
+    if path and os.path.exists(path):
+        with open(path) as f:
+            header = f.readline().strip().split(",")
+            for line in f:
+                row = dict(zip(header, line.strip().split(",")))
+                if row.get("choice") in _CHOICE:
+                    key = (int(row["inter"]), int(row["hidden"]))
+                    entries.setdefault(key, []).append((int(row["rows"]), _CHOICE[row["choice"]]))
+                    tiles = [(float(row[f"fused{t}_us"]), t) for t in (64, 128, 192, 256) if f"fused{t}_us" in row]
+                    if tiles:
+                        fused.setdefault(key, []).append((int(row["rows"]), min(tiles)[1]))
+    _mlp.setdefault("entries", {k: sorted(v) for k, v in entries.items()})
+    _mlp.setdefault("fused", {k: sorted(v) for k, v in fused.items()})
+
+
 def _mlp_entries() -> dict:
     """(inter, hidden) -> sorted [(rows, path)] from the MLP path table (read once)."""
     if "entries" not in _mlp:
-        entries = {}
-        choice = os.environ.get("FLASHGRPO_AMD_MLP_TABLE", "")
-        path = DEFAULT_MLP_TABLE if not choice else (None if choice.lower() == "off" else choice)
-        if path and os.path.exists(path):
-            with open(path) as f:
-                header = f.readline().strip().split(",")
-                for line in f:
-                    row = dict(zip(header, line.strip().split(",")))
-                    if row.get("choice") in _CHOICE:
-                        key = (int(row["inter"]), int(row["hidden"]))
-                        entries.setdefault(key, []).append((int(row["rows"]), _CHOICE[row["choice"]]))
-        _mlp["entries"] = {k: sorted(v) for k, v in entries.items()}
+        _mlp_read()
     return _mlp["entries"]
 
 
@@ -59,37 +77,49 @@ def mlp_table_path(rows: int, inter: int, hidden: int):
     tile height (64 / 128 / 192 / 256), taken from the table entry of these sizes nearest in row count on a log
     scale (ties to the larger count); None when the table has no entry for (inter, hidden)."""
     cands = _mlp_entries().get((int(inter), int(hidden)))
-    if not cands:
-        return None
-    import math
+    return _nearest(cands, rows) if cands else None
 
-    lr = math.log(max(int(rows), 1))
-    return min(cands, key=lambda e: (abs(math.log(e[0]) - lr), -e[0]))[1]
+
+def mlp_table_fused_tile(rows: int, inter: int, hidden: int):
+    """The fused GEMM's fastest measured tile height for this shape (nearest entry, as
+    ``mlp_table_path``), whichever path the table chose; None when the table has no entry."""
+    if "fused" not in _mlp:
+        _mlp_read()
+    cands = _mlp["fused"].get((int(inter), int(hidden)))
+    return _nearest(cands, rows) if cands else None
 
 
 _lin = {}
+
+
+def _linear_read() -> None:
+    """Reads the projection path table once: (kind, cols, hidden) -> sorted [(rows, plan)] with
+    plan (tile_m, tile_n, splits, stages) for the split-K kernel or () for the library, and
+    -> sorted [(rows, split-K plan)] of the best measured split-K plan whichever path won."""
+    entries, split = {}, {}
+    choice = os.environ.get("FLASHGRPO_AMD_LINEAR_TABLE", "")
+    path = DEFAULT_LINEAR_TABLE if not choice else (None if choice.lower() == "off" else choice)
+    if path and os.path.exists(path):
+        with open(path) as f:
+            header = f.readline().strip().split(",")
+            for line in f:
+                row = dict(zip(header, line.strip().split(",")))
+                if row.get("choice") not in ("library", "split_k"):
+                    continue
+                # a table without a stages column was measured with the 2-stage ring
+                sk = (int(row["tile_m"]), int(row["tile_n"]), int(row["splits"]), int(row.get("stages", 2)))
+                key = (row["kind"], int(row["cols"]), int(row["hidden"]))
+                entries.setdefault(key, []).append((int(row["rows"]), sk if row["choice"] == "split_k" else ()))
+                split.setdefault(key, []).append((int(row["rows"]), sk))
+    _lin.setdefault("entries", {k: sorted(v) for k, v in entries.items()})
+    _lin.setdefault("split", {k: sorted(v) for k, v in split.items()})
 
 
 def _linear_entries() -> dict:
     """(kind, cols, hidden) -> sorted [(rows, plan)] from the projection path table (read once);
     plan is (tile_m, tile_n, splits, stages) for the split-K kernel or () for the library."""
     if "entries" not in _lin:
-        entries = {}
-        choice = os.environ.get("FLASHGRPO_AMD_LINEAR_TABLE", "")
-        path = DEFAULT_LINEAR_TABLE if not choice else (None if choice.lower() == "off" else choice)
-        if path and os.path.exists(path):
-            with open(path) as f:
-                header = f.readline().strip().split(",")
-                for line in f:
-                    row = dict(zip(header, line.strip().split(",")))
-                    if row.get("choice") not in ("library", "split_k"):
-                        continue
-                    # a table without a stages column was measured with the 2-stage ring
-                    plan = ((int(row["tile_m"]), int(row["tile_n"]), int(row["splits"]), int(row.get("stages", 2)))
-                            if row["choice"] == "split_k" else ())
-                    key = (row["kind"], int(row["cols"]), int(row["hidden"]))
-                    entries.setdefault(key, []).append((int(row["rows"]), plan))
-        _lin["entries"] = {k: sorted(v) for k, v in entries.items()}
+        _linear_read()
     return _lin["entries"]
 
 
@@ -103,10 +133,16 @@ def linear_table_plan(kind: str, rows: int, cols: int, hidden: int):
         return None
     if int(rows) > 2 * cands[-1][0]:
         return ()
-    import math
+    return _nearest(cands, rows)
 
-    lr = math.log(max(int(rows), 1))
-    return min(cands, key=lambda e: (abs(math.log(e[0]) - lr), -e[0]))[1]
+
+def linear_table_split_plan(kind: str, rows: int, cols: int, hidden: int):
+    """The best measured split-K plan for this shape (nearest entry, as ``linear_table_plan``),
+    whichever path the table chose; None when the table has no such entry."""
+    if "split" not in _lin:
+        _linear_read()
+    cands = _lin["split"].get((kind, int(cols), int(hidden)))
+    return _nearest(cands, rows) if cands else None
 
 
 def use_tuned_gemms(path: str | None = None) -> bool:

@@ -61,3 +61,17 @@ def test_default_plan_satisfies_the_kernel_rules():
         tm, tn, s, ns = default_linear_plan(rows_, cols, hidden)
         assert tm in K.LINEAR_TILES and tn in K.LINEAR_TILES and ns in (2, 3, 4)
         assert K.linear_splits(hidden, s) == s
+
+
+@pytest.mark.skipif(not os.path.exists(TABLE), reason="no projection path table")
+def test_split_plan_lookup_returns_the_measured_split_k_plan_whichever_path_won():
+    for r in rows():
+        plan = tuning.linear_table_split_plan(r["kind"], int(r["rows"]), int(r["cols"]), int(r["hidden"]))
+        assert plan == (int(r["tile_m"]), int(r["tile_n"]), int(r["splits"]), int(r["stages"]))
+
+
+def test_split_plan_lookup_nearest_row_count(monkeypatch):
+    monkeypatch.setitem(tuning._lin, "split", {("o", 64, 128): [(64, (64, 64, 2, 4)), (256, (128, 64, 1, 4))]})
+    assert tuning.linear_table_split_plan("o", 100, 64, 128) == (64, 64, 2, 4)
+    assert tuning.linear_table_split_plan("o", 10 ** 6, 64, 128) == (128, 64, 1, 4)  # no library cut-off
+    assert tuning.linear_table_split_plan("qkv", 64, 64, 128) is None

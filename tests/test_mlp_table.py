@@ -46,3 +46,18 @@ def test_lookup_takes_the_nearest_row_count_on_a_log_scale(monkeypatch):
     assert tuning.mlp_table_path(1, 100, 64) == 0
     assert tuning.mlp_table_path(64, 101, 64) is None         # sizes not in the table
     assert math.isclose(math.log(128) - math.log(64), math.log(256) - math.log(128))
+
+
+@pytest.mark.skipif(not os.path.exists(TABLE), reason="no MLP path table")
+def test_fused_tile_lookup_is_the_fastest_measured_tile_height():
+    for r in rows():
+        t = {h: float(r[f"fused{h}_us"]) for h in (64, 128, 192, 256)}
+        got = tuning.mlp_table_fused_tile(int(r["rows"]), int(r["inter"]), int(r["hidden"]))
+        assert t[got] == min(t.values()), r
+
+
+def test_fused_tile_lookup_nearest_row_count(monkeypatch):
+    monkeypatch.setitem(tuning._mlp, "fused", {(100, 64): [(64, 64), (1024, 256)]})
+    assert tuning.mlp_table_fused_tile(100, 100, 64) == 64
+    assert tuning.mlp_table_fused_tile(5000, 100, 64) == 256
+    assert tuning.mlp_table_fused_tile(64, 101, 64) is None
