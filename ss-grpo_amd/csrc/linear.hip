@@ -87,9 +87,26 @@ struct LinArgs {
   int nks;            // k-steps in total (hidden / 64)
   int ks_per_split;
   int tiles_m, tiles_n, tiles, per_xcd;
+  // ROPE epilogue (one split): the QKV projection's bias, rotary embedding and KV-slot write. The
+  // weight rows (and bias) of every q and k head are pair-interleaved: row 2j of a head holds its
+  // original row j and row 2j + 1 its row j + d/2, so each lane's 4 consecutive output columns
+  // are two whole rotary pairs; v heads keep their order.
+  const uint16_t* bias;  // [cols] bf16 in the weight's row order, or null
+  int num_nodes, q_heads, kv_heads, head_dim;
+  const int32_t* seq_len;
+  const int32_t* pos_offset;
+  int64_t pos_stride;
+  const float* inv_freq;
+  uint16_t* q_out;  // [rows, q_heads, d]
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  int64_t cache_batch, cache_head;
+  int capacity;
+  const int32_t* row_map;
+  int32_t* err_flag;
 };
 
-template <int BM, int BN, int NS>
+template <int BM, int BN, int NS, bool ROPE = false>
 __global__ void __launch_bounds__(256, NS * (BM + BN) * kRowBytes <= 80 * 1024 ? 2 : 1)
     linear_parts_kernel(LinArgs p) {
   constexpr int WM = BM / 2, WN = BN / 2;
@@ -98,7 +115,9 @@ __global__ void __launch_bounds__(256, NS * (BM + BN) * kRowBytes <= 80 * 1024 ?
   constexpr int LA = BM / 32, LB = BN / 32, LPW = LA + LB;  // 1 KB loads per wave per step
   static_assert(FM >= 1 && FN >= 1 && LA * 4 * 8 == BM && LB * 4 * 8 == BN, "tile sizes: multiples of 64");
   static_assert(NS >= 2 && NS * STAGE <= 160 * 1024 && (NS - 1) * LPW < 64, "ring stages: LDS and vmcnt");
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * STAGE];
+  // ROPE: the epilogue's per-row positions and cos / sin table [BM][BN/2] after the ring is idle
+  constexpr int ROPE_LDS = ROPE ? 1024 + BM * (BN / 2) * 8 : 0;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * STAGE > ROPE_LDS ? NS * STAGE : ROPE_LDS];
 
   // XCD-aware order: workgroup b runs on XCD b % 8; XCD x takes tiles x*per_xcd .. +per_xcd-1,
   // which walk down M for one (weight stripe, split) before the next.
@@ -113,6 +132,24 @@ __global__ void __launch_bounds__(256, NS * (BM + BN) * kRowBytes <= 80 * 1024 ?
   const int tid = threadIdx.x, lane = tid & 63, l32 = lane & 31, half = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
+
+  // ROPE: each lane's rows (one per 32-row MFMA tile) -> cache slot and cache row, and thread t < BM
+  // -> the position of tile row t, loaded before the main loop so the loads land while it runs.
+  int r_slot[ROPE ? FM : 1], r_cb[ROPE ? FM : 1], t_pos = 0;
+  if constexpr (ROPE) {
+#pragma unroll
+    for (int k = 0; k < FM; ++k) {
+      const int m = min(m0 + wm * WM + k * 32 + l32, p.rows - 1);
+      const int b = m / p.num_nodes;
+      r_slot[k] = p.seq_len[b] + m - b * p.num_nodes;
+      r_cb[k] = p.row_map ? p.row_map[b] : b;
+    }
+    if (tid < BM) {
+      const int m = min(m0 + tid, p.rows - 1);
+      const int b = m / p.num_nodes, n = m - b * p.num_nodes;
+      t_pos = p.seq_len[b] + p.pos_offset[(int64_t)b * p.pos_stride + n];
+    }
+  }
 
   // Buffer descriptors: rows past the matrix end read as zero (rows >= p.rows, columns >= p.cols).
   const int64_t x_bytes = (int64_t)(p.rows - m0) * p.ldx * 2;
@@ -250,6 +287,77 @@ __global__ void __launch_bounds__(256, NS * (BM + BN) * kRowBytes <= 80 * 1024 ?
   // Epilogue: acc[i][k] lane l holds output row m0 + wm*WM + k*32 + l%32 and the columns
   // n0 + wn*WN + i*32 + 8g + 4*(l/32) + 0..3 in elements 4g..4g+3: 16-byte fp32 stores, the two
   // half-waves of a row writing 32 contiguous bytes.
+  if constexpr (ROPE) {
+    // v = bf16(sum + bias) as the projection's output; q/k pairs (x1, x2) rotated as the rotary
+    // kernel rotates them (each product and the sum rounded to bf16, cos / sin rounded to bf16);
+    // q rows to q_out, k and v rows to their cache slot (slots outside the cache flag an error).
+    const int d = p.head_dim, half_d = d / 2;
+    // cos / sin of every (tile row, column pair) in LDS, rounded to bf16 as the rotary kernel rounds
+    // them: the ring is idle after the last step's barrier, the table is read after the next one
+    int* s_pos = (int*)smem;
+    float2* s_cs = (float2*)(smem + 1024);
+    if (tid < BM) s_pos[tid] = t_pos;
+    __syncthreads();
+    for (int e = tid; e < BM * (BN / 2); e += 256) {
+      const int r = e / (BN / 2), jj = e - r * (BN / 2);
+      const int j = ((n0 + 2 * jj) % d) / 2;
+      const float ang = (float)s_pos[r] * p.inv_freq[j];
+      s_cs[e] = make_float2(fg::round_bf16(cosf(ang)), fg::round_bf16(sinf(ang)));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < FM; ++k) {
+      const int m = m0 + wm * WM + k * 32 + l32;
+      if (m >= p.rows) continue;
+      const bool slot_ok = r_slot[k] >= 0 && r_slot[k] < p.capacity;
+      if (!slot_ok && p.err_flag) atomicOr(p.err_flag, 8);
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = n0 + wn * WN + i * 32 + 8 * g + 4 * half;
+          if (n >= p.cols) continue;
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float bv = p.bias ? fg::bf16_to_f32(p.bias[n + e]) : 0.0f;
+            v[e] = fg::round_bf16(acc[i][k][4 * g + e] + bv);
+          }
+          const int h = n / d, c = n - h * d;
+          if (h >= p.q_heads + p.kv_heads) {  // a v head: columns in order
+            if (slot_ok)
+              *(uint2*)(p.v_cache + (int64_t)r_cb[k] * p.cache_batch +
+                        (int64_t)(h - p.q_heads - p.kv_heads) * p.cache_head + (int64_t)r_slot[k] * d + c) =
+                  make_uint2(fg::pack_bf16x2(v[0], v[1]), fg::pack_bf16x2(v[2], v[3]));
+            continue;
+          }
+          const int j = c / 2;  // pairs j and j + 1: (v[0], v[1]) and (v[2], v[3])
+          float y1[2], y2[2];
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const float2 t = s_cs[(wm * WM + k * 32 + l32) * (BN / 2) + (n - n0) / 2 + q];
+            const float cs = t.x, sn = t.y;
+            const float x1 = v[2 * q], x2 = v[2 * q + 1];
+            {
+#pragma clang fp contract(off)
+              y1[q] = fg::round_bf16(fg::round_bf16(x1 * cs) - fg::round_bf16(x2 * sn));
+              y2[q] = fg::round_bf16(fg::round_bf16(x2 * cs) + fg::round_bf16(x1 * sn));
+            }
+          }
+          uint16_t* dst;
+          if (h < p.q_heads) {
+            dst = p.q_out + ((int64_t)m * p.q_heads + h) * d;
+          } else {
+            if (!slot_ok) continue;
+            dst = p.k_cache + (int64_t)r_cb[k] * p.cache_batch + (int64_t)(h - p.q_heads) * p.cache_head +
+                  (int64_t)r_slot[k] * d;
+          }
+          *(uint32_t*)(dst + j) = fg::pack_bf16x2(y1[0], y1[1]);
+          *(uint32_t*)(dst + j + half_d) = fg::pack_bf16x2(y2[0], y2[1]);
+        }
+    }
+    return;
+  }
   float* dst = p.part + (int64_t)split * p.part_stride;
 #pragma unroll
   for (int k = 0; k < FM; ++k) {
@@ -267,21 +375,33 @@ __global__ void __launch_bounds__(256, NS * (BM + BN) * kRowBytes <= 80 * 1024 ?
   }
 }
 
-template <int BM, int BN, int NS>
+template <int BM, int BN, int NS, bool ROPE>
 void launch(LinArgs p, hipStream_t s) {
   p.tiles_m = (p.rows + BM - 1) / BM;
   p.tiles_n = (p.cols + BN - 1) / BN;
   const int splits = (p.nks + p.ks_per_split - 1) / p.ks_per_split;
   p.tiles = p.tiles_m * p.tiles_n * splits;
   p.per_xcd = (p.tiles + 7) / 8;
-  hipLaunchKernelGGL((linear_parts_kernel<BM, BN, NS>), dim3(8 * p.per_xcd), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((linear_parts_kernel<BM, BN, NS, ROPE>), dim3(8 * p.per_xcd), dim3(256), 0, s, p);
 }
 
-template <int BM, int BN>
+template <int BM, int BN, bool ROPE = false>
 void launch_stages(LinArgs p, int stages, hipStream_t s) {
-  if (stages == 2) launch<BM, BN, 2>(p, s);
-  else if (stages == 3) launch<BM, BN, 3>(p, s);
-  else launch<BM, BN, 4>(p, s);
+  if (stages == 2) launch<BM, BN, 2, ROPE>(p, s);
+  else if (stages == 3) launch<BM, BN, 3, ROPE>(p, s);
+  else launch<BM, BN, 4, ROPE>(p, s);
+}
+
+template <bool ROPE>
+void launch_tiles(LinArgs p, int tile_m, int tile_n, int stages, hipStream_t s) {
+  if (tile_m == 64 && tile_n == 64)
+    launch_stages<64, 64, ROPE>(p, stages, s);
+  else if (tile_m == 64)
+    launch_stages<64, 128, ROPE>(p, stages, s);
+  else if (tile_n == 64)
+    launch_stages<128, 64, ROPE>(p, stages, s);
+  else
+    launch_stages<128, 128, ROPE>(p, stages, s);
 }
 
 // x[r] = bf16(x[r] + bf16(sum_s part[s][r])); h[r] = RMSNorm(x[r]) * g. One workgroup per row,
@@ -374,17 +494,65 @@ int fg_linear_parts(const void* x, int64_t ldx, const void* w, int64_t ldw, floa
   p.cols = cols;
   p.nks = nks;
   p.ks_per_split = per;
-  hipStream_t s = (hipStream_t)stream;
-  const int ns = stages ? stages : 4;
-  if (tile_m == 64 && tile_n == 64)
-    launch_stages<64, 64>(p, ns, s);
-  else if (tile_m == 64)
-    launch_stages<64, 128>(p, ns, s);
-  else if (tile_n == 64)
-    launch_stages<128, 64>(p, ns, s);
-  else
-    launch_stages<128, 128>(p, ns, s);
+  launch_tiles<false>(p, tile_m, tile_n, stages ? stages : 4, (hipStream_t)stream);
   return fg::check_launch("fg_linear_parts");
+}
+
+int fg_linear_rope_kv_write(const void* x, int64_t ldx, const void* w_pairs, int64_t ldw, const void* bias_pairs,
+                            int rows, int hidden, int tile_m, int tile_n, int stages, int batch, int num_nodes,
+                            int q_heads, int kv_heads, int head_dim, const int32_t* seq_len, const int32_t* pos_offset,
+                            int64_t pos_batch_stride, const float* inv_freq, void* q_out, void* k_cache, void* v_cache,
+                            int64_t cache_batch_stride, int64_t cache_head_stride, int capacity,
+                            const int32_t* row_map, int32_t* err_flag, void* stream) {
+  FG_REQUIRE(x && w_pairs && seq_len && pos_offset && inv_freq && q_out && k_cache && v_cache,
+             "fg_linear_rope_kv_write: null pointer");
+  FG_REQUIRE(batch > 0 && num_nodes > 0 && q_heads > 0 && kv_heads > 0 && rows == batch * num_nodes && hidden > 0,
+             "fg_linear_rope_kv_write: bad shape (rows must be batch * num_nodes)");
+  FG_REQUIRE(head_dim > 0 && head_dim % 8 == 0 && head_dim <= 256,
+             "fg_linear_rope_kv_write: head_dim must be a multiple of 8 in [8, 256]");
+  FG_REQUIRE(hidden % kBK == 0, "fg_linear_rope_kv_write: hidden size must be a multiple of 64");
+  FG_REQUIRE(pos_batch_stride == 0 || pos_batch_stride >= num_nodes,
+             "fg_linear_rope_kv_write: pos_batch_stride must be 0 or >= num_nodes");
+  FG_REQUIRE(ldx >= hidden && ldw >= hidden && ldx < (1 << 22) && ldw < (1 << 22) && ldx % 8 == 0 && ldw % 8 == 0 &&
+                 ((uintptr_t)x & 15) == 0 && ((uintptr_t)w_pairs & 15) == 0,
+             "fg_linear_rope_kv_write: x and weight rows must start 16-byte aligned");
+  FG_REQUIRE((((uintptr_t)q_out | (uintptr_t)k_cache | (uintptr_t)v_cache) & 7) == 0 && cache_batch_stride % 4 == 0 &&
+                 cache_head_stride % 4 == 0 && ((uintptr_t)bias_pairs & 7) == 0,
+             "fg_linear_rope_kv_write: outputs must be 8-byte aligned");
+  FG_REQUIRE((tile_m == 64 || tile_m == 128) && (tile_n == 64 || tile_n == 128),
+             "fg_linear_rope_kv_write: tile_m and tile_n must be 64 or 128");
+  FG_REQUIRE(stages == 0 || (stages >= 2 && stages <= 4), "fg_linear_rope_kv_write: stages must be 0 (4), 2, 3 or 4");
+  const int cols = (q_heads + 2 * kv_heads) * head_dim;
+  FG_REQUIRE((int64_t)((rows + tile_m - 1) / tile_m) * ((cols + tile_n - 1) / tile_n) < (1 << 30),
+             "fg_linear_rope_kv_write: too many tiles");
+  LinArgs p{};
+  p.x = (const uint16_t*)x;
+  p.ldx = ldx;
+  p.w = (const uint16_t*)w_pairs;
+  p.ldw = ldw;
+  p.rows = rows;
+  p.cols = cols;
+  p.nks = hidden / kBK;
+  p.ks_per_split = p.nks;  // one split: the epilogue holds the whole sum
+  p.bias = (const uint16_t*)bias_pairs;
+  p.num_nodes = num_nodes;
+  p.q_heads = q_heads;
+  p.kv_heads = kv_heads;
+  p.head_dim = head_dim;
+  p.seq_len = seq_len;
+  p.pos_offset = pos_offset;
+  p.pos_stride = pos_batch_stride;
+  p.inv_freq = inv_freq;
+  p.q_out = (uint16_t*)q_out;
+  p.k_cache = (uint16_t*)k_cache;
+  p.v_cache = (uint16_t*)v_cache;
+  p.cache_batch = cache_batch_stride;
+  p.cache_head = cache_head_stride;
+  p.capacity = capacity;
+  p.row_map = row_map;
+  p.err_flag = err_flag;
+  launch_tiles<true>(p, tile_m, tile_n, stages ? stages : 4, (hipStream_t)stream);
+  return fg::check_launch("fg_linear_rope_kv_write");
 }
 
 int fg_residual_rmsnorm_parts(const float* part, int splits, int rows, int hidden, void* x, int64_t ldx,

@@ -546,6 +546,59 @@ def rope_kv_write_parts(parts, bias, *, batch, num_nodes, q_heads, kv_heads, hea
           _ptr(err_flag), _stream())
 
 
+def rope_pair_rows(t, q_heads, kv_heads, head_dim):
+    """The rows (dim 0) of a q/k/v projection weight [width, K] or bias [width] in the order
+    ``fg_linear_rope_kv_write`` takes: each q and k head's rows pair-interleaved (row 2j holds the
+    head's row j, row 2j + 1 its row j + head_dim/2), the v heads' rows in order. A new tensor."""
+    d, h = int(head_dim), int(q_heads) + int(kv_heads)
+    if d % 2 or t.shape[0] != (h + int(kv_heads)) * d:
+        raise ValueError("rope_pair_rows: rows must be (q_heads + 2 kv_heads) * head_dim with an even head_dim")
+    qk = t[:h * d].reshape(h, 2, d // 2, *t.shape[1:]).transpose(1, 2).reshape(h * d, *t.shape[1:])
+    return torch.cat([qk, t[h * d:]]).contiguous()
+
+
+def linear_rope_kv_write(x, w_pairs, bias_pairs, *, tile=(64, 64), stages=0, batch, num_nodes, q_heads, kv_heads,
+                         head_dim, seq_len, pos_offset, inv_freq, q_out, k_cache, v_cache, row_map=None,
+                         err_flag=None):
+    """The q/k/v projection x [batch*num_nodes, K] . w^T with the bias, rotary embedding and KV-slot
+    write in the GEMM epilogue (``fg_linear_rope_kv_write``): the weight and bias given in
+    ``rope_pair_rows`` order; q rows to q_out [batch*num_nodes, q_heads, d], k / v rows to their
+    cache slots, bit for bit as ``linear_parts`` (one split) + ``rope_kv_write_parts``."""
+    _dev(x, w_pairs, bias_pairs, seq_len, pos_offset, inv_freq, q_out, k_cache, v_cache, row_map)
+    _i32(seq_len, "seq_len")
+    _i32(pos_offset, "pos_offset")
+    _i32(row_map, "row_map")
+    width = (q_heads + 2 * kv_heads) * head_dim
+    if not linear_ok(x, w_pairs) or w_pairs.shape[0] != width or x.shape[0] != batch * num_nodes:
+        raise ValueError(f"linear_rope_kv_write: needs bf16 x [{batch * num_nodes}, K] and w [{width}, K] with "
+                         "K % 64 == 0, unit column strides and 16-byte aligned rows")
+    if bias_pairs is not None and (bias_pairs.dtype != torch.bfloat16 or bias_pairs.numel() != width or
+                                   not bias_pairs.is_contiguous()):
+        raise ValueError("linear_rope_kv_write: bias must be a contiguous bf16 [width] tensor")
+    tm, tn = (int(t) for t in tile)
+    if tm not in LINEAR_TILES or tn not in LINEAR_TILES or int(stages) not in (0, 2, 3, 4):
+        raise ValueError(f"linear_rope_kv_write: tiles in {LINEAR_TILES}, stages 0, 2, 3 or 4")
+    if k_cache.dtype != torch.bfloat16 or k_cache.stride(-1) != 1 or k_cache.stride(-2) != head_dim:
+        raise ValueError("linear_rope_kv_write: cache rows must be contiguous bf16 [.., capacity, d]")
+    if v_cache.stride() != k_cache.stride() or v_cache.shape != k_cache.shape or v_cache.dtype != k_cache.dtype:
+        raise ValueError("linear_rope_kv_write: v_cache must have k_cache's shape, strides and dtype")
+    if not q_out.is_contiguous() or q_out.numel() != batch * num_nodes * q_heads * head_dim or \
+            q_out.dtype != torch.bfloat16:
+        raise ValueError("linear_rope_kv_write: q_out must be a contiguous bf16 [batch * num_nodes, q_heads, d] tensor")
+    if pos_offset.dim() == 2:
+        if tuple(pos_offset.shape) != (batch, num_nodes) or not pos_offset.is_contiguous():
+            raise ValueError("linear_rope_kv_write: per-sequence pos_offset must be contiguous [batch, num_nodes]")
+        pos_stride = num_nodes
+    else:
+        if pos_offset.numel() < num_nodes:
+            raise ValueError("linear_rope_kv_write: pos_offset shorter than num_nodes")
+        pos_stride = 0
+    _call("fg_linear_rope_kv_write", _ptr(x), x.stride(0), _ptr(w_pairs), w_pairs.stride(0), _ptr(bias_pairs),
+          x.shape[0], x.shape[1], tm, tn, int(stages), batch, num_nodes, q_heads, kv_heads, head_dim, _ptr(seq_len),
+          _ptr(pos_offset), pos_stride, _ptr(inv_freq), _ptr(q_out), _ptr(k_cache), _ptr(v_cache), k_cache.stride(0),
+          k_cache.stride(1), k_cache.shape[-2], _ptr(row_map), _ptr(err_flag), _stream())
+
+
 # ------------------------------------------------------------------ sampling / acceptance
 def sample_workspace(rows, device):
     """Scratch that lets unrestricted / greedy draws run split over several workgroups per row."""

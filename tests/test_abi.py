@@ -62,6 +62,12 @@ def test_library_loads_and_reports_errors_without_gpu_work():
     assert rc != 0 and b"stages" in lib.fg_last_error()
     rc = lib.fg_linear_parts(p, 192, p, 192, p, 8, 16, 192, 3, 256, 64, 0, None)
     assert rc != 0 and b"tile_m" in lib.fg_last_error()
+    # the q/k/v projection with its rotary epilogue: rows = batch * num_nodes, tiles of 64 / 128
+    args = [p, 128, p, 128, None, 8, 128, 64, 64, 0, 2, 4, 4, 1, 64, p, p, 0, p, p, p, p, 64 * 16, 64 * 16, 16,
+            None, None, None]
+    assert lib.fg_linear_rope_kv_write(*args[:5], 7, *args[6:]) != 0 and b"batch * num_nodes" in lib.fg_last_error()
+    assert lib.fg_linear_rope_kv_write(*args[:7], 96, *args[8:]) != 0 and b"tile_m" in lib.fg_last_error()
+    assert lib.fg_linear_rope_kv_write(*args[:14], 12, *args[15:]) != 0 and b"head_dim" in lib.fg_last_error()
     rc = lib.fg_residual_rmsnorm_parts(p, 1, 4, 12, p, 12, p, 1e-6, p, 12, None)
     assert rc != 0 and b"multiple of 8" in lib.fg_last_error()
     rc = lib.fg_gate_up_swiglu(None, 64, p, 64, p, 8, 4, 8, 64, 0, None)
@@ -80,3 +86,17 @@ def test_tree_attention_split_policy():
     assert small > 16 * 29 * 28 * 128 * 4                                        # at least two parts of fp32 O
     assert lib.fg_tree_attention_workspace(32, 13, 12, 2, 128, 900) == 0       # parts would be under 8 tiles
     assert lib.fg_tree_attention_workspace(2, 13, 12, 2, 64, 900) == 0         # fp32-only head dim
+
+
+def test_rope_pair_rows_interleaves_each_q_and_k_head():
+    import torch
+
+    from flashgrpo_amd import kernels as K
+
+    Hq, Hkv, d = 2, 1, 8
+    rows = torch.arange((Hq + 2 * Hkv) * d)
+    got = K.rope_pair_rows(rows, Hq, Hkv, d).tolist()
+    pairs = lambda h: [h * d + (j // 2 if j % 2 == 0 else d // 2 + j // 2) for j in range(d)]
+    assert got == pairs(0) + pairs(1) + pairs(2) + list(range(3 * d, 4 * d))  # v head in order
+    w = torch.randn((Hq + 2 * Hkv) * d, 5)
+    assert torch.equal(K.rope_pair_rows(w, Hq, Hkv, d)[1], w[4])

@@ -155,3 +155,67 @@ def test_rope_kv_write_parts_equals_rope_of_rounded_rows(with_bias, per_seq_pos)
     assert torch.equal(kc, kr)
     assert torch.equal(vc, vr)
     assert not torch.equal(kc, cache0)  # the tree slots were written
+
+
+@pytest.mark.parametrize("tile,stages", [((64, 64), 4), ((64, 128), 2), ((128, 64), 3), ((128, 128), 4),
+                                         ((128, 128), 2)])
+@pytest.mark.parametrize("with_bias,per_seq_pos,mapped", [(True, False, False), (False, True, True)])
+def test_linear_rope_kv_write_equals_parts_then_rope(tile, stages, with_bias, per_seq_pos, mapped):
+    """The q/k/v projection with the bias, rotary embedding and KV-slot write in its epilogue
+    (pair-interleaved weight rows) writes exactly what fg_linear_parts (one split, the same tile and
+    ring) followed by fg_rope_kv_write_parts writes: the same q rows and cache slots, the rest of the
+    cache untouched. Ragged row counts, per-sequence position offsets and a row map included."""
+    B, N, Hq, Hkv, d, cap, Kd = 5, 13, 12, 2, 128, 64, 384
+    width = (Hq + 2 * Hkv) * d
+    x, w = operands(B * N, Kd, width, seed=21 + stages)
+    g = torch.Generator(device=DEV).manual_seed(3)
+    bias = (0.1 * torch.randn(width, device=DEV, generator=g)).to(torch.bfloat16) if with_bias else None
+    seq_len = torch.tensor([5, 17, 30, 0, 40], dtype=torch.int32, device=DEV)
+    if per_seq_pos:
+        pos = torch.randint(0, 4, (B, N), dtype=torch.int32, device=DEV, generator=g)
+    else:
+        pos = torch.arange(N, dtype=torch.int32, device=DEV) // 3
+    row_map = torch.tensor([4, 2, 0, 1, 3], dtype=torch.int32, device=DEV) if mapped else None
+    inv_freq = 1.0 / (1.0e6 ** (torch.arange(0, d, 2, device=DEV).float() / d))
+    cache0 = torch.randn(B, Hkv, cap, d, device=DEV, generator=g).to(torch.bfloat16)
+    rope = dict(batch=B, num_nodes=N, q_heads=Hq, kv_heads=Hkv, head_dim=d, seq_len=seq_len, pos_offset=pos,
+                inv_freq=inv_freq, row_map=row_map)
+    kr, vr, qr = cache0.clone(), cache0.clone(), torch.empty(B, N, Hq, d, dtype=torch.bfloat16, device=DEV)
+    parts = K().linear_parts(x, w, splits=1, tile=tile, stages=stages)
+    K().rope_kv_write_parts(parts, bias, q_out=qr, k_cache=kr, v_cache=vr, **rope)
+    wp = K().rope_pair_rows(w, Hq, Hkv, d)
+    bp = None if bias is None else K().rope_pair_rows(bias, Hq, Hkv, d)
+    kc, vc, q = cache0.clone(), cache0.clone(), torch.empty_like(qr)
+    K().linear_rope_kv_write(x, wp, bp, tile=tile, stages=stages, q_out=q, k_cache=kc, v_cache=vc, **rope)
+    torch.cuda.synchronize()
+    assert torch.equal(q, qr)
+    assert torch.equal(kc, kr)
+    assert torch.equal(vc, vr)
+    assert not torch.equal(kc, cache0)
+
+
+def test_linear_rope_kv_write_flags_slots_outside_the_cache():
+    """A row whose cache slot falls outside the cache is not written and sets bit 8 of the error
+    flag, as fg_rope_kv_write_parts does; its q row is still written."""
+    B, N, Hq, Hkv, d, cap, Kd = 2, 4, 4, 1, 64, 8, 128
+    width = (Hq + 2 * Hkv) * d
+    x, w = operands(B * N, Kd, width, seed=4)
+    seq_len = torch.tensor([2, 6], dtype=torch.int32, device=DEV)  # sequence 1's slots 6..9 reach past 8
+    pos = torch.arange(N, dtype=torch.int32, device=DEV)
+    inv_freq = 1.0 / (1.0e6 ** (torch.arange(0, d, 2, device=DEV).float() / d))
+    outs = []
+    for fused in (False, True):
+        kc = torch.zeros(B, Hkv, cap, d, dtype=torch.bfloat16, device=DEV)
+        vc, q = torch.zeros_like(kc), torch.zeros(B, N, Hq, d, dtype=torch.bfloat16, device=DEV)
+        flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+        rope = dict(batch=B, num_nodes=N, q_heads=Hq, kv_heads=Hkv, head_dim=d, seq_len=seq_len, pos_offset=pos,
+                    inv_freq=inv_freq, q_out=q, k_cache=kc, v_cache=vc, err_flag=flag)
+        if fused:
+            K().linear_rope_kv_write(x, K().rope_pair_rows(w, Hq, Hkv, d), None, **rope)
+        else:
+            K().rope_kv_write_parts(K().linear_parts(x, w, splits=1, tile=(64, 64)), None, **rope)
+        torch.cuda.synchronize()
+        outs.append((q, kc, vc, int(flag.item())))
+    assert outs[0][3] == outs[1][3] == 8
+    for a, b in zip(outs[0][:3], outs[1][:3]):
+        assert torch.equal(a, b)
