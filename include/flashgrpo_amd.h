@@ -24,7 +24,8 @@
  *   fg_rmsnorm, fg_swiglu  models/qwen_flashgrpo_wrapper.py:172-180 (HF decoder layer)
  *   fg_gate_up_swiglu   models/qwen_flashgrpo_wrapper.py:172-180 (the HF decoder layer's MLP
  *                       act_fn(gate_proj(x)) * up_proj(x), the two projections and the product in one GEMM)
- *   fg_linear_parts, fg_residual_rmsnorm_parts, fg_rope_kv_write_parts, fg_linear_rope_kv_write
+ *   fg_linear_parts, fg_residual_rmsnorm_parts, fg_rope_kv_write_parts, fg_linear_rope_kv_write,
+ *   fg_rope_cos_sin
  *                       models/qwen_flashgrpo_wrapper.py:172-180 (the HF decoder layer's q/k/v, o and
  *                       down projections, finished with the bias + rotary + cache write or the
  *                       residual add + next RMSNorm)
@@ -201,21 +202,28 @@ int fg_rope_kv_write_parts(const float* part, int splits, const void* bias, int 
                            int64_t cache_batch_stride, int64_t cache_head_stride, int capacity,
                            const int32_t* row_map, int32_t* err_flag, void* stream);
 
+/* table[r][j] = (bf16(cos(a)), bf16(sin(a))) as fp32 pairs, a = (seq_len[b] + pos_offset[b *
+ * pos_batch_stride + n]) * inv_freq[j], for rows r = b * num_nodes + n and j < head_dim / 2: the
+ * rotary values fg_rope_kv_write computes per token, once per forward for fg_linear_rope_kv_write.
+ * Replaces the HF rotary embedding's cos / sin (models/qwen_flashgrpo_wrapper.py:172-180). */
+int fg_rope_cos_sin(const int32_t* seq_len, const int32_t* pos_offset, int64_t pos_batch_stride, const float* inv_freq,
+                    int batch, int num_nodes, int head_dim, float* table, void* stream);
+
 /* The q/k/v projection of rows = batch*num_nodes bf16 rows x [rows, ldx] (hidden a multiple of 64)
  * with the bias, rotary embedding and KV-slot write in the GEMM's epilogue (one split of
  * fg_linear_parts' kernel, tile_m / tile_n 64 or 128, stages 0 (4), 2, 3 or 4): the same values,
  * bit for bit, as fg_linear_parts with one split followed by fg_rope_kv_write_parts. w_pairs and
  * bias_pairs (NULL for none) are the projection's weight rows and bias with every q and k head's
  * rows pair-interleaved -- row 2j of a head holds its row j, row 2j + 1 its row j + head_dim/2 --
- * and the v heads' rows in order; the outputs are in the usual order. Replaces the q/k/v
- * projections with the HF rotary embedding and DynamicCache.update
- * (models/qwen_flashgrpo_wrapper.py:172-180). */
+ * and the v heads' rows in order; cos_sin is fg_rope_cos_sin's table of these rows; the outputs
+ * are in the usual order. Replaces the q/k/v projections with the HF rotary embedding and
+ * DynamicCache.update (models/qwen_flashgrpo_wrapper.py:172-180). */
 int fg_linear_rope_kv_write(const void* x, int64_t ldx, const void* w_pairs, int64_t ldw, const void* bias_pairs,
                             int rows, int hidden, int tile_m, int tile_n, int stages, int batch, int num_nodes,
-                            int q_heads, int kv_heads, int head_dim, const int32_t* seq_len, const int32_t* pos_offset,
-                            int64_t pos_batch_stride, const float* inv_freq, void* q_out, void* k_cache, void* v_cache,
-                            int64_t cache_batch_stride, int64_t cache_head_stride, int capacity,
-                            const int32_t* row_map, int32_t* err_flag, void* stream);
+                            int q_heads, int kv_heads, int head_dim, const int32_t* seq_len, const float* cos_sin,
+                            void* q_out, void* k_cache, void* v_cache, int64_t cache_batch_stride,
+                            int64_t cache_head_stride, int capacity, const int32_t* row_map, int32_t* err_flag,
+                            void* stream);
 
 /* out[r] = [LayerNorm(state[r]) * state_w + state_b, LayerNorm(token[r]) * token_w + token_b]
  * ([rows, 2*hidden], row stride 2*hidden): the ChainDraftCell's normalised inputs side by side.

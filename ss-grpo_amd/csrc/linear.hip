@@ -94,9 +94,7 @@ struct LinArgs {
   const uint16_t* bias;  // [cols] bf16 in the weight's row order, or null
   int num_nodes, q_heads, kv_heads, head_dim;
   const int32_t* seq_len;
-  const int32_t* pos_offset;
-  int64_t pos_stride;
-  const float* inv_freq;
+  const float2* cos_sin;  // [rows, d/2] (cos, sin) of each row's angles, rounded to bf16
   uint16_t* q_out;  // [rows, q_heads, d]
   uint16_t* k_cache;
   uint16_t* v_cache;
@@ -115,8 +113,8 @@ __global__ void __launch_bounds__(256, NS * (BM + BN) * kRowBytes <= 80 * 1024 ?
   constexpr int LA = BM / 32, LB = BN / 32, LPW = LA + LB;  // 1 KB loads per wave per step
   static_assert(FM >= 1 && FN >= 1 && LA * 4 * 8 == BM && LB * 4 * 8 == BN, "tile sizes: multiples of 64");
   static_assert(NS >= 2 && NS * STAGE <= 160 * 1024 && (NS - 1) * LPW < 64, "ring stages: LDS and vmcnt");
-  // ROPE: the epilogue's per-row positions and cos / sin table [BM][BN/2] after the ring is idle
-  constexpr int ROPE_LDS = ROPE ? 1024 + BM * (BN / 2) * 8 : 0;
+  // ROPE: the epilogue's cos / sin table [BM][BN/2] after the ring is idle
+  constexpr int ROPE_LDS = ROPE ? BM * (BN / 2) * 8 : 0;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[NS * STAGE > ROPE_LDS ? NS * STAGE : ROPE_LDS];
 
   // XCD-aware order: workgroup b runs on XCD b % 8; XCD x takes tiles x*per_xcd .. +per_xcd-1,
@@ -133,9 +131,12 @@ __global__ void __launch_bounds__(256, NS * (BM + BN) * kRowBytes <= 80 * 1024 ?
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
 
-  // ROPE: each lane's rows (one per 32-row MFMA tile) -> cache slot and cache row, and thread t < BM
-  // -> the position of tile row t, loaded before the main loop so the loads land while it runs.
-  int r_slot[ROPE ? FM : 1], r_cb[ROPE ? FM : 1], t_pos = 0;
+  // ROPE: each lane's rows (one per 32-row MFMA tile) -> cache slot and cache row, and the tile's
+  // (row, column pair) entries of the cos / sin table (RE per thread), loaded before the main loop
+  // so the loads land while it runs.
+  constexpr int RE = ROPE ? BM * (BN / 2) / 256 : 1;
+  int r_slot[ROPE ? FM : 1], r_cb[ROPE ? FM : 1];
+  float2 t_cs[RE];
   if constexpr (ROPE) {
 #pragma unroll
     for (int k = 0; k < FM; ++k) {
@@ -144,10 +145,12 @@ __global__ void __launch_bounds__(256, NS * (BM + BN) * kRowBytes <= 80 * 1024 ?
       r_slot[k] = p.seq_len[b] + m - b * p.num_nodes;
       r_cb[k] = p.row_map ? p.row_map[b] : b;
     }
-    if (tid < BM) {
-      const int m = min(m0 + tid, p.rows - 1);
-      const int b = m / p.num_nodes, n = m - b * p.num_nodes;
-      t_pos = p.seq_len[b] + p.pos_offset[(int64_t)b * p.pos_stride + n];
+    const int hd = p.head_dim / 2;
+#pragma unroll
+    for (int u = 0; u < RE; ++u) {
+      const int e = u * 256 + tid, r = e / (BN / 2), jj = e - r * (BN / 2);
+      const int j = ((n0 + 2 * jj) % p.head_dim) / 2;
+      t_cs[u] = p.cos_sin[(int64_t)min(m0 + r, p.rows - 1) * hd + j];
     }
   }
 
@@ -292,18 +295,11 @@ __global__ void __launch_bounds__(256, NS * (BM + BN) * kRowBytes <= 80 * 1024 ?
     // kernel rotates them (each product and the sum rounded to bf16, cos / sin rounded to bf16);
     // q rows to q_out, k and v rows to their cache slot (slots outside the cache flag an error).
     const int d = p.head_dim, half_d = d / 2;
-    // cos / sin of every (tile row, column pair) in LDS, rounded to bf16 as the rotary kernel rounds
-    // them: the ring is idle after the last step's barrier, the table is read after the next one
-    int* s_pos = (int*)smem;
-    float2* s_cs = (float2*)(smem + 1024);
-    if (tid < BM) s_pos[tid] = t_pos;
-    __syncthreads();
-    for (int e = tid; e < BM * (BN / 2); e += 256) {
-      const int r = e / (BN / 2), jj = e - r * (BN / 2);
-      const int j = ((n0 + 2 * jj) % d) / 2;
-      const float ang = (float)s_pos[r] * p.inv_freq[j];
-      s_cs[e] = make_float2(fg::round_bf16(cosf(ang)), fg::round_bf16(sinf(ang)));
-    }
+    // the tile's cos / sin entries to LDS (the ring is idle after the last step's barrier): lane
+    // (row, pair) reads them back after the barrier
+    float2* s_cs = (float2*)smem;
+#pragma unroll
+    for (int u = 0; u < RE; ++u) s_cs[u * 256 + tid] = t_cs[u];
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < FM; ++k) {
@@ -373,6 +369,23 @@ __global__ void __launch_bounds__(256, NS * (BM + BN) * kRowBytes <= 80 * 1024 ?
               make_float4(acc[i][k][4 * g], acc[i][k][4 * g + 1], acc[i][k][4 * g + 2], acc[i][k][4 * g + 3]);
       }
   }
+}
+
+// table[r][j] = (bf16(cos(pos_r * inv_freq[j])), bf16(sin(pos_r * inv_freq[j]))) for row r = b *
+// num_nodes + n at position seq_len[b] + pos_offset[b * pos_stride + n]: the values the rotary
+// kernel computes per token, once per forward for every layer's fused epilogue.
+__global__ void __launch_bounds__(256) rope_cos_sin_kernel(const int32_t* __restrict__ seq_len,
+                                                           const int32_t* __restrict__ pos_offset, int64_t pos_stride,
+                                                           const float* __restrict__ inv_freq, int num_nodes, int half,
+                                                           int64_t total, float2* __restrict__ table) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= total) return;
+  const int64_t r = e / half;
+  const int j = (int)(e - r * half);
+  const int b = (int)(r / num_nodes), n = (int)(r - (int64_t)b * num_nodes);
+  const int pos = seq_len[b] + pos_offset[(int64_t)b * pos_stride + n];
+  const float ang = (float)pos * inv_freq[j];
+  table[e] = make_float2(fg::round_bf16(cosf(ang)), fg::round_bf16(sinf(ang)));
 }
 
 template <int BM, int BN, int NS, bool ROPE>
@@ -498,21 +511,34 @@ int fg_linear_parts(const void* x, int64_t ldx, const void* w, int64_t ldw, floa
   return fg::check_launch("fg_linear_parts");
 }
 
+int fg_rope_cos_sin(const int32_t* seq_len, const int32_t* pos_offset, int64_t pos_batch_stride, const float* inv_freq,
+                    int batch, int num_nodes, int head_dim, float* table, void* stream) {
+  FG_REQUIRE(seq_len && pos_offset && inv_freq && table, "fg_rope_cos_sin: null pointer");
+  FG_REQUIRE(batch > 0 && num_nodes > 0 && head_dim > 0 && head_dim % 2 == 0, "fg_rope_cos_sin: bad shape");
+  FG_REQUIRE(pos_batch_stride == 0 || pos_batch_stride >= num_nodes,
+             "fg_rope_cos_sin: pos_batch_stride must be 0 or >= num_nodes");
+  FG_REQUIRE(((uintptr_t)table & 7) == 0, "fg_rope_cos_sin: table must be 8-byte aligned");
+  const int64_t total = (int64_t)batch * num_nodes * (head_dim / 2);
+  FG_REQUIRE((total + 255) / 256 < (1ll << 31), "fg_rope_cos_sin: too many rows");
+  hipLaunchKernelGGL(rope_cos_sin_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     seq_len, pos_offset, pos_batch_stride, inv_freq, num_nodes, head_dim / 2, total, (float2*)table);
+  return fg::check_launch("fg_rope_cos_sin");
+}
+
 int fg_linear_rope_kv_write(const void* x, int64_t ldx, const void* w_pairs, int64_t ldw, const void* bias_pairs,
                             int rows, int hidden, int tile_m, int tile_n, int stages, int batch, int num_nodes,
-                            int q_heads, int kv_heads, int head_dim, const int32_t* seq_len, const int32_t* pos_offset,
-                            int64_t pos_batch_stride, const float* inv_freq, void* q_out, void* k_cache, void* v_cache,
-                            int64_t cache_batch_stride, int64_t cache_head_stride, int capacity,
-                            const int32_t* row_map, int32_t* err_flag, void* stream) {
-  FG_REQUIRE(x && w_pairs && seq_len && pos_offset && inv_freq && q_out && k_cache && v_cache,
+                            int q_heads, int kv_heads, int head_dim, const int32_t* seq_len, const float* cos_sin,
+                            void* q_out, void* k_cache, void* v_cache, int64_t cache_batch_stride,
+                            int64_t cache_head_stride, int capacity, const int32_t* row_map, int32_t* err_flag,
+                            void* stream) {
+  FG_REQUIRE(x && w_pairs && seq_len && cos_sin && q_out && k_cache && v_cache,
              "fg_linear_rope_kv_write: null pointer");
   FG_REQUIRE(batch > 0 && num_nodes > 0 && q_heads > 0 && kv_heads > 0 && rows == batch * num_nodes && hidden > 0,
              "fg_linear_rope_kv_write: bad shape (rows must be batch * num_nodes)");
   FG_REQUIRE(head_dim > 0 && head_dim % 8 == 0 && head_dim <= 256,
              "fg_linear_rope_kv_write: head_dim must be a multiple of 8 in [8, 256]");
   FG_REQUIRE(hidden % kBK == 0, "fg_linear_rope_kv_write: hidden size must be a multiple of 64");
-  FG_REQUIRE(pos_batch_stride == 0 || pos_batch_stride >= num_nodes,
-             "fg_linear_rope_kv_write: pos_batch_stride must be 0 or >= num_nodes");
+  FG_REQUIRE(((uintptr_t)cos_sin & 7) == 0, "fg_linear_rope_kv_write: cos_sin must be 8-byte aligned");
   FG_REQUIRE(ldx >= hidden && ldw >= hidden && ldx < (1 << 22) && ldw < (1 << 22) && ldx % 8 == 0 && ldw % 8 == 0 &&
                  ((uintptr_t)x & 15) == 0 && ((uintptr_t)w_pairs & 15) == 0,
              "fg_linear_rope_kv_write: x and weight rows must start 16-byte aligned");
@@ -540,9 +566,7 @@ int fg_linear_rope_kv_write(const void* x, int64_t ldx, const void* w_pairs, int
   p.kv_heads = kv_heads;
   p.head_dim = head_dim;
   p.seq_len = seq_len;
-  p.pos_offset = pos_offset;
-  p.pos_stride = pos_batch_stride;
-  p.inv_freq = inv_freq;
+  p.cos_sin = (const float2*)cos_sin;
   p.q_out = (uint16_t*)q_out;
   p.k_cache = (uint16_t*)k_cache;
   p.v_cache = (uint16_t*)v_cache;

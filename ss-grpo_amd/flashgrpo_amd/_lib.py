@@ -49,8 +49,9 @@ SIGNATURES = {
     "fg_residual_rmsnorm_parts": (_I, [_P, _I, _I, _I, _P, _I64, _P, _F, _P, _I64, _P]),
     "fg_rope_kv_write_parts": (_I, [_P, _I, _P, _I, _I, _I, _I, _I, _I, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I,
                                     _P, _P, _P]),
-    "fg_linear_rope_kv_write": (_I, [_P, _I64, _P, _I64, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I64,
-                                    _P, _P, _P, _P, _I64, _I64, _I, _P, _P, _P]),
+    "fg_rope_cos_sin": (_I, [_P, _P, _I64, _P, _I, _I, _I, _P, _P]),
+    "fg_linear_rope_kv_write": (_I, [_P, _I64, _P, _I64, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P,
+                                    _P, _P, _P, _I64, _I64, _I, _P, _P, _P]),
     "fg_sample_workspace": (_SZ, [_I]),
     "fg_sample_tokens": (_I, [_P, _I, _I64, _I, _I, _P, _P, _P, _I, _I, _U64, _U64, _P, _I, _F, _I, _I, _U32, _P,
                               _P, _SZ, _P]),

@@ -557,16 +557,43 @@ def rope_pair_rows(t, q_heads, kv_heads, head_dim):
     return torch.cat([qk, t[h * d:]]).contiguous()
 
 
-def linear_rope_kv_write(x, w_pairs, bias_pairs, *, tile=(64, 64), stages=0, batch, num_nodes, q_heads, kv_heads,
-                         head_dim, seq_len, pos_offset, inv_freq, q_out, k_cache, v_cache, row_map=None,
-                         err_flag=None):
-    """The q/k/v projection x [batch*num_nodes, K] . w^T with the bias, rotary embedding and KV-slot
-    write in the GEMM epilogue (``fg_linear_rope_kv_write``): the weight and bias given in
-    ``rope_pair_rows`` order; q rows to q_out [batch*num_nodes, q_heads, d], k / v rows to their
-    cache slots, bit for bit as ``linear_parts`` (one split) + ``rope_kv_write_parts``."""
-    _dev(x, w_pairs, bias_pairs, seq_len, pos_offset, inv_freq, q_out, k_cache, v_cache, row_map)
+def rope_cos_sin(*, batch, num_nodes, head_dim, seq_len, pos_offset, inv_freq, out=None):
+    """fp32 [batch*num_nodes, head_dim/2, 2]: (cos, sin) of each row's rotary angles rounded to bf16
+    (``fg_rope_cos_sin``), the table ``linear_rope_kv_write`` reads."""
+    _dev(seq_len, pos_offset, inv_freq, out)
     _i32(seq_len, "seq_len")
     _i32(pos_offset, "pos_offset")
+    pos_stride = _pos_stride(pos_offset, batch, num_nodes, "rope_cos_sin")
+    shape = (batch * num_nodes, head_dim // 2, 2)
+    if out is None:
+        out = torch.empty(shape, dtype=torch.float32, device=seq_len.device)
+    elif out.dtype != torch.float32 or tuple(out.shape) != shape or not out.is_contiguous():
+        raise ValueError(f"rope_cos_sin: out must be a contiguous fp32 {list(shape)} tensor")
+    _call("fg_rope_cos_sin", _ptr(seq_len), _ptr(pos_offset), pos_stride, _ptr(inv_freq), batch, num_nodes, head_dim,
+          _ptr(out), _stream())
+    return out
+
+
+def _pos_stride(pos_offset, batch, num_nodes, what):
+    if pos_offset.dim() == 2:
+        if tuple(pos_offset.shape) != (batch, num_nodes) or not pos_offset.is_contiguous():
+            raise ValueError(f"{what}: per-sequence pos_offset must be contiguous [batch, num_nodes]")
+        return num_nodes
+    if pos_offset.numel() < num_nodes:
+        raise ValueError(f"{what}: pos_offset shorter than num_nodes")
+    return 0
+
+
+def linear_rope_kv_write(x, w_pairs, bias_pairs, *, tile=(64, 64), stages=0, batch, num_nodes, q_heads, kv_heads,
+                         head_dim, seq_len, q_out, k_cache, v_cache, cos_sin=None, pos_offset=None, inv_freq=None,
+                         row_map=None, err_flag=None):
+    """The q/k/v projection x [batch*num_nodes, K] . w^T with the bias, rotary embedding and KV-slot
+    write in the GEMM epilogue (``fg_linear_rope_kv_write``): the weight and bias given in
+    ``rope_pair_rows`` order, the rows' rotary table ``cos_sin`` (``rope_cos_sin``; made here from
+    pos_offset and inv_freq when not given); q rows to q_out [batch*num_nodes, q_heads, d], k / v
+    rows to their cache slots, bit for bit as ``linear_parts`` (one split) + ``rope_kv_write_parts``."""
+    _dev(x, w_pairs, bias_pairs, seq_len, cos_sin, q_out, k_cache, v_cache, row_map)
+    _i32(seq_len, "seq_len")
     _i32(row_map, "row_map")
     width = (q_heads + 2 * kv_heads) * head_dim
     if not linear_ok(x, w_pairs) or w_pairs.shape[0] != width or x.shape[0] != batch * num_nodes:
@@ -585,18 +612,16 @@ def linear_rope_kv_write(x, w_pairs, bias_pairs, *, tile=(64, 64), stages=0, bat
     if not q_out.is_contiguous() or q_out.numel() != batch * num_nodes * q_heads * head_dim or \
             q_out.dtype != torch.bfloat16:
         raise ValueError("linear_rope_kv_write: q_out must be a contiguous bf16 [batch * num_nodes, q_heads, d] tensor")
-    if pos_offset.dim() == 2:
-        if tuple(pos_offset.shape) != (batch, num_nodes) or not pos_offset.is_contiguous():
-            raise ValueError("linear_rope_kv_write: per-sequence pos_offset must be contiguous [batch, num_nodes]")
-        pos_stride = num_nodes
-    else:
-        if pos_offset.numel() < num_nodes:
-            raise ValueError("linear_rope_kv_write: pos_offset shorter than num_nodes")
-        pos_stride = 0
+    if cos_sin is None:
+        cos_sin = rope_cos_sin(batch=batch, num_nodes=num_nodes, head_dim=head_dim, seq_len=seq_len,
+                               pos_offset=pos_offset, inv_freq=inv_freq)
+    elif cos_sin.dtype != torch.float32 or cos_sin.numel() != batch * num_nodes * head_dim or \
+            not cos_sin.is_contiguous():
+        raise ValueError("linear_rope_kv_write: cos_sin must be rope_cos_sin's table of these rows")
     _call("fg_linear_rope_kv_write", _ptr(x), x.stride(0), _ptr(w_pairs), w_pairs.stride(0), _ptr(bias_pairs),
           x.shape[0], x.shape[1], tm, tn, int(stages), batch, num_nodes, q_heads, kv_heads, head_dim, _ptr(seq_len),
-          _ptr(pos_offset), pos_stride, _ptr(inv_freq), _ptr(q_out), _ptr(k_cache), _ptr(v_cache), k_cache.stride(0),
-          k_cache.stride(1), k_cache.shape[-2], _ptr(row_map), _ptr(err_flag), _stream())
+          _ptr(cos_sin), _ptr(q_out), _ptr(k_cache), _ptr(v_cache), k_cache.stride(0), k_cache.stride(1),
+          k_cache.shape[-2], _ptr(row_map), _ptr(err_flag), _stream())
 
 
 # ------------------------------------------------------------------ sampling / acceptance

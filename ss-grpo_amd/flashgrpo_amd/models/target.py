@@ -31,8 +31,8 @@ import torch.nn.functional as F
 
 from .. import kernels as K
 from .. import timing
-from ..tuning import (linear_table_plan, linear_table_split_plan, mlp_table_fused_tile, mlp_table_path,
-                      use_tuned_gemms)
+from ..tuning import (linear_table_plan, linear_table_split_plan, linear_table_times, mlp_table_fused_tile,
+                      mlp_table_path, use_tuned_gemms)
 
 MAX_TREE_NODES = 64      # tree nodes per forward (64-bit ancestor masks)
 MAX_CHAIN_TOKENS = 8192  # new tokens per forward without masks (a causal chain)
@@ -588,6 +588,13 @@ class TargetModel:
         # outside inference mode
         with torch.inference_mode():
             _read_hf_weights(unwrap_causal_lm(src), self.cfg, self.device, self.dtype, into=self.w)
+            cfg = self.cfg
+            for lw in self.w["layers"]:  # derived copies, refreshed in place as well
+                if lw.get("qkv_w_pairs") is not None:
+                    lw["qkv_w_pairs"].copy_(K.rope_pair_rows(lw["qkv_w"], cfg.q_heads, cfg.kv_heads, cfg.head_dim))
+                    if lw.get("qkv_b_pairs") is not None:
+                        lw["qkv_b_pairs"].copy_(K.rope_pair_rows(lw["qkv_b"], cfg.q_heads, cfg.kv_heads,
+                                                                 cfg.head_dim))
         self._hf_key = key
         return True
 
@@ -699,7 +706,18 @@ class TargetModel:
             if h is None:
                 h = K.rmsnorm(x, lw["input_norm"], cfg.rms_eps, out=self._buf("h", (T, H)))
             plan = self._linear_plan("qkv", h, lw["qkv_w"])
-            if plan:
+            if plan and len(plan) == 5:  # the projection with the rotary + cache write in its epilogue
+                wp, bp = self._rope_pairs(l)
+                cs = st.get("rope_cs")
+                if cs is None:  # the rows' rotary table, once per forward
+                    cs = st["rope_cs"] = K.rope_cos_sin(batch=B, num_nodes=N, head_dim=d, seq_len=seq_len,
+                                                        pos_offset=pos_offset, inv_freq=self.inv_freq,
+                                                        out=self._buf("rope_cs", (T, d // 2, 2), torch.float32))
+                K.linear_rope_kv_write(h, wp, bp, tile=plan[:2], stages=plan[3], batch=B, num_nodes=N,
+                                       q_heads=cfg.q_heads, kv_heads=cfg.kv_heads, head_dim=d, seq_len=seq_len,
+                                       cos_sin=cs, q_out=q, k_cache=cache.k(l), v_cache=cache.v(l), row_map=row_map,
+                                       err_flag=err_flag)
+            elif plan:
                 parts = self._linear_parts(h, lw["qkv_w"], plan)
                 K.rope_kv_write_parts(parts, lw["qkv_b"], batch=B, num_nodes=N, q_heads=cfg.q_heads,
                                       kv_heads=cfg.kv_heads, head_dim=d, seq_len=seq_len, pos_offset=pos_offset,
@@ -747,14 +765,38 @@ class TargetModel:
                 x.addmm_(act, lw["down_w"].t())
 
     def _linear_plan(self, kind: str, x: torch.Tensor, w: torch.Tensor):
-        """(tile_m, tile_n, splits, stages) when projection ``kind`` of x by w runs split-K, else None."""
+        """(tile_m, tile_n, splits, stages) when projection ``kind`` of x by w runs split-K, else None;
+        for QKV, (tile_m, tile_n, 1, stages, "rope") when the projection runs with the rotary + cache
+        write in its epilogue (``fg_linear_rope_kv_write``), the measured table's fastest path."""
         if self.split_k_linear is False or not K.linear_ok(x, w):
             return None
         rows, hidden = x.shape
+        cols = w.shape[0]
+        plan = None if self.split_k_linear else linear_path(kind, rows, cols, hidden)
         if self.split_k_linear:  # forced: the best measured split-K plan of the shape, else the default
-            return (linear_table_split_plan(kind, rows, w.shape[0], hidden)
-                    or default_linear_plan(rows, w.shape[0], hidden, _cu_count(x.device)))
-        return linear_path(kind, rows, w.shape[0], hidden)
+            plan = (linear_table_split_plan(kind, rows, cols, hidden)
+                    or default_linear_plan(rows, cols, hidden, _cu_count(x.device)))
+        if kind == "qkv" and x.dtype == torch.bfloat16 and self.cfg.head_dim % 8 == 0:
+            rope = linear_table_times("qkv_rope", rows, cols, hidden)
+            base = linear_table_times("qkv", rows, cols, hidden)
+            if rope is not None and base is not None:
+                # the fused epilogue against the faster of the library and the split-K parts path
+                # (against the parts path alone when split-K is forced)
+                other = base[1] if self.split_k_linear else min(base[0], base[1] if plan else base[0])
+                if rope[1] < other:
+                    return (*rope[2][:2], 1, rope[2][3], "rope")
+        return plan
+
+    def _rope_pairs(self, l: int):
+        """Layer l's q/k/v weight and bias with each q and k head's rows pair-interleaved (the order
+        fg_linear_rope_kv_write takes), made on first use and kept with the layer's weights."""
+        lw = self.w["layers"][l]
+        if lw.get("qkv_w_pairs") is None:
+            cfg = self.cfg
+            lw["qkv_w_pairs"] = K.rope_pair_rows(lw["qkv_w"], cfg.q_heads, cfg.kv_heads, cfg.head_dim)
+            b = lw.get("qkv_b")
+            lw["qkv_b_pairs"] = None if b is None else K.rope_pair_rows(b, cfg.q_heads, cfg.kv_heads, cfg.head_dim)
+        return lw["qkv_w_pairs"], lw["qkv_b_pairs"]
 
     def _linear_parts(self, x: torch.Tensor, w: torch.Tensor, plan) -> torch.Tensor:
         tm, tn, s, ns = plan

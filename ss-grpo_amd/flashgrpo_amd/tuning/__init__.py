@@ -96,7 +96,7 @@ def _linear_read() -> None:
     """Reads the projection path table once: (kind, cols, hidden) -> sorted [(rows, plan)] with
     plan (tile_m, tile_n, splits, stages) for the split-K kernel or () for the library, and
     -> sorted [(rows, split-K plan)] of the best measured split-K plan whichever path won."""
-    entries, split = {}, {}
+    entries, split, times = {}, {}, {}
     choice = os.environ.get("FLASHGRPO_AMD_LINEAR_TABLE", "")
     path = DEFAULT_LINEAR_TABLE if not choice else (None if choice.lower() == "off" else choice)
     if path and os.path.exists(path):
@@ -111,8 +111,11 @@ def _linear_read() -> None:
                 key = (row["kind"], int(row["cols"]), int(row["hidden"]))
                 entries.setdefault(key, []).append((int(row["rows"]), sk if row["choice"] == "split_k" else ()))
                 split.setdefault(key, []).append((int(row["rows"]), sk))
+                times.setdefault(key, []).append((int(row["rows"]), (float(row["library_us"]),
+                                                                     float(row["split_k_us"]), sk)))
     _lin.setdefault("entries", {k: sorted(v) for k, v in entries.items()})
     _lin.setdefault("split", {k: sorted(v) for k, v in split.items()})
+    _lin.setdefault("times", {k: sorted(v) for k, v in times.items()})
 
 
 def _linear_entries() -> dict:
@@ -133,6 +136,19 @@ def linear_table_plan(kind: str, rows: int, cols: int, hidden: int):
         return None
     if int(rows) > 2 * cands[-1][0]:
         return ()
+    return _nearest(cands, rows)
+
+
+def linear_table_times(kind: str, rows: int, cols: int, hidden: int):
+    """(library_us, split_k_us, split-K plan) of the table entry of this kind and these sizes
+    nearest in row count (as ``linear_table_plan``); None when the table has no such entry or the
+    row count is above twice the largest measured one. Kind "qkv_rope" holds the q/k/v projection
+    with the rotary epilogue (``fg_linear_rope_kv_write``) in the split-K columns."""
+    if "times" not in _lin:
+        _linear_read()
+    cands = _lin["times"].get((kind, int(cols), int(hidden)))
+    if not cands or int(rows) > 2 * cands[-1][0]:
+        return None
     return _nearest(cands, rows)
 
 

@@ -12,7 +12,10 @@ a decoder layer can compute the projection together with the op that consumes it
   by ``fg_rmsnorm`` (O, down);
 * ``fg_linear_parts`` followed by the kernel that finishes its fp32 parts
   (``fg_rope_kv_write_parts``, ``fg_residual_rmsnorm_parts``), over tile sizes and split counts
-  that put between 64 and 1024 workgroups on the chip, with a 2- or 4-stage LDS ring.
+  that put between 64 and 1024 workgroups on the chip, with a 2- or 4-stage LDS ring;
+* for QKV also ``fg_linear_rope_kv_write`` (one split, the bias, rotary embedding and cache write
+  in the GEMM's epilogue) over the tile sizes and rings, written as kind ``qkv_rope`` with the
+  same library time and the fused time in the split-K columns.
 
 The verify forward replays its launches as a HIP graph, so each path is timed the same way: one
 graph holding ``batch`` back-to-back calls, the weight rotating over enough copies to exceed the
@@ -117,6 +120,7 @@ def main():
             ws = [(torch.randn(N, Kd, device=dev, generator=g) * 0.02).to(torch.bfloat16) for _ in range(copies)]
             bias = (torch.randn(N, device=dev, generator=g) * 0.02).to(torch.bfloat16) if cfg.qkv_bias else None
             norm_w = torch.ones(H, dtype=torch.bfloat16, device=dev)
+            wp = bp = None  # pair-interleaved copies for the fused QKV epilogue, made on first use
             for rows in sorted(only_rows or (set(GRID) | set(extra))):
                 x = (torch.randn(rows, Kd, device=dev, generator=g) * 0.5).to(torch.bfloat16)
                 res = torch.randn(rows, H, device=dev, generator=g).to(torch.bfloat16)
@@ -170,6 +174,28 @@ def main():
                              f"{choice}")
                 print(f"{cfg.name} {kind} rows {rows}: library {t_lib:.1f}, split-K {top[0]:.1f} "
                       f"(tile {top[1]}x{top[2]}, {top[3]} splits, {top[4]} stages) -> {choice}", flush=True)
+                if kind == "qkv" and not plan:
+                    if wp is None:
+                        wp = [K.rope_pair_rows(w, Hq, Hkv, d) for w in ws]
+                        bp = None if bias is None else K.rope_pair_rows(bias, Hq, Hkv, d)
+                    # the rows' rotary table: made once per forward for all layers, so outside the timing
+                    cs = K.rope_cos_sin(batch=B, num_nodes=nodes, head_dim=d, seq_len=sl, pos_offset=po, inv_freq=inv)
+                    fused_rope = {k: v for k, v in rope.items() if k not in ("pos_offset", "inv_freq")}
+                    fused = None
+                    for tm, tn in TILES:
+                        for ns in STAGES:
+                            def run(tm=tm, tn=tn, ns=ns):
+                                it[0] += 1
+                                K.linear_rope_kv_write(x, wp[it[0] % copies], bp, tile=(tm, tn), stages=ns,
+                                                       cos_sin=cs, **fused_rope)
+                            t = best(run, batch)
+                            if fused is None or t < fused[0]:
+                                fused = (t, tm, tn, ns)
+                    choice = "split_k" if fused[0] < t_lib else "library"
+                    lines.append(f"qkv_rope,{rows},{N},{Kd},{t_lib:.1f},{fused[0]:.1f},{fused[1]},{fused[2]},1,"
+                                 f"{fused[3]},{choice}")
+                    print(f"{cfg.name} qkv_rope rows {rows}: library {t_lib:.1f}, fused {fused[0]:.1f} "
+                          f"(tile {fused[1]}x{fused[2]}, {fused[3]} stages)", flush=True)
                 del x, res, h
             del ws
             torch.cuda.empty_cache()

@@ -63,11 +63,12 @@ def test_library_loads_and_reports_errors_without_gpu_work():
     rc = lib.fg_linear_parts(p, 192, p, 192, p, 8, 16, 192, 3, 256, 64, 0, None)
     assert rc != 0 and b"tile_m" in lib.fg_last_error()
     # the q/k/v projection with its rotary epilogue: rows = batch * num_nodes, tiles of 64 / 128
-    args = [p, 128, p, 128, None, 8, 128, 64, 64, 0, 2, 4, 4, 1, 64, p, p, 0, p, p, p, p, 64 * 16, 64 * 16, 16,
+    args = [p, 128, p, 128, None, 8, 128, 64, 64, 0, 2, 4, 4, 1, 64, p, p, p, p, p, 64 * 16, 64 * 16, 16,
             None, None, None]
     assert lib.fg_linear_rope_kv_write(*args[:5], 7, *args[6:]) != 0 and b"batch * num_nodes" in lib.fg_last_error()
     assert lib.fg_linear_rope_kv_write(*args[:7], 96, *args[8:]) != 0 and b"tile_m" in lib.fg_last_error()
     assert lib.fg_linear_rope_kv_write(*args[:14], 12, *args[15:]) != 0 and b"head_dim" in lib.fg_last_error()
+    assert lib.fg_rope_cos_sin(p, p, 0, p, 2, 4, 63, p, None) != 0 and b"bad shape" in lib.fg_last_error()
     rc = lib.fg_residual_rmsnorm_parts(p, 1, 4, 12, p, 12, p, 1e-6, p, 12, None)
     assert rc != 0 and b"multiple of 8" in lib.fg_last_error()
     rc = lib.fg_gate_up_swiglu(None, 64, p, 64, p, 8, 4, 8, 64, 0, None)

@@ -75,3 +75,26 @@ def test_split_plan_lookup_nearest_row_count(monkeypatch):
     assert tuning.linear_table_split_plan("o", 100, 64, 128) == (64, 64, 2, 4)
     assert tuning.linear_table_split_plan("o", 10 ** 6, 64, 128) == (128, 64, 1, 4)  # no library cut-off
     assert tuning.linear_table_split_plan("qkv", 64, 64, 128) is None
+
+
+@pytest.mark.skipif(not os.path.exists(TABLE), reason="no projection path table")
+def test_fused_rotary_rows_pair_with_qkv_rows():
+    """Every qkv_rope row (the projection with the rotary epilogue) has a qkv row of the same shape
+    measured in the same run (the same library time) and a one-split plan."""
+    by = {(r["kind"], r["rows"], r["cols"], r["hidden"]): r for r in rows()}
+    fused = [r for r in rows() if r["kind"] == "qkv_rope"]
+    assert fused
+    for r in fused:
+        q = by[("qkv", r["rows"], r["cols"], r["hidden"])]
+        assert q["library_us"] == r["library_us"] and r["splits"] == "1", r
+        t = tuning.linear_table_times("qkv_rope", int(r["rows"]), int(r["cols"]), int(r["hidden"]))
+        assert t[:2] == (float(r["library_us"]), float(r["split_k_us"]))
+
+
+def test_times_lookup_nearest_row_count_and_none_beyond_the_range(monkeypatch):
+    monkeypatch.setitem(tuning._lin, "times", {("qkv_rope", 64, 128): [(64, (10.0, 9.0, (64, 64, 1, 4))),
+                                                                       (512, (20.0, 25.0, (128, 64, 1, 2)))]})
+    assert tuning.linear_table_times("qkv_rope", 100, 64, 128) == (10.0, 9.0, (64, 64, 1, 4))
+    assert tuning.linear_table_times("qkv_rope", 1024, 64, 128)[2] == (128, 64, 1, 2)
+    assert tuning.linear_table_times("qkv_rope", 1025, 64, 128) is None
+    assert tuning.linear_table_times("qkv", 64, 64, 128) is None
