@@ -22,7 +22,9 @@ height -- and the fastest; ``mlp_table_path`` looks it up
 (``fg_rope_kv_write``; the residual add and ``fg_rmsnorm``) against the split-K
 ``fg_linear_parts`` with the kernel that finishes its parts, the best tile and split count of the
 latter, and the faster path; ``linear_table_plan`` looks it up
-(``FLASHGRPO_AMD_LINEAR_TABLE=off`` or another path).
+(``FLASHGRPO_AMD_LINEAR_TABLE=off`` or another path). Rows of kind ``qkv_rope`` time the QKV projection
+with its rotary epilogue (``fg_linear_rope_kv_write``) in the split-K columns; ``linear_table_times``
+returns an entry's times.
 """
 from __future__ import annotations
 
